@@ -1,0 +1,289 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Workload ("INT4 decode GEMV sweep over TinyLlama-1.1B
+linear shapes"): one step is the 155 INT4 GEMVs (M=1) of one TinyLlama-1.1B
+decode token -- 22 layers x {q 2048x2048, k 2048x256, v 2048x256,
+o 2048x2048, gate 2048x5632, up 2048x5632, down 5632x2048} + lm_head
+2048x32000 -- each layer with its own weight buffers (646.5 MB of codes and
+scales per step, more than the 256 MB Infinity Cache, so weights stream from
+HBM).  Weights are N(0, 0.02) fp32 packed on the GPU by vm_hip_pack_int4
+(bit-exact with quant.cpp); each layer holds a device copy of its shape's
+packed matrix at its own address.  Activations are N(0, 1) fp32.
+
+Timed region: K graph replays of the captured step on one stream, bracketed
+by HIP events and device synchronisation.  ``value`` is algorithmic bytes
+(codes + scales + fp32 A + fp32 C, each once) per second over the region.
+``roofline.achieved`` uses the kernel's own average duration, measured with
+HIP events around each launch in a separate eager pass.  ``cpu_baseline``
+times the oracle's scalar INT4 path (src/cpu/ops/quantized_matmul.cpp:48-141)
+on one pinned core over a bounded sample of the same step.
+
+Prints one JSON line.  Only --gpus 1 is supported (one GPU per box).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "velo-mind_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+LAYERS = 22
+LAYER_SHAPES = [("q", 2048, 2048), ("k", 2048, 256), ("v", 2048, 256), ("o", 2048, 2048),
+                ("gate", 2048, 5632), ("up", 2048, 5632), ("down", 5632, 2048)]
+LM_HEAD = ("lm_head", 2048, 32000)
+BLOCK = 32
+METRIC = "qmatmul HBM GB/s (% of ~8 TB/s peak); TinyLlama INT4 decode tokens/sec"
+
+
+def algo_bytes(k: int, n: int, m: int = 1) -> int:
+    """Codes + fp32 scales + fp32 A + fp32 C, each counted once."""
+    nb = (k + BLOCK - 1) // BLOCK
+    return ((k + 1) // 2) * n + nb * n * 4 + m * k * 4 + m * n * 4
+
+
+def step_shapes():
+    shapes = []
+    for layer in range(LAYERS):
+        for name, k, n in LAYER_SHAPES:
+            shapes.append((f"L{layer}.{name}", k, n))
+    shapes.append(LM_HEAD)
+    return shapes
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Workload:
+    """Device-resident weights, activations and outputs for one decode step."""
+
+    def __init__(self, H, stream):
+        self.H = H
+        self.stream = stream
+        rng = np.random.default_rng(20240601)
+        self.masters = {}
+        distinct = {(k, n) for _, k, n in LAYER_SHAPES} | {(LM_HEAD[1], LM_HEAD[2])}
+        for k, n in sorted(distinct):
+            w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+            dw = H.DeviceBuffer.from_array(w)
+            packed = H.DeviceBuffer(((k + 1) // 2) * n)
+            scales = H.DeviceBuffer(((k + BLOCK - 1) // BLOCK) * n * 4)
+            H.pack_int4(dw.addr, packed.addr, scales.addr, k, n, BLOCK)
+            H.synchronize()
+            dw.close()
+            self.masters[(k, n)] = (packed, scales)
+        self.x = {k: H.DeviceBuffer.from_array(rng.standard_normal(k, dtype=np.float32)) for k in (2048, 5632)}
+        self.out = {n: H.DeviceBuffer(n * 4) for n in (256, 2048, 5632, 32000)}
+        # every GEMV of the step reads its own copy of the weights
+        self.calls = []
+        lib = H.open_library()
+        for name, k, n in step_shapes():
+            mp, ms = self.masters[(k, n)]
+            if name == LM_HEAD[0]:
+                p, s = mp, ms
+            else:
+                p = H.DeviceBuffer(mp.nbytes)
+                s = H.DeviceBuffer(ms.nbytes)
+                H.check(lib.vm_hip_memcpy_d2d(p.ptr, mp.ptr, mp.nbytes, stream.handle))
+                H.check(lib.vm_hip_memcpy_d2d(s.ptr, ms.ptr, ms.nbytes, stream.handle))
+            self.calls.append((name, k, n, p, s))
+        stream.synchronize()
+        self.bytes_per_step = sum(algo_bytes(k, n) for _, k, n, _, _ in self.calls)
+
+    def launch_step(self) -> None:
+        H, st = self.H, self.stream
+        for _, k, n, p, s in self.calls:
+            H.qmm_f32(self.x[k].addr, p.addr, s.addr, self.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
+
+
+def per_launch_durations(H, wl: Workload, reps: int) -> dict:
+    """Average kernel duration per shape from events around each launch."""
+    st = wl.stream
+    sums: dict = {}
+    counts: dict = {}
+    evs = [(H.Event(), H.Event()) for _ in wl.calls]
+    for _ in range(reps):
+        for (name, k, n, p, s), (e0, e1) in zip(wl.calls, evs):
+            e0.record(st.handle)
+            H.qmm_f32(wl.x[k].addr, p.addr, s.addr, wl.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
+            e1.record(st.handle)
+        st.synchronize()
+        for (name, k, n, _, _), (e0, e1) in zip(wl.calls, evs):
+            key = (k, n)
+            sums[key] = sums.get(key, 0.0) + e0.elapsed_ms(e1)
+            counts[key] = counts.get(key, 0) + 1
+    return {key: sums[key] / counts[key] for key in sums}
+
+
+def cpu_baseline(target_s: float) -> dict:
+    """Oracle scalar INT4 GEMV (reference CPU algorithm), one pinned core."""
+    import oracle as O
+
+    rng = np.random.default_rng(7)
+    mats = {}
+    for _, k, n in LAYER_SHAPES + [LM_HEAD]:
+        if (k, n) not in mats:
+            w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+            p, s = O.quantize_int4(w, BLOCK)
+            mats[(k, n)] = (p.view(np.int8), s, rng.standard_normal((1, k), dtype=np.float32))
+    shapes = step_shapes()
+    cpu = sorted(os.sched_getaffinity(0))[0]
+    prev = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {cpu})
+    try:
+        done_bytes = 0
+        sweeps = 0
+        t0 = time.perf_counter()
+        # whole decode-step sweeps until the bounded sample time is reached
+        while True:
+            for _, k, n in shapes:
+                p, s, x = mats[(k, n)]
+                O.qmm(x, p, s, k, O.QUANT_INT4, BLOCK)
+                done_bytes += algo_bytes(k, n)
+            sweeps += 1
+            if time.perf_counter() - t0 >= target_s:
+                break
+        dt = time.perf_counter() - t0
+    finally:
+        os.sched_setaffinity(0, prev)
+    return {"value": round(done_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{sweeps} full decode-step sweep(s) (155 INT4 GEMVs, M=1) of the oracle's scalar "
+                      f"INT4 loop (src/cpu/ops/quantized_matmul.cpp:48-141), {dt:.1f} s on core {cpu}",
+            "tokens_per_s": round(sweeps / dt, 4)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--event-reps", type=int, default=5, help="eager passes with per-launch events")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; --gpus must be 1 (no multi-GPU path is built)",
+              file=sys.stderr)
+        return 2
+
+    import velomind_hip as H
+
+    H.load()
+    stream = H.Stream()
+    log("bench: packing weights on the GPU")
+    wl = Workload(H, stream)
+    log(f"bench: {len(wl.calls)} GEMVs per step, {wl.bytes_per_step / 1e6:.1f} MB per step")
+
+    # eager warm-up sizes the split-K workspace before any capture
+    for _ in range(2):
+        wl.launch_step()
+    stream.synchronize()
+
+    graph = None
+    if not args.no_graph:
+        graph = H.Graph(stream)
+        graph.begin()
+        wl.launch_step()
+        graph.end()
+
+    def run_step():
+        if graph is not None:
+            graph.launch()
+        else:
+            wl.launch_step()
+
+    for _ in range(args.warmup):
+        run_step()
+    stream.synchronize()
+    H.synchronize()
+
+    e0, e1 = H.Event(), H.Event()
+    wall0 = time.perf_counter()
+    e0.record(stream.handle)
+    for _ in range(args.steps):
+        run_step()
+    e1.record(stream.handle)
+    e1.synchronize()
+    H.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_total = e0.elapsed_ms(e1)
+    ms_per_step = ms_total / args.steps
+    value = wl.bytes_per_step / (ms_per_step * 1e-3) / 1e9
+    log(f"bench: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s (wall {wall:.2f} s)")
+
+    durs = per_launch_durations(H, wl, args.event_reps)
+    per_shape = {}
+    kern_bytes = 0
+    kern_ms = 0.0
+    for (k, n), ms in sorted(durs.items()):
+        count = sum(1 for _, kk, nn, _, _ in wl.calls if (kk, nn) == (k, n))
+        b = algo_bytes(k, n)
+        per_shape[f"{k}x{n}"] = {"launches_per_step": count, "avg_kernel_us": round(ms * 1e3, 3),
+                                 "GB_s": round(b / (ms * 1e-3) / 1e9, 1)}
+        kern_bytes += b * count
+        kern_ms += ms * count
+    achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
+    launches = len(wl.calls)
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("bench: timing CPU baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "tinyllama_1.1b_int4_decode_gemv_sweep",
+            "gemvs_per_step": launches,
+            "layers": LAYERS,
+            "shapes_KxN": [f"{k}x{n}" for _, k, n in LAYER_SHAPES] + [f"{LM_HEAD[1]}x{LM_HEAD[2]}"],
+            "weights": "int4 block 32, quant.cpp layout, packed on GPU from N(0,0.02)",
+            "activations": "fp32 N(0,1), M=1",
+            "bytes_per_step": wl.bytes_per_step,
+            "launch": "eager" if graph is None else "hip_graph",
+        },
+        "gemv_tokens_per_s": round(1e3 / ms_per_step, 1),
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "qmm_gemv_kernel<INT4>",
+            "avg_kernel_us": round(kern_ms / launches * 1e3, 3),
+            "algo_bytes_per_launch": round(kern_bytes / launches),
+        },
+        "per_shape": per_shape,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    if graph is not None:
+        graph.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

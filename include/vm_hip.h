@@ -1,0 +1,186 @@
+/*
+ * vm_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul library
+ * (libvmhip.so).
+ *
+ * Plain pointers and sizes only: no C++ or torch types cross this boundary.
+ * The C++ VeloMind host layer (velo-mind_amd/core) registers
+ * DeviceType::HIP kernels, storage and transfers on top of these entry
+ * points, and ctypes/cgo/JNI callers can bind them directly.
+ *
+ * Conventions
+ *   - Every function returns 0 on success.  A positive value is the
+ *     hipError_t the runtime reported; a negative value is one of the
+ *     VM_HIP_E* codes below.  vm_hip_last_error() returns the message of
+ *     the last failure on the calling thread.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the device's
+ *     default (null) stream.  Compute entry points only enqueue work and
+ *     return; transfers named *_h2d / *_d2h are synchronous on return
+ *     (the reference's MemoryTransfer contract).
+ *   - Matrices use the reference layouts byte for byte (quant.cpp):
+ *       INT8  codes  int8  [K, N]          scales f32 [N] (per column)
+ *                                          or [ceil(K/B), N] (blockwise)
+ *       INT4  codes  uint8 [(K+1)/2, N]    scales f32 [ceil(K/B), N]
+ *             row pair (2r, 2r+1) shares byte row r; the even row is the
+ *             low nibble; nibbles are two's complement.
+ *     Activations A are row-major [M, K]; the output C is row-major [M, N].
+ */
+#ifndef VM_HIP_H
+#define VM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VM_HIP_ABI_VERSION 1
+
+/* Library status codes (negative; positive values are hipError_t). */
+#define VM_HIP_OK           0
+#define VM_HIP_EINVAL      (-1) /* invalid argument (shape, null pointer, dtype)      */
+#define VM_HIP_EUNSUPPORTED (-2) /* valid request that this build does not implement  */
+#define VM_HIP_EINJECTED   (-3) /* failure injected via VELOMIND_FAIL_BACKEND        */
+#define VM_HIP_ENODEVICE   (-4) /* no gfx950 device visible                          */
+
+/* QuantType values: include/velomind/quant.h:18-22. */
+#define VM_HIP_QUANT_INT8 1
+#define VM_HIP_QUANT_INT4 2
+
+/* DataType values: include/velomind/types.h:20-29. */
+#define VM_HIP_DTYPE_F32  0
+#define VM_HIP_DTYPE_F16  4
+#define VM_HIP_DTYPE_BF16 5
+
+/* ---- library / device ------------------------------------------------ */
+
+/* ABI version of the loaded library (VM_HIP_ABI_VERSION). */
+int vm_hip_abi_version(void);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* vm_hip_last_error(void);
+
+/* Number of visible gfx950 devices.  Replaces the reference's
+ * DeviceAvailabilityFn for CUDA (src/cuda/storage.cu:79-83). */
+int vm_hip_device_count(int* count);
+
+/* hipSetDevice / hipGetDevice. */
+int vm_hip_set_device(int device);
+int vm_hip_get_device(int* device);
+
+/* Block until all work on the current device has finished. */
+int vm_hip_device_synchronize(void);
+
+/* ---- memory ------------------------------------------------------------ */
+
+/* Device allocation; *ptr is NULL for bytes == 0.  Replaces the
+ * reference's StorageCreatorFn for CUDA (src/cuda/storage.cu:17-41,
+ * src/internal/registry/storage.h:13). */
+int vm_hip_malloc(void** ptr, size_t bytes);
+int vm_hip_free(void* ptr);
+
+/* Synchronous copies (complete on return).  Replace the reference's
+ * MemoryTransfer{copy_h2d, copy_d2h} (src/cuda/storage.cu:43-78,
+ * src/internal/registry/memory_transfer.h:11-14). */
+int vm_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int vm_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+/* Asynchronous device-to-device copy on `stream`. */
+int vm_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+
+/* ---- streams and events (the reference's per-thread CudaContext,
+ *      src/cuda/cuda_context.h:16-74) -------------------------------- */
+int vm_hip_stream_create(void** stream);
+int vm_hip_stream_destroy(void* stream);
+int vm_hip_stream_synchronize(void* stream);
+int vm_hip_event_create(void** event);
+int vm_hip_event_destroy(void* event);
+int vm_hip_event_record(void* event, void* stream);
+int vm_hip_event_synchronize(void* event);
+int vm_hip_event_elapsed_ms(float* ms, void* start, void* end);
+
+/* ---- HIP graphs (no counterpart in the reference, whose engine rebuilds
+ *      and re-launches its graph every token): capture the launches one
+ *      decode step makes on `stream` once and replay them with a single
+ *      call.  Capture needs a non-null stream, and every quantized-matmul
+ *      shape in the captured region must have run once on that stream
+ *      before capture (the split-K workspace cannot grow while capturing).
+ *      The captured kernels reset their own counters, so the graph holds no
+ *      memset nodes. ------------------------------------------------- */
+int vm_hip_stream_begin_capture(void* stream);
+int vm_hip_stream_end_capture(void* stream, void** graph_exec);
+int vm_hip_graph_launch(void* graph_exec, void* stream);
+int vm_hip_graph_destroy(void* graph_exec);
+
+/* ---- the hot path ------------------------------------------------------ */
+
+/*
+ * C[m, n] = sum_k A[m, k] * W[k, n], W dequantized from `wq`/`scale`.
+ *
+ * Replaces the QuantizedMatMul kernels of the reference's CPU and CUDA
+ * backends: src/cpu/ops/quantized_matmul.cpp:237-267 (dispatch) and
+ * :48-141 (semantics), src/cuda/ops/quantized_matmul.cu:203-266 (launch).
+ *
+ *   quant_type  VM_HIP_QUANT_INT8 or VM_HIP_QUANT_INT4
+ *   block_size  INT8: 0 = one scale per column, > 0 = blockwise scales
+ *               [ceil(k/block_size), n].  INT4: > 0 and even; 0 means 32
+ *               (quantized_matmul.cpp:67).
+ *   rows_m      rows of A and C; batch dimensions of contiguous A/C fold
+ *               into it (quantized_matmul.cu:262).
+ *
+ * Accumulation is fp32.  rows_m <= 4 runs the HBM-bound GEMV kernels;
+ * larger rows_m runs the MFMA GEMM, which rounds A to fp16 (codes are exact
+ * in fp16 and scales stay fp32).  k == 0 writes zeros; rows_m == 0 or
+ * n == 0 is a no-op.
+ */
+int vm_hip_qmm_f32(const float* a, const int8_t* wq, const float* scale, float* c,
+                   int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size,
+                   void* stream);
+
+/*
+ * Same operation for the reference's mixed-precision dtype keys
+ * (src/cpu/ops/quantized_matmul.cpp:363-367): (a, scale, c) dtypes in
+ * {(F32,F32,F32), (F16,F16,F16), (F16,F32,F16), (BF16,BF16,BF16),
+ * (BF16,F32,BF16)}.  Half inputs are widened to fp32, accumulation is fp32
+ * and half outputs are rounded to nearest even (include/velomind/dtype.h:
+ * 53-107).
+ */
+int vm_hip_qmm(const void* a, int a_dtype, const int8_t* wq, const void* scale,
+               int scale_dtype, void* c, int c_dtype, int64_t rows_m, int64_t k, int64_t n,
+               int quant_type, int block_size, void* stream);
+
+/*
+ * Per-column symmetric INT8 quantization of a device fp32 matrix
+ * w[rows, cols] into codes q[rows, cols] and scales[cols], bit-exact with
+ * quantize_weights_int8_per_channel (src/quant.cpp:74-104).
+ */
+int vm_hip_pack_int8(const float* w, int8_t* q, float* scale, int64_t rows, int64_t cols,
+                     void* stream);
+
+/*
+ * Blockwise symmetric INT4 quantization of a device fp32 matrix
+ * w[rows, cols] into packed[(rows+1)/2, cols] and scales[ceil(rows/block),
+ * cols], bit-exact with quantize_weights_int4_block (src/quant.cpp:
+ * 125-175).  `block` must be positive and even (odd blocks make the
+ * reference's pair packing overwrite bytes across blocks; the graph
+ * validation rejects them, src/internal/op_validation.h:180-182).
+ */
+int vm_hip_pack_int4(const float* w, uint8_t* packed, float* scale, int64_t rows,
+                     int64_t cols, int64_t block, void* stream);
+
+/* Inverse maps (src/quant.cpp:106-123 and :177-209). */
+int vm_hip_dequant_int8(const int8_t* q, const float* scale, float* w, int64_t rows,
+                        int64_t cols, void* stream);
+int vm_hip_dequant_int4(const uint8_t* packed, const float* scale, float* w, int64_t rows,
+                        int64_t cols, int64_t block, void* stream);
+
+/* Widen a device fp16/bf16 buffer to fp32 (dtype.h:21-51, :91-95); the
+ * device half of the reference's convert_dtype (src/dtype.cpp:74-95) used
+ * by quantize_storage_int{8,4} for half-precision sources. */
+int vm_hip_half_to_f32(const uint16_t* src, int src_dtype, float* dst, int64_t count,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VM_HIP_H */

@@ -1,0 +1,24 @@
+// Internal launchers shared between the libvmhip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vmhip {
+
+// Decode-shaped GEMV for 1 <= m <= 4 rows (qmm_gemv.hip).  Returns
+// VM_HIP_EUNSUPPORTED when the shape/alignment needs another kernel.
+int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
+                 int n, int quant_type, int block_size, hipStream_t stream);
+
+// Prefill-shaped MFMA GEMM for m > 4 rows (qmm_gemm.hip).
+int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
+                 int n, int quant_type, int block_size, hipStream_t stream);
+
+// Any-shape reference-order kernel used for layouts the fast kernels do
+// not cover (odd N, block sizes that are not multiples of 32).
+int generic_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
+                    int n, int quant_type, int block_size, hipStream_t stream);
+
+}  // namespace vmhip

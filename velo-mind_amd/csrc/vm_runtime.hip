@@ -1,0 +1,372 @@
+// Runtime half of the C ABI: error state, devices, memory, streams,
+// events and the per-stream split-K workspace.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "vm_internal.h"
+
+namespace vmhip {
+
+namespace {
+thread_local std::string t_last_error;
+
+struct WsEntry {
+    void*       base = nullptr;
+    std::size_t partial_floats = 0;
+    std::size_t counter_slots = 0;
+};
+
+std::mutex g_ws_mutex;
+std::map<std::pair<int, hipStream_t>, WsEntry> g_ws;
+
+struct StagingEntry {
+    void*       base = nullptr;
+    std::size_t bytes = 0;
+};
+std::map<std::pair<int, hipStream_t>, StagingEntry> g_staging;
+
+int current_device() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    return dev;
+}
+}  // namespace
+
+void set_error(const std::string& msg) { t_last_error = msg; }
+void clear_error() { t_last_error.clear(); }
+
+int fail_hip(hipError_t err, const char* what) {
+    set_error(std::string(what) + ": " + hipGetErrorName(err) + " (" + hipGetErrorString(err) + ")");
+    return static_cast<int>(err);
+}
+
+int fail_inval(const std::string& what) {
+    set_error(what);
+    return VM_HIP_EINVAL;
+}
+
+int injected_failure(const char* op, const char* stage) {
+    const char* spec = std::getenv("VELOMIND_FAIL_BACKEND");
+    if (!spec) return 0;
+    const std::string key = std::string("HIP:") + op + ":" + stage;
+    if (key != spec) return 0;
+    set_error(std::string(op) + " on HIP at " + stage + ": injected failure");
+    return VM_HIP_EINJECTED;
+}
+
+bool sync_debug_enabled() {
+    const char* v = std::getenv("VELOMIND_HIP_SYNC");
+    return v && v[0] == '1';
+}
+
+int check_launch(const char* op, hipStream_t stream) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        set_error(std::string(op) + " on HIP at launch: " + hipGetErrorName(err) + " (" +
+                  hipGetErrorString(err) + ")");
+        return static_cast<int>(err);
+    }
+    VM_TRY(injected_failure(op, "launch"));
+    VM_TRY(injected_failure(op, "sync"));
+    if (sync_debug_enabled()) {
+        err = hipStreamSynchronize(stream);
+        if (err != hipSuccess) {
+            set_error(std::string(op) + " on HIP at sync: " + hipGetErrorName(err) + " (" +
+                      hipGetErrorString(err) + ")");
+            return static_cast<int>(err);
+        }
+    }
+    return 0;
+}
+
+int get_workspace(hipStream_t stream, std::size_t partial_floats, std::size_t counter_slots,
+                  Workspace* out) {
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    WsEntry& e = g_ws[{dev, stream}];
+    if (e.base == nullptr || e.partial_floats < partial_floats || e.counter_slots < counter_slots) {
+        if (stream != nullptr) {
+            hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+                return fail_inval("QuantizedMatMul: split-K workspace must be sized by an eager call "
+                                  "on this stream before graph capture");
+        }
+        // Grow geometrically so that a sweep of shapes settles quickly.
+        std::size_t pf = std::max(partial_floats, e.partial_floats * 2);
+        std::size_t cs = std::max(counter_slots, e.counter_slots * 2);
+        pf = std::max<std::size_t>(pf, 1 << 16);
+        cs = std::max<std::size_t>(cs, 1024);
+        if (e.base) {
+            // Kernels queued on this stream may still use the old buffer.
+            VM_TRY_HIP(hipStreamSynchronize(stream), "workspace resize: hipStreamSynchronize");
+            VM_TRY_HIP(hipFree(e.base), "workspace resize: hipFree");
+            e.base = nullptr;
+        }
+        const std::size_t counter_bytes = ((cs * sizeof(unsigned)) + 255) & ~std::size_t(255);
+        void* base = nullptr;
+        VM_TRY_HIP(hipMalloc(&base, counter_bytes + pf * sizeof(float)), "workspace: hipMalloc");
+        hipError_t err = hipMemset(base, 0, counter_bytes);
+        if (err != hipSuccess) {
+            (void)hipFree(base);
+            return fail_hip(err, "workspace: hipMemset");
+        }
+        e.base = base;
+        e.partial_floats = pf;
+        e.counter_slots = cs;
+    }
+    const std::size_t counter_bytes = ((e.counter_slots * sizeof(unsigned)) + 255) & ~std::size_t(255);
+    out->counters = static_cast<unsigned*>(e.base);
+    out->partials = reinterpret_cast<float*>(static_cast<char*>(e.base) + counter_bytes);
+    return 0;
+}
+
+void release_workspace(hipStream_t stream) {
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    auto it = g_ws.find({dev, stream});
+    if (it != g_ws.end()) {
+        if (it->second.base) (void)hipFree(it->second.base);
+        g_ws.erase(it);
+    }
+    auto st = g_staging.find({dev, stream});
+    if (st != g_staging.end()) {
+        if (st->second.base) (void)hipFree(st->second.base);
+        g_staging.erase(st);
+    }
+}
+
+int get_staging(hipStream_t stream, std::size_t bytes, void** out) {
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    StagingEntry& e = g_staging[{dev, stream}];
+    if (e.base == nullptr || e.bytes < bytes) {
+        if (stream != nullptr) {
+            hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+                return fail_inval("QuantizedMatMul: staging buffer must be sized by an eager call "
+                                  "on this stream before graph capture");
+        }
+        const std::size_t want = std::max<std::size_t>(std::max(bytes, e.bytes * 2), 1 << 20);
+        if (e.base) {
+            VM_TRY_HIP(hipStreamSynchronize(stream), "staging resize: hipStreamSynchronize");
+            VM_TRY_HIP(hipFree(e.base), "staging resize: hipFree");
+            e.base = nullptr;
+        }
+        VM_TRY_HIP(hipMalloc(&e.base, want), "staging: hipMalloc");
+        e.bytes = want;
+    }
+    *out = e.base;
+    return 0;
+}
+
+int cu_count() {
+    static std::mutex m;
+    static std::map<int, int> cache;
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lock(m);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    cache[dev] = cus;
+    return cus;
+}
+
+}  // namespace vmhip
+
+using namespace vmhip;
+
+extern "C" {
+
+int vm_hip_abi_version(void) { return VM_HIP_ABI_VERSION; }
+
+const char* vm_hip_last_error(void) { return t_last_error.c_str(); }
+
+int vm_hip_device_count(int* count) {
+    if (!count) return fail_inval("vm_hip_device_count: null count");
+    *count = 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    int usable = 0;
+    for (int d = 0; d < n; ++d) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, d) != hipSuccess) continue;
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ++usable;
+    }
+    *count = usable;
+    return 0;
+}
+
+int vm_hip_set_device(int device) {
+    VM_TRY_HIP(hipSetDevice(device), "hipSetDevice");
+    return 0;
+}
+
+int vm_hip_get_device(int* device) {
+    if (!device) return fail_inval("vm_hip_get_device: null device");
+    VM_TRY_HIP(hipGetDevice(device), "hipGetDevice");
+    return 0;
+}
+
+int vm_hip_device_synchronize(void) {
+    VM_TRY_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return 0;
+}
+
+int vm_hip_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail_inval("vm_hip_malloc: null ptr");
+    *ptr = nullptr;
+    if (bytes == 0) return 0;
+    hipError_t err = hipMalloc(ptr, bytes);
+    if (err != hipSuccess) {
+        *ptr = nullptr;
+        set_error("velomind: hipMalloc failed for " + std::to_string(bytes) + " bytes (" +
+                  hipGetErrorName(err) + "): " + hipGetErrorString(err));
+        return static_cast<int>(err);
+    }
+    return 0;
+}
+
+int vm_hip_free(void* ptr) {
+    if (!ptr) return 0;
+    VM_TRY_HIP(hipFree(ptr), "hipFree");
+    return 0;
+}
+
+static int copy_sync(void* dst, const void* src, size_t bytes, void* stream, hipMemcpyKind kind,
+                     const char* what) {
+    if (bytes == 0) return 0;
+    if (!dst || !src) return fail_inval(std::string(what) + ": null pointer");
+    auto s = static_cast<hipStream_t>(stream);
+    hipError_t err = hipMemcpyAsync(dst, src, bytes, kind, s);
+    if (err != hipSuccess) {
+        set_error(std::string("velomind: ") + what + " failed for " + std::to_string(bytes) +
+                  " bytes (" + hipGetErrorName(err) + "): " + hipGetErrorString(err));
+        return static_cast<int>(err);
+    }
+    err = hipStreamSynchronize(s);
+    if (err != hipSuccess) {
+        set_error(std::string("velomind: hipStreamSynchronize (") + what + ") failed (" +
+                  hipGetErrorName(err) + "): " + hipGetErrorString(err));
+        return static_cast<int>(err);
+    }
+    return 0;
+}
+
+int vm_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    return copy_sync(dst, src, bytes, stream, hipMemcpyHostToDevice, "hipMemcpyAsync (H2D)");
+}
+
+int vm_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    return copy_sync(dst, src, bytes, stream, hipMemcpyDeviceToHost, "hipMemcpyAsync (D2H)");
+}
+
+int vm_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return 0;
+    if (!dst || !src) return fail_inval("vm_hip_memcpy_d2d: null pointer");
+    VM_TRY_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)),
+               "hipMemcpyAsync (D2D)");
+    return 0;
+}
+
+int vm_hip_stream_create(void** stream) {
+    if (!stream) return fail_inval("vm_hip_stream_create: null stream");
+    hipStream_t s = nullptr;
+    // Default priority and non-blocking w.r.t. the null stream, like the
+    // reference's CudaStream (src/cuda/cuda_context.h:19).
+    VM_TRY_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    *stream = s;
+    return 0;
+}
+
+int vm_hip_stream_destroy(void* stream) {
+    if (!stream) return 0;
+    auto s = static_cast<hipStream_t>(stream);
+    VM_TRY_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+    release_workspace(s);
+    VM_TRY_HIP(hipStreamDestroy(s), "hipStreamDestroy");
+    return 0;
+}
+
+int vm_hip_stream_synchronize(void* stream) {
+    VM_TRY_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+    return 0;
+}
+
+int vm_hip_event_create(void** event) {
+    if (!event) return fail_inval("vm_hip_event_create: null event");
+    hipEvent_t e = nullptr;
+    VM_TRY_HIP(hipEventCreate(&e), "hipEventCreate");
+    *event = e;
+    return 0;
+}
+
+int vm_hip_event_destroy(void* event) {
+    if (!event) return 0;
+    VM_TRY_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+    return 0;
+}
+
+int vm_hip_event_record(void* event, void* stream) {
+    VM_TRY_HIP(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)),
+               "hipEventRecord");
+    return 0;
+}
+
+int vm_hip_event_synchronize(void* event) {
+    VM_TRY_HIP(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+    return 0;
+}
+
+int vm_hip_event_elapsed_ms(float* ms, void* start, void* end) {
+    if (!ms) return fail_inval("vm_hip_event_elapsed_ms: null ms");
+    VM_TRY_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)),
+               "hipEventElapsedTime");
+    return 0;
+}
+
+int vm_hip_stream_begin_capture(void* stream) {
+    if (!stream) return fail_inval("vm_hip_stream_begin_capture: capture needs a non-null stream");
+    VM_TRY_HIP(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal),
+               "hipStreamBeginCapture");
+    return 0;
+}
+
+int vm_hip_stream_end_capture(void* stream, void** graph_exec) {
+    if (!stream || !graph_exec) return fail_inval("vm_hip_stream_end_capture: null argument");
+    *graph_exec = nullptr;
+    hipGraph_t graph = nullptr;
+    VM_TRY_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (err != hipSuccess) return fail_hip(err, "hipGraphInstantiate");
+    *graph_exec = exec;
+    return 0;
+}
+
+int vm_hip_graph_launch(void* graph_exec, void* stream) {
+    if (!graph_exec) return fail_inval("vm_hip_graph_launch: null graph");
+    VM_TRY_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), static_cast<hipStream_t>(stream)),
+               "hipGraphLaunch");
+    return 0;
+}
+
+int vm_hip_graph_destroy(void* graph_exec) {
+    if (!graph_exec) return 0;
+    VM_TRY_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+    return 0;
+}
+
+}  // extern "C"

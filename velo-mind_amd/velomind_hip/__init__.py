@@ -1,0 +1,306 @@
+"""ctypes binding of libvmhip.so, the C ABI declared in include/vm_hip.h.
+
+This is a thin host-side shim used by tests, bench.py and smoke(): device
+memory comes from vm_hip_malloc, every call checks the returned status and
+raises ``VmHipError`` with vm_hip_last_error() text.  There is no CPU
+fallback: if the library or the GPU is missing, ``load()`` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvmhip.so")
+CORE_LIB_PATH = os.path.join(_HERE, "libvelomind.so")
+
+QUANT_INT8 = 1
+QUANT_INT4 = 2
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 4, 5
+EINVAL, EUNSUPPORTED, EINJECTED, ENODEVICE = -1, -2, -3, -4
+
+_lib: ctypes.CDLL | None = None
+
+
+class VmHipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    p = c_void_p
+    sig = {
+        "vm_hip_abi_version": ([], c_int),
+        "vm_hip_last_error": ([], c_char_p),
+        "vm_hip_device_count": ([POINTER(c_int)], c_int),
+        "vm_hip_set_device": ([c_int], c_int),
+        "vm_hip_get_device": ([POINTER(c_int)], c_int),
+        "vm_hip_device_synchronize": ([], c_int),
+        "vm_hip_malloc": ([POINTER(c_void_p), c_size_t], c_int),
+        "vm_hip_free": ([p], c_int),
+        "vm_hip_memcpy_h2d": ([p, p, c_size_t, p], c_int),
+        "vm_hip_memcpy_d2h": ([p, p, c_size_t, p], c_int),
+        "vm_hip_memcpy_d2d": ([p, p, c_size_t, p], c_int),
+        "vm_hip_stream_create": ([POINTER(c_void_p)], c_int),
+        "vm_hip_stream_destroy": ([p], c_int),
+        "vm_hip_stream_synchronize": ([p], c_int),
+        "vm_hip_event_create": ([POINTER(c_void_p)], c_int),
+        "vm_hip_event_destroy": ([p], c_int),
+        "vm_hip_event_record": ([p, p], c_int),
+        "vm_hip_event_synchronize": ([p], c_int),
+        "vm_hip_event_elapsed_ms": ([POINTER(c_float), p, p], c_int),
+        "vm_hip_stream_begin_capture": ([p], c_int),
+        "vm_hip_stream_end_capture": ([p, POINTER(c_void_p)], c_int),
+        "vm_hip_graph_launch": ([p, p], c_int),
+        "vm_hip_graph_destroy": ([p], c_int),
+        "vm_hip_qmm_f32": ([p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
+        "vm_hip_qmm": ([p, c_int, p, p, c_int, p, c_int, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
+        "vm_hip_pack_int8": ([p, p, p, c_int64, c_int64, p], c_int),
+        "vm_hip_pack_int4": ([p, p, p, c_int64, c_int64, c_int64, p], c_int),
+        "vm_hip_dequant_int8": ([p, p, p, c_int64, c_int64, p], c_int),
+        "vm_hip_dequant_int4": ([p, p, p, c_int64, c_int64, c_int64, p], c_int),
+        "vm_hip_half_to_f32": ([p, c_int, p, c_int64, p], c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+
+
+def exported_symbols() -> list[str]:
+    """Entry points that include/vm_hip.h declares."""
+    return ["vm_hip_abi_version", "vm_hip_last_error", "vm_hip_device_count", "vm_hip_set_device",
+            "vm_hip_get_device", "vm_hip_device_synchronize", "vm_hip_malloc", "vm_hip_free",
+            "vm_hip_memcpy_h2d", "vm_hip_memcpy_d2h", "vm_hip_memcpy_d2d", "vm_hip_stream_create",
+            "vm_hip_stream_destroy", "vm_hip_stream_synchronize", "vm_hip_event_create",
+            "vm_hip_event_destroy", "vm_hip_event_record", "vm_hip_event_synchronize",
+            "vm_hip_event_elapsed_ms", "vm_hip_stream_begin_capture", "vm_hip_stream_end_capture",
+            "vm_hip_graph_launch", "vm_hip_graph_destroy", "vm_hip_qmm_f32", "vm_hip_qmm", "vm_hip_pack_int8",
+            "vm_hip_pack_int4", "vm_hip_dequant_int8", "vm_hip_dequant_int4", "vm_hip_half_to_f32"]
+
+
+def open_library() -> ctypes.CDLL:
+    """dlopen libvmhip.so without touching the GPU (safe on CPU-only hosts)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libvmhip.so not built at {LIB_PATH}; run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        _declare(L)
+        _lib = L
+    return _lib
+
+
+def load() -> ctypes.CDLL:
+    """Open the library and require a visible gfx950 device."""
+    L = open_library()
+    n = c_int(0)
+    check(L.vm_hip_device_count(byref(n)))
+    if n.value < 1:
+        raise VmHipError(ENODEVICE, "no gfx950 device visible to libvmhip")
+    return L
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = open_library().vm_hip_last_error()
+        raise VmHipError(status, msg.decode() if msg else "")
+
+
+def last_error() -> str:
+    msg = open_library().vm_hip_last_error()
+    return msg.decode() if msg else ""
+
+
+class DeviceBuffer:
+    """A device allocation owned by Python (freed on close / GC)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.ptr = c_void_p(None)
+        check(load().vm_hip_malloc(byref(self.ptr), self.nbytes))
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray, stream=None) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.upload(arr, stream)
+        return buf
+
+    @property
+    def addr(self) -> int:
+        return self.ptr.value or 0
+
+    def upload(self, arr: np.ndarray, stream=None) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(open_library().vm_hip_memcpy_h2d(self.ptr, arr.ctypes.data, arr.nbytes, stream))
+
+    def download(self, dtype, shape, stream=None) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        check(open_library().vm_hip_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes, stream))
+        return out
+
+    def close(self) -> None:
+        if self.ptr.value:
+            check(open_library().vm_hip_free(self.ptr))
+            self.ptr = c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        self.handle = c_void_p(None)
+        check(load().vm_hip_stream_create(byref(self.handle)))
+
+    def synchronize(self) -> None:
+        check(open_library().vm_hip_stream_synchronize(self.handle))
+
+    def close(self) -> None:
+        if self.handle.value:
+            check(open_library().vm_hip_stream_destroy(self.handle))
+            self.handle = c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        self.handle = c_void_p(None)
+        check(load().vm_hip_event_create(byref(self.handle)))
+
+    def record(self, stream=None) -> None:
+        check(open_library().vm_hip_event_record(self.handle, stream))
+
+    def synchronize(self) -> None:
+        check(open_library().vm_hip_event_synchronize(self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = c_float(0.0)
+        check(open_library().vm_hip_event_elapsed_ms(byref(ms), self.handle, end.handle))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.handle.value:
+                open_library().vm_hip_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Launches captured on a Stream between begin() and end(), replayed by launch()."""
+
+    def __init__(self, stream: "Stream"):
+        self.stream = stream
+        self.exec = c_void_p(None)
+
+    def begin(self) -> None:
+        check(open_library().vm_hip_stream_begin_capture(self.stream.handle))
+
+    def end(self) -> None:
+        check(open_library().vm_hip_stream_end_capture(self.stream.handle, byref(self.exec)))
+
+    def launch(self) -> None:
+        check(open_library().vm_hip_graph_launch(self.exec, self.stream.handle))
+
+    def close(self) -> None:
+        if self.exec.value:
+            check(open_library().vm_hip_graph_destroy(self.exec))
+            self.exec = c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _h(stream) -> c_void_p | None:
+    if stream is None:
+        return None
+    return stream.handle if isinstance(stream, Stream) else stream
+
+
+def qmm_f32(a: int, wq: int, scale: int, c: int, m: int, k: int, n: int, quant_type: int,
+            block_size: int, stream=None) -> None:
+    """vm_hip_qmm_f32 on raw device addresses."""
+    check(open_library().vm_hip_qmm_f32(a, wq, scale, c, m, k, n, quant_type, block_size, _h(stream)))
+
+
+def qmm(a: int, a_dtype: int, wq: int, scale: int, scale_dtype: int, c: int, c_dtype: int, m: int,
+        k: int, n: int, quant_type: int, block_size: int, stream=None) -> None:
+    check(open_library().vm_hip_qmm(a, a_dtype, wq, scale, scale_dtype, c, c_dtype, m, k, n,
+                                    quant_type, block_size, _h(stream)))
+
+
+def pack_int8(w: int, q: int, scale: int, rows: int, cols: int, stream=None) -> None:
+    check(open_library().vm_hip_pack_int8(w, q, scale, rows, cols, _h(stream)))
+
+
+def pack_int4(w: int, packed: int, scale: int, rows: int, cols: int, block: int, stream=None) -> None:
+    check(open_library().vm_hip_pack_int4(w, packed, scale, rows, cols, block, _h(stream)))
+
+
+def dequant_int8(q: int, scale: int, w: int, rows: int, cols: int, stream=None) -> None:
+    check(open_library().vm_hip_dequant_int8(q, scale, w, rows, cols, _h(stream)))
+
+
+def dequant_int4(packed: int, scale: int, w: int, rows: int, cols: int, block: int, stream=None) -> None:
+    check(open_library().vm_hip_dequant_int4(packed, scale, w, rows, cols, block, _h(stream)))
+
+
+def synchronize() -> None:
+    check(open_library().vm_hip_device_synchronize())
+
+
+# ---- numpy-level conveniences (host arrays in, host arrays out) ----------
+
+def run_qmm(a: np.ndarray, wq: np.ndarray, scale: np.ndarray, k: int, quant_type: int,
+            block_size: int) -> np.ndarray:
+    """Upload, run vm_hip_qmm_f32 on the null stream, download C [m, n]."""
+    a = np.ascontiguousarray(a, np.float32)
+    m = a.shape[0]
+    n = wq.shape[1]
+    da = DeviceBuffer.from_array(a)
+    dw = DeviceBuffer.from_array(np.ascontiguousarray(wq).view(np.int8))
+    ds = DeviceBuffer.from_array(np.ascontiguousarray(scale, np.float32))
+    dc = DeviceBuffer(max(4, m * n * 4))
+    qmm_f32(da.addr, dw.addr, ds.addr, dc.addr, m, k, n, quant_type, block_size)
+    return dc.download(np.float32, (m, n))
+
+
+def run_pack_int8(w: np.ndarray):
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    dw = DeviceBuffer.from_array(w)
+    dq = DeviceBuffer(max(1, rows * cols))
+    ds = DeviceBuffer(max(4, cols * 4))
+    pack_int8(dw.addr, dq.addr, ds.addr, rows, cols)
+    return dq.download(np.int8, (rows, cols)), ds.download(np.float32, (cols,))
+
+
+def run_pack_int4(w: np.ndarray, block: int = 32):
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    prow = (rows + 1) // 2
+    nb = (rows + block - 1) // block
+    dw = DeviceBuffer.from_array(w)
+    dq = DeviceBuffer(max(1, prow * cols))
+    ds = DeviceBuffer(max(4, nb * cols * 4))
+    pack_int4(dw.addr, dq.addr, ds.addr, rows, cols, block)
+    return dq.download(np.uint8, (prow, cols)), ds.download(np.float32, (nb, cols))
