@@ -3,24 +3,38 @@
 // 128-bit loads, dequantizes in registers and accumulates in fp32.
 //
 // Work decomposition
-//   lane  : VEC consecutive columns (VEC bytes of one code row per load)
-//   wave  : 64 lanes -> 64*VEC columns ("column tile")
-//   unit  : 32 logical K rows (INT4: 16 packed byte rows)
-//   WG    : 4 waves on one column tile; wave w takes units w, w+4, ...
-//           of the WG's K range; the 4 waves reduce through LDS
-//   split : grid.y splits K across workgroups; partial sums go to a
-//           per-stream workspace and the last workgroup of a tile (atomic
-//           ticket) adds them in split order, so results are deterministic
+//   lane      : 16 consecutive columns (one 16-byte load per code row)
+//   row group : L lanes side by side cover one 16*L-column row segment;
+//               a wave holds G = 64/L row groups on consecutive chunks
+//   chunk     : 8 logical K rows (INT4: 4 packed byte rows; INT8: 8 rows),
+//               the unit a row group loads and reduces at a time
+//   workgroup : W waves = W*G row groups on one 16*L-column tile; they walk
+//               the workgroup's K range chunk by chunk, two chunks in
+//               flight per row group (the next chunk's codes and scales are
+//               loaded before the current chunk is reduced)
+//   split     : grid.y splits K; the last workgroup of a tile to finish
+//               (atomic ticket) adds the splits' partials in split order, so
+//               results do not depend on scheduling
 //
-// Dequantization: INT8 codes are sign-extended bytes (v_cvt_f32_i32 with
-// an SDWA byte select).  An INT4 byte holds the even row in its low nibble;
-// moving each nibble to the top of a byte ((w << 4) & 0xF0.. and
-// w & 0xF0..) makes the signed byte equal 16*code, so the same SDWA
-// convert applies and the factor 1/16 is folded (exactly) into the scale.
+// Reduction: row groups of a wave combine with xor shuffles, the waves of
+// a workgroup through LDS, splits through the per-stream workspace.  The
+// split handoff uses agent-scope atomic stores/loads (coherent across XCDs,
+// `sc1`) for the partials: each wave waits for its partial stores to be
+// acknowledged (s_waitcnt) before the barrier that precedes the ticket
+// increment, and the last workgroup reads the partials only after it has
+// observed the final ticket.  No L2 write-back or invalidate is needed.
+//
+// Dequantization: INT8 codes are sign-extended bytes (v_cvt_f32_i32 with an
+// SDWA byte select).  An INT4 byte holds the even K row in its low nibble;
+// moving each nibble to the top of a byte ((w << 4) & 0xF0.. and w & 0xF0..)
+// makes the signed byte equal 16*code, so the same SDWA convert applies and
+// the factor 1/16 is folded (exactly) into the scale.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 
 #include "qmm_kernels.h"
 #include "vm_internal.h"
@@ -28,106 +42,132 @@
 namespace vmhip {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-constexpr int kUnitK = 32;
+constexpr int kChunkK = 8;    // logical K rows per chunk
+constexpr int kVec = 16;      // columns per lane
+constexpr int kMaxSplits = 32;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-template <int VEC>
-__device__ __forceinline__ void load_codes(uint32_t (&dst)[VEC / 4], const uint8_t* p) {
-    if constexpr (VEC == 16) {
-        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
-    } else if constexpr (VEC == 8) {
-        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-        dst[0] = v.x; dst[1] = v.y;
-    } else {
-        dst[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
-    }
+template <int KIND>
+struct ChunkShape {
+    static constexpr bool kInt4 = KIND == 2;
+    static constexpr int kRows = kInt4 ? kChunkK / 2 : kChunkK;  // byte rows per chunk
+    static constexpr bool kScaled = KIND != 0;
+};
+
+__device__ __forceinline__ u32x4 load_row(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-template <int VEC>
-__device__ __forceinline__ void load_scales(float (&dst)[VEC], const float* p) {
-#pragma unroll
-    for (int i = 0; i < VEC; i += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(p + i);
-        dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
-    }
+__device__ __forceinline__ float coherent_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Codes and scales of one chunk for one lane.
+template <int KIND>
+struct Chunk {
+    u32x4 w[ChunkShape<KIND>::kRows];
+    float4 s[ChunkShape<KIND>::kScaled ? 4 : 1];
+};
 
 // KIND: 0 = INT8 per-column scale, 1 = INT8 blockwise, 2 = INT4 blockwise.
-template <int KIND, int VEC, int MR>
-__global__ __launch_bounds__(kThreads) void qmm_gemv_kernel(
+// MR: activation rows (1, 2 or 4); L: lanes per row segment; W: waves.
+template <int KIND, int MR, int L, int W>
+__global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
-    float* __restrict__ c, int m, int k, int n, int units_per_block, int units_per_split,
+    float* __restrict__ c, int m, int k, int n, int block_size, int chunks_per_split,
     float* __restrict__ partials, unsigned* __restrict__ counters) {
-    constexpr bool kInt4 = KIND == 2;
-    constexpr int kRows = kInt4 ? kUnitK / 2 : kUnitK;  // byte rows per unit
-    constexpr int kWords = VEC / 4;
+    using CS = ChunkShape<KIND>;
+    constexpr int G = 64 / L;            // row groups per wave
+    constexpr int RG = W * G;            // row groups per workgroup
+    constexpr int kTileCols = kVec * L;
 
-    __shared__ float red[kWaves][MR][64 * VEC];
+    extern __shared__ float smem[];
+    float* xs = smem;                                     // [MR][chunks_per_split * 8]
+    const int xs_len = chunks_per_split * kChunkK;
+    float* red = smem + MR * xs_len;                      // [W][MR][kTileCols]
     __shared__ unsigned ticket;
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = threadIdx.x >> 6;
+    const int rg = wave * G + lane / L;                   // row group in the workgroup
     const int tile = blockIdx.x;
     const int split = blockIdx.y;
     const int splits = gridDim.y;
-    const int col0 = tile * 64 * VEC + lane * VEC;
+    const int col0 = tile * kTileCols + (lane % L) * kVec;
     const bool col_ok = col0 < n;
 
-    const int total_units = (k + kUnitK - 1) / kUnitK;
-    const int byte_rows = kInt4 ? (k + 1) / 2 : k;
-    const int u_begin = split * units_per_split;
-    const int u_end = min(total_units, u_begin + units_per_split);
+    const int total_chunks = (k + kChunkK - 1) / kChunkK;
+    const int byte_rows = CS::kInt4 ? (k + 1) / 2 : k;
+    const int c_begin = split * chunks_per_split;
+    const int c_end = min(total_chunks, c_begin + chunks_per_split);
+    const int k_begin = c_begin * kChunkK;
 
-    float total[MR][VEC];
+    auto load_chunk = [&](int ch, Chunk<KIND>& dst) {
+        const int row0 = ch * CS::kRows;
 #pragma unroll
-    for (int r = 0; r < MR; ++r)
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) total[r][j] = 0.0f;
-
-    for (int u = u_begin + wave; u < u_end; u += kWaves) {
-        const int row0 = u * kRows;
-        uint32_t w[kRows][kWords];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            if (col_ok && row0 + r < byte_rows) {
-                load_codes<VEC>(w[r], wq + static_cast<int64_t>(row0 + r) * n + col0);
-            } else {
-#pragma unroll
-                for (int d = 0; d < kWords; ++d) w[r][d] = 0u;
-            }
+        for (int r = 0; r < CS::kRows; ++r) {
+            if (col_ok && row0 + r < byte_rows)
+                dst.w[r] = load_row(wq + static_cast<int64_t>(row0 + r) * n + col0);
+            else
+                dst.w[r] = u32x4{0u, 0u, 0u, 0u};
         }
-        float sc[VEC];
-        if constexpr (KIND != 0) {
-            const int blk = (u * kUnitK) / units_per_block;  // units_per_block holds block_size
-            if (col_ok) load_scales<VEC>(sc, scale + static_cast<int64_t>(blk) * n + col0);
+        if constexpr (CS::kScaled) {
+            const int blk = (ch * kChunkK) / block_size;
+            const float4* sp = reinterpret_cast<const float4*>(scale + static_cast<int64_t>(blk) * n + col0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dst.s[q] = col_ok ? sp[q] : float4{0.f, 0.f, 0.f, 0.f};
         }
+    };
 
-        float acc[MR][VEC];
-#pragma unroll
-        for (int r = 0; r < MR; ++r)
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) acc[r][j] = 0.0f;
+    // Issue the first chunk's loads, then stage this split's activations.
+    Chunk<KIND> cur, nxt;
+    int ch = c_begin + rg;
+    if (ch < c_end) load_chunk(ch, cur);
 
-        const int kbase = u * kUnitK;
-        if constexpr (kInt4) {
+    for (int i = threadIdx.x; i < MR * xs_len; i += W * 64) {
+        const int r = i / xs_len;
+        const int kk = k_begin + (i - r * xs_len);
+        xs[i] = (r < m && kk < k) ? a[static_cast<int64_t>(r) * k + kk] : 0.0f;
+    }
+    __syncthreads();
+
+    float total[MR][kVec];
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const int ke = kbase + 2 * r;
+    for (int i = 0; i < MR; ++i)
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) total[i][j] = 0.0f;
+
+    for (; ch < c_end; ch += RG) {
+        const bool more = ch + RG < c_end;
+        if (more) load_chunk(ch + RG, nxt);
+
+        const float* xc = xs + (ch * kChunkK - k_begin);
+        float acc[MR][kVec];
+#pragma unroll
+        for (int i = 0; i < MR; ++i)
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) acc[i][j] = 0.0f;
+
+        if constexpr (CS::kInt4) {
+#pragma unroll
+            for (int r = 0; r < CS::kRows; ++r) {
                 float xe[MR], xo[MR];
 #pragma unroll
                 for (int i = 0; i < MR; ++i) {
-                    xe[i] = (i < m && ke < k) ? a[static_cast<int64_t>(i) * k + ke] : 0.0f;
-                    xo[i] = (i < m && ke + 1 < k) ? a[static_cast<int64_t>(i) * k + ke + 1] : 0.0f;
+                    const float2 xp = *reinterpret_cast<const float2*>(xc + i * xs_len + 2 * r);
+                    xe[i] = xp.x;
+                    xo[i] = xp.y;
                 }
 #pragma unroll
-                for (int d = 0; d < kWords; ++d) {
-                    const uint32_t lo8 = (w[r][d] << 4) & 0xF0F0F0F0u;
-                    const uint32_t hi8 = w[r][d] & 0xF0F0F0F0u;
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t wd = cur.w[r][d];
+                    const uint32_t lo8 = (wd << 4) & 0xF0F0F0F0u;
+                    const uint32_t hi8 = wd & 0xF0F0F0F0u;
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
                         const float fl = static_cast<float>(static_cast<int8_t>(lo8 >> (8 * b)));
@@ -142,17 +182,16 @@ __global__ __launch_bounds__(kThreads) void qmm_gemv_kernel(
             }
         } else {
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const int kr = kbase + r;
+            for (int r = 0; r < CS::kRows; ++r) {
                 float x[MR];
 #pragma unroll
-                for (int i = 0; i < MR; ++i)
-                    x[i] = (i < m && kr < k) ? a[static_cast<int64_t>(i) * k + kr] : 0.0f;
+                for (int i = 0; i < MR; ++i) x[i] = xc[i * xs_len + r];
 #pragma unroll
-                for (int d = 0; d < kWords; ++d) {
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t wd = cur.w[r][d];
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
-                        const float f = static_cast<float>(static_cast<int8_t>(w[r][d] >> (8 * b)));
+                        const float f = static_cast<float>(static_cast<int>(wd << (24 - 8 * b)) >> 24);
 #pragma unroll
                         for (int i = 0; i < MR; ++i) acc[i][4 * d + b] = fmaf(x[i], f, acc[i][4 * d + b]);
                     }
@@ -160,46 +199,54 @@ __global__ __launch_bounds__(kThreads) void qmm_gemv_kernel(
             }
         }
 
-        if constexpr (KIND == 0) {
+        if constexpr (CS::kScaled) {
+            const float f = CS::kInt4 ? 0.0625f : 1.0f;  // INT4 accumulated 16*code
+            float sv[kVec];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sv[4 * q] = cur.s[q].x * f; sv[4 * q + 1] = cur.s[q].y * f;
+                sv[4 * q + 2] = cur.s[q].z * f; sv[4 * q + 3] = cur.s[q].w * f;
+            }
 #pragma unroll
             for (int i = 0; i < MR; ++i)
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) total[i][j] += acc[i][j];
+                for (int j = 0; j < kVec; ++j) total[i][j] = fmaf(sv[j], acc[i][j], total[i][j]);
         } else {
-            const float f = kInt4 ? 0.0625f : 1.0f;  // INT4 accumulated 16*code
 #pragma unroll
             for (int i = 0; i < MR; ++i)
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) total[i][j] = fmaf(sc[j] * f, acc[i][j], total[i][j]);
+                for (int j = 0; j < kVec; ++j) total[i][j] += acc[i][j];
         }
+        if (more) cur = nxt;
     }
 
-    // Reduce the 4 waves of the workgroup through LDS.
+    // Row groups of a wave: lanes l and l ^ (L * 2^t) hold the same columns.
 #pragma unroll
-    for (int i = 0; i < MR; ++i)
+    for (int off = L; off < 64; off <<= 1)
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) red[wave][i][lane * VEC + j] = total[i][j];
+        for (int i = 0; i < MR; ++i)
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) total[i][j] += __shfl_xor(total[i][j], off, 64);
+
+    // Waves of the workgroup through LDS.
+    if (lane < L) {
+#pragma unroll
+        for (int i = 0; i < MR; ++i)
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) red[(wave * MR + i) * kTileCols + lane * kVec + j] = total[i][j];
+    }
     __syncthreads();
 
-    const int tile_cols = 64 * VEC;
-    const int tile_col0 = tile * tile_cols;
-    // Each thread finishes (MR * tile_cols) / kThreads outputs.
-    for (int o = threadIdx.x; o < MR * tile_cols; o += kThreads) {
-        const int i = o / tile_cols;
-        const int cc = o - i * tile_cols;
-        float s = red[0][i][cc] + red[1][i][cc] + red[2][i][cc] + red[3][i][cc];
-        red[0][i][cc] = s;
-    }
-
-    const int64_t col_base = tile_col0;
+    const int tile_col0 = tile * kTileCols;
     if (splits == 1) {
-        __syncthreads();
-        for (int o = threadIdx.x; o < MR * tile_cols; o += kThreads) {
-            const int i = o / tile_cols;
-            const int cc = o - i * tile_cols;
+        for (int o = threadIdx.x; o < MR * kTileCols; o += W * 64) {
+            const int i = o / kTileCols;
+            const int cc = o - i * kTileCols;
             const int col = tile_col0 + cc;
             if (i < m && col < n) {
-                float v = red[0][i][cc];
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < W; ++w) v += red[(w * MR + i) * kTileCols + cc];
                 if constexpr (KIND == 0) v *= scale[col];
                 c[static_cast<int64_t>(i) * n + col] = v;
             }
@@ -207,85 +254,143 @@ __global__ __launch_bounds__(kThreads) void qmm_gemv_kernel(
         return;
     }
 
-    // Split-K: publish this split's partial, take a ticket; the last
-    // workgroup of the tile sums all splits in order and writes C.
-    float* my_part = partials + (static_cast<int64_t>(split) * MR) * n;
-    __syncthreads();
-    for (int o = threadIdx.x; o < MR * tile_cols; o += kThreads) {
-        const int i = o / tile_cols;
-        const int cc = o - i * tile_cols;
+    // Split-K handoff.
+    float* my_part = partials + static_cast<int64_t>(split) * MR * n;
+    for (int o = threadIdx.x; o < MR * kTileCols; o += W * 64) {
+        const int i = o / kTileCols;
+        const int cc = o - i * kTileCols;
         const int col = tile_col0 + cc;
-        if (col < n) my_part[static_cast<int64_t>(i) * n + col] = red[0][i][cc];
+        if (col < n) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; ++w) v += red[(w * MR + i) * kTileCols + cc];
+            coherent_store(my_part + static_cast<int64_t>(i) * n + col, v);
+        }
     }
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the ticket
     __syncthreads();
-    if (threadIdx.x == 0) ticket = atomicAdd(&counters[tile], 1u);
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (ticket != static_cast<unsigned>(splits - 1)) return;
-    __threadfence();
 
-    for (int o = threadIdx.x; o < MR * tile_cols; o += kThreads) {
-        const int i = o / tile_cols;
-        const int cc = o - i * tile_cols;
+    for (int o = threadIdx.x; o < MR * kTileCols; o += W * 64) {
+        const int i = o / kTileCols;
+        const int cc = o - i * kTileCols;
         const int col = tile_col0 + cc;
         if (i < m && col < n) {
+            const float* p = partials + static_cast<int64_t>(i) * n + col;
+            const int64_t stride = static_cast<int64_t>(MR) * n;
             float v = 0.0f;
-            for (int s = 0; s < splits; ++s)
-                v += __builtin_nontemporal_load(partials + (static_cast<int64_t>(s) * MR + i) * n + col);
+            // Batches of independent loads, summed in split order.
+            for (int s0 = 0; s0 < splits; s0 += 8) {
+                float t[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) t[u] = (s0 + u < splits) ? coherent_load(p + (s0 + u) * stride) : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v += t[u];
+            }
             if constexpr (KIND == 0) v *= scale[col];
             c[static_cast<int64_t>(i) * n + col] = v;
         }
     }
-    (void)col_base;
-    if (threadIdx.x == 0) counters[tile] = 0u;  // ready for the next call on this stream
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int KIND, int VEC, int MR>
-int launch_gemv(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
-                int n, int block_size, hipStream_t stream) {
-    const int tile_cols = 64 * VEC;
-    const int tiles = (n + tile_cols - 1) / tile_cols;
-    const int total_units = (k + kUnitK - 1) / kUnitK;
-    // Aim for about two workgroups per CU, with at least one unit per wave.
-    const int target_wgs = 2 * cu_count();
-    int splits = std::max(1, target_wgs / std::max(tiles, 1));
-    splits = std::min(splits, std::max(1, total_units / kWaves));
-    splits = std::min(splits, 64);
-    int units_per_split = (total_units + splits - 1) / splits;
-    // Keep the four waves of a workgroup busy on whole rounds of units.
-    units_per_split = ((units_per_split + kWaves - 1) / kWaves) * kWaves;
-    splits = (total_units + units_per_split - 1) / units_per_split;
+struct GemvConfig {
+    int L = 16;
+    int W = 4;
+    int splits = 1;
+    int chunks_per_split = 0;
+};
 
+int mr_for(int m) { return m <= 1 ? 1 : (m <= 2 ? 2 : 4); }
+
+// Picks lanes-per-segment, waves and splits for a shape.  Measured on
+// MI355X over the TinyLlama-1.1B and SmolLM2 shapes: 8 lanes per row segment
+// (128-column tiles) is best everywhere; about 200 workgroups with at least
+// 16 chunks per split balances split-K round trips against per-wave work;
+// 8 waves pay off once a split holds more than 32 chunks.
+GemvConfig choose_config(int kind, int m, int k, int n) {
+    (void)kind;
+    const int mr = mr_for(m);
+    const int total_chunks = (k + kChunkK - 1) / kChunkK;
+    GemvConfig cfg;
+    cfg.L = 8;
+    const int tiles = (n + kVec * cfg.L - 1) / (kVec * cfg.L);
+    int S = 1;
+    while (S * 2 <= 16 && S * 2 * tiles <= 200) S *= 2;
+    while (S > 1 && (total_chunks + S - 1) / S < 16) S /= 2;
+    int cps = (total_chunks + S - 1) / S;
+    cfg.W = cps > 32 ? 8 : 4;
+    // Activations of one split and the cross-wave buffer share 60 KB of LDS.
+    while (S < kMaxSplits &&
+           (static_cast<long>(mr) * cps * kChunkK + static_cast<long>(cfg.W) * mr * kVec * cfg.L) * 4 > 60 * 1024) {
+        S *= 2;
+        cps = (total_chunks + S - 1) / S;
+    }
+    cfg.chunks_per_split = cps;
+    cfg.splits = (total_chunks + cps - 1) / cps;
+
+    // Tuning override for measurement sweeps: VELOMIND_GEMV_CFG="L,W,S".
+    if (const char* env = std::getenv("VELOMIND_GEMV_CFG")) {
+        int L = 0, W = 0, Sx = 0;
+        if (std::sscanf(env, "%d,%d,%d", &L, &W, &Sx) == 3 && (L == 8 || L == 16 || L == 64) &&
+            (W == 4 || W == 8) && Sx >= 1 && Sx <= kMaxSplits) {
+            const int c2 = (total_chunks + Sx - 1) / Sx;
+            const long lds = (static_cast<long>(mr) * c2 * kChunkK + static_cast<long>(W) * mr * kVec * L) * 4;
+            if (lds <= 60 * 1024) {
+                cfg.L = L;
+                cfg.W = W;
+                cfg.chunks_per_split = c2;
+                cfg.splits = (total_chunks + c2 - 1) / c2;
+            }
+        }
+    }
+    return cfg;
+}
+
+template <int KIND, int MR, int L, int W>
+int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
+               int block_size, const GemvConfig& cfg, hipStream_t stream) {
+    const int tiles = (n + kVec * L - 1) / (kVec * L);
     Workspace ws{};
-    if (splits > 1) {
-        VM_TRY(get_workspace(stream, static_cast<std::size_t>(splits) * MR * n,
+    if (cfg.splits > 1) {
+        VM_TRY(get_workspace(stream, static_cast<std::size_t>(cfg.splits) * MR * n,
                              static_cast<std::size_t>(tiles), &ws));
     }
-    dim3 grid(tiles, splits);
-    hipLaunchKernelGGL((qmm_gemv_kernel<KIND, VEC, MR>), grid, dim3(kThreads), 0, stream, a, wq,
-                       scale, c, m, k, n, block_size, units_per_split, ws.partials, ws.counters);
+    const std::size_t lds = (static_cast<std::size_t>(MR) * cfg.chunks_per_split * kChunkK +
+                             static_cast<std::size_t>(W) * MR * kVec * L) * sizeof(float);
+    hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
+                       stream, a, wq, scale, c, m, k, n, block_size, cfg.chunks_per_split, ws.partials,
+                       ws.counters);
     return check_launch("QuantizedMatMul", stream);
 }
 
 template <int KIND, int MR>
-int dispatch_vec(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
-                 int n, int block_size, hipStream_t stream) {
-    const auto aligned = [&](int v) {
-        return n % v == 0 && (reinterpret_cast<uintptr_t>(wq) % v) == 0 &&
-               (reinterpret_cast<uintptr_t>(scale) % 16) == 0;
-    };
-    if (n >= 1024 && aligned(16)) return launch_gemv<KIND, 16, MR>(a, wq, scale, c, m, k, n, block_size, stream);
-    if (n >= 512 && aligned(8)) return launch_gemv<KIND, 8, MR>(a, wq, scale, c, m, k, n, block_size, stream);
-    if (aligned(4)) return launch_gemv<KIND, 4, MR>(a, wq, scale, c, m, k, n, block_size, stream);
+int launch_mr(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
+              int block_size, hipStream_t stream) {
+    const GemvConfig cfg = choose_config(KIND, m, k, n);
+#define VM_GEMV_CASE(LL, WW)                                                                    \
+    if (cfg.L == LL && cfg.W == WW)                                                             \
+        return launch_cfg<KIND, MR, LL, WW>(a, wq, scale, c, m, k, n, block_size, cfg, stream);
+    VM_GEMV_CASE(8, 4)
+    VM_GEMV_CASE(8, 8)
+    VM_GEMV_CASE(16, 4)
+    VM_GEMV_CASE(16, 8)
+    VM_GEMV_CASE(64, 4)
+    VM_GEMV_CASE(64, 8)
+#undef VM_GEMV_CASE
     return VM_HIP_EUNSUPPORTED;
 }
 
 template <int KIND>
-int dispatch_mr(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
-                int n, int block_size, hipStream_t stream) {
-    if (m == 1) return dispatch_vec<KIND, 1>(a, wq, scale, c, m, k, n, block_size, stream);
-    if (m == 2) return dispatch_vec<KIND, 2>(a, wq, scale, c, m, k, n, block_size, stream);
-    return dispatch_vec<KIND, 4>(a, wq, scale, c, m, k, n, block_size, stream);
+int launch_kind(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
+                int block_size, hipStream_t stream) {
+    if (m == 1) return launch_mr<KIND, 1>(a, wq, scale, c, m, k, n, block_size, stream);
+    if (m == 2) return launch_mr<KIND, 2>(a, wq, scale, c, m, k, n, block_size, stream);
+    return launch_mr<KIND, 4>(a, wq, scale, c, m, k, n, block_size, stream);
 }
 
 }  // namespace
@@ -293,15 +398,19 @@ int dispatch_mr(const float* a, const uint8_t* wq, const float* scale, float* c,
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                  int n, int quant_type, int block_size, hipStream_t stream) {
     if (m < 1 || m > 4) return VM_HIP_EUNSUPPORTED;
+    // 16-byte code loads need 16-byte aligned rows; scales are read as float4.
+    if (n % kVec != 0 || reinterpret_cast<uintptr_t>(wq) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(scale) % 16 != 0)
+        return VM_HIP_EUNSUPPORTED;
     if (quant_type == VM_HIP_QUANT_INT4) {
-        if (block_size <= 0 || block_size % kUnitK != 0) return VM_HIP_EUNSUPPORTED;
-        return dispatch_mr<2>(a, wq, scale, c, m, k, n, block_size, stream);
+        if (block_size <= 0 || block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
+        return launch_kind<2>(a, wq, scale, c, m, k, n, block_size, stream);
     }
     if (block_size > 0) {
-        if (block_size % kUnitK != 0) return VM_HIP_EUNSUPPORTED;
-        return dispatch_mr<1>(a, wq, scale, c, m, k, n, block_size, stream);
+        if (block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
+        return launch_kind<1>(a, wq, scale, c, m, k, n, block_size, stream);
     }
-    return dispatch_mr<0>(a, wq, scale, c, m, k, n, 0, stream);
+    return launch_kind<0>(a, wq, scale, c, m, k, n, 0, stream);
 }
 
 }  // namespace vmhip
