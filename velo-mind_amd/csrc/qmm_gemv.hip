@@ -55,8 +55,17 @@ struct ChunkShape {
     static constexpr bool kScaled = KIND != 0;
 };
 
-__device__ __forceinline__ u32x4 load_row(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+// Raw buffer access (gfx9 descriptor word 3 = 0x00020000): loads past
+// `num_records` bytes return zeros instead of faulting, so tails and idle
+// chunks need no branches and every lane issues the same loads.
+constexpr int kBufferFlags = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferFlags);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset), 0, 0));
 }
 
 __device__ __forceinline__ float coherent_load(const float* p) {
@@ -71,7 +80,7 @@ __device__ __forceinline__ void coherent_store(float* p, float v) {
 template <int KIND>
 struct Chunk {
     u32x4 w[ChunkShape<KIND>::kRows];
-    float4 s[ChunkShape<KIND>::kScaled ? 4 : 1];
+    u32x4 s[ChunkShape<KIND>::kScaled ? 4 : 1];
 };
 
 // KIND: 0 = INT8 per-column scale, 1 = INT8 blockwise, 2 = INT4 blockwise.
@@ -80,7 +89,8 @@ template <int KIND, int MR, int L, int W>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
     float* __restrict__ c, int m, int k, int n, int block_size, int chunks_per_split,
-    float* __restrict__ partials, unsigned* __restrict__ counters) {
+    uint32_t code_bytes, uint32_t scale_bytes, int blk_shift, float* __restrict__ partials,
+    unsigned* __restrict__ counters) {
     using CS = ChunkShape<KIND>;
     constexpr int G = 64 / L;            // row groups per wave
     constexpr int RG = W * G;            // row groups per workgroup
@@ -107,46 +117,29 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const int c_end = min(total_chunks, c_begin + chunks_per_split);
     const int k_begin = c_begin * kChunkK;
 
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wq, code_bytes);
+    const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
+    (void)byte_rows;
+
+    // Chunks outside [c_begin, c_end) read past the end of the buffers and
+    // come back as zeros (codes and scales), contributing nothing.
     auto load_chunk = [&](int ch, Chunk<KIND>& dst) {
-        const int row0 = ch * CS::kRows;
+        const bool valid = ch < c_end;
+        const uint32_t off = valid ? static_cast<uint32_t>(ch * CS::kRows) * static_cast<uint32_t>(n) + col0
+                                   : code_bytes;
 #pragma unroll
-        for (int r = 0; r < CS::kRows; ++r) {
-            if (col_ok && row0 + r < byte_rows)
-                dst.w[r] = load_row(wq + static_cast<int64_t>(row0 + r) * n + col0);
-            else
-                dst.w[r] = u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int r = 0; r < CS::kRows; ++r) dst.w[r] = buffer_load16(wrs, off + static_cast<uint32_t>(r * n));
         if constexpr (CS::kScaled) {
-            const int blk = (ch * kChunkK) / block_size;
-            const float4* sp = reinterpret_cast<const float4*>(scale + static_cast<int64_t>(blk) * n + col0);
+            const uint32_t blk = blk_shift >= 0 ? static_cast<uint32_t>(ch) >> blk_shift
+                                                : static_cast<uint32_t>(ch * kChunkK) / static_cast<uint32_t>(block_size);
+            const uint32_t soff = valid ? (blk * static_cast<uint32_t>(n) + col0) * 4u : scale_bytes;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) dst.s[q] = col_ok ? sp[q] : float4{0.f, 0.f, 0.f, 0.f};
+            for (int q = 0; q < 4; ++q) dst.s[q] = buffer_load16(srs, soff + 16u * q);
         }
     };
 
-    // Issue the first chunk's loads, then stage this split's activations.
-    Chunk<KIND> cur, nxt;
-    int ch = c_begin + rg;
-    if (ch < c_end) load_chunk(ch, cur);
-
-    for (int i = threadIdx.x; i < MR * xs_len; i += W * 64) {
-        const int r = i / xs_len;
-        const int kk = k_begin + (i - r * xs_len);
-        xs[i] = (r < m && kk < k) ? a[static_cast<int64_t>(r) * k + kk] : 0.0f;
-    }
-    __syncthreads();
-
-    float total[MR][kVec];
-#pragma unroll
-    for (int i = 0; i < MR; ++i)
-#pragma unroll
-        for (int j = 0; j < kVec; ++j) total[i][j] = 0.0f;
-
-    for (; ch < c_end; ch += RG) {
-        const bool more = ch + RG < c_end;
-        if (more) load_chunk(ch + RG, nxt);
-
-        const float* xc = xs + (ch * kChunkK - k_begin);
+    auto compute_chunk = [&](const Chunk<KIND>& cur, int ch, float (&total)[MR][kVec]) {
+        const float* xc = xs + (min(ch, c_end - 1) * kChunkK - k_begin);
         float acc[MR][kVec];
 #pragma unroll
         for (int i = 0; i < MR; ++i)
@@ -203,10 +196,9 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
             const float f = CS::kInt4 ? 0.0625f : 1.0f;  // INT4 accumulated 16*code
             float sv[kVec];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                sv[4 * q] = cur.s[q].x * f; sv[4 * q + 1] = cur.s[q].y * f;
-                sv[4 * q + 2] = cur.s[q].z * f; sv[4 * q + 3] = cur.s[q].w * f;
-            }
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sv[4 * q + e] = __uint_as_float(cur.s[q][e]) * f;
 #pragma unroll
             for (int i = 0; i < MR; ++i)
 #pragma unroll
@@ -217,8 +209,38 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
 #pragma unroll
                 for (int j = 0; j < kVec; ++j) total[i][j] += acc[i][j];
         }
-        if (more) cur = nxt;
+    };
+
+    // Issue the first chunk's loads, then stage this split's activations.
+    Chunk<KIND> ca, cb;
+    int ch = c_begin + rg;
+    load_chunk(ch, ca);
+
+    for (int i = threadIdx.x; i < MR * xs_len; i += W * 64) {
+        const int r = i / xs_len;
+        const int kk = k_begin + (i - r * xs_len);
+        xs[i] = (r < m && kk < k) ? a[static_cast<int64_t>(r) * k + kk] : 0.0f;
     }
+    __syncthreads();
+
+    float total[MR][kVec];
+#pragma unroll
+    for (int i = 0; i < MR; ++i)
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) total[i][j] = 0.0f;
+
+    // Every row group runs the same number of steps; two buffers alternate
+    // so one chunk's loads are in flight while the other is reduced (loads
+    // past the split read zeros).  An odd last step runs after the loop.
+    const int iters = (c_end - c_begin + RG - 1) / RG;
+    for (int it = 0; it + 1 < iters; it += 2) {
+        load_chunk(ch + RG, cb);
+        compute_chunk(ca, ch, total);
+        load_chunk(ch + 2 * RG, ca);
+        compute_chunk(cb, ch + RG, total);
+        ch += 2 * RG;
+    }
+    if (iters & 1) compute_chunk(ca, ch, total);
 
     // Row groups of a wave: lanes l and l ^ (L * 2^t) hold the same columns.
 #pragma unroll
@@ -362,9 +384,19 @@ int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, 
     }
     const std::size_t lds = (static_cast<std::size_t>(MR) * cfg.chunks_per_split * kChunkK +
                              static_cast<std::size_t>(W) * MR * kVec * L) * sizeof(float);
+    const int64_t byte_rows = KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : k;
+    const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
+    const uint32_t code_bytes = static_cast<uint32_t>(byte_rows * n);
+    const uint32_t scale_bytes = static_cast<uint32_t>(KIND == 0 ? 0 : nblk * n * 4);
+    // Chunk -> scale block is a shift when block_size / 8 is a power of two.
+    int blk_shift = -1;
+    if (KIND != 0) {
+        const int cpb = block_size / kChunkK;
+        if ((cpb & (cpb - 1)) == 0) blk_shift = __builtin_ctz(static_cast<unsigned>(cpb));
+    }
     hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
-                       stream, a, wq, scale, c, m, k, n, block_size, cfg.chunks_per_split, ws.partials,
-                       ws.counters);
+                       stream, a, wq, scale, c, m, k, n, block_size, cfg.chunks_per_split, code_bytes,
+                       scale_bytes, blk_shift, ws.partials, ws.counters);
     return check_launch("QuantizedMatMul", stream);
 }
 
@@ -398,6 +430,8 @@ int launch_kind(const float* a, const uint8_t* wq, const float* scale, float* c,
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                  int n, int quant_type, int block_size, hipStream_t stream) {
     if (m < 1 || m > 4) return VM_HIP_EUNSUPPORTED;
+    // Buffer offsets are 32-bit: codes and scales must stay below 2 GiB.
+    if (static_cast<int64_t>(k) * n >= (int64_t(1) << 31)) return VM_HIP_EUNSUPPORTED;
     // 16-byte code loads need 16-byte aligned rows; scales are read as float4.
     if (n % kVec != 0 || reinterpret_cast<uintptr_t>(wq) % 16 != 0 ||
         reinterpret_cast<uintptr_t>(scale) % 16 != 0)
