@@ -1,0 +1,39 @@
+"""Builds the C++ test binary tests/cpp/velomind_tests (g++, links the
+VeloMind host layer libvelomind.so and libvmhip.so; compiles the CPU oracle
+in as the checker)."""
+from __future__ import annotations
+
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+PKG = os.path.join(ROOT, "velo-mind_amd")
+LIBDIR = os.path.join(PKG, "velomind_hip")
+OUT = os.path.join(HERE, "velomind_tests")
+
+
+def build() -> str:
+    objdir = os.path.join(PKG, "_build", "tests")
+    os.makedirs(objdir, exist_ok=True)
+    oracle_obj = os.path.join(objdir, "qmm_oracle.o")
+    subprocess.run(["gcc", "-O2", "-fPIC", "-std=c11", "-ffp-contract=off", "-c",
+                    os.path.join(ROOT, "oracle", "qmm_oracle.c"), "-o", oracle_obj], check=True)
+    srcs = sorted(glob.glob(os.path.join(HERE, "*.cpp")))
+    cmd = ["g++", "-O1", "-std=c++20", "-Wall", "-pthread",
+           f"-I{os.path.join(PKG, 'core', 'include')}", f"-I{os.path.join(PKG, 'core', 'src')}",
+           f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(ROOT, 'oracle')}", f"-I{HERE}",
+           *srcs, oracle_obj, "-o", OUT + ".tmp", f"-L{LIBDIR}", "-lvelomind", "-lvmhip",
+           f"-Wl,-rpath,{os.path.relpath(LIBDIR, HERE).join(['$ORIGIN/', ''])}", "-lm"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError("C++ test build failed")
+    os.replace(OUT + ".tmp", OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build())

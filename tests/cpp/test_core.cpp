@@ -1,0 +1,256 @@
+// Host-side tests of the VeloMind core subset: operator contract,
+// registries, ABI values, memory planning and build failure handling.
+// They need no GPU (CPU-device graphs run the oracle kernel registered by
+// test_helpers.cpp).  Cases mirror the reference's
+// tests/test_quantization.cpp:57-98 and :413-478, tests/test_basic.cpp:139-145
+// and tests/test_validation.cpp:133-167.
+#include <stdexcept>
+#include <variant>
+
+#include "internal/registry/kernel.h"
+#include "test_helpers.h"
+
+using namespace velomind;
+using namespace vmtest;
+
+TEST_CASE("Op::QuantizedMatMul operator validation", "[core][validation]") {
+    Graph g;
+    auto a = g.input({2, 16, 64}, DataType::Float32);
+    auto b_q = g.input({64, 128}, DataType::Int8);
+    auto scales = g.input({128}, DataType::Float32);
+
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul), std::invalid_argument);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a), std::invalid_argument);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a, b_q), std::invalid_argument);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a, b_q, scales, a), std::invalid_argument);
+
+    auto a_1d = g.input({64}, DataType::Float32);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a_1d, b_q, scales), std::invalid_argument);
+    auto b_3d = g.input({2, 64, 128}, DataType::Int8);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a, b_3d, scales), std::invalid_argument);
+    auto b_bad_k = g.input({32, 128}, DataType::Int8);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a, b_bad_k, scales), std::invalid_argument);
+    auto scales_bad_n = g.input({64}, DataType::Float32);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a, b_q, scales_bad_n), std::invalid_argument);
+
+    auto scales_block = g.input({2, 128}, DataType::Float32);
+    REQUIRE_NOTHROW(g.op(OpDescriptor{Op::QuantizedMatMul, QuantizedMatMulAttrs{.quant_type = QuantType::Int8, .block_size = 32}},
+                         a, b_q, scales_block));
+    auto a_i32 = g.input({2, 16, 64}, DataType::Int32);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a_i32, b_q, scales), std::invalid_argument);
+    auto b_f32 = g.input({64, 128}, DataType::Float32);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, a, b_f32, scales), std::invalid_argument);
+
+    auto c = g.op(Op::QuantizedMatMul, a, b_q, scales);
+    REQUIRE(c.shape() == shape_t({2, 16, 128}));
+    REQUIRE(c.dtype() == DataType::Float32);
+}
+
+TEST_CASE("QuantizedMatMul INT4 contract: packed rows, block scales, even block", "[core][validation]") {
+    Graph g;
+    auto a = g.input({1, 65}, DataType::Float32);
+    auto packed = g.input({33, 40}, DataType::Int8);  // (65 + 1) / 2 rows
+    auto s_blocks = g.input({3, 40}, DataType::Float32);
+    auto s_flat = g.input({120}, DataType::Float32);
+    const auto int4 = [](int bs) {
+        return OpDescriptor{Op::QuantizedMatMul, QuantizedMatMulAttrs{.quant_type = QuantType::Int4, .block_size = bs}};
+    };
+    REQUIRE_NOTHROW(g.op(int4(32), a, packed, s_blocks));
+    REQUIRE_NOTHROW(g.op(int4(32), a, packed, s_flat));
+    REQUIRE_THROWS_AS(g.op(int4(31), a, packed, s_blocks), std::invalid_argument);  // odd block
+    auto packed_bad = g.input({65, 40}, DataType::Int8);
+    REQUIRE_THROWS_AS(g.op(int4(32), a, packed_bad, s_blocks), std::invalid_argument);
+    auto s_bad = g.input({2, 40}, DataType::Float32);
+    REQUIRE_THROWS_AS(g.op(int4(32), a, packed, s_bad), std::invalid_argument);
+    // block_size 0 asks for per-column scales, which the INT4 packer never
+    // produces (reference quirk kept as is).
+    REQUIRE_THROWS_AS(g.op(int4(0), a, packed, s_blocks), std::invalid_argument);
+}
+
+TEST_CASE("QuantizedMatMulAttrs defaults and ABI values", "[core]") {
+    const auto attrs = std::get<QuantizedMatMulAttrs>(default_op_attrs(Op::QuantizedMatMul));
+    REQUIRE(attrs.quant_type == QuantType::Int8);
+    REQUIRE(attrs.block_size == 0);
+    REQUIRE(attrs.trans_b == false);
+    REQUIRE(static_cast<int>(Op::QuantizedMatMul) == 26);
+    REQUIRE(MAX_OPS == 27);
+    REQUIRE(static_cast<int>(DataType::Int8) == 2);
+    REQUIRE(static_cast<int>(DataType::BFloat16) == 5);
+    REQUIRE(static_cast<int>(DeviceType::HIP) == 3);
+    REQUIRE(MAX_DEVICE_TYPES == 4);
+    REQUIRE(static_cast<int>(QuantType::Int4) == 2);
+    REQUIRE(OpAttrs(QuantizedMatMulAttrs{}).index() == 14);
+    REQUIRE(std::string(quant_type_name(QuantType::None)) == "None");
+    REQUIRE(std::string(quant_type_name(QuantType::Int8)) == "Int8");
+    REQUIRE(std::string(quant_type_name(QuantType::Int4)) == "Int4");
+    REQUIRE(std::string(quant_type_name(static_cast<QuantType>(99))) == "Unknown");
+    REQUIRE(std::string(device_type_name(DeviceType::HIP)) == "HIP");
+    REQUIRE(Device::from_string("hip:0") == Device::hip(0));
+    REQUIRE(Device::from_string("HIP") == Device::hip());
+    REQUIRE(!Device::from_string("hip:x").has_value());
+    REQUIRE(!Device::from_string("metal").has_value());
+}
+
+TEST_CASE("HIP registers the reference's five QuantizedMatMul dtype keys", "[core][registry]") {
+    const DataType F32 = DataType::Float32, F16 = DataType::Float16, BF16 = DataType::BFloat16, I8 = DataType::Int8;
+    const std::vector<std::pair<std::vector<DataType>, DataType>> keys = {
+        {{F32, I8, F32}, F32}, {{F16, I8, F16}, F16}, {{F16, I8, F32}, F16}, {{BF16, I8, BF16}, BF16}, {{BF16, I8, F32}, BF16}};
+    for (const auto& [in, out] : keys) {
+        REQUIRE(internal::resolve_op_kernel(Op::QuantizedMatMul, in, out, DeviceType::HIP) != nullptr);
+        REQUIRE(is_op_dtype_supported(DeviceType::HIP, Op::QuantizedMatMul, in, out));
+    }
+    const std::vector<DataType> bad = {F32, I8, F16};
+    REQUIRE(internal::resolve_op_kernel(Op::QuantizedMatMul, bad, F32, DeviceType::HIP) == nullptr);
+    REQUIRE(internal::resolve_op_kernel(Op::MatMul, std::vector<DataType>{F32, F32}, F32, DeviceType::HIP) == nullptr);
+    REQUIRE(internal::resolve_op_kernel(Op::QuantizedMatMul, keys[0].first, F32, DeviceType::CUDA) == nullptr);
+}
+
+TEST_CASE("validate rejects a device without kernels and foreign handles", "[core][validation]") {
+    Graph g;
+    auto a = g.input({1, 64}, DataType::Float32);
+    auto w = g.input({64, 32}, DataType::Int8);
+    auto s = g.input({32}, DataType::Float32);
+    g.op(Op::QuantizedMatMul, a, w, s);
+    REQUIRE_THROWS_AS(g.validate(DeviceType::CUDA), std::invalid_argument);
+    REQUIRE_THROWS_AS(g.validate(DeviceType::ISPC), std::invalid_argument);
+    Graph other;
+    auto x = other.input({1, 64}, DataType::Float32);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, x, w, s), std::invalid_argument);
+    REQUIRE_THROWS_AS(g.mark_output(x), std::invalid_argument);
+}
+
+namespace {
+// A chain of `layers` QMMs on 64x64 weights; returns the final tensor.
+Tensor build_chain(Graph& g, int layers, std::vector<Tensor>& weights) {
+    auto x = g.input({4, 64}, DataType::Float32);
+    Tensor h = x;
+    for (int i = 0; i < layers; ++i) {
+        auto w = g.input({64, 64}, DataType::Int8);
+        auto s = g.input({64}, DataType::Float32);
+        weights.push_back(w);
+        weights.push_back(s);
+        h = g.op(Op::QuantizedMatMul, h, w, s);
+    }
+    weights.insert(weights.begin(), x);
+    return h;
+}
+}  // namespace
+
+TEST_CASE("memory plan: intermediates share one arena", "[core][memory]") {
+    Graph g;
+    std::vector<Tensor> ins;
+    auto out = build_chain(g, 6, ins);
+    g.mark_output(out);
+    auto exec = g.build(DeviceType::CPU);
+    const auto& st = exec->memory_plan_stats();
+    // 5 intermediates of 1 KiB each; a chain needs only two live slots.
+    REQUIRE(st.intermediate_tensor_count == 5);
+    REQUIRE(g.memory_plan_stats().has_value());
+    // dedicated: x, 6 weights, 6 scales, output = 14 allocations + 1 arena
+    REQUIRE(st.allocation_count == 15);
+    REQUIRE(st.reused_tensor_count >= 3);
+    REQUIRE(st.bytes_saved >= 3 * 1024);
+    REQUIRE(exec->num_nodes() == 6);
+    REQUIRE(g.is_built());
+    REQUIRE(g.bound_device() == DeviceType::CPU);
+    REQUIRE_THROWS_AS(g.op(Op::QuantizedMatMul, out, ins[1], ins[2]), std::logic_error);
+    // intermediates are views into the arena
+    int aliases = 0;
+    for (std::size_t i = 0; i < g.tensor_count(); ++i)
+        if (g.tensor_storage_at(i)->is_alias()) ++aliases;
+    REQUIRE(aliases == 5);
+}
+
+TEST_CASE("dead nodes are eliminated when outputs are marked", "[core][memory]") {
+    Graph g;
+    auto a = g.input({1, 64}, DataType::Float32);
+    auto w = g.input({64, 64}, DataType::Int8);
+    auto s = g.input({64}, DataType::Float32);
+    auto keep = g.op(Op::QuantizedMatMul, a, w, s);
+    g.op(Op::QuantizedMatMul, a, w, s);  // unused
+    g.mark_output(keep);
+    auto exec = g.build(DeviceType::CPU);
+    REQUIRE(exec->num_nodes() == 1);
+    REQUIRE(g.outputs().size() == 1);
+}
+
+TEST_CASE("build failure after an allocation is recoverable", "[core][failure]") {
+    Graph g;
+    std::vector<Tensor> ins;
+    auto out = build_chain(g, 3, ins);
+    g.mark_output(out);
+    {
+        ScopedEnv env("VELOMIND_FAIL_GRAPH_BUILD_AFTER_ALLOCATIONS", "2");
+        REQUIRE_THROWS_AS(g.build(DeviceType::CPU), std::runtime_error);
+    }
+    REQUIRE(!g.is_built());
+    for (std::size_t i = 0; i < g.tensor_count(); ++i) REQUIRE(g.tensor_storage_at(i)->data == nullptr);
+    auto exec = g.build(DeviceType::CPU);
+    REQUIRE(exec != nullptr);
+    REQUIRE(g.is_built());
+}
+
+TEST_CASE("CPU graph runs the oracle kernel end to end", "[core][oracle]") {
+    const std::size_t m = 4, k = 576, n = 576;
+    const auto w = generate_random_weights(k, n);
+    const auto a = generate_activations(m, k);
+    std::vector<std::int8_t> q(k * n);
+    std::vector<float> s(n);
+    vmo_quantize_int8_per_channel(w.data(), q.data(), s.data(), k, n);
+    Graph g;
+    auto ta = g.input({(dim_t)m, (dim_t)k}, DataType::Float32);
+    auto tw = g.input({(dim_t)k, (dim_t)n}, DataType::Int8);
+    auto ts = g.input({(dim_t)n}, DataType::Float32);
+    auto tc = g.op(Op::QuantizedMatMul, ta, tw, ts);
+    auto exec = g.build(DeviceType::CPU);
+    ta.copy_from_host(as_bytes(a));
+    tw.copy_from_host(as_bytes(q));
+    ts.copy_from_host(as_bytes(s));
+    exec->execute();
+    std::vector<float> out(m * n), ref(m * n);
+    tc.copy_to_host(as_writeable_bytes(out));
+    vmo_qmm_2d_f32(a.data(), q.data(), s.data(), ref.data(), m, k, n, 1, 0);
+    REQUIRE(max_abs_diff(out, ref) == 0.0f);
+    REQUIRE_THROWS_AS(tc.copy_to_host(std::span<std::byte>()), std::runtime_error);
+}
+
+TEST_CASE("compute_quantization_metrics edge cases", "[core][metrics]") {
+    auto m0 = compute_quantization_metrics(nullptr, nullptr, 0);
+    REQUIRE(m0.max_diff == 0.0f && m0.rmse == 0.0f && m0.cosine_sim == 1.0f);
+    std::vector<float> x = {1.0f, -2.0f, 3.5f};
+    auto m1 = compute_quantization_metrics(x.data(), x.data(), x.size());
+    REQUIRE(m1.max_diff == 0.0f && m1.rmse == 0.0f && m1.snr_db == 100.0f);
+    REQUIRE(std::abs(m1.cosine_sim - 1.0f) < 1e-6f);
+    // agrees with the oracle's restatement on random data
+    auto a = normal(1000, 3), b = normal(1000, 4);
+    auto m2 = compute_quantization_metrics(a.data(), b.data(), a.size());
+    float ref[4];
+    vmo_quant_metrics(a.data(), b.data(), a.size(), ref);
+    REQUIRE(m2.max_diff == ref[0] && m2.rmse == ref[1] && m2.snr_db == ref[2] && m2.cosine_sim == ref[3]);
+}
+
+TEST_CASE("quantize_storage rank and block checks", "[core][validation]") {
+    TensorStorage s1;
+    s1.shape = {16};
+    REQUIRE_THROWS_AS(quantize_storage_int8(s1), std::invalid_argument);
+    TensorStorage s3;
+    s3.shape = {2, 4, 8};
+    REQUIRE_THROWS_AS(quantize_storage_int8(s3), std::invalid_argument);
+    REQUIRE_THROWS_AS(quantize_storage_int4(s1), std::invalid_argument);
+    TensorStorage s2;
+    s2.shape = {4, 8};
+    REQUIRE_THROWS_AS(quantize_storage_int4(s2, 0), std::invalid_argument);
+    REQUIRE_THROWS_AS(quantize_storage_int4(s2, 3), std::invalid_argument);
+}
+
+TEST_CASE("fp16/bf16 value types match the oracle converters", "[core][dtype]") {
+    for (float v : {0.0f, -0.0f, 1.0f, 1.0009765625f, 65504.0f, 65520.0f, 1e-7f, -3.14159f, 1e30f}) {
+        REQUIRE(float16_t(v).to_bits() == vmo_f32_to_f16(v));
+        REQUIRE(bfloat16_t(v).to_bits() == vmo_f32_to_bf16(v));
+    }
+    for (std::uint32_t b = 0; b < 65536; b += 7) {
+        const float a = float16_to_float(static_cast<std::uint16_t>(b));
+        const float r = vmo_f16_to_f32(static_cast<std::uint16_t>(b));
+        REQUIRE((std::isnan(a) && std::isnan(r)) || float_to_bits(a) == float_to_bits(r));
+    }
+}

@@ -1,0 +1,318 @@
+// DeviceType::HIP tests through the VeloMind API: graphs built with
+// g.build(DeviceType::HIP) against the oracle (the reference's CPU
+// algorithm).  Mirrors the reference's tests/test_quantization.cpp
+// (:140-207 numerics, :310-374 cross-backend, :376-411 storage sizes,
+// :448-469 half-precision sources) and the concurrent build/execute stress
+// of tests/test_coverage_matrix.cpp:690-738.
+#include <atomic>
+#include <cstring>
+#include <stdexcept>
+#include <thread>
+
+#include "test_helpers.h"
+
+using namespace velomind;
+using namespace vmtest;
+
+namespace {
+
+struct QmmCase {
+    std::size_t m, k, n;
+    QuantType qt;
+    int block;
+};
+
+// Runs one QMM graph on `device`; weights given as packed codes + scales.
+std::vector<float> run_graph(DeviceType device, const QmmCase& c, const std::vector<float>& a,
+                             const std::vector<std::int8_t>& q, const std::vector<float>& s) {
+    Graph g;
+    const dim_t qrows = c.qt == QuantType::Int4 ? (dim_t)((c.k + 1) / 2) : (dim_t)c.k;
+    auto ta = g.input({(dim_t)c.m, (dim_t)c.k}, DataType::Float32);
+    auto tw = g.input({qrows, (dim_t)c.n}, DataType::Int8);
+    auto ts = c.block > 0 ? g.input({(dim_t)(s.size() / c.n), (dim_t)c.n}, DataType::Float32)
+                          : g.input({(dim_t)c.n}, DataType::Float32);
+    auto tc = g.op(OpDescriptor{Op::QuantizedMatMul, QuantizedMatMulAttrs{.quant_type = c.qt, .block_size = c.block}},
+                   ta, tw, ts);
+    auto exec = g.build(device);
+    ta.copy_from_host(as_bytes(a));
+    tw.copy_from_host(as_bytes(q));
+    ts.copy_from_host(as_bytes(s));
+    exec->execute();
+    std::vector<float> out(c.m * c.n);
+    tc.copy_to_host(as_writeable_bytes(out));
+    return out;
+}
+
+}  // namespace
+
+TEST_CASE("QuantizedMatMul HIP vs CPU oracle on the reference test matrix", "[gpu][quantization]") {
+    REQUIRE_HIP();
+    for (std::size_t m : {1, 4, 16}) {
+        for (auto [k, n] : std::vector<std::pair<std::size_t, std::size_t>>{{64, 64}, {128, 256}, {576, 576}, {576, 1536}}) {
+            const auto w = generate_random_weights(k, n);
+            const auto a = generate_activations(m, k);
+            std::vector<std::int8_t> q(k * n);
+            std::vector<float> s(n);
+            quantize_weights_int8_per_channel(w.data(), q.data(), s.data(), k, n);  // GPU packer
+            std::vector<std::int8_t> q_ref(k * n);
+            std::vector<float> s_ref(n);
+            vmo_quantize_int8_per_channel(w.data(), q_ref.data(), s_ref.data(), k, n);
+            REQUIRE(q == q_ref);
+            REQUIRE(s == s_ref);
+            const QmmCase c{m, k, n, QuantType::Int8, 0};
+            const auto hip = run_graph(DeviceType::HIP, c, a, q, s);
+            const auto cpu = run_graph(DeviceType::CPU, c, a, q, s);
+            require_all_finite(hip);
+            // GEMV path (m <= 4): fp32 end to end, the reference's 1e-4 bound;
+            // MFMA path: fp16 activations, 1e-3 * max|ref|.
+            const float bound = m <= 4 ? 1e-4f : 1e-3f * max_abs(cpu);
+            REQUIRE(max_abs_diff(hip, cpu) < bound);
+        }
+    }
+}
+
+TEST_CASE("INT4 graph: quantize_storage_int4 on HIP, block 32, TinyLlama q shape", "[gpu][quantization]") {
+    REQUIRE_HIP();
+    const std::size_t k = 2048, n = 2048;
+    const auto w = normal(k * n, 7, 0.02f);
+    TensorStorage src;
+    src.shape = {(dim_t)k, (dim_t)n};
+    src.dtype = DataType::Float32;
+    src.data = const_cast<float*>(w.data());
+    src.size_bytes = src.capacity_bytes = w.size() * 4;
+    auto [q, s] = quantize_storage_int4(src, 32, DeviceType::HIP);
+    REQUIRE(q->device == DeviceType::HIP && q->shape == shape_t({1024, 2048}) && q->dtype == DataType::Int8);
+    REQUIRE(s->shape == shape_t({64, 2048}) && s->dtype == DataType::Float32);
+    REQUIRE(q->size_bytes == ((k + 1) / 2) * n);  // tests/test_quantization.cpp:376-390
+
+    std::vector<std::uint8_t> q_host(q->size_bytes), q_ref(q->size_bytes);
+    std::vector<float> s_host(s->size_bytes / 4), s_ref(s->size_bytes / 4);
+    REQUIRE(vm_hip_memcpy_d2h(q_host.data(), q->data, q->size_bytes, nullptr) == 0);
+    REQUIRE(vm_hip_memcpy_d2h(s_host.data(), s->data, s->size_bytes, nullptr) == 0);
+    vmo_quantize_int4_block(w.data(), q_ref.data(), s_ref.data(), k, n, 32);
+    REQUIRE(q_host == q_ref);
+    REQUIRE(s_host == s_ref);
+
+    Graph g;
+    auto x = g.input({1, (dim_t)k}, DataType::Float32);
+    auto tw = g.input(q);
+    auto ts = g.input(s);
+    auto y = g.op(OpDescriptor{Op::QuantizedMatMul, QuantizedMatMulAttrs{.quant_type = QuantType::Int4, .block_size = 32}},
+                  x, tw, ts);
+    auto exec = g.build(DeviceType::HIP);
+    const auto xv = normal(k, 8);
+    x.copy_from_host(as_bytes(xv));
+    exec->execute();
+    std::vector<float> out(n), ref(n);
+    y.copy_to_host(as_writeable_bytes(out));
+    vmo_qmm_2d_f32(xv.data(), reinterpret_cast<const std::int8_t*>(q_ref.data()), s_ref.data(), ref.data(), 1, k, n, 2, 32);
+    REQUIRE(max_abs_diff(out, ref) <= 1e-5f * max_abs(ref));
+}
+
+TEST_CASE("batched activation [2,16,64] folds into the row count", "[gpu][quantization]") {
+    REQUIRE_HIP();
+    const std::size_t k = 64, n = 128;
+    const auto w = generate_random_weights(k, n);
+    std::vector<std::int8_t> q(k * n);
+    std::vector<float> s(n);
+    vmo_quantize_int8_per_channel(w.data(), q.data(), s.data(), k, n);
+    const auto a = generate_activations(32, k);
+    Graph g;
+    auto ta = g.input({2, 16, (dim_t)k}, DataType::Float32);
+    auto tw = g.input({(dim_t)k, (dim_t)n}, DataType::Int8);
+    auto ts = g.input({(dim_t)n}, DataType::Float32);
+    auto tc = g.op(Op::QuantizedMatMul, ta, tw, ts);
+    REQUIRE(tc.shape() == shape_t({2, 16, (dim_t)n}));
+    auto exec = g.build(DeviceType::HIP);
+    ta.copy_from_host(as_bytes(a));
+    tw.copy_from_host(as_bytes(q));
+    ts.copy_from_host(as_bytes(s));
+    exec->execute();
+    std::vector<float> out(32 * n), ref(32 * n);
+    tc.copy_to_host(as_writeable_bytes(out));
+    vmo_qmm_2d_f32(a.data(), q.data(), s.data(), ref.data(), 32, k, n, 1, 0);
+    REQUIRE(max_abs_diff(out, ref) <= 1e-3f * max_abs(ref));
+}
+
+TEST_CASE("Float16 and BFloat16 dtype keys on HIP", "[gpu][quantization][dtype]") {
+    REQUIRE_HIP();
+    const std::size_t m = 2, k = 64, n = 64;
+    const auto w = generate_random_weights(k, n);
+    const auto a32 = generate_activations(m, k);
+    std::vector<std::int8_t> q(k * n);
+    std::vector<float> s32(n);
+    vmo_quantize_int8_per_channel(w.data(), q.data(), s32.data(), k, n);
+    for (DataType dt : {DataType::Float16, DataType::BFloat16}) {
+        for (bool f32_scale : {false, true}) {
+            std::vector<std::uint16_t> a16(m * k), s16(n);
+            for (std::size_t i = 0; i < a16.size(); ++i)
+                a16[i] = dt == DataType::Float16 ? vmo_f32_to_f16(a32[i]) : vmo_f32_to_bf16(a32[i]);
+            for (std::size_t j = 0; j < n; ++j)
+                s16[j] = dt == DataType::Float16 ? vmo_f32_to_f16(s32[j]) : vmo_f32_to_bf16(s32[j]);
+            Graph g;
+            auto ta = g.input({(dim_t)m, (dim_t)k}, dt);
+            auto tw = g.input({(dim_t)k, (dim_t)n}, DataType::Int8);
+            auto ts = g.input({(dim_t)n}, f32_scale ? DataType::Float32 : dt);
+            auto tc = g.op(Op::QuantizedMatMul, ta, tw, ts);
+            REQUIRE(tc.dtype() == dt);
+            auto exec = g.build(DeviceType::HIP);
+            ta.copy_from_host(as_bytes(a16));
+            tw.copy_from_host(as_bytes(q));
+            if (f32_scale) ts.copy_from_host(as_bytes(s32)); else ts.copy_from_host(as_bytes(s16));
+            exec->execute();
+            std::vector<std::uint16_t> out(m * n), ref(m * n);
+            tc.copy_to_host(as_writeable_bytes(out));
+            const int code = dt == DataType::Float16 ? VMO_F16 : VMO_BF16;
+            vmo_qmm_scalar_mixed(a16.data(), code, q.data(), f32_scale ? (const void*)s32.data() : (const void*)s16.data(),
+                                 f32_scale ? VMO_F32 : code, ref.data(), code, m, k, n, 1, 0);
+            for (std::size_t i = 0; i < out.size(); ++i) {
+                const float o = dt == DataType::Float16 ? vmo_f16_to_f32(out[i]) : vmo_bf16_to_f32(out[i]);
+                const float r = dt == DataType::Float16 ? vmo_f16_to_f32(ref[i]) : vmo_bf16_to_f32(ref[i]);
+                REQUIRE(std::isfinite(o));
+                // at most one half-precision ulp apart (summation order)
+                const float ulp = dt == DataType::Float16 ? 1.0f / 1024 : 1.0f / 128;
+                REQUIRE(std::abs(o - r) <= ulp * std::max(std::abs(r), 1e-3f) * 2.0f);
+            }
+        }
+    }
+}
+
+TEST_CASE("quantize_storage_int8 from a Float16 host source", "[gpu][quantization]") {
+    REQUIRE_HIP();
+    const std::size_t rows = 4, cols = 8;
+    std::vector<float16_t> f16(rows * cols);
+    for (std::size_t i = 0; i < f16.size(); ++i) f16[i] = float16_t(static_cast<float>(i + 1) * 0.1f);
+    TensorStorage st;
+    st.shape = {(dim_t)rows, (dim_t)cols};
+    st.dtype = DataType::Float16;
+    st.data = f16.data();
+    st.size_bytes = st.capacity_bytes = f16.size() * 2;
+    auto [q, s] = quantize_storage_int8(st, DeviceType::CPU);
+    REQUIRE(q && s && q->dtype == DataType::Int8 && s->dtype == DataType::Float32);
+    REQUIRE(q->device == DeviceType::CPU);
+    REQUIRE(q->shape == shape_t({(dim_t)rows, (dim_t)cols}) && s->shape == shape_t({(dim_t)cols}));
+    std::vector<float> w32(f16.size());
+    for (std::size_t i = 0; i < f16.size(); ++i) w32[i] = static_cast<float>(f16[i]);
+    std::vector<std::int8_t> q_ref(rows * cols);
+    std::vector<float> s_ref(cols);
+    vmo_quantize_int8_per_channel(w32.data(), q_ref.data(), s_ref.data(), rows, cols);
+    REQUIRE(std::memcmp(q->data, q_ref.data(), q_ref.size()) == 0);
+    REQUIRE(std::memcmp(s->data, s_ref.data(), s_ref.size() * 4) == 0);
+}
+
+TEST_CASE("HIP graph memory plan uses one device arena", "[gpu][memory]") {
+    REQUIRE_HIP();
+    Graph g;
+    auto x = g.input({1, 256}, DataType::Float32);
+    Tensor h = x;
+    std::vector<std::pair<Tensor, Tensor>> ws;
+    for (int i = 0; i < 5; ++i) {
+        auto w = g.input({256, 256}, DataType::Int8);
+        auto s = g.input({256}, DataType::Float32);
+        ws.push_back({w, s});
+        h = g.op(Op::QuantizedMatMul, h, w, s);
+    }
+    g.mark_output(h);
+    auto exec = g.build(DeviceType::HIP);
+    const auto& st = exec->memory_plan_stats();
+    REQUIRE(st.intermediate_tensor_count == 4);
+    REQUIRE(st.allocation_count == 1 + 1 + 10 + 1);  // arena + x + weights/scales + output
+    // run it: identity-like weights (code 127 on the diagonal, scale 1/127)
+    std::vector<std::int8_t> eye(256 * 256, 0);
+    for (int i = 0; i < 256; ++i) eye[i * 256 + i] = 127;
+    std::vector<float> sc(256, 1.0f / 127.0f);
+    for (auto& [w, s] : ws) {
+        w.copy_from_host(as_bytes(eye));
+        s.copy_from_host(as_bytes(sc));
+    }
+    const auto xv = normal(256, 9);
+    x.copy_from_host(as_bytes(xv));
+    exec->execute();
+    std::vector<float> out(256);
+    h.copy_to_host(as_writeable_bytes(out));
+    REQUIRE(max_abs_diff(out, xv) <= 1e-5f * max_abs(xv));
+}
+
+TEST_CASE("bind_input uses an external device buffer", "[gpu][api]") {
+    REQUIRE_HIP();
+    const std::size_t k = 128, n = 64;
+    const auto w = generate_random_weights(k, n);
+    std::vector<std::int8_t> q(k * n);
+    std::vector<float> s(n);
+    vmo_quantize_int8_per_channel(w.data(), q.data(), s.data(), k, n);
+    Graph g;
+    auto ta = g.input({1, (dim_t)k}, DataType::Float32);
+    auto tw = g.input({(dim_t)k, (dim_t)n}, DataType::Int8);
+    auto ts = g.input({(dim_t)n}, DataType::Float32);
+    auto tc = g.op(Op::QuantizedMatMul, ta, tw, ts);
+    auto exec = g.build(DeviceType::HIP);
+    void* dev = nullptr;
+    REQUIRE(vm_hip_malloc(&dev, k * 4) == 0);
+    std::shared_ptr<void> owner(dev, [](void* p) { vm_hip_free(p); });
+    const auto a = generate_activations(1, k);
+    REQUIRE(vm_hip_memcpy_h2d(dev, a.data(), k * 4, nullptr) == 0);
+    exec->bind_input(ta, ExternalBuffer{dev, k * 4, DeviceType::HIP, owner});
+    REQUIRE(ta.data() == dev);
+    tw.copy_from_host(as_bytes(q));
+    ts.copy_from_host(as_bytes(s));
+    exec->execute();
+    std::vector<float> out(n), ref(n);
+    tc.copy_to_host(as_writeable_bytes(out));
+    vmo_qmm_2d_f32(a.data(), q.data(), s.data(), ref.data(), 1, k, n, 1, 0);
+    REQUIRE(max_abs_diff(out, ref) < 1e-4f);
+    REQUIRE_THROWS_AS(exec->bind_input(ta, ExternalBuffer{dev, 4, DeviceType::HIP, owner}), std::invalid_argument);
+    REQUIRE_THROWS_AS(exec->bind_input(tc, ExternalBuffer{dev, k * 4, DeviceType::HIP, owner}), std::invalid_argument);
+}
+
+TEST_CASE("injected backend failures carry the reference's message format", "[gpu][failure]") {
+    REQUIRE_HIP();
+    Graph g;
+    auto ta = g.input({1, 64}, DataType::Float32);
+    auto tw = g.input({64, 32}, DataType::Int8);
+    auto ts = g.input({32}, DataType::Float32);
+    g.op(Op::QuantizedMatMul, ta, tw, ts);
+    auto exec = g.build(DeviceType::HIP);
+    for (const char* stage : {"launch", "sync"}) {
+        const std::string spec = std::string("HIP:QuantizedMatMul:") + stage;
+        ScopedEnv env("VELOMIND_FAIL_BACKEND", spec.c_str());
+        bool thrown = false;
+        try {
+            exec->execute();
+        } catch (const std::runtime_error& e) {
+            const std::string msg = e.what();
+            thrown = msg.find("QuantizedMatMul on HIP output shape=[1,32] at ") != std::string::npos &&
+                     msg.find("injected failure") != std::string::npos;
+        }
+        REQUIRE(thrown);
+    }
+    REQUIRE_NOTHROW(exec->execute());  // recovers once the injection is gone
+}
+
+TEST_CASE("concurrent build and execute on per-thread HIP streams", "[gpu][threads]") {
+    REQUIRE_HIP();
+    const std::size_t k = 512, n = 1024;
+    const auto w = normal(k * n, 21, 0.02f);
+    std::vector<std::int8_t> q(k * n);
+    std::vector<float> s(n);
+    vmo_quantize_int8_per_channel(w.data(), q.data(), s.data(), k, n);
+    std::atomic<int> ok{0};
+    std::vector<std::thread> threads;
+    for (int t = 0; t < 6; ++t) {
+        threads.emplace_back([&, t] {
+            try {
+                for (int it = 0; it < 5; ++it) {
+                    const std::size_t m = 1 + (t + it) % 4;
+                    const auto a = normal(m * k, 100 + t * 10 + it);
+                    const auto out = run_graph(DeviceType::HIP, QmmCase{m, k, n, QuantType::Int8, 0}, a, q, s);
+                    std::vector<float> ref(m * n);
+                    vmo_qmm_2d_f32(a.data(), q.data(), s.data(), ref.data(), m, k, n, 1, 0);
+                    if (max_abs_diff(out, ref) > 1e-5f * max_abs(ref)) return;
+                }
+                ++ok;
+            } catch (...) {
+            }
+        });
+    }
+    for (auto& th : threads) th.join();
+    REQUIRE(ok == 6);
+}

@@ -1,0 +1,72 @@
+// Compiled execution plan of a Graph: resolved kernels in topological order
+// plus the backend's execution context (for HIP: the stream).  The owning
+// Graph must outlive it.  Mirrors the reference's
+// include/velomind/executable.h:176-242.
+#pragma once
+
+#include <cstddef>
+#include <memory>
+#include <vector>
+
+#include "velomind/graph.h"
+#include "velomind/tensor.h"
+#include "velomind/tensor_storage.h"
+#include "velomind_core_export.h"
+
+namespace velomind {
+
+// An externally owned buffer bound to a graph input without a copy.
+struct ExternalBuffer {
+    void* data = nullptr;
+    std::size_t capacity_bytes = 0;
+    DeviceType device = DeviceType::CPU;
+    std::shared_ptr<void> owner;
+};
+
+class VELOMIND_CORE_EXPORT Executable {
+public:
+    using KernelFn = ::velomind::KernelFn;
+
+    struct CompiledNode {
+        KernelFn kernel = nullptr;
+        std::vector<pConstTensorStorage> inputs;
+        std::vector<pTensorStorage> outputs;
+        std::shared_ptr<const void> attrs;  // the node's OpDescriptor
+        std::vector<TensorStorage> input_metadata;
+        std::vector<TensorStorage> output_metadata;
+    };
+
+    struct Impl {
+        pConstGraph graph = nullptr;
+        std::weak_ptr<void> graph_lifetime;
+        DeviceType device = DeviceType::CPU;
+        std::vector<CompiledNode> topo;
+        MemoryPlanStats plan_stats;
+        // Backend execution context created by the device's context hook.
+        std::shared_ptr<void> device_context;
+    };
+
+    Executable() = default;
+    ~Executable();
+    Executable(const Executable&) = delete;
+    Executable& operator=(const Executable&) = delete;
+    Executable(Executable&&) noexcept;
+    Executable& operator=(Executable&&) noexcept;
+
+    // Runs every node in order; for GPU devices work is enqueued on the
+    // context's stream and the stream is synchronized before returning.
+    auto execute() -> void;
+    auto bind_input(Tensor tensor, ExternalBuffer external_buffer) -> void;
+    auto output(Tensor tensor) -> pTensorStorage;
+    auto output(Tensor tensor) const -> pConstTensorStorage;
+    auto memory_plan_stats() const noexcept -> const MemoryPlanStats&;
+    auto num_nodes() const -> std::size_t;
+    auto empty() const -> bool { return num_nodes() == 0; }
+
+private:
+    friend class Graph;
+    friend class internal::GraphCompiler;
+    std::unique_ptr<Impl> _impl;
+};
+
+}  // namespace velomind

@@ -1,0 +1,29 @@
+// HIP backend internals shared by its translation units.
+#pragma once
+
+#include <stdexcept>
+#include <string>
+
+#include "velomind/ops.h"
+#include "velomind/tensor_storage.h"
+#include "vm_hip.h"
+
+namespace velomind::backend::hip {
+
+// Stream of the HIP context active on this thread (nullptr = null stream).
+void* current_stream() noexcept;
+
+// "<op> on HIP output shape=[a,b] at <stage>" (the reference's CUDA
+// message format, src/cuda/ops/backend_error.h:15-23).
+std::string error_context(Op op, const TensorStorage& output, const char* stage);
+
+// Throws for a failed libvmhip status: std::invalid_argument for argument
+// errors, std::runtime_error otherwise; the message carries `context` and
+// vm_hip_last_error().
+[[noreturn]] void throw_status(int status, const std::string& context);
+
+inline void check_status(int status, const std::string& context) {
+    if (status != VM_HIP_OK) throw_status(status, context);
+}
+
+}  // namespace velomind::backend::hip

@@ -1,0 +1,76 @@
+// Op::QuantizedMatMul on DeviceType::HIP: the KernelFn adapter between the
+// VeloMind operator ABI and libvmhip's vm_hip_qmm.  Behaviour follows the
+// reference's adapters (src/cpu/ops/quantized_matmul.cpp:271-360,
+// src/cuda/ops/quantized_matmul.cu:203-266): m and k from A's last two
+// dimensions, n from B, leading batch dimensions of A/C folded into the row
+// count, one launch on the executing thread's stream.  A, B, scales and C
+// must be contiguous (graph tensors are; strided views are rejected with
+// std::invalid_argument rather than read wrongly).
+#include <cstdint>
+#include <string>
+#include <type_traits>
+#include <variant>
+
+#include "backend_hip/hip_runtime.h"
+#include "internal/registry/kernel.h"
+
+namespace velomind::backend::hip {
+
+namespace {
+
+template <typename T>
+constexpr int dtype_code() {
+    if constexpr (std::is_same_v<T, float>) return VM_HIP_DTYPE_F32;
+    if constexpr (std::is_same_v<T, float16_t>) return VM_HIP_DTYPE_F16;
+    if constexpr (std::is_same_v<T, bfloat16_t>) return VM_HIP_DTYPE_BF16;
+}
+
+template <typename TAct, typename TScale, typename TOut>
+void quantized_matmul_hip_impl(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const auto* a = in[0];
+    const auto* w = in[1];
+    const auto* s = in[2];
+    auto* c = out[0];
+    if (!a || !w || !s || !c) throw std::runtime_error("quantized_matmul hip: null storage");
+    const auto& desc = *static_cast<const OpDescriptor*>(attrs);
+    const auto& qa = std::get<QuantizedMatMulAttrs>(desc.attrs);
+
+    if (!a->is_contiguous() || !w->is_contiguous() || !s->is_contiguous() || !c->is_contiguous())
+        throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") +
+                                    ": strided operands are not supported on HIP");
+    const std::size_t rank = a->shape.size();
+    const std::int64_t k = a->shape[rank - 1];
+    const std::int64_t n = w->shape[1];
+    std::int64_t rows = 1;
+    for (std::size_t i = 0; i + 1 < c->shape.size(); ++i) rows *= c->shape[i];
+
+    const int qt = qa.quant_type == QuantType::Int4 ? VM_HIP_QUANT_INT4 : VM_HIP_QUANT_INT8;
+    const int status = vm_hip_qmm(a->data, dtype_code<TAct>(), static_cast<const std::int8_t*>(w->data), s->data,
+                                  dtype_code<TScale>(), c->data, dtype_code<TOut>(), rows, k, n, qt, qa.block_size,
+                                  current_stream());
+    if (status != VM_HIP_OK) {
+        const std::string last = vm_hip_last_error();
+        const char* stage = last.find(" at sync") != std::string::npos ? "sync" : "launch";
+        throw_status(status, error_context(Op::QuantizedMatMul, *c, stage));
+    }
+}
+
+}  // namespace
+
+VELOMIND_REGISTER_QUANTIZED_MATMUL(::velomind::DeviceType::HIP, ::velomind::DataType::Float32,
+                                   ::velomind::DataType::Float32, ::velomind::DataType::Float32,
+                                   quantized_matmul_hip_impl)
+VELOMIND_REGISTER_QUANTIZED_MATMUL(::velomind::DeviceType::HIP, ::velomind::DataType::Float16,
+                                   ::velomind::DataType::Float16, ::velomind::DataType::Float16,
+                                   quantized_matmul_hip_impl)
+VELOMIND_REGISTER_QUANTIZED_MATMUL(::velomind::DeviceType::HIP, ::velomind::DataType::Float16,
+                                   ::velomind::DataType::Float32, ::velomind::DataType::Float16,
+                                   quantized_matmul_hip_impl)
+VELOMIND_REGISTER_QUANTIZED_MATMUL(::velomind::DeviceType::HIP, ::velomind::DataType::BFloat16,
+                                   ::velomind::DataType::BFloat16, ::velomind::DataType::BFloat16,
+                                   quantized_matmul_hip_impl)
+VELOMIND_REGISTER_QUANTIZED_MATMUL(::velomind::DeviceType::HIP, ::velomind::DataType::BFloat16,
+                                   ::velomind::DataType::Float32, ::velomind::DataType::BFloat16,
+                                   quantized_matmul_hip_impl)
+
+}  // namespace velomind::backend::hip

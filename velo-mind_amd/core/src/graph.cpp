@@ -1,0 +1,237 @@
+// Graph construction, dead-code elimination and topological ordering
+// (the reference's src/graph.cpp), written for this build.
+#include "velomind/graph.h"
+
+#include <algorithm>
+#include <queue>
+#include <stdexcept>
+#include <unordered_map>
+
+#include "internal/graph_compiler.h"
+#include "internal/registry/kernel.h"
+#include "internal/registry/shape.h"
+#include "velomind/executable.h"
+
+namespace velomind {
+
+Graph::Graph(std::size_t initial_tensor_capacity, std::size_t initial_node_capacity)
+    : _lifetime(std::make_shared<int>(0)) {
+    _tensors.reserve(initial_tensor_capacity);
+    _nodes.reserve(initial_node_capacity);
+}
+
+Graph::~Graph() = default;
+
+auto Graph::reserve(std::size_t tensor_capacity, std::size_t node_capacity) -> void {
+    if (_built) throw std::logic_error("Graph::reserve: graph is already built");
+    if (tensor_capacity > _tensors.capacity()) _tensors.reserve(tensor_capacity);
+    if (node_capacity > _nodes.capacity()) _nodes.reserve(node_capacity);
+}
+
+auto Graph::tensor_storage_at(std::size_t i) const -> pConstTensorStorage {
+    return i < _tensors.size() ? _tensors[i].get() : nullptr;
+}
+auto Graph::tensor_storage_at(std::size_t i) -> pTensorStorage { return i < _tensors.size() ? _tensors[i].get() : nullptr; }
+auto Graph::shared_storage_at(std::size_t i) const -> std::shared_ptr<TensorStorage> {
+    return i < _tensors.size() ? _tensors[i] : nullptr;
+}
+
+auto Graph::is_input_tensor(std::size_t i) const noexcept -> bool {
+    const auto* s = tensor_storage_at(i);
+    if (!s) return false;
+    for (const auto& n : _nodes)
+        for (auto* o : n.outputs())
+            if (o == s) return false;
+    return true;
+}
+
+auto Graph::is_output_tensor(std::size_t i) const noexcept -> bool {
+    const auto* s = tensor_storage_at(i);
+    if (!s) return false;
+    if (_has_explicit_outputs) return std::find(_explicit_outputs.begin(), _explicit_outputs.end(), s) != _explicit_outputs.end();
+    if (is_input_tensor(i)) return false;
+    for (const auto& n : _nodes)
+        for (auto* in : n.inputs())
+            if (in == s) return false;
+    return true;
+}
+
+auto Graph::input(shape_t shape, DataType dtype) -> Tensor {
+    if (_built) throw std::logic_error("Graph::input: graph is already built");
+    auto s = std::make_shared<TensorStorage>();
+    s->shape = std::move(shape);
+    s->strides = default_strides(s->shape);
+    s->dtype = dtype;
+    s->size_bytes = storage_nbytes(*s);
+    s->capacity_bytes = s->size_bytes;
+    _tensors.push_back(std::move(s));
+    return Tensor{this, _tensors.size() - 1};
+}
+
+auto Graph::input(std::shared_ptr<TensorStorage> storage) -> Tensor {
+    if (_built) throw std::logic_error("Graph::input: graph is already built");
+    if (!storage) throw std::invalid_argument("Graph::input: null storage");
+    if (storage->size_bytes < storage_nbytes(*storage))
+        throw std::invalid_argument("Graph::input: storage capacity is smaller than tensor");
+    if (storage->strides.empty()) storage->strides = default_strides(storage->shape);
+    if (storage->capacity_bytes == 0) storage->capacity_bytes = storage->size_bytes;
+    _tensors.push_back(std::move(storage));
+    return Tensor{this, _tensors.size() - 1};
+}
+
+auto Graph::_op_impl(OpDescriptor desc, std::vector<pConstTensorStorage> inputs) -> Tensor {
+    if (std::holds_alternative<NoAttrs>(desc.attrs)) desc.attrs = default_op_attrs(desc.op);
+    // Shapes and dtypes come only from the signature registry.
+    auto sig = internal::op_signature(desc.op, inputs, desc.attrs);
+    auto out = std::make_shared<TensorStorage>();
+    out->shape = std::move(sig.shape);
+    out->strides = default_strides(out->shape);
+    out->dtype = sig.dtype;
+    out->size_bytes = storage_nbytes(*out);
+    out->capacity_bytes = out->size_bytes;
+    _tensors.push_back(std::move(out));
+    Node node;
+    node._op = std::move(desc);
+    node._inputs = std::move(inputs);
+    node._outputs = {_tensors.back().get()};
+    _nodes.push_back(std::move(node));
+    return Tensor{this, _tensors.size() - 1};
+}
+
+auto Graph::mark_output(Tensor t) -> void {
+    if (_built) throw std::logic_error("Graph::mark_output: graph is already built");
+    if (t.graph() != this || t.storage() == nullptr)
+        throw std::invalid_argument("Graph::mark_output: invalid or foreign tensor handle");
+    _has_explicit_outputs = true;
+    if (std::find(_explicit_outputs.begin(), _explicit_outputs.end(), t.storage()) == _explicit_outputs.end())
+        _explicit_outputs.push_back(t.storage());
+}
+
+auto Graph::set_outputs(std::vector<Tensor> outputs) -> void {
+    if (_built) throw std::logic_error("Graph::set_outputs: graph is already built");
+    for (const auto& t : outputs)
+        if (t.graph() != this || t.storage() == nullptr)
+            throw std::invalid_argument("Graph::set_outputs: invalid or foreign tensor handle");
+    _explicit_outputs.clear();
+    _has_explicit_outputs = !outputs.empty();
+    for (const auto& t : outputs)
+        if (std::find(_explicit_outputs.begin(), _explicit_outputs.end(), t.storage()) == _explicit_outputs.end())
+            _explicit_outputs.push_back(t.storage());
+}
+
+auto Graph::outputs() const -> std::vector<Tensor> {
+    std::vector<Tensor> res;
+    auto* self = const_cast<Graph*>(this);
+    if (_has_explicit_outputs) {
+        for (auto* s : _explicit_outputs)
+            for (std::size_t i = 0; i < _tensors.size(); ++i)
+                if (_tensors[i].get() == s) {
+                    res.emplace_back(self, i);
+                    break;
+                }
+    } else {
+        for (std::size_t i = 0; i < _tensors.size(); ++i)
+            if (is_output_tensor(i)) res.emplace_back(self, i);
+    }
+    return res;
+}
+
+// Nodes reachable backwards from the explicit outputs (all nodes if none).
+auto Graph::_compute_required_nodes() const -> std::vector<bool> {
+    if (!_has_explicit_outputs) return std::vector<bool>(_nodes.size(), true);
+    std::unordered_map<pConstTensorStorage, std::size_t> producer;
+    for (std::size_t i = 0; i < _nodes.size(); ++i)
+        for (auto* o : _nodes[i].outputs()) producer[o] = i;
+    std::vector<bool> req(_nodes.size(), false);
+    std::vector<std::size_t> stack;
+    for (auto* s : _explicit_outputs) {
+        auto it = producer.find(s);
+        if (it != producer.end() && !req[it->second]) {
+            req[it->second] = true;
+            stack.push_back(it->second);
+        }
+    }
+    while (!stack.empty()) {
+        const std::size_t u = stack.back();
+        stack.pop_back();
+        for (auto* in : _nodes[u].inputs()) {
+            auto it = producer.find(in);
+            if (it != producer.end() && !req[it->second]) {
+                req[it->second] = true;
+                stack.push_back(it->second);
+            }
+        }
+    }
+    return req;
+}
+
+// Kahn's algorithm over the required nodes, in insertion order among ready
+// nodes; throws on a cycle.
+auto Graph::_topological_order() const -> std::vector<pConstNode> {
+    const auto req = _compute_required_nodes();
+    std::unordered_map<pConstTensorStorage, std::size_t> producer;
+    for (std::size_t i = 0; i < _nodes.size(); ++i)
+        for (auto* o : _nodes[i].outputs()) producer[o] = i;
+    std::vector<std::size_t> indeg(_nodes.size(), 0);
+    std::vector<std::vector<std::size_t>> users(_nodes.size());
+    std::size_t active = 0;
+    for (std::size_t v = 0; v < _nodes.size(); ++v) {
+        if (!req[v]) continue;
+        ++active;
+        std::vector<std::size_t> deps;
+        for (auto* in : _nodes[v].inputs()) {
+            auto it = producer.find(in);
+            if (it != producer.end() && req[it->second]) deps.push_back(it->second);
+        }
+        std::sort(deps.begin(), deps.end());
+        deps.erase(std::unique(deps.begin(), deps.end()), deps.end());
+        indeg[v] = deps.size();
+        for (std::size_t u : deps) users[u].push_back(v);
+    }
+    std::queue<std::size_t> ready;
+    for (std::size_t v = 0; v < _nodes.size(); ++v)
+        if (req[v] && indeg[v] == 0) ready.push(v);
+    std::vector<pConstNode> order;
+    order.reserve(active);
+    while (!ready.empty()) {
+        const std::size_t u = ready.front();
+        ready.pop();
+        order.push_back(&_nodes[u]);
+        for (std::size_t v : users[u])
+            if (--indeg[v] == 0) ready.push(v);
+    }
+    if (order.size() != active) throw std::invalid_argument("Graph::build: cycle detected in graph");
+    return order;
+}
+
+auto Graph::validate(DeviceType device) const -> void {
+    if (_built) throw std::logic_error("Graph::validate: graph is already built");
+    if (static_cast<std::size_t>(device) >= MAX_DEVICE_TYPES) throw std::invalid_argument("Graph::validate: invalid device");
+    for (const auto& s : _tensors) {
+        if (s->size_bytes < storage_nbytes(*s)) throw std::invalid_argument("Graph::validate: invalid tensor capacity");
+        if (s->data != nullptr && s->device != device)
+            throw std::invalid_argument("Graph::validate: populated storage belongs to another device");
+    }
+    const auto req = _compute_required_nodes();
+    for (std::size_t i = 0; i < _nodes.size(); ++i) {
+        if (!req[i]) continue;
+        const auto& n = _nodes[i];
+        if (n.outputs().empty()) throw std::invalid_argument("Graph::validate: node has no outputs");
+        // Metadata may have changed through shared storages: re-derive.
+        const auto sig = internal::op_signature(n.op().op, n.inputs(), n.op().attrs);
+        const auto* out = n.outputs().front();
+        if (sig.shape != out->shape || sig.dtype != out->dtype)
+            throw std::invalid_argument("Graph::validate: output metadata no longer matches signature");
+        std::vector<DataType> dtypes;
+        for (auto* in : n.inputs()) dtypes.push_back(in->dtype);
+        if (!internal::resolve_op_kernel(n.op().op, dtypes, out->dtype, device))
+            throw std::invalid_argument(std::string("Graph::validate: unsupported kernel for ") + op_name(n.op().op));
+    }
+    (void)_topological_order();
+}
+
+auto Graph::build(DeviceType device) -> std::unique_ptr<Executable> {
+    return internal::GraphCompiler::compile(*this, device);
+}
+
+}  // namespace velomind

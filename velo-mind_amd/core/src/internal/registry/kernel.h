@@ -1,0 +1,70 @@
+// Per-device operator kernel table keyed by (op, input dtypes, output
+// dtype), filled at static-initialisation time by backend registration
+// macros and read-only afterwards (the reference's
+// src/internal/registry/kernel.h:15-43 and :192-204).
+#pragma once
+
+#include "internal/registry/macros.h"
+
+#include <array>
+#include <cstddef>
+#include <span>
+#include <vector>
+
+#include "velomind/dtype.h"
+#include "velomind/executable.h"
+#include "velomind/ops.h"
+#include "velomind/types.h"
+
+namespace velomind::internal {
+
+// Up to four input dtypes; num_inputs says how many take part in matching.
+struct KernelDtypeKey {
+    std::array<DataType, 4> input_dtypes{};
+    std::size_t num_inputs = 0;
+    DataType output_dtype = DataType::Float32;
+};
+
+auto operator==(const KernelDtypeKey& a, const KernelDtypeKey& b) noexcept -> bool;
+
+struct KernelEntry {
+    KernelDtypeKey key;
+    Executable::KernelFn fn = nullptr;
+};
+
+auto op_kernels(DeviceType device) -> std::array<std::vector<KernelEntry>, MAX_OPS>&;
+
+// Exact-match lookup; nullptr when no kernel is registered.
+auto resolve_op_kernel(Op op, std::span<const DataType> input_dtypes, DataType output_dtype, DeviceType device)
+    -> Executable::KernelFn;
+
+auto register_op_kernel(DeviceType device, Op op, KernelDtypeKey key, Executable::KernelFn fn) -> void;
+
+template <DataType D> struct dtype_to_type;
+template <> struct dtype_to_type<DataType::Float32> { using type = float; };
+template <> struct dtype_to_type<DataType::Int32> { using type = std::int32_t; };
+template <> struct dtype_to_type<DataType::Int8> { using type = std::int8_t; };
+template <> struct dtype_to_type<DataType::Bool> { using type = bool; };
+template <> struct dtype_to_type<DataType::Float16> { using type = float16_t; };
+template <> struct dtype_to_type<DataType::BFloat16> { using type = bfloat16_t; };
+template <DataType D> using dtype_t = typename dtype_to_type<D>::type;
+
+}  // namespace velomind::internal
+
+
+// Registers FN for (DEVICE, OP_ENUM, KEY) during static initialisation.
+#define VELOMIND_REGISTER_OP_KERNEL(DEVICE, OP_ENUM, KEY, ...)                                    \
+    [[maybe_unused]] static const bool VELOMIND_CONCAT_(_velomind_kr_, __LINE__) = [] {          \
+        ::velomind::internal::register_op_kernel((DEVICE), (OP_ENUM), (KEY), (__VA_ARGS__));     \
+        return true;                                                                             \
+    }();
+
+// QuantizedMatMul: inputs (A: TA, B_q: Int8, scales: TSCALE) -> TC, with
+// NAME a template over the three element types.
+#define VELOMIND_REGISTER_QUANTIZED_MATMUL(DEVICE, TA_DT, TSCALE_DT, TC_DT, NAME)                 \
+    VELOMIND_REGISTER_OP_KERNEL(                                                                 \
+        (DEVICE), ::velomind::Op::QuantizedMatMul,                                               \
+        (::velomind::internal::KernelDtypeKey{{(TA_DT), ::velomind::DataType::Int8, (TSCALE_DT)}, \
+                                              3, (TC_DT)}),                                       \
+        (&NAME<::velomind::internal::dtype_t<TA_DT>, ::velomind::internal::dtype_t<TSCALE_DT>,    \
+               ::velomind::internal::dtype_t<TC_DT>>))

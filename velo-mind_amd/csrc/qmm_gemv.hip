@@ -109,7 +109,6 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const int split = blockIdx.y;
     const int splits = gridDim.y;
     const int col0 = tile * kTileCols + (lane % L) * kVec;
-    const bool col_ok = col0 < n;
 
     const int total_chunks = (k + kChunkK - 1) / kChunkK;
     const int byte_rows = CS::kInt4 ? (k + 1) / 2 : k;
