@@ -125,6 +125,19 @@ def per_launch_durations(H, wl: Workload, reps: int) -> dict:
     return {key: sums[key] / counts[key] for key in sums}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the GEMV from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the counters'
+    reading of a plain copy of known size), or (None, None)."""
+    path = os.path.join(ROOT, "profiles", "gemv_int4_tinyllama_decode_sweep.json")
+    try:
+        with open(path) as f:
+            prof = json.load(f)
+        return int(prof["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def cpu_baseline(target_s: float) -> dict:
     """Oracle scalar INT4 GEMV (reference CPU algorithm), one pinned core."""
     import oracle as O
@@ -170,6 +183,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--event-reps", type=int, default=5, help="eager passes with per-launch events")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run ten 64 MiB device-to-device copies (rocprofv3 counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; --gpus must be 1 (no multi-GPU path is built)",
@@ -180,6 +195,14 @@ def main() -> int:
 
     H.load()
     stream = H.Stream()
+    if args.calibrate_copy:
+        src, dst = H.DeviceBuffer(64 << 20), H.DeviceBuffer(64 << 20)
+        lib = H.open_library()
+        for _ in range(10):
+            H.check(lib.vm_hip_memcpy_d2d(dst.ptr, src.ptr, 64 << 20, stream.handle))
+        stream.synchronize()
+        log("bench: calibration copies done (10 x 64 MiB)")
+        return 0
     log("bench: packing weights on the GPU")
     wl = Workload(H, stream)
     log(f"bench: {len(wl.calls)} GEMVs per step, {wl.bytes_per_step / 1e6:.1f} MB per step")
@@ -234,6 +257,7 @@ def main() -> int:
         kern_ms += ms * count
     achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
     launches = len(wl.calls)
+    traffic, traffic_src = measured_traffic()
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -271,7 +295,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "kernel": "qmm_gemv_kernel<INT4>",
             "avg_kernel_us": round(kern_ms / launches * 1e3, 3),
             "algo_bytes_per_launch": round(kern_bytes / launches),

@@ -1,0 +1,57 @@
+"""Every instantiated GEMV kernel shape, forced through the tuning override
+(VELOMIND_GEMV_CFG="L,W,S"), against the oracle.
+
+The automatic config rule only reaches a few (L, W, S) combinations for the
+shapes of the other tests; this covers the rest: all lane widths L (16-column
+groups per row segment), wave counts W, split counts S (with a partial last
+split), 1/2/4 activation rows, the three weight kinds, a partial last tile and
+more than eight tiles (so the XCD tile renumbering and its identity tail both
+run).  Tolerance: the fp32 GEMV bound of 1e-5 * max|ref|.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+# (L, W) pairs instantiated in velo-mind_amd/csrc/qmm_gemv.hip (kShapes).
+SHAPES = [(1, 4), (2, 4), (2, 8), (4, 4), (4, 8), (8, 4), (8, 8), (16, 4), (16, 8), (16, 16)]
+TOL_GEMV = 1e-5
+
+
+def _check(out, ref):
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(out.astype(np.float64) - ref).max()
+    bound = TOL_GEMV * max(np.abs(ref).max(), 1e-30)
+    assert err <= bound, f"max abs err {err:.3e} > {bound:.3e}"
+
+
+@pytest.mark.parametrize("kind", ["int8", "int8_block", "int4"])
+@pytest.mark.parametrize("L,W", SHAPES)
+def test_forced_config(hip, monkeypatch, L, W, kind):
+    k = 1000                      # 125 chunks of 8: splits of 3 leave a short last split
+    n = 16 * L * 11 - 16 * (L // 2)  # 11 tiles, the last one partial (L >= 2)
+    rng = np.random.default_rng(L * 100 + W)
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    if kind == "int8":
+        q, s = O.quantize_int8(w)
+        qt, block, oq = hip.QUANT_INT8, 0, O.QUANT_INT8
+    elif kind == "int8_block":
+        q = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        s = rng.random(((k + 31) // 32, n)).astype(np.float32) * 0.01
+        qt, block, oq = hip.QUANT_INT8, 32, O.QUANT_INT8
+    else:
+        q, s = O.quantize_int4(w, 32)
+        qt, block, oq = hip.QUANT_INT4, 32, O.QUANT_INT4
+    for m in (1, 2, 4):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        ref = O.qmm(x, q.view(np.int8), s, k, oq, block)
+        for S in (1, 3, 4):
+            monkeypatch.setenv("VELOMIND_GEMV_CFG", f"{L},{W},{S}")
+            print(f"case L={L} W={W} S={S} kind={kind} m={m} k={k} n={n}", flush=True)
+            out = hip.run_qmm(x, q, s, k, qt, block)
+            _check(out, ref)
+    monkeypatch.delenv("VELOMIND_GEMV_CFG")

@@ -16,8 +16,10 @@
 //               (atomic ticket) adds the splits' partials in split order, so
 //               results do not depend on scheduling
 //
-// Reduction: row groups of a wave combine with xor shuffles, the waves of
-// a workgroup through LDS, splits through the per-stream workspace.  The
+// Reduction: row groups of a wave combine with VALU cross-lane operations
+// (DPP row rotations inside 16-lane rows, then the gfx950 permlane16/32
+// swaps across rows and wave halves), the waves of a workgroup through LDS,
+// splits through the per-stream workspace.  The
 // split handoff uses agent-scope atomic stores/loads (coherent across XCDs,
 // `sc1`) for the partials: each wave waits for its partial stores to be
 // acknowledged (s_waitcnt) before the barrier that precedes the ticket
@@ -45,6 +47,7 @@ namespace {
 constexpr int kChunkK = 8;    // logical K rows per chunk
 constexpr int kVec = 16;      // columns per lane
 constexpr int kMaxSplits = 32;
+constexpr int kStageBatch = 4;  // activation loads in flight per thread while staging
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -76,6 +79,41 @@ __device__ __forceinline__ void coherent_store(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// v rotated right by `off` lanes inside each 16-lane row (DPP row_ror).
+__device__ __forceinline__ float dpp_row_ror(float v, int off) {
+    const int ctrl = 0x120 | off;  // row_ror:off, off in 1..15
+    int r = 0;
+    switch (ctrl) {
+        case 0x121: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false); break;
+        case 0x122: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xf, 0xf, false); break;
+        case 0x124: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false); break;
+        default: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false); break;
+    }
+    return __int_as_float(r);
+}
+
+// v_permlane16_swap_b32 exchanges the odd 16-lane rows of `a` with the even
+// rows of `b`; the sum of the two results holds, in even rows, a's row pair
+// sum and, in odd rows, b's.  (The results are read through memcpy: element
+// access on the builtin's returned pair reads the first element twice with
+// this compiler.)
+__device__ __forceinline__ float swap_rows_add(float a, float b) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    unsigned q[2];
+    __builtin_memcpy(q, &p, sizeof q);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+// v_permlane32_swap_b32: the upper 32 lanes of `a` trade places with the
+// lower 32 lanes of `b`; the sum holds a's half sum in lanes 0..31 and b's
+// in lanes 32..63.
+__device__ __forceinline__ float swap_halves_add(float a, float b) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    unsigned q[2];
+    __builtin_memcpy(q, &p, sizeof q);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // Codes and scales of one chunk for one lane.
 template <int KIND>
 struct Chunk {
@@ -89,23 +127,32 @@ template <int KIND, int MR, int L, int W>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
     float* __restrict__ c, int m, int k, int n, int block_size, int chunks_per_split,
-    uint32_t code_bytes, uint32_t scale_bytes, int blk_shift, float* __restrict__ partials,
-    unsigned* __restrict__ counters) {
+    uint32_t code_bytes, uint32_t scale_bytes, uint32_t a_bytes, int a_vec, int blk_shift,
+    float* __restrict__ partials, unsigned* __restrict__ counters) {
     using CS = ChunkShape<KIND>;
     constexpr int G = 64 / L;            // row groups per wave
     constexpr int RG = W * G;            // row groups per workgroup
     constexpr int kTileCols = kVec * L;
 
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     float* xs = smem;                                     // [MR][chunks_per_split * 8]
     const int xs_len = chunks_per_split * kChunkK;
     float* red = smem + MR * xs_len;                      // [W][MR][kTileCols]
+    float* spare = red + W * MR * kTileCols;              // [4], write-only
     __shared__ unsigned ticket;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int rg = wave * G + lane / L;                   // row group in the workgroup
-    const int tile = blockIdx.x;
+    // Workgroups are dispatched to the 8 XCDs round-robin by linear id, and
+    // each XCD has its own L2.  Tiles are renumbered so that each XCD owns a
+    // contiguous run of them: neighbouring tiles share 128-byte code and scale
+    // lines, which are then fetched into one L2 instead of several.
+    int tile = blockIdx.x;
+    {
+        const int full = static_cast<int>(gridDim.x) & ~7;
+        if (tile < full) tile = (tile & 7) * (full >> 3) + (tile >> 3);
+    }
     const int split = blockIdx.y;
     const int splits = gridDim.y;
     const int col0 = tile * kTileCols + (lane % L) * kVec;
@@ -210,15 +257,67 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         }
     };
 
-    // Issue the first chunk's loads, then stage this split's activations.
+    // Issue the first chunk's loads, then stage this split's activations
+    // with kStageBatch buffer loads in flight per thread before the first
+    // LDS write (one memory round trip for up to 4 * 4 * W * 64 elements).  Loads outside a row's
+    // [0, k) use an offset past the buffer and read zeros.  With k % 4 == 0
+    // and a 16-byte aligned A (a_vec) each load covers four elements that
+    // all lie inside one row; otherwise each covers one element.
     Chunk<KIND> ca, cb;
     int ch = c_begin + rg;
     load_chunk(ch, ca);
 
-    for (int i = threadIdx.x; i < MR * xs_len; i += W * 64) {
-        const int r = i / xs_len;
-        const int kk = k_begin + (i - r * xs_len);
-        xs[i] = (r < m && kk < k) ? a[static_cast<int64_t>(r) * k + kk] : 0.0f;
+    {
+        const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
+        constexpr int T = W * 64;
+        if (a_vec) {
+            const int q_per_row = xs_len / 4;  // xs_len is a multiple of 8
+            const int q_total = MR * q_per_row;
+            for (int q0 = threadIdx.x; q0 < q_total; q0 += kStageBatch * T) {
+                u32x4 t[kStageBatch];
+#pragma unroll
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int q = q0 + u * T;
+                    int r = 0;  // q / q_per_row for MR <= 4, without a division
+#pragma unroll
+                    for (int i = 1; i < MR; ++i) r += q >= i * q_per_row ? 1 : 0;
+                    const int kk = k_begin + 4 * (q - r * q_per_row);
+                    const uint32_t off = (q < q_total && r < m && kk < k)
+                                             ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u
+                                             : a_bytes;
+                    t[u] = buffer_load16(ars, off);
+                }
+                // Unconditional writes (surplus ones go to a spare LDS slot)
+                // keep the compiler from sinking loads into per-write branches.
+#pragma unroll
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int q = q0 + u * T;
+                    *reinterpret_cast<u32x4*>(q < q_total ? xs + 4 * q : spare) = t[u];
+                }
+            }
+        } else {
+            const int e_total = MR * xs_len;
+            for (int e0 = threadIdx.x; e0 < e_total; e0 += kStageBatch * T) {
+                uint32_t t[kStageBatch];
+#pragma unroll
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int e = e0 + u * T;
+                    int r = 0;
+#pragma unroll
+                    for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
+                    const int kk = k_begin + (e - r * xs_len);
+                    const uint32_t off = (e < e_total && r < m && kk < k)
+                                             ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u
+                                             : a_bytes;
+                    t[u] = __builtin_amdgcn_raw_buffer_load_b32(ars, static_cast<int>(off), 0, 0);
+                }
+#pragma unroll
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int e = e0 + u * T;
+                    *(e < e_total ? xs + e : spare) = __uint_as_float(t[u]);
+                }
+            }
+        }
     }
     __syncthreads();
 
@@ -241,20 +340,40 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     }
     if (iters & 1) compute_chunk(ca, ch, total);
 
-    // Row groups of a wave: lanes l and l ^ (L * 2^t) hold the same columns.
+    // Row groups of a wave (lanes that agree in lane % L) are summed with
+    // VALU cross-lane operations, then each wave leaves one copy of its
+    // tile's sums in LDS for the cross-wave step.
+    static_assert(L == 1 || L == 2 || L == 4 || L == 8 || L == 16, "L must divide a 16-lane row");
+    {
+        // 1. inside each 16-lane row: rotations by L, 2L, .., 8 (DPP row_ror)
 #pragma unroll
-    for (int off = L; off < 64; off <<= 1)
+        for (int off = L; off < 16; off <<= 1)
+#pragma unroll
+            for (int i = 0; i < MR; ++i)
+#pragma unroll
+                for (int j = 0; j < kVec; ++j) total[i][j] += dpp_row_ror(total[i][j], off);
+        // 2. row pairs: swapping columns j and j + 8 leaves even rows with
+        //    the sum of column j and odd rows with the sum of column j + 8
+        float h[MR][8];
 #pragma unroll
         for (int i = 0; i < MR; ++i)
 #pragma unroll
-            for (int j = 0; j < kVec; ++j) total[i][j] += __shfl_xor(total[i][j], off, 64);
-
-    // Waves of the workgroup through LDS.
-    if (lane < L) {
+            for (int j = 0; j < 8; ++j) h[i][j] = swap_rows_add(total[i][j], total[i][j + 8]);
+        // 3. wave halves: columns j and j + 4 of step 2, same pattern
+        float z[MR][4];
 #pragma unroll
         for (int i = 0; i < MR; ++i)
 #pragma unroll
-            for (int j = 0; j < kVec; ++j) red[(wave * MR + i) * kTileCols + lane * kVec + j] = total[i][j];
+            for (int j = 0; j < 4; ++j) z[i][j] = swap_halves_add(h[i][j], h[i][j + 4]);
+        // lane holds columns 8 * row-parity + 4 * half + (0..3) of its
+        // 16-column group lane % L; one lane per group and row writes.
+        if ((lane & 15) < L) {
+            const int cc = (lane & 15) * kVec + 8 * ((lane >> 4) & 1) + 4 * (lane >> 5);
+#pragma unroll
+            for (int i = 0; i < MR; ++i)
+                *reinterpret_cast<float4*>(red + (wave * MR + i) * kTileCols + cc) =
+                    make_float4(z[i][0], z[i][1], z[i][2], z[i][3]);
+        }
     }
     __syncthreads();
 
@@ -328,46 +447,118 @@ struct GemvConfig {
 
 int mr_for(int m) { return m <= 1 ? 1 : (m <= 2 ? 2 : 4); }
 
-// Picks lanes-per-segment, waves and splits for a shape.  Measured on
-// MI355X over the TinyLlama-1.1B and SmolLM2 shapes: 8 lanes per row segment
-// (128-column tiles) is best everywhere; about 200 workgroups with at least
-// 16 chunks per split balances split-K round trips against per-wave work;
-// 8 waves pay off once a split holds more than 32 chunks.
+// Largest wave count whose register budget (512 / W * 4 VGPRs per lane)
+// holds the kernel without spilling: MR x 16 accumulators, two chunks of
+// codes and scales in flight.
+constexpr int max_waves(int kind, int mr) {
+    return (kind == 0 && mr == 1) ? 16 : (kind == 1 && mr == 4) ? 4 : 8;
+}
+
+// (L, W) pairs the kernel is instantiated for.
+constexpr int kShapes[][2] = {{1, 4}, {2, 4}, {2, 8}, {4, 4}, {4, 8}, {8, 4}, {8, 8}, {16, 4}, {16, 8}, {16, 16}};
+
+bool instantiated(int L, int W) {
+    for (const auto& lw : kShapes)
+        if (lw[0] == L && lw[1] == W) return true;
+    return false;
+}
+
+struct Geometry {
+    int tiles, cps, splits, row_groups, iters, wgs;
+    long lds_bytes;
+};
+
+Geometry geometry(int mr, int k, int n, int L, int W, int S) {
+    Geometry g{};
+    const int chunks = (k + kChunkK - 1) / kChunkK;
+    g.tiles = (n + kVec * L - 1) / (kVec * L);
+    g.cps = (chunks + S - 1) / S;
+    g.splits = (chunks + g.cps - 1) / g.cps;
+    g.row_groups = W * 64 / L;
+    g.iters = (g.cps + g.row_groups - 1) / g.row_groups;
+    g.wgs = g.tiles * g.splits;
+    g.lds_bytes = (static_cast<long>(mr) * g.cps * kChunkK + static_cast<long>(W) * mr * kVec * L + 4) * 4;
+    return g;
+}
+
+GemvConfig make_config(int mr, int k, int n, int L, int W, int S) {
+    const Geometry g = geometry(mr, k, n, L, W, S);
+    GemvConfig cfg;
+    cfg.L = L;
+    cfg.W = W;
+    cfg.splits = g.splits;
+    cfg.chunks_per_split = g.cps;
+    return cfg;
+}
+
+constexpr long kLdsBudget = 60 * 1024;
+
+// Picks lanes-per-segment L, waves W and K splits S for a shape.  The rule
+// follows a sweep of every instantiated (L, W) and S in 1..16 over the
+// TinyLlama-1.1B INT4 and SmolLM2 INT8 decode shapes on MI355X, where it
+// comes within 1% of the per-shape best in total:
+//   - latency-bound shapes (every row group needs at most one chunk with
+//     16- or 32-column tiles and no K split, at most 256 workgroups) run
+//     unsplit on narrow tiles: the split-K handoff costs three memory round
+//     trips, more than the narrow tiles' extra cache-line requests;
+//   - wide outputs (N >= 192 * 128) run unsplit on 128- or 256-column tiles,
+//     about one workgroup per CU, each row group streaming several chunks;
+//   - everything else splits K (S >= 2) so that each row group holds one
+//     chunk, with as many workgroups as fit one per CU (<= 256), then the
+//     fewest splits.
+// The config depends only on the shape, so results are reproducible.
 GemvConfig choose_config(int kind, int m, int k, int n) {
     (void)kind;
     const int mr = mr_for(m);
-    const int total_chunks = (k + kChunkK - 1) / kChunkK;
+    const int chunks = (k + kChunkK - 1) / kChunkK;
+    const int w_max = max_waves(kind, mr);
     GemvConfig cfg;
-    cfg.L = 8;
-    const int tiles = (n + kVec * cfg.L - 1) / (kVec * cfg.L);
-    int S = 1;
-    while (S * 2 <= 16 && S * 2 * tiles <= 200) S *= 2;
-    while (S > 1 && (total_chunks + S - 1) / S < 16) S /= 2;
-    int cps = (total_chunks + S - 1) / S;
-    cfg.W = cps > 32 ? 8 : 4;
-    // Activations of one split and the cross-wave buffer share 60 KB of LDS.
-    while (S < kMaxSplits &&
-           (static_cast<long>(mr) * cps * kChunkK + static_cast<long>(cfg.W) * mr * kVec * cfg.L) * 4 > 60 * 1024) {
-        S *= 2;
-        cps = (total_chunks + S - 1) / S;
+    bool found = false;
+
+    for (int L : {1, 2}) {
+        const Geometry g = geometry(mr, k, n, L, 4, 1);
+        if (chunks <= g.row_groups && g.tiles <= 256 && g.lds_bytes <= kLdsBudget) {
+            cfg = make_config(mr, k, n, L, 4, 1);
+            found = true;
+            break;
+        }
     }
-    cfg.chunks_per_split = cps;
-    cfg.splits = (total_chunks + cps - 1) / cps;
+    if (!found && n >= 192 * 128) {
+        const int L = (n + 127) / 128 <= 256 ? 8 : 16;
+        const int W = std::min(L, w_max);
+        int S = 1;
+        while (S < kMaxSplits && geometry(mr, k, n, L, W, S).lds_bytes > kLdsBudget) S *= 2;
+        cfg = make_config(mr, k, n, L, W, S);
+        found = true;
+    }
+    if (!found) {
+        // (iters, -workgroups, splits) ascending among configs within the
+        // LDS budget, preferring those with at most 256 workgroups.
+        long best_key = 0;
+        for (const auto& lw : kShapes) {
+            const int L = lw[0], W = lw[1];
+            if (L < 2 || L > 8 || W > std::min(8, w_max)) continue;
+            for (int S = 2; S <= kMaxSplits; S *= 2) {
+                const Geometry g = geometry(mr, k, n, L, W, S);
+                if (g.splits != S || g.lds_bytes > kLdsBudget) continue;
+                const long over = g.wgs > 256 ? 1 : 0;
+                const long key = ((over * 64 + std::min(g.iters, 63)) * 4096 + (4095 - std::min(g.wgs, 4095))) * 64 + S;
+                if (!found || key < best_key) {
+                    best_key = key;
+                    cfg = make_config(mr, k, n, L, W, S);
+                    found = true;
+                }
+            }
+        }
+    }
+    if (!found) cfg = make_config(mr, k, n, 8, 4, kMaxSplits);
 
     // Tuning override for measurement sweeps: VELOMIND_GEMV_CFG="L,W,S".
     if (const char* env = std::getenv("VELOMIND_GEMV_CFG")) {
         int L = 0, W = 0, Sx = 0;
-        if (std::sscanf(env, "%d,%d,%d", &L, &W, &Sx) == 3 && (L == 8 || L == 16 || L == 64) &&
-            (W == 4 || W == 8) && Sx >= 1 && Sx <= kMaxSplits) {
-            const int c2 = (total_chunks + Sx - 1) / Sx;
-            const long lds = (static_cast<long>(mr) * c2 * kChunkK + static_cast<long>(W) * mr * kVec * L) * 4;
-            if (lds <= 60 * 1024) {
-                cfg.L = L;
-                cfg.W = W;
-                cfg.chunks_per_split = c2;
-                cfg.splits = (total_chunks + c2 - 1) / c2;
-            }
-        }
+        if (std::sscanf(env, "%d,%d,%d", &L, &W, &Sx) == 3 && instantiated(L, W) && W <= w_max &&
+            Sx >= 1 && Sx <= kMaxSplits && geometry(mr, k, n, L, W, Sx).lds_bytes <= kLdsBudget)
+            cfg = make_config(mr, k, n, L, W, Sx);
     }
     return cfg;
 }
@@ -382,11 +573,13 @@ int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, 
                              static_cast<std::size_t>(tiles), &ws));
     }
     const std::size_t lds = (static_cast<std::size_t>(MR) * cfg.chunks_per_split * kChunkK +
-                             static_cast<std::size_t>(W) * MR * kVec * L) * sizeof(float);
+                             static_cast<std::size_t>(W) * MR * kVec * L + 4) * sizeof(float);
     const int64_t byte_rows = KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : k;
     const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
     const uint32_t code_bytes = static_cast<uint32_t>(byte_rows * n);
     const uint32_t scale_bytes = static_cast<uint32_t>(KIND == 0 ? 0 : nblk * n * 4);
+    const uint32_t a_bytes = static_cast<uint32_t>(static_cast<int64_t>(m) * k * 4);
+    const int a_vec = (k % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0) ? 1 : 0;
     // Chunk -> scale block is a shift when block_size / 8 is a power of two.
     int blk_shift = -1;
     if (KIND != 0) {
@@ -395,7 +588,7 @@ int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, 
     }
     hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
                        stream, a, wq, scale, c, m, k, n, block_size, cfg.chunks_per_split, code_bytes,
-                       scale_bytes, blk_shift, ws.partials, ws.counters);
+                       scale_bytes, a_bytes, a_vec, blk_shift, ws.partials, ws.counters);
     return check_launch("QuantizedMatMul", stream);
 }
 
@@ -404,14 +597,19 @@ int launch_mr(const float* a, const uint8_t* wq, const float* scale, float* c, i
               int block_size, hipStream_t stream) {
     const GemvConfig cfg = choose_config(KIND, m, k, n);
 #define VM_GEMV_CASE(LL, WW)                                                                    \
-    if (cfg.L == LL && cfg.W == WW)                                                             \
-        return launch_cfg<KIND, MR, LL, WW>(a, wq, scale, c, m, k, n, block_size, cfg, stream);
+    if constexpr (WW <= max_waves(KIND, MR))                                                    \
+        if (cfg.L == LL && cfg.W == WW)                                                         \
+            return launch_cfg<KIND, MR, LL, WW>(a, wq, scale, c, m, k, n, block_size, cfg, stream);
+    VM_GEMV_CASE(1, 4)
+    VM_GEMV_CASE(2, 4)
+    VM_GEMV_CASE(2, 8)
+    VM_GEMV_CASE(4, 4)
+    VM_GEMV_CASE(4, 8)
     VM_GEMV_CASE(8, 4)
     VM_GEMV_CASE(8, 8)
     VM_GEMV_CASE(16, 4)
     VM_GEMV_CASE(16, 8)
-    VM_GEMV_CASE(64, 4)
-    VM_GEMV_CASE(64, 8)
+    VM_GEMV_CASE(16, 16)
 #undef VM_GEMV_CASE
     return VM_HIP_EUNSUPPORTED;
 }

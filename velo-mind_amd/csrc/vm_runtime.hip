@@ -112,10 +112,14 @@ int get_workspace(hipStream_t stream, std::size_t partial_floats, std::size_t co
         const std::size_t counter_bytes = ((cs * sizeof(unsigned)) + 255) & ~std::size_t(255);
         void* base = nullptr;
         VM_TRY_HIP(hipMalloc(&base, counter_bytes + pf * sizeof(float)), "workspace: hipMalloc");
-        hipError_t err = hipMemset(base, 0, counter_bytes);
+        // Zero the counters on the stream that will use them: a plain
+        // hipMemset runs on the null stream, which is not ordered with the
+        // non-blocking streams the kernels are launched on.  (Growth is
+        // refused during capture, so this memset is never captured.)
+        hipError_t err = hipMemsetAsync(base, 0, counter_bytes, stream);
         if (err != hipSuccess) {
             (void)hipFree(base);
-            return fail_hip(err, "workspace: hipMemset");
+            return fail_hip(err, "workspace: hipMemsetAsync");
         }
         e.base = base;
         e.partial_floats = pf;
