@@ -14,8 +14,10 @@ packed matrix at its own address.  Activations are N(0, 1) fp32.
 Timed region: K graph replays of the captured step on one stream, bracketed
 by HIP events and device synchronisation.  ``value`` is algorithmic bytes
 (codes + scales + fp32 A + fp32 C, each once) per second over the region.
-``roofline.achieved`` uses the kernel's own average duration, measured with
-HIP events around each launch in a separate eager pass.  ``cpu_baseline``
+``roofline`` covers the dominant kernel (the shape whose launches take the
+most time per step): its algorithmic bytes per launch over its average
+launch duration, from a HIP graph of that shape's launches replayed between
+two events on the launch stream.  ``cpu_baseline``
 times the oracle's scalar INT4 path (src/cpu/ops/quantized_matmul.cpp:48-141)
 on one pinned core over a bounded sample of the same step.
 
@@ -106,36 +108,74 @@ class Workload:
             H.qmm_f32(self.x[k].addr, p.addr, s.addr, self.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
 
 
-def per_launch_durations(H, wl: Workload, reps: int) -> dict:
-    """Average kernel duration per shape from events around each launch."""
+def per_shape_durations(H, wl: Workload, reps: int, use_graph: bool) -> dict:
+    """Average launch duration per shape: for each shape, that shape's
+    launches of the step (each on its own weight copy) are replayed `reps`
+    times between two events on the launch stream, as one HIP graph (or,
+    with use_graph False, as eager launches, which the host's launch rate
+    can bound)."""
     st = wl.stream
-    sums: dict = {}
-    counts: dict = {}
-    evs = [(H.Event(), H.Event()) for _ in wl.calls]
-    for _ in range(reps):
-        for (name, k, n, p, s), (e0, e1) in zip(wl.calls, evs):
-            e0.record(st.handle)
-            H.qmm_f32(wl.x[k].addr, p.addr, s.addr, wl.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
-            e1.record(st.handle)
+    out = {}
+    lib = H.open_library()
+    for key in sorted({(k, n) for _, k, n, _, _ in wl.calls}):
+        calls = [c for c in wl.calls if (c[1], c[2]) == key]
+        count = len(calls)
+        # A shape launched once per step (lm_head) is timed over eight weight
+        # copies (328 MB, more than the Infinity Cache), so the replay's own
+        # overhead is amortised and the weights still stream from HBM.
+        extra = []
+        while len(calls) < 8:
+            _, k, n, p0, s0 = calls[0]
+            p = H.DeviceBuffer(p0.nbytes)
+            s = H.DeviceBuffer(s0.nbytes)
+            H.check(lib.vm_hip_memcpy_d2d(p.ptr, p0.ptr, p0.nbytes, st.handle))
+            H.check(lib.vm_hip_memcpy_d2d(s.ptr, s0.ptr, s0.nbytes, st.handle))
+            extra.append((p, s))
+            calls.append(("copy", k, n, p, s))
+
+        def launch_all():
+            for _, k, n, p, s in calls:
+                H.qmm_f32(wl.x[k].addr, p.addr, s.addr, wl.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
+
+        g = None
+        if use_graph:
+            g = H.Graph(st)
+            g.begin()
+            launch_all()
+            g.end()
+        replay = g.launch if g is not None else launch_all
+        replay()
         st.synchronize()
-        for (name, k, n, _, _), (e0, e1) in zip(wl.calls, evs):
-            key = (k, n)
-            sums[key] = sums.get(key, 0.0) + e0.elapsed_ms(e1)
-            counts[key] = counts.get(key, 0) + 1
-    return {key: sums[key] / counts[key] for key in sums}
+        e0, e1 = H.Event(), H.Event()
+        e0.record(st.handle)
+        for _ in range(reps):
+            replay()
+        e1.record(st.handle)
+        e1.synchronize()
+        out[key] = (e0.elapsed_ms(e1) / (reps * len(calls)), count)
+        if g is not None:
+            g.close()
+        for p, s in extra:
+            p.close()
+            s.close()
+    return out
 
 
-def measured_traffic():
-    """HBM bytes per launch of the GEMV from the committed rocprofv3 counter
-    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the counters'
-    reading of a plain copy of known size), or (None, None)."""
-    path = os.path.join(ROOT, "profiles", "gemv_int4_tinyllama_decode_sweep.json")
+def measured_traffic(shape: str):
+    """HBM bytes per launch of the GEMV of `shape` ("KxN") from the committed
+    rocprofv3 counter summary profiles/gemv_int4_<shape>_traffic.md, whose
+    line "traffic_bytes_per_launch: N" is FETCH_SIZE + WRITE_SIZE per
+    dispatch scaled by the counters' reading of a plain copy of known size;
+    (None, None) when no summary exists for the shape."""
+    path = os.path.join(ROOT, "profiles", f"gemv_int4_{shape}_traffic.md")
     try:
         with open(path) as f:
-            prof = json.load(f)
-        return int(prof["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
-    except (OSError, KeyError, ValueError):
-        return None, None
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
+    except (OSError, ValueError):
+        pass
+    return None, None
 
 
 def cpu_baseline(target_s: float) -> dict:
@@ -181,8 +221,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
-    ap.add_argument("--event-reps", type=int, default=5, help="eager passes with per-launch events")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--shape-reps", type=int, default=20, help="replays per shape for per-launch durations")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--only-shape", default="", help="KxN: launch only this shape's GEMVs (profiling passes)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (rocprofv3 counter calibration)")
     args = ap.parse_args()
@@ -205,6 +246,13 @@ def main() -> int:
         return 0
     log("bench: packing weights on the GPU")
     wl = Workload(H, stream)
+    if args.only_shape:
+        k_only, n_only = (int(v) for v in args.only_shape.split("x"))
+        wl.calls = [c for c in wl.calls if (c[1], c[2]) == (k_only, n_only)]
+        if not wl.calls:
+            log(f"bench: no GEMV of shape {args.only_shape} in the step")
+            return 2
+        wl.bytes_per_step = sum(algo_bytes(k, n) for _, k, n, _, _ in wl.calls)
     log(f"bench: {len(wl.calls)} GEMVs per step, {wl.bytes_per_step / 1e6:.1f} MB per step")
 
     # eager warm-up sizes the split-K workspace before any capture
@@ -244,20 +292,20 @@ def main() -> int:
     value = wl.bytes_per_step / (ms_per_step * 1e-3) / 1e9
     log(f"bench: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s (wall {wall:.2f} s)")
 
-    durs = per_launch_durations(H, wl, args.event_reps)
+    durs = per_shape_durations(H, wl, args.shape_reps, graph is not None)
     per_shape = {}
-    kern_bytes = 0
-    kern_ms = 0.0
-    for (k, n), ms in sorted(durs.items()):
-        count = sum(1 for _, kk, nn, _, _ in wl.calls if (kk, nn) == (k, n))
+    for (k, n), (ms, count) in durs.items():
         b = algo_bytes(k, n)
-        per_shape[f"{k}x{n}"] = {"launches_per_step": count, "avg_kernel_us": round(ms * 1e3, 3),
-                                 "GB_s": round(b / (ms * 1e-3) / 1e9, 1)}
-        kern_bytes += b * count
-        kern_ms += ms * count
-    achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
+        per_shape[f"{k}x{n}"] = {"launches_per_step": count, "avg_launch_us": round(ms * 1e3, 3),
+                                 "algo_bytes_per_launch": b, "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                                 "us_per_step": round(ms * 1e3 * count, 1)}
+    # The roofline is reported for the dominant kernel: the shape whose
+    # launches take the most time per step.
+    (dk, dn), (dms, dcount) = max(durs.items(), key=lambda kv: kv[1][0] * kv[1][1])
+    dbytes = algo_bytes(dk, dn)
+    achieved = dbytes / (dms * 1e-3) / 1e9
     launches = len(wl.calls)
-    traffic, traffic_src = measured_traffic()
+    traffic, traffic_src = measured_traffic(f"{dk}x{dn}")
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -297,9 +345,9 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": "qmm_gemv_kernel<INT4>",
-            "avg_kernel_us": round(kern_ms / launches * 1e3, 3),
-            "algo_bytes_per_launch": round(kern_bytes / launches),
+            "kernel": f"qmm_gemv_kernel, INT4 K={dk} N={dn} (M=1), {dcount} launches per step",
+            "avg_launch_us": round(dms * 1e3, 3),
+            "algo_bytes_per_launch": dbytes,
         },
         "per_shape": per_shape,
         "cpu_baseline": cpu,
