@@ -1,0 +1,98 @@
+"""Every MFMA GEMM tile variant (rows_m > 4), forced through the tuning
+override VELOMIND_GEMM_CFG="BM,BN,S", against the oracle.
+
+Covers the three weight kinds, K splits 1/2/4 (deterministic split-K
+reduction), partial M and N tiles, K ending half-way through a 64-row step,
+INT8 blocks of 32 and 96 rows, and block scales from 1e-7 to 1e3 (the
+per-column power-of-two normalisation keeps fp16 weights in range).
+Bound: the north-star 1e-3 * max|ref| (A is rounded to fp16 on this path).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+# (BM, BN) tile variants instantiated in velo-mind_amd/csrc/qmm_gemm.hip.
+TILES = [(16, 128), (32, 128), (64, 128), (128, 128), (32, 64), (64, 64)]
+TOL = 1e-3
+
+
+def _check(out, ref, tol=TOL):
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(out.astype(np.float64) - ref).max()
+    bound = tol * max(np.abs(ref).max(), 1e-30)
+    assert err <= bound, f"max abs err {err:.3e} > {bound:.3e}"
+
+
+def _weights(kind, k, n, rng, block):
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    if kind == "int8":
+        q, s = O.quantize_int8(w)
+        return q, s, 1, 0
+    if kind == "int8_block":
+        q = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        s = (rng.random(((k + block - 1) // block, n)) * 0.01 + 1e-4).astype(np.float32)
+        return q, s, 1, block
+    q, s = O.quantize_int4(w, block)
+    return q, s, 2, block
+
+
+@pytest.mark.parametrize("kind,block", [("int8", 0), ("int8_block", 32), ("int8_block", 96), ("int4", 32),
+                                        ("int4", 64)])
+@pytest.mark.parametrize("bm,bn", TILES)
+def test_forced_tile(hip, monkeypatch, bm, bn, kind, block):
+    m, k, n = 40, 224, 336        # partial M and N tiles; 224 = 3.5 steps of 64
+    rng = np.random.default_rng(bm * 1000 + bn + block)
+    q, s, qt, blk = _weights(kind, k, n, rng, block)
+    oq = O.QUANT_INT4 if qt == 2 else O.QUANT_INT8
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = O.qmm(x, q.view(np.int8), s, k, oq, blk)
+    for splits in (1, 2, 4):
+        monkeypatch.setenv("VELOMIND_GEMM_CFG", f"{bm},{bn},{splits}")
+        print(f"case BM={bm} BN={bn} S={splits} kind={kind} block={block} m={m} k={k} n={n}", flush=True)
+        out = hip.run_qmm(x, q, s, k, qt, blk)
+        _check(out, ref)
+    monkeypatch.delenv("VELOMIND_GEMM_CFG")
+
+
+@pytest.mark.parametrize("mag", [1e-7, 1e-3, 1e3])
+@pytest.mark.parametrize("qt", ["int4", "int8_block"])
+def test_scale_magnitudes(hip, mag, qt):
+    # Block scales spanning 3 orders of magnitude inside each column.
+    m, k, n, block = 33, 256, 128, 32
+    rng = np.random.default_rng(int(mag * 1e7) % 1000 + 3)
+    nb = k // block
+    spread = 10.0 ** rng.uniform(-1.5, 1.5, (nb, n))
+    s = (mag * spread).astype(np.float32)
+    if qt == "int4":
+        codes = rng.integers(-8, 8, (k, n))
+        packed = np.zeros(((k + 1) // 2, n), np.uint8)
+        packed |= (codes[0::2] & 0xF).astype(np.uint8)
+        packed |= ((codes[1::2] & 0xF) << 4).astype(np.uint8)
+        q, hq, oq = packed, hip.QUANT_INT4, O.QUANT_INT4
+    else:
+        q, hq, oq = rng.integers(-127, 128, (k, n), dtype=np.int8), hip.QUANT_INT8, O.QUANT_INT8
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = O.qmm(x, q.view(np.int8), s, k, oq, block)
+    out = hip.run_qmm(x, q, s, k, hq, block)
+    # columns differ by orders of magnitude: hold each column to its own max
+    ref64 = np.asarray(ref, np.float64)
+    colmax = np.abs(ref64).max(axis=0)
+    err = np.abs(out.astype(np.float64) - ref64).max(axis=0)
+    assert np.all(err <= TOL * np.maximum(colmax, 1e-300)), f"worst column ratio {np.max(err / colmax):.3e}"
+
+
+def test_split_k_deterministic(hip, monkeypatch):
+    m, k, n = 24, 2048, 640
+    rng = np.random.default_rng(5)
+    q, s = O.quantize_int4((rng.standard_normal((k, n)) * 0.02).astype(np.float32), 32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    monkeypatch.setenv("VELOMIND_GEMM_CFG", "32,128,8")
+    outs = [hip.run_qmm(x, q, s, k, hip.QUANT_INT4, 32) for _ in range(3)]
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    _check(outs[0], O.qmm(x, q.view(np.int8), s, k, O.QUANT_INT4, 32))

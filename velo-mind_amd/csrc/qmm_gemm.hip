@@ -1,253 +1,560 @@
-// Prefill-shaped (rows_m > 4) quantized matmul on gfx950 MFMA.
+// Prefill-shaped (rows_m > 4) quantized matmul on gfx950 MFMA
+// (v_mfma_f32_16x16x32_f16, fp32 accumulation).
 //
-// C[M, N] = A[M, K] * W[K, N] with W given as the reference's codes
-// (INT8 [K, N] or INT4 packed [(K+1)/2, N]) and fp32 scales.
+// C[M, N] = A[M, K] * W[K, N] with W given as the reference's codes (INT8
+// [K, N] or INT4 packed [(K+1)/2, N], N contiguous) and fp32 scales.
 //
-// Per K step of 32 (one INT4 scale block):
-//   A tile  BM x 32 fp32 -> fp16 (round to nearest even) -> LDS [BM][32]
-//   B tile  32 x BN codes -> fp16 (exact: |code| <= 127) -> LDS [BN][32],
-//           i.e. K-contiguous per column, the B-operand layout of
-//           v_mfma_f32_16x16x32_f16 (lane l: column l % 16, k 8*(l/16)..+7)
-//   MFMA    each wave owns WM x WN outputs as 16x16 tiles
-//   scales  INT8 per column: applied once in the epilogue; blockwise
-//           (INT4, INT8 with block_size > 0): each step's MFMA result is
-//           multiplied by its block's fp32 scale and added to an fp32
-//           accumulator, so codes and scales are never rounded to fp16.
-// LDS is double-buffered: the next step's global loads are in flight while
-// the current step's MFMAs run; one barrier per step.
+// Pipeline (per workgroup: a BM x BN output tile, four waves, K in steps of
+// 64 rows):
+//   global -> registers  raw buffer loads (zeros past the end), two steps
+//                        ahead of the MFMAs;
+//   registers -> LDS     A: fp32 -> fp16 (RNE), row-major [BM][64];
+//                        B: codes -> fp16 with packed-half magic numbers
+//                        (0x6400 | (code ^ 0x80..) is 1024 + 128 + code),
+//                        times the block scale, stored in the codes' own
+//                        layout [64][BN] (N contiguous, 16-byte writes);
+//   LDS -> MFMA          A operand: ds_read_b128 of 8 consecutive k;
+//                        B operand: two ds_read_b64_tr_b16 transposed reads
+//                        give each lane 8 consecutive k of one column.
+// Columns are kept in the order (c0, c2, c1, c3) inside every group of four
+// in LDS (the order the magic-number unpacking produces); the epilogue
+// writes each result to its true column.
+//
+// Scales.  INT8 per column: applied in the epilogue (fp32).  Blockwise
+// (INT4, INT8 with block_size > 0): B is staged as fp16(code * s / 2^e),
+// where 2^e is a per-column power of two with max_s / 2^e in [0.5, 1) over
+// the workgroup's K range, and the fp32 result is multiplied by 2^e (exact).
+// The normalisation keeps every staged weight inside fp16's normal range
+// whatever the scales' magnitude; the only roundings beyond fp32
+// accumulation are A -> fp16 and (code * s / 2^e) -> fp16, each relative
+// 2^-11 at most.
+//
+// Split-K for small M: each split stores its scaled partial tile
+// with agent-scope stores, the last split of a tile (atomic ticket) adds
+// the partials in split order and writes C, so results are deterministic.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 
 #include "qmm_kernels.h"
+#include "vm_device.h"
 #include "vm_internal.h"
 
 namespace vmhip {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 32;       // K per step
-constexpr int kPad = 8;       // halves of padding per LDS row (80-byte rows)
-constexpr int kRow = kBK + kPad;
-constexpr int kThreads = 256;
+constexpr int kBK = 64;         // K rows per pipeline step
+constexpr int kThreads = 256;   // four waves
+constexpr int kApad = 8;        // halves of padding per LDS row of A
+constexpr int kBpad = 16;       // halves of padding per LDS row of B
+constexpr int kMaxSplits = 16;
+
+typedef __attribute__((address_space(3))) short4v lds_short4;
+
+__device__ __forceinline__ half4v lds_read_tr16(const _Float16* p) {
+    // Generic -> LDS address space: the low 32 bits of a generic LDS pointer
+    // are the LDS offset.
+    auto* lp = (lds_short4*)(uintptr_t)(uint32_t)(uintptr_t)p;
+    return __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(lp));
+}
+
+__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
+    const half2v h = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ uint32_t hmul2(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) * __builtin_bit_cast(half2v, b));
+}
+
+__device__ __forceinline__ uint32_t hsub2(uint32_t a, _Float16 b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) - half2v{b, b});
+}
 
 // KIND: 0 = INT8 per-column, 1 = INT8 blockwise, 2 = INT4 blockwise.
-// BM x BN output tile per workgroup; WAVES_M x WAVES_N = 4 waves.
 template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
-__global__ __launch_bounds__(kThreads) void qmm_gemm_kernel(const float* __restrict__ a,
-                                                            const uint8_t* __restrict__ wq,
-                                                            const float* __restrict__ scale,
-                                                            float* __restrict__ c, int m, int k, int n,
-                                                            int block_size) {
-    static_assert(WAVES_M * WAVES_N == 4, "four waves per workgroup");
-    constexpr bool kInt4 = KIND == 2;
-    constexpr bool kBlockScaled = KIND != 0;
-    constexpr int WM = BM / WAVES_M;
-    constexpr int WN = BN / WAVES_N;
-    constexpr int TM = WM / 16;
-    constexpr int TN = WN / 16;
-    static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 16x16 MFMA tile");
-    constexpr int kAVec = BM * kBK / 4;           // float4 loads of A per step
-    constexpr int kAPerThread = (kAVec + kThreads - 1) / kThreads;
-    constexpr int kBQuads = BN / 4;               // 4-column groups
-    constexpr int kBJobs = kBQuads * (kBK / 4);   // (column quad, k quad) pairs per step
-    constexpr int kBPerThread = (kBJobs + kThreads - 1) / kThreads;
+struct Tile {
+    static constexpr bool kInt4 = KIND == 2;
+    static constexpr bool kBlock = KIND != 0;
+    static constexpr int WM = BM / WAVES_M;
+    static constexpr int WN = BN / WAVES_N;
+    static constexpr int TM = WM / 16;
+    static constexpr int TN = WN / 16;
+    static constexpr int kArow = kBK + kApad;                  // halves per A row
+    static constexpr int kBrow = BN + kBpad;                   // halves per B k-row
+    static constexpr int kAPieces = BM * (kBK / 8);            // 8 floats each
+    static constexpr int kAPass = (kAPieces + kThreads - 1) / kThreads;
+    static constexpr int kBRows = kInt4 ? kBK / 2 : kBK;       // code byte rows per step
+    static constexpr int kBPieces = kBRows * (BN / 16);        // 16 bytes each
+    static constexpr int kBPass = (kBPieces + kThreads - 1) / kThreads;
+    static constexpr int kQB = BN / 4;                         // column quads
+    static constexpr int kRedRows = kThreads / kQB;
+    static_assert(WAVES_M * WAVES_N == 4, "four waves");
+    static_assert(TM >= 1 && TN >= 1 && WM % 16 == 0 && WN % 16 == 0, "16x16 MFMA tiles");
+    static_assert(BN % 16 == 0 && kThreads % kQB == 0, "tile shape");
+};
 
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM][kRow];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[2][BN][kRow];
-    __shared__ float sS[2][kBlockScaled ? BN : 1];
+template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
+struct Stage {
+    using T = Tile<KIND, BM, BN, WAVES_M, WAVES_N>;
+    u32x4 a[T::kAPass][2];
+    u32x4 b[T::kBPass];
+    u32x4 s[T::kBlock ? T::kBPass : 1][T::kBlock ? 4 : 1];
+};
+
+template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
+__global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
+    const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
+    float* __restrict__ c, int m, int k, int n, int block_size, int steps_per_split, int tiles_n, int tiles_m,
+    uint32_t a_bytes, uint32_t code_bytes, uint32_t scale_bytes, float* __restrict__ partials,
+    unsigned* __restrict__ counters) {
+    using T = Tile<KIND, BM, BN, WAVES_M, WAVES_N>;
+    using S = Stage<KIND, BM, BN, WAVES_M, WAVES_N>;
+
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * T::kArow];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][kBK * T::kBrow];
+    __shared__ float sPow[T::kBlock ? BN : 1];   // 2^e per column (physical order)
+    __shared__ float sInv[T::kBlock ? BN : 1];   // 2^-e
+    __shared__ float sRed[T::kBlock ? T::kRedRows * BN : 1];
+    __shared__ unsigned ticket;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave / WAVES_N;
     const int wn = wave % WAVES_N;
-    const int n0 = blockIdx.x * BN;
-    const int m0 = blockIdx.y * BM;
-    const int steps = k / kBK;  // dispatch guarantees k % 32 == 0
+    // One-dimensional grid over (split, tile row, tile column), column
+    // fastest.  Workgroups go to the 8 XCDs round-robin by id; renumbering
+    // gives each XCD a contiguous run, so the workgroups sharing one L2
+    // mostly share one A panel (the operand every column tile re-reads).
+    int lin = blockIdx.x;
+    {
+        const int full = static_cast<int>(gridDim.x) & ~7;
+        if (lin < full) lin = (lin & 7) * (full >> 3) + (lin >> 3);
+    }
+    const int tile_x = lin % tiles_n;
+    const int tile_y = (lin / tiles_n) % tiles_m;
+    const int split = lin / (tiles_n * tiles_m);
+    const int splits = static_cast<int>(gridDim.x) / (tiles_n * tiles_m);
+    const int n0 = tile_x * BN;
+    const int m0 = tile_y * BM;
+    const int total_steps = (k + kBK - 1) / kBK;
+    const int step0 = split * steps_per_split;
+    const int nsteps = min(total_steps, step0 + steps_per_split) - step0;
+    const int k_begin = step0 * kBK;
+    const int k_end = min(k, k_begin + nsteps * kBK);
 
-    // Register staging of one step's global data.
-    float4 ra[kAPerThread];
-    uint32_t rb[kBPerThread][kInt4 ? 2 : 4];
-    float4 rs = {0.f, 0.f, 0.f, 0.f};
+    const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wq, code_bytes);
+    const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
 
-    auto load_global = [&](int step) {
-        const int k0 = step * kBK;
+    // ---- per-column normalisation of block scales over this split's K range
+    if constexpr (T::kBlock) {
+        const int b0 = k_begin / block_size;
+        const int b1 = (k_end + block_size - 1) / block_size;
+        const int q = tid % T::kQB;
+        float mx[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int b = b0 + tid / T::kQB; b < b1; b += 4 * T::kRedRows) {
+            u32x4 v[4];
 #pragma unroll
-        for (int i = 0; i < kAPerThread; ++i) {
-            const int f = tid + i * kThreads;
-            const int row = f / (kBK / 4);
-            const int c4 = f % (kBK / 4);
-            ra[i] = float4{0.f, 0.f, 0.f, 0.f};
-            if (f < kAVec && m0 + row < m)
-                ra[i] = *reinterpret_cast<const float4*>(a + static_cast<int64_t>(m0 + row) * k + k0 + c4 * 4);
-        }
-#pragma unroll
-        for (int i = 0; i < kBPerThread; ++i) {
-            const int job = tid + i * kThreads;
-            const int quad = job % kBQuads;
-            const int kq = job / kBQuads;  // k rows 4*kq .. 4*kq+3 of the step
-            const int col = n0 + quad * 4;
-            const bool ok = job < kBJobs && col < n;
-            if constexpr (kInt4) {
-                const int prow = (k0 + kq * 4) / 2;  // two packed rows hold four k rows
-#pragma unroll
-                for (int r = 0; r < 2; ++r)
-                    rb[i][r] = ok ? *reinterpret_cast<const uint32_t*>(wq + static_cast<int64_t>(prow + r) * n + col) : 0u;
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    rb[i][r] = ok ? *reinterpret_cast<const uint32_t*>(wq + static_cast<int64_t>(k0 + kq * 4 + r) * n + col) : 0u;
+            for (int u = 0; u < 4; ++u) {
+                const int bb = b + u * T::kRedRows;
+                const uint32_t off = bb < b1 ? (static_cast<uint32_t>(bb) * n + n0 + 4 * q) * 4u : scale_bytes;
+                v[u] = buffer_load16(srs, off);
             }
-        }
-        if constexpr (kBlockScaled) {
-            if (tid < BN / 4) {
-                const int blk = k0 / block_size;
-                const int col = n0 + tid * 4;
-                rs = col < n ? *reinterpret_cast<const float4*>(scale + static_cast<int64_t>(blk) * n + col)
-                             : float4{0.f, 0.f, 0.f, 0.f};
-            }
-        }
-    };
-
-    auto store_lds = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < kAPerThread; ++i) {
-            const int f = tid + i * kThreads;
-            if (f < kAVec) {
-                const int row = f / (kBK / 4);
-                const int c4 = f % (kBK / 4);
-                half4 h = {static_cast<_Float16>(ra[i].x), static_cast<_Float16>(ra[i].y),
-                           static_cast<_Float16>(ra[i].z), static_cast<_Float16>(ra[i].w)};
-                *reinterpret_cast<half4*>(&sA[buf][row][c4 * 4]) = h;
-            }
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], fabsf(__uint_as_float(v[u][e])));
         }
 #pragma unroll
-        for (int i = 0; i < kBPerThread; ++i) {
-            const int job = tid + i * kThreads;
-            if (job >= kBJobs) continue;
-            const int quad = job % kBQuads;
-            const int kq = job / kBQuads;
-            // codes[r][col] for the 4 k rows and 4 columns of this job
+        for (int e = 0; e < 4; ++e) sRed[(tid / T::kQB) * BN + 4 * q + e] = mx[e];
+        __syncthreads();
+        if (tid < BN) {
+            float mm = 0.f;
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                half4 h;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    int code;
-                    if constexpr (kInt4) {
-                        const uint32_t byte = (rb[i][r >> 1] >> (8 * cc)) & 0xFFu;
-                        const int nib = (r & 1) ? static_cast<int>(byte >> 4) : static_cast<int>(byte & 0xFu);
-                        code = nib >= 8 ? nib - 16 : nib;
-                    } else {
-                        code = static_cast<int8_t>((rb[i][r] >> (8 * cc)) & 0xFFu);
-                    }
-                    h[r] = static_cast<_Float16>(code);
-                }
-                *reinterpret_cast<half4*>(&sB[buf][quad * 4 + cc][kq * 4]) = h;
-            }
+            for (int r = 0; r < T::kRedRows; ++r) mm = fmaxf(mm, sRed[r * BN + tid]);
+            int e = 0;
+            if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
+            sPow[tid] = ldexpf(1.0f, e);
+            sInv[tid] = ldexpf(1.0f, -e);
         }
-        if constexpr (kBlockScaled) {
-            if (tid < BN / 4) *reinterpret_cast<float4*>(&sS[buf][tid * 4]) = rs;
-        }
-    };
-
-    floatx4 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-
-    const int frag_row = lane % 16;
-    const int frag_k = 8 * (lane / 16);
-    for (int step = 0; step < steps; ++step) {
-        const int buf = step & 1;
-        if (step + 1 < steps) load_global(step + 1);
-
-        half8 bf[TN];
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-            bf[j] = *reinterpret_cast<const half8*>(&sB[buf][wn * WN + j * 16 + frag_row][frag_k]);
-        float sv[TN];
-        if constexpr (kBlockScaled) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) sv[j] = sS[buf][wn * WN + j * 16 + frag_row];
-        }
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const half8 af = *reinterpret_cast<const half8*>(&sA[buf][wm * WM + i * 16 + frag_row][frag_k]);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                if constexpr (kBlockScaled) {
-                    const floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(sv[j], d[e], acc[i][j][e]);
-                } else {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-        if (step + 1 < steps) store_lds(buf ^ 1);
         __syncthreads();
     }
 
-    // D layout: lane l holds rows 4*(l/16)+e, column l%16 of each tile.
+    // ---- global -> registers for one step
+    auto load_step = [&](int s, S& st) {
+        const int k0 = (step0 + s) * kBK;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * WN + j * 16 + frag_row;
-        if (col >= n) continue;
-        const float s = KIND == 0 ? scale[col] : 1.0f;
+        for (int p = 0; p < T::kAPass; ++p) {
+            const int piece = tid + p * kThreads;
+            const int row = piece / (kBK / 8);
+            const int kk = k0 + 8 * (piece % (kBK / 8));
+            const bool ok = piece < T::kAPieces && m0 + row < m && kk < k_end;
+            const uint32_t off = ok ? (static_cast<uint32_t>(m0 + row) * k + kk) * 4u : a_bytes;
+            st.a[p][0] = buffer_load16(ars, off);
+            st.a[p][1] = buffer_load16(ars, ok ? off + 16u : a_bytes);
+        }
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
+        for (int p = 0; p < T::kBPass; ++p) {
+            const int piece = tid + p * kThreads;
+            const int row = piece / (BN / 16);            // code byte row within the step
+            const int col = n0 + 16 * (piece % (BN / 16));
+            const int krow = T::kInt4 ? k0 / 2 + row : k0 + row;
+            const int klog = T::kInt4 ? k0 + 2 * row : k0 + row;   // first logical K row of the piece
+            const bool ok = piece < T::kBPieces && klog < k_end;
+            st.b[p] = buffer_load16(wrs, ok ? static_cast<uint32_t>(krow) * n + col : code_bytes);
+            if constexpr (T::kBlock) {
+                const uint32_t blk = static_cast<uint32_t>(klog) / static_cast<uint32_t>(block_size);
+                const uint32_t soff = ok ? (blk * n + col) * 4u : scale_bytes;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = m0 + wm * WM + i * 16 + 4 * (lane / 16) + e;
-                if (row < m) c[static_cast<int64_t>(row) * n + col] = acc[i][j][e] * s;
+                for (int qd = 0; qd < 4; ++qd) st.s[p][qd] = buffer_load16(srs, soff + 16u * qd);
             }
         }
+    };
+
+    // ---- registers -> fp16 registers (VALU only) -> LDS
+    struct Packed {
+        u32x4 a[T::kAPass];
+        u32x4 b[T::kBPass][T::kInt4 ? 4 : 2];
+    };
+    auto convert_step = [&](const S& st, Packed& pk) {
+#pragma unroll
+        for (int p = 0; p < T::kAPass; ++p) {
+            pk.a[p][0] = pk_f16(__uint_as_float(st.a[p][0][0]), __uint_as_float(st.a[p][0][1]));
+            pk.a[p][1] = pk_f16(__uint_as_float(st.a[p][0][2]), __uint_as_float(st.a[p][0][3]));
+            pk.a[p][2] = pk_f16(__uint_as_float(st.a[p][1][0]), __uint_as_float(st.a[p][1][1]));
+            pk.a[p][3] = pk_f16(__uint_as_float(st.a[p][1][2]), __uint_as_float(st.a[p][1][3]));
+        }
+#pragma unroll
+        for (int p = 0; p < T::kBPass; ++p) {
+            const int piece = tid + p * kThreads;
+            const int cl = 16 * (piece % (BN / 16));      // local column of the piece
+            // normalised scales, paired in (c0, c2), (c1, c3) order per quad
+            uint32_t sn[8];
+            if constexpr (T::kBlock) {
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    const float* inv = sInv + cl + 4 * qd;
+                    sn[2 * qd] = pk_f16(__uint_as_float(st.s[p][qd][0]) * inv[0], __uint_as_float(st.s[p][qd][2]) * inv[2]);
+                    sn[2 * qd + 1] = pk_f16(__uint_as_float(st.s[p][qd][1]) * inv[1], __uint_as_float(st.s[p][qd][3]) * inv[3]);
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                if constexpr (T::kInt4) {
+                    const uint32_t x = st.b[p][d] ^ 0x88888888u;
+                    uint32_t e02 = hsub2((x & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
+                    uint32_t e13 = hsub2(((x >> 8) & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
+                    uint32_t o02 = hsub2(((x >> 4) & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
+                    uint32_t o13 = hsub2(((x >> 12) & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
+                    // b[p][0..1]: even K row, 16 columns; b[p][2..3]: odd K row
+                    pk.b[p][d / 2][2 * (d % 2)] = hmul2(e02, sn[2 * d]);
+                    pk.b[p][d / 2][2 * (d % 2) + 1] = hmul2(e13, sn[2 * d + 1]);
+                    pk.b[p][2 + d / 2][2 * (d % 2)] = hmul2(o02, sn[2 * d]);
+                    pk.b[p][2 + d / 2][2 * (d % 2) + 1] = hmul2(o13, sn[2 * d + 1]);
+                } else {
+                    const uint32_t x = st.b[p][d] ^ 0x80808080u;
+                    uint32_t e02 = hsub2((x & 0x00FF00FFu) | 0x64006400u, static_cast<_Float16>(1152.0f));
+                    uint32_t e13 = hsub2(((x >> 8) & 0x00FF00FFu) | 0x64006400u, static_cast<_Float16>(1152.0f));
+                    if constexpr (T::kBlock) {
+                        e02 = hmul2(e02, sn[2 * d]);
+                        e13 = hmul2(e13, sn[2 * d + 1]);
+                    }
+                    pk.b[p][d / 2][2 * (d % 2)] = e02;
+                    pk.b[p][d / 2][2 * (d % 2) + 1] = e13;
+                }
+            }
+        }
+    };
+    auto write_step = [&](const Packed& pk, int buf) {
+        _Float16* la = sA[buf];
+        _Float16* lb = sB[buf];
+#pragma unroll
+        for (int p = 0; p < T::kAPass; ++p) {
+            const int piece = tid + p * kThreads;
+            if (piece < T::kAPieces) {
+                const int row = piece / (kBK / 8);
+                const int kc = 8 * (piece % (kBK / 8));
+                *reinterpret_cast<u32x4*>(la + row * T::kArow + kc) = pk.a[p];
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < T::kBPass; ++p) {
+            const int piece = tid + p * kThreads;
+            if (piece >= T::kBPieces) continue;
+            const int row = piece / (BN / 16);
+            const int cl = 16 * (piece % (BN / 16));
+            if constexpr (T::kInt4) {
+                _Float16* r0 = lb + (2 * row) * T::kBrow + cl;
+                _Float16* r1 = r0 + T::kBrow;
+                *reinterpret_cast<u32x4*>(r0) = pk.b[p][0];
+                *reinterpret_cast<u32x4*>(r0 + 8) = pk.b[p][1];
+                *reinterpret_cast<u32x4*>(r1) = pk.b[p][2];
+                *reinterpret_cast<u32x4*>(r1 + 8) = pk.b[p][3];
+            } else {
+                _Float16* r0 = lb + row * T::kBrow + cl;
+                *reinterpret_cast<u32x4*>(r0) = pk.b[p][0];
+                *reinterpret_cast<u32x4*>(r0 + 8) = pk.b[p][1];
+            }
+        }
+    };
+    auto store_step = [&](const S& st, int buf) {
+        Packed pk;
+        convert_step(st, pk);
+        write_step(pk, buf);
+    };
+
+    floatx4 acc[T::TM][T::TN];
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int fr = lane & 15;        // fragment row (A) / column (B)
+    const int fg = lane >> 4;        // 8-k group
+    struct Frags {
+        half8v a[T::TM];
+        half8v b[T::TN];
+    };
+    auto read_frags = [&](int buf, int kh, Frags& f) {
+        const _Float16* la = sA[buf];
+        const _Float16* lb = sB[buf];
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+            f.a[i] = *reinterpret_cast<const half8v*>(la + (wm * T::WM + i * 16 + fr) * T::kArow + kh * 32 + 8 * fg);
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j) {
+            // lane L of each 16-lane group points at row base + L/4,
+            // columns 4 * (L % 4) .. + 3: the transposed read returns,
+            // for lane i, rows base .. base + 3 of column i.
+            const _Float16* p = lb + (kh * 32 + 8 * fg + (fr >> 2)) * T::kBrow + wn * T::WN + j * 16 + 4 * (fr & 3);
+            const half4v lo = lds_read_tr16(p);
+            const half4v hi = lds_read_tr16(p + 4 * T::kBrow);
+            f.b[j] = half8v{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+    };
+    auto mfma_frags = [&](const Frags& f) {
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < T::TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+    // One pipeline step: all fragment reads of the current buffer are issued
+    // first, the next stage is converted in registers while they are in
+    // flight, the MFMAs follow, and the converted stage is written to the
+    // other buffer while the MFMAs drain.
+    auto step = [&](int cur, const S& next_raw) {
+        Frags f0, f1;
+        read_frags(cur, 0, f0);
+        read_frags(cur, 1, f1);
+        Packed pk;
+        convert_step(next_raw, pk);
+        mfma_frags(f0);
+        mfma_frags(f1);
+        write_step(pk, cur ^ 1);
+    };
+
+    // ---- main loop: LDS double buffer, register stages two steps ahead.
+    // Loads and stores are unconditional (steps past the end read zeros):
+    // with a fixed number of loads per iteration the compiler's vmcnt waits
+    // release each stage as soon as its own loads are in, leaving the next
+    // stage's loads in flight.
+    S st0, st1;
+    load_step(0, st0);
+    load_step(1, st1);
+    store_step(st0, 0);
+    load_step(2, st0);
+    __syncthreads();
+    for (int s = 0; s < nsteps; s += 2) {
+        step(0, st1);
+        __syncthreads();
+        load_step(s + 3, st1);
+        if (s + 1 >= nsteps) break;
+        step(1, st0);
+        __syncthreads();
+        load_step(s + 4, st0);
     }
+
+    // ---- epilogue.  D layout: lane holds rows 4 * (lane / 16) + e, column
+    // lane % 16 of each 16x16 tile (LDS column order).
+    auto col_of = [&](int j) {
+        const int nl = wn * T::WN + j * 16 + fr;
+        return (nl & ~3) | ((nl & 1) << 1) | ((nl >> 1) & 1);   // (c0, c2, c1, c3) -> physical
+    };
+    float colscale[T::TN];
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) {
+        const int cp = col_of(j);
+        if constexpr (T::kBlock) {
+            colscale[j] = sPow[cp];
+        } else {
+            colscale[j] = __uint_as_float(buffer_load4(srs, (n0 + cp < n) ? static_cast<uint32_t>(n0 + cp) * 4u : scale_bytes));
+        }
+    }
+
+    if (splits == 1) {
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j) {
+            const int col = n0 + col_of(j);
+            if (col >= n) continue;
+#pragma unroll
+            for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = m0 + wm * T::WM + i * 16 + 4 * fg + e;
+                    if (row < m) c[static_cast<int64_t>(row) * n + col] = acc[i][j][e] * colscale[j];
+                }
+        }
+        return;
+    }
+
+    float* part = partials + static_cast<int64_t>(split) * m * n;
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) {
+        const int col = n0 + col_of(j);
+        if (col >= n) continue;
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = m0 + wm * T::WM + i * 16 + 4 * fg + e;
+                if (row < m) coherent_store(part + static_cast<int64_t>(row) * n + col, acc[i][j][e] * colscale[j]);
+            }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the ticket
+    __syncthreads();
+    const int tile = tile_y * tiles_n + tile_x;
+    if (tid == 0) ticket = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != static_cast<unsigned>(splits - 1)) return;
+    const int64_t stride = static_cast<int64_t>(m) * n;
+    for (int idx = tid; idx < BM * BN; idx += kThreads) {
+        const int row = m0 + idx / BN;
+        const int col = n0 + idx % BN;
+        if (row >= m || col >= n) continue;
+        const float* p = partials + static_cast<int64_t>(row) * n + col;
+        float v = 0.f;
+        for (int s0 = 0; s0 < splits; s0 += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = s0 + u < splits ? coherent_load(p + (s0 + u) * stride) : 0.f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        c[static_cast<int64_t>(row) * n + col] = v;
+    }
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct GemmConfig {
+    int bm = 128, bn = 128, splits = 1;
+};
+
+// Tile and split choice, from a sweep of every tile variant and split count
+// over config-3 shapes (K = 2048, N = 5632, M = 16..512) on MI355X: up to
+// 128 rows, 32 x 64 tiles (many small workgroups hide load latency best);
+// beyond, 128 x 128 tiles (least LDS traffic per MFMA).  K splits (at
+// least four 64-row steps each) are added until about two workgroups per
+// CU, while the fp32 partials stay under a quarter of the code bytes.
+GemmConfig choose_gemm(int kind, int m, int k, int n) {
+    GemmConfig cfg;
+    if (m <= 128) {
+        cfg.bm = 32;
+        cfg.bn = 64;
+    } else {
+        cfg.bm = 128;
+        cfg.bn = 128;
+    }
+    const long tiles = static_cast<long>((m + cfg.bm - 1) / cfg.bm) * ((n + cfg.bn - 1) / cfg.bn);
+    const int steps = (k + kBK - 1) / kBK;
+    const double code_bytes = kind == 2 ? 0.5 * k * n : 1.0 * k * n;
+    int s = 1;
+    while (s * 2 <= 8 && tiles * s * 2 <= 512 && steps / (s * 2) >= 4 &&
+           4.0 * s * 2 * m * n <= 0.25 * code_bytes)
+        s *= 2;
+    cfg.splits = s;
+    // Tuning override for measurement sweeps: VELOMIND_GEMM_CFG="BM,BN,S".
+    if (const char* env = std::getenv("VELOMIND_GEMM_CFG")) {
+        int bm = 0, bn = 0, sx = 0;
+        if (std::sscanf(env, "%d,%d,%d", &bm, &bn, &sx) == 3 && sx >= 1 && sx <= kMaxSplits &&
+            ((bn == 128 && (bm == 16 || bm == 32 || bm == 64 || bm == 128)) ||
+             (bn == 64 && (bm == 32 || bm == 64)))) {
+            cfg.bm = bm;
+            cfg.bn = bn;
+            cfg.splits = sx;
+        }
+    }
+    return cfg;
 }
 
 template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
 int launch(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n, int block_size,
-           hipStream_t stream) {
-    dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
-    hipLaunchKernelGGL((qmm_gemm_kernel<KIND, BM, BN, WAVES_M, WAVES_N>), grid, dim3(kThreads), 0, stream, a, wq,
-                       scale, c, m, k, n, block_size);
+           int splits, hipStream_t stream) {
+    const int tiles_n = (n + BN - 1) / BN;
+    const int tiles_m = (m + BM - 1) / BM;
+    const int steps = (k + kBK - 1) / kBK;
+    const int sps = (steps + splits - 1) / splits;
+    splits = (steps + sps - 1) / sps;
+    Workspace ws{};
+    if (splits > 1) {
+        VM_TRY(get_workspace(stream, static_cast<std::size_t>(splits) * m * n,
+                             static_cast<std::size_t>(tiles_m) * tiles_n, &ws));
+    }
+    const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
+    const uint32_t a_bytes = static_cast<uint32_t>(static_cast<int64_t>(m) * k * 4);
+    const uint32_t code_bytes =
+        static_cast<uint32_t>((KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : static_cast<int64_t>(k)) * n);
+    const uint32_t scale_bytes = static_cast<uint32_t>((KIND == 0 ? 1 : nblk) * n * 4);
+    hipLaunchKernelGGL((qmm_mfma_kernel<KIND, BM, BN, WAVES_M, WAVES_N>), dim3(tiles_n * tiles_m * splits),
+                       dim3(kThreads), 0, stream, a, wq, scale, c, m, k, n, block_size, sps, tiles_n, tiles_m,
+                       a_bytes, code_bytes, scale_bytes, ws.partials, ws.counters);
     return check_launch("QuantizedMatMul", stream);
 }
 
 template <int KIND>
 int launch_kind(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
                 int block_size, hipStream_t stream) {
-    if (m <= 16) return launch<KIND, 16, 128, 1, 4>(a, wq, scale, c, m, k, n, block_size, stream);
-    if (m <= 32) return launch<KIND, 32, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, stream);
-    if (m <= 64) return launch<KIND, 64, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, stream);
-    return launch<KIND, 128, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, stream);
+    const GemmConfig cfg = choose_gemm(KIND, m, k, n);
+    if (cfg.bn == 128) {
+        if (cfg.bm == 16) return launch<KIND, 16, 128, 1, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        if (cfg.bm == 32) return launch<KIND, 32, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        if (cfg.bm == 64) return launch<KIND, 64, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        return launch<KIND, 128, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+    }
+    if (cfg.bm == 32) return launch<KIND, 32, 64, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+    return launch<KIND, 64, 64, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
 }
 
 }  // namespace
 
 int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
                  int quant_type, int block_size, hipStream_t stream) {
-    // Whole 32-row steps, dword-aligned code rows and float4-aligned A/scales.
-    if (k % kBK != 0 || n % 4 != 0 || reinterpret_cast<uintptr_t>(a) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(wq) % 4 != 0 || reinterpret_cast<uintptr_t>(scale) % 16 != 0)
+    // 64-row steps may end half-way (k % 32 == 0); 16-byte code pieces need
+    // whole 16-column groups; buffer offsets are 32-bit.
+    if (k % 32 != 0 || n % 16 != 0) return VM_HIP_EUNSUPPORTED;
+    if (static_cast<int64_t>(m) * k * 4 >= (int64_t(1) << 31) || static_cast<int64_t>(k) * n >= (int64_t(1) << 31) ||
+        static_cast<int64_t>(m) * n * 4 * kMaxSplits >= (int64_t(1) << 40))
         return VM_HIP_EUNSUPPORTED;
-    if (static_cast<int64_t>(m) > 65535 * 128) return VM_HIP_EUNSUPPORTED;
+    // one-dimensional grid of at most 2^30 workgroups
+    if (((static_cast<int64_t>(m) + 15) / 16) * ((n + 63) / 64) * kMaxSplits >= (int64_t(1) << 30))
+        return VM_HIP_EUNSUPPORTED;
     if (quant_type == VM_HIP_QUANT_INT4) {
-        if (block_size <= 0 || block_size % kBK != 0) return VM_HIP_EUNSUPPORTED;
+        if (block_size <= 0 || block_size % 32 != 0) return VM_HIP_EUNSUPPORTED;
         return launch_kind<2>(a, wq, scale, c, m, k, n, block_size, stream);
     }
     if (block_size > 0) {
-        if (block_size % kBK != 0) return VM_HIP_EUNSUPPORTED;
+        if (block_size % 32 != 0) return VM_HIP_EUNSUPPORTED;
         return launch_kind<1>(a, wq, scale, c, m, k, n, block_size, stream);
     }
     return launch_kind<0>(a, wq, scale, c, m, k, n, 0, stream);

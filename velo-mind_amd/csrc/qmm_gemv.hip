@@ -39,6 +39,7 @@
 #include <cstdlib>
 
 #include "qmm_kernels.h"
+#include "vm_device.h"
 #include "vm_internal.h"
 
 namespace vmhip {
@@ -49,35 +50,12 @@ constexpr int kVec = 16;      // columns per lane
 constexpr int kMaxSplits = 32;
 constexpr int kStageBatch = 4;  // activation loads in flight per thread while staging
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 template <int KIND>
 struct ChunkShape {
     static constexpr bool kInt4 = KIND == 2;
     static constexpr int kRows = kInt4 ? kChunkK / 2 : kChunkK;  // byte rows per chunk
     static constexpr bool kScaled = KIND != 0;
 };
-
-// Raw buffer access (gfx9 descriptor word 3 = 0x00020000): loads past
-// `num_records` bytes return zeros instead of faulting, so tails and idle
-// chunks need no branches and every lane issues the same loads.
-constexpr int kBufferFlags = 0x00020000;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferFlags);
-}
-
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset), 0, 0));
-}
-
-__device__ __forceinline__ float coherent_load(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void coherent_store(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // v rotated right by `off` lanes inside each 16-lane row (DPP row_ror).
 __device__ __forceinline__ float dpp_row_ror(float v, int off) {
