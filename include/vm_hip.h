@@ -179,6 +179,85 @@ int vm_hip_dequant_int4(const uint8_t* packed, const float* scale, float* w, int
 int vm_hip_half_to_f32(const uint16_t* src, int src_dtype, float* dst, int64_t count,
                        void* stream);
 
+/* ---- the rest of the LLaMA graph (fp32, contiguous row-major) ----------
+ * Each entry point has the semantics of the reference CPU kernel it cites,
+ * so a graph of these operators built on DeviceType::HIP computes what the
+ * reference's graph (examples/common/llama/llama_graph.cpp:14-330)
+ * computes on the CPU.  Shape validation beyond what the kernel needs to
+ * stay in bounds is the graph layer's job (src/internal/op_validation.h). */
+
+/* out[i, :] = table[idx[i], :]; table [vocab, hidden], idx int32 [count].
+ * Replaces src/cpu/ops/embedding.cpp:16-33.  Indices outside [0, vocab)
+ * produce zero rows; the executor rejects them before launch, as the
+ * reference does (src/executable.cpp:54-66). */
+int vm_hip_embedding_f32(const float* table, int64_t vocab, int64_t hidden, const int32_t* idx,
+                         int64_t count, float* out, void* stream);
+
+/* y[r, :] = x[r, :] / sqrt(mean(x[r, :]^2) + eps) * w, over the last axis
+ * of length dim.  Replaces src/cpu/ops/rmsnorm.cpp:17-60. */
+int vm_hip_rmsnorm_f32(const float* x, const float* w, float* y, int64_t rows, int64_t dim,
+                       float eps, void* stream);
+
+/* Rotary embedding of rows of head_dim values: with h = head_dim / 2 and
+ * p = (cos_rows > 1 ? r % cos_rows : 0),
+ *   y[r, j]     = x[r, j] * cos[p, j] - x[r, j + h] * sin[p, j]
+ *   y[r, j + h] = x[r, j + h] * cos[p, j] + x[r, j] * sin[p, j].
+ * Replaces src/cpu/ops/rotary_embedding.cpp:16-45. */
+int vm_hip_rope_f32(const float* x, const float* cos_table, const float* sin_table, float* y,
+                    int64_t rows, int64_t head_dim, int64_t cos_rows, void* stream);
+
+/* y = x transposed by `perm` (rank 1..6; perm NULL reverses the axes).
+ * Replaces src/cpu/ops/transpose.cpp:17-68. */
+int vm_hip_transpose_f32(const float* x, float* y, int rank, const int64_t* in_shape,
+                         const int* perm, void* stream);
+
+/* Strided slice: y[o] = x[begins + o * steps] per axis, with begins and
+ * out_shape already clamped as the reference's signature clamps them.
+ * Replaces src/cpu/ops/slice.cpp:21-110. */
+int vm_hip_slice_f32(const float* x, float* y, int rank, const int64_t* in_shape,
+                     const int64_t* begins, const int64_t* steps, const int64_t* out_shape,
+                     void* stream);
+
+/* Concat of two tensors along one axis: for each of `outer` leading
+ * indices, a's block of a_block elements then b's of b_block.  Replaces
+ * src/cpu/ops/concat.cpp:19-72. */
+int vm_hip_concat_f32(const float* a, const float* b, float* y, int64_t outer, int64_t a_block,
+                      int64_t b_block, void* stream);
+
+/* Repeat heads: x [outer, kv_heads, inner] -> y [outer, kv_heads * repeats,
+ * inner], output head h copying input head h / repeats.  Replaces
+ * src/cpu/ops/repeat_kv.cpp:20-62. */
+int vm_hip_repeat_kv_f32(const float* x, float* y, int64_t outer, int64_t kv_heads,
+                         int64_t repeats, int64_t inner, void* stream);
+
+/* Elementwise y = a + b, a * b or sigmoid(a) over n elements.  Replace
+ * src/cpu/ops/add.cpp:16-26, mul.cpp:16-26 and sigmoid.cpp:17-27. */
+#define VM_HIP_EW_ADD     0
+#define VM_HIP_EW_MUL     1
+#define VM_HIP_EW_SIGMOID 2
+int vm_hip_elementwise_f32(int op, const float* a, const float* b, float* y, int64_t n,
+                           void* stream);
+
+/* Softmax along one axis of a tensor viewed as [outer, cols, inner].
+ * Replaces src/cpu/ops/softmax.cpp:18-48. */
+int vm_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t cols, int64_t inner,
+                       void* stream);
+
+/* Batched matrix product C[b] = A[b] B[b], A [batch, m, k], B [batch, k, n],
+ * C [batch, m, n], fp32 throughout.  Replaces the fp32 path of
+ * src/cpu/ops/matmul.cpp (equal batch dimensions, shape_helpers.h:36-84). */
+int vm_hip_matmul_f32(const float* a, const float* b, float* c, int64_t batch, int64_t m,
+                      int64_t k, int64_t n, void* stream);
+
+/* Attention with grouped KV heads: q [batch, hq, sq, d], k [batch, hk, sk,
+ * d], v [batch, hk, sk, dv] -> o [batch, hq, sq, dv]; query head h reads KV
+ * head h / (hq / hk).  scale <= 0 means 1/sqrt(d).  With `causal`, query
+ * row i sees keys 0 .. sk - sq + i.  Replaces
+ * src/cpu/ops/fused_attention.cpp:22-138. */
+int vm_hip_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t batch,
+                         int64_t hq, int64_t hk, int64_t sq, int64_t sk, int64_t d, int64_t dv,
+                         float scale, int causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

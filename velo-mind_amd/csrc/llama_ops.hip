@@ -1,0 +1,481 @@
+// The LLaMA graph's other operators on gfx950 (fp32, contiguous tensors):
+// everything the reference's decode/prefill graph
+// (examples/common/llama/llama_graph.cpp:14-304) runs besides
+// QuantizedMatMul.  Semantics follow the reference's CPU kernels
+// (src/cpu/ops/*.cpp, cited per entry point in include/vm_hip.h).
+//
+// All of these move a few KB to a few MB per call, so they are simple
+// grid-stride kernels with 16-byte accesses where the shapes allow; the
+// exception is attention, which keeps each query row's scores in LDS.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "vm_hip.h"
+#include "vm_internal.h"
+
+namespace vmhip {
+namespace {
+
+constexpr int kT = 256;
+
+int grid_for(int64_t work) {
+    const int64_t b = (work + kT - 1) / kT;
+    return static_cast<int>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+// ---- Embedding: out[i, :] = table[idx[i], :] (embedding.cpp:17-33).
+// Rows of out-of-range indices are zero; the executor rejects such indices
+// before launching (executable.cpp:54-66).
+__global__ void embedding_kernel(const float* __restrict__ table, int64_t vocab, int64_t hidden,
+                                 const int32_t* __restrict__ idx, int64_t count, float* __restrict__ out) {
+    const int64_t total = count * hidden;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * kT) {
+        const int64_t i = e / hidden;
+        const int64_t j = e - i * hidden;
+        const int64_t t = idx[i];
+        out[e] = (t >= 0 && t < vocab) ? table[t * hidden + j] : 0.0f;
+    }
+}
+
+// ---- RMSNorm over the last axis: y = x / sqrt(mean(x^2) + eps) * w
+// (rmsnorm.cpp:17-60), one workgroup per row.
+__global__ __launch_bounds__(kT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                     float* __restrict__ y, int64_t dim, float eps) {
+    __shared__ float part[kT / 64];
+    const float* xr = x + blockIdx.x * dim;
+    float* yr = y + blockIdx.x * dim;
+    float s = 0.0f;
+    for (int64_t i = threadIdx.x; i < dim; i += kT) s = fmaf(xr[i], xr[i], s);
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kT / 64; ++i) tot += part[i];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(dim) + eps);
+    for (int64_t i = threadIdx.x; i < dim; i += kT) yr[i] = xr[i] * inv * w[i];
+}
+
+// ---- Rotary embedding on rows of head_dim (rotary_embedding.cpp:17-45):
+// the first and second halves rotate by (cos, sin) of position
+// row % cos_rows.
+__global__ void rope_kernel(const float* __restrict__ x, const float* __restrict__ cs, const float* __restrict__ sn,
+                            float* __restrict__ y, int64_t rows, int64_t head_dim, int64_t cos_rows) {
+    const int64_t half = head_dim / 2;
+    const int64_t total = rows * half;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * kT) {
+        const int64_t r = e / half;
+        const int64_t j = e - r * half;
+        const int64_t pos = cos_rows > 1 ? r % cos_rows : 0;
+        const float a = x[r * head_dim + j];
+        const float b = x[r * head_dim + j + half];
+        const float c = cs[pos * half + j];
+        const float s = sn[pos * half + j];
+        y[r * head_dim + j] = a * c - b * s;
+        y[r * head_dim + j + half] = b * c + a * s;
+    }
+}
+
+// ---- Up to rank-6 index arithmetic for transpose and slice.
+struct Dims {
+    int rank;
+    int64_t out_shape[6];
+    int64_t in_step[6];   // input offset per unit step of each OUTPUT axis
+    int64_t in_base;
+};
+
+__global__ void gather_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t total, Dims d) {
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * kT) {
+        int64_t rem = e;
+        int64_t off = d.in_base;
+        for (int ax = d.rank - 1; ax >= 0; --ax) {
+            const int64_t c = rem % d.out_shape[ax];
+            rem /= d.out_shape[ax];
+            off += c * d.in_step[ax];
+        }
+        y[e] = x[off];
+    }
+}
+
+// ---- Concat of two tensors along an axis (concat.cpp:17-60): per outer
+// index, a's block then b's block.
+__global__ void concat_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ y,
+                              int64_t outer, int64_t a_block, int64_t b_block) {
+    const int64_t o_block = a_block + b_block;
+    const int64_t total = outer * o_block;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * kT) {
+        const int64_t o = e / o_block;
+        const int64_t r = e - o * o_block;
+        y[e] = r < a_block ? a[o * a_block + r] : b[o * b_block + (r - a_block)];
+    }
+}
+
+// ---- RepeatKV (repeat_kv.cpp:17-56): head h of the output copies input
+// head h / repeats.
+__global__ void repeat_kv_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t outer, int64_t kv_heads,
+                                 int64_t repeats, int64_t inner) {
+    const int64_t q_heads = kv_heads * repeats;
+    const int64_t total = outer * q_heads * inner;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * kT) {
+        const int64_t t = e % inner;
+        const int64_t h = (e / inner) % q_heads;
+        const int64_t o = e / (inner * q_heads);
+        y[e] = x[(o * kv_heads + h / repeats) * inner + t];
+    }
+}
+
+// ---- Elementwise Add / Mul / Sigmoid (add.cpp, mul.cpp, sigmoid.cpp).
+__global__ void elementwise_kernel(int op, const float* __restrict__ a, const float* __restrict__ b,
+                                   float* __restrict__ y, int64_t n) {
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < n;
+         e += static_cast<int64_t>(gridDim.x) * kT) {
+        const float x = a[e];
+        float r;
+        if (op == VM_HIP_EW_ADD) r = x + b[e];
+        else if (op == VM_HIP_EW_MUL) r = x * b[e];
+        else r = 1.0f / (1.0f + expf(-x));
+        y[e] = r;
+    }
+}
+
+// ---- Softmax along an axis of [outer, cols, inner] (softmax.cpp:18-48).
+// inner == 1: one wave per row, lanes over the columns.  Otherwise one
+// thread per (outer, inner) row walks its strided column.
+__global__ __launch_bounds__(kT) void softmax_rows_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                          int64_t rows, int64_t cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = blockIdx.x * static_cast<int64_t>(kT / 64) + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* xr = x + r * cols;
+    float* yr = y + r * cols;
+    float mx = -INFINITY;
+    for (int64_t j = lane; j < cols; j += 64) mx = fmaxf(mx, xr[j]);
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    float sum = 0.0f;
+    for (int64_t j = lane; j < cols; j += 64) sum += expf(xr[j] - mx);
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    for (int64_t j = lane; j < cols; j += 64) yr[j] = expf(xr[j] - mx) / sum;
+}
+
+__global__ void softmax_strided_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t outer,
+                                       int64_t cols, int64_t inner) {
+    const int64_t rows = outer * inner;
+    for (int64_t r = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; r < rows;
+         r += static_cast<int64_t>(gridDim.x) * kT) {
+        const int64_t base = (r / inner) * cols * inner + r % inner;
+        float mx = x[base];
+        for (int64_t j = 1; j < cols; ++j) mx = fmaxf(mx, x[base + j * inner]);
+        float sum = 0.0f;
+        for (int64_t j = 0; j < cols; ++j) sum += expf(x[base + j * inner] - mx);
+        for (int64_t j = 0; j < cols; ++j) y[base + j * inner] = expf(x[base + j * inner] - mx) / sum;
+    }
+}
+
+// ---- Batched fp32 matrix product C[b] = A[b] B[b] (matmul.cpp, fp32 path).
+// 64x64 output tile per workgroup, 4x4 per thread, K in steps of 16 through
+// LDS.  fp32 FMA keeps the result within rounding of the reference's fp32
+// dot products.
+constexpr int kMmTile = 64;
+constexpr int kMmK = 16;
+
+__global__ __launch_bounds__(kT) void matmul_f32_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                        float* __restrict__ c, int64_t m, int64_t k, int64_t n) {
+    __shared__ float sA[kMmK][kMmTile + 4];
+    __shared__ float sB[kMmK][kMmTile + 4];
+    const int64_t bat = blockIdx.z;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.y) * kMmTile;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kMmTile;
+    const float* ab = a + bat * m * k;
+    const float* bb = b + bat * k * n;
+    float* cb = c + bat * m * n;
+    const int tx = threadIdx.x & 15;   // column group
+    const int ty = threadIdx.x >> 4;   // row group
+    float acc[4][4] = {};
+    for (int64_t k0 = 0; k0 < k; k0 += kMmK) {
+        // A tile: 64 rows x 16 k, stored transposed (k-major) in LDS.
+        for (int e = threadIdx.x; e < kMmTile * kMmK; e += kT) {
+            const int r = e / kMmK, kk = e % kMmK;
+            const int64_t gr = row0 + r, gk = k0 + kk;
+            sA[kk][r] = (gr < m && gk < k) ? ab[gr * k + gk] : 0.0f;
+        }
+        for (int e = threadIdx.x; e < kMmTile * kMmK; e += kT) {
+            const int kk = e / kMmTile, cc = e % kMmTile;
+            const int64_t gk = k0 + kk, gc = col0 + cc;
+            sB[kk][cc] = (gk < k && gc < n) ? bb[gk * n + gc] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kMmK; ++kk) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = sA[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = sB[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t gr = row0 + ty * 4 + i;
+        if (gr >= m) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t gc = col0 + tx * 4 + j;
+            if (gc < n) cb[gr * n + gc] = acc[i][j];
+        }
+    }
+}
+
+// ---- Attention with grouped KV heads (fused_attention.cpp:20-139): one
+// wave per query row.  Scores of the row's visible keys go to LDS (lanes
+// over keys), softmax with the row maximum, then lanes over the value
+// dimension accumulate p_j * v_j.  Query head h reads KV head h / (Hq / Hk);
+// causal rows see keys 0 .. Sk - Sq + i.
+__global__ __launch_bounds__(64) void attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                       const float* __restrict__ v, float* __restrict__ o,
+                                                       int64_t hq, int64_t hk, int64_t sq, int64_t sk, int64_t d,
+                                                       int64_t dv, float scale, int causal) {
+    extern __shared__ float sh[];
+    float* qs = sh;          // [d]
+    float* sc = sh + d;      // [sk]
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;              // (batch, head, query row)
+    const int64_t i = row % sq;
+    const int64_t bh = row / sq;
+    const int64_t h = bh % hq;
+    const int64_t bidx = bh / hq;
+    const int64_t g = hq / hk;
+    const int64_t hkv = h / g;
+    const float* qr = q + row * d;
+    const float* kb = k + (bidx * hk + hkv) * sk * d;
+    const float* vb = v + (bidx * hk + hkv) * sk * dv;
+    float* orow = o + row * dv;
+
+    int64_t valid = sk;
+    if (causal) {
+        valid = sk - sq + i + 1;
+        valid = valid < 0 ? 0 : (valid > sk ? sk : valid);
+    }
+    for (int64_t t = lane; t < d; t += 64) qs[t] = qr[t];
+    __syncthreads();
+    if (valid == 0) {
+        for (int64_t t = lane; t < dv; t += 64) orow[t] = 0.0f;
+        return;
+    }
+    float mx = -INFINITY;
+    for (int64_t j = lane; j < valid; j += 64) {
+        const float* kr = kb + j * d;
+        float dot = 0.0f;
+        for (int64_t t = 0; t < d; ++t) dot = fmaf(qs[t], kr[t], dot);
+        const float s = dot * scale;
+        sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    float sum = 0.0f;
+    for (int64_t j = lane; j < valid; j += 64) {
+        const float p = expf(sc[j] - mx);
+        sc[j] = p;
+        sum += p;
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    __syncthreads();
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    for (int64_t t = lane; t < dv; t += 64) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < valid; ++j) acc = fmaf(sc[j], vb[j * dv + t], acc);
+        orow[t] = acc * inv;
+    }
+}
+
+}  // namespace
+}  // namespace vmhip
+
+using namespace vmhip;
+
+namespace {
+
+hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int vm_hip_embedding_f32(const float* table, int64_t vocab, int64_t hidden, const int32_t* idx, int64_t count,
+                         float* out, void* stream) {
+    clear_error();
+    if (vocab < 0 || hidden < 0 || count < 0) return fail_inval("Embedding: negative size");
+    if (count == 0 || hidden == 0) return 0;
+    if (!table || !idx || !out) return fail_inval("Embedding: null pointer");
+    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(count * hidden)), dim3(kT), 0, S(stream), table, vocab, hidden,
+                       idx, count, out);
+    return check_launch("Embedding", S(stream));
+}
+
+int vm_hip_rmsnorm_f32(const float* x, const float* w, float* y, int64_t rows, int64_t dim, float eps, void* stream) {
+    clear_error();
+    if (rows < 0 || dim < 0) return fail_inval("RMSNorm: negative size");
+    if (rows == 0 || dim == 0) return 0;
+    if (!x || !w || !y) return fail_inval("RMSNorm: null pointer");
+    if (rows > 0x7fffffff) return fail_inval("RMSNorm: too many rows");
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kT), 0, S(stream), x, w, y, dim, eps);
+    return check_launch("RMSNorm", S(stream));
+}
+
+int vm_hip_rope_f32(const float* x, const float* cos_table, const float* sin_table, float* y, int64_t rows,
+                    int64_t head_dim, int64_t cos_rows, void* stream) {
+    clear_error();
+    if (rows < 0 || head_dim < 0 || cos_rows < 1 || head_dim % 2 != 0) return fail_inval("RotaryEmbedding: bad shape");
+    if (rows == 0 || head_dim == 0) return 0;
+    if (!x || !cos_table || !sin_table || !y) return fail_inval("RotaryEmbedding: null pointer");
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(rows * head_dim / 2)), dim3(kT), 0, S(stream), x, cos_table,
+                       sin_table, y, rows, head_dim, cos_rows);
+    return check_launch("RotaryEmbedding", S(stream));
+}
+
+int vm_hip_transpose_f32(const float* x, float* y, int rank, const int64_t* in_shape, const int* perm, void* stream) {
+    clear_error();
+    if (rank < 1 || rank > 6 || !in_shape) return fail_inval("Transpose: rank must be 1..6");
+    Dims d{};
+    d.rank = rank;
+    int64_t in_stride[6];
+    int64_t total = 1;
+    int64_t stride = 1;
+    for (int ax = rank - 1; ax >= 0; --ax) {
+        if (in_shape[ax] < 0) return fail_inval("Transpose: negative dimension");
+        in_stride[ax] = stride;
+        stride *= in_shape[ax] > 0 ? in_shape[ax] : 1;
+    }
+    bool seen[6] = {false, false, false, false, false, false};
+    for (int ax = 0; ax < rank; ++ax) {
+        const int p = perm ? perm[ax] : rank - 1 - ax;
+        if (p < 0 || p >= rank || seen[p]) return fail_inval("Transpose: invalid permutation");
+        seen[p] = true;
+        d.out_shape[ax] = in_shape[p];
+        d.in_step[ax] = in_stride[p];
+        total *= in_shape[p];
+    }
+    if (total == 0) return 0;
+    if (!x || !y) return fail_inval("Transpose: null pointer");
+    hipLaunchKernelGGL(gather_kernel, dim3(grid_for(total)), dim3(kT), 0, S(stream), x, y, total, d);
+    return check_launch("Transpose", S(stream));
+}
+
+int vm_hip_slice_f32(const float* x, float* y, int rank, const int64_t* in_shape, const int64_t* begins,
+                     const int64_t* steps, const int64_t* out_shape, void* stream) {
+    clear_error();
+    if (rank < 1 || rank > 6 || !in_shape || !begins || !steps || !out_shape)
+        return fail_inval("Slice: rank must be 1..6");
+    Dims d{};
+    d.rank = rank;
+    int64_t stride = 1, total = 1;
+    for (int ax = rank - 1; ax >= 0; --ax) {
+        if (out_shape[ax] < 0 || steps[ax] < 1 || begins[ax] < 0) return fail_inval("Slice: bad bounds");
+        if (out_shape[ax] > 0 && begins[ax] + (out_shape[ax] - 1) * steps[ax] >= in_shape[ax])
+            return fail_inval("Slice: out of range");
+        d.out_shape[ax] = out_shape[ax];
+        d.in_step[ax] = steps[ax] * stride;
+        d.in_base += begins[ax] * stride;
+        stride *= in_shape[ax];
+        total *= out_shape[ax];
+    }
+    if (total == 0) return 0;
+    if (!x || !y) return fail_inval("Slice: null pointer");
+    hipLaunchKernelGGL(gather_kernel, dim3(grid_for(total)), dim3(kT), 0, S(stream), x, y, total, d);
+    return check_launch("Slice", S(stream));
+}
+
+int vm_hip_concat_f32(const float* a, const float* b, float* y, int64_t outer, int64_t a_block, int64_t b_block,
+                      void* stream) {
+    clear_error();
+    if (outer < 0 || a_block < 0 || b_block < 0) return fail_inval("Concat: negative size");
+    if (outer == 0 || a_block + b_block == 0) return 0;
+    if ((a_block && !a) || (b_block && !b) || !y) return fail_inval("Concat: null pointer");
+    hipLaunchKernelGGL(concat_kernel, dim3(grid_for(outer * (a_block + b_block))), dim3(kT), 0, S(stream), a, b, y,
+                       outer, a_block, b_block);
+    return check_launch("Concat", S(stream));
+}
+
+int vm_hip_repeat_kv_f32(const float* x, float* y, int64_t outer, int64_t kv_heads, int64_t repeats, int64_t inner,
+                         void* stream) {
+    clear_error();
+    if (outer < 0 || kv_heads < 0 || repeats < 1 || inner < 0) return fail_inval("RepeatKV: bad shape");
+    if (outer == 0 || kv_heads == 0 || inner == 0) return 0;
+    if (!x || !y) return fail_inval("RepeatKV: null pointer");
+    hipLaunchKernelGGL(repeat_kv_kernel, dim3(grid_for(outer * kv_heads * repeats * inner)), dim3(kT), 0, S(stream),
+                       x, y, outer, kv_heads, repeats, inner);
+    return check_launch("RepeatKV", S(stream));
+}
+
+int vm_hip_elementwise_f32(int op, const float* a, const float* b, float* y, int64_t n, void* stream) {
+    clear_error();
+    if (op != VM_HIP_EW_ADD && op != VM_HIP_EW_MUL && op != VM_HIP_EW_SIGMOID) return fail_inval("elementwise: bad op");
+    if (n < 0) return fail_inval("elementwise: negative size");
+    if (n == 0) return 0;
+    if (!a || !y || (op != VM_HIP_EW_SIGMOID && !b)) return fail_inval("elementwise: null pointer");
+    hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(n)), dim3(kT), 0, S(stream), op, a, b, y, n);
+    return check_launch(op == VM_HIP_EW_ADD ? "Add" : op == VM_HIP_EW_MUL ? "Mul" : "Sigmoid", S(stream));
+}
+
+int vm_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t cols, int64_t inner, void* stream) {
+    clear_error();
+    if (outer < 0 || cols < 0 || inner < 0) return fail_inval("Softmax: negative size");
+    if (outer == 0 || cols == 0 || inner == 0) return 0;
+    if (!x || !y) return fail_inval("Softmax: null pointer");
+    if (inner == 1) {
+        const int64_t blocks = (outer + kT / 64 - 1) / (kT / 64);
+        if (blocks > 0x7fffffff) return fail_inval("Softmax: too many rows");
+        hipLaunchKernelGGL(softmax_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kT), 0, S(stream), x, y,
+                           outer, cols);
+    } else {
+        hipLaunchKernelGGL(softmax_strided_kernel, dim3(grid_for(outer * inner)), dim3(kT), 0, S(stream), x, y, outer,
+                           cols, inner);
+    }
+    return check_launch("Softmax", S(stream));
+}
+
+int vm_hip_matmul_f32(const float* a, const float* b, float* c, int64_t batch, int64_t m, int64_t k, int64_t n,
+                      void* stream) {
+    clear_error();
+    if (batch < 0 || m < 0 || k < 0 || n < 0) return fail_inval("MatMul: negative size");
+    if (batch == 0 || m == 0 || n == 0) return 0;
+    if (!a || !b || !c) return fail_inval("MatMul: null pointer");
+    const int64_t gx = (n + kMmTile - 1) / kMmTile, gy = (m + kMmTile - 1) / kMmTile;
+    if (gx > 0x7fffffff || gy > 65535 || batch > 65535) return fail_inval("MatMul: grid too large");
+    hipLaunchKernelGGL(matmul_f32_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy),
+                                               static_cast<unsigned>(batch)),
+                       dim3(kT), 0, S(stream), a, b, c, m, k, n);
+    return check_launch("MatMul", S(stream));
+}
+
+int vm_hip_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t hq,
+                         int64_t hk, int64_t sq, int64_t sk, int64_t d, int64_t dv, float scale, int causal,
+                         void* stream) {
+    clear_error();
+    if (batch < 0 || hq < 0 || hk < 1 || sq < 0 || sk < 0 || d < 1 || dv < 1 || hq % hk != 0)
+        return fail_inval("FusedAttention: bad shape");
+    if (causal && sk < sq) return fail_inval("FusedAttention: causal attention requires Sk >= Sq");
+    const int64_t rows = batch * hq * sq;
+    if (rows == 0) return 0;
+    if (!q || !o || (sk > 0 && (!k || !v))) return fail_inval("FusedAttention: null pointer");
+    const int64_t lds = (d + sk) * static_cast<int64_t>(sizeof(float));
+    if (lds > 64 * 1024) return fail_inval("FusedAttention: Sk + D exceeds 16384 on this kernel");
+    if (rows > 0x7fffffff) return fail_inval("FusedAttention: too many rows");
+    const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(d));
+    hipLaunchKernelGGL(attention_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), static_cast<size_t>(lds),
+                       S(stream), q, k, v, o, hq, hk, sq, sk, d, dv, sc, causal ? 1 : 0);
+    return check_launch("FusedAttention", S(stream));
+}
+
+}  // extern "C"

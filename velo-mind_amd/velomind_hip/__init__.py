@@ -64,6 +64,17 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_dequant_int8": ([p, p, p, c_int64, c_int64, p], c_int),
         "vm_hip_dequant_int4": ([p, p, p, c_int64, c_int64, c_int64, p], c_int),
         "vm_hip_half_to_f32": ([p, c_int, p, c_int64, p], c_int),
+        "vm_hip_embedding_f32": ([p, c_int64, c_int64, p, c_int64, p, p], c_int),
+        "vm_hip_rmsnorm_f32": ([p, p, p, c_int64, c_int64, c_float, p], c_int),
+        "vm_hip_rope_f32": ([p, p, p, p, c_int64, c_int64, c_int64, p], c_int),
+        "vm_hip_transpose_f32": ([p, p, c_int, p, p, p], c_int),
+        "vm_hip_slice_f32": ([p, p, c_int, p, p, p, p, p], c_int),
+        "vm_hip_concat_f32": ([p, p, p, c_int64, c_int64, c_int64, p], c_int),
+        "vm_hip_repeat_kv_f32": ([p, p, c_int64, c_int64, c_int64, c_int64, p], c_int),
+        "vm_hip_elementwise_f32": ([c_int, p, p, p, c_int64, p], c_int),
+        "vm_hip_softmax_f32": ([p, p, c_int64, c_int64, c_int64, p], c_int),
+        "vm_hip_matmul_f32": ([p, p, p, c_int64, c_int64, c_int64, c_int64, p], c_int),
+        "vm_hip_attention_f32": ([p, p, p, p] + [c_int64] * 7 + [c_float, c_int, p], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -80,7 +91,10 @@ def exported_symbols() -> list[str]:
             "vm_hip_event_destroy", "vm_hip_event_record", "vm_hip_event_synchronize",
             "vm_hip_event_elapsed_ms", "vm_hip_stream_begin_capture", "vm_hip_stream_end_capture",
             "vm_hip_graph_launch", "vm_hip_graph_destroy", "vm_hip_qmm_f32", "vm_hip_qmm", "vm_hip_pack_int8",
-            "vm_hip_pack_int4", "vm_hip_dequant_int8", "vm_hip_dequant_int4", "vm_hip_half_to_f32"]
+            "vm_hip_pack_int4", "vm_hip_dequant_int8", "vm_hip_dequant_int4", "vm_hip_half_to_f32",
+            "vm_hip_embedding_f32", "vm_hip_rmsnorm_f32", "vm_hip_rope_f32", "vm_hip_transpose_f32",
+            "vm_hip_slice_f32", "vm_hip_concat_f32", "vm_hip_repeat_kv_f32", "vm_hip_elementwise_f32",
+            "vm_hip_softmax_f32", "vm_hip_matmul_f32", "vm_hip_attention_f32"]
 
 
 def open_library() -> ctypes.CDLL:
@@ -304,3 +318,120 @@ def run_pack_int4(w: np.ndarray, block: int = 32):
     ds = DeviceBuffer(max(4, nb * cols * 4))
     pack_int4(dw.addr, dq.addr, ds.addr, rows, cols, block)
     return dq.download(np.uint8, (prow, cols)), ds.download(np.float32, (nb, cols))
+
+
+# ---- LLaMA graph operators, numpy level (one call each, null stream) ----
+
+EW_ADD, EW_MUL, EW_SIGMOID = 0, 1, 2
+
+
+def _dev(a: np.ndarray, dtype=np.float32) -> DeviceBuffer:
+    return DeviceBuffer.from_array(np.ascontiguousarray(a, dtype))
+
+
+def _out(shape) -> DeviceBuffer:
+    return DeviceBuffer(max(4, int(np.prod(shape)) * 4))
+
+
+def _i64(vals) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(vals, np.int64))
+
+
+def run_embedding(table: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    idx = np.ascontiguousarray(idx, np.int32)
+    shape = idx.shape + (table.shape[1],)
+    dt, di, do = _dev(table), _dev(idx.reshape(-1) if idx.size else np.zeros(1, np.int32), np.int32), _out(shape)
+    check(open_library().vm_hip_embedding_f32(dt.ptr, table.shape[0], table.shape[1], di.ptr, idx.size, do.ptr, None))
+    return do.download(np.float32, shape)
+
+
+def run_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    dx, dw, dy = _dev(x), _dev(w), _out(x.shape)
+    check(open_library().vm_hip_rmsnorm_f32(dx.ptr, dw.ptr, dy.ptr, x.size // x.shape[-1], x.shape[-1], eps, None))
+    return dy.download(np.float32, x.shape)
+
+
+def run_rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    d = x.shape[-1]
+    cos_rows = cos.shape[0] if cos.ndim >= 2 else 1
+    dx, dc, ds, dy = _dev(x), _dev(cos), _dev(sin), _out(x.shape)
+    check(open_library().vm_hip_rope_f32(dx.ptr, dc.ptr, ds.ptr, dy.ptr, x.size // d, d, cos_rows, None))
+    return dy.download(np.float32, x.shape)
+
+
+def run_transpose(x: np.ndarray, perm=None) -> np.ndarray:
+    perm_eff = tuple(perm) if perm else tuple(reversed(range(x.ndim)))
+    out_shape = tuple(x.shape[p] for p in perm_eff)
+    dx, dy = _dev(x), _out(out_shape)
+    shape = _i64(x.shape)
+    perm_arr = np.ascontiguousarray(np.asarray(perm_eff, np.int32))
+    check(open_library().vm_hip_transpose_f32(dx.ptr, dy.ptr, x.ndim, shape.ctypes.data,
+                                              perm_arr.ctypes.data if perm else None, None))
+    return dy.download(np.float32, out_shape)
+
+
+def run_slice(x: np.ndarray, begins, steps, out_shape) -> np.ndarray:
+    dx, dy = _dev(x), _out(out_shape)
+    a, b, c, d = _i64(x.shape), _i64(begins), _i64(steps), _i64(out_shape)
+    check(open_library().vm_hip_slice_f32(dx.ptr, dy.ptr, x.ndim, a.ctypes.data, b.ctypes.data, c.ctypes.data,
+                                          d.ctypes.data, None))
+    return dy.download(np.float32, tuple(out_shape))
+
+
+def run_concat(a: np.ndarray, b: np.ndarray, axis: int) -> np.ndarray:
+    axis = axis % a.ndim
+    outer = int(np.prod(a.shape[:axis]))
+    ab = int(np.prod(a.shape[axis:]))
+    bb = int(np.prod(b.shape[axis:]))
+    shape = list(a.shape)
+    shape[axis] += b.shape[axis]
+    da, db, dy = _dev(a), _dev(b), _out(shape)
+    check(open_library().vm_hip_concat_f32(da.ptr, db.ptr, dy.ptr, outer, ab, bb, None))
+    return dy.download(np.float32, tuple(shape))
+
+
+def run_repeat_kv(x: np.ndarray, repeats: int, axis: int) -> np.ndarray:
+    axis = axis % x.ndim
+    outer = int(np.prod(x.shape[:axis]))
+    inner = int(np.prod(x.shape[axis + 1:]))
+    shape = list(x.shape)
+    shape[axis] *= repeats
+    dx, dy = _dev(x), _out(shape)
+    check(open_library().vm_hip_repeat_kv_f32(dx.ptr, dy.ptr, outer, x.shape[axis], repeats, inner, None))
+    return dy.download(np.float32, tuple(shape))
+
+
+def run_elementwise(op: int, a: np.ndarray, b: np.ndarray | None = None) -> np.ndarray:
+    da, dy = _dev(a), _out(a.shape)
+    db = _dev(b) if b is not None else None
+    check(open_library().vm_hip_elementwise_f32(op, da.ptr, db.ptr if db else None, dy.ptr, a.size, None))
+    return dy.download(np.float32, a.shape)
+
+
+def run_softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
+    axis = axis % x.ndim
+    outer = int(np.prod(x.shape[:axis]))
+    inner = int(np.prod(x.shape[axis + 1:]))
+    dx, dy = _dev(x), _out(x.shape)
+    check(open_library().vm_hip_softmax_f32(dx.ptr, dy.ptr, outer, x.shape[axis], inner, None))
+    return dy.download(np.float32, x.shape)
+
+
+def run_matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    batch = int(np.prod(a.shape[:-2]))
+    m, k, n = a.shape[-2], a.shape[-1], b.shape[-1]
+    shape = a.shape[:-1] + (n,)
+    da, db, dc = _dev(a), _dev(b), _out(shape)
+    check(open_library().vm_hip_matmul_f32(da.ptr, db.ptr, dc.ptr, batch, m, k, n, None))
+    return dc.download(np.float32, shape)
+
+
+def run_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool) -> np.ndarray:
+    hq, sq, d = q.shape[-3:]
+    hk, sk, dv = k.shape[-3], k.shape[-2], v.shape[-1]
+    batch = int(np.prod(q.shape[:-3]))
+    shape = q.shape[:-1] + (dv,)
+    dq, dk, dvv, do = _dev(q), _dev(k), _dev(v), _out(shape)
+    check(open_library().vm_hip_attention_f32(dq.ptr, dk.ptr, dvv.ptr, do.ptr, batch, hq, hk, sq, sk, d, dv,
+                                              scale, 1 if causal else 0, None))
+    return do.download(np.float32, shape)
