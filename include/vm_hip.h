@@ -258,6 +258,76 @@ int vm_hip_attention_f32(const float* q, const float* k, const float* v, float* 
                          int64_t hq, int64_t hk, int64_t sq, int64_t sk, int64_t d, int64_t dv,
                          float scale, int causal, void* stream);
 
+/* ---- the resident decoder (velomind::examples::llama::HipLlamaDecoder) ---
+ * Fused forms of reference graph nodes for a decoder that keeps its KV
+ * cache resident ([Hkv, max_seq, D] per layer, appended in place) and reads
+ * the current position from device memory (`pos`, one int32), so one
+ * decode step is a fixed launch sequence a HIP graph can replay.  The
+ * reference has no such entry points: its engine rebuilds the graph every
+ * token (examples/common/llama/llama_engine.cpp:395-455); each one below
+ * names the graph nodes it computes. */
+
+/* dst[i] ~ N(mean, stddev^2): SplitMix64 counter hash + Box-Muller; the
+ * same (seed, n) gives the same values on every call.  Synthetic weights
+ * (the reference's FillSyntheticFn, llama_engine.h:56-57). */
+int vm_hip_fill_normal_f32(float* dst, int64_t n, uint64_t seed, float mean, float stddev,
+                           void* stream);
+
+/* h[r] += delta[r] (skipped when delta is NULL), then
+ * hn[r] = rmsnorm(h[r]) * w: the residual Add followed by the next RMSNorm
+ * (llama_graph.cpp:121-127, add.cpp, rmsnorm.cpp:17-60). */
+int vm_hip_add_rmsnorm_f32(float* h, const float* delta, const float* w, float* hn, int64_t rows,
+                           int64_t dim, float eps, void* stream);
+
+/* From the fused projection qkv [rows, (heads + 2 kv_heads) * head_dim]
+ * (q heads, then k heads, then v heads) at positions p = *pos + r: RoPE on
+ * q into q_out [heads, rows, head_dim] and on k into k_cache at row p, v
+ * copied into v_cache at row p; caches [kv_heads, max_seq, head_dim];
+ * cos/sin tables [max_seq, head_dim / 2].  Replaces Reshape + Transpose +
+ * RotaryEmbedding + Concat of llama_graph.cpp:63-85, :296-300.  Rows with
+ * p >= max_seq are not written. */
+int vm_hip_rope_kv_append_f32(const float* qkv, int64_t rows, const float* cos_table,
+                              const float* sin_table, const int32_t* pos, float* q_out,
+                              float* k_cache, float* v_cache, int64_t heads, int64_t kv_heads,
+                              int64_t head_dim, int64_t max_seq, void* stream);
+
+/* One query row per head, q [heads, head_dim], at position *pos over keys
+ * 0..*pos of the caches; out [heads * head_dim].  Grouped heads are read
+ * directly (no RepeatKV); scale <= 0 means 1/sqrt(head_dim).  head_dim 64
+ * or 128, at most 16 query heads per KV head.  Replaces RepeatKV +
+ * FusedAttention (or MatMul/Softmax/MatMul) + Transpose + Reshape of a
+ * decode step (llama_graph.cpp:88-118, fused_attention.cpp:22-138). */
+int vm_hip_attention_decode_f32(const float* q, const float* k_cache, const float* v_cache,
+                                const int32_t* pos, float* out, int64_t heads, int64_t kv_heads,
+                                int64_t head_dim, int64_t max_seq, float scale, void* stream);
+
+/* Causal attention of q [heads, rows, head_dim] at positions *pos + i over
+ * the caches; out [rows, heads * head_dim] (token-major).  head_dim 64.
+ * The prefill counterpart of vm_hip_attention_decode_f32. */
+int vm_hip_attention_prefill_f32(const float* q, const float* k_cache, const float* v_cache,
+                                 const int32_t* pos, float* out, int64_t rows, int64_t heads,
+                                 int64_t kv_heads, int64_t head_dim, int64_t max_seq, float scale,
+                                 void* stream);
+
+/* out[r, j] = sigmoid(g) * g * u with g = gate_up[r, j] and
+ * u = gate_up[r, inter + j]: Sigmoid + Mul + Mul of the SwiGLU block
+ * (llama_graph.cpp:22-28) on the fused gate|up projection. */
+int vm_hip_silu_mul_f32(const float* gate_up, float* out, int64_t rows, int64_t inter,
+                        void* stream);
+
+/* *token_out = first index of the maximum of x[0..n) (NaN skipped), the
+ * reference's sample_argmax (examples/tinyllama/sample.cpp:18-38).  With
+ * pos != NULL the token is also written to tokens[*pos + 1] (when that is
+ * below max_seq and tokens != NULL) and *pos is incremented. */
+int vm_hip_argmax_f32(const float* x, int64_t n, int32_t* token_out, int32_t* pos,
+                      int32_t* tokens, int64_t max_seq, void* stream);
+
+/* Asynchronous 2-D device copy: `rows` rows of `width` bytes from src
+ * (row pitch spitch) to dst (row pitch dpitch).  Used to assemble fused
+ * weight matrices column block by column block. */
+int vm_hip_memcpy_2d_d2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
+                         size_t rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

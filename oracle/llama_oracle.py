@@ -363,15 +363,14 @@ def decode(cfg: LlamaConfig, w: LlamaWeights, token: int, pos: int, kv: dict, fu
 
 
 def greedy(cfg: LlamaConfig, w: LlamaWeights, prompt, steps: int, fused: bool = False):
-    """Prefill then `steps` greedy tokens (argmax, first maximum) as the
-    reference engine samples (examples/tinyllama/sample.cpp)."""
+    """Prefill, then `steps` decode steps with greedy sampling (first index
+    of the maximum, examples/tinyllama/sample.cpp:18-38): returns the
+    steps + 1 sampled tokens and the last logits."""
     logits, kv = prefill(cfg, w, prompt, last_only=True, fused=fused)
-    out = []
     pos = len(prompt)
-    tok = int(np.argmax(logits[-1]))
+    out = [int(np.argmax(logits[-1]))]
     for _ in range(steps):
-        out.append(tok)
-        logits = decode(cfg, w, tok, pos, kv, fused)
+        logits = decode(cfg, w, out[-1], pos, kv, fused)
         pos += 1
-        tok = int(np.argmax(logits[-1]))
+        out.append(int(np.argmax(logits[-1])))
     return out, logits

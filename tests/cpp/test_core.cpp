@@ -8,6 +8,7 @@
 #include <variant>
 
 #include "internal/registry/kernel.h"
+#include "internal/registry/shape.h"
 #include "test_helpers.h"
 
 using namespace velomind;
@@ -101,8 +102,23 @@ TEST_CASE("HIP registers the reference's five QuantizedMatMul dtype keys", "[cor
     }
     const std::vector<DataType> bad = {F32, I8, F16};
     REQUIRE(internal::resolve_op_kernel(Op::QuantizedMatMul, bad, F32, DeviceType::HIP) == nullptr);
-    REQUIRE(internal::resolve_op_kernel(Op::MatMul, std::vector<DataType>{F32, F32}, F32, DeviceType::HIP) == nullptr);
+    REQUIRE(internal::resolve_op_kernel(Op::MatMul, std::vector<DataType>{F16, F16}, F16, DeviceType::HIP) == nullptr);
     REQUIRE(internal::resolve_op_kernel(Op::QuantizedMatMul, keys[0].first, F32, DeviceType::CUDA) == nullptr);
+}
+
+TEST_CASE("HIP registers fp32 kernels for every operator of the LLaMA graph", "[core][registry]") {
+    const DataType F32 = DataType::Float32, I32 = DataType::Int32;
+    using V = std::vector<DataType>;
+    const std::vector<std::pair<Op, V>> ops = {
+        {Op::Embedding, {F32, I32}}, {Op::RMSNorm, {F32, F32}}, {Op::RotaryEmbedding, {F32, F32, F32}},
+        {Op::Reshape, {F32}}, {Op::Transpose, {F32}}, {Op::Slice, {F32}}, {Op::Concat, {F32, F32}},
+        {Op::RepeatKV, {F32}}, {Op::Add, {F32, F32}}, {Op::Mul, {F32, F32}}, {Op::Sigmoid, {F32}},
+        {Op::Softmax, {F32}}, {Op::MatMul, {F32, F32}}, {Op::FusedAttention, {F32, F32, F32}}};
+    for (const auto& [op, in] : ops) {
+        REQUIRE(internal::resolve_op_kernel(op, in, F32, DeviceType::HIP) != nullptr);
+        REQUIRE(internal::get_op_signature(op) != nullptr);
+    }
+    REQUIRE(internal::resolve_op_kernel(Op::Sub, V{F32, F32}, F32, DeviceType::HIP) == nullptr);
 }
 
 TEST_CASE("validate rejects a device without kernels and foreign handles", "[core][validation]") {

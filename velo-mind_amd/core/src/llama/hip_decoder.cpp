@@ -1,0 +1,369 @@
+// HipLlamaDecoder: the LLaMA forward pass of the reference graph
+// (examples/common/llama/llama_graph.cpp:14-330) as a resident decoder.
+//
+// Weights.  Q|K|V and gate|up are packed as single matrices
+// ([hidden, (H + 2 Hkv) D] and [hidden, 2 I]): quant.cpp packs every
+// column independently (per-column INT8 scales, per-column INT4 blocks), so
+// the packed fused matrix is byte for byte the three (two) packed matrices
+// side by side, and one GEMV reads all of them.
+//
+// Step.  One token (or a prompt) runs as
+//   embedding -> per layer [add+rmsnorm, QKV, rope+append, attention, O,
+//   add+rmsnorm, gate|up, silu*mul, down] -> add+rmsnorm -> lm_head -> argmax
+// with every position read from a device int32, so a decode step is a
+// fixed launch sequence that is captured once as a HIP graph and replayed
+// per token; the argmax writes the next token where the embedding reads it
+// and advances the position.
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "velomind/llama/llama_hip.h"
+#include "vm_hip.h"
+
+namespace velomind::examples::llama {
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != VM_HIP_OK) throw std::runtime_error(std::string("HipLlamaDecoder: ") + what + ": " + vm_hip_last_error());
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    std::size_t bytes = 0;
+    DevBuf() = default;
+    explicit DevBuf(std::size_t n) : bytes(n) {
+        if (n) check(vm_hip_malloc(&p, n), "allocation");
+    }
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr; }
+    DevBuf& operator=(DevBuf&& o) noexcept {
+        std::swap(p, o.p);
+        std::swap(bytes, o.bytes);
+        return *this;
+    }
+    ~DevBuf() {
+        if (p) (void)vm_hip_free(p);
+    }
+    template <typename T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+// One packed linear [k, n].
+struct Packed {
+    DevBuf codes, scales;
+    std::int64_t k = 0, n = 0;
+};
+
+}  // namespace
+
+struct HipLlamaDecoder::Impl {
+    Config cfg;
+    int qt = VM_HIP_QUANT_INT4;
+    int block = 32;
+    std::int64_t H = 0, Hk = 0, D = 0, hidden = 0, inter = 0, vocab = 0, qkv_n = 0;
+    std::size_t max_seq = 0;
+    void* stream = nullptr;
+    void* graph = nullptr;
+    void* ev0 = nullptr;
+    void* ev1 = nullptr;
+
+    // Weights.
+    std::vector<Packed> qkv, o, gate_up, down;
+    Packed lm_head;
+    std::shared_ptr<TensorStorage> embed, final_norm;
+    std::vector<std::shared_ptr<TensorStorage>> attn_norm, ffn_norm;
+    // KV cache [layers][Hkv][max_seq][D] for K, then V; RoPE tables [max_seq][D/2].
+    DevBuf kcache, vcache, cos_t, sin_t;
+    // Activations sized for max_seq rows.
+    DevBuf h, hn, qkv_out, q, ctx, attn_out, gu, act, down_out, logits;
+    DevBuf idx, token, pos, tokens;
+    std::size_t seq = 0;  // positions filled in the cache
+
+    float* kc(std::size_t l) const { return kcache.as<float>() + l * Hk * max_seq * D; }
+    float* vc(std::size_t l) const { return vcache.as<float>() + l * Hk * max_seq * D; }
+
+    void pack(Packed& dst, const float* w, std::int64_t k, std::int64_t n) {
+        dst.k = k;
+        dst.n = n;
+        if (qt == VM_HIP_QUANT_INT4) {
+            const std::int64_t nb = (k + block - 1) / block;
+            dst.codes = DevBuf(static_cast<std::size_t>((k + 1) / 2 * n));
+            dst.scales = DevBuf(static_cast<std::size_t>(nb * n * 4));
+            check(vm_hip_pack_int4(w, dst.codes.as<std::uint8_t>(), dst.scales.as<float>(), k, n, block, stream),
+                  "pack_int4");
+        } else {
+            dst.codes = DevBuf(static_cast<std::size_t>(k * n));
+            dst.scales = DevBuf(static_cast<std::size_t>(n * 4));
+            check(vm_hip_pack_int8(w, dst.codes.as<std::int8_t>(), dst.scales.as<float>(), k, n, stream),
+                  "pack_int8");
+        }
+    }
+
+    // Packs [k, n_1 + n_2 + ...] assembled column block by column block.
+    void pack_fused(Packed& dst, std::initializer_list<std::shared_ptr<TensorStorage>> parts, std::int64_t k) {
+        std::int64_t n = 0;
+        for (auto& p : parts) n += p->shape[1];
+        DevBuf tmp(static_cast<std::size_t>(k * n * 4));
+        std::int64_t col = 0;
+        for (auto& p : parts) {
+            const std::int64_t w = p->shape[1];
+            check(vm_hip_memcpy_2d_d2d(tmp.as<float>() + col, static_cast<std::size_t>(n * 4), p->data,
+                                       static_cast<std::size_t>(w * 4), static_cast<std::size_t>(w * 4),
+                                       static_cast<std::size_t>(k), stream),
+                  "fuse weights");
+            col += w;
+        }
+        pack(dst, tmp.as<float>(), k, n);
+        check(vm_hip_stream_synchronize(stream), "pack");  // tmp is freed on return
+    }
+
+    void qmm(const float* a, const Packed& w, float* c, std::int64_t rows) {
+        check(vm_hip_qmm_f32(a, static_cast<const std::int8_t*>(w.codes.p), w.scales.as<float>(), c, rows, w.k, w.n,
+                             qt, qt == VM_HIP_QUANT_INT4 ? block : 0, stream),
+              "quantized matmul");
+    }
+
+    // Layers over `rows` tokens whose first position is *pos; leaves the
+    // last row's logits in `logits`.
+    void forward(std::int64_t rows) {
+        const float eps = cfg.rms_norm_eps;
+        float* hp = h.as<float>();
+        float* hnp = hn.as<float>();
+        const auto* posp = pos.as<std::int32_t>();
+        check(vm_hip_embedding_f32(static_cast<const float*>(embed->data), vocab, hidden,
+                                   rows == 1 ? token.as<std::int32_t>() : idx.as<std::int32_t>(), rows, hp, stream),
+              "embedding");
+        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+            check(vm_hip_add_rmsnorm_f32(hp, l == 0 ? nullptr : down_out.as<float>(),
+                                         static_cast<const float*>(attn_norm[l]->data), hnp, rows, hidden, eps, stream),
+                  "add_rmsnorm");
+            qmm(hnp, qkv[l], qkv_out.as<float>(), rows);
+            check(vm_hip_rope_kv_append_f32(qkv_out.as<float>(), rows, cos_t.as<float>(), sin_t.as<float>(), posp,
+                                            q.as<float>(), kc(l), vc(l), H, Hk, D,
+                                            static_cast<std::int64_t>(max_seq), stream),
+                  "rope_kv_append");
+            if (rows == 1)
+                check(vm_hip_attention_decode_f32(q.as<float>(), kc(l), vc(l), posp, ctx.as<float>(), H, Hk, D,
+                                                  static_cast<std::int64_t>(max_seq), 1.0f, stream),
+                      "attention_decode");
+            else
+                check(vm_hip_attention_prefill_f32(q.as<float>(), kc(l), vc(l), posp, ctx.as<float>(), rows, H, Hk, D,
+                                                   static_cast<std::int64_t>(max_seq), 1.0f, stream),
+                      "attention_prefill");
+            qmm(ctx.as<float>(), o[l], attn_out.as<float>(), rows);
+            check(vm_hip_add_rmsnorm_f32(hp, attn_out.as<float>(), static_cast<const float*>(ffn_norm[l]->data), hnp,
+                                         rows, hidden, eps, stream),
+                  "add_rmsnorm");
+            qmm(hnp, gate_up[l], gu.as<float>(), rows);
+            check(vm_hip_silu_mul_f32(gu.as<float>(), act.as<float>(), rows, inter, stream), "silu_mul");
+            qmm(act.as<float>(), down[l], down_out.as<float>(), rows);
+        }
+        // Only the last row reaches the head (slice_last_token, llama_graph.cpp:141-158).
+        const std::int64_t last = (rows - 1) * hidden;
+        check(vm_hip_add_rmsnorm_f32(hp + last, down_out.as<float>() + last,
+                                     static_cast<const float*>(final_norm->data), hnp, 1, hidden, eps, stream),
+              "add_rmsnorm");
+        qmm(hnp, lm_head, logits.as<float>(), 1);
+    }
+
+    void set_pos(std::int64_t p) {
+        const std::int32_t v = static_cast<std::int32_t>(p);
+        check(vm_hip_memcpy_h2d(pos.p, &v, 4, stream), "position upload");
+    }
+};
+
+HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_type, int block_size,
+                                 std::size_t max_seq)
+    : _impl(std::make_unique<Impl>()), _max_seq(max_seq) {
+    auto& m = *_impl;
+    m.cfg = weights.config();
+    const Config& c = m.cfg;
+    if (quant_type == QuantType::None) throw std::invalid_argument("HipLlamaDecoder: weights must be quantized");
+    m.qt = quant_type == QuantType::Int4 ? VM_HIP_QUANT_INT4 : VM_HIP_QUANT_INT8;
+    if (m.qt == VM_HIP_QUANT_INT8 && block_size > 0)
+        throw std::invalid_argument("HipLlamaDecoder: INT8 weights are packed per column (block_size 0)");
+    m.block = m.qt == VM_HIP_QUANT_INT4 ? (block_size > 0 ? block_size : 32) : 0;
+    if (m.qt == VM_HIP_QUANT_INT4 && m.block % 2) throw std::invalid_argument("HipLlamaDecoder: INT4 block must be even");
+    m.H = static_cast<std::int64_t>(c.num_heads);
+    m.Hk = static_cast<std::int64_t>(c.effective_num_kv_heads());
+    m.D = static_cast<std::int64_t>(c.head_dim());
+    m.hidden = static_cast<std::int64_t>(c.hidden_size);
+    m.inter = static_cast<std::int64_t>(c.intermediate_size);
+    m.vocab = static_cast<std::int64_t>(c.vocab_size);
+    m.qkv_n = (m.H + 2 * m.Hk) * m.D;
+    m.max_seq = max_seq;
+    if (max_seq == 0 || max_seq > (1u << 20)) throw std::invalid_argument("HipLlamaDecoder: max_seq out of range");
+    if (m.D != 64 && m.D != 128) throw std::invalid_argument("HipLlamaDecoder: head_dim must be 64 or 128");
+    if (m.H / m.Hk > 16) throw std::invalid_argument("HipLlamaDecoder: at most 16 query heads per KV head");
+    check(vm_hip_stream_create(&m.stream), "stream");
+    check(vm_hip_event_create(&m.ev0), "event");
+    check(vm_hip_event_create(&m.ev1), "event");
+
+    using W = LlamaWeight;
+    m.embed = weights.storage(W::Embed);
+    m.final_norm = weights.storage(W::FinalNorm);
+    m.qkv.resize(c.num_layers);
+    m.o.resize(c.num_layers);
+    m.gate_up.resize(c.num_layers);
+    m.down.resize(c.num_layers);
+    for (std::size_t l = 0; l < c.num_layers; ++l) {
+        m.attn_norm.push_back(weights.storage(W::AttnNorm, l));
+        m.ffn_norm.push_back(weights.storage(W::FfnNorm, l));
+        m.pack_fused(m.qkv[l], {weights.storage(W::Wq, l), weights.storage(W::Wk, l), weights.storage(W::Wv, l)},
+                     m.hidden);
+        m.pack(m.o[l], static_cast<const float*>(weights.storage(W::Wo, l)->data), m.hidden, m.hidden);
+        m.pack_fused(m.gate_up[l], {weights.storage(W::Gate, l), weights.storage(W::Up, l)}, m.hidden);
+        m.pack(m.down[l], static_cast<const float*>(weights.storage(W::Down, l)->data), m.inter, m.hidden);
+    }
+    m.pack(m.lm_head, static_cast<const float*>(weights.storage(W::LmHead)->data), m.hidden, m.vocab);
+
+    const std::size_t kv = c.num_layers * m.Hk * max_seq * m.D * 4;
+    m.kcache = DevBuf(kv);
+    m.vcache = DevBuf(kv);
+    std::vector<float> cs, sn;
+    compute_rope_cache(max_seq, c.head_dim(), c.rope_theta, cs, sn, 0);
+    m.cos_t = DevBuf(cs.size() * 4);
+    m.sin_t = DevBuf(sn.size() * 4);
+    check(vm_hip_memcpy_h2d(m.cos_t.p, cs.data(), cs.size() * 4, m.stream), "rope tables");
+    check(vm_hip_memcpy_h2d(m.sin_t.p, sn.data(), sn.size() * 4, m.stream), "rope tables");
+
+    const std::size_t rows = max_seq;
+    m.h = DevBuf(rows * m.hidden * 4);
+    m.hn = DevBuf(rows * m.hidden * 4);
+    m.qkv_out = DevBuf(rows * m.qkv_n * 4);
+    m.q = DevBuf(rows * m.H * m.D * 4);
+    m.ctx = DevBuf(rows * m.hidden * 4);
+    m.attn_out = DevBuf(rows * m.hidden * 4);
+    m.gu = DevBuf(rows * 2 * m.inter * 4);
+    m.act = DevBuf(rows * m.inter * 4);
+    m.down_out = DevBuf(rows * m.hidden * 4);
+    m.logits = DevBuf(m.vocab * 4);
+    m.idx = DevBuf(rows * 4);
+    m.token = DevBuf(4);
+    m.pos = DevBuf(4);
+    m.tokens = DevBuf(rows * 4);
+    check(vm_hip_stream_synchronize(m.stream), "setup");
+}
+
+HipLlamaDecoder::~HipLlamaDecoder() {
+    if (!_impl) return;
+    auto& m = *_impl;
+    if (m.stream) (void)vm_hip_stream_synchronize(m.stream);
+    if (m.graph) (void)vm_hip_graph_destroy(m.graph);
+    if (m.ev0) (void)vm_hip_event_destroy(m.ev0);
+    if (m.ev1) (void)vm_hip_event_destroy(m.ev1);
+    // Buffers are freed by their destructors after the stream is idle.
+    void* s = m.stream;
+    _impl.reset();
+    if (s) (void)vm_hip_stream_destroy(s);
+}
+
+auto HipLlamaDecoder::logits() const -> std::vector<float> {
+    auto& m = *_impl;
+    std::vector<float> out(static_cast<std::size_t>(m.vocab));
+    check(vm_hip_memcpy_d2h(out.data(), m.logits.p, out.size() * 4, m.stream), "logits download");
+    return out;
+}
+
+auto HipLlamaDecoder::prefill(std::span<const std::int32_t> tokens) -> std::vector<float> {
+    auto& m = *_impl;
+    if (tokens.empty() || tokens.size() > _max_seq)
+        throw std::invalid_argument("HipLlamaDecoder::prefill: prompt length must be in [1, max_seq]");
+    check(vm_hip_memcpy_h2d(m.idx.p, tokens.data(), tokens.size_bytes(), m.stream), "token upload");
+    check(vm_hip_memcpy_h2d(m.tokens.p, tokens.data(), tokens.size_bytes(), m.stream), "token upload");
+    if (tokens.size() == 1) check(vm_hip_memcpy_h2d(m.token.p, tokens.data(), 4, m.stream), "token upload");
+    m.set_pos(0);
+    m.forward(static_cast<std::int64_t>(tokens.size()));
+    m.seq = tokens.size();
+    m.set_pos(static_cast<std::int64_t>(m.seq) - 1);  // position of the last processed token
+    return logits();
+}
+
+auto HipLlamaDecoder::forward_step(std::int32_t token, std::size_t pos) -> std::vector<float> {
+    auto& m = *_impl;
+    if (pos > m.seq || pos >= _max_seq) throw std::invalid_argument("HipLlamaDecoder::forward_step: bad position");
+    check(vm_hip_memcpy_h2d(m.token.p, &token, 4, m.stream), "token upload");
+    m.set_pos(static_cast<std::int64_t>(pos));
+    m.forward(1);
+    m.seq = pos + 1;
+    return logits();
+}
+
+auto HipLlamaDecoder::generate(std::span<const std::int32_t> prompt, std::size_t steps, bool use_graph)
+    -> std::vector<std::int32_t> {
+    auto& m = *_impl;
+    if (prompt.empty() || prompt.size() + steps + 1 > _max_seq)
+        throw std::invalid_argument("HipLlamaDecoder::generate: prompt + steps + 1 must fit in max_seq");
+    check(vm_hip_event_record(m.ev0, m.stream), "event");
+    check(vm_hip_memcpy_h2d(m.idx.p, prompt.data(), prompt.size_bytes(), m.stream), "token upload");
+    check(vm_hip_memcpy_h2d(m.tokens.p, prompt.data(), prompt.size_bytes(), m.stream), "token upload");
+    if (prompt.size() == 1) check(vm_hip_memcpy_h2d(m.token.p, prompt.data(), 4, m.stream), "token upload");
+    m.set_pos(0);
+    m.forward(static_cast<std::int64_t>(prompt.size()));
+    m.set_pos(static_cast<std::int64_t>(prompt.size()) - 1);
+    // First generated token from the prompt's logits; *pos becomes its position.
+    auto* tok = m.token.as<std::int32_t>();
+    auto* posp = m.pos.as<std::int32_t>();
+    auto* seqp = m.tokens.as<std::int32_t>();
+    const auto ms = static_cast<std::int64_t>(_max_seq);
+    check(vm_hip_argmax_f32(m.logits.as<float>(), m.vocab, tok, posp, seqp, ms, m.stream), "argmax");
+    check(vm_hip_event_record(m.ev1, m.stream), "event");
+    check(vm_hip_event_synchronize(m.ev1), "prefill");
+    float ms_prefill = 0.0f;
+    check(vm_hip_event_elapsed_ms(&ms_prefill, m.ev0, m.ev1), "event");
+    _prefill_s = ms_prefill * 1e-3;
+
+    auto step = [&] {
+        m.forward(1);
+        check(vm_hip_argmax_f32(m.logits.as<float>(), m.vocab, tok, posp, seqp, ms, m.stream), "argmax");
+    };
+    std::size_t done = 0;
+    _decode_steps_timed = 0;
+    if (steps > 0 && use_graph) {
+        // The first step runs eagerly: it sizes the per-stream split-K
+        // workspaces (the prefill above may have regrown them), then the
+        // step is captured against those buffers and replayed.  The graph is
+        // captured again on every call, so it never holds a buffer that a
+        // later prefill has reallocated.
+        step();
+        done = 1;
+        if (m.graph) {
+            check(vm_hip_graph_destroy(m.graph), "graph destroy");
+            m.graph = nullptr;
+        }
+        if (steps > 1) {
+            check(vm_hip_stream_begin_capture(m.stream), "graph capture");
+            try {
+                step();
+            } catch (...) {
+                void* g = nullptr;
+                (void)vm_hip_stream_end_capture(m.stream, &g);
+                if (g) (void)vm_hip_graph_destroy(g);
+                throw;
+            }
+            check(vm_hip_stream_end_capture(m.stream, &m.graph), "graph capture");
+        }
+    }
+    check(vm_hip_event_record(m.ev0, m.stream), "event");
+    _decode_steps_timed = steps - done;
+    if (m.graph && use_graph)
+        for (; done < steps; ++done) check(vm_hip_graph_launch(m.graph, m.stream), "graph launch");
+    else
+        for (; done < steps; ++done) step();
+    check(vm_hip_event_record(m.ev1, m.stream), "event");
+    check(vm_hip_event_synchronize(m.ev1), "decode");
+    float ms_decode = 0.0f;
+    check(vm_hip_event_elapsed_ms(&ms_decode, m.ev0, m.ev1), "event");
+    _decode_s = ms_decode * 1e-3;
+    m.seq = prompt.size() + steps;
+
+    std::vector<std::int32_t> out(steps + 1);
+    check(vm_hip_memcpy_d2h(out.data(), seqp + prompt.size(), out.size() * 4, m.stream), "token download");
+    return out;
+}
+
+}  // namespace velomind::examples::llama

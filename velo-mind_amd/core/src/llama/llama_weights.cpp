@@ -1,0 +1,232 @@
+// LlamaWeightSet and GraphLlamaSession (see velomind/llama/llama_hip.h).
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "velomind/executable.h"
+#include "velomind/llama/llama_hip.h"
+#include "vm_hip.h"
+
+namespace velomind::examples::llama {
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != VM_HIP_OK) throw std::runtime_error(std::string(what) + ": " + vm_hip_last_error());
+}
+
+std::shared_ptr<TensorStorage> device_f32(const shape_t& shape) {
+    TensorStorage meta;
+    meta.shape = shape;
+    meta.dtype = DataType::Float32;
+    auto s = TensorStorage::allocate(storage_nbytes(meta), DeviceType::HIP);
+    s->shape = shape;
+    s->dtype = DataType::Float32;
+    return s;
+}
+
+constexpr int kLinearKinds[] = {static_cast<int>(LlamaWeight::Wq),   static_cast<int>(LlamaWeight::Wk),
+                                static_cast<int>(LlamaWeight::Wv),   static_cast<int>(LlamaWeight::Wo),
+                                static_cast<int>(LlamaWeight::Gate), static_cast<int>(LlamaWeight::Up),
+                                static_cast<int>(LlamaWeight::Down)};
+
+}  // namespace
+
+auto llama_weight_shape(const Config& c, LlamaWeight kind) -> shape_t {
+    const auto h = static_cast<dim_t>(c.hidden_size);
+    const auto kv = static_cast<dim_t>(c.effective_num_kv_heads() * c.head_dim());
+    const auto i = static_cast<dim_t>(c.intermediate_size);
+    const auto v = static_cast<dim_t>(c.vocab_size);
+    switch (kind) {
+        case LlamaWeight::Embed: return {v, h};
+        case LlamaWeight::FinalNorm: return {h};
+        case LlamaWeight::LmHead: return {h, v};
+        case LlamaWeight::AttnNorm: return {h};
+        case LlamaWeight::FfnNorm: return {h};
+        case LlamaWeight::Wq: return {h, static_cast<dim_t>(c.num_heads * c.head_dim())};
+        case LlamaWeight::Wk: return {h, kv};
+        case LlamaWeight::Wv: return {h, kv};
+        case LlamaWeight::Wo: return {h, h};
+        case LlamaWeight::Gate: return {h, i};
+        case LlamaWeight::Up: return {h, i};
+        case LlamaWeight::Down: return {i, h};
+    }
+    throw std::invalid_argument("llama_weight_shape: unknown weight kind");
+}
+
+LlamaWeightSet::LlamaWeightSet(const Config& cfg) : _cfg(cfg) {
+    if (cfg.num_heads == 0 || cfg.hidden_size % cfg.num_heads != 0 || cfg.num_layers == 0 || cfg.vocab_size == 0 ||
+        cfg.intermediate_size == 0 || cfg.num_heads % cfg.effective_num_kv_heads() != 0)
+        throw std::invalid_argument("LlamaWeightSet: inconsistent config");
+    _w.resize(3 + (kLlamaWeightKinds - 3) * cfg.num_layers);
+    for (int k = 0; k < kLlamaWeightKinds; ++k) {
+        const auto kind = static_cast<LlamaWeight>(k);
+        const std::size_t layers = llama_weight_per_layer(kind) ? cfg.num_layers : 1;
+        for (std::size_t l = 0; l < layers; ++l) _w[slot(kind, l)] = device_f32(llama_weight_shape(cfg, kind));
+    }
+}
+
+auto LlamaWeightSet::slot(LlamaWeight kind, std::size_t layer) const -> std::size_t {
+    const int k = static_cast<int>(kind);
+    if (k < 0 || k >= kLlamaWeightKinds) throw std::invalid_argument("LlamaWeightSet: unknown weight kind");
+    if (!llama_weight_per_layer(kind)) return static_cast<std::size_t>(k);
+    if (layer >= _cfg.num_layers) throw std::out_of_range("LlamaWeightSet: layer out of range");
+    return 3 + static_cast<std::size_t>(k - 3) * _cfg.num_layers + layer;
+}
+
+void LlamaWeightSet::set(LlamaWeight kind, std::size_t layer, std::span<const float> host) {
+    auto& s = _w[slot(kind, layer)];
+    if (host.size() != storage_numel(*s))
+        throw std::invalid_argument("LlamaWeightSet::set: expected " + std::to_string(storage_numel(*s)) +
+                                    " values, got " + std::to_string(host.size()));
+    check(vm_hip_memcpy_h2d(s->data, host.data(), host.size_bytes(), nullptr), "LlamaWeightSet::set");
+}
+
+void LlamaWeightSet::fill_synthetic(std::uint64_t seed, float stddev) {
+    for (int k = 0; k < kLlamaWeightKinds; ++k) {
+        const auto kind = static_cast<LlamaWeight>(k);
+        const bool norm = kind == LlamaWeight::FinalNorm || kind == LlamaWeight::AttnNorm || kind == LlamaWeight::FfnNorm;
+        const std::size_t layers = llama_weight_per_layer(kind) ? _cfg.num_layers : 1;
+        for (std::size_t l = 0; l < layers; ++l) {
+            auto& s = _w[slot(kind, l)];
+            const std::uint64_t tseed = seed ^ (0x100000001B3ull * (static_cast<std::uint64_t>(k) * 4099 + l + 1));
+            check(vm_hip_fill_normal_f32(static_cast<float*>(s->data), static_cast<std::int64_t>(storage_numel(*s)),
+                                         tseed, norm ? 1.0f : 0.0f, stddev, nullptr),
+                  "LlamaWeightSet::fill_synthetic");
+        }
+    }
+    check(vm_hip_device_synchronize(), "LlamaWeightSet::fill_synthetic");
+}
+
+auto LlamaWeightSet::storage(LlamaWeight kind, std::size_t layer) const -> std::shared_ptr<TensorStorage> {
+    return _w[slot(kind, layer)];
+}
+
+// ------------------------------------------------------------ graph session
+
+GraphLlamaSession::GraphLlamaSession(std::shared_ptr<const LlamaWeightSet> weights, QuantType quant_type,
+                                     int block_size, bool use_fused_attention)
+    : _weights(std::move(weights)), _qt(quant_type), _block(block_size), _fused(use_fused_attention) {
+    if (!_weights) throw std::invalid_argument("GraphLlamaSession: null weights");
+    if (_qt == QuantType::Int8 && _block > 0)
+        throw std::invalid_argument("GraphLlamaSession: INT8 weights are packed per column (block_size 0)");
+    if (_qt == QuantType::Int4 && _block <= 0) _block = 32;  // the packer's block (quant.h:89)
+    const auto& cfg = _weights->config();
+    const std::size_t n = 7 * cfg.num_layers + 1;
+    _lin.resize(n);
+    _scale.resize(n);
+    for (std::size_t i = 0; i < n; ++i) {
+        const bool head = i + 1 == n;
+        const auto kind = head ? LlamaWeight::LmHead : static_cast<LlamaWeight>(kLinearKinds[i % 7]);
+        auto src = _weights->storage(kind, head ? 0 : i / 7);
+        if (_qt == QuantType::None) {
+            _lin[i] = src;
+        } else {
+            auto packed = _qt == QuantType::Int4 ? quantize_storage_int4(*src, static_cast<std::size_t>(_block),
+                                                                         DeviceType::HIP)
+                                                 : quantize_storage_int8(*src, DeviceType::HIP);
+            _lin[i] = packed.first;
+            _scale[i] = packed.second;
+        }
+    }
+}
+
+void GraphLlamaSession::bind(Graph& g, ForwardWeights& w) const {
+    const auto& cfg = _weights->config();
+    w.graph = &g;
+    w.use_fused_attention = _fused;
+    w.quant_type = _qt;
+    w.quant_block_size = _block;
+    w.w_embed = g.input(_weights->storage(LlamaWeight::Embed));
+    w.w_final_norm = g.input(_weights->storage(LlamaWeight::FinalNorm));
+    std::vector<Tensor>* lin[] = {&w.wq, &w.wk, &w.wv, &w.wo, &w.w_gate, &w.w_up, &w.w_down};
+    std::vector<Tensor>* scl[] = {&w.wq_scale,     &w.wk_scale,   &w.wv_scale,    &w.wo_scale,
+                                  &w.w_gate_scale, &w.w_up_scale, &w.w_down_scale};
+    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+        w.w_attn_norm.push_back(g.input(_weights->storage(LlamaWeight::AttnNorm, l)));
+        w.w_ffn_norm.push_back(g.input(_weights->storage(LlamaWeight::FfnNorm, l)));
+        for (int j = 0; j < 7; ++j) {
+            lin[j]->push_back(g.input(_lin[l * 7 + j]));
+            if (_qt != QuantType::None) scl[j]->push_back(g.input(_scale[l * 7 + j]));
+        }
+    }
+    w.w_lm_head = g.input(_lin.back());
+    if (_qt != QuantType::None) w.w_lm_head_scale = g.input(_scale.back());
+}
+
+auto GraphLlamaSession::prefill(std::span<const std::int32_t> tokens) -> std::vector<float> {
+    if (tokens.empty()) throw std::invalid_argument("GraphLlamaSession::prefill: tokens is empty");
+    const auto& cfg = _weights->config();
+    const auto s = static_cast<dim_t>(tokens.size());
+    const auto half = static_cast<dim_t>(cfg.head_dim() / 2);
+    Graph g;
+    auto tok = g.input({s}, DataType::Int32);
+    ForwardWeights w;
+    bind(g, w);
+    w.cos_cache = g.input({s, half}, DataType::Float32);
+    w.sin_cache = g.input({s, half}, DataType::Float32);
+    if (!_fused) w.causal_mask = g.input({static_cast<dim_t>(cfg.num_heads), s, s}, DataType::Float32);
+    KVCacheHandles kv;
+    auto logits = build_forward_graph_prefill(g, cfg, tok, w, &kv, true);
+    auto exec = g.build(DeviceType::HIP);
+    tok.copy_from_host(std::as_bytes(tokens));
+    std::vector<float> c, sn, mask;
+    compute_rope_cache(tokens.size(), cfg.head_dim(), cfg.rope_theta, c, sn, 0);
+    w.cos_cache.copy_from_host(std::as_bytes(std::span(c)));
+    w.sin_cache.copy_from_host(std::as_bytes(std::span(sn)));
+    if (!_fused) {
+        compute_causal_mask(cfg.num_heads, tokens.size(), mask);
+        w.causal_mask.copy_from_host(std::as_bytes(std::span(mask)));
+    }
+    exec->execute();
+    _k.clear();
+    _v.clear();
+    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+        _k.push_back(kv.k[l].shared_storage());
+        _v.push_back(kv.v[l].shared_storage());
+    }
+    _seq_len = tokens.size();
+    std::vector<float> out(cfg.vocab_size);
+    logits.copy_to_host(std::as_writable_bytes(std::span(out)));
+    return out;
+}
+
+auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std::vector<float> {
+    if (_seq_len == 0) {
+        const std::int32_t one[1] = {token};
+        return prefill(one);
+    }
+    if (pos != _seq_len) throw std::invalid_argument("GraphLlamaSession::forward_step: pos must equal the cache length");
+    const auto& cfg = _weights->config();
+    const auto half = static_cast<dim_t>(cfg.head_dim() / 2);
+    Graph g;
+    auto tok = g.input({1}, DataType::Int32);
+    ForwardWeights w;
+    bind(g, w);
+    w.cos_cache = g.input({1, half}, DataType::Float32);
+    w.sin_cache = g.input({1, half}, DataType::Float32);
+    KVCacheHandles kv_in, kv_out;
+    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+        kv_in.k.push_back(g.input(_k[l]));
+        kv_in.v.push_back(g.input(_v[l]));
+    }
+    auto logits = build_forward_graph_decode(g, cfg, tok, w, kv_in, &kv_out);
+    auto exec = g.build(DeviceType::HIP);
+    const std::int32_t one[1] = {token};
+    tok.copy_from_host(std::as_bytes(std::span(one)));
+    std::vector<float> c, sn;
+    compute_rope_cache(1, cfg.head_dim(), cfg.rope_theta, c, sn, pos);
+    w.cos_cache.copy_from_host(std::as_bytes(std::span(c)));
+    w.sin_cache.copy_from_host(std::as_bytes(std::span(sn)));
+    exec->execute();
+    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+        _k[l] = kv_out.k[l].shared_storage();
+        _v[l] = kv_out.v[l].shared_storage();
+    }
+    _seq_len = pos + 1;
+    std::vector<float> out(cfg.vocab_size);
+    logits.copy_to_host(std::as_writable_bytes(std::span(out)));
+    return out;
+}
+
+}  // namespace velomind::examples::llama

@@ -284,6 +284,17 @@ int vm_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
     return 0;
 }
 
+int vm_hip_memcpy_2d_d2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t rows,
+                         void* stream) {
+    if (width == 0 || rows == 0) return 0;
+    if (!dst || !src) return fail_inval("vm_hip_memcpy_2d_d2d: null pointer");
+    if (width > dpitch || width > spitch) return fail_inval("vm_hip_memcpy_2d_d2d: width exceeds a pitch");
+    VM_TRY_HIP(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyDeviceToDevice,
+                                static_cast<hipStream_t>(stream)),
+               "hipMemcpy2DAsync (D2D)");
+    return 0;
+}
+
 int vm_hip_stream_create(void** stream) {
     if (!stream) return fail_inval("vm_hip_stream_create: null stream");
     hipStream_t s = nullptr;

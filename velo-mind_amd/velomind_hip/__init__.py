@@ -75,6 +75,14 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_softmax_f32": ([p, p, c_int64, c_int64, c_int64, p], c_int),
         "vm_hip_matmul_f32": ([p, p, p, c_int64, c_int64, c_int64, c_int64, p], c_int),
         "vm_hip_attention_f32": ([p, p, p, p] + [c_int64] * 7 + [c_float, c_int, p], c_int),
+        "vm_hip_fill_normal_f32": ([p, c_int64, ctypes.c_uint64, c_float, c_float, p], c_int),
+        "vm_hip_add_rmsnorm_f32": ([p, p, p, p, c_int64, c_int64, c_float, p], c_int),
+        "vm_hip_rope_kv_append_f32": ([p, c_int64, p, p, p, p, p, p] + [c_int64] * 4 + [p], c_int),
+        "vm_hip_attention_decode_f32": ([p, p, p, p, p] + [c_int64] * 4 + [c_float, p], c_int),
+        "vm_hip_attention_prefill_f32": ([p, p, p, p, p] + [c_int64] * 5 + [c_float, p], c_int),
+        "vm_hip_silu_mul_f32": ([p, p, c_int64, c_int64, p], c_int),
+        "vm_hip_argmax_f32": ([p, c_int64, p, p, p, c_int64, p], c_int),
+        "vm_hip_memcpy_2d_d2d": ([p, c_size_t, p, c_size_t, c_size_t, c_size_t, p], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -94,7 +102,9 @@ def exported_symbols() -> list[str]:
             "vm_hip_pack_int4", "vm_hip_dequant_int8", "vm_hip_dequant_int4", "vm_hip_half_to_f32",
             "vm_hip_embedding_f32", "vm_hip_rmsnorm_f32", "vm_hip_rope_f32", "vm_hip_transpose_f32",
             "vm_hip_slice_f32", "vm_hip_concat_f32", "vm_hip_repeat_kv_f32", "vm_hip_elementwise_f32",
-            "vm_hip_softmax_f32", "vm_hip_matmul_f32", "vm_hip_attention_f32"]
+            "vm_hip_softmax_f32", "vm_hip_matmul_f32", "vm_hip_attention_f32", "vm_hip_fill_normal_f32",
+            "vm_hip_add_rmsnorm_f32", "vm_hip_rope_kv_append_f32", "vm_hip_attention_decode_f32",
+            "vm_hip_attention_prefill_f32", "vm_hip_silu_mul_f32", "vm_hip_argmax_f32", "vm_hip_memcpy_2d_d2d"]
 
 
 def open_library() -> ctypes.CDLL:
