@@ -294,7 +294,7 @@ int vm_hip_rope_kv_append_f32(const float* qkv, int64_t rows, const float* cos_t
 /* One query row per head, q [heads, head_dim], at position *pos over keys
  * 0..*pos of the caches; out [heads * head_dim].  Grouped heads are read
  * directly (no RepeatKV); scale <= 0 means 1/sqrt(head_dim).  head_dim 64
- * or 128, at most 16 query heads per KV head.  Replaces RepeatKV +
+ * or 128, at most 16 query heads per KV head, 16-byte aligned operands.  Replaces RepeatKV +
  * FusedAttention (or MatMul/Softmax/MatMul) + Transpose + Reshape of a
  * decode step (llama_graph.cpp:88-118, fused_attention.cpp:22-138). */
 int vm_hip_attention_decode_f32(const float* q, const float* k_cache, const float* v_cache,

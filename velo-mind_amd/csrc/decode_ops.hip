@@ -30,6 +30,8 @@ constexpr int kT = 256;
 
 hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 // ---- SplitMix64 (Steele, Lea & Flood 2014) as a counter-based generator and
 // the Box-Muller transform: element 2j and 2j+1 come from the pair
 // (mix(seed + (2j+1) * golden), mix(seed + (2j+2) * golden)).
@@ -59,6 +61,68 @@ __global__ void fill_normal_kernel(float* __restrict__ dst, int64_t n, uint64_t 
 // ---- h += delta (optional), hn = rmsnorm(h) * w, one workgroup per row.
 // The add is the reference's Add node (add.cpp) and the norm its RMSNorm
 // (rmsnorm.cpp:17-60) on the sum.
+//
+// Rows of at most 1024 * NV floats (dim % 4 == 0, 16-byte aligned rows)
+// stay in registers: every thread issues all of its 16-byte loads of h,
+// delta and w before the first use (one memory round trip), the sum of
+// squares is reduced once, and h / hn are written from registers.  Buffer
+// loads past the row return zeros, which add nothing to the sum.
+template <int NV>
+__global__ __launch_bounds__(kT) void add_rmsnorm_vec_kernel(float* __restrict__ h, const float* __restrict__ delta,
+                                                             const float* __restrict__ w, float* __restrict__ hn,
+                                                             int dim, float eps) {
+    __shared__ float part[kT / 64];
+    const uint32_t row_bytes = static_cast<uint32_t>(dim) * 4u;
+    float* hr = h + static_cast<int64_t>(blockIdx.x) * dim;
+    float* nr = hn + static_cast<int64_t>(blockIdx.x) * dim;
+    const __amdgpu_buffer_rsrc_t hrs = buffer_rsrc(hr, row_bytes);
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(w, row_bytes);
+    u32x4 hv[NV], dv[NV], wv[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const uint32_t off = (threadIdx.x + u * kT) * 16u;
+        hv[u] = buffer_load16(hrs, off);
+        wv[u] = buffer_load16(wrs, off);
+    }
+    if (delta) {
+        const __amdgpu_buffer_rsrc_t drs = buffer_rsrc(delta + static_cast<int64_t>(blockIdx.x) * dim, row_bytes);
+#pragma unroll
+        for (int u = 0; u < NV; ++u) dv[u] = buffer_load16(drs, (threadIdx.x + u * kT) * 16u);
+    }
+    float x[NV][4];
+    float s = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float v = __uint_as_float(hv[u][e]);
+            if (delta) v = v + __uint_as_float(dv[u][e]);
+            x[u][e] = v;
+            s = fmaf(v, v, s);
+        }
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kT / 64; ++i) tot += part[i];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(dim) + eps);
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int i4 = threadIdx.x + u * kT;
+        if (4 * i4 < dim) {
+            if (delta) *reinterpret_cast<float4*>(hr + 4 * i4) = make_float4(x[u][0], x[u][1], x[u][2], x[u][3]);
+            float4 y;
+            y.x = x[u][0] * inv * __uint_as_float(wv[u][0]);
+            y.y = x[u][1] * inv * __uint_as_float(wv[u][1]);
+            y.z = x[u][2] * inv * __uint_as_float(wv[u][2]);
+            y.w = x[u][3] * inv * __uint_as_float(wv[u][3]);
+            *reinterpret_cast<float4*>(nr + 4 * i4) = y;
+        }
+    }
+}
+
+// Any row length or alignment: strided loop over the row.
 __global__ __launch_bounds__(kT) void add_rmsnorm_kernel(float* __restrict__ h, const float* __restrict__ delta,
                                                          const float* __restrict__ w, float* __restrict__ hn,
                                                          int64_t dim, float eps) {
@@ -137,8 +201,21 @@ __global__ void rope_kv_append_kernel(const float* __restrict__ qkv, const float
 }
 
 // ---- Decode attention over the resident cache: query rows [H, 1, D] at
-// position *pos see keys 0..*pos.  Grid (chunks, Hkv): each workgroup takes
-// CHUNK keys and the G = H / Hkv query heads of its KV head.
+// position *pos see keys 0 .. *pos (n = *pos + 1 keys).  Grid (chunks, Hkv),
+// chunks = ceil(max_seq / CHUNK) so that the launch does not depend on the
+// position; workgroups whose chunk starts at or past n exit at once.  A
+// workgroup takes CHUNK keys of one KV head and the G = H / Hkv query heads
+// that share it (no RepeatKV copy):
+//   1. every thread issues its 16-byte loads of q, K and V (one memory
+//      round trip) into LDS;
+//   2. thread (j, g-slot) scores key j against its query heads; the CHUNK
+//      lanes of a key row reduce max and sum with cross-lane shuffles;
+//   3. thread (g, float4 column) accumulates p . V over the chunk.
+// With one chunk the result is written directly.  Otherwise each chunk
+// stores (m, l, o) with agent-scope stores, takes a ticket once they are
+// acknowledged, and the last chunk of the KV head merges the partials in
+// chunk order (online softmax rescaling), reading them in batches of
+// independent loads.  The per-stream counters are reset by the merger.
 template <int D, int CHUNK>
 __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __restrict__ q,
                                                               const float* __restrict__ k_cache,
@@ -148,110 +225,175 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
                                                               float* __restrict__ partials,
                                                               unsigned* __restrict__ counters) {
     constexpr int kMaxG = 16;
-    __shared__ float sq[kMaxG][D];
-    __shared__ float sk[CHUNK][D + 1];
-    __shared__ float sv[CHUNK][D];
+    constexpr int D4 = D / 4;
+    constexpr int kKS = D + 4;             // padded key row in LDS (floats)
+    constexpr int kPart = D + 4;           // partial record: m, l, -, -, o[0..D)
+    constexpr int QV = (kMaxG * D4 + kT - 1) / kT;
+    constexpr int KV = CHUNK * D4 / kT;    // 16-byte loads per thread for a K (or V) chunk
+    constexpr int GS = kT / CHUNK;         // query-head slots while scoring
+    constexpr int GI = kMaxG / GS;
+    constexpr int PS = kT / D4;            // query-head slots while accumulating p . V
+    static_assert(CHUNK * D4 % kT == 0 && 64 % CHUNK == 0 && kT % D4 == 0, "tile shape");
+    __shared__ __align__(16) float sq[kMaxG * D];
+    __shared__ __align__(16) float sk[CHUNK * kKS];
+    __shared__ __align__(16) float sv[CHUNK * D];
     __shared__ float sp[kMaxG][CHUNK];
     __shared__ float sm[kMaxG], sl[kMaxG];
     __shared__ unsigned ticket;
 
     const int chunk = blockIdx.x;
-    const int chunks = gridDim.x;
     const int hk = blockIdx.y;
-    const int g_n = heads / kv_heads;
+    const int G = heads / kv_heads;
     const int tid = threadIdx.x;
     const int n_keys = min(pos[0] + 1, max_seq);
+    const int nc = (n_keys + CHUNK - 1) / CHUNK;
+    if (chunk >= nc) return;
     const int k0 = chunk * CHUNK;
-    const int nk = max(0, min(CHUNK, n_keys - k0));
-    constexpr int kPart = D + 2;
+    const int nk = min(CHUNK, n_keys - k0);
 
-    if (nk > 0) {
-        for (int e = tid; e < g_n * D; e += kT) sq[e / D][e % D] = q[(hk * g_n + e / D) * D + e % D];
-        const float* kb = k_cache + (static_cast<int64_t>(hk) * max_seq + k0) * D;
-        const float* vb = v_cache + (static_cast<int64_t>(hk) * max_seq + k0) * D;
-        for (int e = tid; e < nk * D; e += kT) {
-            sk[e / D][e % D] = kb[e];
-            sv[e / D][e % D] = vb[e];
+    {
+        const __amdgpu_buffer_rsrc_t qrs = buffer_rsrc(q + static_cast<int64_t>(hk) * G * D,
+                                                       static_cast<uint32_t>(G * D) * 4u);
+        const uint32_t kv_bytes = static_cast<uint32_t>(nk * D) * 4u;
+        const int64_t kv_off = (static_cast<int64_t>(hk) * max_seq + k0) * D;
+        const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(k_cache + kv_off, kv_bytes);
+        const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(v_cache + kv_off, kv_bytes);
+        u32x4 tq[QV], tk[KV], tv[KV];
+#pragma unroll
+        for (int u = 0; u < QV; ++u) tq[u] = buffer_load16(qrs, (tid + u * kT) * 16u);
+#pragma unroll
+        for (int u = 0; u < KV; ++u) {
+            tk[u] = buffer_load16(krs, (tid + u * kT) * 16u);
+            tv[u] = buffer_load16(vrs, (tid + u * kT) * 16u);
         }
-        __syncthreads();
-        for (int e = tid; e < g_n * CHUNK; e += kT) {
-            const int g = e / CHUNK, j = e % CHUNK;
-            float s = -INFINITY;
-            if (j < nk) {
-                float dot = 0.0f;
-#pragma unroll 16
-                for (int t = 0; t < D; ++t) dot = fmaf(sq[g][t], sk[j][t], dot);
-                s = dot * scale;
-            }
-            sp[g][j] = s;
+#pragma unroll
+        for (int u = 0; u < QV; ++u) {
+            const int e = tid + u * kT;
+            if (e < kMaxG * D4) *reinterpret_cast<u32x4*>(sq + 4 * e) = tq[u];
         }
-        __syncthreads();
-        // Softmax partials per query head: one wave per head, lanes over keys.
-        const int wave = tid >> 6, lane = tid & 63;
-        for (int g = wave; g < g_n; g += kT / 64) {
-            float mx = -INFINITY;
-            for (int j = lane; j < CHUNK; j += 64) mx = fmaxf(mx, sp[g][j]);
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            float sum = 0.0f;
-            for (int j = lane; j < CHUNK; j += 64) {
-                const float pv = j < nk ? expf(sp[g][j] - mx) : 0.0f;
-                sp[g][j] = pv;
-                sum += pv;
-            }
-            for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-            if (lane == 0) {
-                sm[g] = mx;
-                sl[g] = sum;
+#pragma unroll
+        for (int u = 0; u < KV; ++u) {
+            const int e = tid + u * kT;
+            const int j = e / D4, c = e - j * D4;
+            *reinterpret_cast<u32x4*>(sk + j * kKS + 4 * c) = tk[u];
+            *reinterpret_cast<u32x4*>(sv + 4 * e) = tv[u];
+        }
+    }
+    __syncthreads();
+
+    // Scores: thread (j = tid % CHUNK, slot = tid / CHUNK), heads slot + i * GS.
+    {
+        const int j = tid % CHUNK, slot = tid / CHUNK;
+        float sc[GI];
+#pragma unroll
+        for (int i = 0; i < GI; ++i) sc[i] = 0.0f;
+#pragma unroll 4
+        for (int c = 0; c < D4; ++c) {
+            const float4 kv = *reinterpret_cast<const float4*>(sk + j * kKS + 4 * c);
+#pragma unroll
+            for (int i = 0; i < GI; ++i) {
+                const int g = slot + i * GS;
+                if (g < G) {
+                    const float4 qv = *reinterpret_cast<const float4*>(sq + g * D + 4 * c);
+                    sc[i] = fmaf(qv.x, kv.x, sc[i]);
+                    sc[i] = fmaf(qv.y, kv.y, sc[i]);
+                    sc[i] = fmaf(qv.z, kv.z, sc[i]);
+                    sc[i] = fmaf(qv.w, kv.w, sc[i]);
+                }
             }
         }
-        __syncthreads();
-        for (int e = tid; e < g_n * D; e += kT) {
-            const int g = e / D, t = e % D;
-            float acc = 0.0f;
-            for (int j = 0; j < nk; ++j) acc = fmaf(sp[g][j], sv[j][t], acc);
-            float* part = partials + (static_cast<int64_t>(hk * g_n + g) * chunks + chunk) * kPart;
-            coherent_store(part + 2 + t, acc);
-            if (t == 0) {
+#pragma unroll
+        for (int i = 0; i < GI; ++i) {
+            const int g = slot + i * GS;
+            if (g < G) {
+                const float sv_ = j < nk ? sc[i] * scale : -INFINITY;
+                float mx = sv_;
+#pragma unroll
+                for (int off = CHUNK / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+                const float p = j < nk ? expf(sv_ - mx) : 0.0f;
+                float sum = p;
+#pragma unroll
+                for (int off = CHUNK / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+                sp[g][j] = p;
+                if (j == 0) {
+                    sm[g] = mx;
+                    sl[g] = sum;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // p . V: thread (c4 = tid % D4, slot = tid / D4), heads slot + i * PS.
+    const int c4 = tid % D4, pslot = tid / D4;
+    for (int g = pslot; g < G; g += PS) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int jj = 0; jj < nk; ++jj) {
+            const float p = sp[g][jj];
+            const float4 v = *reinterpret_cast<const float4*>(sv + jj * D + 4 * c4);
+            acc.x = fmaf(p, v.x, acc.x);
+            acc.y = fmaf(p, v.y, acc.y);
+            acc.z = fmaf(p, v.z, acc.z);
+            acc.w = fmaf(p, v.w, acc.w);
+        }
+        if (nc == 1) {
+            const float inv = 1.0f / sl[g];
+            *reinterpret_cast<float4*>(out + (static_cast<int64_t>(hk) * G + g) * D + 4 * c4) =
+                make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        } else {
+            float* part = partials + ((static_cast<int64_t>(hk) * G + g) * gridDim.x + chunk) * kPart;
+            coherent_store(part + 4 + 4 * c4 + 0, acc.x);
+            coherent_store(part + 4 + 4 * c4 + 1, acc.y);
+            coherent_store(part + 4 + 4 * c4 + 2, acc.z);
+            coherent_store(part + 4 + 4 * c4 + 3, acc.w);
+            if (c4 == 0) {
                 coherent_store(part, sm[g]);
                 coherent_store(part + 1, sl[g]);
             }
         }
-    } else {
-        for (int g = tid; g < g_n; g += kT) {
-            float* part = partials + (static_cast<int64_t>(hk * g_n + g) * chunks + chunk) * kPart;
-            coherent_store(part, -INFINITY);
-            coherent_store(part + 1, 0.0f);
-        }
     }
+    if (nc == 1) return;
     __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the ticket
     __syncthreads();
     if (tid == 0) ticket = __hip_atomic_fetch_add(&counters[hk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (ticket != static_cast<unsigned>(chunks - 1)) return;
+    if (ticket != static_cast<unsigned>(nc - 1)) return;
 
-    // Merge: O = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M), chunks in order.
-    for (int g = tid; g < g_n; g += kT) {
-        const float* base = partials + static_cast<int64_t>(hk * g_n + g) * chunks * kPart;
-        float mx = -INFINITY;
-        for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, coherent_load(base + c * kPart));
-        float l = 0.0f;
-        for (int c = 0; c < chunks; ++c) {
-            const float mc = coherent_load(base + c * kPart);
-            if (mc > -INFINITY) l += coherent_load(base + c * kPart + 1) * expf(mc - mx);
+    // Merge in chunk order: running (M, L, O) rescaled by exp(M - M').
+    constexpr int kB = 16;
+    for (int g = pslot; g < G; g += PS) {
+        const float* base = partials + (static_cast<int64_t>(hk) * G + g) * gridDim.x * kPart;
+        float M = -INFINITY, Lsum = 0.0f;
+        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int c0 = 0; c0 < nc; c0 += kB) {
+            float mc[kB], lc[kB], oc[kB][4];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                const float* rec = base + (c0 + u) * kPart;
+                const bool ok = c0 + u < nc;
+                mc[u] = ok ? coherent_load(rec) : -INFINITY;
+                lc[u] = ok ? coherent_load(rec + 1) : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) oc[u][e] = ok ? coherent_load(rec + 4 + 4 * c4 + e) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                if (c0 + u < nc) {
+                    const float Mn = fmaxf(M, mc[u]);
+                    const float a = M > -INFINITY ? expf(M - Mn) : 0.0f;
+                    const float b = expf(mc[u] - Mn);
+                    Lsum = fmaf(Lsum, a, lc[u] * b);
+                    O.x = fmaf(O.x, a, oc[u][0] * b);
+                    O.y = fmaf(O.y, a, oc[u][1] * b);
+                    O.z = fmaf(O.z, a, oc[u][2] * b);
+                    O.w = fmaf(O.w, a, oc[u][3] * b);
+                    M = Mn;
+                }
+            }
         }
-        sm[g] = mx;
-        sl[g] = l > 0.0f ? 1.0f / l : 0.0f;
-    }
-    __syncthreads();
-    for (int e = tid; e < g_n * D; e += kT) {
-        const int g = e / D, t = e % D;
-        const float* base = partials + static_cast<int64_t>(hk * g_n + g) * chunks * kPart;
-        float acc = 0.0f;
-        for (int c = 0; c < chunks; ++c) {
-            const float mc = coherent_load(base + c * kPart);
-            if (mc > -INFINITY) acc += coherent_load(base + c * kPart + 2 + t) * expf(mc - sm[g]);
-        }
-        out[(hk * g_n + g) * D + t] = acc * sl[g];
+        const float inv = 1.0f / Lsum;
+        *reinterpret_cast<float4*>(out + (static_cast<int64_t>(hk) * G + g) * D + 4 * c4) =
+            make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
     }
     if (tid == 0) __hip_atomic_store(&counters[hk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -363,34 +505,82 @@ __global__ void silu_mul_kernel(const float* __restrict__ gu, float* __restrict_
     }
 }
 
+// Four elements per thread (inter % 4 == 0, 16-byte aligned operands); the
+// same arithmetic as silu_mul_kernel.
+__global__ void silu_mul_vec_kernel(const float4* __restrict__ gu, float4* __restrict__ out, int rows, int inter4) {
+    const int e = blockIdx.x * kT + threadIdx.x;
+    if (e >= rows * inter4) return;
+    const int r = e / inter4, j = e - r * inter4;
+    const float4 g = gu[r * 2 * inter4 + j];
+    const float4 u = gu[r * 2 * inter4 + inter4 + j];
+    float4 y;
+    y.x = ((1.0f / (1.0f + expf(-g.x))) * g.x) * u.x;
+    y.y = ((1.0f / (1.0f + expf(-g.y))) * g.y) * u.y;
+    y.z = ((1.0f / (1.0f + expf(-g.z))) * g.z) * u.z;
+    y.w = ((1.0f / (1.0f + expf(-g.w))) * g.w) * u.w;
+    out[e] = y;
+}
+
 // ---- Greedy sampling: first index of the maximum, NaN skipped
-// (examples/tinyllama/sample.cpp:18-38).  One workgroup of 1024 threads.
-// With `pos`, the token is also stored at tokens[*pos + 1] (the sequence
-// buffer) and *pos advances by one.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int64_t n,
-                                                      int32_t* __restrict__ token_out, int32_t* __restrict__ pos,
-                                                      int32_t* __restrict__ tokens, int64_t max_seq) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
+// (examples/tinyllama/sample.cpp:18-38).  One workgroup of 1024 threads;
+// each pass issues all of a thread's loads (kArgVec 16-byte loads, 32768
+// elements per pass for the workgroup) before comparing, so a 32000-entry
+// vocabulary costs one memory round trip.  Elements are visited in
+// increasing index order per thread and ties resolve to the lower index,
+// so the result is the first maximum whatever the schedule.  With `pos`,
+// the token is also stored at tokens[*pos + 1] (the sequence buffer) and
+// *pos advances by one.
+constexpr int kArgT = 1024;
+constexpr int kArgVec = 8;
+
+__device__ __forceinline__ bool argmax_better(float v1, int i1, float v2, int i2) {
+    if (i2 < 0) return false;
+    if (i1 < 0) return true;
+    return v2 > v1 || (v2 == v1 && i2 < i1);
+}
+
+__global__ __launch_bounds__(kArgT) void argmax_kernel(const float* __restrict__ x, int64_t n,
+                                                       int32_t* __restrict__ token_out, int32_t* __restrict__ pos,
+                                                       int32_t* __restrict__ tokens, int64_t max_seq, int vec) {
+    __shared__ float bv[kArgT / 64];
+    __shared__ int bi[kArgT / 64];
     float best = -INFINITY;
     int idx = -1;
-    for (int64_t i = threadIdx.x; i < n; i += 1024) {
-        const float v = x[i];
-        if (v != v) continue;
-        if (idx < 0 || v > best) {
-            best = v;
-            idx = static_cast<int>(i);
+    if (vec) {
+        // 16-byte aligned x: element 4q + c of pass p is x[p * 32768 + 4 * (tid + u * 1024) + c].
+        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(x, static_cast<uint32_t>(n) * 4u);
+        constexpr int kPass = kArgT * kArgVec * 4;
+        for (int64_t p0 = 0; p0 < n; p0 += kPass) {
+            u32x4 t[kArgVec];
+#pragma unroll
+            for (int u = 0; u < kArgVec; ++u)
+                t[u] = buffer_load16(rs, static_cast<uint32_t>(p0 + 4 * (threadIdx.x + u * kArgT)) * 4u);
+#pragma unroll
+            for (int u = 0; u < kArgVec; ++u)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int64_t i = p0 + 4 * (threadIdx.x + u * kArgT) + c;
+                    const float v = __uint_as_float(t[u][c]);
+                    if (i < n && v == v && (idx < 0 || v > best)) {
+                        best = v;
+                        idx = static_cast<int>(i);
+                    }
+                }
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < n; i += kArgT) {
+            const float v = x[i];
+            if (v != v) continue;
+            if (idx < 0 || v > best) {
+                best = v;
+                idx = static_cast<int>(i);
+            }
         }
     }
-    auto better = [](float v1, int i1, float v2, int i2) {
-        if (i2 < 0) return false;
-        if (i1 < 0) return true;
-        return v2 > v1 || (v2 == v1 && i2 < i1);
-    };
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(best, off, 64);
         const int oi = __shfl_xor(idx, off, 64);
-        if (better(best, idx, ov, oi)) {
+        if (argmax_better(best, idx, ov, oi)) {
             best = ov;
             idx = oi;
         }
@@ -403,8 +593,8 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     if (threadIdx.x == 0) {
         float b = bv[0];
         int bidx = bi[0];
-        for (int w = 1; w < 16; ++w)
-            if (better(b, bidx, bv[w], bi[w])) {
+        for (int w = 1; w < kArgT / 64; ++w)
+            if (argmax_better(b, bidx, bv[w], bi[w])) {
                 b = bv[w];
                 bidx = bi[w];
             }
@@ -446,8 +636,22 @@ int vm_hip_add_rmsnorm_f32(float* h, const float* delta, const float* w, float* 
     if (rows == 0 || dim == 0) return 0;
     if (!h || !w || !hn) return fail_inval("add_rmsnorm: null pointer");
     if (rows > 0x7fffffff) return fail_inval("add_rmsnorm: too many rows");
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kT), 0, S(stream), h, delta, w,
-                       hn, dim, eps);
+    const dim3 grid(static_cast<unsigned>(rows));
+    const bool vec = dim % 4 == 0 && dim <= 8 * 4 * kT && aligned16(h) && aligned16(w) && aligned16(hn) &&
+                     (!delta || aligned16(delta));
+    if (vec) {
+        const int d = static_cast<int>(dim);
+        if (dim <= 4 * kT)
+            hipLaunchKernelGGL(add_rmsnorm_vec_kernel<1>, grid, dim3(kT), 0, S(stream), h, delta, w, hn, d, eps);
+        else if (dim <= 2 * 4 * kT)
+            hipLaunchKernelGGL(add_rmsnorm_vec_kernel<2>, grid, dim3(kT), 0, S(stream), h, delta, w, hn, d, eps);
+        else if (dim <= 4 * 4 * kT)
+            hipLaunchKernelGGL(add_rmsnorm_vec_kernel<4>, grid, dim3(kT), 0, S(stream), h, delta, w, hn, d, eps);
+        else
+            hipLaunchKernelGGL(add_rmsnorm_vec_kernel<8>, grid, dim3(kT), 0, S(stream), h, delta, w, hn, d, eps);
+    } else {
+        hipLaunchKernelGGL(add_rmsnorm_kernel, grid, dim3(kT), 0, S(stream), h, delta, w, hn, dim, eps);
+    }
     return check_launch("add_rmsnorm", S(stream));
 }
 
@@ -482,7 +686,10 @@ int vm_hip_attention_decode_f32(const float* q, const float* k_cache, const floa
     const int64_t chunks = (max_seq + chunk - 1) / chunk;
     if (chunks > 65535) return fail_inval("attention_decode: max_seq too large");
     Workspace ws;
-    int st = get_workspace(S(stream), static_cast<std::size_t>(heads * chunks * (head_dim + 2)),
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+        return fail_inval("attention_decode: operands must be 16-byte aligned");
+    if (max_seq * head_dim > (int64_t{1} << 28)) return fail_inval("attention_decode: cache too large");
+    int st = get_workspace(S(stream), static_cast<std::size_t>(heads * chunks * (head_dim + 4)),
                            static_cast<std::size_t>(kv_heads), &ws);
     if (st) return st;
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
@@ -524,8 +731,15 @@ int vm_hip_silu_mul_f32(const float* gate_up, float* out, int64_t rows, int64_t 
     if (rows < 0 || inter < 0) return fail_inval("silu_mul: negative size");
     if (rows == 0 || inter == 0) return 0;
     if (!gate_up || !out) return fail_inval("silu_mul: null pointer");
-    hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(rows * inter)), dim3(kT), 0, S(stream), gate_up, out, rows,
-                       inter);
+    if (inter % 4 == 0 && rows * inter <= 0x7fffffff && aligned16(gate_up) && aligned16(out)) {
+        const int total4 = static_cast<int>(rows * inter / 4);
+        hipLaunchKernelGGL(silu_mul_vec_kernel, dim3((total4 + kT - 1) / kT), dim3(kT), 0, S(stream),
+                           reinterpret_cast<const float4*>(gate_up), reinterpret_cast<float4*>(out),
+                           static_cast<int>(rows), static_cast<int>(inter / 4));
+    } else {
+        hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(rows * inter)), dim3(kT), 0, S(stream), gate_up, out, rows,
+                           inter);
+    }
     return check_launch("silu_mul", S(stream));
 }
 
@@ -534,7 +748,8 @@ int vm_hip_argmax_f32(const float* x, int64_t n, int32_t* token_out, int32_t* po
     clear_error();
     if (n < 1 || n > 0x7fffffff) return fail_inval("argmax: n must be in [1, 2^31)");
     if (!x || !token_out) return fail_inval("argmax: null pointer");
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, S(stream), x, n, token_out, pos, tokens, max_seq);
+    const int vec = aligned16(x) && n < (int64_t{1} << 29) ? 1 : 0;
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgT), 0, S(stream), x, n, token_out, pos, tokens, max_seq, vec);
     return check_launch("argmax", S(stream));
 }
 
