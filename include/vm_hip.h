@@ -322,6 +322,51 @@ int vm_hip_silu_mul_f32(const float* gate_up, float* out, int64_t rows, int64_t 
 int vm_hip_argmax_f32(const float* x, int64_t n, int32_t* token_out, int32_t* pos,
                       int32_t* tokens, int64_t max_seq, void* stream);
 
+/* ---- Split-K decode GEMV with consumer-side reduction -------------------
+ * No counterpart in the reference: the resident decoder's projections.
+ * One activation row (M = 1) times a packed [k, n] matrix (quant.cpp
+ * layout, as vm_hip_qmm_f32); split s of the K range writes its partial
+ * sums to out[s * n + j] for s < slices, and the kernel that reads the
+ * result adds the slices in order s = 0, 1, ...  The slice count is a
+ * function of (k, n, quant_type, block_size, max_slices) only:
+ * vm_hip_gemv_slices_count returns it.  INT4 blocks and INT8 blocks must
+ * hold a multiple of 8 byte rows (INT8 per-column scales: block_size 0);
+ * n % 16 == 0 and k % 4 == 0.  The activation row comes from
+ *   VM_HIP_GEMV_SRC_PLAIN   act[k]
+ *   VM_HIP_GEMV_SRC_SLICES  the sum of act_slices slices [act_slices][k]
+ *   VM_HIP_GEMV_SRC_SWIGLU  silu(g) * u, g and u the sums of act_slices
+ *                           slices [act_slices][2k] of a fused gate|up
+ *                           projection (g = columns 0..k-1, u = k..2k-1),
+ *                           the Sigmoid/Mul/Mul of llama_graph.cpp:22-28 */
+#define VM_HIP_GEMV_SRC_PLAIN  0
+#define VM_HIP_GEMV_SRC_SLICES 1
+#define VM_HIP_GEMV_SRC_SWIGLU 2
+int vm_hip_gemv_slices_count(int64_t k, int64_t n, int quant_type, int block_size, int max_slices,
+                             int* slices);
+int vm_hip_qmm_gemv_slices_f32(const float* act, int act_kind, int64_t act_slices, const int8_t* wq,
+                               const float* scale, float* out, int64_t k, int64_t n, int quant_type,
+                               int block_size, int max_slices, void* stream);
+
+/* Consumers of partial slices (no counterpart in the reference; the
+ * decode step of the resident decoder):
+ *   add_rmsnorm_slices  one row: h += sum of delta_slices slices
+ *                       [delta_slices][dim] (in order; 0 = no residual),
+ *                       hn = rmsnorm(h) * w; dim % 4 == 0, dim <= 8192,
+ *                       16-byte aligned operands
+ *   rope_kv_append_slices  vm_hip_rope_kv_append_f32 for one row whose
+ *                       projection is qkv_slices slices [qkv_slices][width]
+ *   argmax_slices       vm_hip_argmax_f32 of the sum of slices [slices][n]
+ *   slices_sum          out[j] = sum over s of in[s * n + j] */
+int vm_hip_add_rmsnorm_slices_f32(float* h, const float* delta, int64_t delta_slices, const float* w,
+                                  float* hn, int64_t dim, float eps, void* stream);
+int vm_hip_rope_kv_append_slices_f32(const float* qkv, int64_t qkv_slices, const float* cos_table,
+                                     const float* sin_table, const int32_t* pos, float* q_out,
+                                     float* k_cache, float* v_cache, int64_t heads, int64_t kv_heads,
+                                     int64_t head_dim, int64_t max_seq, void* stream);
+int vm_hip_argmax_slices_f32(const float* x, int64_t slices, int64_t n, int32_t* token_out,
+                             int32_t* pos, int32_t* tokens, int64_t max_seq, void* stream);
+int vm_hip_slices_sum_f32(const float* in, int64_t slices, int64_t n, float* out, void* stream);
+
 /* Asynchronous 2-D device copy: `rows` rows of `width` bytes from src
  * (row pitch spitch) to dst (row pitch dpitch).  Used to assemble fused
  * weight matrices column block by column block. */

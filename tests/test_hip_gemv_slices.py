@@ -1,0 +1,213 @@
+"""Split-K decode GEMV with consumer-side reduction
+(vm_hip_qmm_gemv_slices_f32) and the kernels that consume its partial
+slices (add_rmsnorm_slices, rope_kv_append_slices, argmax_slices,
+slices_sum), against the oracle through the C ABI.
+
+The sum of the slices must equal the reference QuantizedMatMul
+(src/cpu/ops/quantized_matmul.cpp:48-141) within 1e-5 of max|ref|: fp32
+accumulation on both sides, only the summation order differs, and a wrong
+nibble, scale index, block or slice would miss the bound by orders of
+magnitude.  Argmax results and copied values are exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import llama_oracle as L
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _normal(shape, seed, std=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * std).astype(np.float32)
+
+
+def _close(out, ref, rel, what=""):
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(np.asarray(out, np.float64) - ref).max()
+    bound = rel * max(np.abs(ref).max(), 1e-30)
+    assert err <= bound, f"{what}: max abs err {err:.3e} > {bound:.3e}"
+
+
+def _dev(hip, a, dtype=np.float32):
+    return hip.DeviceBuffer.from_array(np.ascontiguousarray(a, dtype))
+
+
+def _pack(k, n, qt, block, seed):
+    w = _normal((k, n), seed, 0.02)
+    if qt == O.QUANT_INT4:
+        p, s = O.quantize_int4(w, block)
+        return p.view(np.int8), s
+    if block:
+        # INT8 blockwise scales, the reference's blocked INT8 path
+        # (quantized_matmul.cpp:97-122): per (block, column) max / 127.
+        nb = (k + block - 1) // block
+        s = np.ones((nb, n), np.float32)
+        q = np.zeros((k, n), np.int8)
+        for b in range(nb):
+            blk = w[b * block:(b + 1) * block]
+            mx = np.abs(blk).max(axis=0)
+            sc = np.where(mx > 0, mx / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+            s[b] = sc
+            q[b * block:(b + 1) * block] = np.clip(np.round(blk / sc), -127, 127).astype(np.int8)
+        return q, s
+    return O.quantize_int8(w)
+
+
+def _count(hip, k, n, qt, block, max_slices):
+    import ctypes
+    out = ctypes.c_int(0)
+    hip.check(hip.open_library().vm_hip_gemv_slices_count(k, n, qt, block, max_slices, ctypes.byref(out)))
+    return out.value
+
+
+def _run(hip, x_src, kind, act_slices, q, s, k, n, qt, block, max_slices=64):
+    lib = hip.open_library()
+    sl = _count(hip, k, n, qt, block, max_slices)
+    assert 1 <= sl <= max_slices
+    dx, dq, ds, do = _dev(hip, x_src), _dev(hip, q, np.int8), _dev(hip, s), hip.DeviceBuffer(sl * n * 4)
+    hip.check(lib.vm_hip_qmm_gemv_slices_f32(dx.ptr, kind, act_slices, dq.ptr, ds.ptr, do.ptr, k, n, qt, block,
+                                             max_slices, None))
+    return do.download(np.float32, (sl, n)), sl
+
+
+CASES = [
+    # (k, n, quant, block, max_slices): TinyLlama INT4 decode shapes, SmolLM2 INT8, tails
+    (2048, 2560, O.QUANT_INT4, 32, 64),
+    (2048, 2048, O.QUANT_INT4, 32, 64),
+    (5632, 2048, O.QUANT_INT4, 32, 22),
+    (2048, 11264, O.QUANT_INT4, 32, 64),
+    (2048, 32000, O.QUANT_INT4, 32, 8),
+    (960, 1600, O.QUANT_INT4, 32, 64),      # partial last tile, K not a multiple of a workgroup's rows
+    (64, 16, O.QUANT_INT4, 32, 64),
+    (2048, 2048, O.QUANT_INT4, 64, 64),
+    (960, 1600, O.QUANT_INT8, 0, 64),       # SmolLM2-360M q|k|v
+    (2560, 960, O.QUANT_INT8, 0, 22),       # SmolLM2-360M down
+    (960, 49152, O.QUANT_INT8, 0, 8),       # SmolLM2-360M lm_head
+    (1024, 512, O.QUANT_INT8, 32, 64),      # INT8 blockwise
+]
+
+
+@pytest.mark.parametrize("k,n,qt,block,max_slices", CASES)
+def test_gemv_slices_plain(hip, k, n, qt, block, max_slices):
+    q, s = _pack(k, n, qt, block, k * 7 + n)
+    x = _normal((1, k), k + n)
+    print(f"case gemv_slices plain k={k} n={n} qt={qt} block={block}", flush=True)
+    out, sl = _run(hip, x, hip.GEMV_SRC_PLAIN, 0, q, s, k, n, qt, block, max_slices)
+    ref = O.qmm(x, q, s, k, qt, block)
+    _close(out.sum(axis=0, dtype=np.float64), ref[0], TOL, f"{sl} slices")
+
+
+@pytest.mark.parametrize("in_slices", [1, 3, 16, 22])
+def test_gemv_slices_from_slices(hip, in_slices):
+    k, n = 2048, 2048
+    q, s = _pack(k, n, O.QUANT_INT4, 32, 5)
+    src = _normal((in_slices, k), in_slices)
+    x = src[0].copy()
+    for i in range(1, in_slices):
+        x = (x + src[i]).astype(np.float32)
+    print(f"case gemv_slices from {in_slices} slices", flush=True)
+    out, _ = _run(hip, src, hip.GEMV_SRC_SLICES, in_slices, q, s, k, n, O.QUANT_INT4, 32)
+    _close(out.sum(axis=0, dtype=np.float64), O.qmm(x[None], q, s, k, O.QUANT_INT4, 32)[0], TOL)
+
+
+@pytest.mark.parametrize("k,n,qt,block,in_slices", [(5632, 2048, O.QUANT_INT4, 32, 16),
+                                                     (2560, 960, O.QUANT_INT8, 0, 15),
+                                                     (256, 64, O.QUANT_INT4, 32, 1)])
+def test_gemv_slices_swiglu(hip, k, n, qt, block, in_slices):
+    q, s = _pack(k, n, qt, block, 9)
+    gu = _normal((in_slices, 2 * k), k, 0.7)
+    g, u = gu[0, :k].copy(), gu[0, k:].copy()
+    for i in range(1, in_slices):
+        g = (g + gu[i, :k]).astype(np.float32)
+        u = (u + gu[i, k:]).astype(np.float32)
+    x = L.silu_mul(g, u)
+    print(f"case gemv_slices swiglu k={k} n={n} in_slices={in_slices}", flush=True)
+    out, _ = _run(hip, gu, hip.GEMV_SRC_SWIGLU, in_slices, q, s, k, n, qt, block, 22)
+    _close(out.sum(axis=0, dtype=np.float64), O.qmm(x[None], q, s, k, qt, block)[0], TOL)
+
+
+def test_gemv_slices_is_deterministic_and_counts_are_stable(hip):
+    k, n = 5632, 2048
+    q, s = _pack(k, n, O.QUANT_INT4, 32, 1)
+    x = _normal((1, k), 2)
+    a, sa = _run(hip, x, hip.GEMV_SRC_PLAIN, 0, q, s, k, n, O.QUANT_INT4, 32, 22)
+    b, sb = _run(hip, x, hip.GEMV_SRC_PLAIN, 0, q, s, k, n, O.QUANT_INT4, 32, 22)
+    assert sa == sb == _count(hip, k, n, O.QUANT_INT4, 32, 22)
+    assert np.array_equal(a, b)
+    # a tighter slice limit gives fewer slices, same result within fp32 rounding
+    c, sc = _run(hip, x, hip.GEMV_SRC_PLAIN, 0, q, s, k, n, O.QUANT_INT4, 32, 11)
+    assert sc <= 11
+    _close(c.sum(axis=0, dtype=np.float64), a.sum(axis=0, dtype=np.float64), TOL)
+
+
+def test_gemv_slices_rejects_unsupported(hip):
+    import ctypes
+    lib = hip.open_library()
+    out = ctypes.c_int(0)
+    assert lib.vm_hip_gemv_slices_count(2048, 100, O.QUANT_INT4, 32, 64, ctypes.byref(out)) == hip.EINVAL
+    assert lib.vm_hip_gemv_slices_count(2048, 2048, O.QUANT_INT8, 8, 64, ctypes.byref(out)) == hip.EUNSUPPORTED
+    assert lib.vm_hip_gemv_slices_count(5632, 2048, O.QUANT_INT4, 32, 2, ctypes.byref(out)) == hip.EUNSUPPORTED
+    buf = hip.DeviceBuffer(1 << 20)
+    assert lib.vm_hip_qmm_gemv_slices_f32(buf.addr + 4, hip.GEMV_SRC_PLAIN, 0, buf.ptr, buf.ptr, buf.ptr, 256, 64,
+                                          O.QUANT_INT4, 32, 64, None) == hip.EINVAL      # unaligned activation
+
+
+@pytest.mark.parametrize("dim,slices", [(2048, 0), (2048, 1), (2048, 16), (960, 22), (5632, 4), (8192, 3)])
+def test_add_rmsnorm_slices(hip, dim, slices):
+    h = _normal(dim, dim, 2.0)
+    d = _normal((max(slices, 1), dim), slices + 1)
+    w = np.random.default_rng(3).uniform(0.5, 1.5, dim).astype(np.float32)
+    dh, dd, dw, dn = _dev(hip, h), _dev(hip, d), _dev(hip, w), hip.DeviceBuffer(dim * 4)
+    print(f"case add_rmsnorm_slices dim={dim} slices={slices}", flush=True)
+    hip.check(hip.open_library().vm_hip_add_rmsnorm_slices_f32(dh.ptr, dd.ptr if slices else None, slices, dw.ptr,
+                                                               dn.ptr, dim, 1e-5, None))
+    ref_h = h.copy()
+    for i in range(slices):
+        ref_h = (ref_h + d[i]).astype(np.float32)
+    assert np.array_equal(dh.download(np.float32, (dim,)), ref_h)   # same additions in the same order
+    _close(dn.download(np.float32, (dim,)), L.rmsnorm(ref_h, w, 1e-5), 1e-5, "rmsnorm")
+
+
+def test_rope_kv_append_slices(hip):
+    heads, kv_heads, d, max_seq, p0, slices = 8, 2, 64, 40, 17, 5
+    width = (heads + 2 * kv_heads) * d
+    qkv = _normal((slices, width), 4)
+    tot = qkv[0].copy()
+    for i in range(1, slices):
+        tot = (tot + qkv[i]).astype(np.float32)
+    cos, sin = L.rope_cache(max_seq, d, 10000.0)
+    kc0, vc0 = _normal((kv_heads, max_seq, d), 5), _normal((kv_heads, max_seq, d), 6)
+    dq, dc, ds = _dev(hip, qkv), _dev(hip, cos), _dev(hip, sin)
+    dk, dv, dqo = _dev(hip, kc0), _dev(hip, vc0), hip.DeviceBuffer(heads * d * 4)
+    dpos = _dev(hip, np.array([p0], np.int32), np.int32)
+    hip.check(hip.open_library().vm_hip_rope_kv_append_slices_f32(dq.ptr, slices, dc.ptr, ds.ptr, dpos.ptr, dqo.ptr,
+                                                                  dk.ptr, dv.ptr, heads, kv_heads, d, max_seq, None))
+    c, s = cos[p0:p0 + 1], sin[p0:p0 + 1]
+    qs = tot[:heads * d].reshape(heads, 1, d)
+    ks = tot[heads * d:(heads + kv_heads) * d].reshape(kv_heads, 1, d)
+    vs = tot[(heads + kv_heads) * d:].reshape(kv_heads, d)
+    _close(dqo.download(np.float32, (heads, 1, d)), L.rope(qs, c, s), 1e-6, "q")
+    kc, vc = kc0.copy(), vc0.copy()
+    kc[:, p0] = L.rope(ks, c, s)[:, 0]
+    vc[:, p0] = vs
+    _close(dk.download(np.float32, kc.shape), kc, 1e-6, "k cache")
+    assert np.array_equal(dv.download(np.float32, vc.shape), vc)
+
+
+@pytest.mark.parametrize("n,slices", [(32000, 8), (49152, 4), (1000, 3), (37, 2)])
+def test_argmax_and_sum_of_slices(hip, n, slices):
+    x = _normal((slices, n), n)
+    tot = x[0].copy()
+    for i in range(1, slices):
+        tot = (tot + x[i]).astype(np.float32)
+    dx, dt, ds = _dev(hip, x), hip.DeviceBuffer(4), hip.DeviceBuffer(n * 4)
+    lib = hip.open_library()
+    hip.check(lib.vm_hip_argmax_slices_f32(dx.ptr, slices, n, dt.ptr, None, None, 0, None))
+    hip.check(lib.vm_hip_slices_sum_f32(dx.ptr, slices, n, ds.ptr, None))
+    assert np.array_equal(ds.download(np.float32, (n,)), tot)
+    assert int(dt.download(np.int32, (1,))[0]) == int(np.argmax(tot))

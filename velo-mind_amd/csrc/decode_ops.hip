@@ -58,6 +58,22 @@ __global__ void fill_normal_kernel(float* __restrict__ dst, int64_t n, uint64_t 
     }
 }
 
+// With `slices` > 1 the projection arrives as split-K partial slices
+// [slices][rows * width] (vm_hip_qmm_gemv_slices_f32); each value read is
+// their sum in slice order.
+__device__ __forceinline__ float slice_sum(const float* p, int slices, int64_t stride) {
+    float v = p[0];
+    for (int s0 = 1; s0 < slices; s0 += 8) {
+        float t[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = s0 + e < slices ? p[(s0 + e) * stride] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (s0 + e < slices) v += t[e];
+    }
+    return v;
+}
+
 // ---- h += delta (optional), hn = rmsnorm(h) * w, one workgroup per row.
 // The add is the reference's Add node (add.cpp) and the norm its RMSNorm
 // (rmsnorm.cpp:17-60) on the sum.
@@ -149,6 +165,87 @@ __global__ __launch_bounds__(kT) void add_rmsnorm_kernel(float* __restrict__ h, 
     for (int64_t i = threadIdx.x; i < dim; i += kT) nr[i] = hr[i] * inv * w[i];
 }
 
+// ---- One row: h += sum of `slices` split-K partial slices of the
+// previous projection ([slices][dim], added in slice order), hn =
+// rmsnorm(h) * w.  The residual Add and RMSNorm of llama_graph.cpp:118-
+// 136 on the consumer side of vm_hip_qmm_gemv_slices_f32.  512 threads,
+// NV float4 of the row per thread (dim <= 2048 * NV, dim % 4 == 0), every
+// load of a batch of slices issued before its first use.
+constexpr int kNormT = 512;
+
+template <int NV>
+__global__ __launch_bounds__(kNormT) void add_rmsnorm_slices_kernel(float* __restrict__ h,
+                                                                    const float* __restrict__ delta, int slices,
+                                                                    const float* __restrict__ w,
+                                                                    float* __restrict__ hn, int dim, float eps) {
+    __shared__ float part[kNormT / 64];
+    const uint32_t row_bytes = static_cast<uint32_t>(dim) * 4u;
+    const __amdgpu_buffer_rsrc_t hrs = buffer_rsrc(h, row_bytes);
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(w, row_bytes);
+    const __amdgpu_buffer_rsrc_t drs = buffer_rsrc(delta, static_cast<uint32_t>(slices) * row_bytes);
+    float x[NV][4];
+    u32x4 wv[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const uint32_t off = (threadIdx.x + u * kNormT) * 16u;
+        const u32x4 hv = buffer_load16(hrs, off);
+        wv[u] = buffer_load16(wrs, off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[u][e] = __uint_as_float(hv[e]);
+    }
+    // The residual plus the slices in order: ((h + d0) + d1) + ...
+    for (int s0 = 0; s0 < slices; s0 += 8) {
+        u32x4 dv[8][NV];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int u = 0; u < NV; ++u)
+                // Past the row a load would reach the next slice: read zeros instead.
+                dv[e][u] = buffer_load16(drs, (s0 + e < slices && 4 * (threadIdx.x + u * kNormT) < dim)
+                                                  ? (static_cast<uint32_t>(s0 + e) * row_bytes +
+                                                     (threadIdx.x + u * kNormT) * 16u)
+                                                  : 0xfffffff0u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (s0 + e < slices)
+#pragma unroll
+                for (int u = 0; u < NV; ++u)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) x[u][c] = x[u][c] + __uint_as_float(dv[e][u][c]);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s = fmaf(x[u][c], x[u][c], s);
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormT / 64; ++i) tot += part[i];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(dim) + eps);
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int i4 = threadIdx.x + u * kNormT;
+        if (4 * i4 < dim) {
+            if (slices > 0) *reinterpret_cast<float4*>(h + 4 * i4) = make_float4(x[u][0], x[u][1], x[u][2], x[u][3]);
+            float4 y;
+            y.x = x[u][0] * inv * __uint_as_float(wv[u][0]);
+            y.y = x[u][1] * inv * __uint_as_float(wv[u][1]);
+            y.z = x[u][2] * inv * __uint_as_float(wv[u][2]);
+            y.w = x[u][3] * inv * __uint_as_float(wv[u][3]);
+            *reinterpret_cast<float4*>(hn + 4 * i4) = y;
+        }
+    }
+}
+
+// ---- out[j] = sum over s of in[s * n + j], slices in order.
+__global__ void slices_sum_kernel(const float* __restrict__ in, int slices, int64_t n, float* __restrict__ out) {
+    for (int64_t j = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; j < n; j += static_cast<int64_t>(gridDim.x) * kT)
+        out[j] = slice_sum(in + j, slices, n);
+}
+
 // ---- RoPE on the fused QKV projection and in-place KV append.
 // qkv rows: [S, (H + 2 Hkv) * D] = q heads, k heads, v heads.  Row r sits
 // at position p = *pos + r: q is rotated into q_out [H, S, D] (the graph's
@@ -159,7 +256,7 @@ __global__ void rope_kv_append_kernel(const float* __restrict__ qkv, const float
                                       const float* __restrict__ sin_t, const int32_t* __restrict__ pos,
                                       float* __restrict__ q_out, float* __restrict__ k_cache,
                                       float* __restrict__ v_cache, int64_t rows, int64_t heads, int64_t kv_heads,
-                                      int64_t d, int64_t max_seq) {
+                                      int64_t d, int64_t max_seq, int slices) {
     const int64_t half = d / 2;
     const int64_t width = (heads + 2 * kv_heads) * d;
     const int64_t p0 = pos[0];
@@ -178,7 +275,8 @@ __global__ void rope_kv_append_kernel(const float* __restrict__ qkv, const float
             const int64_t hh = t / half;
             const int64_t j = t - hh * half;
             const float* x = src + hh * d;
-            const float a = x[j], b = x[j + half];
+            const int64_t stride = rows * width;
+            const float a = slice_sum(x + j, slices, stride), b = slice_sum(x + j + half, slices, stride);
             const float c = cos_t[p * half + j], s = sin_t[p * half + j];
             const float y0 = a * c - b * s;
             const float y1 = b * c + a * s;
@@ -195,7 +293,7 @@ __global__ void rope_kv_append_kernel(const float* __restrict__ qkv, const float
             const int64_t u = t - rot;
             const int64_t hv = u / d;
             const int64_t j = u - hv * d;
-            v_cache[(hv * max_seq + p) * d + j] = src[(heads + kv_heads + hv) * d + j];
+            v_cache[(hv * max_seq + p) * d + j] = slice_sum(src + (heads + kv_heads + hv) * d + j, slices, rows * width);
         }
     }
 }
@@ -541,26 +639,46 @@ __device__ __forceinline__ bool argmax_better(float v1, int i1, float v2, int i2
 
 __global__ __launch_bounds__(kArgT) void argmax_kernel(const float* __restrict__ x, int64_t n,
                                                        int32_t* __restrict__ token_out, int32_t* __restrict__ pos,
-                                                       int32_t* __restrict__ tokens, int64_t max_seq, int vec) {
+                                                       int32_t* __restrict__ tokens, int64_t max_seq, int vec,
+                                                       int slices) {
     __shared__ float bv[kArgT / 64];
     __shared__ int bi[kArgT / 64];
     float best = -INFINITY;
     int idx = -1;
     if (vec) {
         // 16-byte aligned x: element 4q + c of pass p is x[p * 32768 + 4 * (tid + u * 1024) + c].
-        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(x, static_cast<uint32_t>(n) * 4u);
+        // Slices (split-K partial logits [slices][n]) are added in slice
+        // order before the comparison.
+        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(x, static_cast<uint32_t>(n * slices) * 4u);
         constexpr int kPass = kArgT * kArgVec * 4;
         for (int64_t p0 = 0; p0 < n; p0 += kPass) {
-            u32x4 t[kArgVec];
+            float t[kArgVec][4];
+            {
+                u32x4 l[kArgVec];
 #pragma unroll
-            for (int u = 0; u < kArgVec; ++u)
-                t[u] = buffer_load16(rs, static_cast<uint32_t>(p0 + 4 * (threadIdx.x + u * kArgT)) * 4u);
+                for (int u = 0; u < kArgVec; ++u)
+                    l[u] = buffer_load16(rs, static_cast<uint32_t>(p0 + 4 * (threadIdx.x + u * kArgT)) * 4u);
+#pragma unroll
+                for (int u = 0; u < kArgVec; ++u)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) t[u][c] = __uint_as_float(l[u][c]);
+            }
+            for (int sl = 1; sl < slices; ++sl) {
+                u32x4 l[kArgVec];
+#pragma unroll
+                for (int u = 0; u < kArgVec; ++u)
+                    l[u] = buffer_load16(rs, static_cast<uint32_t>(sl * n + p0 + 4 * (threadIdx.x + u * kArgT)) * 4u);
+#pragma unroll
+                for (int u = 0; u < kArgVec; ++u)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) t[u][c] += __uint_as_float(l[u][c]);
+            }
 #pragma unroll
             for (int u = 0; u < kArgVec; ++u)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int64_t i = p0 + 4 * (threadIdx.x + u * kArgT) + c;
-                    const float v = __uint_as_float(t[u][c]);
+                    const float v = t[u][c];
                     if (i < n && v == v && (idx < 0 || v > best)) {
                         best = v;
                         idx = static_cast<int>(i);
@@ -569,7 +687,8 @@ __global__ __launch_bounds__(kArgT) void argmax_kernel(const float* __restrict__
         }
     } else {
         for (int64_t i = threadIdx.x; i < n; i += kArgT) {
-            const float v = x[i];
+            float v = x[i];
+            for (int sl = 1; sl < slices; ++sl) v += x[sl * n + i];
             if (v != v) continue;
             if (idx < 0 || v > best) {
                 best = v;
@@ -666,7 +785,7 @@ int vm_hip_rope_kv_append_f32(const float* qkv, int64_t rows, const float* cos_t
         return fail_inval("rope_kv_append: null pointer");
     const int64_t work = rows * ((heads + kv_heads) * (head_dim / 2) + kv_heads * head_dim);
     hipLaunchKernelGGL(rope_kv_append_kernel, dim3(grid_for(work)), dim3(kT), 0, S(stream), qkv, cos_table, sin_table,
-                       pos, q_out, k_cache, v_cache, rows, heads, kv_heads, head_dim, max_seq);
+                       pos, q_out, k_cache, v_cache, rows, heads, kv_heads, head_dim, max_seq, 1);
     return check_launch("rope_kv_append", S(stream));
 }
 
@@ -749,8 +868,68 @@ int vm_hip_argmax_f32(const float* x, int64_t n, int32_t* token_out, int32_t* po
     if (n < 1 || n > 0x7fffffff) return fail_inval("argmax: n must be in [1, 2^31)");
     if (!x || !token_out) return fail_inval("argmax: null pointer");
     const int vec = aligned16(x) && n < (int64_t{1} << 29) ? 1 : 0;
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgT), 0, S(stream), x, n, token_out, pos, tokens, max_seq, vec);
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgT), 0, S(stream), x, n, token_out, pos, tokens, max_seq, vec,
+                       1);
     return check_launch("argmax", S(stream));
+}
+
+int vm_hip_add_rmsnorm_slices_f32(float* h, const float* delta, int64_t delta_slices, const float* w, float* hn,
+                                  int64_t dim, float eps, void* stream) {
+    clear_error();
+    if (dim < 4 || dim % 4 != 0 || dim > 4 * 2048) return fail_inval("add_rmsnorm_slices: dim must be a multiple of 4 in [4, 8192]");
+    if (delta_slices < 0 || delta_slices > 4096) return fail_inval("add_rmsnorm_slices: delta_slices must be in [0, 4096]");
+    if (!h || !w || !hn || (delta_slices > 0 && !delta)) return fail_inval("add_rmsnorm_slices: null pointer");
+    if (!aligned16(h) || !aligned16(w) || !aligned16(hn) || (delta && !aligned16(delta)))
+        return fail_inval("add_rmsnorm_slices: operands must be 16-byte aligned");
+    if (delta_slices * dim * 4 > 0x7fffffffLL) return fail_inval("add_rmsnorm_slices: slices too large");
+    const int d = static_cast<int>(dim), sl = static_cast<int>(delta_slices);
+    const float* dp = delta ? delta : w;
+    if (dim <= 4 * kNormT)
+        hipLaunchKernelGGL(add_rmsnorm_slices_kernel<1>, dim3(1), dim3(kNormT), 0, S(stream), h, dp, sl, w, hn, d, eps);
+    else if (dim <= 2 * 4 * kNormT)
+        hipLaunchKernelGGL(add_rmsnorm_slices_kernel<2>, dim3(1), dim3(kNormT), 0, S(stream), h, dp, sl, w, hn, d, eps);
+    else
+        hipLaunchKernelGGL(add_rmsnorm_slices_kernel<4>, dim3(1), dim3(kNormT), 0, S(stream), h, dp, sl, w, hn, d, eps);
+    return check_launch("add_rmsnorm_slices", S(stream));
+}
+
+int vm_hip_rope_kv_append_slices_f32(const float* qkv, int64_t qkv_slices, const float* cos_table,
+                                     const float* sin_table, const int32_t* pos, float* q_out, float* k_cache,
+                                     float* v_cache, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                     int64_t max_seq, void* stream) {
+    clear_error();
+    if (heads < 1 || kv_heads < 1 || head_dim < 2 || head_dim % 2 || max_seq < 1 || heads % kv_heads)
+        return fail_inval("rope_kv_append_slices: bad shape");
+    if (qkv_slices < 1 || qkv_slices > 4096) return fail_inval("rope_kv_append_slices: qkv_slices must be in [1, 4096]");
+    if (!qkv || !cos_table || !sin_table || !pos || !q_out || !k_cache || !v_cache)
+        return fail_inval("rope_kv_append_slices: null pointer");
+    const int64_t work = (heads + kv_heads) * (head_dim / 2) + kv_heads * head_dim;
+    hipLaunchKernelGGL(rope_kv_append_kernel, dim3(grid_for(work)), dim3(kT), 0, S(stream), qkv, cos_table, sin_table,
+                       pos, q_out, k_cache, v_cache, int64_t{1}, heads, kv_heads, head_dim, max_seq,
+                       static_cast<int>(qkv_slices));
+    return check_launch("rope_kv_append_slices", S(stream));
+}
+
+int vm_hip_argmax_slices_f32(const float* x, int64_t slices, int64_t n, int32_t* token_out, int32_t* pos,
+                             int32_t* tokens, int64_t max_seq, void* stream) {
+    clear_error();
+    if (n < 1 || n > 0x7fffffff) return fail_inval("argmax_slices: n must be in [1, 2^31)");
+    if (slices < 1 || slices > 4096) return fail_inval("argmax_slices: slices must be in [1, 4096]");
+    if (!x || !token_out) return fail_inval("argmax_slices: null pointer");
+    const int vec = aligned16(x) && n % 4 == 0 && n * slices < (int64_t{1} << 29) ? 1 : 0;
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgT), 0, S(stream), x, n, token_out, pos, tokens, max_seq, vec,
+                       static_cast<int>(slices));
+    return check_launch("argmax_slices", S(stream));
+}
+
+int vm_hip_slices_sum_f32(const float* in, int64_t slices, int64_t n, float* out, void* stream) {
+    clear_error();
+    if (n < 0 || slices < 1 || slices > 4096) return fail_inval("slices_sum: bad size");
+    if (n == 0) return 0;
+    if (!in || !out) return fail_inval("slices_sum: null pointer");
+    hipLaunchKernelGGL(slices_sum_kernel, dim3(grid_for(n)), dim3(kT), 0, S(stream), in, static_cast<int>(slices), n,
+                       out);
+    return check_launch("slices_sum", S(stream));
 }
 
 }  // extern "C"

@@ -83,6 +83,12 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_silu_mul_f32": ([p, p, c_int64, c_int64, p], c_int),
         "vm_hip_argmax_f32": ([p, c_int64, p, p, p, c_int64, p], c_int),
         "vm_hip_memcpy_2d_d2d": ([p, c_size_t, p, c_size_t, c_size_t, c_size_t, p], c_int),
+        "vm_hip_gemv_slices_count": ([c_int64, c_int64, c_int, c_int, c_int, POINTER(c_int)], c_int),
+        "vm_hip_qmm_gemv_slices_f32": ([p, c_int, c_int64, p, p, p, c_int64, c_int64, c_int, c_int, c_int, p], c_int),
+        "vm_hip_add_rmsnorm_slices_f32": ([p, p, c_int64, p, p, c_int64, c_float, p], c_int),
+        "vm_hip_rope_kv_append_slices_f32": ([p, c_int64, p, p, p, p, p, p] + [c_int64] * 4 + [p], c_int),
+        "vm_hip_argmax_slices_f32": ([p, c_int64, c_int64, p, p, p, c_int64, p], c_int),
+        "vm_hip_slices_sum_f32": ([p, c_int64, c_int64, p, p], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -104,7 +110,9 @@ def exported_symbols() -> list[str]:
             "vm_hip_slice_f32", "vm_hip_concat_f32", "vm_hip_repeat_kv_f32", "vm_hip_elementwise_f32",
             "vm_hip_softmax_f32", "vm_hip_matmul_f32", "vm_hip_attention_f32", "vm_hip_fill_normal_f32",
             "vm_hip_add_rmsnorm_f32", "vm_hip_rope_kv_append_f32", "vm_hip_attention_decode_f32",
-            "vm_hip_attention_prefill_f32", "vm_hip_silu_mul_f32", "vm_hip_argmax_f32", "vm_hip_memcpy_2d_d2d"]
+            "vm_hip_attention_prefill_f32", "vm_hip_silu_mul_f32", "vm_hip_argmax_f32", "vm_hip_memcpy_2d_d2d",
+            "vm_hip_gemv_slices_count", "vm_hip_qmm_gemv_slices_f32", "vm_hip_add_rmsnorm_slices_f32",
+            "vm_hip_rope_kv_append_slices_f32", "vm_hip_argmax_slices_f32", "vm_hip_slices_sum_f32"]
 
 
 def open_library() -> ctypes.CDLL:
@@ -333,6 +341,7 @@ def run_pack_int4(w: np.ndarray, block: int = 32):
 # ---- LLaMA graph operators, numpy level (one call each, null stream) ----
 
 EW_ADD, EW_MUL, EW_SIGMOID = 0, 1, 2
+GEMV_SRC_PLAIN, GEMV_SRC_SLICES, GEMV_SRC_SWIGLU = 0, 1, 2
 
 
 def _dev(a: np.ndarray, dtype=np.float32) -> DeviceBuffer:
