@@ -338,9 +338,41 @@ int vm_hip_argmax_f32(const float* x, int64_t n, int32_t* token_out, int32_t* po
  *                           slices [act_slices][2k] of a fused gate|up
  *                           projection (g = columns 0..k-1, u = k..2k-1),
  *                           the Sigmoid/Mul/Mul of llama_graph.cpp:22-28 */
-#define VM_HIP_GEMV_SRC_PLAIN  0
-#define VM_HIP_GEMV_SRC_SLICES 1
-#define VM_HIP_GEMV_SRC_SWIGLU 2
+#define VM_HIP_GEMV_SRC_PLAIN   0
+#define VM_HIP_GEMV_SRC_SLICES  1
+#define VM_HIP_GEMV_SRC_SWIGLU  2
+/* NORMRES  residual Add + RMSNorm in front of the projection
+ *          (llama_graph.cpp:118-136): h = act + sum of `slices` slices of
+ *          delta [slices][k] (0 slices: h = act), x = h * norm_w.  The
+ *          norm's 1/rms is left to the consumer (the projection is linear):
+ *          split s writes sum(h^2) over its K range to ss_out[s]; h_out
+ *          (optional) receives h.
+ * ATTN     x = decode attention output merged from per-chunk partials
+ *          act[(head * chunks + c) * (head_dim + 4)] = {m, l, -, -,
+ *          o[head_dim]} (vm_hip_attention_decode_slices_f32), chunks c with
+ *          c * chunk <= min(*pos, max_seq - 1), in chunk order.
+ * SWIGLU with ss_in != NULL first multiplies g and u by
+ *          1 / sqrt(sum(ss_in[0..ss_count)) / ss_dim + eps). */
+#define VM_HIP_GEMV_SRC_NORMRES 3
+#define VM_HIP_GEMV_SRC_ATTN    4
+typedef struct vm_hip_gemv_src {
+    int kind;               /* VM_HIP_GEMV_SRC_*                                   */
+    int slices;             /* SLICES/SWIGLU: act slices; NORMRES: delta slices     */
+    const float* act;       /* x, slices, residual h or attention partials          */
+    const float* delta;     /* NORMRES                                             */
+    const float* norm_w;    /* NORMRES                                             */
+    float* h_out;           /* NORMRES, optional                                   */
+    float* ss_out;          /* NORMRES, optional: [slices of this GEMV]             */
+    const float* ss_in;     /* SWIGLU, optional                                    */
+    int ss_count;
+    float ss_dim;
+    float eps;
+    const int32_t* pos;     /* ATTN                                                */
+    int head_dim, chunk, chunks, max_seq;   /* ATTN partial layout                 */
+} vm_hip_gemv_src;
+int vm_hip_qmm_gemv_slices_src_f32(const vm_hip_gemv_src* src, const int8_t* wq, const float* scale,
+                                   float* out, int64_t k, int64_t n, int quant_type, int block_size,
+                                   int max_slices, void* stream);
 int vm_hip_gemv_slices_count(int64_t k, int64_t n, int quant_type, int block_size, int max_slices,
                              int* slices);
 int vm_hip_qmm_gemv_slices_f32(const float* act, int act_kind, int64_t act_slices, const int8_t* wq,
@@ -366,6 +398,28 @@ int vm_hip_rope_kv_append_slices_f32(const float* qkv, int64_t qkv_slices, const
 int vm_hip_argmax_slices_f32(const float* x, int64_t slices, int64_t n, int32_t* token_out,
                              int32_t* pos, int32_t* tokens, int64_t max_seq, void* stream);
 int vm_hip_slices_sum_f32(const float* in, int64_t slices, int64_t n, float* out, void* stream);
+
+/* Decode attention fused with the split-K projection in front of it (no
+ * counterpart in the reference; the resident decoder's one-token step):
+ * q, the new key and the new value are the sums of qkv_slices slices
+ * [qkv_slices][(heads + 2 kv_heads) head_dim] times the RMSNorm scale
+ * 1 / sqrt(sum(ss[0..ss_count)) / ss_dim + eps) (ss_count 0: scale 1);
+ * q and the key are rotated at p = *pos (tables as
+ * vm_hip_rope_kv_append_f32), the key and value are written to the caches
+ * at row p, and attention over keys 0..p leaves one record per (head,
+ * chunk) in `partials` ([heads][chunks][head_dim + 4] = {m, l, -, -, o}),
+ * merged by the consumer (VM_HIP_GEMV_SRC_ATTN).  vm_hip_attention_decode_
+ * chunks gives the chunk length and count for (head_dim, max_seq).
+ * slices_sum_scaled: slices_sum times the RMSNorm scale of ss. */
+int vm_hip_attention_decode_chunks(int64_t head_dim, int64_t max_seq, int* chunk, int* chunks);
+int vm_hip_attention_decode_slices_f32(const float* qkv, int64_t qkv_slices, const float* ss,
+                                       int64_t ss_count, float ss_dim, float eps,
+                                       const float* cos_table, const float* sin_table,
+                                       const int32_t* pos, float* k_cache, float* v_cache,
+                                       float* partials, int64_t heads, int64_t kv_heads,
+                                       int64_t head_dim, int64_t max_seq, float scale, void* stream);
+int vm_hip_slices_sum_scaled_f32(const float* in, int64_t slices, int64_t n, const float* ss,
+                                 int64_t ss_count, float ss_dim, float eps, float* out, void* stream);
 
 /* Asynchronous 2-D device copy: `rows` rows of `width` bytes from src
  * (row pitch spitch) to dst (row pitch dpitch).  Used to assemble fused

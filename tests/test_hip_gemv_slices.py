@@ -211,3 +211,125 @@ def test_argmax_and_sum_of_slices(hip, n, slices):
     hip.check(lib.vm_hip_slices_sum_f32(dx.ptr, slices, n, ds.ptr, None))
     assert np.array_equal(ds.download(np.float32, (n,)), tot)
     assert int(dt.download(np.int32, (1,))[0]) == int(np.argmax(tot))
+
+
+def _src(hip, **kw):
+    s = hip.GemvSrc()
+    for key, val in kw.items():
+        setattr(s, key, val)
+    return s
+
+
+def _run_src(hip, src, q, s, k, n, qt, block, max_slices=64):
+    import ctypes
+    sl = _count(hip, k, n, qt, block, max_slices)
+    dq, ds, do = _dev(hip, q, np.int8), _dev(hip, s), hip.DeviceBuffer(sl * n * 4)
+    hip.check(hip.open_library().vm_hip_qmm_gemv_slices_src_f32(ctypes.byref(src), dq.ptr, ds.ptr, do.ptr, k, n, qt,
+                                                                 block, max_slices, None))
+    return do.download(np.float32, (sl, n)), sl
+
+
+@pytest.mark.parametrize("k,n,qt,block,delta_slices", [(2048, 2560, O.QUANT_INT4, 32, 22),
+                                                       (2048, 11264, O.QUANT_INT4, 32, 16),
+                                                       (960, 1600, O.QUANT_INT8, 0, 20),
+                                                       (2048, 2560, O.QUANT_INT4, 32, 0)])
+def test_gemv_slices_residual_norm_source(hip, k, n, qt, block, delta_slices):
+    """NORMRES: x = (h + sum delta) * w staged per split; the consumer's
+    scale 1/rms from the per-split sums of squares completes RMSNorm."""
+    q, s = _pack(k, n, qt, block, 21)
+    h = _normal(k, 1, 2.0)
+    d = _normal((max(delta_slices, 1), k), 2)
+    w = np.random.default_rng(4).uniform(0.5, 1.5, k).astype(np.float32)
+    sl = _count(hip, k, n, qt, block, 64)
+    dh, dd, dw = _dev(hip, h), _dev(hip, d), _dev(hip, w)
+    dho, dss = hip.DeviceBuffer(k * 4), hip.DeviceBuffer(sl * 4)
+    src = _src(hip, kind=hip.GEMV_SRC_NORMRES, slices=delta_slices, act=dh.addr, delta=dd.addr if delta_slices else None,
+               norm_w=dw.addr, h_out=dho.addr, ss_out=dss.addr)
+    print(f"case gemv_slices normres k={k} n={n} delta_slices={delta_slices}", flush=True)
+    out, _ = _run_src(hip, src, q, s, k, n, qt, block)
+    ref_h = h.copy()
+    for i in range(delta_slices):
+        ref_h = (ref_h + d[i]).astype(np.float32)
+    # the slices are added in a fixed grouping of their own (per staging part)
+    _close(dho.download(np.float32, (k,)), ref_h, 1e-6, "residual")
+    ss = dss.download(np.float32, (sl,)).astype(np.float64)
+    assert abs(ss.sum() - (ref_h.astype(np.float64) ** 2).sum()) <= 1e-5 * (ref_h.astype(np.float64) ** 2).sum()
+    inv = 1.0 / np.sqrt(ss.sum() / k + 1e-5)
+    ref = O.qmm(L.rmsnorm(ref_h, w, 1e-5)[None], q, s, k, qt, block)[0]
+    _close(out.sum(axis=0, dtype=np.float64) * inv, ref, TOL, "normed projection")
+
+
+@pytest.mark.parametrize("heads,kv_heads,d,max_seq,p,slices", [(32, 4, 64, 584, 530, 16),
+                                                                (32, 4, 64, 584, 0, 16),
+                                                                (32, 4, 64, 584, 63, 3),
+                                                                (15, 5, 64, 264, 200, 15),
+                                                                (8, 2, 128, 100, 64, 4)])
+def test_attention_decode_slices_and_merge_source(hip, heads, kv_heads, d, max_seq, p, slices):
+    """Fused decode attention (slice sums, RMSNorm scale, RoPE, in-place
+    K/V append, per-chunk partials) followed by the output projection that
+    merges the partials while staging: against the oracle's RMSNorm-scaled
+    q/k/v, RoPE, attention and QuantizedMatMul."""
+    import ctypes
+    lib = hip.open_library()
+    width = (heads + 2 * kv_heads) * d
+    hidden = heads * d
+    qkv = _normal((slices, width), p + 1)
+    ss = np.abs(_normal(7, 3, 50.0)) + 1.0
+    inv = np.float32(1.0 / np.sqrt(ss.astype(np.float32).sum(dtype=np.float32) / np.float32(hidden) + np.float32(1e-5)))
+    cos, sin = L.rope_cache(max_seq, d, 10000.0)
+    kc0, vc0 = _normal((kv_heads, max_seq, d), 5), _normal((kv_heads, max_seq, d), 6)
+    ch, chs = ctypes.c_int(0), ctypes.c_int(0)
+    hip.check(lib.vm_hip_attention_decode_chunks(d, max_seq, ctypes.byref(ch), ctypes.byref(chs)))
+    dqkv, dss, dc, dsn = _dev(hip, qkv), _dev(hip, ss), _dev(hip, cos), _dev(hip, sin)
+    dk, dv = _dev(hip, kc0), _dev(hip, vc0)
+    dpos = _dev(hip, np.array([p], np.int32), np.int32)
+    dpart = hip.DeviceBuffer(heads * chs.value * (d + 4) * 4)
+    print(f"case attention_decode_slices H={heads} Hkv={kv_heads} D={d} p={p} slices={slices}", flush=True)
+    hip.check(lib.vm_hip_attention_decode_slices_f32(dqkv.ptr, slices, dss.ptr, ss.size, float(hidden), 1e-5, dc.ptr,
+                                                     dsn.ptr, dpos.ptr, dk.ptr, dv.ptr, dpart.ptr, heads, kv_heads, d,
+                                                     max_seq, 1.0, None))
+    tot = qkv[0].copy()
+    for i in range(1, slices):
+        tot = (tot + qkv[i]).astype(np.float32)
+    tot = (tot * inv).astype(np.float32)
+    c, s_ = cos[p:p + 1], sin[p:p + 1]
+    qr = L.rope(tot[:hidden].reshape(heads, 1, d), c, s_)
+    kr = L.rope(tot[hidden:hidden + kv_heads * d].reshape(kv_heads, 1, d), c, s_)[:, 0]
+    vr = tot[hidden + kv_heads * d:].reshape(kv_heads, d)
+    kc, vc = kc0.copy(), vc0.copy()
+    kc[:, p], vc[:, p] = kr, vr
+    _close(dk.download(np.float32, kc.shape), kc, 1e-5, "k cache")
+    _close(dv.download(np.float32, vc.shape), vc, 1e-5, "v cache")
+    ctx = L.attention(qr, kc[:, :p + 1], vc[:, :p + 1], 1.0, causal=False)[:, 0].reshape(1, hidden)
+    # the output projection merges the partials while staging
+    qo, so = _pack(hidden, 256, O.QUANT_INT4, 32, 8)
+    src = _src(hip, kind=hip.GEMV_SRC_ATTN, act=dpart.addr, pos=dpos.addr, head_dim=d, chunk=ch.value,
+               chunks=chs.value, max_seq=max_seq)
+    out, _ = _run_src(hip, src, qo, so, hidden, 256, O.QUANT_INT4, 32)
+    _close(out.sum(axis=0, dtype=np.float64), O.qmm(ctx, qo, so, hidden, O.QUANT_INT4, 32)[0], 1e-4, "o projection")
+
+
+def test_swiglu_source_applies_the_norm_scale_and_scaled_slice_sum(hip):
+    import ctypes
+    k, n, sl_in = 512, 256, 4
+    q, s = _pack(k, n, O.QUANT_INT4, 32, 31)
+    gu = _normal((sl_in, 2 * k), 8)
+    ss = np.array([100.0, 50.0, 25.0], np.float32)
+    iv = np.float32(1.0 / np.sqrt(ss.sum(dtype=np.float32) / np.float32(700.0) + np.float32(1e-5)))
+    g, u = gu[0, :k].copy(), gu[0, k:].copy()
+    for i in range(1, sl_in):
+        g, u = (g + gu[i, :k]).astype(np.float32), (u + gu[i, k:]).astype(np.float32)
+    x = L.silu_mul((g * iv).astype(np.float32), (u * iv).astype(np.float32))
+    dgu, dss = _dev(hip, gu), _dev(hip, ss)
+    src = _src(hip, kind=hip.GEMV_SRC_SWIGLU, slices=sl_in, act=dgu.addr, ss_in=dss.addr, ss_count=3, ss_dim=700.0,
+               eps=1e-5)
+    out, sl = _run_src(hip, src, q, s, k, n, O.QUANT_INT4, 32)
+    _close(out.sum(axis=0, dtype=np.float64), O.qmm(x[None], q, s, k, O.QUANT_INT4, 32)[0], TOL, "swiglu")
+    # slices_sum_scaled: the projection's slices times the same scale
+    do = hip.DeviceBuffer(n * 4)
+    dsl = _dev(hip, out)
+    hip.check(hip.open_library().vm_hip_slices_sum_scaled_f32(dsl.ptr, sl, n, dss.ptr, 3, 700.0, 1e-5, do.ptr, None))
+    tot = out[0].copy()
+    for i in range(1, sl):
+        tot = (tot + out[i]).astype(np.float32)
+    _close(do.download(np.float32, (n,)), tot * iv, 1e-6, "scaled sum")

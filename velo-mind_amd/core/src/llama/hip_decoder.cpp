@@ -61,6 +61,10 @@ struct Packed {
 }  // namespace
 
 struct HipLlamaDecoder::Impl {
+    // Slice limits per projection: what each consumer reads with few
+    // memory round trips (the residual norm and the SwiGLU staging add the
+    // slices of a whole row; argmax scans the vocabulary once per slice).
+    static constexpr int kMaxQkv = 16, kMaxO = 16, kMaxGu = 16, kMaxDown = 22, kMaxLm = 4;
     Config cfg;
     int qt = VM_HIP_QUANT_INT4;
     int block = 32;
@@ -82,6 +86,13 @@ struct HipLlamaDecoder::Impl {
     DevBuf h, hn, qkv_out, q, ctx, attn_out, gu, act, down_out, logits;
     DevBuf idx, token, pos, tokens;
     std::size_t seq = 0;  // positions filled in the cache
+    // One-token steps: projections leave split-K partial slices that their
+    // consumers add (vm_hip_qmm_gemv_slices_f32); counts per projection.
+    bool sliced = false;
+    int s_qkv = 0, s_o = 0, s_gu = 0, s_down = 0, s_lm = 0;
+    DevBuf qkv_sl, o_sl, gu_sl, down_sl, lm_sl;
+    DevBuf h2, ss_attn, ss_ffn, ss_final, att_part;   // second residual buffer, norm partials, attention records
+    int att_chunk = 0, att_chunks = 0;
 
     float* kc(std::size_t l) const { return kcache.as<float>() + l * Hk * max_seq * D; }
     float* vc(std::size_t l) const { return vcache.as<float>() + l * Hk * max_seq * D; }
@@ -119,6 +130,101 @@ struct HipLlamaDecoder::Impl {
         }
         pack(dst, tmp.as<float>(), k, n);
         check(vm_hip_stream_synchronize(stream), "pack");  // tmp is freed on return
+    }
+
+    int block_arg() const { return qt == VM_HIP_QUANT_INT4 ? block : 0; }
+
+    // Slice count of the split-K GEMV for `w`, or 0 when the shape or block
+    // size needs the final-output kernel.
+    int slices_for(const Packed& w, int max_slices) const {
+        int sl = 0;
+        if (vm_hip_gemv_slices_count(w.k, w.n, qt, block_arg(), max_slices, &sl) != VM_HIP_OK) return 0;
+        return sl;
+    }
+
+    void gemv_slices(const float* act, int kind, int act_slices, const Packed& w, float* out, int max_slices) {
+        check(vm_hip_qmm_gemv_slices_f32(act, kind, act_slices, static_cast<const std::int8_t*>(w.codes.p),
+                                         w.scales.as<float>(), out, w.k, w.n, qt, block_arg(), max_slices, stream),
+              "quantized matmul (slices)");
+    }
+
+    void gemv_src(const vm_hip_gemv_src& src, const Packed& w, float* out, int max_slices) {
+        check(vm_hip_qmm_gemv_slices_src_f32(&src, static_cast<const std::int8_t*>(w.codes.p), w.scales.as<float>(), out,
+                                             w.k, w.n, qt, block_arg(), max_slices, stream),
+              "quantized matmul (slices)");
+    }
+
+    // Residual + RMSNorm staged in front of a projection: x = (h + sum of
+    // delta slices) * w; the projection's consumer applies 1/rms from ss.
+    static vm_hip_gemv_src normres(const float* h_in, const float* delta, int delta_slices, const void* norm_w,
+                                   float* h_out, float* ss_out) {
+        vm_hip_gemv_src src{};
+        src.kind = VM_HIP_GEMV_SRC_NORMRES;
+        src.act = h_in;
+        src.delta = delta_slices > 0 ? delta : nullptr;
+        src.slices = delta_slices;
+        src.norm_w = static_cast<const float*>(norm_w);
+        src.h_out = h_out;
+        src.ss_out = ss_out;
+        return src;
+    }
+
+    // One token at *pos, five launches per layer:
+    //   QKV (residual + RMSNorm staged)  ->  attention (slice sums, 1/rms,
+    //   RoPE, in-place K/V append, chunk partials)  ->  O (partials merged
+    //   while staging)  ->  gate|up (residual + RMSNorm staged)  ->  down
+    //   (SwiGLU with 1/rms staged from the gate|up slices)
+    // then the final norm staged in front of lm_head, whose slices stay in
+    // lm_sl (greedy argmax does not need the positive 1/rms scale).  The
+    // residual stream alternates between h (embedding, after each layer)
+    // and h2 (after attention).
+    void forward_one_sliced() {
+        const float eps = cfg.rms_norm_eps;
+        float* ha = h.as<float>();
+        float* hb = h2.as<float>();
+        const auto* posp = pos.as<std::int32_t>();
+        const float dim = static_cast<float>(hidden);
+        check(vm_hip_embedding_f32(static_cast<const float*>(embed->data), vocab, hidden, token.as<std::int32_t>(), 1,
+                                   ha, stream),
+              "embedding");
+        vm_hip_gemv_src attn_src{};
+        attn_src.kind = VM_HIP_GEMV_SRC_ATTN;
+        attn_src.act = att_part.as<float>();
+        attn_src.pos = posp;
+        attn_src.head_dim = static_cast<int>(D);
+        attn_src.chunk = att_chunk;
+        attn_src.chunks = att_chunks;
+        attn_src.max_seq = static_cast<int>(max_seq);
+        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+            gemv_src(normres(ha, down_sl.as<float>(), l == 0 ? 0 : s_down, attn_norm[l]->data, hb, ss_attn.as<float>()),
+                     qkv[l], qkv_sl.as<float>(), kMaxQkv);
+            check(vm_hip_attention_decode_slices_f32(qkv_sl.as<float>(), s_qkv, ss_attn.as<float>(), s_qkv, dim, eps,
+                                                     cos_t.as<float>(), sin_t.as<float>(), posp, kc(l), vc(l),
+                                                     att_part.as<float>(), H, Hk, D,
+                                                     static_cast<std::int64_t>(max_seq), 1.0f, stream),
+                  "attention_decode");
+            gemv_src(attn_src, o[l], o_sl.as<float>(), kMaxO);
+            gemv_src(normres(hb, o_sl.as<float>(), s_o, ffn_norm[l]->data, ha, ss_ffn.as<float>()), gate_up[l],
+                     gu_sl.as<float>(), kMaxGu);
+            vm_hip_gemv_src sw{};
+            sw.kind = VM_HIP_GEMV_SRC_SWIGLU;
+            sw.act = gu_sl.as<float>();
+            sw.slices = s_gu;
+            sw.ss_in = ss_ffn.as<float>();
+            sw.ss_count = s_gu;
+            sw.ss_dim = dim;
+            sw.eps = eps;
+            gemv_src(sw, down[l], down_sl.as<float>(), kMaxDown);
+        }
+        gemv_src(normres(ha, down_sl.as<float>(), s_down, final_norm->data, nullptr, ss_final.as<float>()), lm_head,
+                 lm_sl.as<float>(), kMaxLm);
+    }
+
+    // Logits of the last sliced step (the final norm's 1/rms applied).
+    void sliced_logits() {
+        check(vm_hip_slices_sum_scaled_f32(lm_sl.as<float>(), s_lm, vocab, ss_final.as<float>(), s_lm,
+                                           static_cast<float>(hidden), cfg.rms_norm_eps, logits.as<float>(), stream),
+              "logits");
     }
 
     void qmm(const float* a, const Packed& w, float* c, std::int64_t rows) {
@@ -246,6 +352,27 @@ HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_
     m.token = DevBuf(4);
     m.pos = DevBuf(4);
     m.tokens = DevBuf(rows * 4);
+    m.s_qkv = m.slices_for(m.qkv[0], Impl::kMaxQkv);
+    m.s_o = m.slices_for(m.o[0], Impl::kMaxO);
+    m.s_gu = m.slices_for(m.gate_up[0], Impl::kMaxGu);
+    m.s_down = m.slices_for(m.down[0], Impl::kMaxDown);
+    m.s_lm = m.slices_for(m.lm_head, Impl::kMaxLm);
+    m.sliced = m.s_qkv && m.s_o && m.s_gu && m.s_down && m.s_lm && m.hidden % 4 == 0 && m.inter % 4 == 0 &&
+               m.H * m.D == m.hidden &&
+               vm_hip_attention_decode_chunks(m.D, static_cast<std::int64_t>(max_seq), &m.att_chunk, &m.att_chunks) ==
+                   VM_HIP_OK;
+    if (m.sliced) {
+        m.h2 = DevBuf(static_cast<std::size_t>(m.hidden * 4));
+        m.ss_attn = DevBuf(static_cast<std::size_t>(m.s_qkv * 4));
+        m.ss_ffn = DevBuf(static_cast<std::size_t>(m.s_gu * 4));
+        m.ss_final = DevBuf(static_cast<std::size_t>(m.s_lm * 4));
+        m.att_part = DevBuf(static_cast<std::size_t>(m.H * m.att_chunks * (m.D + 4) * 4));
+        m.qkv_sl = DevBuf(static_cast<std::size_t>(m.s_qkv * m.qkv_n * 4));
+        m.o_sl = DevBuf(static_cast<std::size_t>(m.s_o * m.hidden * 4));
+        m.gu_sl = DevBuf(static_cast<std::size_t>(m.s_gu * 2 * m.inter * 4));
+        m.down_sl = DevBuf(static_cast<std::size_t>(m.s_down * m.hidden * 4));
+        m.lm_sl = DevBuf(static_cast<std::size_t>(m.s_lm * m.vocab * 4));
+    }
     check(vm_hip_stream_synchronize(m.stream), "setup");
 }
 
@@ -288,7 +415,12 @@ auto HipLlamaDecoder::forward_step(std::int32_t token, std::size_t pos) -> std::
     if (pos > m.seq || pos >= _max_seq) throw std::invalid_argument("HipLlamaDecoder::forward_step: bad position");
     check(vm_hip_memcpy_h2d(m.token.p, &token, 4, m.stream), "token upload");
     m.set_pos(static_cast<std::int64_t>(pos));
-    m.forward(1);
+    if (m.sliced) {
+        m.forward_one_sliced();
+        m.sliced_logits();
+    } else {
+        m.forward(1);
+    }
     m.seq = pos + 1;
     return logits();
 }
@@ -318,8 +450,14 @@ auto HipLlamaDecoder::generate(std::span<const std::int32_t> prompt, std::size_t
     _prefill_s = ms_prefill * 1e-3;
 
     auto step = [&] {
-        m.forward(1);
-        check(vm_hip_argmax_f32(m.logits.as<float>(), m.vocab, tok, posp, seqp, ms, m.stream), "argmax");
+        if (m.sliced) {
+            m.forward_one_sliced();
+            check(vm_hip_argmax_slices_f32(m.lm_sl.as<float>(), m.s_lm, m.vocab, tok, posp, seqp, ms, m.stream),
+                  "argmax");
+        } else {
+            m.forward(1);
+            check(vm_hip_argmax_f32(m.logits.as<float>(), m.vocab, tok, posp, seqp, ms, m.stream), "argmax");
+        }
     };
     std::size_t done = 0;
     _decode_steps_timed = 0;

@@ -241,9 +241,18 @@ __global__ __launch_bounds__(kNormT) void add_rmsnorm_slices_kernel(float* __res
 }
 
 // ---- out[j] = sum over s of in[s * n + j], slices in order.
-__global__ void slices_sum_kernel(const float* __restrict__ in, int slices, int64_t n, float* __restrict__ out) {
+// With per-split sums of squares `ss` the sum is multiplied by the RMSNorm
+// scale 1 / sqrt(sum(ss) / ss_dim + eps) (see VM_HIP_GEMV_SRC_NORMRES).
+__global__ void slices_sum_kernel(const float* __restrict__ in, int slices, int64_t n, float* __restrict__ out,
+                                  const float* __restrict__ ss, int ss_count, float ss_dim, float eps) {
+    float iv = 1.0f;
+    if (ss && ss_count > 0) {
+        float t = 0.0f;
+        for (int i = 0; i < ss_count; ++i) t += ss[i];
+        iv = 1.0f / sqrtf(t / ss_dim + eps);
+    }
     for (int64_t j = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; j < n; j += static_cast<int64_t>(gridDim.x) * kT)
-        out[j] = slice_sum(in + j, slices, n);
+        out[j] = slice_sum(in + j, slices, n) * iv;
 }
 
 // ---- RoPE on the fused QKV projection and in-place KV append.
@@ -494,6 +503,252 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
             make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
     }
     if (tid == 0) __hip_atomic_store(&counters[hk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- Decode attention fused with its producer's reduction and RoPE: one
+// query row per head at position p = *pos, keys 0..p, the projection
+// arriving as split-K partial slices [qkv_slices][(H + 2 Hkv) D] whose
+// RMSNorm scale 1/rms comes from per-split sums of squares `ss` (see
+// VM_HIP_GEMV_SRC_NORMRES; none: scale 1).  Grid (chunks, Hkv) as
+// attention_decode_kernel.  Each workgroup
+//   1. issues its K/V chunk loads from the cache and, as float4 tasks,
+//      the slice sums of its G query heads (and, in the last chunk, of the
+//      new key and value), scaled by 1/rms;
+//   2. rotates q (and the new key) with the RoPE tables at p
+//      (rotary_embedding.cpp:16-45); the last chunk writes the new key and
+//      value into the caches at row p and into its own LDS tiles (no other
+//      workgroup reads row p);
+//   3. scores, softmax partial and p . V as attention_decode_kernel, and
+//      stores the chunk's record {m, l, 0, 0, o[D]} with plain stores at
+//      part[((hk * G + g) * chunks + chunk) * (D + 4)].
+// The merge over chunks is left to the consumer (VM_HIP_GEMV_SRC_ATTN).
+template <int D, int CHUNK>
+__global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
+    const float* __restrict__ qkv, int qkv_slices, const float* __restrict__ ss, int ss_count, float ss_dim,
+    float eps, const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int32_t* __restrict__ pos,
+    float* __restrict__ k_cache, float* __restrict__ v_cache, float* __restrict__ part, int heads, int kv_heads,
+    int max_seq, float scale) {
+    constexpr int kMaxG = 16;
+    constexpr int D4 = D / 4;
+    constexpr int HALF = D / 2;
+    constexpr int kKS = D + 4;
+    constexpr int kPart = D + 4;
+    constexpr int KV = CHUNK * D4 / kT;
+    constexpr int GS = kT / CHUNK;
+    constexpr int GI = kMaxG / GS;
+    constexpr int PS = kT / D4;
+    constexpr int kB = 16;   // slices per batch of loads
+    static_assert(CHUNK * D4 % kT == 0 && 64 % CHUNK == 0 && kT % D4 == 0 && kT % HALF == 0, "tile shape");
+    __shared__ __align__(16) float sq[kMaxG * D];
+    __shared__ __align__(16) float sk[CHUNK * kKS];
+    __shared__ __align__(16) float sv[CHUNK * D];
+    __shared__ __align__(16) float knew[D];
+    __shared__ __align__(16) float vnew[D];
+    __shared__ float sp[kMaxG][CHUNK];
+    __shared__ float sm[kMaxG], sl[kMaxG];
+
+    const int chunk = blockIdx.x;
+    const int hk = blockIdx.y;
+    const int G = heads / kv_heads;
+    const int tid = threadIdx.x;
+    const int n_keys = min(pos[0] + 1, max_seq);
+    const int nc = (n_keys + CHUNK - 1) / CHUNK;
+    if (chunk >= nc) return;
+    const int p = n_keys - 1;
+    const int k0 = chunk * CHUNK;
+    const int nk = min(CHUNK, n_keys - k0);
+    const bool last = chunk == nc - 1;
+    const int width = (heads + 2 * kv_heads) * D;
+
+    // 1. Loads, the small ones first (vector memory counters retire in
+    //    issue order): the RoPE tables at p for this thread's pair index,
+    //    the slice sums (tasks [0, G*D4) query float4s, then in the last
+    //    chunk D4 key and D4 value float4s), then the K/V chunk from the
+    //    cache (row p of the last chunk is replaced below).
+    const int jr_pair = tid % HALF;   // pair index of every RoPE task of this thread (kT % HALF == 0)
+    const float rc = cos_t[static_cast<int64_t>(p) * HALF + jr_pair];
+    const float rs = sin_t[static_cast<int64_t>(p) * HALF + jr_pair];
+    const int tasks1 = G * D4 + (last ? 2 * D4 : 0);
+    constexpr int kTasksMax = (kMaxG * D4 + 2 * D4 + kT - 1) / kT;
+    const __amdgpu_buffer_rsrc_t qrs = buffer_rsrc(qkv, static_cast<uint32_t>(qkv_slices * width) * 4u);
+    auto task_col = [&](int t, float*& dst) {
+        if (t < G * D4) {
+            dst = sq + 4 * t;
+            return (hk * G) * D + 4 * t;
+        }
+        if (t < G * D4 + D4) {
+            dst = knew + 4 * (t - G * D4);
+            return (heads + hk) * D + 4 * (t - G * D4);
+        }
+        dst = vnew + 4 * (t - G * D4 - D4);
+        return (heads + kv_heads + hk) * D + 4 * (t - G * D4 - D4);
+    };
+    u32x4 l0[kTasksMax][kB];
+#pragma unroll
+    for (int i = 0; i < kTasksMax; ++i) {
+        const int t = tid + i * kT;
+        float* dst = nullptr;
+        const int col = t < tasks1 ? task_col(t, dst) : 0;
+#pragma unroll
+        for (int e = 0; e < kB; ++e)
+            l0[i][e] = buffer_load16(qrs, (t < tasks1 && e < qkv_slices)
+                                              ? static_cast<uint32_t>(e * width + col) * 4u : 0xfffffff0u);
+    }
+    const uint32_t kv_bytes = static_cast<uint32_t>(nk * D) * 4u;
+    const int64_t kv_off = (static_cast<int64_t>(hk) * max_seq + k0) * D;
+    u32x4 tk[KV], tv[KV];
+    {
+        const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(k_cache + kv_off, kv_bytes);
+        const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(v_cache + kv_off, kv_bytes);
+#pragma unroll
+        for (int u = 0; u < KV; ++u) {
+            tk[u] = buffer_load16(krs, (tid + u * kT) * 16u);
+            tv[u] = buffer_load16(vrs, (tid + u * kT) * 16u);
+        }
+    }
+    {
+        float iv = 1.0f;
+        if (ss && ss_count > 0) {
+            float t = 0.0f;
+            for (int i = 0; i < ss_count; ++i) t += ss[i];
+            iv = 1.0f / sqrtf(t / ss_dim + eps);
+        }
+#pragma unroll
+        for (int i = 0; i < kTasksMax; ++i) {
+            const int t = tid + i * kT;
+            if (t >= tasks1) continue;
+            float* dst = nullptr;
+            const int col = task_col(t, dst);
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int e = 0; e < kB; ++e)
+                if (e < qkv_slices) {   // slices in order
+                    a.x += __uint_as_float(l0[i][e][0]);
+                    a.y += __uint_as_float(l0[i][e][1]);
+                    a.z += __uint_as_float(l0[i][e][2]);
+                    a.w += __uint_as_float(l0[i][e][3]);
+                }
+            for (int s0 = kB; s0 < qkv_slices; s0 += kB) {   // more than kB slices
+                u32x4 l[kB];
+#pragma unroll
+                for (int e = 0; e < kB; ++e)
+                    l[e] = buffer_load16(qrs, s0 + e < qkv_slices ? static_cast<uint32_t>((s0 + e) * width + col) * 4u
+                                                                 : 0xfffffff0u);
+#pragma unroll
+                for (int e = 0; e < kB; ++e)
+                    if (s0 + e < qkv_slices) {
+                        a.x += __uint_as_float(l[e][0]);
+                        a.y += __uint_as_float(l[e][1]);
+                        a.z += __uint_as_float(l[e][2]);
+                        a.w += __uint_as_float(l[e][3]);
+                    }
+            }
+            *reinterpret_cast<float4*>(dst) = make_float4(a.x * iv, a.y * iv, a.z * iv, a.w * iv);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < KV; ++u) {
+        const int e = tid + u * kT;
+        const int j = e / D4, c = e - j * D4;
+        *reinterpret_cast<u32x4*>(sk + j * kKS + 4 * c) = tk[u];
+        *reinterpret_cast<u32x4*>(sv + 4 * e) = tv[u];
+    }
+    __syncthreads();
+
+    // 2. RoPE at p: query pairs, then (last chunk) the key pairs and value copy.
+    {
+        const int tasks = G * HALF + (last ? HALF + D : 0);
+        const int jr = p - k0;   // the new key's row in this chunk (last chunk)
+        for (int t = tid; t < tasks; t += kT) {
+            if (t < G * HALF + HALF) {
+                const bool is_q = t < G * HALF;
+                const int g = is_q ? t / HALF : 0;
+                const int j = is_q ? t - g * HALF : t - G * HALF;
+                float* x = is_q ? sq + g * D : knew;
+                const float c = rc, sn = rs;   // j == tid % HALF for every task of this thread
+                const float a = x[j], b = x[j + HALF];
+                const float y0 = a * c - b * sn;
+                const float y1 = b * c + a * sn;
+                if (is_q) {
+                    x[j] = y0;
+                    x[j + HALF] = y1;
+                } else {
+                    sk[jr * kKS + j] = y0;
+                    sk[jr * kKS + j + HALF] = y1;
+                    float* kc = k_cache + (static_cast<int64_t>(hk) * max_seq + p) * D;
+                    kc[j] = y0;
+                    kc[j + HALF] = y1;
+                }
+            } else {
+                const int d = t - G * HALF - HALF;
+                const float v = vnew[d];
+                sv[jr * D + d] = v;
+                v_cache[(static_cast<int64_t>(hk) * max_seq + p) * D + d] = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. Scores and softmax partials: thread (j = tid % CHUNK, slot = tid / CHUNK).
+    {
+        const int j = tid % CHUNK, slot = tid / CHUNK;
+        float sc[GI];
+#pragma unroll
+        for (int i = 0; i < GI; ++i) sc[i] = 0.0f;
+#pragma unroll 4
+        for (int c = 0; c < D4; ++c) {
+            const float4 kv = *reinterpret_cast<const float4*>(sk + j * kKS + 4 * c);
+#pragma unroll
+            for (int i = 0; i < GI; ++i) {
+                const int g = slot + i * GS;
+                if (g < G) {
+                    const float4 qv = *reinterpret_cast<const float4*>(sq + g * D + 4 * c);
+                    sc[i] = fmaf(qv.x, kv.x, sc[i]);
+                    sc[i] = fmaf(qv.y, kv.y, sc[i]);
+                    sc[i] = fmaf(qv.z, kv.z, sc[i]);
+                    sc[i] = fmaf(qv.w, kv.w, sc[i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < GI; ++i) {
+            const int g = slot + i * GS;
+            if (g < G) {
+                const float sv_ = j < nk ? sc[i] * scale : -INFINITY;
+                float mx = sv_;
+#pragma unroll
+                for (int off = CHUNK / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+                const float pr = j < nk ? expf(sv_ - mx) : 0.0f;
+                float sum = pr;
+#pragma unroll
+                for (int off = CHUNK / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+                sp[g][j] = pr;
+                if (j == 0) {
+                    sm[g] = mx;
+                    sl[g] = sum;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // p . V: thread (c4 = tid % D4, slot = tid / D4); the chunk's record.
+    const int c4 = tid % D4, pslot = tid / D4;
+    for (int g = pslot; g < G; g += PS) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+        for (int jj = 0; jj < nk; ++jj) {
+            const float pr = sp[g][jj];
+            const float4 v = *reinterpret_cast<const float4*>(sv + jj * D + 4 * c4);
+            acc.x = fmaf(pr, v.x, acc.x);
+            acc.y = fmaf(pr, v.y, acc.y);
+            acc.z = fmaf(pr, v.z, acc.z);
+            acc.w = fmaf(pr, v.w, acc.w);
+        }
+        float* rec = part + ((static_cast<int64_t>(hk) * G + g) * gridDim.x + chunk) * kPart;
+        *reinterpret_cast<float4*>(rec + 4 + 4 * c4) = acc;
+        if (c4 == 0) *reinterpret_cast<float4*>(rec) = make_float4(sm[g], sl[g], 0.0f, 0.0f);
+    }
 }
 
 // ---- Prefill attention over the resident cache: q [H, S, D] rows at
@@ -928,7 +1183,68 @@ int vm_hip_slices_sum_f32(const float* in, int64_t slices, int64_t n, float* out
     if (n == 0) return 0;
     if (!in || !out) return fail_inval("slices_sum: null pointer");
     hipLaunchKernelGGL(slices_sum_kernel, dim3(grid_for(n)), dim3(kT), 0, S(stream), in, static_cast<int>(slices), n,
-                       out);
+                       out, static_cast<const float*>(nullptr), 0, 1.0f, 0.0f);
+    return check_launch("slices_sum", S(stream));
+}
+
+int vm_hip_attention_decode_chunks(int64_t head_dim, int64_t max_seq, int* chunk, int* chunks) {
+    clear_error();
+    if (!chunk || !chunks) return fail_inval("attention_decode_chunks: null pointer");
+    if (head_dim != 64 && head_dim != 128) {
+        set_error("attention_decode: head_dim must be 64 or 128");
+        return VM_HIP_EUNSUPPORTED;
+    }
+    if (max_seq < 1 || max_seq > (1 << 24)) return fail_inval("attention_decode_chunks: bad max_seq");
+    // 32 keys per workgroup: twice the workgroups of 64-key chunks for the
+    // same cache, which shortens each workgroup's serial score / p.V phases
+    // (measured faster at TinyLlama decode lengths).
+    *chunk = 32;
+    *chunks = static_cast<int>((max_seq + *chunk - 1) / *chunk);
+    return 0;
+}
+
+int vm_hip_attention_decode_slices_f32(const float* qkv, int64_t qkv_slices, const float* ss, int64_t ss_count,
+                                       float ss_dim, float eps, const float* cos_table, const float* sin_table,
+                                       const int32_t* pos, float* k_cache, float* v_cache, float* partials,
+                                       int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t max_seq,
+                                       float scale, void* stream) {
+    clear_error();
+    int chunk = 0, chunks = 0;
+    VM_TRY(vm_hip_attention_decode_chunks(head_dim, max_seq, &chunk, &chunks));
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads) return fail_inval("attention_decode_slices: bad shape");
+    if (heads / kv_heads > 16) return fail_inval("attention_decode_slices: more than 16 query heads per KV head");
+    if (qkv_slices < 1 || qkv_slices > 4096) return fail_inval("attention_decode_slices: qkv_slices must be in [1, 4096]");
+    if (ss_count < 0 || (ss_count > 0 && (!ss || ss_dim <= 0.0f)))
+        return fail_inval("attention_decode_slices: ss needs ss_count >= 1 and ss_dim > 0");
+    if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !partials)
+        return fail_inval("attention_decode_slices: null pointer");
+    if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(partials))
+        return fail_inval("attention_decode_slices: operands must be 16-byte aligned");
+    if (max_seq * head_dim > (int64_t{1} << 28) || qkv_slices * (heads + 2 * kv_heads) * head_dim * 4 > 0x7fffffffLL ||
+        heads > 65535 || kv_heads > 65535)
+        return fail_inval("attention_decode_slices: too large");
+    const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+    const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(kv_heads));
+    const int sl = static_cast<int>(qkv_slices), sc_n = static_cast<int>(ss_count);
+    if (head_dim == 64)
+        hipLaunchKernelGGL((attention_decode_slices_kernel<64, 32>), grid, dim3(kT), 0, S(stream), qkv, sl, ss, sc_n,
+                           ss_dim, eps, cos_table, sin_table, pos, k_cache, v_cache, partials,
+                           static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(max_seq), sc);
+    else
+        hipLaunchKernelGGL((attention_decode_slices_kernel<128, 32>), grid, dim3(kT), 0, S(stream), qkv, sl, ss, sc_n,
+                           ss_dim, eps, cos_table, sin_table, pos, k_cache, v_cache, partials,
+                           static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(max_seq), sc);
+    return check_launch("attention_decode_slices", S(stream));
+}
+
+int vm_hip_slices_sum_scaled_f32(const float* in, int64_t slices, int64_t n, const float* ss, int64_t ss_count,
+                                 float ss_dim, float eps, float* out, void* stream) {
+    clear_error();
+    if (n < 0 || slices < 1 || slices > 4096 || ss_count < 0) return fail_inval("slices_sum: bad size");
+    if (n == 0) return 0;
+    if (!in || !out || (ss_count > 0 && (!ss || ss_dim <= 0.0f))) return fail_inval("slices_sum: null pointer");
+    hipLaunchKernelGGL(slices_sum_kernel, dim3(grid_for(n)), dim3(kT), 0, S(stream), in, static_cast<int>(slices), n,
+                       out, ss, static_cast<int>(ss_count), ss_dim, eps);
     return check_launch("slices_sum", S(stream));
 }
 

@@ -22,17 +22,32 @@
 // workgroup add through LDS.
 //
 // Activation sources (the consumer side of the previous kernel):
-//   PLAIN   x[k]: each lane loads its own 2R (INT4) or R (INT8) values
-//   SLICES  x = sum of `in_slices` slices [in_slices][k], staged in LDS
-//   SWIGLU  x[j] = silu(g[j]) * u[j] with g, u the sums of `in_slices`
-//           slices of a fused gate|up projection [in_slices][2k], staged
-//           in LDS (the Sigmoid, Mul, Mul of llama_graph.cpp:22-28)
+//   PLAIN    x[k]: each lane loads its own 2R (INT4) or R (INT8) values
+//   SLICES   x = sum of `slices` slices [slices][k], staged in LDS
+//   SWIGLU   x[j] = silu(g[j]) * u[j] with g, u the sums of `slices`
+//            slices of a fused gate|up projection [slices][2k], staged in
+//            LDS (the Sigmoid, Mul, Mul of llama_graph.cpp:22-28); with
+//            per-split sums of squares `ss_in` from the producer, g and u
+//            are first multiplied by that row's 1/rms (see NORMRES)
+//   NORMRES  the residual Add and RMSNorm in front of a projection
+//            (llama_graph.cpp:118-136): h = act + sum of `slices` delta
+//            slices, x = h * w.  RMSNorm's 1/rms is a scalar, so it is
+//            left to the consumer of this GEMV's output (the projection is
+//            linear): each split writes the sum of squares of h over its K
+//            range to ss_out[split], and workgroups of tile 0 write h to
+//            h_out.  Every workgroup stages only its own K range.
+//   ATTN     the output of decode attention, merged while staging: the
+//            per-chunk softmax partials (m, l, o[head_dim]) of the
+//            attention kernel are combined in chunk order (online softmax
+//            rescaling) for the workgroup's heads
 //
 // Dequantization matches the final-output GEMV: INT4 nibbles moved to the
 // top of a byte give 16 * code (factor 1/16 folded into the scale), INT8
 // codes are sign-extended bytes; fp32 FMA accumulation throughout.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdint>
 
 #include "vm_device.h"
@@ -45,6 +60,8 @@ constexpr int kTileCols = 256;
 constexpr int kGemvSrcPlain = VM_HIP_GEMV_SRC_PLAIN;
 constexpr int kGemvSrcSlices = VM_HIP_GEMV_SRC_SLICES;
 constexpr int kGemvSrcSwiglu = VM_HIP_GEMV_SRC_SWIGLU;
+constexpr int kGemvSrcNormRes = VM_HIP_GEMV_SRC_NORMRES;
+constexpr int kGemvSrcAttn = VM_HIP_GEMV_SRC_ATTN;
 
 __device__ __forceinline__ float swap_rows_add(float a, float b) {
     auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
@@ -66,10 +83,19 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 // KIND: 0 = INT8 per-column scale, 1 = INT8 blockwise, 2 = INT4 blockwise.
+__device__ __forceinline__ float inv_rms(const float* __restrict__ ss, int count, float dim, float eps) {
+    if (!ss || count <= 0) return 1.0f;
+    float t = 0.0f;
+    for (int i = 0; i < count; ++i) t += ss[i];
+    return 1.0f / sqrtf(t / dim + eps);
+}
+
 template <int KIND, int R, int W, int SRC>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
-    const float* __restrict__ act, int in_slices, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
+    vm_hip_gemv_src src, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
     float* __restrict__ out, int k, int n, int block_size, uint32_t code_bytes, uint32_t scale_bytes) {
+    const float* __restrict__ act = src.act;
+    const int in_slices = src.slices;
     constexpr bool kInt4 = KIND == 2;
     constexpr int kRowsWave = 4 * R;                  // byte rows per wave
     constexpr int kRowsWg = W * kRowsWave;            // byte rows per workgroup
@@ -79,6 +105,9 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
     static_assert(kXLane % 4 == 0, "a lane's activations are whole float4s");
     __shared__ __align__(16) float red[W][kTileCols];
     __shared__ __align__(16) float xs[SRC == kGemvSrcPlain ? 4 : kXWg];
+    __shared__ __align__(16) float stage_g[SRC == kGemvSrcPlain ? 4 : W * 64 * 4];
+    __shared__ __align__(16) float stage_u[(SRC == kGemvSrcSwiglu || SRC == kGemvSrcAttn) ? W * 64 * 4 : 4];
+    __shared__ float ssp[W * 2];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -97,35 +126,120 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
     const int row0 = wave_row0 + rl * R;
     const int byte_rows = kInt4 ? (k + 1) / 2 : k;
 
-    // Codes: rows past the matrix and columns past n read zeros.
-    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wq, code_bytes);
+    // Load order matters: vector memory counters retire in issue order, so
+    // the staged activations (L2/MALL hits) are requested before the
+    // weights (HBM) -- waiting for them then does not wait for the weight
+    // stream, and staging overlaps it.
+    //
+    // Staging the workgroup's K range in LDS (sources other than PLAIN), in
+    // two levels so that every thread has at most a few loads in flight:
+    //   1. thread t = part * NQ + q takes float4 group q (four consecutive K
+    //      values) and a contiguous range of the slices (attention chunks)
+    //      of part `part`, and leaves the partial sum (partial softmax
+    //      merge) in LDS;
+    //   2. thread q < NQ combines the parts in order and applies the
+    //      source's elementwise tail (residual, SwiGLU, norm weight).
+    // The grouping of the additions is fixed, so results do not depend on
+    // scheduling.
+    constexpr int T = W * 64;
+    constexpr int NQ = kXWg / 4;
+    constexpr int P = T / NQ;
+    static_assert(T % NQ == 0 && P >= 1, "staging parts");
+    constexpr int kPer = 4;   // loads of one kind in flight per thread (one batch covers 4P slices)
+    const int kw0 = wg_row0 * kKPerRow;
+    const int q = threadIdx.x % NQ;
+    const int part = threadIdx.x / NQ;
+    const int kk = kw0 + 4 * q;
+    const bool ok = kk < k;
+    constexpr bool kNorm = SRC == kGemvSrcNormRes;
+    constexpr bool kAttn = SRC == kGemvSrcAttn;
+    constexpr int kSrcMult = SRC == kGemvSrcSwiglu ? 2 : 1;
+    u32x4 tg[kPer], tu[kPer];
+    u32x4 hres = {0u, 0u, 0u, 0u}, nwv = {0u, 0u, 0u, 0u};
     u32x4 w[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = row0 + r;
-        const uint32_t off = (col_ok && row < byte_rows)
-                                 ? static_cast<uint32_t>(row) * static_cast<uint32_t>(n) + static_cast<uint32_t>(col0)
-                                 : code_bytes;
-        w[r] = buffer_load16(wrs, off);
-    }
-    // After the row-lane reduction this lane keeps columns col0 + keep .. +3.
-    const int keep = 8 * (rl & 1) + 4 * (rl >> 1);
     u32x4 sv;
-    {
-        const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
-        uint32_t soff = scale_bytes;
-        if (col_ok) {
-            if constexpr (KIND == 0) {
-                soff = static_cast<uint32_t>(col0 + keep) * 4u;
+    const int keep = 8 * (rl & 1) + 4 * (rl >> 1);   // columns kept after the row-lane reduction
+    auto issue_weights = [&]() {
+        // Codes: rows past the matrix and columns past n read zeros.
+        const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wq, code_bytes);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = row0 + r;
+            const uint32_t off = (col_ok && row < byte_rows)
+                                     ? static_cast<uint32_t>(row) * static_cast<uint32_t>(n) + static_cast<uint32_t>(col0)
+                                     : code_bytes;
+            w[r] = buffer_load16(wrs, off);
+        }
+        {
+            const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
+            uint32_t soff = scale_bytes;
+            if (col_ok) {
+                if constexpr (KIND == 0) {
+                    soff = static_cast<uint32_t>(col0 + keep) * 4u;
+                } else {
+                    // The wave's byte rows lie in one block (checked by the host).
+                    const int blk = (wave_row0 * kKPerRow) / block_size;
+                    if (wave_row0 < byte_rows)
+                        soff = (static_cast<uint32_t>(blk) * static_cast<uint32_t>(n) + static_cast<uint32_t>(col0 + keep)) * 4u;
+                }
+            }
+            sv = buffer_load16(srs, soff);
+        }
+
+    };
+    // The attention source's addresses depend on *pos (a scalar load): its
+    // weights go first so that they do not wait for that round trip.
+    if constexpr (SRC == kGemvSrcAttn) issue_weights();
+    int lo = 0, hi = 0;                       // this part's slice / chunk range
+    uint32_t slice_stride = 0, head_base = 0;
+    int d0 = 0, rec = 0;
+    __amdgpu_buffer_rsrc_t drs = buffer_rsrc(act, 0u);
+    if constexpr (SRC != kGemvSrcPlain) {
+        if constexpr (kAttn) {
+            const int D = src.head_dim;
+            const int head = kk / D;
+            d0 = kk - head * D;
+            const int n_keys = min(src.pos[0] + 1, src.max_seq);
+            const int nc = (n_keys + src.chunk - 1) / src.chunk;
+            const int per = (nc + P - 1) / P;
+            lo = part * per;
+            hi = min(nc, lo + per);
+            rec = D + 4;
+            head_base = static_cast<uint32_t>(head) * static_cast<uint32_t>(src.chunks * rec);
+            drs = buffer_rsrc(act, static_cast<uint32_t>(k / D) * static_cast<uint32_t>(src.chunks * rec) * 4u);
+        } else {
+            slice_stride = static_cast<uint32_t>(k) * kSrcMult;
+            drs = buffer_rsrc(kNorm ? src.delta : act, static_cast<uint32_t>(in_slices) * slice_stride * 4u);
+            const int per = (in_slices + P - 1) / P;
+            lo = part * per;
+            hi = min(in_slices, lo + per);
+        }
+        // first batch of loads
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) {
+            const bool v = ok && lo + e < hi;
+            if constexpr (kAttn) {
+                const uint32_t r0 = head_base + static_cast<uint32_t>((lo + e) * rec);
+                tg[e] = buffer_load16(drs, v ? (r0 + 4u + static_cast<uint32_t>(d0)) * 4u : 0xfffffff0u);
+                tu[e] = buffer_load16(drs, v ? r0 * 4u : 0xfffffff0u);
             } else {
-                // The wave's byte rows lie in one block (checked by the host).
-                const int blk = (wave_row0 * kKPerRow) / block_size;
-                if (wave_row0 < byte_rows)
-                    soff = (static_cast<uint32_t>(blk) * static_cast<uint32_t>(n) + static_cast<uint32_t>(col0 + keep)) * 4u;
+                const uint32_t base = static_cast<uint32_t>(lo + e) * slice_stride + static_cast<uint32_t>(kk);
+                tg[e] = buffer_load16(drs, v ? base * 4u : 0xfffffff0u);
+                if constexpr (SRC == kGemvSrcSwiglu)
+                    tu[e] = buffer_load16(drs, v ? (base + static_cast<uint32_t>(k)) * 4u : 0xfffffff0u);
             }
         }
-        sv = buffer_load16(srs, soff);
+        if constexpr (kNorm) {
+            if (part == 0) {
+                const __amdgpu_buffer_rsrc_t hrs = buffer_rsrc(act, static_cast<uint32_t>(k) * 4u);
+                const __amdgpu_buffer_rsrc_t nrs = buffer_rsrc(src.norm_w, static_cast<uint32_t>(k) * 4u);
+                hres = buffer_load16(hrs, ok ? static_cast<uint32_t>(kk) * 4u : 0xfffffff0u);
+                nwv = buffer_load16(nrs, ok ? static_cast<uint32_t>(kk) * 4u : 0xfffffff0u);
+            }
+        }
     }
+
+    if constexpr (SRC != kGemvSrcAttn) issue_weights();
 
     // Activations for the lane's K range [row0 * kKPerRow, + kXLane).
     u32x4 xv[kXLane / 4];
@@ -135,30 +249,26 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
 #pragma unroll
         for (int i = 0; i < kXLane / 4; ++i) xv[i] = buffer_load16(ars, static_cast<uint32_t>(kk0 + 4 * i) * 4u);
     } else {
-        // Stage the workgroup's K range: thread t sums the slices of float4
-        // group t (four consecutive K values), all loads issued at once.
-        const int kw0 = wg_row0 * kKPerRow;
-        constexpr int kSrcMult = SRC == kGemvSrcSwiglu ? 2 : 1;
-        const uint32_t slice_stride = static_cast<uint32_t>(k) * kSrcMult;   // floats per slice
-        const __amdgpu_buffer_rsrc_t ars =
-            buffer_rsrc(act, static_cast<uint32_t>(in_slices) * slice_stride * 4u);
-        for (int q = threadIdx.x; q < kXWg / 4; q += W * 64) {
-            const int kk = kw0 + 4 * q;
-            const bool ok = kk < k;
-            float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
-            for (int s0 = 0; s0 < in_slices; s0 += 8) {
-                u32x4 tg[8], tu[8];
+        float4* pg = reinterpret_cast<float4*>(stage_g);     // [P][NQ]
+        float4* pu = reinterpret_cast<float4*>(stage_u);     // [P][NQ] (SwiGLU up / attention M, L)
+        float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+        float M = -INFINITY, Lsum = 0.0f;
+        for (int c0 = lo;; c0 += kPer) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const bool v = ok && s0 + e < in_slices;
-                    const uint32_t base = static_cast<uint32_t>(s0 + e) * slice_stride + static_cast<uint32_t>(kk);
-                    tg[e] = buffer_load16(ars, v ? base * 4u : 0xfffffff0u);
-                    if constexpr (SRC == kGemvSrcSwiglu)
-                        tu[e] = buffer_load16(ars, v ? (base + static_cast<uint32_t>(k)) * 4u : 0xfffffff0u);
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    if (s0 + e < in_slices) {   // slices added in order
+            for (int e = 0; e < kPer; ++e) {
+                if (c0 + e < hi) {   // slices / chunks in order
+                    if constexpr (kAttn) {
+                        const float mc = __uint_as_float(tu[e][0]);
+                        const float Mn = fmaxf(M, mc);
+                        const float al = M > -INFINITY ? expf(M - Mn) : 0.0f;
+                        const float be = expf(mc - Mn);
+                        Lsum = fmaf(Lsum, al, __uint_as_float(tu[e][1]) * be);
+                        g.x = fmaf(g.x, al, __uint_as_float(tg[e][0]) * be);
+                        g.y = fmaf(g.y, al, __uint_as_float(tg[e][1]) * be);
+                        g.z = fmaf(g.z, al, __uint_as_float(tg[e][2]) * be);
+                        g.w = fmaf(g.w, al, __uint_as_float(tg[e][3]) * be);
+                        M = Mn;
+                    } else {
                         g.x += __uint_as_float(tg[e][0]);
                         g.y += __uint_as_float(tg[e][1]);
                         g.z += __uint_as_float(tg[e][2]);
@@ -172,13 +282,99 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
                     }
                 }
             }
-            if constexpr (SRC == kGemvSrcSwiglu) {
-                if (ok) g = make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
+            if (c0 + kPer >= hi) break;
+            // further batches (more than kPer slices or chunks per part)
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+                const int c = c0 + kPer + e;
+                const bool v = ok && c < hi;
+                if constexpr (kAttn) {
+                    const uint32_t r0 = head_base + static_cast<uint32_t>(c * rec);
+                    tg[e] = buffer_load16(drs, v ? (r0 + 4u + static_cast<uint32_t>(d0)) * 4u : 0xfffffff0u);
+                    tu[e] = buffer_load16(drs, v ? r0 * 4u : 0xfffffff0u);
+                } else {
+                    const uint32_t base = static_cast<uint32_t>(c) * slice_stride + static_cast<uint32_t>(kk);
+                    tg[e] = buffer_load16(drs, v ? base * 4u : 0xfffffff0u);
+                    if constexpr (SRC == kGemvSrcSwiglu)
+                        tu[e] = buffer_load16(drs, v ? (base + static_cast<uint32_t>(k)) * 4u : 0xfffffff0u);
+                }
+            }
+        }
+        pg[part * NQ + q] = g;
+        if constexpr (kAttn)
+            pu[part * NQ + q] = make_float4(M, Lsum, 0.0f, 0.0f);
+        else if constexpr (SRC == kGemvSrcSwiglu)
+            pu[part * NQ + q] = u;
+        __syncthreads();
+
+        float ss_part = 0.0f;
+        if (threadIdx.x < NQ) {
+            g = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (kAttn) {
+                M = -INFINITY;
+                Lsum = 0.0f;
+                for (int pp = 0; pp < P; ++pp) {   // parts in chunk order
+                    const float4 ml = pu[pp * NQ + q];
+                    if (ml.y > 0.0f) {
+                        const float4 o = pg[pp * NQ + q];
+                        const float Mn = fmaxf(M, ml.x);
+                        const float al = M > -INFINITY ? expf(M - Mn) : 0.0f;
+                        const float be = expf(ml.x - Mn);
+                        Lsum = fmaf(Lsum, al, ml.y * be);
+                        g.x = fmaf(g.x, al, o.x * be);
+                        g.y = fmaf(g.y, al, o.y * be);
+                        g.z = fmaf(g.z, al, o.z * be);
+                        g.w = fmaf(g.w, al, o.w * be);
+                        M = Mn;
+                    }
+                }
+                const float il = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
+                g = make_float4(g.x * il, g.y * il, g.z * il, g.w * il);
+            } else {
+                u = g;
+                if constexpr (kNorm)   // the residual first: h + (part 0) + (part 1) + ...
+                    g = make_float4(__uint_as_float(hres[0]), __uint_as_float(hres[1]), __uint_as_float(hres[2]),
+                                    __uint_as_float(hres[3]));
+                for (int pp = 0; pp < P; ++pp) {
+                    const float4 a2 = pg[pp * NQ + q];
+                    g = make_float4(g.x + a2.x, g.y + a2.y, g.z + a2.z, g.w + a2.w);
+                    if constexpr (SRC == kGemvSrcSwiglu) {
+                        const float4 b2 = pu[pp * NQ + q];
+                        u = make_float4(u.x + b2.x, u.y + b2.y, u.z + b2.z, u.w + b2.w);
+                    }
+                }
+                if constexpr (SRC == kGemvSrcSwiglu) {
+                    const float iv = inv_rms(src.ss_in, src.ss_count, src.ss_dim, src.eps);
+                    g = make_float4(g.x * iv, g.y * iv, g.z * iv, g.w * iv);
+                    u = make_float4(u.x * iv, u.y * iv, u.z * iv, u.w * iv);
+                    g = make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
+                }
+                if constexpr (kNorm) {
+                    if (ok) {
+                        if (src.h_out && blockIdx.x == 0) *reinterpret_cast<float4*>(src.h_out + kk) = g;
+                        ss_part = fmaf(g.x, g.x, fmaf(g.y, g.y, fmaf(g.z, g.z, g.w * g.w)));
+                        g = make_float4(g.x * __uint_as_float(nwv[0]), g.y * __uint_as_float(nwv[1]),
+                                        g.z * __uint_as_float(nwv[2]), g.w * __uint_as_float(nwv[3]));
+                    }
+                }
             }
             // K values past k stay zero (their codes are zero too).
             *reinterpret_cast<float4*>(xs + 4 * q) = ok ? g : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+        if constexpr (kNorm) {
+            // Sum of squares of h over this split's K range (tile 0 writes it).
+            for (int off = 32; off > 0; off >>= 1) ss_part += __shfl_xor(ss_part, off, 64);
+            if (lane == 0) ssp[wave] = ss_part;
+        }
         __syncthreads();
+        if constexpr (kNorm) {
+            if (src.ss_out && blockIdx.x == 0 && threadIdx.x == 0) {
+                float t = 0.0f;
+#pragma unroll
+                for (int ww = 0; ww < W; ++ww) t += ssp[ww];
+                src.ss_out[split] = t;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < kXLane / 4; ++i)
             xv[i] = *reinterpret_cast<const u32x4*>(xs + (kk0 - kw0) + 4 * i);
@@ -282,23 +478,23 @@ bool choose_slices_config(int kind, int64_t k, int64_t n, int block, int max_sli
 }
 
 template <int KIND, int R, int W, int SRC>
-void launch_slices(const float* act, int in_slices, const uint8_t* wq, const float* scale, float* out, int k, int n,
+void launch_slices(const vm_hip_gemv_src& src, const uint8_t* wq, const float* scale, float* out, int k, int n,
                    int block, int splits, hipStream_t stream) {
     const int tiles = (n + kTileCols - 1) / kTileCols;
     const int64_t rows = KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : k;
     const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block - 1) / block;
     const uint32_t code_bytes = static_cast<uint32_t>(rows * n);
     const uint32_t scale_bytes = static_cast<uint32_t>(KIND == 0 ? static_cast<int64_t>(n) * 4 : nblk * n * 4);
-    hipLaunchKernelGGL((qmm_gemv_slices_kernel<KIND, R, W, SRC>), dim3(tiles, splits), dim3(W * 64), 0, stream, act,
-                       in_slices, wq, scale, out, k, n, block, code_bytes, scale_bytes);
+    hipLaunchKernelGGL((qmm_gemv_slices_kernel<KIND, R, W, SRC>), dim3(tiles, splits), dim3(W * 64), 0, stream, src,
+                       wq, scale, out, k, n, block, code_bytes, scale_bytes);
 }
 
 template <int KIND, int SRC>
-void dispatch_rw(const SlicesConfig& c, const float* act, int in_slices, const uint8_t* wq, const float* scale,
+void dispatch_rw(const SlicesConfig& c, const vm_hip_gemv_src& src, const uint8_t* wq, const float* scale,
                  float* out, int k, int n, int block, hipStream_t stream) {
 #define VM_SLICES_CASE(RR, WW)                                                                              \
     if (c.R == RR && c.W == WW)                                                                             \
-        return launch_slices<KIND, RR, WW, SRC>(act, in_slices, wq, scale, out, k, n, block, c.splits, stream);
+        return launch_slices<KIND, RR, WW, SRC>(src, wq, scale, out, k, n, block, c.splits, stream);
     if constexpr (KIND == 2) {
         VM_SLICES_CASE(4, 4)
         VM_SLICES_CASE(4, 8)
@@ -353,20 +549,38 @@ int vm_hip_gemv_slices_count(int64_t k, int64_t n, int quant_type, int block_siz
     return 0;
 }
 
-int vm_hip_qmm_gemv_slices_f32(const float* act, int act_kind, int64_t act_slices, const int8_t* wq,
-                               const float* scale, float* out, int64_t k, int64_t n, int quant_type, int block_size,
-                               int max_slices, void* stream) {
+int vm_hip_qmm_gemv_slices_src_f32(const vm_hip_gemv_src* src, const int8_t* wq, const float* scale, float* out,
+                                   int64_t k, int64_t n, int quant_type, int block_size, int max_slices,
+                                   void* stream) {
     int s = 0;
     VM_TRY(vm_hip_gemv_slices_count(k, n, quant_type, block_size, max_slices, &s));
-    if (!act || !wq || !scale || !out) return fail_inval("gemv_slices: null pointer");
-    if (act_kind != VM_HIP_GEMV_SRC_PLAIN && act_kind != VM_HIP_GEMV_SRC_SLICES && act_kind != VM_HIP_GEMV_SRC_SWIGLU)
+    if (!src || !src->act || !wq || !scale || !out) return fail_inval("gemv_slices: null pointer");
+    const int kindsrc = src->kind;
+    if (kindsrc < VM_HIP_GEMV_SRC_PLAIN || kindsrc > VM_HIP_GEMV_SRC_ATTN)
         return fail_inval("gemv_slices: unknown activation source");
-    if (act_kind != VM_HIP_GEMV_SRC_PLAIN && (act_slices < 1 || act_slices > 4096))
-        return fail_inval("gemv_slices: act_slices must be in [1, 4096]");
-    if (k % 4 != 0 || reinterpret_cast<uintptr_t>(act) % 16 != 0)
+    const bool sliced = kindsrc == VM_HIP_GEMV_SRC_SLICES || kindsrc == VM_HIP_GEMV_SRC_SWIGLU;
+    if (sliced && (src->slices < 1 || src->slices > 4096)) return fail_inval("gemv_slices: slices must be in [1, 4096]");
+    if (kindsrc == VM_HIP_GEMV_SRC_NORMRES) {
+        if (src->slices < 0 || src->slices > 4096 || (src->slices > 0 && !src->delta) || !src->norm_w)
+            return fail_inval("gemv_slices: residual source needs norm_w and slices in [0, 4096] with delta");
+        if ((src->delta && reinterpret_cast<uintptr_t>(src->delta) % 16) ||
+            reinterpret_cast<uintptr_t>(src->norm_w) % 16 || (src->h_out && reinterpret_cast<uintptr_t>(src->h_out) % 16))
+            return fail_inval("gemv_slices: residual operands must be 16-byte aligned");
+    }
+    if ((kindsrc == VM_HIP_GEMV_SRC_SWIGLU && src->ss_in) && (src->ss_count < 1 || src->ss_dim <= 0.0f))
+        return fail_inval("gemv_slices: ss_in needs ss_count >= 1 and ss_dim > 0");
+    if (kindsrc == VM_HIP_GEMV_SRC_ATTN) {
+        if (!src->pos || src->head_dim < 4 || src->head_dim % 4 || k % src->head_dim || src->chunk < 1 ||
+            src->chunks < 1 || src->max_seq < 1 || static_cast<int64_t>(src->chunks) * src->chunk < src->max_seq)
+            return fail_inval("gemv_slices: attention source needs pos, head_dim | k and chunks * chunk >= max_seq");
+        if ((k / src->head_dim) * src->chunks * (src->head_dim + 4) * 4 > 0x7fffffffLL)
+            return fail_inval("gemv_slices: attention partials too large");
+    }
+    if (k % 4 != 0 || reinterpret_cast<uintptr_t>(src->act) % 16 != 0)
         return fail_inval("gemv_slices: k % 4 == 0 and a 16-byte aligned activation required");
     const int64_t rows = quant_type == VM_HIP_QUANT_INT4 ? (k + 1) / 2 : k;
-    const int64_t src_floats = act_kind == VM_HIP_GEMV_SRC_PLAIN ? k : act_slices * k * (act_kind == VM_HIP_GEMV_SRC_SWIGLU ? 2 : 1);
+    const int64_t src_floats = sliced ? src->slices * k * (kindsrc == VM_HIP_GEMV_SRC_SWIGLU ? 2 : 1)
+                                      : (kindsrc == VM_HIP_GEMV_SRC_NORMRES ? std::max<int64_t>(k, src->slices * k) : k);
     if (rows * n > 0x7fffffffLL || s * n > 0x7fffffffLL || src_floats * 4 > 0x7fffffffLL)
         return fail_inval("gemv_slices: operands must stay below 2 GiB");
     VM_TRY(injected_failure("QuantizedMatMul", "launch"));
@@ -380,15 +594,16 @@ int vm_hip_qmm_gemv_slices_f32(const float* act, int act_kind, int64_t act_slice
     const int block = kind == 2 ? (block_size > 0 ? block_size : 32) : block_size;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const auto* wb = reinterpret_cast<const uint8_t*>(wq);
-    const int ki = static_cast<int>(k), ni = static_cast<int>(n), sl = static_cast<int>(act_slices);
+    const int ki = static_cast<int>(k), ni = static_cast<int>(n);
 #define VM_SLICES_SRC(KINDV)                                                                                    \
     do {                                                                                                      \
-        if (act_kind == VM_HIP_GEMV_SRC_PLAIN)                                                                \
-            dispatch_rw<KINDV, kGemvSrcPlain>(cfg, act, 0, wb, scale, out, ki, ni, block, st);                \
-        else if (act_kind == VM_HIP_GEMV_SRC_SLICES)                                                          \
-            dispatch_rw<KINDV, kGemvSrcSlices>(cfg, act, sl, wb, scale, out, ki, ni, block, st);              \
-        else                                                                                                  \
-            dispatch_rw<KINDV, kGemvSrcSwiglu>(cfg, act, sl, wb, scale, out, ki, ni, block, st);              \
+        switch (kindsrc) {                                                                                    \
+            case VM_HIP_GEMV_SRC_PLAIN: dispatch_rw<KINDV, kGemvSrcPlain>(cfg, *src, wb, scale, out, ki, ni, block, st); break; \
+            case VM_HIP_GEMV_SRC_SLICES: dispatch_rw<KINDV, kGemvSrcSlices>(cfg, *src, wb, scale, out, ki, ni, block, st); break; \
+            case VM_HIP_GEMV_SRC_SWIGLU: dispatch_rw<KINDV, kGemvSrcSwiglu>(cfg, *src, wb, scale, out, ki, ni, block, st); break; \
+            case VM_HIP_GEMV_SRC_NORMRES: dispatch_rw<KINDV, kGemvSrcNormRes>(cfg, *src, wb, scale, out, ki, ni, block, st); break; \
+            default: dispatch_rw<KINDV, kGemvSrcAttn>(cfg, *src, wb, scale, out, ki, ni, block, st); break;     \
+        }                                                                                                     \
     } while (0)
     if (kind == 2)
         VM_SLICES_SRC(2);
@@ -398,6 +613,21 @@ int vm_hip_qmm_gemv_slices_f32(const float* act, int act_kind, int64_t act_slice
         VM_SLICES_SRC(0);
 #undef VM_SLICES_SRC
     return check_launch("QuantizedMatMul", st);
+}
+
+int vm_hip_qmm_gemv_slices_f32(const float* act, int act_kind, int64_t act_slices, const int8_t* wq,
+                               const float* scale, float* out, int64_t k, int64_t n, int quant_type, int block_size,
+                               int max_slices, void* stream) {
+    clear_error();
+    if (act_kind != VM_HIP_GEMV_SRC_PLAIN && act_kind != VM_HIP_GEMV_SRC_SLICES && act_kind != VM_HIP_GEMV_SRC_SWIGLU)
+        return fail_inval("gemv_slices: unknown activation source");
+    vm_hip_gemv_src src{};
+    src.kind = act_kind;
+    src.act = act;
+    src.slices = act_kind == VM_HIP_GEMV_SRC_PLAIN ? 0 : static_cast<int>(std::min<int64_t>(act_slices, 1 << 20));
+    if (act_kind != VM_HIP_GEMV_SRC_PLAIN && (act_slices < 1 || act_slices > 4096))
+        return fail_inval("gemv_slices: act_slices must be in [1, 4096]");
+    return vm_hip_qmm_gemv_slices_src_f32(&src, wq, scale, out, k, n, quant_type, block_size, max_slices, stream);
 }
 
 }  // extern "C"

@@ -31,6 +31,14 @@ class VmHipError(RuntimeError):
         self.status = status
 
 
+class GemvSrc(ctypes.Structure):
+    """vm_hip_gemv_src (include/vm_hip.h)."""
+    _fields_ = [("kind", c_int), ("slices", c_int), ("act", c_void_p), ("delta", c_void_p), ("norm_w", c_void_p),
+                ("h_out", c_void_p), ("ss_out", c_void_p), ("ss_in", c_void_p), ("ss_count", c_int),
+                ("ss_dim", c_float), ("eps", c_float), ("pos", c_void_p), ("head_dim", c_int), ("chunk", c_int),
+                ("chunks", c_int), ("max_seq", c_int)]
+
+
 def _declare(L: ctypes.CDLL) -> None:
     p = c_void_p
     sig = {
@@ -89,6 +97,12 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_rope_kv_append_slices_f32": ([p, c_int64, p, p, p, p, p, p] + [c_int64] * 4 + [p], c_int),
         "vm_hip_argmax_slices_f32": ([p, c_int64, c_int64, p, p, p, c_int64, p], c_int),
         "vm_hip_slices_sum_f32": ([p, c_int64, c_int64, p, p], c_int),
+        "vm_hip_qmm_gemv_slices_src_f32": ([POINTER(GemvSrc), p, p, p, c_int64, c_int64, c_int, c_int, c_int, p],
+                                           c_int),
+        "vm_hip_attention_decode_chunks": ([c_int64, c_int64, POINTER(c_int), POINTER(c_int)], c_int),
+        "vm_hip_attention_decode_slices_f32": ([p, c_int64, p, c_int64, c_float, c_float, p, p, p, p, p, p,
+                                                c_int64, c_int64, c_int64, c_int64, c_float, p], c_int),
+        "vm_hip_slices_sum_scaled_f32": ([p, c_int64, c_int64, p, c_int64, c_float, c_float, p, p], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -112,7 +126,9 @@ def exported_symbols() -> list[str]:
             "vm_hip_add_rmsnorm_f32", "vm_hip_rope_kv_append_f32", "vm_hip_attention_decode_f32",
             "vm_hip_attention_prefill_f32", "vm_hip_silu_mul_f32", "vm_hip_argmax_f32", "vm_hip_memcpy_2d_d2d",
             "vm_hip_gemv_slices_count", "vm_hip_qmm_gemv_slices_f32", "vm_hip_add_rmsnorm_slices_f32",
-            "vm_hip_rope_kv_append_slices_f32", "vm_hip_argmax_slices_f32", "vm_hip_slices_sum_f32"]
+            "vm_hip_rope_kv_append_slices_f32", "vm_hip_argmax_slices_f32", "vm_hip_slices_sum_f32",
+            "vm_hip_qmm_gemv_slices_src_f32", "vm_hip_attention_decode_chunks", "vm_hip_attention_decode_slices_f32",
+            "vm_hip_slices_sum_scaled_f32"]
 
 
 def open_library() -> ctypes.CDLL:
@@ -341,7 +357,7 @@ def run_pack_int4(w: np.ndarray, block: int = 32):
 # ---- LLaMA graph operators, numpy level (one call each, null stream) ----
 
 EW_ADD, EW_MUL, EW_SIGMOID = 0, 1, 2
-GEMV_SRC_PLAIN, GEMV_SRC_SLICES, GEMV_SRC_SWIGLU = 0, 1, 2
+GEMV_SRC_PLAIN, GEMV_SRC_SLICES, GEMV_SRC_SWIGLU, GEMV_SRC_NORMRES, GEMV_SRC_ATTN = 0, 1, 2, 3, 4
 
 
 def _dev(a: np.ndarray, dtype=np.float32) -> DeviceBuffer:
