@@ -21,6 +21,13 @@ two events on the launch stream.  ``cpu_baseline``
 times the oracle's scalar INT4 path (src/cpu/ops/quantized_matmul.cpp:48-141)
 on one pinned core over a bounded sample of the same step.
 
+``e2e`` adds the metric's second half, TinyLlama INT4 decode tokens/s
+(512-token prompt, 256 greedy tokens) and SmolLM2-360M
+INT8 (config 4: 128 + 128), on the resident HIP decoder with synthetic
+weights: prefill and decode tokens/s, and the decode step's weight stream
+(packed codes + scales of every QuantizedMatMul per token) as GB/s and as a
+fraction of HBM peak.
+
 Prints one JSON line.  Only --gpus 1 is supported (one GPU per box).
 """
 from __future__ import annotations
@@ -215,6 +222,70 @@ def cpu_baseline(target_s: float) -> dict:
             "tokens_per_s": round(sweeps / dt, 4)}
 
 
+E2E_MODELS = {
+    # TinyLlama-1.1B shapes, synthetic INT4 weights,
+    # 512-token uniform-random prompt, 256 greedy decode tokens.
+    "tinyllama_1.1b_int4": dict(cfg=dict(vocab_size=32000, hidden_size=2048, intermediate_size=5632, num_layers=22,
+                                         num_heads=32, num_kv_heads=4, rms_norm_eps=1e-5, rope_theta=10000.0),
+                                quant=2, block=32, prompt=512, steps=256),
+    # SmolLM2-360M shapes, synthetic INT8 weights,
+    # 128-token prompt, 128 greedy decode tokens (tied embeddings: the
+    # lm_head is its own packed copy of the embedding's transpose here).
+    "smollm2_360m_int8": dict(cfg=dict(vocab_size=49152, hidden_size=960, intermediate_size=2560, num_layers=32,
+                                       num_heads=15, num_kv_heads=5, rms_norm_eps=1e-5, rope_theta=100000.0),
+                              quant=1, block=0, prompt=128, steps=128),
+}
+
+
+def decode_weight_bytes(c: dict, quant: int, block: int) -> int:
+    """Packed codes + scales the decode step streams per token: every
+    linear of every layer plus lm_head (QuantizedMatMul weights only)."""
+    h, i, d = c["hidden_size"], c["intermediate_size"], c["hidden_size"] // c["num_heads"]
+    kv = c["num_kv_heads"] * d
+    shapes = [(h, h), (h, kv), (h, kv), (h, h), (h, i), (h, i), (i, h)] * c["num_layers"] + [(h, c["vocab_size"])]
+    tot = 0
+    for k, n in shapes:
+        if quant == 2:
+            tot += ((k + 1) // 2) * n + ((k + block - 1) // block) * n * 4
+        else:
+            tot += k * n + n * 4
+    return tot
+
+
+def e2e_bench(name: str) -> dict:
+    """Greedy generation on the resident HIP decoder (HIP-graph decode
+    steps); device-event timing of the prefill and of the decode steps."""
+    from velomind_hip import llama as VL
+
+    spec = E2E_MODELS[name]
+
+    class Cfg:
+        pass
+
+    cfg = Cfg()
+    for k, v in spec["cfg"].items():
+        setattr(cfg, k, v)
+    w = VL.Weights(cfg)
+    w.fill_synthetic(20240601, 0.02)
+    sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"], max_seq=spec["prompt"] + spec["steps"] + 1)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, spec["prompt"]).astype(np.int32)
+    sess.generate(prompt, 8)  # warm-up (also sizes the workspaces)
+    _, (pf_s, dec_s, nd) = sess.generate(prompt, spec["steps"])
+    wb = decode_weight_bytes(spec["cfg"], spec["quant"], spec["block"])
+    dec_tps = nd / dec_s
+    out = {"prompt_tokens": spec["prompt"], "decode_tokens": spec["steps"], "decode_steps_timed": nd,
+           "prefill_tokens_per_s": round(spec["prompt"] / pf_s, 1), "prefill_ms": round(pf_s * 1e3, 3),
+           "decode_tokens_per_s": round(dec_tps, 1), "decode_us_per_token": round(dec_s / nd * 1e6, 1),
+           "decode_weight_bytes_per_token": wb, "decode_weight_GB_s": round(wb * dec_tps / 1e9, 1),
+           "decode_frac_of_hbm_peak": round(wb * dec_tps / 1e9 / HBM_PEAK_GBS, 4),
+           "weights": ("int4 block 32" if spec["quant"] == 2 else "int8 per column") +
+                      ", synthetic N(0, 0.02), packed on the GPU",
+           "engine": "resident HIP decoder, HIP-graph decode steps, greedy argmax on device"}
+    sess.close()
+    w.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -224,6 +295,7 @@ def main() -> int:
     ap.add_argument("--shape-reps", type=int, default=20, help="replays per shape for per-launch durations")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--only-shape", default="", help="KxN: launch only this shape's GEMVs (profiling passes)")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode legs (configs 4 and 5)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (rocprofv3 counter calibration)")
     args = ap.parse_args()
@@ -307,6 +379,15 @@ def main() -> int:
     launches = len(wl.calls)
     traffic, traffic_src = measured_traffic(f"{dk}x{dn}")
 
+    e2e = None
+    if not args.no_e2e and not args.only_shape:
+        e2e = {}
+        for name in E2E_MODELS:
+            log(f"bench: end-to-end {name}")
+            e2e[name] = e2e_bench(name)
+            log(f"bench: {name}: prefill {e2e[name]['prefill_tokens_per_s']} tok/s, "
+                f"decode {e2e[name]['decode_tokens_per_s']} tok/s")
+
     cpu = None
     if args.cpu_seconds > 0:
         log("bench: timing CPU baseline")
@@ -350,6 +431,7 @@ def main() -> int:
             "algo_bytes_per_launch": dbytes,
         },
         "per_shape": per_shape,
+        "e2e": e2e,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
