@@ -252,7 +252,7 @@ def decode_weight_bytes(c: dict, quant: int, block: int) -> int:
     return tot
 
 
-def e2e_bench(name: str) -> dict:
+def e2e_bench(name: str, use_graph: bool = True) -> dict:
     """Greedy generation on the resident HIP decoder (HIP-graph decode
     steps); device-event timing of the prefill and of the decode steps."""
     from velomind_hip import llama as VL
@@ -269,8 +269,8 @@ def e2e_bench(name: str) -> dict:
     w.fill_synthetic(20240601, 0.02)
     sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"], max_seq=spec["prompt"] + spec["steps"] + 1)
     prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, spec["prompt"]).astype(np.int32)
-    sess.generate(prompt, 8)  # warm-up (also sizes the workspaces)
-    _, (pf_s, dec_s, nd) = sess.generate(prompt, spec["steps"])
+    sess.generate(prompt, 8, use_hip_graph=use_graph)  # warm-up (also sizes the workspaces)
+    _, (pf_s, dec_s, nd) = sess.generate(prompt, spec["steps"], use_hip_graph=use_graph)
     wb = decode_weight_bytes(spec["cfg"], spec["quant"], spec["block"])
     dec_tps = nd / dec_s
     out = {"prompt_tokens": spec["prompt"], "decode_tokens": spec["steps"], "decode_steps_timed": nd,
@@ -280,7 +280,8 @@ def e2e_bench(name: str) -> dict:
            "decode_frac_of_hbm_peak": round(wb * dec_tps / 1e9 / HBM_PEAK_GBS, 4),
            "weights": ("int4 block 32" if spec["quant"] == 2 else "int8 per column") +
                       ", synthetic N(0, 0.02), packed on the GPU",
-           "engine": "resident HIP decoder, HIP-graph decode steps, greedy argmax on device"}
+           "engine": "resident HIP decoder, " + ("HIP-graph" if use_graph else "eager") +
+                     " decode steps, greedy argmax on device"}
     sess.close()
     w.close()
     return out
@@ -296,6 +297,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--only-shape", default="", help="KxN: launch only this shape's GEMVs (profiling passes)")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decode legs (configs 4 and 5)")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="only the end-to-end legs, printed as one JSON line (profiling passes; with --no-graph "
+                         "the decode steps launch eagerly so that rocprofv3 can trace them)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (rocprofv3 counter calibration)")
     args = ap.parse_args()
@@ -315,6 +319,15 @@ def main() -> int:
             H.check(lib.vm_hip_memcpy_d2d(dst.ptr, src.ptr, 64 << 20, stream.handle))
         stream.synchronize()
         log("bench: calibration copies done (10 x 64 MiB)")
+        return 0
+    if args.e2e_only:
+        e2e = {}
+        for name in E2E_MODELS:
+            log(f"bench: end-to-end {name}")
+            e2e[name] = e2e_bench(name, use_graph=not args.no_graph)
+            log(f"bench: {name}: prefill {e2e[name]['prefill_tokens_per_s']} tok/s, "
+                f"decode {e2e[name]['decode_tokens_per_s']} tok/s")
+        print(json.dumps({"metric": METRIC, "e2e": e2e}), flush=True)
         return 0
     log("bench: packing weights on the GPU")
     wl = Workload(H, stream)
