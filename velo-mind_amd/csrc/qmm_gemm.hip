@@ -461,28 +461,42 @@ struct GemmConfig {
     int bm = 128, bn = 128, splits = 1;
 };
 
-// Tile and split choice, from a sweep of every tile variant and split count
-// over config-3 shapes (K = 2048, N = 5632, M = 16..512) on MI355X: up to
-// 128 rows, 32 x 64 tiles (many small workgroups hide load latency best);
-// beyond, 128 x 128 tiles (least LDS traffic per MFMA).  K splits (at
-// least four 64-row steps each) are added until about two workgroups per
-// CU, while the fp32 partials stay under a quarter of the code bytes.
+// Tile and split choice, from sweeps of every tile variant and split count
+// on MI355X over config-3 shapes (K = 2048, N = 5632, M = 16..512) and the
+// TinyLlama / SmolLM2 prefill projections (M = 512: N = 2048..11264, K =
+// 2048 and 5632; M = 128: K, N = 960..5120):
+//   M <= 128: 32 x 64 tiles (many small workgroups hide load latency best);
+//     K splits (at least four 64-row steps each) until about two workgroups
+//     per CU, while the fp32 partials stay under a quarter of the code
+//     bytes -- or, with fewer than 128 tiles, while each split keeps at
+//     least eight steps;
+//   M > 128: 64 x 128 tiles; K splits of at least twenty 64-row steps up
+//     to ~512 workgroups (K = 5632: 4 splits); 32 x 128 when an unsplit
+//     grid would hold fewer than 150 tiles (N = 2048: 27.5 us vs 42.1 us
+//     with the former 128 x 128 tiles).
 GemmConfig choose_gemm(int kind, int m, int k, int n) {
     GemmConfig cfg;
+    const int steps = (k + kBK - 1) / kBK;
+    const double code_bytes = kind == 2 ? 0.5 * k * n : 1.0 * k * n;
+    auto tiles_of = [&](int bm, int bn) {
+        return static_cast<long>((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    };
+    int s = 1;
     if (m <= 128) {
         cfg.bm = 32;
         cfg.bn = 64;
+        const long tiles = tiles_of(cfg.bm, cfg.bn);
+        while (s * 2 <= 8 && tiles * s * 2 <= 512 &&
+               ((steps / (s * 2) >= 4 && 4.0 * s * 2 * m * n <= 0.25 * code_bytes) ||
+                (tiles < 128 && steps / (s * 2) >= 8)))
+            s *= 2;
     } else {
-        cfg.bm = 128;
+        cfg.bm = 64;
         cfg.bn = 128;
+        const long tiles = tiles_of(cfg.bm, cfg.bn);
+        while (s * 2 <= 4 && tiles * s * 2 <= 512 && steps / (s * 2) >= 20) s *= 2;
+        if (s == 1 && tiles < 150) cfg.bm = 32;
     }
-    const long tiles = static_cast<long>((m + cfg.bm - 1) / cfg.bm) * ((n + cfg.bn - 1) / cfg.bn);
-    const int steps = (k + kBK - 1) / kBK;
-    const double code_bytes = kind == 2 ? 0.5 * k * n : 1.0 * k * n;
-    int s = 1;
-    while (s * 2 <= 8 && tiles * s * 2 <= 512 && steps / (s * 2) >= 4 &&
-           4.0 * s * 2 * m * n <= 0.25 * code_bytes)
-        s *= 2;
     cfg.splits = s;
     // Tuning override for measurement sweeps: VELOMIND_GEMM_CFG="BM,BN,S".
     if (const char* env = std::getenv("VELOMIND_GEMM_CFG")) {
