@@ -184,9 +184,11 @@ def test_rope_kv_append(hip):
     assert np.array_equal(dv.download(np.float32, vc.shape), vc)
 
 
-@pytest.mark.parametrize("rows,p0", [(19, 0), (64, 0), (70, 10)])
-def test_attention_prefill(hip, rows, p0):
-    heads, kv_heads, d, max_seq = 8, 2, 64, 96
+@pytest.mark.parametrize("rows,p0,heads,kv_heads,max_seq", [(19, 0, 8, 2, 96), (64, 0, 8, 2, 96), (70, 10, 8, 2, 96),
+                                                        (200, 0, 32, 4, 256), (130, 77, 15, 5, 256),
+                                                        (1, 40, 8, 8, 64)])
+def test_attention_prefill(hip, rows, p0, heads, kv_heads, max_seq):
+    d = 64
     rng = np.random.default_rng(rows + p0)
     q = rng.standard_normal((heads, rows, d)).astype(np.float32)
     kc = rng.standard_normal((kv_heads, max_seq, d)).astype(np.float32)

@@ -751,11 +751,23 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
     }
 }
 
-// ---- Prefill attention over the resident cache: q [H, S, D] rows at
-// positions *pos + i, causal over keys 0 .. *pos + i; output [S, H, D]
-// (token-major, the layout the output projection reads).  Grid
-// (ceil(S/64), H): 64 query rows per workgroup, four threads per row, key
-// tiles of 64 through LDS with an online softmax.
+// ---- Prefill attention over the resident cache with fp32 matrix cores:
+// q [H, S, D] rows at positions *pos + i see keys 0 .. *pos + i (causal);
+// out [S, H, D] (token-major, the layout the output projection reads).
+// Grid (ceil(S/64), H), four waves; wave w owns query rows r0 + 16w .. +15
+// and walks 64-key tiles staged in LDS with an online softmax.
+//
+// v_mfma_f32_16x16x4_f32 (fp32 inputs and accumulation, so no precision is
+// given up against the fp32 reference) holds A[i][k] in lane i + 16k,
+// B[k][j] in lane j + 16k and D[i][j] in lane j + 16 (i / 4), element i % 4.
+// Scores are computed transposed, S^T = K Q^T, so lane (row r = lane % 16,
+// group g = lane / 16) holds row r's scores for keys 16b + 4g + e: exactly
+// the A operand of P V once the product's reduction index is ordered as
+// key(s, k) = 16 (s / 4) + 4k + s % 4 (the order of a sum's terms is free).
+// Row statistics live in the lanes of row r (shared across the four
+// groups); output row 4g + e fetches its factor from lane 4g + e.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <int D>
 __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __restrict__ q,
                                                                const float* __restrict__ k_cache,
@@ -763,84 +775,137 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
                                                                const int32_t* __restrict__ pos,
                                                                float* __restrict__ out, int rows, int heads,
                                                                int kv_heads, int max_seq, float scale) {
-    constexpr int kRows = 64, kKeys = 64, kDq = D / 4;
-    __shared__ float sq[kRows][D + 1];
-    __shared__ float sk[kKeys][D + 1];
-    __shared__ float sv[kKeys][D];
-    __shared__ float sp[kRows][kKeys + 1];
+    static_assert(D == 64, "one 16-dim slab per lane group");
+    constexpr int KT = 64;          // keys per tile
+    constexpr int PITCH = D + 4;    // LDS row pitch in floats (conflict-free 16-byte reads)
+    __shared__ __align__(16) float sk[KT * PITCH];
+    __shared__ __align__(16) float sv[KT * PITCH];
     const int h = blockIdx.y;
     const int hk = h / (heads / kv_heads);
-    const int r0 = blockIdx.x * kRows;
+    const int r0 = blockIdx.x * 64;
     const int tid = threadIdx.x;
-    const int row = tid >> 2, sub = tid & 3;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
     const int p0 = pos[0];
     const int n_keys = min(p0 + rows, max_seq);
-    const int last_key = min(p0 + min(r0 + kRows, rows), n_keys);  // keys visible to the tile's last row
+    const int qrow = r0 + 16 * wave + lr;     // the query row whose Q this lane holds
+    const bool row_ok = qrow < rows;
+    const int my_last = p0 + qrow;            // keys <= my_last are visible to row qrow
 
-    for (int e = tid; e < kRows * D; e += kT) {
-        const int rr = e / D, t = e % D;
-        sq[rr][t] = (r0 + rr < rows) ? q[(static_cast<int64_t>(h) * rows + r0 + rr) * D + t] : 0.0f;
-    }
-    const int my_pos = p0 + r0 + row;  // absolute position of this thread's query row
-    float m = -INFINITY, l = 0.0f;
-    float acc[kDq];
+    // Q fragment: Q[qrow][16 lg + s], s = 0..15.
+    float qf[16];
+    {
+        const float* qp = q + (static_cast<int64_t>(h) * rows + (row_ok ? qrow : 0)) * D + 16 * lg;
 #pragma unroll
-    for (int i = 0; i < kDq; ++i) acc[i] = 0.0f;
+        for (int c = 0; c < 4; ++c) {
+            const float4 v = row_ok ? *reinterpret_cast<const float4*>(qp + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qf[4 * c + 0] = v.x;
+            qf[4 * c + 1] = v.y;
+            qf[4 * c + 2] = v.z;
+            qf[4 * c + 3] = v.w;
+        }
+    }
+    const int wg_end = min(p0 + min(r0 + 64, rows), n_keys);   // keys < wg_end reach some row of the tile
     const float* kb = k_cache + static_cast<int64_t>(hk) * max_seq * D;
     const float* vb = v_cache + static_cast<int64_t>(hk) * max_seq * D;
+    f32x4 acc[4];   // O[row 4 lg + e][dim 16 db + lr]
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;   // statistics of row lr of this wave
 
-    for (int k0 = 0; k0 < last_key; k0 += kKeys) {
-        __syncthreads();
-        const int nk = min(kKeys, last_key - k0);
-        for (int e = tid; e < kKeys * D; e += kT) {
-            const int j = e / D, t = e % D;
-            const bool ok = j < nk;
-            sk[j][t] = ok ? kb[static_cast<int64_t>(k0 + j) * D + t] : 0.0f;
-            sv[j][t] = ok ? vb[static_cast<int64_t>(k0 + j) * D + t] : 0.0f;
+    for (int k0 = 0; k0 < wg_end; k0 += KT) {
+        const int nk = min(KT, n_keys - k0);
+        __syncthreads();   // the previous tile is consumed
+#pragma unroll
+        for (int u = 0; u < KT * D / 4 / kT; ++u) {
+            const int e = tid + u * kT;
+            const int j = e / (D / 4), c = e - j * (D / 4);
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (j < nk) {
+                kv = *reinterpret_cast<const float4*>(kb + static_cast<int64_t>(k0 + j) * D + 4 * c);
+                vv = *reinterpret_cast<const float4*>(vb + static_cast<int64_t>(k0 + j) * D + 4 * c);
+            }
+            *reinterpret_cast<float4*>(sk + j * PITCH + 4 * c) = kv;
+            *reinterpret_cast<float4*>(sv + j * PITCH + 4 * c) = vv;
         }
         __syncthreads();
-        float tile_max = -INFINITY;
-        float s_loc[kKeys / 4];
+
+        // S^T = K Q^T for the four 16-key blocks.
+        f32x4 st[4];
 #pragma unroll
-        for (int u = 0; u < kKeys / 4; ++u) {
-            const int j = sub + 4 * u;
-            float dot = 0.0f;
-#pragma unroll 16
-            for (int t = 0; t < D; ++t) dot = fmaf(sq[row][t], sk[j][t], dot);
-            const bool vis = (j < nk) && (k0 + j <= my_pos);
-            s_loc[u] = vis ? dot * scale : -INFINITY;
-            tile_max = fmaxf(tile_max, s_loc[u]);
+        for (int nb = 0; nb < 4; ++nb) {
+            const float* krow = sk + (16 * nb + lr) * PITCH + 16 * lg;
+            float ka[16];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float4 v = *reinterpret_cast<const float4*>(krow + 4 * c);
+                ka[4 * c + 0] = v.x;
+                ka[4 * c + 1] = v.y;
+                ka[4 * c + 2] = v.z;
+                ka[4 * c + 3] = v.w;
+            }
+            f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 16; ++s) d = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[s], qf[s], d, 0, 0, 0);
+            st[nb] = d;
         }
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 1, 64));
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 2, 64));
-        const float m_new = fmaxf(m, tile_max);
-        float psum = 0.0f;
+        // Scale, causal mask, online softmax of row lr.
+        float mt = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < kKeys / 4; ++u) {
-            const float pv = s_loc[u] > -INFINITY ? expf(s_loc[u] - m_new) : 0.0f;
-            sp[row][sub + 4 * u] = pv;
-            psum += pv;
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int key = k0 + 16 * nb + 4 * lg + e;
+                const bool vis = row_ok && key <= my_last && key < n_keys;
+                const float v = vis ? st[nb][e] * scale : -INFINITY;
+                st[nb][e] = v;
+                mt = fmaxf(mt, v);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float m_new = fmaxf(m_run, mt);
+        float lt = 0.0f;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float pv = st[nb][e] > -INFINITY ? expf(st[nb][e] - m_new) : 0.0f;
+                st[nb][e] = pv;
+                lt += pv;
+            }
+        lt += __shfl_xor(lt, 16, 64);
+        lt += __shfl_xor(lt, 32, 64);
+        const float alpha = m_run > -INFINITY ? expf(m_run - m_new) : 0.0f;
+        l_run = l_run * alpha + lt;
+        m_run = m_new;
+        // Rescale the output rows 4 lg + e by their rows' factors.
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float ae = __shfl(alpha, 4 * lg + e, 64);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db][e] *= ae;
         }
-        psum += __shfl_xor(psum, 1, 64);
-        psum += __shfl_xor(psum, 2, 64);
-        const float alpha = m > -INFINITY ? expf(m - m_new) : 0.0f;
-        l = l * alpha + psum;
-        m = m_new;
+        // O += P V.
 #pragma unroll
-        for (int i = 0; i < kDq; ++i) acc[i] *= alpha;
-        __syncthreads();
-        for (int j = 0; j < nk; ++j) {
-            const float pv = sp[row][j];
+        for (int db = 0; db < 4; ++db) {
 #pragma unroll
-            for (int i = 0; i < kDq; ++i) acc[i] = fmaf(pv, sv[j][sub + 4 * i], acc[i]);
+            for (int s = 0; s < 16; ++s) {
+                const int key = 16 * (s / 4) + 4 * lg + (s % 4);
+                const float bv = sv[key * PITCH + 16 * db + lr];
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[s / 4][s % 4], bv, acc[db], 0, 0, 0);
+            }
         }
     }
-    const int r = r0 + row;
-    if (r < rows) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float* o = out + (static_cast<int64_t>(r) * heads + h) * D;
 #pragma unroll
-        for (int i = 0; i < kDq; ++i) o[sub + 4 * i] = acc[i] * inv;
+    for (int e = 0; e < 4; ++e) {
+        const float le = __shfl(l_run, 4 * lg + e, 64);
+        const float inv = le > 0.0f ? 1.0f / le : 0.0f;
+        const int row = r0 + 16 * wave + 4 * lg + e;
+        if (row < rows) {
+            float* o = out + (static_cast<int64_t>(row) * heads + h) * D + lr;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[16 * db] = acc[db][e] * inv;
+        }
     }
 }
 
