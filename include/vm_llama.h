@@ -84,6 +84,21 @@ void vm_llama_session_destroy(vm_llama_session* s);
 int vm_llama_prefill(vm_llama_session* s, const int32_t* tokens, int64_t n, float* logits_out);
 int vm_llama_forward_step(vm_llama_session* s, int32_t token, int64_t pos, float* logits_out);
 
+/* Pre-packed weights (no counterpart in the reference, which packs at bind
+ * time): every linear packed on the GPU once (quant.cpp layout, bit-exact),
+ * saved to / loaded from a safetensors file of I8 codes and F32 scales
+ * (names and metadata: velomind/llama/llama_packed.h).  A resident session
+ * created from packed weights does no packing and keeps its own copy of the
+ * linears (the packed handle may be destroyed after it is created). */
+typedef struct vm_llama_packed vm_llama_packed;
+int vm_llama_pack(const vm_llama_weights* w, int quant_type, int block_size, vm_llama_packed** out);
+int vm_llama_packed_save(const vm_llama_packed* p, const char* path);
+/* The model config recorded in a packed file. */
+int vm_llama_packed_config(const char* path, vm_llama_config* out);
+int vm_llama_packed_load(const char* path, const vm_llama_config* cfg, vm_llama_packed** out);
+void vm_llama_packed_destroy(vm_llama_packed* p);
+int vm_llama_session_create_packed(const vm_llama_packed* p, int64_t max_seq, vm_llama_session** out);
+
 /* Greedy decoding: prefill, then `steps` decode steps; out_tokens receives
  * steps + 1 tokens (the first from the prompt's logits).  timing (may be
  * NULL) receives {prefill seconds, decode seconds, decode steps timed}:

@@ -89,9 +89,13 @@ private:
     std::size_t _seq_len = 0;
 };
 
+class PackedLlamaWeights;
+
 class VELOMIND_CORE_EXPORT HipLlamaDecoder {
 public:
     HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_type, int block_size, std::size_t max_seq);
+    // From pre-packed weights (velomind/llama/llama_packed.h): no packing.
+    HipLlamaDecoder(const PackedLlamaWeights& packed, std::size_t max_seq);
     ~HipLlamaDecoder();
     HipLlamaDecoder(const HipLlamaDecoder&) = delete;
     HipLlamaDecoder& operator=(const HipLlamaDecoder&) = delete;

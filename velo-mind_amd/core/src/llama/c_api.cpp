@@ -8,12 +8,17 @@
 #include <string>
 
 #include "velomind/llama/llama_hip.h"
+#include "velomind/llama/llama_packed.h"
 
 using namespace velomind;
 using namespace velomind::examples::llama;
 
 struct vm_llama_weights {
     std::shared_ptr<LlamaWeightSet> set;
+};
+
+struct vm_llama_packed {
+    std::shared_ptr<PackedLlamaWeights> p;
 };
 
 struct vm_llama_session {
@@ -180,6 +185,58 @@ int vm_llama_generate(vm_llama_session* s, const int32_t* prompt, int64_t n, int
             timing[1] = std::chrono::duration<double>(t2 - t1).count();
             timing[2] = static_cast<double>(steps);
         }
+    });
+}
+
+int vm_llama_pack(const vm_llama_weights* w, int quant_type, int block_size, vm_llama_packed** out) {
+    return guarded([&] {
+        if (!w || !out) throw std::invalid_argument("vm_llama_pack: null pointer");
+        auto p = std::make_unique<vm_llama_packed>();
+        p->p = PackedLlamaWeights::pack(*w->set, to_quant(quant_type), block_size);
+        *out = p.release();
+    });
+}
+
+int vm_llama_packed_save(const vm_llama_packed* p, const char* path) {
+    return guarded([&] {
+        if (!p || !path) throw std::invalid_argument("vm_llama_packed_save: null pointer");
+        p->p->save(path);
+    });
+}
+
+int vm_llama_packed_config(const char* path, vm_llama_config* out) {
+    return guarded([&] {
+        if (!path || !out) throw std::invalid_argument("vm_llama_packed_config: null pointer");
+        const Config c = llama_packed_config(path);
+        out->vocab_size = static_cast<int64_t>(c.vocab_size);
+        out->hidden_size = static_cast<int64_t>(c.hidden_size);
+        out->intermediate_size = static_cast<int64_t>(c.intermediate_size);
+        out->num_layers = static_cast<int64_t>(c.num_layers);
+        out->num_heads = static_cast<int64_t>(c.num_heads);
+        out->num_kv_heads = static_cast<int64_t>(c.num_kv_heads);
+        out->rms_norm_eps = c.rms_norm_eps;
+        out->rope_theta = c.rope_theta;
+    });
+}
+
+int vm_llama_packed_load(const char* path, const vm_llama_config* cfg, vm_llama_packed** out) {
+    return guarded([&] {
+        if (!path || !cfg || !out) throw std::invalid_argument("vm_llama_packed_load: null pointer");
+        auto p = std::make_unique<vm_llama_packed>();
+        p->p = PackedLlamaWeights::load(path, to_config(*cfg));
+        *out = p.release();
+    });
+}
+
+void vm_llama_packed_destroy(vm_llama_packed* p) { delete p; }
+
+int vm_llama_session_create_packed(const vm_llama_packed* p, int64_t max_seq, vm_llama_session** out) {
+    return guarded([&] {
+        if (!p || !out) throw std::invalid_argument("vm_llama_session_create_packed: null pointer");
+        if (max_seq <= 0) throw std::invalid_argument("vm_llama_session_create_packed: max_seq must be positive");
+        auto s = std::make_unique<vm_llama_session>();
+        s->resident = std::make_unique<HipLlamaDecoder>(*p->p, static_cast<std::size_t>(max_seq));
+        *out = s.release();
     });
 }
 

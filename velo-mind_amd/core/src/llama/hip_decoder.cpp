@@ -20,6 +20,7 @@
 #include <string>
 
 #include "velomind/llama/llama_hip.h"
+#include "velomind/llama/llama_packed.h"
 #include "vm_hip.h"
 
 namespace velomind::examples::llama {
@@ -227,6 +228,44 @@ struct HipLlamaDecoder::Impl {
               "logits");
     }
 
+    void setup(const Config& config, QuantType quant_type, int block_size, std::size_t max_seq_len);
+    void allocate();
+
+    // A packed linear assembled from already packed parts placed side by
+    // side (columns of each part in order): quant.cpp packs every column on
+    // its own, so this is byte for byte the packing of the concatenated
+    // fp32 matrix.
+    void assemble(Packed& dst, std::initializer_list<const PackedLinear*> parts) {
+        const std::int64_t k = (*parts.begin())->k;
+        std::int64_t n = 0;
+        for (const auto* p : parts) {
+            if (p->k != k) throw std::invalid_argument("HipLlamaDecoder: fused parts differ in K");
+            n += p->n;
+        }
+        const bool int4 = qt == VM_HIP_QUANT_INT4;
+        const std::int64_t code_rows = int4 ? (k + 1) / 2 : k;
+        const std::int64_t scale_rows = int4 ? (k + block - 1) / block : 1;
+        dst.k = k;
+        dst.n = n;
+        dst.codes = DevBuf(static_cast<std::size_t>(code_rows * n));
+        dst.scales = DevBuf(static_cast<std::size_t>(scale_rows * n * 4));
+        std::int64_t col = 0;
+        for (const auto* p : parts) {
+            if (p->codes->size_bytes != static_cast<std::size_t>(code_rows * p->n) ||
+                p->scales->size_bytes != static_cast<std::size_t>(scale_rows * p->n * 4))
+                throw std::invalid_argument("HipLlamaDecoder: packed part has the wrong size for its quantization");
+            check(vm_hip_memcpy_2d_d2d(dst.codes.as<std::uint8_t>() + col, static_cast<std::size_t>(n), p->codes->data,
+                                       static_cast<std::size_t>(p->n), static_cast<std::size_t>(p->n),
+                                       static_cast<std::size_t>(code_rows), stream),
+                  "assemble codes");
+            check(vm_hip_memcpy_2d_d2d(dst.scales.as<float>() + col, static_cast<std::size_t>(n * 4), p->scales->data,
+                                       static_cast<std::size_t>(p->n * 4), static_cast<std::size_t>(p->n * 4),
+                                       static_cast<std::size_t>(scale_rows), stream),
+                  "assemble scales");
+            col += p->n;
+        }
+    }
+
     void qmm(const float* a, const Packed& w, float* c, std::int64_t rows) {
         check(vm_hip_qmm_f32(a, static_cast<const std::int8_t*>(w.codes.p), w.scales.as<float>(), c, rows, w.k, w.n,
                              qt, qt == VM_HIP_QUANT_INT4 ? block : 0, stream),
@@ -282,11 +321,9 @@ struct HipLlamaDecoder::Impl {
     }
 };
 
-HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_type, int block_size,
-                                 std::size_t max_seq)
-    : _impl(std::make_unique<Impl>()), _max_seq(max_seq) {
-    auto& m = *_impl;
-    m.cfg = weights.config();
+void HipLlamaDecoder::Impl::setup(const Config& config, QuantType quant_type, int block_size, std::size_t max_seq_len) {
+    auto& m = *this;
+    m.cfg = config;
     const Config& c = m.cfg;
     if (quant_type == QuantType::None) throw std::invalid_argument("HipLlamaDecoder: weights must be quantized");
     m.qt = quant_type == QuantType::Int4 ? VM_HIP_QUANT_INT4 : VM_HIP_QUANT_INT8;
@@ -301,32 +338,19 @@ HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_
     m.inter = static_cast<std::int64_t>(c.intermediate_size);
     m.vocab = static_cast<std::int64_t>(c.vocab_size);
     m.qkv_n = (m.H + 2 * m.Hk) * m.D;
-    m.max_seq = max_seq;
-    if (max_seq == 0 || max_seq > (1u << 20)) throw std::invalid_argument("HipLlamaDecoder: max_seq out of range");
+    m.max_seq = max_seq_len;
+    if (max_seq_len == 0 || max_seq_len > (1u << 20)) throw std::invalid_argument("HipLlamaDecoder: max_seq out of range");
     if (m.D != 64 && m.D != 128) throw std::invalid_argument("HipLlamaDecoder: head_dim must be 64 or 128");
     if (m.H / m.Hk > 16) throw std::invalid_argument("HipLlamaDecoder: at most 16 query heads per KV head");
     check(vm_hip_stream_create(&m.stream), "stream");
     check(vm_hip_event_create(&m.ev0), "event");
     check(vm_hip_event_create(&m.ev1), "event");
+}
 
-    using W = LlamaWeight;
-    m.embed = weights.storage(W::Embed);
-    m.final_norm = weights.storage(W::FinalNorm);
-    m.qkv.resize(c.num_layers);
-    m.o.resize(c.num_layers);
-    m.gate_up.resize(c.num_layers);
-    m.down.resize(c.num_layers);
-    for (std::size_t l = 0; l < c.num_layers; ++l) {
-        m.attn_norm.push_back(weights.storage(W::AttnNorm, l));
-        m.ffn_norm.push_back(weights.storage(W::FfnNorm, l));
-        m.pack_fused(m.qkv[l], {weights.storage(W::Wq, l), weights.storage(W::Wk, l), weights.storage(W::Wv, l)},
-                     m.hidden);
-        m.pack(m.o[l], static_cast<const float*>(weights.storage(W::Wo, l)->data), m.hidden, m.hidden);
-        m.pack_fused(m.gate_up[l], {weights.storage(W::Gate, l), weights.storage(W::Up, l)}, m.hidden);
-        m.pack(m.down[l], static_cast<const float*>(weights.storage(W::Down, l)->data), m.inter, m.hidden);
-    }
-    m.pack(m.lm_head, static_cast<const float*>(weights.storage(W::LmHead)->data), m.hidden, m.vocab);
-
+void HipLlamaDecoder::Impl::allocate() {
+    auto& m = *this;
+    const Config& c = m.cfg;
+    const std::size_t max_seq = m.max_seq;
     const std::size_t kv = c.num_layers * m.Hk * max_seq * m.D * 4;
     m.kcache = DevBuf(kv);
     m.vcache = DevBuf(kv);
@@ -374,6 +398,58 @@ HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_
         m.lm_sl = DevBuf(static_cast<std::size_t>(m.s_lm * m.vocab * 4));
     }
     check(vm_hip_stream_synchronize(m.stream), "setup");
+}
+
+HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_type, int block_size,
+                                 std::size_t max_seq)
+    : _impl(std::make_unique<Impl>()), _max_seq(max_seq) {
+    auto& m = *_impl;
+    m.setup(weights.config(), quant_type, block_size, max_seq);
+    const Config& c = m.cfg;
+    using W = LlamaWeight;
+    m.embed = weights.storage(W::Embed);
+    m.final_norm = weights.storage(W::FinalNorm);
+    m.qkv.resize(c.num_layers);
+    m.o.resize(c.num_layers);
+    m.gate_up.resize(c.num_layers);
+    m.down.resize(c.num_layers);
+    for (std::size_t l = 0; l < c.num_layers; ++l) {
+        m.attn_norm.push_back(weights.storage(W::AttnNorm, l));
+        m.ffn_norm.push_back(weights.storage(W::FfnNorm, l));
+        m.pack_fused(m.qkv[l], {weights.storage(W::Wq, l), weights.storage(W::Wk, l), weights.storage(W::Wv, l)},
+                     m.hidden);
+        m.pack(m.o[l], static_cast<const float*>(weights.storage(W::Wo, l)->data), m.hidden, m.hidden);
+        m.pack_fused(m.gate_up[l], {weights.storage(W::Gate, l), weights.storage(W::Up, l)}, m.hidden);
+        m.pack(m.down[l], static_cast<const float*>(weights.storage(W::Down, l)->data), m.inter, m.hidden);
+    }
+    m.pack(m.lm_head, static_cast<const float*>(weights.storage(W::LmHead)->data), m.hidden, m.vocab);
+
+    m.allocate();
+}
+
+HipLlamaDecoder::HipLlamaDecoder(const PackedLlamaWeights& packed, std::size_t max_seq)
+    : _impl(std::make_unique<Impl>()), _max_seq(max_seq) {
+    auto& m = *_impl;
+    m.setup(packed.config(), packed.quant_type(), packed.block_size(), max_seq);
+    const Config& c = m.cfg;
+    using W = LlamaWeight;
+    m.embed = packed.dense(W::Embed);
+    m.final_norm = packed.dense(W::FinalNorm);
+    m.qkv.resize(c.num_layers);
+    m.o.resize(c.num_layers);
+    m.gate_up.resize(c.num_layers);
+    m.down.resize(c.num_layers);
+    for (std::size_t l = 0; l < c.num_layers; ++l) {
+        m.attn_norm.push_back(packed.dense(W::AttnNorm, l));
+        m.ffn_norm.push_back(packed.dense(W::FfnNorm, l));
+        m.assemble(m.qkv[l], {&packed.linear(W::Wq, l), &packed.linear(W::Wk, l), &packed.linear(W::Wv, l)});
+        m.assemble(m.o[l], {&packed.linear(W::Wo, l)});
+        m.assemble(m.gate_up[l], {&packed.linear(W::Gate, l), &packed.linear(W::Up, l)});
+        m.assemble(m.down[l], {&packed.linear(W::Down, l)});
+    }
+    m.assemble(m.lm_head, {&packed.linear(W::LmHead)});
+    check(vm_hip_stream_synchronize(m.stream), "assemble");
+    m.allocate();
 }
 
 HipLlamaDecoder::~HipLlamaDecoder() {

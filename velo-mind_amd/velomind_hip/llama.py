@@ -42,8 +42,17 @@ def lib() -> ctypes.CDLL:
         L.vm_llama_prefill.argtypes = [p, p, c_int64, p]
         L.vm_llama_forward_step.argtypes = [p, c_int32, c_int64, p]
         L.vm_llama_generate.argtypes = [p, p, c_int64, c_int64, c_int, p, p]
+        L.vm_llama_pack.argtypes = [p, c_int, c_int, POINTER(c_void_p)]
+        L.vm_llama_packed_save.argtypes = [p, c_char_p]
+        L.vm_llama_packed_config.argtypes = [c_char_p, POINTER(LlamaConfigC)]
+        L.vm_llama_packed_load.argtypes = [c_char_p, POINTER(LlamaConfigC), POINTER(c_void_p)]
+        L.vm_llama_packed_destroy.argtypes = [p]
+        L.vm_llama_packed_destroy.restype = None
+        L.vm_llama_session_create_packed.argtypes = [p, c_int64, POINTER(c_void_p)]
         for name in ("vm_llama_weights_create", "vm_llama_weights_set", "vm_llama_weights_fill_synthetic",
-                     "vm_llama_session_create", "vm_llama_prefill", "vm_llama_forward_step", "vm_llama_generate"):
+                     "vm_llama_session_create", "vm_llama_prefill", "vm_llama_forward_step", "vm_llama_generate",
+                     "vm_llama_pack", "vm_llama_packed_save", "vm_llama_packed_config", "vm_llama_packed_load",
+                     "vm_llama_session_create_packed"):
             getattr(L, name).restype = c_int
         _lib = L
     return _lib
@@ -59,8 +68,7 @@ class Weights:
 
     def __init__(self, cfg):
         self.cfg = cfg
-        c = LlamaConfigC(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size, cfg.num_layers, cfg.num_heads,
-                         cfg.num_kv_heads, cfg.rms_norm_eps, cfg.rope_theta)
+        c = _config_c(cfg)
         self.handle = c_void_p(None)
         _check(lib().vm_llama_weights_create(byref(c), byref(self.handle)))
 
@@ -98,6 +106,54 @@ class Weights:
             pass
 
 
+def _config_c(cfg) -> LlamaConfigC:
+    return LlamaConfigC(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size, cfg.num_layers, cfg.num_heads,
+                        cfg.num_kv_heads, cfg.rms_norm_eps, cfg.rope_theta)
+
+
+class PackedWeights:
+    """Every linear packed once on the GPU (quant.cpp layout), savable to and
+    loadable from a safetensors file of I8 codes and F32 scales."""
+
+    def __init__(self, cfg, handle: c_void_p):
+        self.cfg = cfg
+        self.handle = handle
+
+    @classmethod
+    def pack(cls, weights: Weights, quant_type: int, block_size: int = 0) -> "PackedWeights":
+        h = c_void_p(None)
+        _check(lib().vm_llama_pack(weights.handle, quant_type, block_size, byref(h)))
+        return cls(weights.cfg, h)
+
+    @staticmethod
+    def file_config(path: str) -> LlamaConfigC:
+        c = LlamaConfigC()
+        _check(lib().vm_llama_packed_config(str(path).encode(), byref(c)))
+        return c
+
+    @classmethod
+    def load(cls, path: str, cfg=None) -> "PackedWeights":
+        """Loads a packed file; `cfg` defaults to the config the file records."""
+        c = _config_c(cfg) if cfg is not None else cls.file_config(path)
+        h = c_void_p(None)
+        _check(lib().vm_llama_packed_load(str(path).encode(), byref(c), byref(h)))
+        return cls(cfg if cfg is not None else c, h)
+
+    def save(self, path: str) -> None:
+        _check(lib().vm_llama_packed_save(self.handle, str(path).encode()))
+
+    def close(self) -> None:
+        if self.handle.value:
+            lib().vm_llama_packed_destroy(self.handle)
+            self.handle = c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Session:
     def __init__(self, weights: Weights, engine: int, quant_type: int, block_size: int = 0,
                  fused_attention: bool = False, max_seq: int = 0):
@@ -106,6 +162,16 @@ class Session:
         self.handle = c_void_p(None)
         _check(lib().vm_llama_session_create(weights.handle, engine, quant_type, block_size, int(fused_attention),
                                              max_seq, byref(self.handle)))
+
+    @classmethod
+    def from_packed(cls, packed: PackedWeights, max_seq: int) -> "Session":
+        """A resident-decoder session over pre-packed weights (no packing)."""
+        s = cls.__new__(cls)
+        s.weights = packed
+        s.vocab = int(packed.cfg.vocab_size)
+        s.handle = c_void_p(None)
+        _check(lib().vm_llama_session_create_packed(packed.handle, max_seq, byref(s.handle)))
+        return s
 
     def prefill(self, tokens) -> np.ndarray:
         t = np.ascontiguousarray(tokens, np.int32)
