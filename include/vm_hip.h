@@ -421,6 +421,29 @@ int vm_hip_attention_decode_slices_f32(const float* qkv, int64_t qkv_slices, con
 int vm_hip_slices_sum_scaled_f32(const float* in, int64_t slices, int64_t n, const float* ss,
                                  int64_t ss_count, float ss_dim, float eps, float* out, void* stream);
 
+/* Up to four device regions (each below 2 GiB) that a launch reads into the
+ * memory-side cache (MI355X Infinity Cache, 256 MB) with extra workgroups,
+ * so that the launches after it find those bytes there instead of in HBM.
+ * The loaded data is discarded; results do not depend on it. */
+#define VM_HIP_PREFETCH_MAX 4
+typedef struct vm_hip_prefetch {
+    const void* ptr[VM_HIP_PREFETCH_MAX];
+    uint64_t bytes[VM_HIP_PREFETCH_MAX];
+    int count;
+} vm_hip_prefetch;
+
+/* vm_hip_attention_decode_slices_f32 whose launch also prefetches
+ * `prefetch` (null or count 0: none) with otherwise idle CUs: the resident
+ * decoder passes the next projections' weights. No counterpart in the
+ * reference (a decode-step building block). */
+int vm_hip_attention_decode_slices_prefetch_f32(const float* qkv, int64_t qkv_slices, const float* ss,
+                                                int64_t ss_count, float ss_dim, float eps,
+                                                const float* cos_table, const float* sin_table,
+                                                const int32_t* pos, float* k_cache, float* v_cache,
+                                                float* partials, int64_t heads, int64_t kv_heads,
+                                                int64_t head_dim, int64_t max_seq, float scale,
+                                                const vm_hip_prefetch* prefetch, void* stream);
+
 /* Asynchronous 2-D device copy: `rows` rows of `width` bytes from src
  * (row pitch spitch) to dst (row pitch dpitch).  Used to assemble fused
  * weight matrices column block by column block. */

@@ -309,6 +309,60 @@ def test_attention_decode_slices_and_merge_source(hip, heads, kv_heads, d, max_s
     _close(out.sum(axis=0, dtype=np.float64), O.qmm(ctx, qo, so, hidden, O.QUANT_INT4, 32)[0], 1e-4, "o projection")
 
 
+def test_attention_decode_prefetch_workgroups_change_nothing(hip):
+    """The prefetching variant (extra workgroups that read other buffers
+    into the Infinity Cache) writes the same caches and partials, bit for
+    bit, as the plain launch; bad prefetch lists are refused."""
+    import ctypes
+    lib = hip.open_library()
+    heads, kv_heads, d, max_seq, p, slices = 32, 4, 64, 300, 250, 16
+    width = (heads + 2 * kv_heads) * d
+    qkv = _normal((slices, width), 41)
+    ss = np.abs(_normal(5, 42, 50.0)) + 1.0
+    cos, sin = L.rope_cache(max_seq, d, 10000.0)
+    kc0, vc0 = _normal((kv_heads, max_seq, d), 43), _normal((kv_heads, max_seq, d), 44)
+    ch, chs = ctypes.c_int(0), ctypes.c_int(0)
+    hip.check(lib.vm_hip_attention_decode_chunks(d, max_seq, ctypes.byref(ch), ctypes.byref(chs)))
+    dqkv, dss, dc, dsn = _dev(hip, qkv), _dev(hip, ss), _dev(hip, cos), _dev(hip, sin)
+    dpos = _dev(hip, np.array([p], np.int32), np.int32)
+    regions = [_dev(hip, _normal(n, 45 + i)) for i, n in enumerate((3 << 18, 12345, 1 << 20))]
+    pf = hip.Prefetch()
+    for i, r in enumerate(regions):
+        pf.ptr[i] = r.addr
+        pf.bytes[i] = r.nbytes - (5 if i == 1 else 0)   # a ragged region
+    pf.count = len(regions)
+    outs = []
+    print("case attention_decode_slices prefetch", flush=True)
+    for use_pf in (False, True):
+        dk, dv = _dev(hip, kc0), _dev(hip, vc0)
+        dpart = hip.DeviceBuffer(heads * chs.value * (d + 4) * 4)
+        args = (dqkv.ptr, slices, dss.ptr, ss.size, float(2048), 1e-5, dc.ptr, dsn.ptr, dpos.ptr, dk.ptr, dv.ptr,
+                dpart.ptr, heads, kv_heads, d, max_seq, 1.0)
+        if use_pf:
+            hip.check(lib.vm_hip_attention_decode_slices_prefetch_f32(*args, ctypes.byref(pf), None))
+        else:
+            hip.check(lib.vm_hip_attention_decode_slices_f32(*args, None))
+        hip.synchronize()
+        n_rec = heads * chs.value * (d + 4)
+        outs.append((dk.download(np.float32, kc0.shape), dv.download(np.float32, vc0.shape),
+                     dpart.download(np.float32, (n_rec,))))
+    (k0, v0, r0), (k1, v1, r1) = outs
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+    # records of chunks past the position are never written: compare the written ones
+    rec = r0.reshape(heads, chs.value, d + 4)[:, :(p + ch.value) // ch.value]
+    assert np.array_equal(rec, r1.reshape(heads, chs.value, d + 4)[:, :(p + ch.value) // ch.value])
+    bad = hip.Prefetch()
+    bad.count = 5
+    dk, dv = _dev(hip, kc0), _dev(hip, vc0)
+    dpart = hip.DeviceBuffer(heads * chs.value * (d + 4) * 4)
+    args = (dqkv.ptr, slices, dss.ptr, ss.size, float(2048), 1e-5, dc.ptr, dsn.ptr, dpos.ptr, dk.ptr, dv.ptr,
+            dpart.ptr, heads, kv_heads, d, max_seq, 1.0)
+    assert lib.vm_hip_attention_decode_slices_prefetch_f32(*args, ctypes.byref(bad), None) != 0
+    bad.count = 1
+    bad.bytes[0] = 64   # non-empty region without a pointer
+    assert lib.vm_hip_attention_decode_slices_prefetch_f32(*args, ctypes.byref(bad), None) != 0
+
+
 def test_swiglu_source_applies_the_norm_scale_and_scaled_slice_sum(hip):
     import ctypes
     k, n, sl_in = 512, 256, 4

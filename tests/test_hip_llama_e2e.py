@@ -145,6 +145,26 @@ def test_resident_generate_matches_oracle_greedy(llama, qt, block):
     assert list(toks_graph) == ref_tokens
 
 
+def test_resident_decode_prefetch_changes_no_result(llama, monkeypatch):
+    """The decode step's prefetch of the next weights into the Infinity
+    Cache (on unless VELOMIND_DECODE_PREFETCH=0) leaves logits and greedy
+    tokens bit-identical."""
+    cfg, w = _gqa(seed=9)
+    dev = llama.Weights.from_oracle(cfg, w)
+    print("case resident prefetch on/off", flush=True)
+    res = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("VELOMIND_DECODE_PREFETCH", flag)
+        s = llama.Session(dev, llama.ENGINE_RESIDENT, 2, 32, max_seq=40)
+        logits = [s.prefill([3, 1, 4])] + [s.forward_step(t, pos) for pos, t in ((3, 1), (4, 5))]
+        toks, _ = s.generate([2, 7, 1], 8, use_hip_graph=True)
+        res.append((logits, list(toks)))
+        s.close()
+    for a, b in zip(res[0][0], res[1][0]):
+        assert np.array_equal(a, b)
+    assert res[0][1] == res[1][1]
+
+
 def test_graph_and_resident_engines_agree_on_gqa_int4(llama):
     cfg, w = _gqa(seed=3)
     dev = llama.Weights.from_oracle(cfg, w)

@@ -16,6 +16,7 @@
 //    the GEMV.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
@@ -505,6 +506,43 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
     if (tid == 0) __hip_atomic_store(&counters[hk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- Prefetch into the memory-side cache.  A decode step is a chain of
+// latency-bound launches that leave many CUs idle; extra workgroups of one
+// launch read (and discard) the weights of the launches that follow, which
+// then find them in the 256 MB Infinity Cache instead of HBM.  Workgroup q
+// of n reads bytes [q*slab, (q+1)*slab) of the concatenated regions with
+// 16-byte loads, kBatch in flight per thread.  The loaded words feed a
+// store that never happens (pf.count is never negative) so that the loads
+// are kept.
+__device__ void prefetch_slab(const vm_hip_prefetch& pf, int q, int n, float* sink) {
+    constexpr int kBatch = 8;
+    uint64_t total = 0;
+    for (int r = 0; r < pf.count; ++r) total += pf.bytes[r];
+    const uint64_t slab = ((total + n - 1) / n + 15) & ~uint64_t(15);
+    const uint64_t lo = static_cast<uint64_t>(q) * slab, hi = min(total, lo + slab);
+    uint32_t acc = 0;
+    uint64_t base = 0;
+    for (int r = 0; r < pf.count; ++r) {
+        const uint64_t b0 = max(lo, base), b1 = min(hi, base + pf.bytes[r]);
+        if (b0 < b1) {
+            const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(pf.ptr[r], static_cast<uint32_t>(pf.bytes[r]));
+            const uint32_t e = static_cast<uint32_t>(b1 - base);
+            for (uint32_t o = static_cast<uint32_t>(b0 - base) + threadIdx.x * 16u; o < e; o += kT * 16u * kBatch) {
+                u32x4 v[kBatch];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const uint32_t off = o + static_cast<uint32_t>(u) * kT * 16u;
+                    v[u] = buffer_load16(rs, off < e ? off : 0xfffffff0u);
+                }
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+            }
+        }
+        base += pf.bytes[r];
+    }
+    if (pf.count < 0 && acc == 0x9E3779B9u) sink[0] = 0.0f;
+}
+
 // ---- Decode attention fused with its producer's reduction and RoPE: one
 // query row per head at position p = *pos, keys 0..p, the projection
 // arriving as split-K partial slices [qkv_slices][(H + 2 Hkv) D] whose
@@ -522,12 +560,17 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
 //      stores the chunk's record {m, l, 0, 0, o[D]} with plain stores at
 //      part[((hk * G + g) * chunks + chunk) * (D + 4)].
 // The merge over chunks is left to the consumer (VM_HIP_GEMV_SRC_ATTN).
+// Workgroups past chunks * kv_heads are prefetchers (see prefetch_slab).
 template <int D, int CHUNK>
 __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
     const float* __restrict__ qkv, int qkv_slices, const float* __restrict__ ss, int ss_count, float ss_dim,
     float eps, const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int32_t* __restrict__ pos,
     float* __restrict__ k_cache, float* __restrict__ v_cache, float* __restrict__ part, int heads, int kv_heads,
-    int max_seq, float scale) {
+    int max_seq, float scale, int chunks, vm_hip_prefetch pf, int pf_wgs) {
+    if (static_cast<int>(blockIdx.x) >= chunks * kv_heads) {
+        prefetch_slab(pf, static_cast<int>(blockIdx.x) - chunks * kv_heads, pf_wgs, part);
+        return;
+    }
     constexpr int kMaxG = 16;
     constexpr int D4 = D / 4;
     constexpr int HALF = D / 2;
@@ -547,28 +590,25 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
     __shared__ float sp[kMaxG][CHUNK];
     __shared__ float sm[kMaxG], sl[kMaxG];
 
-    const int chunk = blockIdx.x;
-    const int hk = blockIdx.y;
+    const int chunk = static_cast<int>(blockIdx.x) % chunks;
+    const int hk = static_cast<int>(blockIdx.x) / chunks;
     const int G = heads / kv_heads;
     const int tid = threadIdx.x;
-    const int n_keys = min(pos[0] + 1, max_seq);
-    const int nc = (n_keys + CHUNK - 1) / CHUNK;
-    if (chunk >= nc) return;
-    const int p = n_keys - 1;
     const int k0 = chunk * CHUNK;
-    const int nk = min(CHUNK, n_keys - k0);
-    const bool last = chunk == nc - 1;
     const int width = (heads + 2 * kv_heads) * D;
 
-    // 1. Loads, the small ones first (vector memory counters retire in
-    //    issue order): the RoPE tables at p for this thread's pair index,
-    //    the slice sums (tasks [0, G*D4) query float4s, then in the last
-    //    chunk D4 key and D4 value float4s), then the K/V chunk from the
-    //    cache (row p of the last chunk is replaced below).
-    const int jr_pair = tid % HALF;   // pair index of every RoPE task of this thread (kT % HALF == 0)
-    const float rc = cos_t[static_cast<int64_t>(p) * HALF + jr_pair];
-    const float rs = sin_t[static_cast<int64_t>(p) * HALF + jr_pair];
-    const int tasks1 = G * D4 + (last ? 2 * D4 : 0);
+    // 1. Loads.  Those that do not depend on the position are issued before
+    //    it is known (its scalar load is a memory round trip of its own):
+    //    the slice sums (tasks [0, G*D4) query float4s, then D4 key and D4
+    //    value float4s, used by the last chunk only) and the chunk's K/V
+    //    rows from the cache, all CHUNK of them within max_seq (rows past
+    //    the position are masked below; row p of the last chunk is
+    //    replaced).  Small loads go first: vector memory counters retire in
+    //    issue order, so waiting for the slices does not wait for K/V.
+    //    Workgroups past the last chunk issue the same loads and skip all
+    //    stores (no early return, which would let the loads be moved after
+    //    the position test).
+    const int tasks1 = G * D4 + 2 * D4;
     constexpr int kTasksMax = (kMaxG * D4 + 2 * D4 + kT - 1) / kT;
     const __amdgpu_buffer_rsrc_t qrs = buffer_rsrc(qkv, static_cast<uint32_t>(qkv_slices * width) * 4u);
     auto task_col = [&](int t, float*& dst) {
@@ -594,7 +634,7 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
             l0[i][e] = buffer_load16(qrs, (t < tasks1 && e < qkv_slices)
                                               ? static_cast<uint32_t>(e * width + col) * 4u : 0xfffffff0u);
     }
-    const uint32_t kv_bytes = static_cast<uint32_t>(nk * D) * 4u;
+    const uint32_t kv_bytes = static_cast<uint32_t>(max(0, min(CHUNK, max_seq - k0)) * D) * 4u;
     const int64_t kv_off = (static_cast<int64_t>(hk) * max_seq + k0) * D;
     u32x4 tk[KV], tv[KV];
     {
@@ -606,6 +646,16 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
             tv[u] = buffer_load16(vrs, (tid + u * kT) * 16u);
         }
     }
+    // The position: keys 0..p; chunks at or past nc are inactive.
+    const int n_keys = min(pos[0] + 1, max_seq);
+    const int nc = (n_keys + CHUNK - 1) / CHUNK;
+    const bool active = chunk < nc;
+    const int p = n_keys - 1;
+    const int nk = active ? min(CHUNK, n_keys - k0) : 0;
+    const bool last = chunk == nc - 1;
+    const int jr_pair = tid % HALF;   // pair index of every RoPE task of this thread (kT % HALF == 0)
+    const float rc = cos_t[static_cast<int64_t>(p) * HALF + jr_pair];
+    const float rs = sin_t[static_cast<int64_t>(p) * HALF + jr_pair];
     {
         float iv = 1.0f;
         if (ss && ss_count > 0) {
@@ -745,9 +795,11 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
             acc.z = fmaf(pr, v.z, acc.z);
             acc.w = fmaf(pr, v.w, acc.w);
         }
-        float* rec = part + ((static_cast<int64_t>(hk) * G + g) * gridDim.x + chunk) * kPart;
-        *reinterpret_cast<float4*>(rec + 4 + 4 * c4) = acc;
-        if (c4 == 0) *reinterpret_cast<float4*>(rec) = make_float4(sm[g], sl[g], 0.0f, 0.0f);
+        if (active) {
+            float* rec = part + ((static_cast<int64_t>(hk) * G + g) * chunks + chunk) * kPart;
+            *reinterpret_cast<float4*>(rec + 4 + 4 * c4) = acc;
+            if (c4 == 0) *reinterpret_cast<float4*>(rec) = make_float4(sm[g], sl[g], 0.0f, 0.0f);
+        }
     }
 }
 
@@ -1051,6 +1103,25 @@ int grid_for(int64_t work) {
     return static_cast<int>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
 }
 
+// Validates a prefetch list and sizes its workgroups: about 96 KB each
+// (two dozen 16-byte loads per thread), at most 256.
+int prefetch_plan(const vm_hip_prefetch* in, vm_hip_prefetch* out, int* wgs) {
+    *out = vm_hip_prefetch{};
+    *wgs = 0;
+    if (!in || in->count == 0) return 0;
+    if (in->count < 0 || in->count > VM_HIP_PREFETCH_MAX) return fail_inval("prefetch: count must be in [0, 4]");
+    uint64_t total = 0;
+    for (int r = 0; r < in->count; ++r) {
+        if (in->bytes[r] >= (uint64_t{1} << 31) || (in->bytes[r] > 0 && !in->ptr[r]))
+            return fail_inval("prefetch: each region must be non-null and below 2 GiB");
+        total += in->bytes[r];
+    }
+    *out = *in;
+    constexpr uint64_t kSlab = 96 * 1024;
+    *wgs = static_cast<int>(std::min<uint64_t>(256, (total + kSlab - 1) / kSlab));
+    return 0;
+}
+
 }  // namespace
 }  // namespace vmhip
 
@@ -1273,6 +1344,17 @@ int vm_hip_attention_decode_slices_f32(const float* qkv, int64_t qkv_slices, con
                                        const int32_t* pos, float* k_cache, float* v_cache, float* partials,
                                        int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t max_seq,
                                        float scale, void* stream) {
+    return vm_hip_attention_decode_slices_prefetch_f32(qkv, qkv_slices, ss, ss_count, ss_dim, eps, cos_table,
+                                                       sin_table, pos, k_cache, v_cache, partials, heads, kv_heads,
+                                                       head_dim, max_seq, scale, nullptr, stream);
+}
+
+int vm_hip_attention_decode_slices_prefetch_f32(const float* qkv, int64_t qkv_slices, const float* ss,
+                                                int64_t ss_count, float ss_dim, float eps, const float* cos_table,
+                                                const float* sin_table, const int32_t* pos, float* k_cache,
+                                                float* v_cache, float* partials, int64_t heads, int64_t kv_heads,
+                                                int64_t head_dim, int64_t max_seq, float scale,
+                                                const vm_hip_prefetch* prefetch, void* stream) {
     clear_error();
     int chunk = 0, chunks = 0;
     VM_TRY(vm_hip_attention_decode_chunks(head_dim, max_seq, &chunk, &chunks));
@@ -1288,17 +1370,24 @@ int vm_hip_attention_decode_slices_f32(const float* qkv, int64_t qkv_slices, con
     if (max_seq * head_dim > (int64_t{1} << 28) || qkv_slices * (heads + 2 * kv_heads) * head_dim * 4 > 0x7fffffffLL ||
         heads > 65535 || kv_heads > 65535)
         return fail_inval("attention_decode_slices: too large");
+    vm_hip_prefetch pf{};
+    int pf_wgs = 0;
+    VM_TRY(prefetch_plan(prefetch, &pf, &pf_wgs));
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
-    const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(kv_heads));
+    const int64_t wgs = static_cast<int64_t>(chunks) * kv_heads + pf_wgs;
+    if (wgs > 0x7fffffff) return fail_inval("attention_decode_slices: too large");
+    const dim3 grid(static_cast<unsigned>(wgs));
     const int sl = static_cast<int>(qkv_slices), sc_n = static_cast<int>(ss_count);
     if (head_dim == 64)
         hipLaunchKernelGGL((attention_decode_slices_kernel<64, 32>), grid, dim3(kT), 0, S(stream), qkv, sl, ss, sc_n,
                            ss_dim, eps, cos_table, sin_table, pos, k_cache, v_cache, partials,
-                           static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(max_seq), sc);
+                           static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(max_seq), sc, chunks,
+                           pf, pf_wgs);
     else
         hipLaunchKernelGGL((attention_decode_slices_kernel<128, 32>), grid, dim3(kT), 0, S(stream), qkv, sl, ss, sc_n,
                            ss_dim, eps, cos_table, sin_table, pos, k_cache, v_cache, partials,
-                           static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(max_seq), sc);
+                           static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(max_seq), sc, chunks,
+                           pf, pf_wgs);
     return check_launch("attention_decode_slices", S(stream));
 }
 

@@ -39,6 +39,11 @@ class GemvSrc(ctypes.Structure):
                 ("chunks", c_int), ("max_seq", c_int)]
 
 
+class Prefetch(ctypes.Structure):
+    """vm_hip_prefetch (include/vm_hip.h)."""
+    _fields_ = [("ptr", c_void_p * 4), ("bytes", ctypes.c_uint64 * 4), ("count", c_int)]
+
+
 def _declare(L: ctypes.CDLL) -> None:
     p = c_void_p
     sig = {
@@ -103,6 +108,9 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_attention_decode_slices_f32": ([p, c_int64, p, c_int64, c_float, c_float, p, p, p, p, p, p,
                                                 c_int64, c_int64, c_int64, c_int64, c_float, p], c_int),
         "vm_hip_slices_sum_scaled_f32": ([p, c_int64, c_int64, p, c_int64, c_float, c_float, p, p], c_int),
+        "vm_hip_attention_decode_slices_prefetch_f32": ([p, c_int64, p, c_int64, c_float, c_float, p, p, p, p, p, p,
+                                                         c_int64, c_int64, c_int64, c_int64, c_float,
+                                                         POINTER(Prefetch), p], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -128,7 +136,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_gemv_slices_count", "vm_hip_qmm_gemv_slices_f32", "vm_hip_add_rmsnorm_slices_f32",
             "vm_hip_rope_kv_append_slices_f32", "vm_hip_argmax_slices_f32", "vm_hip_slices_sum_f32",
             "vm_hip_qmm_gemv_slices_src_f32", "vm_hip_attention_decode_chunks", "vm_hip_attention_decode_slices_f32",
-            "vm_hip_slices_sum_scaled_f32"]
+            "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32"]
 
 
 def open_library() -> ctypes.CDLL:
