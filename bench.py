@@ -21,6 +21,10 @@ two events on the launch stream.  ``cpu_baseline``
 times the oracle's scalar INT4 path (src/cpu/ops/quantized_matmul.cpp:48-141)
 on one pinned core over a bounded sample of the same step.
 
+``gemm`` is BASELINE config 3, the MFMA path (M in {16, 128, 512}, K 2048,
+N 5632, INT8 and INT4): TFLOP/s as a fraction of the dense fp16 MFMA peak
+(2.5 PFLOP/s) and algorithmic GB/s.
+
 ``e2e`` adds the metric's second half, TinyLlama INT4 decode tokens/s
 (512-token prompt, 256 greedy tokens) and SmolLM2-360M
 INT8 (config 4: 128 + 128), on the resident HIP decoder with synthetic
@@ -287,6 +291,81 @@ def e2e_bench(name: str, use_graph: bool = True) -> dict:
     return out
 
 
+GEMM_K, GEMM_N = 2048, 5632
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def gemm_setup(H):
+    """BASELINE config 3 operands: W [2048, 5632] N(0, 0.02) packed on the
+    GPU as INT8 (per column) and INT4 (block 32); A [512, 2048] N(0, 1)."""
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((GEMM_K, GEMM_N), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    dw = H.DeviceBuffer.from_array(w)
+    packs = {}
+    for qt in (H.QUANT_INT8, H.QUANT_INT4):
+        if qt == H.QUANT_INT4:
+            p = H.DeviceBuffer(GEMM_K // 2 * GEMM_N)
+            s = H.DeviceBuffer(GEMM_K // BLOCK * GEMM_N * 4)
+            H.pack_int4(dw.addr, p.addr, s.addr, GEMM_K, GEMM_N, BLOCK)
+            packs[qt] = (p, s, BLOCK)
+        else:
+            p = H.DeviceBuffer(GEMM_K * GEMM_N)
+            s = H.DeviceBuffer(GEMM_N * 4)
+            H.pack_int8(dw.addr, p.addr, s.addr, GEMM_K, GEMM_N)
+            packs[qt] = (p, s, 0)
+    H.synchronize()
+    dw.close()
+    a = H.DeviceBuffer.from_array(rng.standard_normal((512, GEMM_K), dtype=np.float32))
+    c = H.DeviceBuffer(512 * GEMM_N * 4)
+    return packs, a, c
+
+
+def gemm_bench(H, stream, reps: int = 10) -> dict:
+    """Config 3, the MFMA path: M in {16, 128, 512} x INT8 / INT4, each a
+    HIP graph of 20 launches replayed `reps` times between events.  FLOPs
+    2*M*K*N; algorithmic bytes codes + scales + fp32 A + fp32 C."""
+    packs, a, c = gemm_setup(H)
+    out = {}
+    for m in (16, 128, 512):
+        for qt in (H.QUANT_INT8, H.QUANT_INT4):
+            p, s, blk = packs[qt]
+
+            def launch():
+                H.qmm_f32(a.addr, p.addr, s.addr, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
+
+            launch()
+            stream.synchronize()
+            g = H.Graph(stream)
+            g.begin()
+            for _ in range(20):
+                launch()
+            g.end()
+            g.launch()
+            stream.synchronize()
+            e0, e1 = H.Event(), H.Event()
+            e0.record(stream.handle)
+            for _ in range(reps):
+                g.launch()
+            e1.record(stream.handle)
+            e1.synchronize()
+            g.close()
+            us = e0.elapsed_ms(e1) * 1e3 / (20 * reps)
+            flops = 2.0 * m * GEMM_K * GEMM_N
+            codes = GEMM_K * GEMM_N if qt == H.QUANT_INT8 else GEMM_K // 2 * GEMM_N
+            scales = GEMM_N * 4 if qt == H.QUANT_INT8 else GEMM_K // BLOCK * GEMM_N * 4
+            nbytes = codes + scales + 4 * m * GEMM_K + 4 * m * GEMM_N
+            tf = flops / (us * 1e-6) / 1e12
+            out[f"M{m}_{'int8' if qt == H.QUANT_INT8 else 'int4'}"] = {
+                "us": round(us, 2), "TFLOP_s": round(tf, 1), "frac_of_mfma_f16_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    for p, s, _ in packs.values():
+        p.close()
+        s.close()
+    a.close()
+    c.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,6 +379,10 @@ def main() -> int:
     ap.add_argument("--e2e-only", action="store_true",
                     help="only the end-to-end legs, printed as one JSON line (profiling passes; with --no-graph "
                          "the decode steps launch eagerly so that rocprofv3 can trace them)")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg (config 3)")
+    ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg, printed as one JSON line")
+    ap.add_argument("--gemm-profile", default="",
+                    help="M,QT,REPS: only REPS eager launches of one config-3 GEMM (rocprofv3 counter passes)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (rocprofv3 counter calibration)")
     args = ap.parse_args()
@@ -319,6 +402,18 @@ def main() -> int:
             H.check(lib.vm_hip_memcpy_d2d(dst.ptr, src.ptr, 64 << 20, stream.handle))
         stream.synchronize()
         log("bench: calibration copies done (10 x 64 MiB)")
+        return 0
+    if args.gemm_profile:
+        m, qt, reps = (int(v) for v in args.gemm_profile.split(","))
+        packs, a, c = gemm_setup(H)
+        p, s, blk = packs[qt]
+        for _ in range(reps):
+            H.qmm_f32(a.addr, p.addr, s.addr, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
+        stream.synchronize()
+        log(f"bench: {reps} GEMM launches M={m} quant_type={qt} done")
+        return 0
+    if args.gemm_only:
+        print(json.dumps({"metric": METRIC, "gemm": gemm_bench(H, stream)}), flush=True)
         return 0
     if args.e2e_only:
         e2e = {}
@@ -401,6 +496,11 @@ def main() -> int:
             log(f"bench: {name}: prefill {e2e[name]['prefill_tokens_per_s']} tok/s, "
                 f"decode {e2e[name]['decode_tokens_per_s']} tok/s")
 
+    gemm = None
+    if not args.no_gemm and not args.only_shape:
+        log("bench: prefill GEMM (config 3)")
+        gemm = gemm_bench(H, stream)
+
     cpu = None
     if args.cpu_seconds > 0:
         log("bench: timing CPU baseline")
@@ -445,6 +545,7 @@ def main() -> int:
         },
         "per_shape": per_shape,
         "e2e": e2e,
+        "gemm": gemm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

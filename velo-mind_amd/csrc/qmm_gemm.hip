@@ -54,7 +54,10 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;         // K rows per pipeline step
 constexpr int kThreads = 256;   // four waves
-constexpr int kApad = 8;        // halves of padding per LDS row of A
+// LDS row padding (halves).  Measured on MI355X (M = 512, K = 2048, N =
+// 5632): A rows padded by 16 halves have 20% fewer bank conflicts than by
+// 8; B padding of 8, 16 or 32 makes no difference, none doubles the time.
+constexpr int kApad = 16;       // halves of padding per LDS row of A
 constexpr int kBpad = 16;       // halves of padding per LDS row of B
 constexpr int kMaxSplits = 16;
 
@@ -465,7 +468,8 @@ struct GemmConfig {
 // on MI355X over config-3 shapes (K = 2048, N = 5632, M = 16..512) and the
 // TinyLlama / SmolLM2 prefill projections (M = 512: N = 2048..11264, K =
 // 2048 and 5632; M = 128: K, N = 960..5120):
-//   M <= 128: 32 x 64 tiles (many small workgroups hide load latency best);
+//   M <= 128: 32 x 64 tiles (many small workgroups hide load latency best),
+//     64 x 64 for INT4 with M > 64;
 //     K splits (at least four 64-row steps each) until about two workgroups
 //     per CU, while the fp32 partials stay under a quarter of the code
 //     bytes -- or, with fewer than 128 tiles, while each split keeps at
@@ -483,7 +487,9 @@ GemmConfig choose_gemm(int kind, int m, int k, int n) {
     };
     int s = 1;
     if (m <= 128) {
-        cfg.bm = 32;
+        // INT4 with 64 < M <= 128: 64 x 64 tiles halve the nibble unpacking
+        // per MFMA (K = 2048, N = 5632, M = 128: 27.0 us vs 34.2 us).
+        cfg.bm = (kind == 2 && m > 64) ? 64 : 32;
         cfg.bn = 64;
         const long tiles = tiles_of(cfg.bm, cfg.bn);
         while (s * 2 <= 8 && tiles * s * 2 <= 512 &&
