@@ -29,7 +29,10 @@ def test_int4_kat_ties_and_nibbles(hip):
     assert packed[:, 0].tolist() == [0xF7, 0x13]
 
 
-@pytest.mark.parametrize("rows,cols", [(128, 256), (576, 1536), (33, 17), (1, 5), (7, 1)])
+@pytest.mark.parametrize("rows,cols", [(128, 256), (576, 1536), (33, 17), (1, 5), (7, 1),
+                                       # two-pass path: ragged row chunks, columns past the last
+                                       # full workgroup, a single chunk, many chunks
+                                       (1000, 1028), (64, 260), (4099, 2048), (97, 4096)])
 def test_int8_bit_exact(hip, rows, cols):
     w = ref_inputs.generate_random_weights(rows, cols, -1.5, 1.5)
     w[:, 0] = 0.0  # an all-zero column takes scale 1.0

@@ -10,6 +10,7 @@
 // reference's float->int8 cast of NaN/Inf is undefined).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "vm_internal.h"
@@ -48,6 +49,96 @@ __global__ __launch_bounds__(kColsPerWg * kRowGroups) void pack_int8_kernel(
         float v = roundf(w[r * cols + c] * inv);
         v = v < -127.0f ? -127.0f : (127.0f < v ? 127.0f : v);
         q[r * cols + c] = static_cast<int8_t>(v);
+    }
+}
+
+// Two-pass INT8 packing for wide matrices (cols % 4 == 0, aligned): one
+// workgroup of the single-pass kernel scans all rows of 64 columns, a
+// serial chain of loads that leaves the GPU mostly idle (2048 x 5632:
+// 350 us).  Here thread (x, chunk) owns four adjacent columns:
+//   pass 1: the maximum |w| of its columns over one chunk of rows
+//           (16-byte loads, kPackUnroll in flight), one partial per chunk;
+//   pass 2: the column maxima from the partials (max is exact in any
+//           order), then quant.cpp's scale / reciprocal / round / clamp for
+//           its columns over one chunk of rows, four codes per 4-byte store.
+// The comparison `v > m` skips NaN, as the single-pass kernel does.
+constexpr int kPackThreads = 256;
+constexpr int kPackUnroll = 8;
+
+__global__ __launch_bounds__(kPackThreads) void pack_int8_colmax_kernel(const float* __restrict__ w,
+                                                                        float* __restrict__ part, int64_t rows,
+                                                                        int64_t cols, int64_t rows_per_chunk) {
+    const int64_t c4 = (static_cast<int64_t>(blockIdx.x) * kPackThreads + threadIdx.x) * 4;
+    if (c4 >= cols) return;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
+    const int64_t r1 = min(rows, r0 + rows_per_chunk);
+    float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t r = r0; r < r1; r += kPackUnroll) {
+        float4 v[kPackUnroll];
+#pragma unroll
+        for (int u = 0; u < kPackUnroll; ++u)
+            v[u] = r + u < r1 ? *reinterpret_cast<const float4*>(w + (r + u) * cols + c4)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < kPackUnroll; ++u) {
+            const float a[4] = {fabsf(v[u].x), fabsf(v[u].y), fabsf(v[u].z), fabsf(v[u].w)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (a[e] > m[e]) m[e] = a[e];
+        }
+    }
+    *reinterpret_cast<float4*>(part + static_cast<int64_t>(blockIdx.y) * cols + c4) = make_float4(m[0], m[1], m[2], m[3]);
+}
+
+__device__ __forceinline__ uint32_t int8_code(float x, float inv) {
+    float v = roundf(x * inv);
+    v = v < -127.0f ? -127.0f : (127.0f < v ? 127.0f : v);
+    return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(v)));
+}
+
+__global__ __launch_bounds__(kPackThreads) void pack_int8_quantize_kernel(
+    const float* __restrict__ w, const float* __restrict__ part, int chunks, int8_t* __restrict__ q,
+    float* __restrict__ scale, int64_t rows, int64_t cols, int64_t rows_per_chunk) {
+    const int64_t c4 = (static_cast<int64_t>(blockIdx.x) * kPackThreads + threadIdx.x) * 4;
+    if (c4 >= cols) return;
+    float amax[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i0 = 0; i0 < chunks; i0 += kPackUnroll) {
+        float4 pv[kPackUnroll];
+#pragma unroll
+        for (int u = 0; u < kPackUnroll; ++u)
+            pv[u] = i0 + u < chunks ? *reinterpret_cast<const float4*>(part + static_cast<int64_t>(i0 + u) * cols + c4)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < kPackUnroll; ++u) {
+            const float a[4] = {pv[u].x, pv[u].y, pv[u].z, pv[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (a[e] > amax[e]) amax[e] = a[e];
+        }
+    }
+    float inv[4];
+    float sc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        sc[e] = amax[e] > 0.0f ? amax[e] / 127.0f : 1.0f;   // quant.cpp:94-96
+        inv[e] = 1.0f / sc[e];
+    }
+    if (blockIdx.y == 0) *reinterpret_cast<float4*>(scale + c4) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
+    const int64_t r1 = min(rows, r0 + rows_per_chunk);
+    for (int64_t r = r0; r < r1; r += kPackUnroll) {
+        float4 v[kPackUnroll];
+#pragma unroll
+        for (int u = 0; u < kPackUnroll; ++u)
+            v[u] = r + u < r1 ? *reinterpret_cast<const float4*>(w + (r + u) * cols + c4)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < kPackUnroll; ++u) {
+            if (r + u >= r1) break;
+            const uint32_t word = int8_code(v[u].x, inv[0]) | (int8_code(v[u].y, inv[1]) << 8) |
+                                  (int8_code(v[u].z, inv[2]) << 16) | (int8_code(v[u].w, inv[3]) << 24);
+            *reinterpret_cast<uint32_t*>(q + (r + u) * cols + c4) = word;
+        }
     }
 }
 
@@ -161,6 +252,28 @@ int vm_hip_pack_int8(const float* w, int8_t* q, float* scale, int64_t rows, int6
     if (!w || !q || !scale) return fail_inval("vm_hip_pack_int8: null pointer");
     VM_TRY(injected_failure("QuantizePack", "launch"));
     auto s = static_cast<hipStream_t>(stream);
+    // Two passes for matrices wide and tall enough to fill the GPU, when
+    // 16-byte loads apply and the stream is not being captured (the row
+    // partials use the stream's workspace, sized here).
+    const bool vec = cols % 4 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(q) % 4 == 0 && reinterpret_cast<uintptr_t>(scale) % 16 == 0;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (s) (void)hipStreamIsCapturing(s, &cap);
+    if (vec && rows >= 64 && cols >= 256 && cap == hipStreamCaptureStatusNone) {
+        const int64_t col_groups = (cols / 4 + kPackThreads - 1) / kPackThreads;
+        // about 512 workgroups per pass, at least 32 rows and at most 64 chunks
+        int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((512 + col_groups - 1) / col_groups, rows / 32));
+        chunks = std::min<int64_t>(chunks, 64);   // pass 2 reads every chunk's partial
+        const int64_t rpc = (rows + chunks - 1) / chunks;
+        chunks = (rows + rpc - 1) / rpc;
+        Workspace ws{};
+        VM_TRY(get_workspace(s, static_cast<std::size_t>(chunks * cols), 0, &ws));
+        const dim3 grid(static_cast<unsigned>(col_groups), static_cast<unsigned>(chunks));
+        hipLaunchKernelGGL(pack_int8_colmax_kernel, grid, dim3(kPackThreads), 0, s, w, ws.partials, rows, cols, rpc);
+        hipLaunchKernelGGL(pack_int8_quantize_kernel, grid, dim3(kPackThreads), 0, s, w, ws.partials,
+                           static_cast<int>(chunks), q, scale, rows, cols, rpc);
+        return check_launch("QuantizePack", s);
+    }
     hipLaunchKernelGGL(pack_int8_kernel, dim3(grid_1d(cols, kColsPerWg)), dim3(kColsPerWg * kRowGroups),
                        0, s, w, q, scale, rows, cols);
     return check_launch("QuantizePack", s);
