@@ -397,6 +397,19 @@ int vm_hip_rope_kv_append_slices_f32(const float* qkv, int64_t qkv_slices, const
                                      int64_t head_dim, int64_t max_seq, void* stream);
 int vm_hip_argmax_slices_f32(const float* x, int64_t slices, int64_t n, int32_t* token_out,
                              int32_t* pos, int32_t* tokens, int64_t max_seq, void* stream);
+
+/* vm_hip_argmax_slices_f32 across workgroups (each scans 1024 elements of
+ * every slice; the last to finish reduces the candidates).  `workspace`:
+ * at least vm_hip_argmax_workspace_bytes(n) bytes of device memory,
+ * 16-byte aligned and zeroed before its first use; every call leaves it
+ * zeroed again.  Calls that share a workspace must not overlap.  Falls back
+ * to vm_hip_argmax_slices_f32 for unaligned x, n % 4 != 0 or more than 2^29
+ * elements.  No counterpart in the reference (greedy sampling on the
+ * device for the resident decoder). */
+int64_t vm_hip_argmax_workspace_bytes(int64_t n);
+int vm_hip_argmax_slices_ws_f32(const float* x, int64_t slices, int64_t n, int32_t* token_out,
+                                int32_t* pos, int32_t* tokens, int64_t max_seq, void* workspace,
+                                int64_t workspace_bytes, void* stream);
 int vm_hip_slices_sum_f32(const float* in, int64_t slices, int64_t n, float* out, void* stream);
 
 /* Decode attention fused with the split-K projection in front of it (no

@@ -213,6 +213,43 @@ def test_argmax_and_sum_of_slices(hip, n, slices):
     assert int(dt.download(np.int32, (1,))[0]) == int(np.argmax(tot))
 
 
+@pytest.mark.parametrize("n,slices", [(32000, 4), (49152, 4), (1000, 3), (4096, 9), (37, 2), (1028, 1)])
+def test_argmax_across_workgroups(hip, n, slices):
+    """vm_hip_argmax_slices_ws_f32 (one candidate per 1024 elements, the last
+    workgroup reduces): the sum of slices' first maximum, NaN skipped, the
+    position advanced and the token recorded; repeated calls reuse the
+    workspace (its ticket is reset); ties across workgroups resolve to the
+    lowest index."""
+    x = _normal((slices, n), n + 3)
+    tot = x[0].copy()
+    for i in range(1, slices):
+        tot = (tot + x[i]).astype(np.float32)
+    lib = hip.open_library()
+    wsb = lib.vm_hip_argmax_workspace_bytes(n)
+    assert wsb >= 256 + 8 * ((n + 1023) // 1024)
+    ws = _dev(hip, np.zeros(wsb // 4 + 1, np.float32))
+    dx, dt = _dev(hip, x), hip.DeviceBuffer(4)
+    dpos = _dev(hip, np.array([3], np.int32), np.int32)
+    dseq = _dev(hip, np.full(8, -7, np.int32), np.int32)
+    print(f"case argmax_ws n={n} slices={slices}", flush=True)
+    for call in range(3):
+        hip.check(lib.vm_hip_argmax_slices_ws_f32(dx.ptr, slices, n, dt.ptr, dpos.ptr, dseq.ptr, 8, ws.ptr, wsb, None))
+        assert int(dt.download(np.int32, (1,))[0]) == int(np.argmax(tot)), call
+    assert int(dpos.download(np.int32, (1,))[0]) == 6
+    seq = dseq.download(np.int32, (8,))
+    assert list(seq[4:7]) == [int(np.argmax(tot))] * 3 and seq[7] == -7
+    if n >= 3000:
+        # equal maxima in two workgroups and a NaN: the lower index wins
+        y = x.copy()
+        y[:, :] = 0.0
+        y[0, 2100] = y[0, 1500] = 9.0
+        y[0, 5] = np.nan
+        dy = _dev(hip, y)
+        hip.check(lib.vm_hip_argmax_slices_ws_f32(dy.ptr, slices, n, dt.ptr, None, None, 0, ws.ptr, wsb, None))
+        assert int(dt.download(np.int32, (1,))[0]) == 1500
+    assert lib.vm_hip_argmax_slices_ws_f32(dx.ptr, slices, n, dt.ptr, None, None, 0, ws.ptr, 16, None) != 0
+
+
 def _src(hip, **kw):
     s = hip.GemvSrc()
     for key, val in kw.items():

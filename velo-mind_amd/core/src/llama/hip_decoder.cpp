@@ -19,6 +19,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "velomind/llama/llama_hip.h"
 #include "velomind/llama/llama_packed.h"
@@ -90,6 +91,7 @@ struct HipLlamaDecoder::Impl {
     // Activations sized for max_seq rows.
     DevBuf h, hn, qkv_out, q, ctx, attn_out, gu, act, down_out, logits;
     DevBuf idx, token, pos, tokens;
+    DevBuf am_ws;   // argmax workspace
     std::size_t seq = 0;  // positions filled in the cache
     // One-token steps: projections leave split-K partial slices that their
     // consumers add (vm_hip_qmm_gemv_slices_f32); counts per projection.
@@ -411,6 +413,10 @@ void HipLlamaDecoder::Impl::allocate() {
         m.ss_ffn = DevBuf(static_cast<std::size_t>(m.s_gu * 4));
         m.ss_final = DevBuf(static_cast<std::size_t>(m.s_lm * 4));
         m.att_part = DevBuf(static_cast<std::size_t>(m.H * m.att_chunks * (m.D + 4) * 4));
+        // the multi-workgroup argmax's ticket and candidates (zeroed once)
+        m.am_ws = DevBuf(static_cast<std::size_t>(vm_hip_argmax_workspace_bytes(m.vocab)));
+        const std::vector<unsigned char> zeros(m.am_ws.bytes, 0);
+        check(vm_hip_memcpy_h2d(m.am_ws.p, zeros.data(), zeros.size(), m.stream), "argmax workspace");
         m.qkv_sl = DevBuf(static_cast<std::size_t>(m.s_qkv * m.qkv_n * 4));
         m.o_sl = DevBuf(static_cast<std::size_t>(m.s_o * m.hidden * 4));
         m.gu_sl = DevBuf(static_cast<std::size_t>(m.s_gu * 2 * m.inter * 4));
@@ -548,7 +554,8 @@ auto HipLlamaDecoder::generate(std::span<const std::int32_t> prompt, std::size_t
     auto step = [&] {
         if (m.sliced) {
             m.forward_one_sliced();
-            check(vm_hip_argmax_slices_f32(m.lm_sl.as<float>(), m.s_lm, m.vocab, tok, posp, seqp, ms, m.stream),
+            check(vm_hip_argmax_slices_ws_f32(m.lm_sl.as<float>(), m.s_lm, m.vocab, tok, posp, seqp, ms, m.am_ws.p,
+                                              static_cast<std::int64_t>(m.am_ws.bytes), m.stream),
                   "argmax");
         } else {
             m.forward(1);

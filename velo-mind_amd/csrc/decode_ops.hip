@@ -1098,6 +1098,108 @@ __global__ __launch_bounds__(kArgT) void argmax_kernel(const float* __restrict__
     }
 }
 
+// ---- Greedy argmax over the sum of split-K slices, across workgroups.
+// The single-workgroup argmax_kernel reads every slice of the vocabulary
+// through one CU; here workgroup w takes elements [1024 w, 1024 (w + 1))
+// (a float4 per thread), issues the loads of up to kAmSl slices at once,
+// adds them in slice order, and leaves its first maximum (NaN skipped) in
+// the workspace; the last workgroup to finish (atomic ticket; the partials
+// are stored with agent-scope stores and acknowledged before it) reduces
+// the candidates with the same rule -- maximum, lowest index on ties, so
+// the result does not depend on which workgroup finishes last -- writes
+// the token, advances *pos and resets the ticket for the next call.
+constexpr int kAmT = 256;
+constexpr int kAmPer = 4 * kAmT;
+constexpr int kAmSl = 8;
+
+__global__ __launch_bounds__(kAmT) void argmax_slices_multi_kernel(
+    const float* __restrict__ x, int n, int slices, int32_t* __restrict__ token_out, int32_t* __restrict__ pos,
+    int32_t* __restrict__ tokens, int64_t max_seq, float* __restrict__ part_v, int* __restrict__ part_i,
+    unsigned* __restrict__ counter) {
+    __shared__ float bv[kAmT / 64];
+    __shared__ int bi[kAmT / 64];
+    __shared__ unsigned ticket;
+    const int tid = threadIdx.x;
+    const int base = static_cast<int>(blockIdx.x) * kAmPer + 4 * tid;
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(x, static_cast<uint32_t>(n) * static_cast<uint32_t>(slices) * 4u);
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < slices; s0 += kAmSl) {
+        u32x4 l[kAmSl];
+#pragma unroll
+        for (int u = 0; u < kAmSl; ++u)
+            l[u] = buffer_load16(rs, (s0 + u < slices && base < n)
+                                         ? (static_cast<uint32_t>(s0 + u) * static_cast<uint32_t>(n) + base) * 4u
+                                         : 0xfffffff0u);
+#pragma unroll
+        for (int u = 0; u < kAmSl; ++u)
+            if (s0 + u < slices) {   // slices in order; slice 0 is taken as is
+#pragma unroll
+                for (int c = 0; c < 4; ++c) t[c] = s0 + u == 0 ? __uint_as_float(l[u][c]) : t[c] + __uint_as_float(l[u][c]);
+            }
+    }
+    float best = -INFINITY;
+    int idx = -1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float v = t[c];
+        if (base + c < n && v == v && (idx < 0 || v > best)) {
+            best = v;
+            idx = base + c;
+        }
+    }
+    auto reduce = [&]() {
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(best, off, 64);
+            const int oi = __shfl_xor(idx, off, 64);
+            if (argmax_better(best, idx, ov, oi)) {
+                best = ov;
+                idx = oi;
+            }
+        }
+        if ((tid & 63) == 0) {
+            bv[tid >> 6] = best;
+            bi[tid >> 6] = idx;
+        }
+        __syncthreads();
+        if (tid == 0)
+            for (int w = 1; w < kAmT / 64; ++w)
+                if (argmax_better(best, idx, bv[w], bi[w])) {
+                    best = bv[w];
+                    idx = bi[w];
+                }
+    };
+    reduce();
+    if (tid == 0) {
+        coherent_store(part_v + blockIdx.x, best);
+        __hip_atomic_store(part_i + blockIdx.x, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);   // partial acknowledged before the ticket
+        ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (ticket != gridDim.x - 1) return;
+    best = -INFINITY;
+    idx = -1;
+    for (int w = tid; w < static_cast<int>(gridDim.x); w += kAmT) {
+        const float v = coherent_load(part_v + w);
+        const int i = __hip_atomic_load(part_i + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (argmax_better(best, idx, v, i)) {
+            best = v;
+            idx = i;
+        }
+    }
+    __syncthreads();   // bv / bi are reused
+    reduce();
+    if (tid == 0) {
+        token_out[0] = idx;
+        if (pos) {
+            const int next = pos[0] + 1;
+            if (tokens && next >= 0 && next < max_seq) tokens[next] = idx;
+            pos[0] = next;
+        }
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 int grid_for(int64_t work) {
     const int64_t b = (work + kT - 1) / kT;
     return static_cast<int>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
@@ -1310,6 +1412,33 @@ int vm_hip_argmax_slices_f32(const float* x, int64_t slices, int64_t n, int32_t*
     const int vec = aligned16(x) && n % 4 == 0 && n * slices < (int64_t{1} << 29) ? 1 : 0;
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgT), 0, S(stream), x, n, token_out, pos, tokens, max_seq, vec,
                        static_cast<int>(slices));
+    return check_launch("argmax_slices", S(stream));
+}
+
+int64_t vm_hip_argmax_workspace_bytes(int64_t n) {
+    if (n < 1) return 0;
+    const int64_t wgs = (n + kAmPer - 1) / kAmPer;
+    return 256 + wgs * 8;   // ticket, then per-workgroup value and index
+}
+
+int vm_hip_argmax_slices_ws_f32(const float* x, int64_t slices, int64_t n, int32_t* token_out, int32_t* pos,
+                                int32_t* tokens, int64_t max_seq, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+    clear_error();
+    if (n < 1 || n > 0x7fffffff) return fail_inval("argmax_slices: n must be in [1, 2^31)");
+    if (slices < 1 || slices > 4096) return fail_inval("argmax_slices: slices must be in [1, 4096]");
+    if (!x || !token_out || !workspace) return fail_inval("argmax_slices: null pointer");
+    if (workspace_bytes < vm_hip_argmax_workspace_bytes(n) || !aligned16(workspace))
+        return fail_inval("argmax_slices: workspace smaller than vm_hip_argmax_workspace_bytes(n) or unaligned");
+    // 16-byte loads need aligned rows; buffer offsets are 32-bit
+    if (!aligned16(x) || n % 4 != 0 || n * slices >= (int64_t{1} << 29))
+        return vm_hip_argmax_slices_f32(x, slices, n, token_out, pos, tokens, max_seq, stream);
+    const int64_t wgs = (n + kAmPer - 1) / kAmPer;
+    auto* ws = static_cast<unsigned char*>(workspace);
+    hipLaunchKernelGGL(argmax_slices_multi_kernel, dim3(static_cast<unsigned>(wgs)), dim3(kAmT), 0, S(stream), x,
+                       static_cast<int>(n), static_cast<int>(slices), token_out, pos, tokens, max_seq,
+                       reinterpret_cast<float*>(ws + 256), reinterpret_cast<int*>(ws + 256 + 4 * wgs),
+                       reinterpret_cast<unsigned*>(ws));
     return check_launch("argmax_slices", S(stream));
 }
 

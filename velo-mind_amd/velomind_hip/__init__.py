@@ -108,6 +108,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_attention_decode_slices_f32": ([p, c_int64, p, c_int64, c_float, c_float, p, p, p, p, p, p,
                                                 c_int64, c_int64, c_int64, c_int64, c_float, p], c_int),
         "vm_hip_slices_sum_scaled_f32": ([p, c_int64, c_int64, p, c_int64, c_float, c_float, p, p], c_int),
+        "vm_hip_argmax_workspace_bytes": ([c_int64], c_int64),
+        "vm_hip_argmax_slices_ws_f32": ([p, c_int64, c_int64, p, p, p, c_int64, p, c_int64, p], c_int),
         "vm_hip_attention_decode_slices_prefetch_f32": ([p, c_int64, p, c_int64, c_float, c_float, p, p, p, p, p, p,
                                                          c_int64, c_int64, c_int64, c_int64, c_float,
                                                          POINTER(Prefetch), p], c_int),
@@ -136,7 +138,8 @@ def exported_symbols() -> list[str]:
             "vm_hip_gemv_slices_count", "vm_hip_qmm_gemv_slices_f32", "vm_hip_add_rmsnorm_slices_f32",
             "vm_hip_rope_kv_append_slices_f32", "vm_hip_argmax_slices_f32", "vm_hip_slices_sum_f32",
             "vm_hip_qmm_gemv_slices_src_f32", "vm_hip_attention_decode_chunks", "vm_hip_attention_decode_slices_f32",
-            "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32"]
+            "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32",
+            "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32"]
 
 
 def open_library() -> ctypes.CDLL:
