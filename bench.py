@@ -220,7 +220,18 @@ def cpu_baseline(target_s: float) -> dict:
         dt = time.perf_counter() - t0
     finally:
         os.sched_setaffinity(0, prev)
+    model, flags = "", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and not model:
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
     return {"value": round(done_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "host": {"nproc": os.cpu_count(), "model": model, "avx2": "avx2" in flags, "fma": "fma" in flags},
             "sample": f"{sweeps} full decode-step sweep(s) (155 INT4 GEMVs, M=1) of the oracle's scalar "
                       f"INT4 loop (src/cpu/ops/quantized_matmul.cpp:48-141), {dt:.1f} s on core {cpu}",
             "tokens_per_s": round(sweeps / dt, 4)}
@@ -472,6 +483,20 @@ def main() -> int:
     value = wl.bytes_per_step / (ms_per_step * 1e-3) / 1e9
     log(f"bench: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s (wall {wall:.2f} s)")
 
+    # Per-step distribution (median and P95, as the reference's
+    # benchmarks/stats_helper.h:19-40 reports): steps after the timed
+    # region, each between its own pair of events.
+    ev = [H.Event() for _ in range(min(args.steps, 100) + 1)]
+    ev[0].record(stream.handle)
+    for i in range(1, len(ev)):
+        run_step()
+        ev[i].record(stream.handle)
+    ev[-1].synchronize()
+    per_step = np.array([ev[i - 1].elapsed_ms(ev[i]) for i in range(1, len(ev))])
+    step_stats = {"samples": int(per_step.size), "median_ms": round(float(np.median(per_step)), 5),
+                  "p95_ms": round(float(np.percentile(per_step, 95)), 5),
+                  "min_ms": round(float(per_step.min()), 5), "max_ms": round(float(per_step.max()), 5)}
+
     durs = per_shape_durations(H, wl, args.shape_reps, graph is not None)
     per_shape = {}
     for (k, n), (ms, count) in durs.items():
@@ -543,6 +568,7 @@ def main() -> int:
             "avg_launch_us": round(dms * 1e3, 3),
             "algo_bytes_per_launch": dbytes,
         },
+        "step_stats": step_stats,
         "per_shape": per_shape,
         "e2e": e2e,
         "gemm": gemm,
