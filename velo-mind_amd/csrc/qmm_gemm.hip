@@ -474,7 +474,8 @@ struct GemmConfig {
 //     per CU, while the fp32 partials stay under a quarter of the code
 //     bytes -- or, with fewer than 128 tiles, while each split keeps at
 //     least eight steps;
-//   M > 128: 64 x 128 tiles; K splits of at least twenty 64-row steps up
+//   M > 128: 64 x 128 tiles (INT8 per column unsplit: 64 x 64); K splits
+//     of at least twenty 64-row steps up
 //     to ~512 workgroups (K = 5632: 4 splits); 32 x 128 when an unsplit
 //     grid would hold fewer than 150 tiles (N = 2048: 27.5 us vs 42.1 us
 //     with the former 128 x 128 tiles).
@@ -502,6 +503,10 @@ GemmConfig choose_gemm(int kind, int m, int k, int n) {
         const long tiles = tiles_of(cfg.bm, cfg.bn);
         while (s * 2 <= 4 && tiles * s * 2 <= 512 && steps / (s * 2) >= 20) s *= 2;
         if (s == 1 && tiles < 150) cfg.bm = 32;
+        // INT8 per column, unsplit: 64 x 64 (M = 512, K = 2048, N = 5632:
+        // 35.2 us vs 37.6 us; its B dequantisation is cheap enough that the
+        // doubled workgroup count wins)
+        if (kind == 0 && s == 1 && cfg.bm == 64) cfg.bn = 64;
     }
     cfg.splits = s;
     // Tuning override for measurement sweeps: VELOMIND_GEMM_CFG="BM,BN,S".
