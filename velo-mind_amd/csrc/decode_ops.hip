@@ -865,21 +865,36 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
     for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;   // statistics of row lr of this wave
 
-    for (int k0 = 0; k0 < wg_end; k0 += KT) {
-        const int nk = min(KT, n_keys - k0);
-        __syncthreads();   // the previous tile is consumed
+    // K/V tiles pass through registers one tile ahead: the next tile's
+    // loads are issued as soon as the current one is in LDS, so they are in
+    // flight during its scores and p . V.
+    constexpr int kU = KT * D / 4 / kT;   // float4s of K (and of V) per thread per tile
+    float4 nk_reg[kU], nv_reg[kU];
+    auto load_tile = [&](int t0) {
+        const int nkt = min(KT, n_keys - t0);
 #pragma unroll
-        for (int u = 0; u < KT * D / 4 / kT; ++u) {
+        for (int u = 0; u < kU; ++u) {
             const int e = tid + u * kT;
             const int j = e / (D / 4), c = e - j * (D / 4);
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (j < nk) {
-                kv = *reinterpret_cast<const float4*>(kb + static_cast<int64_t>(k0 + j) * D + 4 * c);
-                vv = *reinterpret_cast<const float4*>(vb + static_cast<int64_t>(k0 + j) * D + 4 * c);
+            nk_reg[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            nv_reg[u] = nk_reg[u];
+            if (j < nkt) {
+                nk_reg[u] = *reinterpret_cast<const float4*>(kb + static_cast<int64_t>(t0 + j) * D + 4 * c);
+                nv_reg[u] = *reinterpret_cast<const float4*>(vb + static_cast<int64_t>(t0 + j) * D + 4 * c);
             }
-            *reinterpret_cast<float4*>(sk + j * PITCH + 4 * c) = kv;
-            *reinterpret_cast<float4*>(sv + j * PITCH + 4 * c) = vv;
         }
+    };
+    if (wg_end > 0) load_tile(0);
+    for (int k0 = 0; k0 < wg_end; k0 += KT) {
+        __syncthreads();   // the previous tile is consumed
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int e = tid + u * kT;
+            const int j = e / (D / 4), c = e - j * (D / 4);
+            *reinterpret_cast<float4*>(sk + j * PITCH + 4 * c) = nk_reg[u];
+            *reinterpret_cast<float4*>(sv + j * PITCH + 4 * c) = nv_reg[u];
+        }
+        if (k0 + KT < wg_end) load_tile(k0 + KT);
         __syncthreads();
 
         // S^T = K Q^T for the four 16-key blocks.
