@@ -104,6 +104,9 @@ int vm_hip_event_elapsed_ms(float* ms, void* start, void* end);
  *      call.  Capture needs a non-null stream, and every quantized-matmul
  *      shape in the captured region must have run once on that stream
  *      before capture (the split-K workspace cannot grow while capturing).
+ *      Eager calls after the capture may grow the stream's workspace; the
+ *      graph keeps the buffers it captured, which stay allocated until the
+ *      stream is destroyed (destroy graphs before their stream).
  *      The captured kernels reset their own counters, so the graph holds no
  *      memset nodes. ------------------------------------------------- */
 int vm_hip_stream_begin_capture(void* stream);

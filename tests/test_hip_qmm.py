@@ -187,6 +187,45 @@ def test_deterministic_and_stream_workspace_reuse(hip):
     _check(dsmall.download(np.float32, (256,)), ref2, TOL_GEMV)
 
 
+def test_graph_keeps_workspace_after_growth(hip):
+    """A split-K GEMV captured in a graph still replays correctly after an
+    eager call on the same stream has grown the stream's workspace (the
+    graph holds the old buffer's address, which must stay allocated)."""
+    k, n = 2048, 2048
+    p, s = _int4(k, n, 81)
+    x = _normal((1, k), 82)
+    da, dp, ds = (hip.DeviceBuffer.from_array(v) for v in (x, p, s))
+    st = hip.Stream()
+    d_eager, d_graph = hip.DeviceBuffer(n * 4), hip.DeviceBuffer(n * 4)
+    hip.qmm_f32(da.addr, dp.addr, ds.addr, d_eager.addr, 1, k, n, hip.QUANT_INT4, 32, st)   # sizes the workspace
+    g = hip.Graph(st)
+    g.begin()
+    hip.qmm_f32(da.addr, dp.addr, ds.addr, d_graph.addr, 1, k, n, hip.QUANT_INT4, 32, st)
+    g.end()
+    # The two-pass INT8 pack of a 2048 x 8192 matrix keeps 64 x 8192 row
+    # partials in the same workspace: more than the GEMV sized it for.
+    rows, cols = 2048, 8192
+    w = _normal((rows, cols), 83, 0.02)
+    dw = hip.DeviceBuffer.from_array(w)
+    dq, dsc = hip.DeviceBuffer(rows * cols), hip.DeviceBuffer(cols * 4)
+    hip.pack_int8(dw.addr, dq.addr, dsc.addr, rows, cols, st)
+    st.synchronize()
+    filler = hip.DeviceBuffer.from_array(np.full(1 << 22, 0xFF, np.uint8))   # reuses freed memory, if any
+    eager = d_eager.download(np.float32, (n,))
+    for _ in range(3):
+        d_graph.upload(np.zeros(n, np.float32))
+        g.launch()
+        st.synchronize()
+        assert np.array_equal(d_graph.download(np.float32, (n,)).view(np.uint32), eager.view(np.uint32))
+    g.close()
+    st.close()
+    del filler
+    q_ref, s_ref = O.quantize_int8(w)
+    assert np.array_equal(dq.download(np.int8, (rows, cols)), q_ref.view(np.int8))
+    assert np.array_equal(dsc.download(np.float32, (cols,)).view(np.uint32), s_ref.view(np.uint32))
+    _check(eager, O.qmm(x, p.view(np.int8), s, k, O.QUANT_INT4, 32)[0], TOL_GEMV)
+
+
 @pytest.mark.parametrize("a_dt,s_dt", [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")])
 def test_mixed_dtype_keys(hip, a_dt, s_dt):
     # quantized_matmul.cpp:363-367 dtype keys; outputs rounded like dtype.h.

@@ -9,6 +9,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "vm_internal.h"
 
@@ -17,10 +18,14 @@ namespace vmhip {
 namespace {
 thread_local std::string t_last_error;
 
+// A grown workspace or staging buffer is retired, not freed: HIP graphs
+// captured earlier on the stream hold its address and may be replayed
+// later.  Retired buffers are freed with the stream (vm_hip_stream_destroy).
 struct WsEntry {
     void*       base = nullptr;
     std::size_t partial_floats = 0;
     std::size_t counter_slots = 0;
+    std::vector<void*> retired;
 };
 
 std::mutex g_ws_mutex;
@@ -29,6 +34,7 @@ std::map<std::pair<int, hipStream_t>, WsEntry> g_ws;
 struct StagingEntry {
     void*       base = nullptr;
     std::size_t bytes = 0;
+    std::vector<void*> retired;
 };
 std::map<std::pair<int, hipStream_t>, StagingEntry> g_staging;
 
@@ -104,9 +110,8 @@ int get_workspace(hipStream_t stream, std::size_t partial_floats, std::size_t co
         pf = std::max<std::size_t>(pf, 1 << 16);
         cs = std::max<std::size_t>(cs, 1024);
         if (e.base) {
-            // Kernels queued on this stream may still use the old buffer.
-            VM_TRY_HIP(hipStreamSynchronize(stream), "workspace resize: hipStreamSynchronize");
-            VM_TRY_HIP(hipFree(e.base), "workspace resize: hipFree");
+            // Queued kernels and captured graphs may still use the old buffer.
+            e.retired.push_back(e.base);
             e.base = nullptr;
         }
         const std::size_t counter_bytes = ((cs * sizeof(unsigned)) + 255) & ~std::size_t(255);
@@ -137,11 +142,13 @@ void release_workspace(hipStream_t stream) {
     auto it = g_ws.find({dev, stream});
     if (it != g_ws.end()) {
         if (it->second.base) (void)hipFree(it->second.base);
+        for (void* p : it->second.retired) (void)hipFree(p);
         g_ws.erase(it);
     }
     auto st = g_staging.find({dev, stream});
     if (st != g_staging.end()) {
         if (st->second.base) (void)hipFree(st->second.base);
+        for (void* p : st->second.retired) (void)hipFree(p);
         g_staging.erase(st);
     }
 }
@@ -159,8 +166,7 @@ int get_staging(hipStream_t stream, std::size_t bytes, void** out) {
         }
         const std::size_t want = std::max<std::size_t>(std::max(bytes, e.bytes * 2), 1 << 20);
         if (e.base) {
-            VM_TRY_HIP(hipStreamSynchronize(stream), "staging resize: hipStreamSynchronize");
-            VM_TRY_HIP(hipFree(e.base), "staging resize: hipFree");
+            e.retired.push_back(e.base);
             e.base = nullptr;
         }
         VM_TRY_HIP(hipMalloc(&e.base, want), "staging: hipMalloc");
