@@ -4,7 +4,7 @@
 The automatic config rule only reaches a few (L, W, S) combinations for the
 shapes of the other tests; this covers the rest: all lane widths L (16-column
 groups per row segment), wave counts W, split counts S (with a partial last
-split), 1/2/4 activation rows, the three weight kinds, a partial last tile and
+split; 3 and 5 splits leave a split tree with unpaired nodes), 1/2/4 activation rows, the three weight kinds, a partial last tile and
 more than eight tiles (so the XCD tile renumbering and its identity tail both
 run).  Tolerance: the fp32 GEMV bound of 1e-5 * max|ref|.
 """
@@ -49,7 +49,7 @@ def test_forced_config(hip, monkeypatch, L, W, kind):
     for m in (1, 2, 4):
         x = rng.standard_normal((m, k)).astype(np.float32)
         ref = O.qmm(x, q.view(np.int8), s, k, oq, block)
-        for S in (1, 3, 4):
+        for S in (1, 3, 4, 5):
             monkeypatch.setenv("VELOMIND_GEMV_CFG", f"{L},{W},{S}")
             print(f"case L={L} W={W} S={S} kind={kind} m={m} k={k} n={n}", flush=True)
             out = hip.run_qmm(x, q, s, k, qt, block)

@@ -187,6 +187,31 @@ def test_deterministic_and_stream_workspace_reuse(hip):
     _check(dsmall.download(np.float32, (256,)), ref2, TOL_GEMV)
 
 
+@pytest.mark.parametrize("k,n", [(2048, 5632), (5632, 2048), (2560, 960)])
+def test_split_tree_zero_columns(hip, k, n):
+    """Split-K shapes (the pair-word tree) with all-zero weight columns, so
+    every split's sum for them is zero (its fp32 bits are 0, the pattern
+    an empty pair-word half holds before encoding): the tree must still see
+    every split arrive, those outputs are exactly zero, and repeated calls
+    are bit-identical."""
+    w = _normal((k, n), 91, 0.02)
+    w[:, ::7] = 0.0
+    x = -np.abs(_normal((1, k), 92))
+    for qt in ("int8", "int4"):
+        if qt == "int8":
+            q, s = O.quantize_int8(w)
+            ref = O.qmm(x, q, s, k, O.QUANT_INT8, 0)
+            out = hip.run_qmm(x, q, s, k, hip.QUANT_INT8, 0)
+        else:
+            q, s = O.quantize_int4(w, 32)
+            ref = O.qmm(x, q.view(np.int8), s, k, O.QUANT_INT4, 32)
+            out = hip.run_qmm(x, q, s, k, hip.QUANT_INT4, 32)
+        assert not out[0, ::7].any(), qt
+        _check(out, ref, TOL_GEMV)
+        again = hip.run_qmm(x, q, s, k, hip.QUANT_INT8 if qt == "int8" else hip.QUANT_INT4, 0 if qt == "int8" else 32)
+        assert np.array_equal(out.view(np.uint32), again.view(np.uint32)), qt
+
+
 def test_graph_keeps_workspace_after_growth(hip):
     """A split-K GEMV captured in a graph still replays correctly after an
     eager call on the same stream has grown the stream's workspace (the

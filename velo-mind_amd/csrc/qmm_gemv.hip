@@ -12,19 +12,16 @@
 //               the workgroup's K range chunk by chunk, two chunks in
 //               flight per row group (the next chunk's codes and scales are
 //               loaded before the current chunk is reduced)
-//   split     : grid.y splits K; the last workgroup of a tile to finish
-//               (atomic ticket) adds the splits' partials in split order, so
-//               results do not depend on scheduling
+//   split     : grid.y splits K; the splits' sums meet in a binary tree of
+//               64-bit pair words (atomic OR with return), summed in a fixed
+//               grouping, so results do not depend on scheduling
 //
 // Reduction: row groups of a wave combine with VALU cross-lane operations
 // (DPP row rotations inside 16-lane rows, then the gfx950 permlane16/32
 // swaps across rows and wave halves), the waves of a workgroup through LDS,
-// splits through the per-stream workspace.  The
-// split handoff uses agent-scope atomic stores/loads (coherent across XCDs,
-// `sc1`) for the partials: each wave waits for its partial stores to be
-// acknowledged (s_waitcnt) before the barrier that precedes the ticket
-// increment, and the last workgroup reads the partials only after it has
-// observed the final ticket.  No L2 write-back or invalidate is needed.
+// splits through the pair words in the per-stream workspace.  The pair
+// words are agent-scope atomics (coherent across XCDs), so no L2 write-back,
+// invalidate or barrier is needed, and no workgroup waits for another.
 //
 // Dequantization: INT8 codes are sign-extended bytes (v_cvt_f32_i32 with an
 // SDWA byte select).  An INT4 byte holds the even K row in its low nibble;
@@ -106,7 +103,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
     float* __restrict__ c, int m, int k, int n, int block_size, int chunks_per_split,
     uint32_t code_bytes, uint32_t scale_bytes, uint32_t a_bytes, int a_vec, int blk_shift,
-    float* __restrict__ partials, unsigned* __restrict__ counters) {
+    unsigned long long* __restrict__ pairs) {
     using CS = ChunkShape<KIND>;
     constexpr int G = 64 / L;            // row groups per wave
     constexpr int RG = W * G;            // row groups per workgroup
@@ -117,7 +114,6 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const int xs_len = chunks_per_split * kChunkK;
     float* red = smem + MR * xs_len;                      // [W][MR][kTileCols]
     float* spare = red + W * MR * kTileCols;              // [4], write-only
-    __shared__ unsigned ticket;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -372,48 +368,61 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         return;
     }
 
-    // Split-K handoff.
-    float* my_part = partials + static_cast<int64_t>(split) * MR * n;
+    // Split-K handoff through a binary tree of pair words: one 64-bit word
+    // per output and tree node, zero between launches.  At level l the
+    // subtrees of 2^l splits are paired: each side ORs its sum, encoded as
+    // its fp32 bits with the sign bit flipped (never 0 once -0 is turned
+    // into +0), into its half of the node's word.  The side whose atomic
+    // returns the other half already set adds the two in split order,
+    // clears the word and moves up; the other side is done.  The root's
+    // holder writes C.  One atomic round trip per level, no barrier and no
+    // wait on another workgroup; the grouping of the sum is fixed by the
+    // tree, so results do not depend on scheduling.
     for (int o = threadIdx.x; o < MR * kTileCols; o += W * 64) {
         const int i = o / kTileCols;
         const int cc = o - i * kTileCols;
         const int col = tile_col0 + cc;
-        if (col < n) {
-            float v = 0.0f;
+        if (i >= m || col >= n) continue;
+        float v = 0.0f;
 #pragma unroll
-            for (int w = 0; w < W; ++w) v += red[(w * MR + i) * kTileCols + cc];
-            coherent_store(my_part + static_cast<int64_t>(i) * n + col, v);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the ticket
-    __syncthreads();
-    if (threadIdx.x == 0)
-        ticket = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (ticket != static_cast<unsigned>(splits - 1)) return;
-
-    for (int o = threadIdx.x; o < MR * kTileCols; o += W * 64) {
-        const int i = o / kTileCols;
-        const int cc = o - i * kTileCols;
-        const int col = tile_col0 + cc;
-        if (i < m && col < n) {
-            const float* p = partials + static_cast<int64_t>(i) * n + col;
-            const int64_t stride = static_cast<int64_t>(MR) * n;
-            float v = 0.0f;
-            // Batches of independent loads, summed in split order.
-            for (int s0 = 0; s0 < splits; s0 += 8) {
-                float t[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) t[u] = (s0 + u < splits) ? coherent_load(p + (s0 + u) * stride) : 0.0f;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v += t[u];
+        for (int w = 0; w < W; ++w) v += red[(w * MR + i) * kTileCols + cc];
+        bool last = true;
+        int64_t level_base = 0;
+        for (int lvl = 0; (1 << lvl) < splits; ++lvl) {
+            const int node = split >> (lvl + 1);
+            const int half = (split >> lvl) & 1;
+            // A lower half whose upper partner lies past the last split
+            // moves up alone.
+            if (half == 1 || ((2 * node + 1) << lvl) < splits) {
+                unsigned long long* word = pairs + level_base + (static_cast<int64_t>(node) * MR + i) * n + col;
+                const unsigned enc = __float_as_uint(v + 0.0f) ^ 0x80000000u;
+                const unsigned long long mine = half ? static_cast<unsigned long long>(enc) << 32 : enc;
+                const unsigned long long old =
+                    __hip_atomic_fetch_or(word, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const unsigned other = half ? static_cast<unsigned>(old) : static_cast<unsigned>(old >> 32);
+                if (other == 0u) {
+                    last = false;
+                    break;
+                }
+                __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float po = __uint_as_float(other ^ 0x80000000u);
+                v = half ? po + v : v + po;
             }
-            if constexpr (KIND == 0) v *= scale[col];
-            c[static_cast<int64_t>(i) * n + col] = v;
+            level_base += static_cast<int64_t>((splits + (2 << lvl) - 1) >> (lvl + 1)) * MR * n;
         }
+        if (!last) continue;
+        if constexpr (KIND == 0) v *= scale[col];
+        c[static_cast<int64_t>(i) * n + col] = v;
     }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Pair words of every level of the split tree (level l has
+// ceil(splits / 2^(l+1)) nodes), per activation row and column.
+std::size_t tree_words(int splits, int mr, int n) {
+    std::size_t nodes = 0;
+    for (int lvl = 0; (1 << lvl) < splits; ++lvl)
+        nodes += static_cast<std::size_t>((splits + (2 << lvl) - 1) >> (lvl + 1));
+    return nodes * static_cast<std::size_t>(mr) * static_cast<std::size_t>(n);
 }
 
 struct GemvConfig {
@@ -472,24 +481,27 @@ GemvConfig make_config(int mr, int k, int n, int L, int W, int S) {
 constexpr long kLdsBudget = 60 * 1024;
 
 // Picks lanes-per-segment L, waves W and K splits S for a shape.  The rule
-// follows a sweep of every instantiated (L, W) and S in 1..16 over the
+// follows a sweep of every instantiated (L, W) and S in 1..32 over the
 // TinyLlama-1.1B INT4 and SmolLM2 INT8 decode shapes on MI355X, where it
-// comes within 1% of the per-shape best in total:
+// lands within 0.25 us of the per-shape best:
 //   - latency-bound shapes (every row group needs at most one chunk with
 //     16- or 32-column tiles and no K split, at most 256 workgroups) run
-//     unsplit on narrow tiles: the split-K handoff costs three memory round
-//     trips, more than the narrow tiles' extra cache-line requests;
+//     unsplit on narrow tiles;
 //   - wide outputs (N >= 192 * 128) run unsplit on 128- or 256-column tiles,
 //     about one workgroup per CU, each row group streaming several chunks;
-//   - everything else splits K (S >= 2) so that each row group holds one
-//     chunk, with as many workgroups as fit one per CU (<= 256), then the
-//     fewest splits.
+//   - everything else splits K so that every row group holds exactly one
+//     chunk (all loads in flight at once), on row segments of at least 32
+//     bytes, with at most 256 workgroups of at most 32 KB of codes each, and
+//     takes the fewest tree levels, then the fewest waves (idle row groups
+//     cost time), then the narrowest tile;
+//   - shapes none of these fit take one chunk per row group with the most
+//     workgroups up to 256, then the fewest splits.
 // The config depends only on the shape, so results are reproducible.
 GemvConfig choose_config(int kind, int m, int k, int n) {
-    (void)kind;
     const int mr = mr_for(m);
     const int chunks = (k + kChunkK - 1) / kChunkK;
     const int w_max = max_waves(kind, mr);
+    const int seg_div = kind == 2 ? 2 : 1;  // code bytes per column: 1/2 (INT4) or 1
     GemvConfig cfg;
     bool found = false;
 
@@ -508,6 +520,27 @@ GemvConfig choose_config(int kind, int m, int k, int n) {
         while (S < kMaxSplits && geometry(mr, k, n, L, W, S).lds_bytes > kLdsBudget) S *= 2;
         cfg = make_config(mr, k, n, L, W, S);
         found = true;
+    }
+    if (!found) {
+        long best_key = 0;
+        for (const auto& lw : kShapes) {
+            const int L = lw[0], W = lw[1];
+            const int seg_bytes = kVec * L / seg_div;
+            if (W > std::min(8, w_max) || seg_bytes < 32) continue;
+            for (int S = 2, levels = 1; S <= kMaxSplits; S *= 2, ++levels) {
+                const Geometry g = geometry(mr, k, n, L, W, S);
+                const long wg_bytes = static_cast<long>(g.cps) * kChunkK / seg_div * seg_bytes;
+                if (g.splits != S || g.iters != 1 || g.wgs > 256 || g.lds_bytes > kLdsBudget ||
+                    wg_bytes > 32 * 1024)
+                    continue;
+                const long key = (static_cast<long>(levels) * 64 + W) * 64 + L;
+                if (!found || key < best_key) {
+                    best_key = key;
+                    cfg = make_config(mr, k, n, L, W, S);
+                    found = true;
+                }
+            }
+        }
     }
     if (!found) {
         // (iters, -workgroups, splits) ascending among configs within the
@@ -546,10 +579,9 @@ int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, 
                int block_size, const GemvConfig& cfg, hipStream_t stream) {
     const int tiles = (n + kVec * L - 1) / (kVec * L);
     Workspace ws{};
-    if (cfg.splits > 1) {
-        VM_TRY(get_workspace(stream, static_cast<std::size_t>(cfg.splits) * MR * n,
-                             static_cast<std::size_t>(tiles), &ws));
-    }
+    if (cfg.splits > 1)  // two 32-bit counter slots per pair word
+        VM_TRY(get_workspace(stream, 0, 2 * tree_words(cfg.splits, MR, n), &ws));
+    unsigned long long* pairs = reinterpret_cast<unsigned long long*>(ws.counters);
     const std::size_t lds = (static_cast<std::size_t>(MR) * cfg.chunks_per_split * kChunkK +
                              static_cast<std::size_t>(W) * MR * kVec * L + 4) * sizeof(float);
     const int64_t byte_rows = KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : k;
@@ -566,7 +598,7 @@ int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, 
     }
     hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
                        stream, a, wq, scale, c, m, k, n, block_size, cfg.chunks_per_split, code_bytes,
-                       scale_bytes, a_bytes, a_vec, blk_shift, ws.partials, ws.counters);
+                       scale_bytes, a_bytes, a_vec, blk_shift, pairs);
     return check_launch("QuantizedMatMul", stream);
 }
 
