@@ -25,6 +25,10 @@ on one pinned core over a bounded sample of the same step.
 N 5632, INT8 and INT4): TFLOP/s as a fraction of the dense fp16 MFMA peak
 (2.5 PFLOP/s) and algorithmic GB/s.
 
+``gemv_large`` runs the same GEMV kernel at 70B-class shapes (150-660 MB
+per launch) where latency no longer dominates: GB/s and fraction of HBM
+peak, showing what the kernel sustains once a launch is long enough.
+
 ``e2e`` adds the metric's second half, TinyLlama INT4 decode tokens/s
 (512-token prompt, 256 greedy tokens) and SmolLM2-360M
 INT8 (config 4: 128 + 128), on the resident HIP decoder with synthetic
@@ -377,6 +381,67 @@ def gemm_bench(H, stream, reps: int = 10) -> dict:
     return out
 
 
+LARGE_SHAPES = ((8192, 28672), (28672, 8192), (8192, 128256))
+
+
+def large_gemv_bench(H, stream, reps: int = 5) -> dict:
+    """Decode GEMVs (M=1, INT4 block 32) at 70B-class shapes, where a launch
+    moves 150-660 MB and latency no longer dominates: Llama-3-70B-shaped
+    gate/up (8192 x 28672), down (28672 x 8192) and lm_head (8192 x 128256).
+    Weights N(0, 0.02) drawn and packed on the GPU; enough copies per HIP
+    graph (>= 700 MB) that replays read cold HBM, not the 256 MB Infinity
+    Cache.  Same kernel and config rule as the sweep."""
+    lib = H.open_library()
+    rng = np.random.default_rng(5)
+    out = {}
+    for k, n in LARGE_SHAPES:
+        x = H.DeviceBuffer.from_array(rng.standard_normal(k, dtype=np.float32))
+        c = H.DeviceBuffer(n * 4)
+        w = H.DeviceBuffer(k * n * 4)
+        H.check(lib.vm_hip_fill_normal_f32(w.ptr, k * n, 77, 0.0, 0.02, None))
+        pb, sb = k // 2 * n, k // BLOCK * n * 4
+        copies = max(2, -(-700_000_000 // (pb + sb)))
+        packs = []
+        for i in range(copies):
+            p, s = H.DeviceBuffer(pb), H.DeviceBuffer(sb)
+            if i == 0:
+                H.pack_int4(w.addr, p.addr, s.addr, k, n, BLOCK)
+            else:
+                H.check(lib.vm_hip_memcpy_d2d(p.ptr, packs[0][0].ptr, pb, None))
+                H.check(lib.vm_hip_memcpy_d2d(s.ptr, packs[0][1].ptr, sb, None))
+            packs.append((p, s))
+        H.synchronize()
+        w.close()
+        for p, s in packs:
+            H.qmm_f32(x.addr, p.addr, s.addr, c.addr, 1, k, n, H.QUANT_INT4, BLOCK, stream)
+        stream.synchronize()
+        g = H.Graph(stream)
+        g.begin()
+        for p, s in packs:
+            H.qmm_f32(x.addr, p.addr, s.addr, c.addr, 1, k, n, H.QUANT_INT4, BLOCK, stream)
+        g.end()
+        g.launch()
+        stream.synchronize()
+        e0, e1 = H.Event(), H.Event()
+        e0.record(stream.handle)
+        for _ in range(reps):
+            g.launch()
+        e1.record(stream.handle)
+        e1.synchronize()
+        g.close()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * copies)
+        nbytes = algo_bytes(k, n)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[f"{k}x{n}"] = {"us": round(us, 2), "algo_bytes": nbytes, "GB_s": round(gbs, 1),
+                           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+        for p, s in packs:
+            p.close()
+            s.close()
+        x.close()
+        c.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -391,6 +456,7 @@ def main() -> int:
                     help="only the end-to-end legs, printed as one JSON line (profiling passes; with --no-graph "
                          "the decode steps launch eagerly so that rocprofv3 can trace them)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg (config 3)")
+    ap.add_argument("--no-large", action="store_true", help="skip the 70B-class decode GEMV leg")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg, printed as one JSON line")
     ap.add_argument("--gemm-profile", default="",
                     help="M,QT,REPS: only REPS eager launches of one config-3 GEMM (rocprofv3 counter passes)")
@@ -526,6 +592,11 @@ def main() -> int:
         log("bench: prefill GEMM (config 3)")
         gemm = gemm_bench(H, stream)
 
+    large = None
+    if not args.no_large and not args.only_shape:
+        log("bench: 70B-class decode GEMVs")
+        large = large_gemv_bench(H, stream)
+
     cpu = None
     if args.cpu_seconds > 0:
         log("bench: timing CPU baseline")
@@ -572,6 +643,7 @@ def main() -> int:
         "per_shape": per_shape,
         "e2e": e2e,
         "gemm": gemm,
+        "gemv_large": large,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

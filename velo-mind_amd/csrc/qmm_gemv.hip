@@ -488,20 +488,24 @@ constexpr long kLdsBudget = 60 * 1024;
 //     16- or 32-column tiles and no K split, at most 256 workgroups) run
 //     unsplit on narrow tiles;
 //   - wide outputs (N >= 192 * 128) run unsplit on 128- or 256-column tiles,
-//     about one workgroup per CU, each row group streaming several chunks;
+//     about one workgroup per CU or more, each row group streaming several
+//     chunks;
 //   - everything else splits K so that every row group holds exactly one
-//     chunk (all loads in flight at once), on row segments of at least 32
-//     bytes, with at most 256 workgroups of at most 32 KB of codes each, and
-//     takes the fewest tree levels, then the fewest waves (idle row groups
-//     cost time), then the narrowest tile;
-//   - shapes none of these fit take one chunk per row group with the most
-//     workgroups up to 256, then the fewest splits.
+//     chunk (all loads in flight at once), on tiles of at least 64 (INT4) or
+//     32 (INT8) columns, with at most 256 workgroups of at most 64 KB (INT4)
+//     or 32 KB (INT8) of codes each, and takes the fewest tree levels, then
+//     the fewest waves (idle row groups cost time), then the narrowest tile;
+//   - larger shapes that none of these fit are bandwidth-bound: wide tiles
+//     and enough workgroups to fill the GPU (70B-class projections, e.g.
+//     28672 x 8192 INT4: 3.6 -> 4.1 TB/s against the previous fallback).
 // The config depends only on the shape, so results are reproducible.
 GemvConfig choose_config(int kind, int m, int k, int n) {
     const int mr = mr_for(m);
     const int chunks = (k + kChunkK - 1) / kChunkK;
     const int w_max = max_waves(kind, mr);
-    const int seg_div = kind == 2 ? 2 : 1;  // code bytes per column: 1/2 (INT4) or 1
+    const int min_cols = kind == 2 ? 64 : 32;
+    const long max_wg_bytes = kind == 2 ? 64 * 1024 : 32 * 1024;
+    const int rows_per_chunk = kind == 2 ? kChunkK / 2 : kChunkK;  // code byte rows
     GemvConfig cfg;
     bool found = false;
 
@@ -515,7 +519,9 @@ GemvConfig choose_config(int kind, int m, int k, int n) {
     }
     if (!found && n >= 192 * 128) {
         const int L = (n + 127) / 128 <= 256 ? 8 : 16;
-        const int W = std::min(L, w_max);
+        // 256-column tiles over a long K stream best with four waves
+        // (8192 x 128256 INT4: 5.1 -> 5.5 TB/s); short K keeps more waves.
+        const int W = (L == 16 && k >= 4096) ? 4 : std::min(L, w_max);
         int S = 1;
         while (S < kMaxSplits && geometry(mr, k, n, L, W, S).lds_bytes > kLdsBudget) S *= 2;
         cfg = make_config(mr, k, n, L, W, S);
@@ -525,13 +531,12 @@ GemvConfig choose_config(int kind, int m, int k, int n) {
         long best_key = 0;
         for (const auto& lw : kShapes) {
             const int L = lw[0], W = lw[1];
-            const int seg_bytes = kVec * L / seg_div;
-            if (W > std::min(8, w_max) || seg_bytes < 32) continue;
+            if (W > std::min(8, w_max) || kVec * L < min_cols) continue;
             for (int S = 2, levels = 1; S <= kMaxSplits; S *= 2, ++levels) {
                 const Geometry g = geometry(mr, k, n, L, W, S);
-                const long wg_bytes = static_cast<long>(g.cps) * kChunkK / seg_div * seg_bytes;
+                const long wg_bytes = static_cast<long>(g.cps) * rows_per_chunk * kVec * L;
                 if (g.splits != S || g.iters != 1 || g.wgs > 256 || g.lds_bytes > kLdsBudget ||
-                    wg_bytes > 32 * 1024)
+                    wg_bytes > max_wg_bytes)
                     continue;
                 const long key = (static_cast<long>(levels) * 64 + W) * 64 + L;
                 if (!found || key < best_key) {
@@ -543,23 +548,18 @@ GemvConfig choose_config(int kind, int m, int k, int n) {
         }
     }
     if (!found) {
-        // (iters, -workgroups, splits) ascending among configs within the
-        // LDS budget, preferring those with at most 256 workgroups.
-        long best_key = 0;
-        for (const auto& lw : kShapes) {
-            const int L = lw[0], W = lw[1];
-            if (L < 2 || L > 8 || W > std::min(8, w_max)) continue;
-            for (int S = 2; S <= kMaxSplits; S *= 2) {
-                const Geometry g = geometry(mr, k, n, L, W, S);
-                if (g.splits != S || g.lds_bytes > kLdsBudget) continue;
-                const long over = g.wgs > 256 ? 1 : 0;
-                const long key = ((over * 64 + std::min(g.iters, 63)) * 4096 + (4095 - std::min(g.wgs, 4095))) * 64 + S;
-                if (!found || key < best_key) {
-                    best_key = key;
-                    cfg = make_config(mr, k, n, L, W, S);
-                    found = true;
-                }
-            }
+        // Bandwidth-bound shapes (tens of MB and more): 128-column tiles
+        // (256 for N >= 14336), four waves, and the fewest splits that give
+        // at least 192 workgroups; each row group streams many chunks.
+        const int L = n >= 14336 ? 16 : 8;
+        const int W = 4;
+        int S = 1;
+        while (S < kMaxSplits && (geometry(mr, k, n, L, W, S).wgs < 192 ||
+                                  geometry(mr, k, n, L, W, S).lds_bytes > kLdsBudget))
+            S *= 2;
+        if (geometry(mr, k, n, L, W, S).lds_bytes <= kLdsBudget) {
+            cfg = make_config(mr, k, n, L, W, S);
+            found = true;
         }
     }
     if (!found) cfg = make_config(mr, k, n, 8, 4, kMaxSplits);
