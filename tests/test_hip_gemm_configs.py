@@ -1,5 +1,6 @@
 """Every MFMA GEMM tile variant (rows_m > 4), forced through the tuning
-override VELOMIND_GEMM_CFG="BM,BN,S", against the oracle.
+override VELOMIND_GEMM_CFG="BM,BN,S" (or "BM,BN,S,D" for the variants
+that keep all D K-steps of a split in flight), against the oracle.
 
 Covers the three weight kinds, K splits 1/2/4 (deterministic split-K
 reduction), partial M and N tiles, K ending half-way through a 64-row step,
@@ -17,7 +18,7 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 # (BM, BN) tile variants instantiated in velo-mind_amd/csrc/qmm_gemm.hip.
-TILES = [(16, 128), (32, 128), (64, 128), (128, 128), (32, 64), (64, 64)]
+TILES = [(16, 128), (32, 128), (64, 128), (128, 128), (16, 64), (32, 64), (64, 64)]
 TOL = 1e-3
 
 
@@ -54,6 +55,29 @@ def test_forced_tile(hip, monkeypatch, bm, bn, kind, block):
     for splits in (1, 2, 4):
         monkeypatch.setenv("VELOMIND_GEMM_CFG", f"{bm},{bn},{splits}")
         print(f"case BM={bm} BN={bn} S={splits} kind={kind} block={block} m={m} k={k} n={n}", flush=True)
+        out = hip.run_qmm(x, q, s, k, qt, blk)
+        _check(out, ref)
+    monkeypatch.delenv("VELOMIND_GEMM_CFG")
+
+
+@pytest.mark.parametrize("kind,block", [("int8", 0), ("int8_block", 32), ("int8_block", 96), ("int4", 32),
+                                        ("int4", 64)])
+@pytest.mark.parametrize("bm,deep", [(16, 4), (16, 8), (32, 4), (32, 8)])
+@pytest.mark.parametrize("m", [5, 16, 40])
+def test_forced_deep(hip, monkeypatch, bm, deep, kind, block, m):
+    # K = 992 rows = 15.5 steps of 64: with D steps in flight the split
+    # count is at least ceil(16 / D), and the last split is partial (its
+    # trailing steps read zeros); N = 336 leaves a partial column tile.
+    k, n = 992, 336
+    rng = np.random.default_rng(bm * 100 + deep * 10 + m + block)
+    q, s, qt, blk = _weights(kind, k, n, rng, block)
+    oq = O.QUANT_INT4 if qt == 2 else O.QUANT_INT8
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = O.qmm(x, q.view(np.int8), s, k, oq, blk)
+    steps = (k + 63) // 64
+    for splits in sorted({-(-steps // deep), -(-steps // deep) + 1, 16}):
+        monkeypatch.setenv("VELOMIND_GEMM_CFG", f"{bm},64,{splits},{deep}")
+        print(f"case BM={bm} D={deep} S={splits} kind={kind} block={block} m={m} k={k} n={n}", flush=True)
         out = hip.run_qmm(x, q, s, k, qt, blk)
         _check(out, ref)
     monkeypatch.delenv("VELOMIND_GEMM_CFG")

@@ -34,6 +34,7 @@
 // the partials in split order and writes C, so results are deterministic.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -114,7 +115,11 @@ struct Stage {
     u32x4 s[T::kBlock ? T::kBPass : 1][T::kBlock ? 4 : 1];
 };
 
-template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
+// DEEP = 0: a two-step register pipeline over the split's K steps.
+// DEEP > 0 (small M, at most DEEP steps per split): every step's loads are
+// issued before the first MFMA, so the workgroup waits for one memory round
+// trip instead of one per pipeline step.
+template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N, int DEEP>
 __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
     float* __restrict__ c, int m, int k, int n, int block_size, int steps_per_split, int tiles_n, int tiles_m,
@@ -161,38 +166,41 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
 
     // ---- per-column normalisation of block scales over this split's K range
-    if constexpr (T::kBlock) {
-        const int b0 = k_begin / block_size;
-        const int b1 = (k_end + block_size - 1) / block_size;
-        const int q = tid % T::kQB;
-        float mx[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int b = b0 + tid / T::kQB; b < b1; b += 4 * T::kRedRows) {
-            u32x4 v[4];
+    auto normalise_scales = [&]() {
+        if constexpr (T::kBlock) {
+            const int b0 = k_begin / block_size;
+            const int b1 = (k_end + block_size - 1) / block_size;
+            const int q = tid % T::kQB;
+            float mx[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int b = b0 + tid / T::kQB; b < b1; b += 4 * T::kRedRows) {
+                u32x4 v[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int bb = b + u * T::kRedRows;
-                const uint32_t off = bb < b1 ? (static_cast<uint32_t>(bb) * n + n0 + 4 * q) * 4u : scale_bytes;
-                v[u] = buffer_load16(srs, off);
+                for (int u = 0; u < 4; ++u) {
+                    const int bb = b + u * T::kRedRows;
+                    const uint32_t off = bb < b1 ? (static_cast<uint32_t>(bb) * n + n0 + 4 * q) * 4u : scale_bytes;
+                    v[u] = buffer_load16(srs, off);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], fabsf(__uint_as_float(v[u][e])));
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+            for (int e = 0; e < 4; ++e) sRed[(tid / T::kQB) * BN + 4 * q + e] = mx[e];
+            __syncthreads();
+            if (tid < BN) {
+                float mm = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], fabsf(__uint_as_float(v[u][e])));
+                for (int r = 0; r < T::kRedRows; ++r) mm = fmaxf(mm, sRed[r * BN + tid]);
+                int e = 0;
+                if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
+                sPow[tid] = ldexpf(1.0f, e);
+                sInv[tid] = ldexpf(1.0f, -e);
+            }
+            __syncthreads();
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sRed[(tid / T::kQB) * BN + 4 * q + e] = mx[e];
-        __syncthreads();
-        if (tid < BN) {
-            float mm = 0.f;
-#pragma unroll
-            for (int r = 0; r < T::kRedRows; ++r) mm = fmaxf(mm, sRed[r * BN + tid]);
-            int e = 0;
-            if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
-            sPow[tid] = ldexpf(1.0f, e);
-            sInv[tid] = ldexpf(1.0f, -e);
-        }
-        __syncthreads();
-    }
+    };
+    if constexpr (DEEP == 0) normalise_scales();
 
     // ---- global -> registers for one step
     auto load_step = [&](int s, S& st) {
@@ -368,25 +376,52 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
         write_step(pk, cur ^ 1);
     };
 
-    // ---- main loop: LDS double buffer, register stages two steps ahead.
-    // Loads and stores are unconditional (steps past the end read zeros):
-    // with a fixed number of loads per iteration the compiler's vmcnt waits
-    // release each stage as soon as its own loads are in, leaving the next
-    // stage's loads in flight.
-    S st0, st1;
-    load_step(0, st0);
-    load_step(1, st1);
-    store_step(st0, 0);
-    load_step(2, st0);
-    __syncthreads();
-    for (int s = 0; s < nsteps; s += 2) {
-        step(0, st1);
+    if constexpr (DEEP > 0) {
+        // ---- all of the split's steps in flight (nsteps <= DEEP; steps past
+        // the split read zeros), then the LDS double buffer as below.  The
+        // vector-memory counter retires loads in issue order, so each step
+        // is released as soon as its own loads are in.
+        S st[DEEP];
+#pragma unroll
+        for (int s = 0; s < DEEP; ++s) load_step(s, st[s]);
+        normalise_scales();   // its scale loads queue behind the steps' loads
+        store_step(st[0], 0);
         __syncthreads();
-        load_step(s + 3, st1);
-        if (s + 1 >= nsteps) break;
-        step(1, st0);
+#pragma unroll
+        for (int s = 0; s < DEEP; ++s) {
+            if (s >= nsteps) break;
+            if (s + 1 < DEEP) {
+                step(s & 1, st[s + 1]);
+            } else {
+                Frags f0, f1;
+                read_frags(s & 1, 0, f0);
+                read_frags(s & 1, 1, f1);
+                mfma_frags(f0);
+                mfma_frags(f1);
+            }
+            __syncthreads();
+        }
+    } else {
+        // ---- main loop: LDS double buffer, register stages two steps ahead.
+        // Loads and stores are unconditional (steps past the end read zeros):
+        // with a fixed number of loads per iteration the compiler's vmcnt
+        // waits release each stage as soon as its own loads are in, leaving
+        // the next stage's loads in flight.
+        S st0, st1;
+        load_step(0, st0);
+        load_step(1, st1);
+        store_step(st0, 0);
+        load_step(2, st0);
         __syncthreads();
-        load_step(s + 4, st0);
+        for (int s = 0; s < nsteps; s += 2) {
+            step(0, st1);
+            __syncthreads();
+            load_step(s + 3, st1);
+            if (s + 1 >= nsteps) break;
+            step(1, st0);
+            __syncthreads();
+            load_step(s + 4, st0);
+        }
     }
 
     // ---- epilogue.  D layout: lane holds rows 4 * (lane / 16) + e, column
@@ -461,7 +496,7 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 }
 
 struct GemmConfig {
-    int bm = 128, bn = 128, splits = 1;
+    int bm = 128, bn = 128, splits = 1, deep = 0;
 };
 
 // Tile and split choice, from sweeps of every tile variant and split count
@@ -490,7 +525,9 @@ GemmConfig choose_gemm(int kind, int m, int k, int n) {
     if (m <= 128) {
         // INT4 with 64 < M <= 128: 64 x 64 tiles halve the nibble unpacking
         // per MFMA (K = 2048, N = 5632, M = 128: 27.0 us vs 34.2 us).
-        cfg.bm = (kind == 2 && m > 64) ? 64 : 32;
+        // M <= 16 (and INT8 M <= 32): 16-row tiles, no MFMA rows wasted on
+        // padding.
+        cfg.bm = (kind == 2 && m > 64) ? 64 : ((m <= 16 || (kind != 2 && m <= 32)) ? 16 : 32);
         cfg.bn = 64;
         const long tiles = tiles_of(cfg.bm, cfg.bn);
         while (s * 2 <= 8 && tiles * s * 2 <= 512 &&
@@ -509,21 +546,38 @@ GemmConfig choose_gemm(int kind, int m, int k, int n) {
         if (kind == 0 && s == 1 && cfg.bm == 64) cfg.bn = 64;
     }
     cfg.splits = s;
-    // Tuning override for measurement sweeps: VELOMIND_GEMM_CFG="BM,BN,S".
+    // M <= 32: every K step of a split in flight at once (8 steps INT8, 4
+    // INT4, whose scale registers double a step's), with as many more splits
+    // as that needs (at most kMaxSplits).  K = 2048, N = 5632: M = 16 INT8
+    // 13.3 -> 10.9 us, INT4 15.5 -> 12.5; M = 32 INT8 15.7 -> 12.8.
+    if (m <= 32) {
+        const int deep = kind == 2 ? 4 : 8;
+        const int need = (steps + deep - 1) / deep;
+        if (need <= kMaxSplits) {
+            cfg.deep = deep;
+            cfg.splits = std::max(s, need);
+        }
+    }
+    // Tuning override for measurement sweeps: VELOMIND_GEMM_CFG="BM,BN,S"
+    // or "BM,BN,S,D" (D = steps in flight, 4 or 8, for 16 x 64 and 32 x 64).
     if (const char* env = std::getenv("VELOMIND_GEMM_CFG")) {
-        int bm = 0, bn = 0, sx = 0;
-        if (std::sscanf(env, "%d,%d,%d", &bm, &bn, &sx) == 3 && sx >= 1 && sx <= kMaxSplits &&
+        int bm = 0, bn = 0, sx = 0, d = 0;
+        const int got = std::sscanf(env, "%d,%d,%d,%d", &bm, &bn, &sx, &d);
+        const bool deep_ok = d == 0 || ((d == 4 || d == 8) && bn == 64 && (bm == 16 || bm == 32) &&
+                                        (steps + sx - 1) / sx <= d);
+        if (got >= 3 && sx >= 1 && sx <= kMaxSplits && deep_ok &&
             ((bn == 128 && (bm == 16 || bm == 32 || bm == 64 || bm == 128)) ||
-             (bn == 64 && (bm == 32 || bm == 64)))) {
+             (bn == 64 && (bm == 16 || bm == 32 || bm == 64)))) {
             cfg.bm = bm;
             cfg.bn = bn;
             cfg.splits = sx;
+            cfg.deep = d;
         }
     }
     return cfg;
 }
 
-template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
+template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N, int DEEP = 0>
 int launch(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n, int block_size,
            int splits, hipStream_t stream) {
     const int tiles_n = (n + BN - 1) / BN;
@@ -541,7 +595,8 @@ int launch(const float* a, const uint8_t* wq, const float* scale, float* c, int 
     const uint32_t code_bytes =
         static_cast<uint32_t>((KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : static_cast<int64_t>(k)) * n);
     const uint32_t scale_bytes = static_cast<uint32_t>((KIND == 0 ? 1 : nblk) * n * 4);
-    hipLaunchKernelGGL((qmm_mfma_kernel<KIND, BM, BN, WAVES_M, WAVES_N>), dim3(tiles_n * tiles_m * splits),
+    if (DEEP > 0 && sps > DEEP) return fail_inval("QuantizedMatMul: internal error: K steps per split exceed the pipeline depth");
+    hipLaunchKernelGGL((qmm_mfma_kernel<KIND, BM, BN, WAVES_M, WAVES_N, DEEP>), dim3(tiles_n * tiles_m * splits),
                        dim3(kThreads), 0, stream, a, wq, scale, c, m, k, n, block_size, sps, tiles_n, tiles_m,
                        a_bytes, code_bytes, scale_bytes, ws.partials, ws.counters);
     return check_launch("QuantizedMatMul", stream);
@@ -551,6 +606,15 @@ template <int KIND>
 int launch_kind(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
                 int block_size, hipStream_t stream) {
     const GemmConfig cfg = choose_gemm(KIND, m, k, n);
+    if (cfg.deep == 8) {
+        if (cfg.bm == 16) return launch<KIND, 16, 64, 1, 4, 8>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        return launch<KIND, 32, 64, 2, 2, 8>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+    }
+    if (cfg.deep == 4) {
+        if (cfg.bm == 16) return launch<KIND, 16, 64, 1, 4, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        return launch<KIND, 32, 64, 2, 2, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+    }
+    if (cfg.bn == 64 && cfg.bm == 16) return launch<KIND, 16, 64, 1, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
     if (cfg.bn == 128) {
         if (cfg.bm == 16) return launch<KIND, 16, 128, 1, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
         if (cfg.bm == 32) return launch<KIND, 32, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
