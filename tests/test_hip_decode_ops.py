@@ -184,9 +184,12 @@ def test_rope_kv_append(hip):
     assert np.array_equal(dv.download(np.float32, vc.shape), vc)
 
 
+# (512, 0, ...) is TinyLlama's 512-token prefill (eight 64-key tiles for the
+# last query rows); (256, 300, ...) continues a cached prefix.
 @pytest.mark.parametrize("rows,p0,heads,kv_heads,max_seq", [(19, 0, 8, 2, 96), (64, 0, 8, 2, 96), (70, 10, 8, 2, 96),
                                                         (200, 0, 32, 4, 256), (130, 77, 15, 5, 256),
-                                                        (1, 40, 8, 8, 64)])
+                                                        (1, 40, 8, 8, 64), (512, 0, 32, 4, 768),
+                                                        (256, 300, 16, 4, 768)])
 def test_attention_prefill(hip, rows, p0, heads, kv_heads, max_seq):
     d = 64
     rng = np.random.default_rng(rows + p0)

@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kNormT) void add_rmsnorm_slices_kernel(float* __res
 #pragma unroll
             for (int u = 0; u < NV; ++u)
                 // Past the row a load would reach the next slice: read zeros instead.
-                dv[e][u] = buffer_load16(drs, (s0 + e < slices && 4 * (threadIdx.x + u * kNormT) < dim)
+                dv[e][u] = buffer_load16(drs, (s0 + e < slices && 4 * static_cast<int>(threadIdx.x + u * kNormT) < dim)
                                                   ? (static_cast<uint32_t>(s0 + e) * row_bytes +
                                                      (threadIdx.x + u * kNormT) * 16u)
                                                   : 0xfffffff0u);
