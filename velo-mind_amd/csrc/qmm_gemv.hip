@@ -494,7 +494,8 @@ constexpr long kLdsBudget = 60 * 1024;
 //     chunk (all loads in flight at once), on tiles of at least 64 (INT4) or
 //     32 (INT8) columns, with at most 256 workgroups of at most 64 KB (INT4)
 //     or 32 KB (INT8) of codes each, and takes the fewest tree levels, then
-//     the fewest waves (idle row groups cost time), then the narrowest tile;
+//     the fewest waves (idle row groups cost time), then the narrowest tile
+//     (with 2-4 activation rows, four waves on those tiles and splits);
 //   - larger shapes that none of these fit are bandwidth-bound: wide tiles
 //     and enough workgroups to fill the GPU (70B-class projections, e.g.
 //     28672 x 8192 INT4: 3.6 -> 4.1 TB/s against the previous fallback).
@@ -546,6 +547,12 @@ GemvConfig choose_config(int kind, int m, int k, int n) {
                 }
             }
         }
+        // Two or four activation rows: the same tiles and splits on four
+        // waves, each row group taking two chunks (M = 2 / 4, TinyLlama
+        // gate 2048 x 5632: 7.49 -> 7.14 / 9.24 -> 8.64 us; down 5632 x 2048:
+        // 8.15 -> 7.83 / 9.99 -> 9.40 us).
+        if (found && mr >= 2 && cfg.W == 8 && geometry(mr, k, n, cfg.L, 4, cfg.splits).lds_bytes <= kLdsBudget)
+            cfg = make_config(mr, k, n, cfg.L, 4, cfg.splits);
     }
     if (!found) {
         // Bandwidth-bound shapes (tens of MB and more): 128-column tiles
