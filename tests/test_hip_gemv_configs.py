@@ -55,3 +55,32 @@ def test_forced_config(hip, monkeypatch, L, W, kind):
             out = hip.run_qmm(x, q, s, k, qt, block)
             _check(out, ref)
     monkeypatch.delenv("VELOMIND_GEMV_CFG")
+
+
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+@pytest.mark.parametrize("splits", [7, 13, 31])
+def test_deep_split_trees(hip, monkeypatch, kind, splits):
+    """Split-K trees of up to five levels with unpaired nodes (7, 13 and 31
+    splits of K = 3968, 496 chunks), one and three activation rows."""
+    k, n = 3968, 256
+    rng = np.random.default_rng(splits * 10 + len(kind))
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    if kind == "int8":
+        q, s = O.quantize_int8(w)
+        qt, block, oq = hip.QUANT_INT8, 0, O.QUANT_INT8
+    else:
+        q, s = O.quantize_int4(w, 32)
+        qt, block, oq = hip.QUANT_INT4, 32, O.QUANT_INT4
+    chunks = k // 8
+    cps = -(-chunks // splits)
+    assert -(-chunks // cps) == splits     # the override yields exactly this many splits
+    for m in (1, 3):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        ref = O.qmm(x, q.view(np.int8), s, k, oq, block)
+        monkeypatch.setenv("VELOMIND_GEMV_CFG", f"8,4,{splits}")
+        print(f"case deep tree S={splits} kind={kind} m={m}", flush=True)
+        out = hip.run_qmm(x, q, s, k, qt, block)
+        again = hip.run_qmm(x, q, s, k, qt, block)
+        _check(out, ref)
+        assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
+    monkeypatch.delenv("VELOMIND_GEMV_CFG")
