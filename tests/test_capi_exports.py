@@ -12,7 +12,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _declared(header: str) -> list[str]:
-    text = open(os.path.join(ROOT, "include", header)).read()
+    with open(os.path.join(ROOT, "include", header)) as f:
+        text = f.read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(vm_hip_[a-z0-9_]+)\s*\(", text)))
 
@@ -32,7 +33,8 @@ def test_abi_version_without_gpu():
 
 
 def _declared_llama() -> list[str]:
-    text = open(os.path.join(ROOT, "include", "vm_llama.h")).read()
+    with open(os.path.join(ROOT, "include", "vm_llama.h")) as f:
+        text = f.read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(vm_llama_[a-z0-9_]+)\s*\(", text)))
 
