@@ -135,7 +135,9 @@ def test_f32_to_f16_matches_ieee_rne_in_normal_range():
                         # exact ties between two float16 neighbours around 1.0
                         np.float32([1 + 2 ** -11, 1 + 3 * 2 ** -11, 2048 + 1, 2048 + 3])])
     ours = O.f32_to_f16_bits(x)
-    assert np.array_equal(ours, x.astype(np.float16).view(np.uint16))
+    with np.errstate(over="ignore"):   # 65520 and +-1e6 round to +-inf on purpose
+        ref = x.astype(np.float16)
+    assert np.array_equal(ours, ref.view(np.uint16))
     assert O.f32_to_f16_bits(np.float32([np.nan]))[0] & 0x7E00 == 0x7E00
 
 
