@@ -77,6 +77,9 @@ TEST_CASE("QuantizedMatMulAttrs defaults and ABI values", "[core]") {
     REQUIRE(MAX_OPS == 27);
     REQUIRE(static_cast<int>(DataType::Int8) == 2);
     REQUIRE(static_cast<int>(DataType::BFloat16) == 5);
+    REQUIRE(static_cast<int>(DeviceType::CPU) == 0);
+    REQUIRE(static_cast<int>(DeviceType::CUDA) == 1);
+    REQUIRE(static_cast<int>(DeviceType::ISPC) == 2);
     REQUIRE(static_cast<int>(DeviceType::HIP) == 3);
     REQUIRE(MAX_DEVICE_TYPES == 4);
     REQUIRE(static_cast<int>(QuantType::Int4) == 2);
@@ -104,6 +107,46 @@ TEST_CASE("HIP registers the reference's five QuantizedMatMul dtype keys", "[cor
     REQUIRE(internal::resolve_op_kernel(Op::QuantizedMatMul, bad, F32, DeviceType::HIP) == nullptr);
     REQUIRE(internal::resolve_op_kernel(Op::MatMul, std::vector<DataType>{F16, F16}, F16, DeviceType::HIP) == nullptr);
     REQUIRE(internal::resolve_op_kernel(Op::QuantizedMatMul, keys[0].first, F32, DeviceType::CUDA) == nullptr);
+}
+
+TEST_CASE("HIP QuantizedMatMul refuses INT4 nodes whose scales are too short", "[core][validation]") {
+    // INT4 with block_size 0 passes the operator contract with per-column
+    // scales [n] (the reference's shape_helpers.h:318-330), but the kernel
+    // reads ceil(k / 32) * n of them (quantized_matmul.cpp:67).  The HIP
+    // adapter throws before any device call, so this runs without a GPU.
+    const std::vector<DataType> key = {DataType::Float32, DataType::Int8, DataType::Float32};
+    KernelFn fn = internal::resolve_op_kernel(Op::QuantizedMatMul, key, DataType::Float32, DeviceType::HIP);
+    REQUIRE(fn != nullptr);
+    const std::int64_t k = 64, n = 40;
+    std::vector<float> a_host(k), c_host(n), s_host(2 * n);
+    std::vector<std::int8_t> w_host((k / 2) * n);
+    TensorStorage a, w, s, c;
+    a.shape = {1, k};
+    a.data = a_host.data();
+    w.shape = {k / 2, n};
+    w.dtype = DataType::Int8;
+    w.data = w_host.data();
+    s.shape = {n};
+    s.data = s_host.data();
+    c.shape = {1, n};
+    c.data = c_host.data();
+    for (TensorStorage* t : {&a, &w, &s, &c}) {
+        t->device = DeviceType::HIP;
+        t->size_bytes = storage_nbytes(*t);
+    }
+    const TensorStorage* in[3] = {&a, &w, &s};
+    TensorStorage* out[1] = {&c};
+    OpDescriptor desc{Op::QuantizedMatMul, QuantizedMatMulAttrs{QuantType::Int4, 0, false}};
+    REQUIRE_THROWS_AS(fn(in, out, &desc), std::invalid_argument);
+    // blockwise INT4 with too few block rows is refused the same way
+    OpDescriptor desc32{Op::QuantizedMatMul, QuantizedMatMulAttrs{QuantType::Int4, 32, false}};
+    s.shape = {1, n};
+    REQUIRE_THROWS_AS(fn(in, out, &desc32), std::invalid_argument);
+    // INT8 blockwise: ceil(64 / 16) = 4 block rows needed, 2 given
+    OpDescriptor desc8{Op::QuantizedMatMul, QuantizedMatMulAttrs{QuantType::Int8, 16, false}};
+    w.shape = {k, n};
+    s.shape = {2, n};
+    REQUIRE_THROWS_AS(fn(in, out, &desc8), std::invalid_argument);
 }
 
 TEST_CASE("HIP registers fp32 kernels for every operator of the LLaMA graph", "[core][registry]") {
@@ -243,6 +286,52 @@ TEST_CASE("compute_quantization_metrics edge cases", "[core][metrics]") {
     float ref[4];
     vmo_quant_metrics(a.data(), b.data(), a.size(), ref);
     REQUIRE(m2.max_diff == ref[0] && m2.rmse == ref[1] && m2.snr_db == ref[2] && m2.cosine_sim == ref[3]);
+}
+
+TEST_CASE("compute_quantization_metrics on the reference's round-trip inputs", "[core][metrics]") {
+    // tests/test_quantization.cpp:100-138: 128x256 U(-1.5, 1.5) from
+    // std::mt19937(1337) (libstdc++ uniform_real_distribution<float>), packed
+    // and unpacked by quant.cpp's schemes (the oracle's restatement here).
+    const std::size_t rows = 128, cols = 256;
+    std::vector<float> orig(rows * cols);
+    std::mt19937 rng(1337);
+    std::uniform_real_distribution<float> dist(-1.5f, 1.5f);
+    for (auto& v : orig) v = dist(rng);
+
+    std::vector<std::int8_t> q8(rows * cols);
+    std::vector<float> s8(cols), recon8(rows * cols);
+    vmo_quantize_int8_per_channel(orig.data(), q8.data(), s8.data(), rows, cols);
+    vmo_dequantize_int8_per_channel(q8.data(), s8.data(), recon8.data(), rows, cols);
+    const auto m8 = compute_quantization_metrics(orig.data(), recon8.data(), orig.size());
+    float r8[4];
+    vmo_quant_metrics(orig.data(), recon8.data(), orig.size(), r8);
+    REQUIRE(m8.max_diff == r8[0]);
+    REQUIRE(m8.rmse == r8[1]);
+    REQUIRE(m8.snr_db == r8[2]);
+    REQUIRE(m8.cosine_sim == r8[3]);
+    REQUIRE(m8.max_diff < 0.025f);
+    REQUIRE(m8.rmse < 0.01f);
+    REQUIRE(m8.cosine_sim > 0.999f);
+    REQUIRE(m8.snr_db > 40.0f);
+
+    const std::size_t bs = 32, nblk = (rows + bs - 1) / bs;
+    std::vector<std::uint8_t> q4(((rows + 1) / 2) * cols);
+    std::vector<float> s4(nblk * cols), recon4(rows * cols);
+    vmo_quantize_int4_block(orig.data(), q4.data(), s4.data(), rows, cols, bs);
+    vmo_dequantize_int4_block(q4.data(), s4.data(), recon4.data(), rows, cols, bs);
+    const auto m4 = compute_quantization_metrics(orig.data(), recon4.data(), orig.size());
+    float r4[4];
+    vmo_quant_metrics(orig.data(), recon4.data(), orig.size(), r4);
+    REQUIRE(m4.max_diff == r4[0]);
+    REQUIRE(m4.rmse == r4[1]);
+    REQUIRE(m4.snr_db == r4[2]);
+    REQUIRE(m4.cosine_sim == r4[3]);
+    REQUIRE(m4.max_diff < 0.15f);
+    REQUIRE(m4.rmse < 0.08f);
+    REQUIRE(m4.cosine_sim > 0.99f);
+    REQUIRE(m4.snr_db > 20.0f);
+    // the two schemes are told apart: INT4's error is several times INT8's
+    REQUIRE(m4.rmse > 4.0f * m8.rmse);
 }
 
 TEST_CASE("quantize_storage rank and block checks", "[core][validation]") {

@@ -45,6 +45,19 @@ void quantized_matmul_hip_impl(const pConstTensorStorage* in, const pTensorStora
     for (std::size_t i = 0; i + 1 < c->shape.size(); ++i) rows *= c->shape[i];
 
     const int qt = qa.quant_type == QuantType::Int4 ? VM_HIP_QUANT_INT4 : VM_HIP_QUANT_INT8;
+    // The kernels read ceil(k / bs) * n scales, with bs = 32 for INT4 when
+    // block_size <= 0 (quantized_matmul.cpp:67).  The operator contract lets
+    // such an INT4 node through with per-column scales [n]
+    // (shape_helpers.h:318-330); on the device that would read past the
+    // allocation, so it is refused here instead.
+    const std::int64_t bs = (qt == VM_HIP_QUANT_INT4 && qa.block_size <= 0) ? 32 : qa.block_size;
+    const std::int64_t nblk = bs > 0 ? (k + bs - 1) / bs : 1;
+    const std::uint64_t need_scales = static_cast<std::uint64_t>(k > 0 ? nblk : 0) * static_cast<std::uint64_t>(n);
+    if (storage_numel(*s) < need_scales)
+        throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") + ": scales hold " +
+                                    std::to_string(storage_numel(*s)) + " values, the kernel reads " +
+                                    std::to_string(need_scales) + " (" + std::to_string(nblk) + " blocks of " +
+                                    std::to_string(bs > 0 ? bs : k) + " rows x " + std::to_string(n) + " columns)");
     const int status = vm_hip_qmm(a->data, dtype_code<TAct>(), static_cast<const std::int8_t*>(w->data), s->data,
                                   dtype_code<TScale>(), c->data, dtype_code<TOut>(), rows, k, n, qt, qa.block_size,
                                   current_stream());
