@@ -32,8 +32,21 @@ public:
         std::vector<pConstTensorStorage> inputs;
         std::vector<pTensorStorage> outputs;
         std::shared_ptr<const void> attrs;  // the node's OpDescriptor
-        std::vector<TensorStorage> input_metadata;
-        std::vector<TensorStorage> output_metadata;
+    };
+
+    // A storage the plan reads or writes, with the metadata it had at build
+    // time.  Each storage appears once, however many nodes touch it.
+    struct WatchedStorage {
+        pConstTensorStorage live = nullptr;
+        TensorStorage frozen;
+    };
+
+    // Embedding node whose device-resident indices are read back and range
+    // checked before the node launches.
+    struct IndexGuard {
+        std::size_t node = 0;               // position in topo
+        pConstTensorStorage indices = nullptr;
+        dim_t vocab_rows = 0;
     };
 
     struct Impl {
@@ -41,9 +54,14 @@ public:
         std::weak_ptr<void> graph_lifetime;
         DeviceType device = DeviceType::CPU;
         std::vector<CompiledNode> topo;
+        std::vector<WatchedStorage> watched;
+        std::vector<IndexGuard> index_guards;   // ascending node order
         MemoryPlanStats plan_stats;
         // Backend execution context created by the device's context hook.
         std::shared_ptr<void> device_context;
+
+        // Fills `watched` and `index_guards` from `topo` (called once, at build).
+        void derive_run_plan();
     };
 
     Executable() = default;

@@ -1,11 +1,22 @@
-// Executable: runs compiled nodes in order under the device's execution
-// context and synchronizes at the boundary (the reference's
-// src/executable.cpp, with the CUDA #ifdefs replaced by the registered
-// device-context hooks).
+// Executable: replays a compiled plan.
+//
+// The work that does not depend on the run is done once, at build
+// (Impl::derive_run_plan): the set of distinct storages the plan touches,
+// each with a frozen copy of its metadata, and the positions of the
+// Embedding nodes whose indices must be range checked on the host.  A run
+// then (1) verifies every watched storage against its frozen copy, before
+// anything is launched, so a bad tensor late in the plan cannot leave
+// earlier outputs half-written; (2) enqueues the kernels in order under the
+// device's execution context, pausing at each index guard to drain the
+// context and read the indices back; (3) drains the context before
+// returning.  The device context hooks stand in for the reference's CUDA
+// blocks; the checks, their order and messages are the reference's contract
+// (src/executable.cpp:27-81, :83-109).
 #include "velomind/executable.h"
 
 #include <cstdint>
 #include <stdexcept>
+#include <unordered_set>
 #include <vector>
 
 #include "internal/registry/device_context.h"
@@ -14,15 +25,91 @@
 
 namespace velomind {
 
+namespace {
+
+// Waits for the work enqueued on an executable's context, if it has one.
+class ContextDrain {
+public:
+    ContextDrain(DeviceType device, void* ctx) : _sync(internal::get_device_context_hooks(device).synchronize), _ctx(ctx) {}
+    void operator()() const {
+        if (_sync && _ctx) _sync(_ctx);
+    }
+
+private:
+    void (*_sync)(void*) = nullptr;
+    void* _ctx = nullptr;
+};
+
+void require_live(const Executable::Impl* impl, const char* who) {
+    if (!impl) throw std::logic_error(std::string(who) + ": not built");
+    if (impl->graph_lifetime.expired()) throw std::logic_error(std::string(who) + ": owning graph has been destroyed");
+}
+
+bool same_layout(const TensorStorage& a, const TensorStorage& b) {
+    return a.shape == b.shape && a.dtype == b.dtype && a.device == b.device && a.size_bytes == b.size_bytes;
+}
+
+void verify_watched(const Executable::WatchedStorage& w) {
+    if (!same_layout(*w.live, w.frozen))
+        throw std::invalid_argument("Executable::execute: tensor metadata changed after build");
+    if (!w.live->data && storage_nbytes(*w.live) > 0)
+        throw std::invalid_argument("Executable::execute: tensor buffer is null");
+}
+
+// Embedding indices may be produced by an earlier node on the device, so
+// the guard drains the context first and checks the values actually there
+// (the reference's executable.cpp:54-72).
+void check_index_guard(const Executable::IndexGuard& g, const ContextDrain& drain) {
+    const std::size_t count = storage_numel(*g.indices);
+    if (count == 0) return;
+    drain();
+    const auto transfer = internal::get_memory_transfer(g.indices->device);
+    if (!transfer.copy_d2h) throw std::runtime_error("Embedding: no index readback transfer");
+    std::vector<std::int32_t> host(count);
+    transfer.copy_d2h(host.data(), g.indices->data, count * sizeof(std::int32_t));
+    for (const std::int32_t v : host)
+        if (v < 0 || static_cast<dim_t>(v) >= g.vocab_rows)
+            throw std::invalid_argument("Embedding: index out of vocabulary range");
+}
+
+// First violated rule of Executable::bind_input, or nullptr (the rules and
+// their order are the reference's, src/executable.cpp:83-109).
+const char* bind_violation(const TensorStorage& slot, const ExternalBuffer& buf, DeviceType plan_device) {
+    if (buf.device != plan_device || slot.device != plan_device) return "device mismatch";
+    if (buf.capacity_bytes < slot.size_bytes) return "insufficient buffer capacity";
+    const bool needs_memory = slot.size_bytes > 0;
+    if (needs_memory && (buf.data == nullptr || buf.owner == nullptr)) return "nonempty buffer requires data and owner";
+    if (buf.owner && buf.owner.get() != buf.data) return "owner must alias buffer data";
+    if (buf.data && reinterpret_cast<std::uintptr_t>(buf.data) % data_type_size(slot.dtype) != 0)
+        return "unaligned buffer";
+    return nullptr;
+}
+
+}  // namespace
+
+void Executable::Impl::derive_run_plan() {
+    watched.clear();
+    index_guards.clear();
+    std::unordered_set<pConstTensorStorage> seen;
+    auto watch = [&](pConstTensorStorage s) {
+        if (seen.insert(s).second) watched.push_back(WatchedStorage{s, *s});
+    };
+    for (std::size_t i = 0; i < topo.size(); ++i) {
+        const CompiledNode& cn = topo[i];
+        for (pConstTensorStorage s : cn.inputs) watch(s);
+        for (pConstTensorStorage s : cn.outputs) watch(s);
+        const auto& desc = *static_cast<const OpDescriptor*>(cn.attrs.get());
+        if (desc.op == Op::Embedding && cn.inputs.size() >= 2)
+            index_guards.push_back(IndexGuard{i, cn.inputs[1], cn.inputs[0]->shape.empty() ? 0 : cn.inputs[0]->shape[0]});
+    }
+}
+
 Executable::~Executable() {
-    if (_impl && _impl->device_context) {
-        const auto hooks = internal::get_device_context_hooks(_impl->device);
-        if (hooks.synchronize) {
-            try {
-                hooks.synchronize(_impl->device_context.get());
-            } catch (...) {
-            }
-        }
+    if (!_impl || !_impl->device_context) return;
+    try {
+        ContextDrain(_impl->device, _impl->device_context.get())();
+    } catch (...) {
+        // a destructor must not throw; the error was the last run's to report
     }
 }
 
@@ -30,67 +117,37 @@ Executable::Executable(Executable&&) noexcept = default;
 Executable& Executable::operator=(Executable&&) noexcept = default;
 
 auto Executable::execute() -> void {
-    if (!_impl) throw std::logic_error("Executable::execute: not built");
-    if (_impl->graph_lifetime.expired()) throw std::logic_error("Executable::execute: owning graph has been destroyed");
-    const auto check = [](const TensorStorage& now, const TensorStorage& then) {
-        if (now.shape != then.shape || now.dtype != then.dtype || now.device != then.device ||
-            now.size_bytes != then.size_bytes)
-            throw std::invalid_argument("Executable::execute: tensor metadata changed after build");
-        if (storage_nbytes(now) > 0 && !now.data) throw std::invalid_argument("Executable::execute: tensor buffer is null");
-    };
-    // Check every node first so that a bad late node cannot leave earlier
-    // outputs half-written.
-    for (const auto& cn : _impl->topo) {
-        for (std::size_t i = 0; i < cn.inputs.size(); ++i) check(*cn.inputs[i], cn.input_metadata[i]);
-        for (std::size_t i = 0; i < cn.outputs.size(); ++i) check(*cn.outputs[i], cn.output_metadata[i]);
-    }
-    const auto hooks = internal::get_device_context_hooks(_impl->device);
-    internal::ScopedDeviceContext scope(_impl->device, _impl->device_context.get());
-    for (auto& cn : _impl->topo) {
-        const auto& desc = *static_cast<const OpDescriptor*>(cn.attrs.get());
-        if (desc.op == Op::Embedding) {
-            // Indices may come from an earlier node: read them back and
-            // range-check before the gather (executable.cpp:54-72).
-            const auto& idx = *cn.inputs[1];
-            const auto count = storage_numel(idx);
-            std::vector<std::int32_t> host(count);
-            if (count) {
-                if (hooks.synchronize && _impl->device_context) hooks.synchronize(_impl->device_context.get());
-                const auto t = internal::get_memory_transfer(idx.device);
-                if (!t.copy_d2h) throw std::runtime_error("Embedding: no index readback transfer");
-                t.copy_d2h(host.data(), idx.data, count * sizeof(std::int32_t));
-            }
-            for (auto v : host)
-                if (v < 0 || v >= cn.inputs[0]->shape[0])
-                    throw std::invalid_argument("Embedding: index out of vocabulary range");
-        }
+    require_live(_impl.get(), "Executable::execute");
+    Impl& plan = *_impl;
+    for (const WatchedStorage& w : plan.watched) verify_watched(w);
+
+    const ContextDrain drain(plan.device, plan.device_context.get());
+    internal::ScopedDeviceContext scope(plan.device, plan.device_context.get());
+    auto guard = plan.index_guards.cbegin();
+    for (std::size_t i = 0; i < plan.topo.size(); ++i) {
+        for (; guard != plan.index_guards.cend() && guard->node == i; ++guard) check_index_guard(*guard, drain);
+        const CompiledNode& cn = plan.topo[i];
         cn.kernel(cn.inputs.data(), cn.outputs.data(), cn.attrs.get());
     }
-    if (hooks.synchronize && _impl->device_context) hooks.synchronize(_impl->device_context.get());
+    drain();
 }
 
 auto Executable::bind_input(Tensor t, ExternalBuffer buf) -> void {
-    if (!_impl) throw std::logic_error("Executable::bind_input: not built");
-    if (_impl->graph_lifetime.expired()) throw std::logic_error("Executable::bind_input: owning graph has been destroyed");
+    require_live(_impl.get(), "Executable::bind_input");
     if (t.graph() != _impl->graph || !t.storage()) throw std::invalid_argument("Executable::bind_input: invalid or foreign tensor");
-    auto* g = const_cast<Graph*>(_impl->graph);
-    if (!g->is_input_tensor(t.index())) throw std::invalid_argument("Executable::bind_input: tensor is not a graph input");
-    auto* s = g->tensor_storage_at(t.index());
-    if (buf.device != _impl->device || s->device != _impl->device)
-        throw std::invalid_argument("Executable::bind_input: device mismatch");
-    if (buf.capacity_bytes < s->size_bytes) throw std::invalid_argument("Executable::bind_input: insufficient buffer capacity");
-    if (s->size_bytes > 0 && (!buf.data || !buf.owner))
-        throw std::invalid_argument("Executable::bind_input: nonempty buffer requires data and owner");
-    if (buf.owner && buf.owner.get() != buf.data) throw std::invalid_argument("Executable::bind_input: owner must alias buffer data");
-    if (buf.data && reinterpret_cast<std::uintptr_t>(buf.data) % data_type_size(s->dtype) != 0)
-        throw std::invalid_argument("Executable::bind_input: unaligned buffer");
-    s->external_owner = std::move(buf.owner);
-    s->data = buf.data;
+    auto* owner_graph = const_cast<Graph*>(_impl->graph);
+    if (!owner_graph->is_input_tensor(t.index()))
+        throw std::invalid_argument("Executable::bind_input: tensor is not a graph input");
+    TensorStorage* slot = owner_graph->tensor_storage_at(t.index());
+    if (const char* why = bind_violation(*slot, buf, _impl->device))
+        throw std::invalid_argument(std::string("Executable::bind_input: ") + why);
+    slot->data = buf.data;
+    slot->external_owner = std::move(buf.owner);
 }
 
 auto Executable::output(Tensor t) -> pTensorStorage {
-    if (!_impl || _impl->graph_lifetime.expired() || t.graph() != _impl->graph) return nullptr;
-    return const_cast<Graph*>(_impl->graph)->tensor_storage_at(t.index());
+    const auto* self = this;
+    return const_cast<pTensorStorage>(self->output(t));
 }
 
 auto Executable::output(Tensor t) const -> pConstTensorStorage {

@@ -237,13 +237,11 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         for (auto* in : node->inputs()) {
             auto* s = remap.at(in);
             cn.inputs.push_back(s);
-            cn.input_metadata.push_back(*s);
             dtypes.push_back(in->dtype);
         }
         for (auto* out : node->outputs()) {
             auto* s = remap.at(out);
             cn.outputs.push_back(s);
-            cn.output_metadata.push_back(*s);
         }
         if (cn.outputs.empty()) throw std::runtime_error("velomind: op node has no outputs");
         cn.kernel = resolve_op_kernel(node->op().op, dtypes, node->outputs().front()->dtype, device);
@@ -252,6 +250,7 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
                                                [](const void* p) { delete static_cast<const OpDescriptor*>(p); });
         impl->topo.push_back(std::move(cn));
     }
+    impl->derive_run_plan();
 
     // Commit.
     graph._tensors.swap(staged);
