@@ -461,9 +461,8 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
         }
     }
     if (nc == 1) return;
-    __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the ticket
     __syncthreads();
-    if (tid == 0) ticket = __hip_atomic_fetch_add(&counters[hk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) ticket = ticket_take(&counters[hk], static_cast<unsigned>(nc));
     __syncthreads();
     if (ticket != static_cast<unsigned>(nc - 1)) return;
 
@@ -1187,8 +1186,7 @@ __global__ __launch_bounds__(kAmT) void argmax_slices_multi_kernel(
     if (tid == 0) {
         coherent_store(part_v + blockIdx.x, best);
         __hip_atomic_store(part_i + blockIdx.x, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);   // partial acknowledged before the ticket
-        ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket = ticket_take(counter, gridDim.x);
     }
     __syncthreads();
     if (ticket != gridDim.x - 1) return;

@@ -30,8 +30,9 @@
 // 2^-11 at most.
 //
 // Split-K for small M: each split stores its scaled partial tile
-// with agent-scope stores, the last split of a tile (atomic ticket) adds
-// the partials in split order and writes C, so results are deterministic.
+// with agent-scope stores, the last split of a tile (acquire-release atomic
+// ticket) adds the partials in split order and writes C, so results are
+// deterministic.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -470,10 +471,9 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
                 if (row < m) coherent_store(part + static_cast<int64_t>(row) * n + col, acc[i][j][e] * colscale[j]);
             }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the ticket
     __syncthreads();
     const int tile = tile_y * tiles_n + tile_x;
-    if (tid == 0) ticket = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) ticket = ticket_take(&counters[tile], static_cast<unsigned>(splits));
     __syncthreads();
     if (ticket != static_cast<unsigned>(splits - 1)) return;
     const int64_t stride = static_cast<int64_t>(m) * n;

@@ -36,4 +36,27 @@ __device__ __forceinline__ void coherent_store(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Split-K ticket hand-off, ordered by the memory model rather than by
+// hardware write-through alone.  Every thread of the workgroup stores its
+// partials, then __syncthreads() makes those stores happen-before thread
+// 0's ticket, an agent-scope release RMW.  The RMWs on one counter form a
+// release sequence, so the thread that draws the last ticket and then
+// issues an agent-scope acquire fence synchronizes with every earlier
+// workgroup; its __syncthreads() passes that on to the rest of its
+// workgroup before they load the partials.  Only the last arriver pays for
+// the acquire.  On gfx950 the release is a buffer_wbl2 sc1 + vmcnt wait
+// before the atomic, the acquire a buffer_inv sc1.
+__device__ __forceinline__ unsigned ticket_release(unsigned* counter) {
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void ticket_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+// Thread 0's ticket with the acquire taken when it is the last of `count`.
+__device__ __forceinline__ unsigned ticket_take(unsigned* counter, unsigned count) {
+    const unsigned t = ticket_release(counter);
+    if (t == count - 1u) ticket_acquire();
+    return t;
+}
+
 }  // namespace vmhip
