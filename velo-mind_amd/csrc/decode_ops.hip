@@ -461,6 +461,7 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
         }
     }
     if (nc == 1) return;
+    publish_partials();
     __syncthreads();
     if (tid == 0) ticket = ticket_take(&counters[hk], static_cast<unsigned>(nc));
     __syncthreads();
@@ -1186,6 +1187,7 @@ __global__ __launch_bounds__(kAmT) void argmax_slices_multi_kernel(
     if (tid == 0) {
         coherent_store(part_v + blockIdx.x, best);
         __hip_atomic_store(part_i + blockIdx.x, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        publish_partials();
         ticket = ticket_take(counter, gridDim.x);
     }
     __syncthreads();

@@ -30,9 +30,8 @@
 // 2^-11 at most.
 //
 // Split-K for small M: each split stores its scaled partial tile
-// with agent-scope stores, the last split of a tile (acquire-release atomic
-// ticket) adds the partials in split order and writes C, so results are
-// deterministic.
+// with agent-scope stores, the last split of a tile (atomic ticket) adds
+// the partials in split order and writes C, so results are deterministic.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -471,6 +470,7 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
                 if (row < m) coherent_store(part + static_cast<int64_t>(row) * n + col, acc[i][j][e] * colscale[j]);
             }
     }
+    publish_partials();
     __syncthreads();
     const int tile = tile_y * tiles_n + tile_x;
     if (tid == 0) ticket = ticket_take(&counters[tile], static_cast<unsigned>(splits));
