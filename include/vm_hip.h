@@ -140,6 +140,25 @@ int vm_hip_qmm_f32(const float* a, const int8_t* wq, const float* scale, float* 
                    void* stream);
 
 /*
+ * vm_hip_qmm_f32 without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same arguments, kernels and results as vm_hip_qmm_f32.  Its split-K
+ * scratch is a static device array of VM_HIP_QMM_NOALLOC_SCRATCH_BYTES per
+ * GPU (VM_HIP_QMM_NOALLOC_COUNTER_BYTES of counters, the rest fp32
+ * partials), held until the process ends; a shape that needs more returns
+ * VM_HIP_EINVAL before launching anything.  All calls on one GPU share that
+ * array: calls that overlap on one GPU (other streams, other host threads)
+ * race and must be serialized by the caller.
+ */
+#define VM_HIP_QMM_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define VM_HIP_QMM_NOALLOC_COUNTER_BYTES (2u << 20)
+int vm_hip_qmm_f32_noalloc(const float* a, const int8_t* wq, const float* scale, float* c,
+                           int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size,
+                           void* stream);
+
+/*
  * Same operation for the reference's mixed-precision dtype keys
  * (src/cpu/ops/quantized_matmul.cpp:363-367): (a, scale, c) dtypes in
  * {(F32,F32,F32), (F16,F16,F16), (F16,F32,F16), (BF16,BF16,BF16),

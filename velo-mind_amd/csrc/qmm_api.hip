@@ -117,9 +117,7 @@ int generic_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float
 
 }  // namespace vmhip
 
-using namespace vmhip;
-
-namespace {
+namespace vmhip {
 
 int validate_qmm(const void* a, const int8_t* wq, const void* scale, const void* c, int64_t m,
                  int64_t k, int64_t n, int quant_type, int block_size) {
@@ -160,7 +158,9 @@ int qmm_f32_impl(const float* a, const int8_t* wq, const float* scale, float* c,
     return rc;
 }
 
-}  // namespace
+}  // namespace vmhip
+
+using namespace vmhip;
 
 extern "C" {
 

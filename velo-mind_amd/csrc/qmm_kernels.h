@@ -21,4 +21,13 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
 int generic_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                     int n, int quant_type, int block_size, hipStream_t stream);
 
+// Argument checks of vm_hip_qmm_f32 (0 or an error status).
+int validate_qmm(const void* a, const int8_t* wq, const void* scale, const void* c, int64_t m, int64_t k,
+                 int64_t n, int quant_type, int block_size);
+
+// Routing behind vm_hip_qmm_f32 for validated arguments: GEMV (rows <= 4),
+// MFMA GEMM (rows > 4) or the generic kernel.
+int qmm_f32_impl(const float* a, const int8_t* wq, const float* scale, float* c, int64_t m, int64_t k,
+                 int64_t n, int quant_type, int block_size, hipStream_t stream);
+
 }  // namespace vmhip

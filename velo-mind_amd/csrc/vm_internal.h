@@ -54,6 +54,30 @@ void release_workspace(hipStream_t stream);
 // previous contents are not preserved across growth).
 int get_staging(hipStream_t stream, std::size_t bytes, void** out);
 
+// While an instance is alive, get_workspace() on this thread hands out the
+// caller's fixed region (counters first, then partials) instead of the
+// per-stream allocation, and fails with a message naming `who` when a call
+// needs more than the region holds; get_staging() fails.  Used by the entry
+// points that must not allocate.
+struct FixedRegion {
+    void*       base = nullptr;
+    std::size_t counter_slots = 0;
+    std::size_t partial_floats = 0;
+    const char* who = "";
+};
+
+class FixedWorkspaceScope {
+public:
+    FixedWorkspaceScope(void* base, std::size_t counter_slots, std::size_t partial_floats, const char* who);
+    ~FixedWorkspaceScope();
+    FixedWorkspaceScope(const FixedWorkspaceScope&) = delete;
+    FixedWorkspaceScope& operator=(const FixedWorkspaceScope&) = delete;
+
+private:
+    FixedRegion _region;
+    const FixedRegion* _previous;
+};
+
 // Number of compute units of the current device (cached per device).
 int cu_count();
 

@@ -38,6 +38,8 @@ struct StagingEntry {
 };
 std::map<std::pair<int, hipStream_t>, StagingEntry> g_staging;
 
+thread_local const FixedRegion* t_fixed = nullptr;
+
 int current_device() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -92,8 +94,27 @@ int check_launch(const char* op, hipStream_t stream) {
     return 0;
 }
 
+FixedWorkspaceScope::FixedWorkspaceScope(void* base, std::size_t counter_slots, std::size_t partial_floats,
+                                         const char* who)
+    : _region{base, counter_slots, partial_floats, who}, _previous(t_fixed) {
+    t_fixed = &_region;
+}
+
+FixedWorkspaceScope::~FixedWorkspaceScope() { t_fixed = _previous; }
+
 int get_workspace(hipStream_t stream, std::size_t partial_floats, std::size_t counter_slots,
                   Workspace* out) {
+    if (const FixedRegion* f = t_fixed) {
+        const std::size_t counter_bytes = f->counter_slots * sizeof(unsigned);
+        if (counter_slots > f->counter_slots || partial_floats > f->partial_floats)
+            return fail_inval(std::string(f->who) + ": this shape's split-K scratch needs " +
+                              std::to_string(counter_slots * sizeof(unsigned)) + " bytes of counters and " +
+                              std::to_string(partial_floats * sizeof(float)) + " bytes of partials; the static scratch holds " +
+                              std::to_string(counter_bytes) + " and " + std::to_string(f->partial_floats * sizeof(float)));
+        out->counters = static_cast<unsigned*>(f->base);
+        out->partials = reinterpret_cast<float*>(static_cast<char*>(f->base) + counter_bytes);
+        return 0;
+    }
     const int dev = current_device();
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     WsEntry& e = g_ws[{dev, stream}];
@@ -154,6 +175,8 @@ void release_workspace(hipStream_t stream) {
 }
 
 int get_staging(hipStream_t stream, std::size_t bytes, void** out) {
+    if (const FixedRegion* f = t_fixed)
+        return fail_inval(std::string(f->who) + ": dtype staging would allocate; only fp32 operands are accepted");
     const int dev = current_device();
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     StagingEntry& e = g_staging[{dev, stream}];

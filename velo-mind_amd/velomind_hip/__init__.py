@@ -71,6 +71,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_graph_launch": ([p, p], c_int),
         "vm_hip_graph_destroy": ([p], c_int),
         "vm_hip_qmm_f32": ([p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
+        "vm_hip_qmm_f32_noalloc": ([p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_qmm": ([p, c_int, p, p, c_int, p, c_int, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_pack_int8": ([p, p, p, c_int64, c_int64, p], c_int),
         "vm_hip_pack_int4": ([p, p, p, c_int64, c_int64, c_int64, p], c_int),
@@ -128,7 +129,8 @@ def exported_symbols() -> list[str]:
             "vm_hip_stream_destroy", "vm_hip_stream_synchronize", "vm_hip_event_create",
             "vm_hip_event_destroy", "vm_hip_event_record", "vm_hip_event_synchronize",
             "vm_hip_event_elapsed_ms", "vm_hip_stream_begin_capture", "vm_hip_stream_end_capture",
-            "vm_hip_graph_launch", "vm_hip_graph_destroy", "vm_hip_qmm_f32", "vm_hip_qmm", "vm_hip_pack_int8",
+            "vm_hip_graph_launch", "vm_hip_graph_destroy", "vm_hip_qmm_f32", "vm_hip_qmm_f32_noalloc", "vm_hip_qmm",
+            "vm_hip_pack_int8",
             "vm_hip_pack_int4", "vm_hip_dequant_int8", "vm_hip_dequant_int4", "vm_hip_half_to_f32",
             "vm_hip_embedding_f32", "vm_hip_rmsnorm_f32", "vm_hip_rope_f32", "vm_hip_transpose_f32",
             "vm_hip_slice_f32", "vm_hip_concat_f32", "vm_hip_repeat_kv_f32", "vm_hip_elementwise_f32",
@@ -299,6 +301,12 @@ def qmm_f32(a: int, wq: int, scale: int, c: int, m: int, k: int, n: int, quant_t
             block_size: int, stream=None) -> None:
     """vm_hip_qmm_f32 on raw device addresses."""
     check(open_library().vm_hip_qmm_f32(a, wq, scale, c, m, k, n, quant_type, block_size, _h(stream)))
+
+
+def qmm_f32_noalloc(a: int, wq: int, scale: int, c: int, m: int, k: int, n: int, quant_type: int,
+                    block_size: int, stream=None) -> None:
+    """vm_hip_qmm_f32_noalloc on raw device addresses (static split-K scratch)."""
+    check(open_library().vm_hip_qmm_f32_noalloc(a, wq, scale, c, m, k, n, quant_type, block_size, _h(stream)))
 
 
 def qmm(a: int, a_dtype: int, wq: int, scale: int, scale_dtype: int, c: int, c_dtype: int, m: int,
