@@ -204,6 +204,69 @@ class LlamaConfig:
         return self.hidden_size // self.num_heads
 
 
+# ------------------------------------------- linears: exact, dense, GPU-rounded
+
+# How a packed Linear computes (Linear.mode):
+#   LINEAR_EXACT  the C oracle's QuantizedMatMul (quantized_matmul.cpp:48-267,
+#                 the reference's own loop order; slow, the default)
+#   LINEAR_DENSE  dequantized weights (quant.cpp:106-123, :177-209) times x
+#                 with fp32 BLAS: the same sum in another order, for models
+#                 too large for the scalar loop
+#   LINEAR_HIP    LINEAR_DENSE, except that products with more than
+#                 HIP_GEMV_MAX_ROWS rows use the weights as the HIP MFMA path
+#                 stages them (round_block_weights: blockwise weights rounded
+#                 to fp16 once, a fixed function of the weights).  That path
+#                 takes the activations at fp32-equivalent precision
+#                 (split_rows_fp16), so nothing activation-dependent is
+#                 rounded and GPU results can be held to fp32-summation bounds
+LINEAR_EXACT, LINEAR_DENSE, LINEAR_HIP = "exact", "dense", "hip"
+HIP_GEMV_MAX_ROWS = 4
+
+
+def split_rows_fp16(x: np.ndarray) -> np.ndarray:
+    """The HIP MFMA path's staging of A (rows > 4): row r is scaled by 2^x_r
+    with max|row| * 2^x_r in [2^14, 2^15) (x_r = 0 for an all-zero row or one
+    holding an infinity or NaN) and split into hi = fp16(a * 2^x_r) and
+    lo = fp16(a * 2^x_r - hi) (fp16 rounding to nearest even, subnormals
+    included); returns (hi + lo) * 2^-x_r in float64, the value the MFMAs
+    multiply (22 significant bits of each element)."""
+    x = np.ascontiguousarray(x, f32)
+    special = ~np.isfinite(x).all(axis=-1)
+    amax = np.where(special, f32(0), np.abs(x).max(axis=-1) if x.shape[-1] else f32(0))
+    _, e = np.frexp(amax.astype(np.float64))
+    xr = np.where(amax > 0, 15 - e, 0).astype(np.int64)
+    scaled = np.ldexp(x.astype(np.float64), xr[..., None]).astype(f32)          # exact
+    with np.errstate(over="ignore", invalid="ignore"):
+        hi = scaled.astype(np.float16)
+        rest = scaled - hi.astype(f32)                                          # exact in fp32
+        rest = np.where(np.isfinite(rest) & (np.abs(rest) <= 65504), rest, f32(0))
+        lo = rest.astype(np.float16)
+        total = hi.astype(np.float64) + lo.astype(np.float64)
+    return np.ldexp(total, -xr[..., None])
+
+
+def round_block_weights(codes: np.ndarray, scales: np.ndarray, block: int) -> np.ndarray:
+    """numpy restatement of the C oracle's vmo_hip_block_weights (which
+    Linear.gemm_weights uses for speed; the two are checked against each
+    other).  The HIP MFMA path's blockwise weights: with 2^e per column (max scale
+    / 2^e in [0.5, 1)), w = fp16(code * fp16(s / 2^e)) * 2^e, both roundings
+    to nearest even.  (The kernel takes e over each workgroup's K range; the
+    roundings are relative and so independent of e while s / 2^e stays in
+    fp16's normal range, as it does unless a block scale is 2^14 times
+    smaller than its column's largest.)  codes: [K, N] integers; scales:
+    [ceil(K / block), N].  Returns fp32 [K, N] (exact)."""
+    k = codes.shape[0]
+    sc = np.ascontiguousarray(scales, f32)
+    smax = sc.max(axis=0)
+    _, e = np.frexp(np.where(smax > 0, smax, 1).astype(np.float64))
+    e = np.where(smax > 0, e, 0).astype(np.int64)
+    s16 = np.ldexp(sc.astype(np.float64), -e[None, :]).astype(np.float16).astype(f32)
+    rows = np.repeat(s16, block, axis=0)[:k]
+    prod = codes.astype(f32) * rows                      # exact in fp32
+    prod16 = prod.astype(np.float16).astype(f32)
+    return np.ldexp(prod16, e[None, :].astype(np.int32)).astype(f32)
+
+
 @dataclass
 class Linear:
     """One linear of the graph: fp32 W [K, N], or packed codes + scales
@@ -215,6 +278,43 @@ class Linear:
     n: int = 0
     quant_type: int = 0
     block: int = 0
+    mode: str = LINEAR_EXACT
+    _dense: np.ndarray | None = field(default=None, repr=False)
+    _gemm: np.ndarray | None = field(default=None, repr=False)
+
+    def codes(self) -> np.ndarray:
+        """Integer codes [K, N] (INT4 nibbles sign-extended, quant.cpp:17-22)."""
+        if self.quant_type == Q.QUANT_INT8:
+            return self.q.view(np.int8)
+        b = self.q.view(np.uint8)
+        lo = (b & 0xF).astype(np.int8)
+        hi = (b >> 4).astype(np.int8)
+        lo = np.where(lo >= 8, lo - 16, lo).astype(np.int8)
+        hi = np.where(hi >= 8, hi - 16, hi).astype(np.int8)
+        out = np.empty((2 * b.shape[0], b.shape[1]), np.int8)
+        out[0::2], out[1::2] = lo, hi
+        return out[: self.k]
+
+    def dense(self) -> np.ndarray:
+        """fp32 W [K, N]: as given, or dequantized by the pinned oracle."""
+        if self.quant_type == Q.QUANT_NONE:
+            return self.w
+        if self._dense is None:
+            if self.quant_type == Q.QUANT_INT8:
+                self._dense = Q.dequantize_int8(self.q.view(np.int8), self.s)
+            else:
+                self._dense = Q.dequantize_int4(self.q.view(np.uint8), self.s, self.k, self.block)
+        return self._dense
+
+    def gemm_weights(self) -> np.ndarray:
+        """W as the HIP MFMA path stages it: INT8 per-column codes are exact
+        (the scale multiplies the fp32 result), blockwise weights are
+        round_block_weights()."""
+        if self.quant_type == Q.QUANT_INT8 and self.block == 0:
+            return self.dense()
+        if self._gemm is None:
+            self._gemm = Q.hip_block_weights(self.q, self.s.reshape(-1, self.n), self.k, self.block, self.quant_type)
+        return self._gemm
 
     def __call__(self, x: np.ndarray) -> np.ndarray:
         """llama_graph.cpp:30-44 (apply_linear): QuantizedMatMul when the
@@ -222,8 +322,12 @@ class Linear:
         x2 = np.ascontiguousarray(x.reshape(-1, x.shape[-1]), dtype=f32)
         if self.quant_type == Q.QUANT_NONE:
             y = (x2 @ self.w.astype(f32)).astype(f32)
-        else:
+        elif self.mode == LINEAR_EXACT:
             y = Q.qmm(x2, self.q.view(np.int8), self.s, self.k, self.quant_type, self.block)
+        elif self.mode == LINEAR_HIP and x2.shape[0] > HIP_GEMV_MAX_ROWS:
+            y = (x2 @ self.gemm_weights()).astype(f32)
+        else:
+            y = (x2 @ self.dense()).astype(f32)
         return y.reshape(x.shape[:-1] + (y.shape[-1],))
 
 
@@ -292,6 +396,45 @@ def quantize_linears(w: LlamaWeights, quant_type: int, block: int = 0) -> LlamaW
     for name in ("wq", "wk", "wv", "wo", "gate", "up", "down"):
         setattr(out, name, [pack(lin) for lin in getattr(w, name)])
     return out
+
+
+def set_linear_mode(w: LlamaWeights, mode: str) -> LlamaWeights:
+    """Sets every packed linear of `w` (and the lm_head) to `mode`."""
+    for lin in [w.lm_head] + [lin for name in ("wq", "wk", "wv", "wo", "gate", "up", "down")
+                              for lin in getattr(w, name)]:
+        lin.mode = mode
+    return w
+
+
+def load_packed(tensors: dict, cfg: LlamaConfig, quant_type: int, block: int = 0) -> LlamaWeights:
+    """Weights from the pre-packed safetensors layout (`<hf linear name>
+    .codes` I8 [K or (K+1)/2, N], `.scales` F32, embedding and norms F32;
+    names as the HF checkpoint's, the [in, out] orientation of the graph).
+    The codes and scales are taken as they are: the oracle dequantizes
+    them, so the comparison measures the kernels, not the packing."""
+    def lin(name: str, k: int) -> Linear:
+        q = np.ascontiguousarray(tensors[name + ".codes"])
+        sc = np.ascontiguousarray(tensors[name + ".scales"], f32)
+        n = q.shape[1]
+        rows = k if quant_type == Q.QUANT_INT8 else (k + 1) // 2
+        if q.shape[0] != rows:
+            raise ValueError(f"{name}.codes: {q.shape[0]} rows, expected {rows}")
+        return Linear(q=q, s=sc, k=k, n=n, quant_type=quant_type, block=block if quant_type == Q.QUANT_INT4 else 0)
+
+    hid, inter = cfg.hidden_size, cfg.intermediate_size
+    w = LlamaWeights(embed=np.ascontiguousarray(tensors["model.embed_tokens.weight"], f32),
+                     final_norm=np.ascontiguousarray(tensors["model.norm.weight"], f32),
+                     lm_head=lin("lm_head.weight", hid))
+    for layer in range(cfg.num_layers):
+        p = f"model.layers.{layer}."
+        w.attn_norm.append(np.ascontiguousarray(tensors[p + "input_layernorm.weight"], f32))
+        w.ffn_norm.append(np.ascontiguousarray(tensors[p + "post_attention_layernorm.weight"], f32))
+        for name, hf, k in (("wq", "self_attn.q_proj", hid), ("wk", "self_attn.k_proj", hid),
+                            ("wv", "self_attn.v_proj", hid), ("wo", "self_attn.o_proj", hid),
+                            ("gate", "mlp.gate_proj", hid), ("up", "mlp.up_proj", hid),
+                            ("down", "mlp.down_proj", inter)):
+            getattr(w, name).append(lin(p + hf + ".weight", k))
+    return w
 
 
 def _layer(cfg: LlamaConfig, w: LlamaWeights, layer: int, h: np.ndarray, pos0: int, kv: dict | None,

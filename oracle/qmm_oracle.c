@@ -10,6 +10,7 @@
 #include "qmm_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #if defined(__x86_64__)
@@ -351,4 +352,62 @@ uint16_t vmo_f32_to_bf16(float f) {
     if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu)) return (uint16_t)((x >> 16) | 0x40u);
     x += 0x7FFFu + ((x >> 16) & 1u);
     return (uint16_t)(x >> 16);
+}
+
+/* ---- model of the HIP MFMA path's roundings (see qmm_oracle.h) ---- */
+
+float vmo_round_f16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, sizeof u);
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return x;                           /* NaN */
+    if (a >= 0x477FF000u) return (u >> 31) ? -INFINITY : INFINITY;   /* >= 65520 */
+    if (a < 0x38800000u) {                                   /* below 2^-14: subnormal grid 2^-24 */
+        const double r = nearbyint((double)x * 0x1p24) * 0x1p-24;
+        return (float)r;
+    }
+    /* normal range: keep 11 significant bits, ties to even */
+    u = (u + 0xFFFu + ((u >> 13) & 1u)) & ~0x1FFFu;
+    float r;
+    memcpy(&r, &u, sizeof r);
+    return r;
+}
+
+void vmo_hip_block_weights(const int8_t* b_q, const float* scale, float* dst, size_t rows, size_t cols,
+                           size_t block_size, int quant_type) {
+    if (!b_q || !scale || !dst || rows == 0 || cols == 0 || block_size == 0) return;
+    const size_t nblk = (rows + block_size - 1) / block_size;
+    int* ex = (int*)malloc(cols * sizeof(int));
+    float* s16 = (float*)malloc(cols * sizeof(float));
+    if (!ex || !s16) {
+        free(ex);
+        free(s16);
+        return;
+    }
+    for (size_t c = 0; c < cols; ++c) {
+        float smax = 0.0f;
+        for (size_t b = 0; b < nblk; ++b)
+            if (fabsf(scale[b * cols + c]) > smax) smax = fabsf(scale[b * cols + c]);
+        ex[c] = 0;
+        if (smax > 0.0f && smax <= 3.0e38f) (void)frexpf(smax, &ex[c]);
+    }
+    for (size_t b = 0; b < nblk; ++b) {
+        for (size_t c = 0; c < cols; ++c) s16[c] = vmo_round_f16(ldexpf(scale[b * cols + c], -ex[c]));
+        const size_t r1 = (b + 1) * block_size < rows ? (b + 1) * block_size : rows;
+        for (size_t r = b * block_size; r < r1; ++r) {
+            float* out = dst + r * cols;
+            for (size_t c = 0; c < cols; ++c) {
+                int code;
+                if (quant_type == VMO_QUANT_INT4) {
+                    const unsigned byte = (uint8_t)b_q[(r / 2) * cols + c];
+                    code = nib_to_int((r & 1) ? byte >> 4 : byte);
+                } else {
+                    code = b_q[r * cols + c];
+                }
+                out[c] = ldexpf(vmo_round_f16((float)code * s16[c]), ex[c]);
+            }
+        }
+    }
+    free(ex);
+    free(s16);
 }

@@ -6,7 +6,8 @@ Covers the three weight kinds, K splits 1/2/4 (deterministic split-K
 reduction), partial M and N tiles, K ending half-way through a 64-row step,
 INT8 blocks of 32 and 96 rows, and block scales from 1e-7 to 1e3 (the
 per-column power-of-two normalisation keeps fp16 weights in range).
-Bound: the north-star 1e-3 * max|ref| (A is rounded to fp16 on this path).
+Bound: the north-star 1e-3 * max|ref|; test_activation_magnitudes also
+holds the path to fp32 summation bounds against a model of its staging.
 """
 from __future__ import annotations
 
@@ -120,3 +121,47 @@ def test_split_k_deterministic(hip, monkeypatch):
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
     _check(outs[0], O.qmm(x, q.view(np.int8), s, k, O.QUANT_INT4, 32))
+
+
+def _magnitude_rows(rng, k):
+    """Rows of A at |a| ~ 1e-6, 1, 1e5, 1e6 and 1e30, and one row whose
+    entries span 1e-6 .. 1e6 (the MFMA path stages each row with its own
+    power-of-two scale, split into two fp16 parts)."""
+    base = rng.standard_normal((6, k)).astype(np.float32)
+    mags = np.array([1e-6, 1.0, 1e5, 1e6, 1e30], np.float32)
+    x = base.copy()
+    x[:5] *= mags[:, None]
+    x[5] *= (10.0 ** rng.uniform(-6, 6, k)).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("kind,block", [("int8", 0), ("int8_block", 32), ("int4", 32)])
+@pytest.mark.parametrize("reps", [1, 8, 30])      # m = 6, 48, 180: DEEP, small-M and large-M tiles
+def test_activation_magnitudes(hip, kind, block, reps):
+    import llama_oracle as LO
+
+    k, n = 256, 320
+    rng = np.random.default_rng(17 + reps)
+    q, s, qt, blk = _weights(kind, k, n, rng, block)
+    oq = O.QUANT_INT4 if qt == 2 else O.QUANT_INT8
+    x = np.tile(_magnitude_rows(rng, k), (reps, 1))
+    print(f"case magnitudes kind={kind} m={x.shape[0]} k={k} n={n}", flush=True)
+    out = hip.run_qmm(x, q, s, k, qt, blk).astype(np.float64)
+    assert np.isfinite(out).all()
+    ref = np.asarray(O.qmm(x, q.view(np.int8), s, k, oq, blk), np.float64)
+    rowmax = np.abs(ref).max(axis=1)
+    err = np.abs(out - ref).max(axis=1)
+    assert np.all(err <= TOL * rowmax), f"worst row ratio {np.max(err / rowmax):.3e}"
+    # Against the model of what the MFMAs multiply (A split into two fp16
+    # parts, blockwise weights staged in fp16) the only difference left is
+    # fp32 summation of 2k products: |err| <= 2k * 2^-24 * sum_k |a * w|.
+    lin = LO.Linear(q=q, s=s, k=k, n=n, quant_type=oq, block=blk, mode=LO.LINEAR_HIP)
+    wh = lin.gemm_weights().astype(np.float64)
+    model = LO.split_rows_fp16(x) @ wh
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wh)
+    bound = 2 * k * 2.0 ** -24 * 1.01 * mag + 1e-300
+    assert np.all(np.abs(out - model) <= bound), f"worst ratio {np.max(np.abs(out - model) / bound):.3e}"
+    if kind == "int8":
+        # per-column INT8 stages nothing: fp32-equivalent against the reference loop
+        bound = (2.0 ** -22 + 2 * k * 2.0 ** -24) * 1.01 * mag + 1e-300
+        assert np.all(np.abs(out - ref) <= bound), f"worst ratio {np.max(np.abs(out - ref) / bound):.3e}"

@@ -6,14 +6,13 @@ build_forward_graph_{prefill,decode} built on DeviceType::HIP per call);
 RESIDENT is the resident decoder (fused weights, in-place KV cache, device
 positions, HIP-graph decode steps).
 
-Tolerances (relative to max |logit| of the oracle):
-  1e-4  paths whose matmuls all run the fp32-accumulating GEMV (prompts of
-        at most 4 tokens, decode steps): only summation order differs
-  2e-2  prompts of more than 4 tokens, whose projections run the MFMA GEMM
-        with activations rounded to fp16 (each matmul is within 1e-3 of its
-        reference; the error grows through the layers)
-Quantized runs compare against the oracle's quantized model (the same
-quant.cpp packing), so the bound measures the kernels, not quantization.
+Tolerance: 1e-4 of max |logit| of the oracle, everywhere.  Quantized runs
+compare against the oracle's quantized model (the same quant.cpp packing)
+in its LINEAR_HIP mode: projections of more than 4 rows use the blockwise
+weights as the MFMA path stages them in fp16 (round_block_weights, pinned
+in tests/test_oracle_llama.py); that path takes activations at
+fp32-equivalent precision, so what is left is fp32 summation order and the
+bound measures the kernels, not quantization or fp16.
 """
 from __future__ import annotations
 
@@ -79,7 +78,7 @@ QUANTS = [(0, 0), (1, 0), (2, 32)]   # (quant_type, block): fp32, INT8 per colum
 
 
 def _oracle_weights(w, qt, block):
-    return w if qt == 0 else L.quantize_linears(w, qt, block)
+    return w if qt == 0 else L.set_linear_mode(L.quantize_linears(w, qt, block), L.LINEAR_HIP)
 
 
 @pytest.mark.parametrize("fused", [False, True])
@@ -99,7 +98,7 @@ def test_graph_engine_toy_llama(llama, qt, block, fused):
         _close(s.forward_step(tok, pos), ref[0], 1e-4, f"decode pos {pos}")
     # The reference's own toy prompt (test_tinyllama_e2e.cpp:67), 5 tokens: GEMM path.
     ref, _ = L.prefill(cfg, ow, [1, 2, 3, 4, 5], last_only=True, fused=fused)
-    _close(s.prefill([1, 2, 3, 4, 5]), ref[0], 1e-4 if qt == 0 else 2e-2, "prefill 5")
+    _close(s.prefill([1, 2, 3, 4, 5]), ref[0], 1e-4, "prefill 5")
 
 
 @pytest.mark.parametrize("qt,block", QUANTS[1:])
@@ -127,7 +126,7 @@ def test_resident_decoder_matches_oracle(llama, qt, block):
     # Longer prompt: GEMM projections and the tiled prefill attention.
     prompt = list(range(7, 7 + 70, 3))[:19]
     ref, _ = L.prefill(cfg, ow, prompt, last_only=True)
-    _close(s.prefill(prompt), ref[0], 2e-2, "prefill 19")
+    _close(s.prefill(prompt), ref[0], 1e-4, "prefill 19")
 
 
 @pytest.mark.parametrize("qt,block", QUANTS[1:])

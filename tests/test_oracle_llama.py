@@ -216,3 +216,147 @@ def test_layout_ops_against_numpy():
     assert np.array_equal(L.embedding(x[0], idx), x[0][idx])
     with pytest.raises(IndexError):
         L.embedding(x[0], np.array([4], np.int32))
+
+
+# ------------------------------------------- linear modes (dense, HIP-rounded)
+
+def _packed_linear(rng, k, n, qt, mode):
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    if qt == Q.QUANT_INT8:
+        q, s = Q.quantize_int8(w)
+        return L.Linear(q=q, s=s, k=k, n=n, quant_type=qt, block=0, mode=mode)
+    q, s = Q.quantize_int4(w, 32)
+    return L.Linear(q=q, s=s, k=k, n=n, quant_type=qt, block=32, mode=mode)
+
+
+@pytest.mark.parametrize("qt", [Q.QUANT_INT8, Q.QUANT_INT4])
+@pytest.mark.parametrize("m", [1, 3, 9])
+def test_dense_mode_matches_the_scalar_oracle(qt, m):
+    rng = np.random.default_rng(7 + m)
+    k, n = 96, 48
+    lin = _packed_linear(rng, k, n, qt, L.LINEAR_EXACT)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    exact = lin(x)
+    lin.mode = L.LINEAR_DENSE
+    dense = lin(x)
+    assert np.abs(dense - exact).max() <= 1e-5 * np.abs(exact).max()
+    lin.mode = L.LINEAR_HIP
+    hipr = lin(x)
+    if m <= L.HIP_GEMV_MAX_ROWS or qt == Q.QUANT_INT8:
+        # the GEMV path, and INT8 per-column weights on the MFMA path, are fp32
+        assert np.abs(hipr - exact).max() <= 1e-5 * np.abs(exact).max()
+    else:
+        err = np.abs(hipr - exact).max() / np.abs(exact).max()
+        assert 0 < err <= 1e-3                       # the fp16 staging of blockwise weights, bounded
+
+
+def test_codes_unpack_to_the_dequantized_weights():
+    rng = np.random.default_rng(3)
+    for qt in (Q.QUANT_INT8, Q.QUANT_INT4):
+        lin = _packed_linear(rng, 70, 32, qt, L.LINEAR_DENSE)
+        c = lin.codes().astype(np.float32)
+        assert c.shape == (70, 32) and np.abs(c).max() <= (127 if qt == Q.QUANT_INT8 else 7)
+        scale = lin.s.reshape(-1, 32)
+        per_row = scale if qt == Q.QUANT_INT8 else np.repeat(scale, 32, axis=0)[:70]
+        assert np.array_equal(c * per_row, lin.dense())
+
+
+def test_split_rows_fp16_closed_forms():
+    # a tie of hi (1 + 2^-11 between 1 and 1 + 2^-10) is carried by lo
+    tie = np.float32(1 + 2.0 ** -11)
+    r = L.split_rows_fp16(np.array([[1.75, tie, -tie]], np.float32))
+    assert r.tolist() == [[1.75, float(tie), -float(tie)]]
+    # large rows: 1e6 = 999936 (hi) + 64 (lo); no overflow
+    r = L.split_rows_fp16(np.array([[1e6, 3.0, -2.5e5], [1e30, -7e29, 1.0]], np.float32))
+    assert r[0].tolist() == [1e6, 3.0, -2.5e5]
+    assert r[1, :2].tolist() == [float(np.float32(1e30)), float(np.float32(-7e29))]
+    assert r[1, 2] == 0.0      # 1e-30 of its row's maximum: below fp16's subnormals after scaling
+    # 22 significant bits: an element needing 24 loses at most 2^-23 of itself
+    x = np.array([[1.0, 1 + 2.0 ** -11 - 2.0 ** -23, 1 + 2.0 ** -23]], np.float32)
+    r = L.split_rows_fp16(x)
+    assert r[0, 1] == 1 + 2.0 ** -11 and r[0, 2] == 1 + 2.0 ** -23
+    rng = np.random.default_rng(2)
+    y = (rng.standard_normal((4, 512)) * 10.0 ** rng.uniform(-6, 6, (4, 512))).astype(np.float32)
+    ry = L.split_rows_fp16(y)
+    rowmax = np.abs(y).max(axis=1, keepdims=True).astype(np.float64)
+    assert np.all(np.abs(ry - y) <= np.maximum(2.0 ** -22 * np.abs(y), 2.0 ** -37 * rowmax))
+    # all-zero rows stay zero; a row holding an infinity is not scaled
+    r = L.split_rows_fp16(np.array([[0.0, 0.0], [np.inf, 1.0]], np.float32))
+    assert r[0].tolist() == [0.0, 0.0] and r[1, 0] == np.inf and r[1, 1] == 1.0
+
+
+def test_round_block_weights_closed_forms():
+    codes = np.array([[7, -3], [1, 5], [-7, 0], [2, 7]], np.int8)
+    # power-of-two scales: every rounding is exact
+    s = np.array([[2.0 ** -6, 2.0 ** -9], [2.0 ** -20, 0.5]], np.float32)
+    w = L.round_block_weights(codes, s, 2)
+    assert np.array_equal(w, codes.astype(np.float32) * np.repeat(s, 2, axis=0))
+    # scale 1 + 2^-12 rounds to 1 in fp16; 1 + 2^-10 is exact, but
+    # 7 * (1 + 2^-10) = 7 + 1.75 ulp rounds to 7 + 2 ulp = 7 + 2^-7
+    s = np.array([[1 + 2.0 ** -12, 1 + 2.0 ** -10]], np.float32)
+    w = L.round_block_weights(np.array([[3, 7]], np.int8), s, 32)
+    assert w.tolist() == [[3.0, 7 + 2.0 ** -7]]
+    # the column normalisation keeps tiny scales in fp16's normal range
+    s = np.array([[1.5 * 2.0 ** -20]], np.float32)
+    w = L.round_block_weights(np.array([[7]], np.int8), s, 32)
+    assert w[0, 0] == np.float32(7 * 1.5 * 2.0 ** -20)
+
+
+def test_load_packed_reads_the_packed_layout():
+    rng = np.random.default_rng(5)
+    cfg = L.LlamaConfig(vocab_size=40, hidden_size=64, intermediate_size=96, num_layers=2, num_heads=4,
+                        num_kv_heads=2)
+    d = cfg.head_dim
+    shapes = {"self_attn.q_proj": (64, 64), "self_attn.k_proj": (64, 2 * d), "self_attn.v_proj": (64, 2 * d),
+              "self_attn.o_proj": (64, 64), "mlp.gate_proj": (64, 96), "mlp.up_proj": (64, 96),
+              "mlp.down_proj": (96, 64)}
+    tensors, ref = {}, {}
+    for layer in range(2):
+        for hf, (k, n) in shapes.items():
+            q, s = Q.quantize_int4((rng.standard_normal((k, n)) * 0.02).astype(np.float32), 32)
+            name = f"model.layers.{layer}.{hf}.weight"
+            tensors[name + ".codes"], tensors[name + ".scales"] = q.view(np.int8), s
+            ref[name] = (q, s)
+        tensors[f"model.layers.{layer}.input_layernorm.weight"] = np.ones(64, np.float32)
+        tensors[f"model.layers.{layer}.post_attention_layernorm.weight"] = np.ones(64, np.float32)
+    q, s = Q.quantize_int4((rng.standard_normal((64, 40)) * 0.02).astype(np.float32), 32)
+    tensors["lm_head.weight.codes"], tensors["lm_head.weight.scales"] = q.view(np.int8), s
+    tensors["model.embed_tokens.weight"] = rng.standard_normal((40, 64)).astype(np.float32)
+    tensors["model.norm.weight"] = np.ones(64, np.float32)
+    w = L.load_packed(tensors, cfg, Q.QUANT_INT4, 32)
+    assert w.down[1].k == 96 and w.down[1].n == 64 and w.wk[0].n == 2 * d
+    assert np.array_equal(w.gate[1].q.view(np.uint8), ref["model.layers.1.mlp.gate_proj.weight"][0])
+    # the model runs in every linear mode and they agree
+    logits_exact, _ = L.prefill(cfg, w, [3, 1, 4, 1, 5, 9], last_only=True)
+    L.set_linear_mode(w, L.LINEAR_DENSE)
+    logits_dense, _ = L.prefill(cfg, w, [3, 1, 4, 1, 5, 9], last_only=True)
+    assert np.abs(logits_dense - logits_exact).max() <= 1e-5 * np.abs(logits_exact).max()
+
+
+def test_c_rounding_model_matches_numpy():
+    """vmo_round_f16 against numpy's float32 -> float16 conversion (IEEE
+    binary16, ties to even) over normals, ties, subnormals, overflow; and
+    vmo_hip_block_weights against the numpy restatement."""
+    rng = np.random.default_rng(13)
+    x = np.concatenate([
+        (rng.standard_normal(20000) * 10.0 ** rng.uniform(-9, 5, 20000)).astype(np.float32),
+        np.array([65504, 65519.99, 65520, 1e6, 2.0 ** -14, 2.0 ** -24, 3 * 2.0 ** -26, 2.0 ** -25,
+                  1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -(1 + 2.0 ** -11), 0.0, -0.0], np.float32),
+        ((np.arange(4096, dtype=np.float32) + 0.5) * np.float32(2.0 ** -12)),   # exact ties
+    ])
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).astype(np.float32)
+    got = Q.round_f16(x)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    for qt in (Q.QUANT_INT8, Q.QUANT_INT4):
+        k, n, block = 96, 40, 32
+        w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+        if qt == Q.QUANT_INT4:
+            q, s = Q.quantize_int4(w, block)
+        else:
+            q = rng.integers(-127, 128, (k, n), dtype=np.int8)
+            s = (rng.random((k // block, n)) * 10.0 ** rng.uniform(-3, 1, (k // block, n))).astype(np.float32)
+        lin = L.Linear(q=q, s=s, k=k, n=n, quant_type=qt, block=block)
+        c_model = Q.hip_block_weights(q, s, k, block, qt)
+        np_model = L.round_block_weights(lin.codes(), s.reshape(-1, n), block)
+        assert np.array_equal(c_model, np_model)

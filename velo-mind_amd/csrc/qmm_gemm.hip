@@ -4,11 +4,20 @@
 // C[M, N] = A[M, K] * W[K, N] with W given as the reference's codes (INT8
 // [K, N] or INT4 packed [(K+1)/2, N], N contiguous) and fp32 scales.
 //
+// A is first split once per call (a_split_f16_kernel): each row r is
+// multiplied by 2^x_r, the power of two that puts its largest magnitude in
+// [2^14, 2^15), and written as two fp16 parts hi = fp16(a * 2^x_r) and
+// lo = fp16(a * 2^x_r - hi), so that hi + lo carries 22 significant bits of
+// any finite fp32 row without overflow or underflow.  Both parts go through
+// the MFMAs (products with the exact fp16 codes are exact, accumulation is
+// fp32), and the epilogue multiplies by 2^-x_r, which is exact: the
+// activations are used at fp32-equivalent precision.
+//
 // Pipeline (per workgroup: a BM x BN output tile, four waves, K in steps of
 // 64 rows):
 //   global -> registers  raw buffer loads (zeros past the end), two steps
 //                        ahead of the MFMAs;
-//   registers -> LDS     A: fp32 -> fp16 (RNE), row-major [BM][64];
+//   registers -> LDS     A: the hi and lo parts as loaded, row-major [BM][64];
 //                        B: codes -> fp16 with packed-half magic numbers
 //                        (0x6400 | (code ^ 0x80..) is 1024 + 128 + code),
 //                        times the block scale, stored in the codes' own
@@ -25,9 +34,10 @@
 // where 2^e is a per-column power of two with max_s / 2^e in [0.5, 1) over
 // the workgroup's K range, and the fp32 result is multiplied by 2^e (exact).
 // The normalisation keeps every staged weight inside fp16's normal range
-// whatever the scales' magnitude; the only roundings beyond fp32
-// accumulation are A -> fp16 and (code * s / 2^e) -> fp16, each relative
-// 2^-11 at most.
+// whatever the scales' magnitude.  Beyond fp32 accumulation the only
+// rounding is then (code * s / 2^e) -> fp16 for blockwise weights (relative
+// 2^-11, a fixed function of the weights) and A's split (relative 2^-22);
+// INT8 per-column codes are exact and their scales apply in fp32.
 //
 // Split-K for small M: each split stores its scaled partial tile
 // with agent-scope stores, the last split of a tile (atomic ticket) adds
@@ -95,7 +105,7 @@ struct Tile {
     static constexpr int TN = WN / 16;
     static constexpr int kArow = kBK + kApad;                  // halves per A row
     static constexpr int kBrow = BN + kBpad;                   // halves per B k-row
-    static constexpr int kAPieces = BM * (kBK / 8);            // 8 floats each
+    static constexpr int kAPieces = BM * (kBK / 8);            // 8 halves (16 bytes) each
     static constexpr int kAPass = (kAPieces + kThreads - 1) / kThreads;
     static constexpr int kBRows = kInt4 ? kBK / 2 : kBK;       // code byte rows per step
     static constexpr int kBPieces = kBRows * (BN / 16);        // 16 bytes each
@@ -110,7 +120,8 @@ struct Tile {
 template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
 struct Stage {
     using T = Tile<KIND, BM, BN, WAVES_M, WAVES_N>;
-    u32x4 a[T::kAPass][2];
+    u32x4 a[T::kAPass];
+    u32x4 al[T::kAPass];
     u32x4 b[T::kBPass];
     u32x4 s[T::kBlock ? T::kBPass : 1][T::kBlock ? 4 : 1];
 };
@@ -121,18 +132,23 @@ struct Stage {
 // trip instead of one per pipeline step.
 template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N, int DEEP>
 __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
-    const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
-    float* __restrict__ c, int m, int k, int n, int block_size, int steps_per_split, int tiles_n, int tiles_m,
-    uint32_t a_bytes, uint32_t code_bytes, uint32_t scale_bytes, float* __restrict__ partials,
+    const _Float16* __restrict__ a, const int* __restrict__ row_exp, const uint8_t* __restrict__ wq,
+    const float* __restrict__ scale, float* __restrict__ c, int m, int k, int n, int block_size,
+    int steps_per_split, int tiles_n, int tiles_m,
+    uint32_t a_bytes, uint32_t lo_offset, uint32_t code_bytes, uint32_t scale_bytes, float* __restrict__ partials,
     unsigned* __restrict__ counters) {
     using T = Tile<KIND, BM, BN, WAVES_M, WAVES_N>;
     using S = Stage<KIND, BM, BN, WAVES_M, WAVES_N>;
 
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * T::kArow];
+    __shared__ __attribute__((aligned(16))) _Float16 sAl[2][BM * T::kArow];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][kBK * T::kBrow];
     __shared__ float sPow[T::kBlock ? BN : 1];   // 2^e per column (physical order)
     __shared__ float sInv[T::kBlock ? BN : 1];   // 2^-e
-    __shared__ float sRed[T::kBlock ? T::kRedRows * BN : 1];
+    // The scale-normalisation scratch lives in the second B buffer: it is
+    // used (and released by a barrier) before any B step is written there.
+    float* sRed = reinterpret_cast<float*>(sB[1]);
+    static_assert(!T::kBlock || T::kRedRows * BN * 4 <= kBK * T::kBrow * 2, "sRed fits in a B buffer");
     __shared__ unsigned ticket;
 
     const int tid = threadIdx.x;
@@ -211,9 +227,9 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
             const int row = piece / (kBK / 8);
             const int kk = k0 + 8 * (piece % (kBK / 8));
             const bool ok = piece < T::kAPieces && m0 + row < m && kk < k_end;
-            const uint32_t off = ok ? (static_cast<uint32_t>(m0 + row) * k + kk) * 4u : a_bytes;
-            st.a[p][0] = buffer_load16(ars, off);
-            st.a[p][1] = buffer_load16(ars, ok ? off + 16u : a_bytes);
+            const uint32_t off = (static_cast<uint32_t>(m0 + row) * k + kk) * 2u;
+            st.a[p] = buffer_load16(ars, ok ? off : a_bytes);
+            st.al[p] = buffer_load16(ars, ok ? off + lo_offset : a_bytes);
         }
 #pragma unroll
         for (int p = 0; p < T::kBPass; ++p) {
@@ -236,15 +252,14 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     // ---- registers -> fp16 registers (VALU only) -> LDS
     struct Packed {
         u32x4 a[T::kAPass];
+        u32x4 al[T::kAPass];
         u32x4 b[T::kBPass][T::kInt4 ? 4 : 2];
     };
     auto convert_step = [&](const S& st, Packed& pk) {
 #pragma unroll
         for (int p = 0; p < T::kAPass; ++p) {
-            pk.a[p][0] = pk_f16(__uint_as_float(st.a[p][0][0]), __uint_as_float(st.a[p][0][1]));
-            pk.a[p][1] = pk_f16(__uint_as_float(st.a[p][0][2]), __uint_as_float(st.a[p][0][3]));
-            pk.a[p][2] = pk_f16(__uint_as_float(st.a[p][1][0]), __uint_as_float(st.a[p][1][1]));
-            pk.a[p][3] = pk_f16(__uint_as_float(st.a[p][1][2]), __uint_as_float(st.a[p][1][3]));
+            pk.a[p] = st.a[p];
+            pk.al[p] = st.al[p];
         }
 #pragma unroll
         for (int p = 0; p < T::kBPass; ++p) {
@@ -289,6 +304,7 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     };
     auto write_step = [&](const Packed& pk, int buf) {
         _Float16* la = sA[buf];
+        _Float16* lal = sAl[buf];
         _Float16* lb = sB[buf];
 #pragma unroll
         for (int p = 0; p < T::kAPass; ++p) {
@@ -297,6 +313,7 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
                 const int row = piece / (kBK / 8);
                 const int kc = 8 * (piece % (kBK / 8));
                 *reinterpret_cast<u32x4*>(la + row * T::kArow + kc) = pk.a[p];
+                *reinterpret_cast<u32x4*>(lal + row * T::kArow + kc) = pk.al[p];
             }
         }
 #pragma unroll
@@ -335,14 +352,19 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     const int fg = lane >> 4;        // 8-k group
     struct Frags {
         half8v a[T::TM];
+        half8v al[T::TM];
         half8v b[T::TN];
     };
     auto read_frags = [&](int buf, int kh, Frags& f) {
         const _Float16* la = sA[buf];
+        const _Float16* lal = sAl[buf];
         const _Float16* lb = sB[buf];
 #pragma unroll
-        for (int i = 0; i < T::TM; ++i)
-            f.a[i] = *reinterpret_cast<const half8v*>(la + (wm * T::WM + i * 16 + fr) * T::kArow + kh * 32 + 8 * fg);
+        for (int i = 0; i < T::TM; ++i) {
+            const int off = (wm * T::WM + i * 16 + fr) * T::kArow + kh * 32 + 8 * fg;
+            f.a[i] = *reinterpret_cast<const half8v*>(la + off);
+            f.al[i] = *reinterpret_cast<const half8v*>(lal + off);
+        }
 #pragma unroll
         for (int j = 0; j < T::TN; ++j) {
             // lane L of each 16-lane group points at row base + L/4,
@@ -359,7 +381,10 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
             for (int j = 0; j < T::TN; ++j)
+            {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.al[i], f.b[j], acc[i][j], 0, 0, 0);
+            }
     };
     // One pipeline step: all fragment reads of the current buffer are issued
     // first, the next stage is converted in registers while they are in
@@ -441,6 +466,16 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
         }
     }
 
+    // 2^-x of each of the lane's rows undoes the staging scale (exact).
+    int neg_exp[T::TM][4];
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = m0 + wm * T::WM + i * 16 + 4 * fg + e;
+            neg_exp[i][e] = row < m ? -row_exp[row] : 0;
+        }
+
     if (splits == 1) {
 #pragma unroll
         for (int j = 0; j < T::TN; ++j) {
@@ -451,7 +486,8 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int row = m0 + wm * T::WM + i * 16 + 4 * fg + e;
-                    if (row < m) c[static_cast<int64_t>(row) * n + col] = acc[i][j][e] * colscale[j];
+                    if (row < m)
+                        c[static_cast<int64_t>(row) * n + col] = ldexpf(acc[i][j][e] * colscale[j], neg_exp[i][e]);
                 }
         }
         return;
@@ -467,7 +503,9 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int row = m0 + wm * T::WM + i * 16 + 4 * fg + e;
-                if (row < m) coherent_store(part + static_cast<int64_t>(row) * n + col, acc[i][j][e] * colscale[j]);
+                if (row < m)
+                    coherent_store(part + static_cast<int64_t>(row) * n + col,
+                                   ldexpf(acc[i][j][e] * colscale[j], neg_exp[i][e]));
             }
     }
     publish_partials();
@@ -493,6 +531,65 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
         c[static_cast<int64_t>(row) * n + col] = v;
     }
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A [m, k] fp32 -> two fp16 parts with a power-of-two scale per row: x_r
+// is chosen so that max_k |a[r, k]| * 2^x_r lies in [2^14, 2^15) (x_r = 0
+// for an all-zero row, or one holding an infinity or NaN, which then
+// reaches the output as the reference's fp32 arithmetic would propagate
+// it); hi = fp16(a * 2^x_r) and lo = fp16(a * 2^x_r - hi), the difference
+// being exact in fp32.  hi at ah[r * k + c], lo at ah[m * k + r * k + c].
+// One workgroup per row; the row is read twice (max, then split), the
+// second time from L2.
+__global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restrict__ a,
+                                                          _Float16* __restrict__ ah,
+                                                          int* __restrict__ row_exp, int m, int k, int vec) {
+    __shared__ float wmax[4];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float* src = a + static_cast<int64_t>(row) * k;
+    const int vecs = k >> 2;   // k % 32 == 0 on this path
+    auto load4 = [&](int v) {
+        if (vec) return reinterpret_cast<const float4*>(src)[v];
+        return make_float4(src[4 * v], src[4 * v + 1], src[4 * v + 2], src[4 * v + 3]);
+    };
+    float mx = 0.0f;
+    bool special = false;
+    for (int v = tid; v < vecs; v += 256) {
+        const float4 x = load4(v);
+        const float t = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+        special |= !(fabsf(x.x) <= 3.4028235e38f) || !(fabsf(x.y) <= 3.4028235e38f) ||
+                   !(fabsf(x.z) <= 3.4028235e38f) || !(fabsf(x.w) <= 3.4028235e38f);
+        mx = fmaxf(mx, t);
+    }
+    // an infinity or NaN anywhere in the row disables the scaling
+    if (special) mx = __builtin_inff();
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int x = 0;
+    if (mx > 0.0f && mx <= 3.4028235e38f) {
+        int e = 0;
+        (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
+        x = 15 - e;
+    }
+    if (tid == 0) row_exp[row] = x;
+    half4v* hi = reinterpret_cast<half4v*>(ah + static_cast<int64_t>(row) * k);
+    half4v* lo = reinterpret_cast<half4v*>(ah + (static_cast<int64_t>(m) + row) * k);
+    for (int v = tid; v < vecs; v += 256) {
+        const float4 y = load4(v);
+        const float s0 = ldexpf(y.x, x), s1 = ldexpf(y.y, x), s2 = ldexpf(y.z, x), s3 = ldexpf(y.w, x);
+        const half4v h = {static_cast<_Float16>(s0), static_cast<_Float16>(s1), static_cast<_Float16>(s2),
+                          static_cast<_Float16>(s3)};
+        hi[v] = h;
+        // an infinite part (|a| beyond fp16 in an unscaled row) leaves lo at 0
+        auto rest = [](float s, _Float16 hh) {
+            const float d = s - static_cast<float>(hh);
+            return static_cast<_Float16>(d == d && fabsf(d) <= 65504.0f ? d : 0.0f);
+        };
+        lo[v] = half4v{rest(s0, h[0]), rest(s1, h[1]), rest(s2, h[2]), rest(s3, h[3])};
+    }
 }
 
 struct GemmConfig {
@@ -578,8 +675,8 @@ GemmConfig choose_gemm(int kind, int m, int k, int n) {
 }
 
 template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N, int DEEP = 0>
-int launch(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n, int block_size,
-           int splits, hipStream_t stream) {
+int launch(const _Float16* a, const int* row_exp, const uint8_t* wq, const float* scale, float* c, int m, int k,
+           int n, int block_size, int splits, hipStream_t stream) {
     const int tiles_n = (n + BN - 1) / BN;
     const int tiles_m = (m + BM - 1) / BM;
     const int steps = (k + kBK - 1) / kBK;
@@ -591,38 +688,39 @@ int launch(const float* a, const uint8_t* wq, const float* scale, float* c, int 
                              static_cast<std::size_t>(tiles_m) * tiles_n, &ws));
     }
     const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
-    const uint32_t a_bytes = static_cast<uint32_t>(static_cast<int64_t>(m) * k * 4);
+    const uint32_t lo_offset = static_cast<uint32_t>(static_cast<int64_t>(m) * k * 2);
+    const uint32_t a_bytes = 2u * lo_offset;   // hi, then lo
     const uint32_t code_bytes =
         static_cast<uint32_t>((KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : static_cast<int64_t>(k)) * n);
     const uint32_t scale_bytes = static_cast<uint32_t>((KIND == 0 ? 1 : nblk) * n * 4);
     if (DEEP > 0 && sps > DEEP) return fail_inval("QuantizedMatMul: internal error: K steps per split exceed the pipeline depth");
     hipLaunchKernelGGL((qmm_mfma_kernel<KIND, BM, BN, WAVES_M, WAVES_N, DEEP>), dim3(tiles_n * tiles_m * splits),
-                       dim3(kThreads), 0, stream, a, wq, scale, c, m, k, n, block_size, sps, tiles_n, tiles_m,
-                       a_bytes, code_bytes, scale_bytes, ws.partials, ws.counters);
+                       dim3(kThreads), 0, stream, a, row_exp, wq, scale, c, m, k, n, block_size, sps, tiles_n, tiles_m,
+                       a_bytes, lo_offset, code_bytes, scale_bytes, ws.partials, ws.counters);
     return check_launch("QuantizedMatMul", stream);
 }
 
 template <int KIND>
-int launch_kind(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
-                int block_size, hipStream_t stream) {
+int launch_kind(const _Float16* a, const int* row_exp, const uint8_t* wq, const float* scale, float* c, int m,
+                int k, int n, int block_size, hipStream_t stream) {
     const GemmConfig cfg = choose_gemm(KIND, m, k, n);
     if (cfg.deep == 8) {
-        if (cfg.bm == 16) return launch<KIND, 16, 64, 1, 4, 8>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
-        return launch<KIND, 32, 64, 2, 2, 8>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        if (cfg.bm == 16) return launch<KIND, 16, 64, 1, 4, 8>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        return launch<KIND, 32, 64, 2, 2, 8>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
     }
     if (cfg.deep == 4) {
-        if (cfg.bm == 16) return launch<KIND, 16, 64, 1, 4, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
-        return launch<KIND, 32, 64, 2, 2, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        if (cfg.bm == 16) return launch<KIND, 16, 64, 1, 4, 4>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        return launch<KIND, 32, 64, 2, 2, 4>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
     }
-    if (cfg.bn == 64 && cfg.bm == 16) return launch<KIND, 16, 64, 1, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+    if (cfg.bn == 64 && cfg.bm == 16) return launch<KIND, 16, 64, 1, 4>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
     if (cfg.bn == 128) {
-        if (cfg.bm == 16) return launch<KIND, 16, 128, 1, 4>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
-        if (cfg.bm == 32) return launch<KIND, 32, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
-        if (cfg.bm == 64) return launch<KIND, 64, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
-        return launch<KIND, 128, 128, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        if (cfg.bm == 16) return launch<KIND, 16, 128, 1, 4>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        if (cfg.bm == 32) return launch<KIND, 32, 128, 2, 2>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        if (cfg.bm == 64) return launch<KIND, 64, 128, 2, 2>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+        return launch<KIND, 128, 128, 2, 2>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
     }
-    if (cfg.bm == 32) return launch<KIND, 32, 64, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
-    return launch<KIND, 64, 64, 2, 2>(a, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+    if (cfg.bm == 32) return launch<KIND, 32, 64, 2, 2>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
+    return launch<KIND, 64, 64, 2, 2>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
 }
 
 }  // namespace
@@ -632,21 +730,33 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
     // 64-row steps may end half-way (k % 32 == 0); 16-byte code pieces need
     // whole 16-column groups; buffer offsets are 32-bit.
     if (k % 32 != 0 || n % 16 != 0) return VM_HIP_EUNSUPPORTED;
+    // (A's two fp16 parts take m * k * 4 bytes, addressed with 32-bit offsets)
     if (static_cast<int64_t>(m) * k * 4 >= (int64_t(1) << 31) || static_cast<int64_t>(k) * n >= (int64_t(1) << 31) ||
         static_cast<int64_t>(m) * n * 4 * kMaxSplits >= (int64_t(1) << 40))
         return VM_HIP_EUNSUPPORTED;
     // one-dimensional grid of at most 2^30 workgroups
     if (((static_cast<int64_t>(m) + 15) / 16) * ((n + 63) / 64) * kMaxSplits >= (int64_t(1) << 30))
         return VM_HIP_EUNSUPPORTED;
+    int kind = 0;
     if (quant_type == VM_HIP_QUANT_INT4) {
         if (block_size <= 0 || block_size % 32 != 0) return VM_HIP_EUNSUPPORTED;
-        return launch_kind<2>(a, wq, scale, c, m, k, n, block_size, stream);
-    }
-    if (block_size > 0) {
+        kind = 2;
+    } else if (block_size > 0) {
         if (block_size % 32 != 0) return VM_HIP_EUNSUPPORTED;
-        return launch_kind<1>(a, wq, scale, c, m, k, n, block_size, stream);
+        kind = 1;
     }
-    return launch_kind<0>(a, wq, scale, c, m, k, n, 0, stream);
+    // A's row-scaled fp16 parts (hi, lo) and row exponents, staged for this call.
+    const std::size_t half_bytes = (static_cast<std::size_t>(m) * k * 4 + 255) & ~std::size_t(255);
+    void* aux = nullptr;
+    VM_TRY(get_aux(stream, half_bytes + static_cast<std::size_t>(m) * sizeof(int), &aux));
+    auto* ah = static_cast<_Float16*>(aux);
+    auto* row_exp = reinterpret_cast<int*>(static_cast<char*>(aux) + half_bytes);
+    hipLaunchKernelGGL(a_split_f16_kernel, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k,
+                       reinterpret_cast<uintptr_t>(a) % 16 == 0 ? 1 : 0);
+    VM_TRY(check_launch("QuantizedMatMul", stream));
+    if (kind == 2) return launch_kind<2>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
+    if (kind == 1) return launch_kind<1>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
+    return launch_kind<0>(ah, row_exp, wq, scale, c, m, k, n, 0, stream);
 }
 
 }  // namespace vmhip

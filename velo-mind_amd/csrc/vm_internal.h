@@ -54,16 +54,23 @@ void release_workspace(hipStream_t stream);
 // previous contents are not preserved across growth).
 int get_staging(hipStream_t stream, std::size_t bytes, void** out);
 
+// Per-stream buffer for operands a kernel prepares for the next kernel of
+// the same call (the MFMA GEMM's fp16 copy of A with its row exponents).
+// Grows like the workspace; refused during capture.
+int get_aux(hipStream_t stream, std::size_t bytes, void** out);
+
 // While an instance is alive, get_workspace() on this thread hands out the
 // caller's fixed region (counters first, then partials) instead of the
-// per-stream allocation, and fails with a message naming `who` when a call
-// needs more than the region holds; get_staging() fails.  Used by the entry
-// points that must not allocate.
+// per-stream allocation, get_aux() hands out the end of the partials area,
+// and either fails with a message naming `who` when a call needs more than
+// the region holds; get_staging() fails.  Used by the entry points that
+// must not allocate.
 struct FixedRegion {
     void*       base = nullptr;
     std::size_t counter_slots = 0;
     std::size_t partial_floats = 0;
     const char* who = "";
+    std::size_t aux_bytes = 0;   // taken from the end of the partials area
 };
 
 class FixedWorkspaceScope {
@@ -75,7 +82,7 @@ public:
 
 private:
     FixedRegion _region;
-    const FixedRegion* _previous;
+    FixedRegion* _previous;
 };
 
 // Number of compute units of the current device (cached per device).

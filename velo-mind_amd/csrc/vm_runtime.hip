@@ -38,7 +38,14 @@ struct StagingEntry {
 };
 std::map<std::pair<int, hipStream_t>, StagingEntry> g_staging;
 
-thread_local const FixedRegion* t_fixed = nullptr;
+thread_local FixedRegion* t_fixed = nullptr;
+
+struct AuxEntry {
+    void*       base = nullptr;
+    std::size_t bytes = 0;
+    std::vector<void*> retired;
+};
+std::map<std::pair<int, hipStream_t>, AuxEntry> g_aux;
 
 int current_device() {
     int dev = 0;
@@ -106,11 +113,13 @@ int get_workspace(hipStream_t stream, std::size_t partial_floats, std::size_t co
                   Workspace* out) {
     if (const FixedRegion* f = t_fixed) {
         const std::size_t counter_bytes = f->counter_slots * sizeof(unsigned);
-        if (counter_slots > f->counter_slots || partial_floats > f->partial_floats)
+        const std::size_t room = f->partial_floats - (f->aux_bytes + sizeof(float) - 1) / sizeof(float);
+        if (counter_slots > f->counter_slots || partial_floats > room)
             return fail_inval(std::string(f->who) + ": this shape's split-K scratch needs " +
                               std::to_string(counter_slots * sizeof(unsigned)) + " bytes of counters and " +
                               std::to_string(partial_floats * sizeof(float)) + " bytes of partials; the static scratch holds " +
-                              std::to_string(counter_bytes) + " and " + std::to_string(f->partial_floats * sizeof(float)));
+                              std::to_string(counter_bytes) + " and " + std::to_string(room * sizeof(float)) +
+                              (f->aux_bytes ? " (after " + std::to_string(f->aux_bytes) + " bytes of staged A)" : std::string()));
         out->counters = static_cast<unsigned*>(f->base);
         out->partials = reinterpret_cast<float*>(static_cast<char*>(f->base) + counter_bytes);
         return 0;
@@ -157,6 +166,39 @@ int get_workspace(hipStream_t stream, std::size_t partial_floats, std::size_t co
     return 0;
 }
 
+int get_aux(hipStream_t stream, std::size_t bytes, void** out) {
+    bytes = (bytes + 255) & ~std::size_t(255);
+    if (FixedRegion* f = t_fixed) {
+        const std::size_t area = f->partial_floats * sizeof(float);
+        if (bytes > area)
+            return fail_inval(std::string(f->who) + ": staging A for the MFMA path needs " + std::to_string(bytes) +
+                              " bytes; the static scratch holds " + std::to_string(area));
+        f->aux_bytes = bytes;
+        *out = static_cast<char*>(f->base) + f->counter_slots * sizeof(unsigned) + (area - bytes);
+        return 0;
+    }
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    AuxEntry& e = g_aux[{dev, stream}];
+    if (e.base == nullptr || e.bytes < bytes) {
+        if (stream != nullptr) {
+            hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+                return fail_inval("QuantizedMatMul: the staged-A buffer must be sized by an eager call "
+                                  "on this stream before graph capture");
+        }
+        const std::size_t want = std::max<std::size_t>(std::max(bytes, e.bytes * 2), 1 << 20);
+        if (e.base) {
+            e.retired.push_back(e.base);
+            e.base = nullptr;
+        }
+        VM_TRY_HIP(hipMalloc(&e.base, want), "staged A: hipMalloc");
+        e.bytes = want;
+    }
+    *out = e.base;
+    return 0;
+}
+
 void release_workspace(hipStream_t stream) {
     const int dev = current_device();
     std::lock_guard<std::mutex> lock(g_ws_mutex);
@@ -165,6 +207,12 @@ void release_workspace(hipStream_t stream) {
         if (it->second.base) (void)hipFree(it->second.base);
         for (void* p : it->second.retired) (void)hipFree(p);
         g_ws.erase(it);
+    }
+    auto ax = g_aux.find({dev, stream});
+    if (ax != g_aux.end()) {
+        if (ax->second.base) (void)hipFree(ax->second.base);
+        for (void* p : ax->second.retired) (void)hipFree(p);
+        g_aux.erase(ax);
     }
     auto st = g_staging.find({dev, stream});
     if (st != g_staging.end()) {
