@@ -70,6 +70,9 @@ int vm_llama_weights_create(const vm_llama_config* cfg, vm_llama_weights** out);
 int vm_llama_weights_set(vm_llama_weights* w, int kind, int64_t layer, const float* host, int64_t numel);
 /* Linears and embedding ~ N(0, stddev^2), norms ~ N(1, stddev^2), on the GPU. */
 int vm_llama_weights_fill_synthetic(vm_llama_weights* w, uint64_t seed, float stddev);
+/* Tied embeddings: lm_head := embedding^T on the GPU (the reference loaders'
+ * fallback when tie_word_embeddings is set, model_loader.cpp:74-144). */
+int vm_llama_weights_tie_lm_head(vm_llama_weights* w);
 void vm_llama_weights_destroy(vm_llama_weights* w);
 
 /* quant_type: 0 none (graph engine only), 1 INT8 per column, 2 INT4 with

@@ -59,6 +59,11 @@ public:
     // ~ N(1, stddev^2), each tensor from its own seed derived from (seed,
     // kind, layer), generated on the GPU.
     void fill_synthetic(std::uint64_t seed, float stddev);
+    // Tied embeddings: lm_head [hidden, vocab] becomes the embedding's
+    // transpose, as the reference loaders do when tie_word_embeddings is set
+    // (examples/tinyllama/model_loader.cpp:74-144, "lm_head falls back to
+    // the embedding").
+    void tie_lm_head_to_embedding();
     auto storage(LlamaWeight kind, std::size_t layer = 0) const -> std::shared_ptr<TensorStorage>;
 
 private:

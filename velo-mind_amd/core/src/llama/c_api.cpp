@@ -106,6 +106,13 @@ int vm_llama_weights_fill_synthetic(vm_llama_weights* w, uint64_t seed, float st
     });
 }
 
+int vm_llama_weights_tie_lm_head(vm_llama_weights* w) {
+    return guarded([&] {
+        if (!w) throw std::invalid_argument("vm_llama_weights_tie_lm_head: null weights");
+        w->set->tie_lm_head_to_embedding();
+    });
+}
+
 void vm_llama_weights_destroy(vm_llama_weights* w) { delete w; }
 
 int vm_llama_session_create(const vm_llama_weights* w, int engine, int quant_type, int block_size, int fused_attention,

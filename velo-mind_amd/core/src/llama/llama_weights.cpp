@@ -98,6 +98,16 @@ void LlamaWeightSet::fill_synthetic(std::uint64_t seed, float stddev) {
     check(vm_hip_device_synchronize(), "LlamaWeightSet::fill_synthetic");
 }
 
+void LlamaWeightSet::tie_lm_head_to_embedding() {
+    const auto& emb = _w[slot(LlamaWeight::Embed, 0)];
+    auto& head = _w[slot(LlamaWeight::LmHead, 0)];
+    const std::int64_t shape[2] = {emb->shape[0], emb->shape[1]};
+    check(vm_hip_transpose_f32(static_cast<const float*>(emb->data), static_cast<float*>(head->data), 2, shape,
+                               nullptr, nullptr),
+          "LlamaWeightSet::tie_lm_head_to_embedding");
+    check(vm_hip_device_synchronize(), "LlamaWeightSet::tie_lm_head_to_embedding");
+}
+
 auto LlamaWeightSet::storage(LlamaWeight kind, std::size_t layer) const -> std::shared_ptr<TensorStorage> {
     return _w[slot(kind, layer)];
 }

@@ -34,6 +34,7 @@ def lib() -> ctypes.CDLL:
         L.vm_llama_weights_create.argtypes = [POINTER(LlamaConfigC), POINTER(c_void_p)]
         L.vm_llama_weights_set.argtypes = [p, c_int, c_int64, p, c_int64]
         L.vm_llama_weights_fill_synthetic.argtypes = [p, c_uint64, c_float]
+        L.vm_llama_weights_tie_lm_head.argtypes = [p]
         L.vm_llama_weights_destroy.argtypes = [p]
         L.vm_llama_weights_destroy.restype = None
         L.vm_llama_session_create.argtypes = [p, c_int, c_int, c_int, c_int, c_int64, POINTER(c_void_p)]
@@ -50,6 +51,7 @@ def lib() -> ctypes.CDLL:
         L.vm_llama_packed_destroy.restype = None
         L.vm_llama_session_create_packed.argtypes = [p, c_int64, POINTER(c_void_p)]
         for name in ("vm_llama_weights_create", "vm_llama_weights_set", "vm_llama_weights_fill_synthetic",
+                     "vm_llama_weights_tie_lm_head",
                      "vm_llama_session_create", "vm_llama_prefill", "vm_llama_forward_step", "vm_llama_generate",
                      "vm_llama_pack", "vm_llama_packed_save", "vm_llama_packed_config", "vm_llama_packed_load",
                      "vm_llama_session_create_packed"):
@@ -78,6 +80,10 @@ class Weights:
 
     def fill_synthetic(self, seed: int, stddev: float) -> None:
         _check(lib().vm_llama_weights_fill_synthetic(self.handle, seed, stddev))
+
+    def tie_lm_head(self) -> None:
+        """lm_head := embedding^T (tied embeddings)."""
+        _check(lib().vm_llama_weights_tie_lm_head(self.handle))
 
     @classmethod
     def from_oracle(cls, cfg, w) -> "Weights":
