@@ -34,7 +34,9 @@ peak, showing what the kernel sustains once a launch is long enough.
 INT8 (config 4: 128 + 128), on the resident HIP decoder with synthetic
 weights: prefill and decode tokens/s, and the decode step's weight stream
 (packed codes + scales of every QuantizedMatMul per token) as GB/s and as a
-fraction of HBM peak.
+fraction of HBM peak.  ``persistent_step`` is the same decode with the
+one-launch step vm_hip_decode_step (slower than the default captured
+launch-per-projection step on this GPU, so reported beside it).
 
 Prints one JSON line.  Only --gpus 1 is supported (one GPU per box).
 """
@@ -271,9 +273,13 @@ def decode_weight_bytes(c: dict, quant: int, block: int) -> int:
     return tot
 
 
-def e2e_bench(name: str, use_graph: bool = True) -> dict:
+DECODE_PATHS = {0: "graph", 1: "per-op", 2: "slices", 3: "persistent"}
+
+
+def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False) -> dict:
     """Greedy generation on the resident HIP decoder (HIP-graph decode
-    steps); device-event timing of the prefill and of the decode steps."""
+    steps, or with persistent=True the one-launch step vm_hip_decode_step);
+    device-event timing of the prefill and of the decode steps."""
     from velomind_hip import llama as VL
 
     spec = E2E_MODELS[name]
@@ -286,7 +292,19 @@ def e2e_bench(name: str, use_graph: bool = True) -> dict:
         setattr(cfg, k, v)
     w = VL.Weights(cfg)
     w.fill_synthetic(20240601, 0.02)
-    sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"], max_seq=spec["prompt"] + spec["steps"] + 1)
+    prev = os.environ.get("VELOMIND_DECODE_PERSISTENT")
+    os.environ["VELOMIND_DECODE_PERSISTENT"] = "1" if persistent else "0"
+    try:
+        sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"],
+                          max_seq=spec["prompt"] + spec["steps"] + 1)
+    finally:
+        if prev is None:
+            del os.environ["VELOMIND_DECODE_PERSISTENT"]
+        else:
+            os.environ["VELOMIND_DECODE_PERSISTENT"] = prev
+    path = DECODE_PATHS[sess.decode_path()]
+    if persistent and path != "persistent":
+        raise RuntimeError(f"{name}: the persistent decode step does not cover this shape (path {path})")
     prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, spec["prompt"]).astype(np.int32)
     sess.generate(prompt, 8, use_hip_graph=use_graph)  # warm-up (also sizes the workspaces)
     _, (pf_s, dec_s, nd) = sess.generate(prompt, spec["steps"], use_hip_graph=use_graph)
@@ -299,6 +317,7 @@ def e2e_bench(name: str, use_graph: bool = True) -> dict:
            "decode_frac_of_hbm_peak": round(wb * dec_tps / 1e9 / HBM_PEAK_GBS, 4),
            "weights": ("int4 block 32" if spec["quant"] == 2 else "int8 per column") +
                       ", synthetic N(0, 0.02), packed on the GPU",
+           "decode_path": path,
            "engine": "resident HIP decoder, " + ("HIP-graph" if use_graph else "eager") +
                      " decode steps, greedy argmax on device"}
     sess.close()
@@ -455,6 +474,8 @@ def main() -> int:
     ap.add_argument("--e2e-only", action="store_true",
                     help="only the end-to-end legs, printed as one JSON line (profiling passes; with --no-graph "
                          "the decode steps launch eagerly so that rocprofv3 can trace them)")
+    ap.add_argument("--decode-persistent", action="store_true",
+                    help="with --e2e-only: decode with the one-launch step (vm_hip_decode_step)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg (config 3)")
     ap.add_argument("--no-large", action="store_true", help="skip the 70B-class decode GEMV leg")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg, printed as one JSON line")
@@ -496,9 +517,9 @@ def main() -> int:
         e2e = {}
         for name in E2E_MODELS:
             log(f"bench: end-to-end {name}")
-            e2e[name] = e2e_bench(name, use_graph=not args.no_graph)
+            e2e[name] = e2e_bench(name, use_graph=not args.no_graph, persistent=args.decode_persistent)
             log(f"bench: {name}: prefill {e2e[name]['prefill_tokens_per_s']} tok/s, "
-                f"decode {e2e[name]['decode_tokens_per_s']} tok/s")
+                f"decode {e2e[name]['decode_tokens_per_s']} tok/s ({e2e[name]['decode_path']})")
         print(json.dumps({"metric": METRIC, "e2e": e2e}), flush=True)
         return 0
     log("bench: packing weights on the GPU")
@@ -584,8 +605,11 @@ def main() -> int:
         for name in E2E_MODELS:
             log(f"bench: end-to-end {name}")
             e2e[name] = e2e_bench(name)
+            pers = e2e_bench(name, persistent=True)
+            e2e[name]["persistent_step"] = {k: pers[k] for k in ("decode_tokens_per_s", "decode_us_per_token")}
             log(f"bench: {name}: prefill {e2e[name]['prefill_tokens_per_s']} tok/s, "
-                f"decode {e2e[name]['decode_tokens_per_s']} tok/s")
+                f"decode {e2e[name]['decode_tokens_per_s']} tok/s ({e2e[name]['decode_path']}), "
+                f"persistent step {pers['decode_tokens_per_s']} tok/s")
 
     gemm = None
     if not args.no_gemm and not args.only_shape:

@@ -485,6 +485,72 @@ int vm_hip_attention_decode_slices_prefetch_f32(const float* qkv, int64_t qkv_sl
 int vm_hip_memcpy_2d_d2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
                          size_t rows, void* stream);
 
+/* ---- Persistent decode step ---------------------------------------------
+ * No counterpart in the reference, whose decode loop launches one graph of
+ * ~155 QuantizedMatMul and ~250 other operators per token
+ * (examples/common/llama/llama_engine.cpp:395-455, llama_graph.cpp:247-330).
+ * One greedy LLaMA decode step (head_dim 64) as ONE cooperative launch: one
+ * workgroup per compute unit walks every layer's QKV projection, fused
+ * attention with in-place K/V append, output projection, gate|up and down
+ * projections, the final norm, lm_head and argmax.  Workgroups exchange
+ * data through 64-bit {epoch, value} words that consumers poll, so no
+ * device-wide barrier separates the phases, and each workgroup has its
+ * next projection's weights in flight while it waits.  (On an MI355X this
+ * step is slower than the launch-per-projection step captured in a graph:
+ * TinyLlama shapes ~930 us against ~710 us per token; the resident decoder
+ * uses it only when VELOMIND_DECODE_PERSISTENT=1.)
+ *
+ * Weights are the quant.cpp layout (INT8 per column, or INT4 with blocks
+ * of 32 * m rows): q|k|v fused as [hidden, (heads + 2 kv_heads) * 64] and
+ * gate|up as [hidden, 2 * inter] (packed column by column, so the fused
+ * matrix is byte for byte the parts side by side).  Positions: *pos is the
+ * position of *token; keys 0 .. *pos are attended (the K/V of *pos is
+ * appended first).  With logits_out == NULL the step writes argmax (first
+ * maximum, NaN skipped) to *token and tokens[*pos + 1] (when below max_seq)
+ * and increments *pos; with logits_out it writes the logits [vocab] and
+ * leaves token and pos alone.  `step` must differ between consecutive calls
+ * on one workspace (it tags the exchanged words); the workspace must be
+ * zeroed once before the first step. */
+typedef struct vm_hip_decode_layer {
+    const int8_t* qkv_codes;
+    const float*  qkv_scales;
+    const int8_t* o_codes;
+    const float*  o_scales;
+    const int8_t* gate_up_codes;
+    const float*  gate_up_scales;
+    const int8_t* down_codes;
+    const float*  down_scales;
+    const float*  attn_norm;
+    const float*  ffn_norm;
+} vm_hip_decode_layer;
+
+typedef struct vm_hip_decode_model {
+    int64_t layers, hidden, inter, heads, kv_heads, head_dim, vocab, max_seq;
+    int quant_type, block_size;
+    float eps;
+    const vm_hip_decode_layer* layer;   /* device array of `layers` records */
+    const float*  embed;                /* [vocab, hidden]                  */
+    const float*  final_norm;           /* [hidden]                         */
+    const int8_t* lm_codes;             /* [hidden or (hidden+1)/2, vocab]  */
+    const float*  lm_scales;
+    const float*  cos_table;            /* [max_seq, head_dim / 2]          */
+    const float*  sin_table;
+    float*        k_cache;              /* [layers][kv_heads][max_seq][64]   */
+    float*        v_cache;
+    int32_t*      token;                /* device scalars and the sequence   */
+    int32_t*      pos;
+    int32_t*      tokens;               /* [max_seq]                         */
+} vm_hip_decode_model;
+
+/* Workspace bytes the step needs for this model on the current device
+ * (VM_HIP_EUNSUPPORTED when the shape is outside the kernel's limits). */
+int vm_hip_decode_workspace_bytes(const vm_hip_decode_model* model, int64_t* bytes);
+int vm_hip_decode_step(const vm_hip_decode_model* model, void* workspace, int64_t workspace_bytes,
+                       uint32_t step, float* logits_out, void* stream);
+/* Nonzero when a step since the last call timed out waiting for another
+ * workgroup (results of that step are invalid); clears the flag. */
+int vm_hip_decode_status(void* workspace, int* failed, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -102,6 +102,21 @@ int vm_llama_packed_load(const char* path, const vm_llama_config* cfg, vm_llama_
 void vm_llama_packed_destroy(vm_llama_packed* p);
 int vm_llama_session_create_packed(const vm_llama_packed* p, int64_t max_seq, vm_llama_session** out);
 
+/* How the session runs a one-token decode step:
+ *   VM_LLAMA_DECODE_GRAPH       a Graph per step (graph engine)
+ *   VM_LLAMA_DECODE_PER_OP      resident: one launch per operation
+ *   VM_LLAMA_DECODE_SLICES      resident: split-K slices GEMVs and their
+ *                               consumers, five launches per layer
+ *   VM_LLAMA_DECODE_PERSISTENT  resident: one launch per token
+ *                               (vm_hip_decode_step, where the shape
+ *                               allows and VELOMIND_DECODE_PERSISTENT=1 at
+ *                               session creation) */
+#define VM_LLAMA_DECODE_GRAPH      0
+#define VM_LLAMA_DECODE_PER_OP     1
+#define VM_LLAMA_DECODE_SLICES     2
+#define VM_LLAMA_DECODE_PERSISTENT 3
+int vm_llama_session_decode_path(const vm_llama_session* s, int* path);
+
 /* Greedy decoding: prefill, then `steps` decode steps; out_tokens receives
  * steps + 1 tokens (the first from the prompt's logits).  timing (may be
  * NULL) receives {prefill seconds, decode seconds, decode steps timed}:

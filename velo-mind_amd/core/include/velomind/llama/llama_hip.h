@@ -123,6 +123,11 @@ public:
     auto max_seq() const noexcept -> std::size_t { return _max_seq; }
     // Logits of the most recent step or prefill.
     auto logits() const -> std::vector<float>;
+    // How a one-token step runs: one launch per operation, split-K slices
+    // with their consumers (five launches per layer), or one persistent
+    // launch per token (vm_hip_decode_step).
+    enum class DecodePath { PerOperation = 1, Slices = 2, Persistent = 3 };
+    auto decode_path() const noexcept -> DecodePath;
 
 private:
     struct Impl;

@@ -153,6 +153,13 @@ int vm_llama_forward_step(vm_llama_session* s, int32_t token, int64_t pos, float
     });
 }
 
+int vm_llama_session_decode_path(const vm_llama_session* s, int* path) {
+    return guarded([&] {
+        if (!s || !path) throw std::invalid_argument("vm_llama_session_decode_path: null argument");
+        *path = s->resident ? static_cast<int>(s->resident->decode_path()) : VM_LLAMA_DECODE_GRAPH;
+    });
+}
+
 int vm_llama_generate(vm_llama_session* s, const int32_t* prompt, int64_t n, int64_t steps, int use_hip_graph,
                       int32_t* out_tokens, double* timing) {
     return guarded([&] {

@@ -100,6 +100,15 @@ struct HipLlamaDecoder::Impl {
     DevBuf qkv_sl, o_sl, gu_sl, down_sl, lm_sl;
     DevBuf h2, ss_attn, ss_ffn, ss_final, att_part;   // second residual buffer, norm partials, attention records
     int att_chunk = 0, att_chunks = 0;
+    // One-launch decode steps (vm_hip_decode_step), opted into with
+    // VELOMIND_DECODE_PERSISTENT=1: the model description, its per-layer
+    // weight table on the device and the step's workspace.  Off by default:
+    // on an MI355X the captured launch-per-projection step is faster
+    // (TinyLlama shapes: ~710 us against ~930 us per token).
+    bool persistent = false;
+    vm_hip_decode_model pmodel{};
+    DevBuf player, pws;
+    std::uint32_t pstep = 0;
 
     float* kc(std::size_t l) const { return kcache.as<float>() + l * Hk * max_seq * D; }
     float* vc(std::size_t l) const { return vcache.as<float>() + l * Hk * max_seq * D; }
@@ -241,6 +250,22 @@ struct HipLlamaDecoder::Impl {
         gemv_src(normres(ha, down_sl.as<float>(), s_down, final_norm->data, nullptr, ss_final.as<float>()), lm_head,
                  lm_sl.as<float>(), kMaxLm);
     }
+
+    // One decode step as a single launch; logits (when given) instead of
+    // the greedy token.
+    void persistent_step(float* logits_out) {
+        pstep = pstep + 1 >= (1u << 23) ? 1u : pstep + 1;
+        check(vm_hip_decode_step(&pmodel, pws.p, static_cast<std::int64_t>(pws.bytes), pstep, logits_out, stream),
+              "decode step");
+    }
+
+    void persistent_check() {
+        int failed = 0;
+        check(vm_hip_decode_status(pws.p, &failed, stream), "decode status");
+        if (failed) throw std::runtime_error("HipLlamaDecoder: a decode step timed out waiting for a workgroup");
+    }
+
+    void setup_persistent();
 
     // Logits of the last sliced step (the final norm's 1/rms applied).
     void sliced_logits() {
@@ -426,6 +451,58 @@ void HipLlamaDecoder::Impl::allocate() {
     check(vm_hip_stream_synchronize(m.stream), "setup");
 }
 
+void HipLlamaDecoder::Impl::setup_persistent() {
+    auto& m = *this;
+    const char* env = std::getenv("VELOMIND_DECODE_PERSISTENT");
+    if (!env || env[0] != '1') return;
+    vm_hip_decode_model& d = m.pmodel;
+    d.layers = static_cast<std::int64_t>(m.cfg.num_layers);
+    d.hidden = m.hidden;
+    d.inter = m.inter;
+    d.heads = m.H;
+    d.kv_heads = m.Hk;
+    d.head_dim = m.D;
+    d.vocab = m.vocab;
+    d.max_seq = static_cast<std::int64_t>(m.max_seq);
+    d.quant_type = m.qt;
+    d.block_size = m.block_arg();
+    d.eps = m.cfg.rms_norm_eps;
+    std::int64_t bytes = 0;
+    if (vm_hip_decode_workspace_bytes(&d, &bytes) != VM_HIP_OK) return;   // shape outside the kernel: per-launch path
+    std::vector<vm_hip_decode_layer> table(m.cfg.num_layers);
+    for (std::size_t l = 0; l < m.cfg.num_layers; ++l) {
+        auto& t = table[l];
+        t.qkv_codes = m.qkv[l].codes.as<std::int8_t>();
+        t.qkv_scales = m.qkv[l].scales.as<float>();
+        t.o_codes = m.o[l].codes.as<std::int8_t>();
+        t.o_scales = m.o[l].scales.as<float>();
+        t.gate_up_codes = m.gate_up[l].codes.as<std::int8_t>();
+        t.gate_up_scales = m.gate_up[l].scales.as<float>();
+        t.down_codes = m.down[l].codes.as<std::int8_t>();
+        t.down_scales = m.down[l].scales.as<float>();
+        t.attn_norm = static_cast<const float*>(m.attn_norm[l]->data);
+        t.ffn_norm = static_cast<const float*>(m.ffn_norm[l]->data);
+    }
+    m.player = DevBuf(table.size() * sizeof(vm_hip_decode_layer));
+    check(vm_hip_memcpy_h2d(m.player.p, table.data(), m.player.bytes, m.stream), "decode layer table");
+    m.pws = DevBuf(static_cast<std::size_t>(bytes));
+    const std::vector<unsigned char> zeros(m.pws.bytes, 0);
+    check(vm_hip_memcpy_h2d(m.pws.p, zeros.data(), zeros.size(), m.stream), "decode workspace");
+    d.layer = m.player.as<vm_hip_decode_layer>();
+    d.embed = static_cast<const float*>(m.embed->data);
+    d.final_norm = static_cast<const float*>(m.final_norm->data);
+    d.lm_codes = m.lm_head.codes.as<std::int8_t>();
+    d.lm_scales = m.lm_head.scales.as<float>();
+    d.cos_table = m.cos_t.as<float>();
+    d.sin_table = m.sin_t.as<float>();
+    d.k_cache = m.kcache.as<float>();
+    d.v_cache = m.vcache.as<float>();
+    d.token = m.token.as<std::int32_t>();
+    d.pos = m.pos.as<std::int32_t>();
+    d.tokens = m.tokens.as<std::int32_t>();
+    m.persistent = true;
+}
+
 HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_type, int block_size,
                                  std::size_t max_seq)
     : _impl(std::make_unique<Impl>()), _max_seq(max_seq) {
@@ -451,6 +528,7 @@ HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_
     m.pack(m.lm_head, static_cast<const float*>(weights.storage(W::LmHead)->data), m.hidden, m.vocab);
 
     m.allocate();
+    m.setup_persistent();
 }
 
 HipLlamaDecoder::HipLlamaDecoder(const PackedLlamaWeights& packed, std::size_t max_seq)
@@ -476,6 +554,7 @@ HipLlamaDecoder::HipLlamaDecoder(const PackedLlamaWeights& packed, std::size_t m
     m.assemble(m.lm_head, {&packed.linear(W::LmHead)});
     check(vm_hip_stream_synchronize(m.stream), "assemble");
     m.allocate();
+    m.setup_persistent();
 }
 
 HipLlamaDecoder::~HipLlamaDecoder() {
@@ -498,6 +577,11 @@ auto HipLlamaDecoder::logits() const -> std::vector<float> {
     return out;
 }
 
+auto HipLlamaDecoder::decode_path() const noexcept -> DecodePath {
+    if (_impl->persistent) return DecodePath::Persistent;
+    return _impl->sliced ? DecodePath::Slices : DecodePath::PerOperation;
+}
+
 auto HipLlamaDecoder::prefill(std::span<const std::int32_t> tokens) -> std::vector<float> {
     auto& m = *_impl;
     if (tokens.empty() || tokens.size() > _max_seq)
@@ -517,7 +601,10 @@ auto HipLlamaDecoder::forward_step(std::int32_t token, std::size_t pos) -> std::
     if (pos > m.seq || pos >= _max_seq) throw std::invalid_argument("HipLlamaDecoder::forward_step: bad position");
     check(vm_hip_memcpy_h2d(m.token.p, &token, 4, m.stream), "token upload");
     m.set_pos(static_cast<std::int64_t>(pos));
-    if (m.sliced) {
+    if (m.persistent) {
+        m.persistent_step(m.logits.as<float>());
+        m.persistent_check();
+    } else if (m.sliced) {
         m.forward_one_sliced();
         m.sliced_logits();
     } else {
@@ -552,7 +639,9 @@ auto HipLlamaDecoder::generate(std::span<const std::int32_t> prompt, std::size_t
     _prefill_s = ms_prefill * 1e-3;
 
     auto step = [&] {
-        if (m.sliced) {
+        if (m.persistent) {
+            m.persistent_step(nullptr);
+        } else if (m.sliced) {
             m.forward_one_sliced();
             check(vm_hip_argmax_slices_ws_f32(m.lm_sl.as<float>(), m.s_lm, m.vocab, tok, posp, seqp, ms, m.am_ws.p,
                                               static_cast<std::int64_t>(m.am_ws.bytes), m.stream),
@@ -564,7 +653,8 @@ auto HipLlamaDecoder::generate(std::span<const std::int32_t> prompt, std::size_t
     };
     std::size_t done = 0;
     _decode_steps_timed = 0;
-    if (steps > 0 && use_graph) {
+    // A persistent step is one cooperative launch per token (not captured).
+    if (steps > 0 && use_graph && !m.persistent) {
         // The first step runs eagerly: it sizes the per-stream split-K
         // workspaces (the prefill above may have regrown them), then the
         // step is captured against those buffers and replayed.  The graph is
@@ -597,6 +687,7 @@ auto HipLlamaDecoder::generate(std::span<const std::int32_t> prompt, std::size_t
         for (; done < steps; ++done) step();
     check(vm_hip_event_record(m.ev1, m.stream), "event");
     check(vm_hip_event_synchronize(m.ev1), "decode");
+    if (m.persistent) m.persistent_check();
     float ms_decode = 0.0f;
     check(vm_hip_event_elapsed_ms(&ms_decode, m.ev0, m.ev1), "event");
     _decode_s = ms_decode * 1e-3;

@@ -141,7 +141,8 @@ def exported_symbols() -> list[str]:
             "vm_hip_rope_kv_append_slices_f32", "vm_hip_argmax_slices_f32", "vm_hip_slices_sum_f32",
             "vm_hip_qmm_gemv_slices_src_f32", "vm_hip_attention_decode_chunks", "vm_hip_attention_decode_slices_f32",
             "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32",
-            "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32"]
+            "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32", "vm_hip_decode_workspace_bytes",
+            "vm_hip_decode_step", "vm_hip_decode_status"]
 
 
 def open_library() -> ctypes.CDLL:

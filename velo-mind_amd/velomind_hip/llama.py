@@ -12,6 +12,7 @@ import numpy as np
 from . import CORE_LIB_PATH, load as _load_vmhip
 
 ENGINE_GRAPH, ENGINE_RESIDENT = 0, 1
+DECODE_GRAPH, DECODE_PER_OP, DECODE_SLICES, DECODE_PERSISTENT = 0, 1, 2, 3
 W_EMBED, W_FINAL_NORM, W_LM_HEAD, W_ATTN_NORM, W_FFN_NORM = 0, 1, 2, 3, 4
 W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN = 5, 6, 7, 8, 9, 10, 11
 
@@ -50,11 +51,12 @@ def lib() -> ctypes.CDLL:
         L.vm_llama_packed_destroy.argtypes = [p]
         L.vm_llama_packed_destroy.restype = None
         L.vm_llama_session_create_packed.argtypes = [p, c_int64, POINTER(c_void_p)]
+        L.vm_llama_session_decode_path.argtypes = [p, POINTER(c_int)]
         for name in ("vm_llama_weights_create", "vm_llama_weights_set", "vm_llama_weights_fill_synthetic",
                      "vm_llama_weights_tie_lm_head",
                      "vm_llama_session_create", "vm_llama_prefill", "vm_llama_forward_step", "vm_llama_generate",
                      "vm_llama_pack", "vm_llama_packed_save", "vm_llama_packed_config", "vm_llama_packed_load",
-                     "vm_llama_session_create_packed"):
+                     "vm_llama_session_create_packed", "vm_llama_session_decode_path"):
             getattr(L, name).restype = c_int
         _lib = L
     return _lib
@@ -198,6 +200,12 @@ class Session:
         _check(lib().vm_llama_generate(self.handle, t.ctypes.data, t.size, steps, int(use_hip_graph),
                                        out.ctypes.data, timing.ctypes.data))
         return out, (float(timing[0]), float(timing[1]), int(timing[2]))
+
+    def decode_path(self) -> int:
+        """DECODE_GRAPH / _PER_OP / _SLICES / _PERSISTENT."""
+        v = c_int(-1)
+        _check(lib().vm_llama_session_decode_path(self.handle, byref(v)))
+        return v.value
 
     def close(self) -> None:
         if self.handle.value:
