@@ -21,6 +21,15 @@ two events on the launch stream.  ``cpu_baseline``
 times the oracle's scalar INT4 path (src/cpu/ops/quantized_matmul.cpp:48-141)
 on one pinned core over a bounded sample of the same step.
 
+``per_shape``, ``gemm`` and ``config1_int8_gemv`` time each launch on the
+next of enough weight copies to walk >= 512 MB (twice the Infinity Cache),
+so that their GB/s are HBM figures.
+
+``config1_int8_gemv`` is BASELINE config 1, the INT8 per-column decode GEMV
+at K 576 x N 1536, with its CPU leg: the oracle's restatement of the
+reference's AVX2 streaming decode (quantized_matmul.cpp:146-188) on one
+pinned core.
+
 ``gemm`` is BASELINE config 3, the MFMA path (M in {16, 128, 512}, K 2048,
 N 5632, INT8 and INT4): TFLOP/s as a fraction of the dense fp16 MFMA peak
 (2.5 PFLOP/s) and algorithmic GB/s.
@@ -36,7 +45,9 @@ weights: prefill and decode tokens/s, and the decode step's weight stream
 (packed codes + scales of every QuantizedMatMul per token) as GB/s and as a
 fraction of HBM peak.  ``persistent_step`` is the same decode with the
 one-launch step vm_hip_decode_step (slower than the default captured
-launch-per-projection step on this GPU, so reported beside it).
+launch-per-projection step on this GPU, so reported beside it).  For
+config 4, ``graph_engine`` is the drop-in path: the reference engine's loop
+over a Graph on DeviceType::HIP per call (32 decode steps).
 
 Prints one JSON line.  Only --gpus 1 is supported (one GPU per box).
 """
@@ -49,6 +60,7 @@ import sys
 import time
 
 import numpy as np
+from ctypes import c_void_p
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 for _p in (os.path.join(ROOT, "velo-mind_amd"), os.path.join(ROOT, "oracle")):
@@ -125,56 +137,78 @@ class Workload:
             H.qmm_f32(self.x[k].addr, p.addr, s.addr, self.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
 
 
+ROTATION_BYTES = 512 << 20   # weight copies a timed replay walks: twice the 256 MB Infinity Cache
+
+
+class Rotation:
+    """`copies` device copies of one packed weight (codes, scales) in one
+    allocation, enough that a replay walking them reads at least
+    ROTATION_BYTES, so that every launch streams its weights from HBM rather
+    than from the Infinity Cache of the previous replay."""
+
+    def __init__(self, H, codes, scales, stream, min_copies: int = 1):
+        lib = H.open_library()
+        self.cb, self.sb = codes.nbytes, scales.nbytes
+        self.stride = (self.cb + self.sb + 255) // 256 * 256
+        self.copies = max(min_copies, -(-ROTATION_BYTES // (self.cb + self.sb)))
+        self.buf = H.DeviceBuffer(self.copies * self.stride)
+        base = self.buf.addr
+        for i in range(self.copies):
+            H.check(lib.vm_hip_memcpy_d2d(c_void_p(base + i * self.stride), codes.ptr, self.cb, stream.handle))
+            H.check(lib.vm_hip_memcpy_d2d(c_void_p(base + i * self.stride + self.cb), scales.ptr, self.sb,
+                                          stream.handle))
+        stream.synchronize()
+        self.addrs = [(base + i * self.stride, base + i * self.stride + self.cb) for i in range(self.copies)]
+        self.bytes = self.copies * (self.cb + self.sb)
+
+    def close(self) -> None:
+        self.buf.close()
+
+
+def timed_replay(H, stream, launch_all, reps: int, use_graph: bool = True) -> float:
+    """Milliseconds per replay of launch_all, as one HIP graph (or eager
+    launches) replayed `reps` times between two events on `stream`."""
+    g = None
+    if use_graph:
+        g = H.Graph(stream)
+        g.begin()
+        launch_all()
+        g.end()
+    replay = g.launch if g is not None else launch_all
+    replay()
+    stream.synchronize()
+    e0, e1 = H.Event(), H.Event()
+    e0.record(stream.handle)
+    for _ in range(reps):
+        replay()
+    e1.record(stream.handle)
+    e1.synchronize()
+    if g is not None:
+        g.close()
+    return e0.elapsed_ms(e1) / reps
+
+
 def per_shape_durations(H, wl: Workload, reps: int, use_graph: bool) -> dict:
-    """Average launch duration per shape: for each shape, that shape's
-    launches of the step (each on its own weight copy) are replayed `reps`
-    times between two events on the launch stream, as one HIP graph (or,
-    with use_graph False, as eager launches, which the host's launch rate
-    can bound)."""
+    """Average launch duration per shape: each shape's GEMV launched once
+    per weight copy of a Rotation (>= 512 MB of copies, so every launch
+    reads HBM), the launches replayed `reps` times between two events on
+    the launch stream as one HIP graph (or, with use_graph False, as eager
+    launches, which the host's launch rate can bound)."""
     st = wl.stream
     out = {}
-    lib = H.open_library()
     for key in sorted({(k, n) for _, k, n, _, _ in wl.calls}):
         calls = [c for c in wl.calls if (c[1], c[2]) == key]
         count = len(calls)
-        # A shape launched once per step (lm_head) is timed over eight weight
-        # copies (328 MB, more than the Infinity Cache), so the replay's own
-        # overhead is amortised and the weights still stream from HBM.
-        extra = []
-        while len(calls) < 8:
-            _, k, n, p0, s0 = calls[0]
-            p = H.DeviceBuffer(p0.nbytes)
-            s = H.DeviceBuffer(s0.nbytes)
-            H.check(lib.vm_hip_memcpy_d2d(p.ptr, p0.ptr, p0.nbytes, st.handle))
-            H.check(lib.vm_hip_memcpy_d2d(s.ptr, s0.ptr, s0.nbytes, st.handle))
-            extra.append((p, s))
-            calls.append(("copy", k, n, p, s))
+        k, n = key
+        mp, ms = wl.masters[key]
+        rot = Rotation(H, mp, ms, st)
 
         def launch_all():
-            for _, k, n, p, s in calls:
-                H.qmm_f32(wl.x[k].addr, p.addr, s.addr, wl.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
+            for pa, sa in rot.addrs:
+                H.qmm_f32(wl.x[k].addr, pa, sa, wl.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
 
-        g = None
-        if use_graph:
-            g = H.Graph(st)
-            g.begin()
-            launch_all()
-            g.end()
-        replay = g.launch if g is not None else launch_all
-        replay()
-        st.synchronize()
-        e0, e1 = H.Event(), H.Event()
-        e0.record(st.handle)
-        for _ in range(reps):
-            replay()
-        e1.record(st.handle)
-        e1.synchronize()
-        out[key] = (e0.elapsed_ms(e1) / (reps * len(calls)), count)
-        if g is not None:
-            g.close()
-        for p, s in extra:
-            p.close()
-            s.close()
+        out[key] = (timed_replay(H, st, launch_all, reps, use_graph) / rot.copies, count, rot.copies, rot.bytes)
+        rot.close()
     return out
 
 
@@ -243,6 +277,10 @@ def cpu_baseline(target_s: float) -> dict:
             "tokens_per_s": round(sweeps / dt, 4)}
 
 
+# The drop-in path (graph engine) is timed on config 4, with its decode
+# steps capped so that the leg stays within seconds.
+GRAPH_ENGINE_E2E = {"smollm2_360m_int8": 32}
+
 E2E_MODELS = {
     # TinyLlama-1.1B shapes, synthetic INT4 weights,
     # 512-token uniform-random prompt, 256 greedy decode tokens.
@@ -250,11 +288,12 @@ E2E_MODELS = {
                                          num_heads=32, num_kv_heads=4, rms_norm_eps=1e-5, rope_theta=10000.0),
                                 quant=2, block=32, prompt=512, steps=256),
     # SmolLM2-360M shapes, synthetic INT8 weights,
-    # 128-token prompt, 128 greedy decode tokens (tied embeddings: the
-    # lm_head is its own packed copy of the embedding's transpose here).
+    # 128-token prompt, 128 greedy decode tokens; tied embeddings (the
+    # lm_head is quant.cpp's INT8 packing of the embedding's transpose).
     "smollm2_360m_int8": dict(cfg=dict(vocab_size=49152, hidden_size=960, intermediate_size=2560, num_layers=32,
-                                       num_heads=15, num_kv_heads=5, rms_norm_eps=1e-5, rope_theta=100000.0),
-                              quant=1, block=0, prompt=128, steps=128),
+                                       num_heads=15, num_kv_heads=5, rms_norm_eps=1e-5, rope_theta=100000.0,
+                                       tie_word_embeddings=True),
+                              quant=1, block=0, prompt=128, steps=128, tied=True),
 }
 
 
@@ -276,10 +315,15 @@ def decode_weight_bytes(c: dict, quant: int, block: int) -> int:
 DECODE_PATHS = {0: "graph", 1: "per-op", 2: "slices", 3: "persistent"}
 
 
-def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False) -> dict:
+def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph_engine: bool = False,
+              steps: int = 0) -> dict:
     """Greedy generation on the resident HIP decoder (HIP-graph decode
-    steps, or with persistent=True the one-launch step vm_hip_decode_step);
-    device-event timing of the prefill and of the decode steps."""
+    steps, or with persistent=True the one-launch step vm_hip_decode_step;
+    device-event timing of the prefill and of the decode steps), or with
+    graph_engine=True on the drop-in path: the reference engine's loop
+    (llama_engine.cpp:333-455), one Graph on DeviceType::HIP built and run
+    per call, host argmax over the logits read back, host wall-clock
+    timing."""
     from velomind_hip import llama as VL
 
     spec = E2E_MODELS[name]
@@ -292,25 +336,31 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False) -> di
         setattr(cfg, k, v)
     w = VL.Weights(cfg)
     w.fill_synthetic(20240601, 0.02)
-    prev = os.environ.get("VELOMIND_DECODE_PERSISTENT")
-    os.environ["VELOMIND_DECODE_PERSISTENT"] = "1" if persistent else "0"
-    try:
-        sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"],
-                          max_seq=spec["prompt"] + spec["steps"] + 1)
-    finally:
-        if prev is None:
-            del os.environ["VELOMIND_DECODE_PERSISTENT"]
-        else:
-            os.environ["VELOMIND_DECODE_PERSISTENT"] = prev
+    if spec.get("tied"):
+        w.tie_lm_head()
+    steps = steps or spec["steps"]
+    if graph_engine:
+        sess = VL.Session(w, VL.ENGINE_GRAPH, spec["quant"], spec["block"])
+    else:
+        prev = os.environ.get("VELOMIND_DECODE_PERSISTENT")
+        os.environ["VELOMIND_DECODE_PERSISTENT"] = "1" if persistent else "0"
+        try:
+            sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"],
+                              max_seq=spec["prompt"] + steps + 1)
+        finally:
+            if prev is None:
+                del os.environ["VELOMIND_DECODE_PERSISTENT"]
+            else:
+                os.environ["VELOMIND_DECODE_PERSISTENT"] = prev
     path = DECODE_PATHS[sess.decode_path()]
     if persistent and path != "persistent":
         raise RuntimeError(f"{name}: the persistent decode step does not cover this shape (path {path})")
     prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, spec["prompt"]).astype(np.int32)
-    sess.generate(prompt, 8, use_hip_graph=use_graph)  # warm-up (also sizes the workspaces)
-    _, (pf_s, dec_s, nd) = sess.generate(prompt, spec["steps"], use_hip_graph=use_graph)
+    sess.generate(prompt, 8 if not graph_engine else 2, use_hip_graph=use_graph)  # warm-up (sizes workspaces)
+    _, (pf_s, dec_s, nd) = sess.generate(prompt, steps, use_hip_graph=use_graph)
     wb = decode_weight_bytes(spec["cfg"], spec["quant"], spec["block"])
     dec_tps = nd / dec_s
-    out = {"prompt_tokens": spec["prompt"], "decode_tokens": spec["steps"], "decode_steps_timed": nd,
+    out = {"prompt_tokens": spec["prompt"], "decode_tokens": steps, "decode_steps_timed": nd,
            "prefill_tokens_per_s": round(spec["prompt"] / pf_s, 1), "prefill_ms": round(pf_s * 1e3, 3),
            "decode_tokens_per_s": round(dec_tps, 1), "decode_us_per_token": round(dec_s / nd * 1e6, 1),
            "decode_weight_bytes_per_token": wb, "decode_weight_GB_s": round(wb * dec_tps / 1e9, 1),
@@ -318,8 +368,10 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False) -> di
            "weights": ("int4 block 32" if spec["quant"] == 2 else "int8 per column") +
                       ", synthetic N(0, 0.02), packed on the GPU",
            "decode_path": path,
-           "engine": "resident HIP decoder, " + ("HIP-graph" if use_graph else "eager") +
-                     " decode steps, greedy argmax on device"}
+           "engine": ("graph engine: a Graph on DeviceType::HIP per call (the drop-in Op path), host argmax, "
+                      "host wall-clock timing" if graph_engine else
+                      "resident HIP decoder, " + ("HIP-graph" if use_graph else "eager") +
+                      " decode steps, greedy argmax on device")}
     sess.close()
     w.close()
     return out
@@ -354,36 +406,28 @@ def gemm_setup(H):
     return packs, a, c
 
 
-def gemm_bench(H, stream, reps: int = 10) -> dict:
-    """Config 3, the MFMA path: M in {16, 128, 512} x INT8 / INT4, each a
-    HIP graph of 20 launches replayed `reps` times between events.  FLOPs
-    2*M*K*N; algorithmic bytes codes + scales + fp32 A + fp32 C."""
+def gemm_bench(H, stream, reps: int = 5) -> dict:
+    """Config 3, the MFMA path: M in {16, 128, 512} x INT8 / INT4, launched
+    once per weight copy of a Rotation (>= 512 MB of copies, so that the
+    weights stream from HBM, not from the Infinity Cache), as one HIP graph
+    replayed `reps` times between events.  FLOPs 2*M*K*N; algorithmic bytes
+    codes + scales + fp32 A + fp32 C."""
     packs, a, c = gemm_setup(H)
+    rots = {qt: Rotation(H, p, s, stream) for qt, (p, s, _) in packs.items()}
     out = {}
     for m in (16, 128, 512):
         for qt in (H.QUANT_INT8, H.QUANT_INT4):
-            p, s, blk = packs[qt]
+            blk = packs[qt][2]
+            rot = rots[qt]
 
-            def launch():
-                H.qmm_f32(a.addr, p.addr, s.addr, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
+            def launch_all():
+                for pa, sa in rot.addrs:
+                    H.qmm_f32(a.addr, pa, sa, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
 
-            launch()
+            # an eager pass sizes the split-K and staging workspaces before capture
+            launch_all()
             stream.synchronize()
-            g = H.Graph(stream)
-            g.begin()
-            for _ in range(20):
-                launch()
-            g.end()
-            g.launch()
-            stream.synchronize()
-            e0, e1 = H.Event(), H.Event()
-            e0.record(stream.handle)
-            for _ in range(reps):
-                g.launch()
-            e1.record(stream.handle)
-            e1.synchronize()
-            g.close()
-            us = e0.elapsed_ms(e1) * 1e3 / (20 * reps)
+            us = timed_replay(H, stream, launch_all, reps) * 1e3 / rot.copies
             flops = 2.0 * m * GEMM_K * GEMM_N
             codes = GEMM_K * GEMM_N if qt == H.QUANT_INT8 else GEMM_K // 2 * GEMM_N
             scales = GEMM_N * 4 if qt == H.QUANT_INT8 else GEMM_K // BLOCK * GEMM_N * 4
@@ -391,12 +435,80 @@ def gemm_bench(H, stream, reps: int = 10) -> dict:
             tf = flops / (us * 1e-6) / 1e12
             out[f"M{m}_{'int8' if qt == H.QUANT_INT8 else 'int4'}"] = {
                 "us": round(us, 2), "TFLOP_s": round(tf, 1), "frac_of_mfma_f16_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "rotation": f"{rot.copies} weight copies, {rot.bytes / 2**20:.0f} MiB"}
+    for rot in rots.values():
+        rot.close()
     for p, s, _ in packs.values():
         p.close()
         s.close()
     a.close()
     c.close()
+    return out
+
+
+CONFIG1_K, CONFIG1_N = 576, 1536
+
+
+def config1_bench(H, stream, reps: int = 10, cpu_seconds: float = 3.0) -> dict:
+    """the INT8 per-column decode GEMV (M=1), K 576 x
+    N 1536 (quantized_matmul.cpp:190-235's streaming decode shape).  W
+    N(0, 0.02) packed on the GPU by vm_hip_pack_int8 (bit-exact with
+    quant.cpp); launched once per weight copy of a Rotation (>= 512 MB) in
+    one HIP graph replayed `reps` times.  The CPU leg is the oracle's
+    restatement of decode_stream_int8_avx2 (quantized_matmul.cpp:146-188)
+    on one pinned core, on the same codes (cache-resident: 0.9 MB)."""
+    import oracle as O
+
+    rng = np.random.default_rng(3)
+    k, n = CONFIG1_K, CONFIG1_N
+    w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal(k, dtype=np.float32)
+    dw = H.DeviceBuffer.from_array(w)
+    p, s = H.DeviceBuffer(k * n), H.DeviceBuffer(n * 4)
+    H.pack_int8(dw.addr, p.addr, s.addr, k, n)
+    H.synchronize()
+    dw.close()
+    dx, dc = H.DeviceBuffer.from_array(x), H.DeviceBuffer(n * 4)
+    rot = Rotation(H, p, s, stream)
+
+    def launch_all():
+        for pa, sa in rot.addrs:
+            H.qmm_f32(dx.addr, pa, sa, dc.addr, 1, k, n, H.QUANT_INT8, 0, stream)
+
+    launch_all()
+    stream.synchronize()
+    us = timed_replay(H, stream, launch_all, reps) * 1e3 / rot.copies
+    nbytes = k * n + n * 4 + k * 4 + n * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out = {"shape_KxN": f"{k}x{n}", "us": round(us, 3), "algo_bytes_per_launch": nbytes, "GB_s": round(gbs, 1),
+           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "rotation": f"{rot.copies} weight copies, {rot.bytes / 2**20:.0f} MiB"}
+    rot.close()
+    if cpu_seconds > 0:
+        q = p.download(np.int8, (k, n))
+        sc = s.download(np.float32, (n,))
+        cpu = sorted(os.sched_getaffinity(0))[0]
+        prev = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {cpu})
+        try:
+            calls = 0
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < cpu_seconds:
+                for _ in range(50):
+                    O.qmm_decode_int8(x, q, sc)
+                calls += 50
+            dt = time.perf_counter() - t0
+        finally:
+            os.sched_setaffinity(0, prev)
+        out["cpu_baseline"] = {"value": round(nbytes * calls / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+                               "kind": "port", "us_per_call": round(dt / calls * 1e6, 2),
+                               "avx2_fma": O.has_avx2_fma(),
+                               "sample": f"{calls} calls of the oracle's decode_stream_int8_avx2 restatement "
+                                         f"(quantized_matmul.cpp:146-188) on core {cpu}, {dt:.1f} s, "
+                                         "weights cache-resident"}
+    for b in (p, s, dx, dc):
+        b.close()
     return out
 
 
@@ -480,7 +592,8 @@ def main() -> int:
     ap.add_argument("--no-large", action="store_true", help="skip the 70B-class decode GEMV leg")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg, printed as one JSON line")
     ap.add_argument("--gemm-profile", default="",
-                    help="M,QT,REPS: only REPS eager launches of one config-3 GEMM (rocprofv3 counter passes)")
+                    help="M,QT,REPS: only REPS eager launches of one config-3 GEMM, each on the next weight copy "
+                         "of a >= 512 MB rotation (rocprofv3 counter passes)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (rocprofv3 counter calibration)")
     args = ap.parse_args()
@@ -505,10 +618,12 @@ def main() -> int:
         m, qt, reps = (int(v) for v in args.gemm_profile.split(","))
         packs, a, c = gemm_setup(H)
         p, s, blk = packs[qt]
-        for _ in range(reps):
-            H.qmm_f32(a.addr, p.addr, s.addr, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
+        rot = Rotation(H, p, s, stream)
+        for i in range(reps):
+            pa, sa = rot.addrs[i % rot.copies]
+            H.qmm_f32(a.addr, pa, sa, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
         stream.synchronize()
-        log(f"bench: {reps} GEMM launches M={m} quant_type={qt} done")
+        log(f"bench: {reps} GEMM launches M={m} quant_type={qt} done, walking {rot.copies} weight copies")
         return 0
     if args.gemm_only:
         print(json.dumps({"metric": METRIC, "gemm": gemm_bench(H, stream)}), flush=True)
@@ -586,14 +701,15 @@ def main() -> int:
 
     durs = per_shape_durations(H, wl, args.shape_reps, graph is not None)
     per_shape = {}
-    for (k, n), (ms, count) in durs.items():
+    for (k, n), (ms, count, copies, rbytes) in durs.items():
         b = algo_bytes(k, n)
         per_shape[f"{k}x{n}"] = {"launches_per_step": count, "avg_launch_us": round(ms * 1e3, 3),
                                  "algo_bytes_per_launch": b, "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
-                                 "us_per_step": round(ms * 1e3 * count, 1)}
+                                 "us_per_step": round(ms * 1e3 * count, 1),
+                                 "rotation": f"{copies} weight copies, {rbytes / 2**20:.0f} MiB"}
     # The roofline is reported for the dominant kernel: the shape whose
     # launches take the most time per step.
-    (dk, dn), (dms, dcount) = max(durs.items(), key=lambda kv: kv[1][0] * kv[1][1])
+    (dk, dn), (dms, dcount, _, _) = max(durs.items(), key=lambda kv: kv[1][0] * kv[1][1])
     dbytes = algo_bytes(dk, dn)
     achieved = dbytes / (dms * 1e-3) / 1e9
     launches = len(wl.calls)
@@ -610,11 +726,22 @@ def main() -> int:
             log(f"bench: {name}: prefill {e2e[name]['prefill_tokens_per_s']} tok/s, "
                 f"decode {e2e[name]['decode_tokens_per_s']} tok/s ({e2e[name]['decode_path']}), "
                 f"persistent step {pers['decode_tokens_per_s']} tok/s")
+            if name in GRAPH_ENGINE_E2E:
+                ge = e2e_bench(name, graph_engine=True, steps=GRAPH_ENGINE_E2E[name])
+                e2e[name]["graph_engine"] = {k: ge[k] for k in ("prefill_tokens_per_s", "prefill_ms", "decode_tokens",
+                                                                "decode_tokens_per_s", "decode_us_per_token", "engine")}
+                log(f"bench: {name} graph engine: prefill {ge['prefill_tokens_per_s']} tok/s, "
+                    f"decode {ge['decode_tokens_per_s']} tok/s")
 
     gemm = None
     if not args.no_gemm and not args.only_shape:
         log("bench: prefill GEMM (config 3)")
         gemm = gemm_bench(H, stream)
+
+    config1 = None
+    if not args.only_shape:
+        log("bench: INT8 decode GEMV (config 1)")
+        config1 = config1_bench(H, stream, cpu_seconds=3.0 if args.cpu_seconds > 0 else 0.0)
 
     large = None
     if not args.no_large and not args.only_shape:
@@ -666,6 +793,7 @@ def main() -> int:
         "step_stats": step_stats,
         "per_shape": per_shape,
         "e2e": e2e,
+        "config1_int8_gemv": config1,
         "gemm": gemm,
         "gemv_large": large,
         "cpu_baseline": cpu,

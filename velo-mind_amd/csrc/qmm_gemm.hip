@@ -539,8 +539,11 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 // reaches the output as the reference's fp32 arithmetic would propagate
 // it); hi = fp16(a * 2^x_r) and lo = fp16(a * 2^x_r - hi), the difference
 // being exact in fp32.  hi at ah[r * k + c], lo at ah[m * k + r * k + c].
-// One workgroup per row; the row is read twice (max, then split), the
-// second time from L2.
+// One workgroup per row.  Rows of up to kSplitHeld float4 groups per
+// thread stay in registers between the maximum and the split (one read of
+// A); longer rows are read a second time (from L2).
+constexpr int kSplitHeld = 6;   // k <= 6144 in one read
+
 __global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restrict__ a,
                                                           _Float16* __restrict__ ah,
                                                           int* __restrict__ row_exp, int m, int k, int vec) {
@@ -549,18 +552,30 @@ __global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restric
     const int tid = threadIdx.x;
     const float* src = a + static_cast<int64_t>(row) * k;
     const int vecs = k >> 2;   // k % 32 == 0 on this path
+    const bool held = vecs <= kSplitHeld * 256;
     auto load4 = [&](int v) {
         if (vec) return reinterpret_cast<const float4*>(src)[v];
         return make_float4(src[4 * v], src[4 * v + 1], src[4 * v + 2], src[4 * v + 3]);
     };
+    float4 keep[kSplitHeld];
     float mx = 0.0f;
     bool special = false;
-    for (int v = tid; v < vecs; v += 256) {
-        const float4 x = load4(v);
+    auto scan = [&](const float4& x) {
         const float t = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
         special |= !(fabsf(x.x) <= 3.4028235e38f) || !(fabsf(x.y) <= 3.4028235e38f) ||
                    !(fabsf(x.z) <= 3.4028235e38f) || !(fabsf(x.w) <= 3.4028235e38f);
         mx = fmaxf(mx, t);
+    };
+    if (held) {
+#pragma unroll
+        for (int r = 0; r < kSplitHeld; ++r) {
+            const int v = tid + r * 256;
+            keep[r] = v < vecs ? load4(v) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int r = 0; r < kSplitHeld; ++r) scan(keep[r]);
+    } else {
+        for (int v = tid; v < vecs; v += 256) scan(load4(v));
     }
     // an infinity or NaN anywhere in the row disables the scaling
     if (special) mx = __builtin_inff();
@@ -577,8 +592,7 @@ __global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restric
     if (tid == 0) row_exp[row] = x;
     half4v* hi = reinterpret_cast<half4v*>(ah + static_cast<int64_t>(row) * k);
     half4v* lo = reinterpret_cast<half4v*>(ah + (static_cast<int64_t>(m) + row) * k);
-    for (int v = tid; v < vecs; v += 256) {
-        const float4 y = load4(v);
+    auto split = [&](int v, const float4& y) {
         const float s0 = ldexpf(y.x, x), s1 = ldexpf(y.y, x), s2 = ldexpf(y.z, x), s3 = ldexpf(y.w, x);
         const half4v h = {static_cast<_Float16>(s0), static_cast<_Float16>(s1), static_cast<_Float16>(s2),
                           static_cast<_Float16>(s3)};
@@ -589,6 +603,15 @@ __global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restric
             return static_cast<_Float16>(d == d && fabsf(d) <= 65504.0f ? d : 0.0f);
         };
         lo[v] = half4v{rest(s0, h[0]), rest(s1, h[1]), rest(s2, h[2]), rest(s3, h[3])};
+    };
+    if (held) {
+#pragma unroll
+        for (int r = 0; r < kSplitHeld; ++r) {
+            const int v = tid + r * 256;
+            if (v < vecs) split(v, keep[r]);
+        }
+    } else {
+        for (int v = tid; v < vecs; v += 256) split(v, load4(v));
     }
 }
 
@@ -600,17 +623,15 @@ struct GemmConfig {
 // on MI355X over config-3 shapes (K = 2048, N = 5632, M = 16..512) and the
 // TinyLlama / SmolLM2 prefill projections (M = 512: N = 2048..11264, K =
 // 2048 and 5632; M = 128: K, N = 960..5120):
-//   M <= 128: 32 x 64 tiles (many small workgroups hide load latency best),
-//     64 x 64 for INT4 with M > 64;
+//   M <= 128: 32 x 64 tiles (many small workgroups hide load latency best);
 //     K splits (at least four 64-row steps each) until about two workgroups
 //     per CU, while the fp32 partials stay under a quarter of the code
 //     bytes -- or, with fewer than 128 tiles, while each split keeps at
-//     least eight steps;
-//   M > 128: 64 x 128 tiles (INT8 per column unsplit: 64 x 64); K splits
-//     of at least twenty 64-row steps up
-//     to ~512 workgroups (K = 5632: 4 splits); 32 x 128 when an unsplit
-//     grid would hold fewer than 150 tiles (N = 2048: 27.5 us vs 42.1 us
-//     with the former 128 x 128 tiles).
+//     least eight steps; INT4 with M > 64 at least two splits;
+//   M > 128: 64 x 128 tiles (M = 512, K = 2048, N = 5632, INT8, weights
+//     cold: 51.2 us vs 64.2 with 64 x 64); K splits of at least twenty
+//     64-row steps up to ~512 workgroups (K = 5632: 4 splits); 32 x 128
+//     when an unsplit grid would hold fewer than 150 tiles (N = 2048).
 GemmConfig choose_gemm(int kind, int m, int k, int n) {
     GemmConfig cfg;
     const int steps = (k + kBK - 1) / kBK;
@@ -620,27 +641,25 @@ GemmConfig choose_gemm(int kind, int m, int k, int n) {
     };
     int s = 1;
     if (m <= 128) {
-        // INT4 with 64 < M <= 128: 64 x 64 tiles halve the nibble unpacking
-        // per MFMA (K = 2048, N = 5632, M = 128: 27.0 us vs 34.2 us).
         // M <= 16 (and INT8 M <= 32): 16-row tiles, no MFMA rows wasted on
         // padding.
-        cfg.bm = (kind == 2 && m > 64) ? 64 : ((m <= 16 || (kind != 2 && m <= 32)) ? 16 : 32);
+        cfg.bm = (m <= 16 || (kind != 2 && m <= 32)) ? 16 : 32;
         cfg.bn = 64;
         const long tiles = tiles_of(cfg.bm, cfg.bn);
         while (s * 2 <= 8 && tiles * s * 2 <= 512 &&
                ((steps / (s * 2) >= 4 && 4.0 * s * 2 * m * n <= 0.25 * code_bytes) ||
                 (tiles < 128 && steps / (s * 2) >= 8)))
             s *= 2;
+        // INT4 with 64 < M <= 128: two K splits spread its heavier B
+        // unpacking (K = 2048, N = 5632, M = 128, weights cold: 33.5 us vs
+        // 38.1 unsplit, 38.4 with 64 x 64 tiles)
+        if (kind == 2 && m > 64 && s == 1 && steps >= 16) s = 2;
     } else {
         cfg.bm = 64;
         cfg.bn = 128;
         const long tiles = tiles_of(cfg.bm, cfg.bn);
         while (s * 2 <= 4 && tiles * s * 2 <= 512 && steps / (s * 2) >= 20) s *= 2;
         if (s == 1 && tiles < 150) cfg.bm = 32;
-        // INT8 per column, unsplit: 64 x 64 (M = 512, K = 2048, N = 5632:
-        // 35.2 us vs 37.6 us; its B dequantisation is cheap enough that the
-        // doubled workgroup count wins)
-        if (kind == 0 && s == 1 && cfg.bm == 64) cfg.bn = 64;
     }
     cfg.splits = s;
     // M <= 32: every K step of a split in flight at once (8 steps INT8, 4
