@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdint>
 
+#include "decode_attn.h"
 #include "vm_device.h"
 #include "vm_hip.h"
 #include "vm_internal.h"
@@ -317,7 +318,8 @@ __global__ void rope_kv_append_kernel(const float* __restrict__ qkv, const float
 //   1. every thread issues its 16-byte loads of q, K and V (one memory
 //      round trip) into LDS;
 //   2. thread (j, g-slot) scores key j against its query heads; the CHUNK
-//      lanes of a key row reduce max and sum with cross-lane shuffles;
+//      (= 32) lanes of a key row reduce max and sum with DPP and a row swap
+//      (decode_attn.h);
 //   3. thread (g, float4 column) accumulates p . V over the chunk.
 // With one chunk the result is written directly.  Otherwise each chunk
 // stores (m, l, o) with agent-scope stores, takes a ticket once they are
@@ -338,10 +340,8 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
     constexpr int kPart = D + 4;           // partial record: m, l, -, -, o[0..D)
     constexpr int QV = (kMaxG * D4 + kT - 1) / kT;
     constexpr int KV = CHUNK * D4 / kT;    // 16-byte loads per thread for a K (or V) chunk
-    constexpr int GS = kT / CHUNK;         // query-head slots while scoring
-    constexpr int GI = kMaxG / GS;
-    constexpr int PS = kT / D4;            // query-head slots while accumulating p . V
-    static_assert(CHUNK * D4 % kT == 0 && 64 % CHUNK == 0 && kT % D4 == 0, "tile shape");
+    static_assert(CHUNK == ChunkAttention<D>::kChunk && kMaxG == ChunkAttention<D>::kMaxG, "decode_attn.h tile");
+    static_assert(CHUNK * D4 % kT == 0 && kT % D4 == 0, "tile shape");
     __shared__ __align__(16) float sq[kMaxG * D];
     __shared__ __align__(16) float sk[CHUNK * kKS];
     __shared__ __align__(16) float sv[CHUNK * D];
@@ -389,61 +389,11 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
     }
     __syncthreads();
 
-    // Scores: thread (j = tid % CHUNK, slot = tid / CHUNK), heads slot + i * GS.
-    {
-        const int j = tid % CHUNK, slot = tid / CHUNK;
-        float sc[GI];
-#pragma unroll
-        for (int i = 0; i < GI; ++i) sc[i] = 0.0f;
-#pragma unroll 4
-        for (int c = 0; c < D4; ++c) {
-            const float4 kv = *reinterpret_cast<const float4*>(sk + j * kKS + 4 * c);
-#pragma unroll
-            for (int i = 0; i < GI; ++i) {
-                const int g = slot + i * GS;
-                if (g < G) {
-                    const float4 qv = *reinterpret_cast<const float4*>(sq + g * D + 4 * c);
-                    sc[i] = fmaf(qv.x, kv.x, sc[i]);
-                    sc[i] = fmaf(qv.y, kv.y, sc[i]);
-                    sc[i] = fmaf(qv.z, kv.z, sc[i]);
-                    sc[i] = fmaf(qv.w, kv.w, sc[i]);
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < GI; ++i) {
-            const int g = slot + i * GS;
-            if (g < G) {
-                const float sv_ = j < nk ? sc[i] * scale : -INFINITY;
-                float mx = sv_;
-#pragma unroll
-                for (int off = CHUNK / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-                const float p = j < nk ? expf(sv_ - mx) : 0.0f;
-                float sum = p;
-#pragma unroll
-                for (int off = CHUNK / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-                sp[g][j] = p;
-                if (j == 0) {
-                    sm[g] = mx;
-                    sl[g] = sum;
-                }
-            }
-        }
-    }
+    // Scores, softmax partial and p . V (decode_attn.h).
+    using CA = ChunkAttention<D>;
+    CA::scores(sq, sk, sp, sm, sl, G, nk, scale);
     __syncthreads();
-
-    // p . V: thread (c4 = tid % D4, slot = tid / D4), heads slot + i * PS.
-    const int c4 = tid % D4, pslot = tid / D4;
-    for (int g = pslot; g < G; g += PS) {
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int jj = 0; jj < nk; ++jj) {
-            const float p = sp[g][jj];
-            const float4 v = *reinterpret_cast<const float4*>(sv + jj * D + 4 * c4);
-            acc.x = fmaf(p, v.x, acc.x);
-            acc.y = fmaf(p, v.y, acc.y);
-            acc.z = fmaf(p, v.z, acc.z);
-            acc.w = fmaf(p, v.w, acc.w);
-        }
+    CA::pv(sv, sp, G, nk, [&](int g, int c4, float4 acc) {
         if (nc == 1) {
             const float inv = 1.0f / sl[g];
             *reinterpret_cast<float4*>(out + (static_cast<int64_t>(hk) * G + g) * D + 4 * c4) =
@@ -459,7 +409,7 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
                 coherent_store(part + 1, sl[g]);
             }
         }
-    }
+    });
     if (nc == 1) return;
     publish_partials();
     __syncthreads();
@@ -467,9 +417,11 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
     __syncthreads();
     if (ticket != static_cast<unsigned>(nc - 1)) return;
 
-    // Merge in chunk order: running (M, L, O) rescaled by exp(M - M').
+    // Merge in chunk order: running (M, L, O) rescaled by exp(M - M');
+    // thread (c4 = tid % D4, heads tid / D4 + i * kT / D4).
     constexpr int kB = 16;
-    for (int g = pslot; g < G; g += PS) {
+    const int c4 = tid % D4;
+    for (int g = tid / D4; g < G; g += kT / D4) {
         const float* base = partials + (static_cast<int64_t>(hk) * G + g) * gridDim.x * kPart;
         float M = -INFINITY, Lsum = 0.0f;
         float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -577,11 +529,9 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
     constexpr int kKS = D + 4;
     constexpr int kPart = D + 4;
     constexpr int KV = CHUNK * D4 / kT;
-    constexpr int GS = kT / CHUNK;
-    constexpr int GI = kMaxG / GS;
-    constexpr int PS = kT / D4;
     constexpr int kB = 16;   // slices per batch of loads
-    static_assert(CHUNK * D4 % kT == 0 && 64 % CHUNK == 0 && kT % D4 == 0 && kT % HALF == 0, "tile shape");
+    static_assert(CHUNK == ChunkAttention<D>::kChunk && kMaxG == ChunkAttention<D>::kMaxG, "decode_attn.h tile");
+    static_assert(CHUNK * D4 % kT == 0 && kT % D4 == 0 && kT % HALF == 0, "tile shape");
     __shared__ __align__(16) float sq[kMaxG * D];
     __shared__ __align__(16) float sk[CHUNK * kKS];
     __shared__ __align__(16) float sv[CHUNK * D];
@@ -739,68 +689,17 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
     }
     __syncthreads();
 
-    // 3. Scores and softmax partials: thread (j = tid % CHUNK, slot = tid / CHUNK).
-    {
-        const int j = tid % CHUNK, slot = tid / CHUNK;
-        float sc[GI];
-#pragma unroll
-        for (int i = 0; i < GI; ++i) sc[i] = 0.0f;
-#pragma unroll 4
-        for (int c = 0; c < D4; ++c) {
-            const float4 kv = *reinterpret_cast<const float4*>(sk + j * kKS + 4 * c);
-#pragma unroll
-            for (int i = 0; i < GI; ++i) {
-                const int g = slot + i * GS;
-                if (g < G) {
-                    const float4 qv = *reinterpret_cast<const float4*>(sq + g * D + 4 * c);
-                    sc[i] = fmaf(qv.x, kv.x, sc[i]);
-                    sc[i] = fmaf(qv.y, kv.y, sc[i]);
-                    sc[i] = fmaf(qv.z, kv.z, sc[i]);
-                    sc[i] = fmaf(qv.w, kv.w, sc[i]);
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < GI; ++i) {
-            const int g = slot + i * GS;
-            if (g < G) {
-                const float sv_ = j < nk ? sc[i] * scale : -INFINITY;
-                float mx = sv_;
-#pragma unroll
-                for (int off = CHUNK / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-                const float pr = j < nk ? expf(sv_ - mx) : 0.0f;
-                float sum = pr;
-#pragma unroll
-                for (int off = CHUNK / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-                sp[g][j] = pr;
-                if (j == 0) {
-                    sm[g] = mx;
-                    sl[g] = sum;
-                }
-            }
-        }
-    }
+    // 3. Scores, softmax partial and p . V (decode_attn.h); the chunk's record.
+    using CA = ChunkAttention<D>;
+    CA::scores(sq, sk, sp, sm, sl, G, nk, scale);
     __syncthreads();
-
-    // p . V: thread (c4 = tid % D4, slot = tid / D4); the chunk's record.
-    const int c4 = tid % D4, pslot = tid / D4;
-    for (int g = pslot; g < G; g += PS) {
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-        for (int jj = 0; jj < nk; ++jj) {
-            const float pr = sp[g][jj];
-            const float4 v = *reinterpret_cast<const float4*>(sv + jj * D + 4 * c4);
-            acc.x = fmaf(pr, v.x, acc.x);
-            acc.y = fmaf(pr, v.y, acc.y);
-            acc.z = fmaf(pr, v.z, acc.z);
-            acc.w = fmaf(pr, v.w, acc.w);
-        }
+    CA::pv(sv, sp, G, nk, [&](int g, int c4, float4 acc) {
         if (active) {
             float* rec = part + ((static_cast<int64_t>(hk) * G + g) * chunks + chunk) * kPart;
             *reinterpret_cast<float4*>(rec + 4 + 4 * c4) = acc;
             if (c4 == 0) *reinterpret_cast<float4*>(rec) = make_float4(sm[g], sl[g], 0.0f, 0.0f);
         }
-    }
+    });
 }
 
 // ---- Prefill attention over the resident cache with fp32 matrix cores:
@@ -1309,7 +1208,7 @@ int vm_hip_attention_decode_f32(const float* q, const float* k_cache, const floa
     }
     if (!q || !k_cache || !v_cache || !pos || !out) return fail_inval("attention_decode: null pointer");
     if (max_seq > (1 << 24) || heads > 65535) return fail_inval("attention_decode: too large");
-    const int chunk = head_dim == 64 ? 64 : 32;
+    const int chunk = 32;
     const int64_t chunks = (max_seq + chunk - 1) / chunk;
     if (chunks > 65535) return fail_inval("attention_decode: max_seq too large");
     Workspace ws;
@@ -1322,7 +1221,7 @@ int vm_hip_attention_decode_f32(const float* q, const float* k_cache, const floa
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
     const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(kv_heads));
     if (head_dim == 64)
-        hipLaunchKernelGGL((attention_decode_kernel<64, 64>), grid, dim3(kT), 0, S(stream), q, k_cache, v_cache, pos,
+        hipLaunchKernelGGL((attention_decode_kernel<64, 32>), grid, dim3(kT), 0, S(stream), q, k_cache, v_cache, pos,
                            out, static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(max_seq), sc,
                            ws.partials, ws.counters);
     else

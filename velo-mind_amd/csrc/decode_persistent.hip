@@ -59,6 +59,7 @@
 #include <map>
 #include <mutex>
 
+#include "decode_attn.h"
 #include "vm_device.h"
 #include "vm_internal.h"
 
@@ -869,69 +870,14 @@ __device__ void att_compute(const DecodeArgs& a, int layer, int item, int nc, in
     const int H = static_cast<int>(a.m.heads), Hk = static_cast<int>(a.m.kv_heads);
     const int G = H / Hk;
     const int hk = item / nc, chunk = item - hk * nc;
-    const int k0 = chunk * kAttChunk;
-    const int t = threadIdx.x;
-    const int n_keys = p + 1;
-    const int nk = min(kAttChunk, n_keys - k0);
-    // scores and softmax partials: thread (j = t % 32, slot = t / 32)
-    {
-        constexpr int GS = kT / kAttChunk;    // 8 head slots
-        constexpr int GI = kMaxG / GS;        // 2 heads per slot
-        constexpr int kKS = kD + 4;
-        const int j = t % kAttChunk, slot = t / kAttChunk;
-        float sc[GI];
-#pragma unroll
-        for (int i = 0; i < GI; ++i) sc[i] = 0.0f;
-#pragma unroll 4
-        for (int c = 0; c < kD4; ++c) {
-            const float4 kv = *reinterpret_cast<const float4*>(sm.sk + j * kKS + 4 * c);
-#pragma unroll
-            for (int i = 0; i < GI; ++i) {
-                const int g = slot + i * GS;
-                if (g < G) {
-                    const float4 qv = *reinterpret_cast<const float4*>(sm.sq + g * kD + 4 * c);
-                    sc[i] = fmaf(qv.x, kv.x, sc[i]);
-                    sc[i] = fmaf(qv.y, kv.y, sc[i]);
-                    sc[i] = fmaf(qv.z, kv.z, sc[i]);
-                    sc[i] = fmaf(qv.w, kv.w, sc[i]);
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < GI; ++i) {
-            const int g = slot + i * GS;
-            if (g < G) {
-                const float sv_ = j < nk ? sc[i] : -INFINITY;   // attention scale 1.0 (q pre-scaled by the loaders)
-                float mx = sv_;
-#pragma unroll
-                for (int off = kAttChunk / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-                const float pr = j < nk ? expf(sv_ - mx) : 0.0f;
-                float sum = pr;
-#pragma unroll
-                for (int off = kAttChunk / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-                sm.sp[g][j] = pr;
-                if (j == 0) {
-                    sm.sm[g] = mx;
-                    sm.sl[g] = sum;
-                }
-            }
-        }
-    }
+    const int nk = min(kAttChunk, p + 1 - chunk * kAttChunk);
+    using CA = ChunkAttention<kD>;
+    static_assert(CA::kChunk == kAttChunk && CA::kMaxG == kMaxG, "decode_attn.h tile");
+    // attention scale 1.0: the queries were scaled by their loaders
+    CA::scores(sm.sq, sm.sk, sm.sp, sm.sm, sm.sl, G, nk, 1.0f);
     __syncthreads();
-    // p . V and the chunk's record: thread (c4 = t % 16, pslot = t / 16)
     const uint32_t atag = tag_of(a, layer, kPhAtt);
-    const int c4 = t % kD4, pslot = t / kD4;
-    for (int g = pslot; g < G; g += kT / kD4) {
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-        for (int jj = 0; jj < nk; ++jj) {
-            const float pr = sm.sp[g][jj];
-            const float4 v = *reinterpret_cast<const float4*>(sm.sv + jj * kD + 4 * c4);
-            acc.x = fmaf(pr, v.x, acc.x);
-            acc.y = fmaf(pr, v.y, acc.y);
-            acc.z = fmaf(pr, v.z, acc.z);
-            acc.w = fmaf(pr, v.w, acc.w);
-        }
+    CA::pv(sm.sv, sm.sp, G, nk, [&](int g, int c4, float4 acc) {
         u64* rec = a.att + static_cast<int64_t>((hk * G + g) * a.max_chunks + chunk) * kRec;
         put2(rec + 4 + 4 * c4, acc.x, acc.y, atag);
         put2(rec + 6 + 4 * c4, acc.z, acc.w, atag);
@@ -939,7 +885,7 @@ __device__ void att_compute(const DecodeArgs& a, int layer, int item, int nc, in
             put2(rec, sm.sm[g], sm.sl[g], atag);
             put2(rec + 2, 0.0f, 0.0f, atag);
         }
-    }
+    });
     __syncthreads();   // LDS reused by the next item
 }
 
