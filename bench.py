@@ -21,6 +21,11 @@ two events on the launch stream.  ``cpu_baseline``
 times the oracle's scalar INT4 path (src/cpu/ops/quantized_matmul.cpp:48-141)
 on one pinned core over a bounded sample of the same step.
 
+``grouped_sweep`` is the same 155 GEMVs with the siblings that read one
+activation vector (q | k | v, gate | up) grouped into one launch each, as
+the graph compiler groups them on DeviceType::HIP: 89 launches per step.
+``value`` stays the per-QuantizedMatMul sweep.
+
 ``per_shape``, ``gemm`` and ``config1_int8_gemv`` time each launch on the
 next of enough weight copies to walk >= 512 MB (twice the Infinity Cache),
 so that their GB/s are HBM figures.
@@ -130,11 +135,34 @@ class Workload:
             self.calls.append((name, k, n, p, s))
         stream.synchronize()
         self.bytes_per_step = sum(algo_bytes(k, n) for _, k, n, _, _ in self.calls)
+        self.group_out = {}
 
     def launch_step(self) -> None:
         H, st = self.H, self.stream
         for _, k, n, p, s in self.calls:
             H.qmm_f32(self.x[k].addr, p.addr, s.addr, self.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, st)
+
+    def grouped_calls(self):
+        """The same step with the siblings that read one activation vector
+        grouped as the HIP graph compiler groups them (q | k | v and
+        gate | up per layer): [(k, [(codes, scales, out, n), ...]), ...]."""
+        groups, i = [], 0
+        while i < len(self.calls):
+            name, k, n, p, s = self.calls[i]
+            part = name.split(".")[-1]
+            size = {"q": 3, "gate": 2}.get(part, 1)
+            members = []
+            for name2, k2, n2, p2, s2 in self.calls[i:i + size]:
+                out = self.group_out.setdefault(name2.split(".")[-1], self.H.DeviceBuffer(n2 * 4))
+                members.append((p2.addr, s2.addr, out.addr, n2))
+            groups.append((k, members))
+            i += size
+        return groups
+
+    def launch_grouped_step(self, groups) -> None:
+        H, st = self.H, self.stream
+        for k, members in groups:
+            H.qmm_group_f32(self.x[k].addr, 1, k, members, H.QUANT_INT4, BLOCK, st)
 
 
 ROTATION_BYTES = 512 << 20   # weight copies a timed replay walks: twice the 256 MB Infinity Cache
@@ -699,6 +727,37 @@ def main() -> int:
                   "p95_ms": round(float(np.percentile(per_step, 95)), 5),
                   "min_ms": round(float(per_step.min()), 5), "max_ms": round(float(per_step.max()), 5)}
 
+    # The same sweep with sibling GEMVs grouped (one launch per q | k | v
+    # and per gate | up), as the drop-in graph path runs them on HIP.
+    grouped = None
+    if not args.only_shape:
+        groups = wl.grouped_calls()
+        wl.launch_grouped_step(groups)
+        stream.synchronize()
+        gg = H.Graph(stream)
+        gg.begin()
+        wl.launch_grouped_step(groups)
+        gg.end()
+        for _ in range(args.warmup):
+            gg.launch()
+        stream.synchronize()
+        g0, g1 = H.Event(), H.Event()
+        g0.record(stream.handle)
+        for _ in range(args.steps):
+            gg.launch()
+        g1.record(stream.handle)
+        g1.synchronize()
+        gms = g0.elapsed_ms(g1) / args.steps
+        gg.close()
+        grouped = {"launches_per_step": len(groups), "ms_per_step": round(gms, 5),
+                   "GB_s": round(wl.bytes_per_step / (gms * 1e-3) / 1e9, 1),
+                   "pct_of_hbm_peak": round(100.0 * wl.bytes_per_step / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                   "gemv_tokens_per_s": round(1e3 / gms, 1),
+                   "grouping": "per layer q|k|v (2048 x 2560) and gate|up (2048 x 11264) as one "
+                               "vm_hip_qmm_group_f32 launch each; o, down, lm_head alone",
+                   "algo_bytes_per_step": wl.bytes_per_step}
+        log(f"bench: grouped sweep {gms * 1e3:.1f} us/step, {grouped['GB_s']} GB/s")
+
     durs = per_shape_durations(H, wl, args.shape_reps, graph is not None)
     per_shape = {}
     for (k, n), (ms, count, copies, rbytes) in durs.items():
@@ -791,6 +850,7 @@ def main() -> int:
             "algo_bytes_per_launch": dbytes,
         },
         "step_stats": step_stats,
+        "grouped_sweep": grouped,
         "per_shape": per_shape,
         "e2e": e2e,
         "config1_int8_gemv": config1,

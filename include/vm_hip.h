@@ -131,13 +131,41 @@ int vm_hip_graph_destroy(void* graph_exec);
  *               into it (quantized_matmul.cu:262).
  *
  * Accumulation is fp32.  rows_m <= 4 runs the HBM-bound GEMV kernels;
- * larger rows_m runs the MFMA GEMM, which rounds A to fp16 (codes are exact
- * in fp16 and scales stay fp32).  k == 0 writes zeros; rows_m == 0 or
- * n == 0 is a no-op.
+ * larger rows_m runs the MFMA GEMM, which carries each row of A as two
+ * fp16 parts under a power-of-two row scale (22 significant bits for any
+ * finite fp32 A; INT8 codes are exact in fp16, per-column scales apply in
+ * fp32, blockwise weights are staged as fp16(code * scale / 2^e)).  k == 0
+ * writes zeros; rows_m == 0 or n == 0 is a no-op.
  */
 int vm_hip_qmm_f32(const float* a, const int8_t* wq, const float* scale, float* c,
                    int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size,
                    void* stream);
+
+/*
+ * Sibling quantized matmuls sharing A: for every member g,
+ * C_g[rows_m, n_g] = A[rows_m, k] x W_g (codes_g, scales_g), all with the
+ * same quant_type and block_size.  No counterpart in the reference, whose
+ * graph runs q, k, v (and gate, up) as separate QuantizedMatMul nodes
+ * (examples/common/llama/llama_graph.cpp:118, :132-136); the graph compiler
+ * on DeviceType::HIP groups such siblings into one call.
+ *
+ * rows_m <= 4: ONE GEMV launch covers the members' columns side by side
+ * (weights read once each, one launch and one split-K tail instead of
+ * count); the K split follows the combined width, so each C_g equals the
+ * separate vm_hip_qmm_f32 result up to the grouping of its fp32 partial
+ * sums.  Larger rows_m (or a member the GEMV does not cover): one
+ * vm_hip_qmm_f32 per member.  Each member is checked as vm_hip_qmm_f32
+ * checks its arguments.
+ */
+#define VM_HIP_QMM_GROUP_MAX 4
+typedef struct vm_hip_qmm_member {
+    const int8_t* codes;
+    const float*  scales;
+    float*        c;
+    int64_t       n;
+} vm_hip_qmm_member;
+int vm_hip_qmm_group_f32(const float* a, int64_t rows_m, int64_t k, const vm_hip_qmm_member* members,
+                         int count, int quant_type, int block_size, void* stream);
 
 /*
  * vm_hip_qmm_f32 without any device allocation.  No counterpart in the

@@ -316,3 +316,111 @@ TEST_CASE("concurrent build and execute on per-thread HIP streams", "[gpu][threa
     for (auto& th : threads) th.join();
     REQUIRE(ok == 6);
 }
+
+TEST_CASE("sibling QuantizedMatMuls sharing A run as one grouped step", "[gpu][quantization][group]") {
+    // q | v read x with INT4 block-32 weights and no other input pending:
+    // one grouped step.  k's scales come from an Add that follows q in the
+    // order, so k is not ready at q's step and runs on its own; gate | up
+    // (INT8 per column) read x too but quantise differently: their own
+    // group.  Eight rows of A: no grouping at all.
+    REQUIRE_HIP();
+    const std::size_t k = 256, nq = 256, nkv = 64, ni = 192;
+    auto int4 = [&](std::size_t n, std::uint64_t seed) {
+        const auto w = normal(k * n, seed, 0.02f);
+        std::vector<std::int8_t> q((k / 2) * n);
+        std::vector<float> s((k / 32) * n);
+        vmo_quantize_int4_block(w.data(), reinterpret_cast<std::uint8_t*>(q.data()), s.data(), k, n, 32);
+        return std::pair{q, s};
+    };
+    auto int8 = [&](std::size_t n, std::uint64_t seed) {
+        const auto w = normal(k * n, seed, 0.02f);
+        std::vector<std::int8_t> q(k * n);
+        std::vector<float> s(n);
+        vmo_quantize_int8_per_channel(w.data(), q.data(), s.data(), k, n);
+        return std::pair{q, s};
+    };
+    const auto [wq, sq] = int4(nq, 1);
+    const auto [wk, sk] = int4(nkv, 2);
+    const auto [wv, sv] = int4(nkv, 3);
+    const auto [wg, sg] = int8(ni, 4);
+    const auto [wu, su] = int8(ni, 5);
+    const QuantizedMatMulAttrs a4{.quant_type = QuantType::Int4, .block_size = 32};
+    const QuantizedMatMulAttrs a8{.quant_type = QuantType::Int8, .block_size = 0};
+    const std::vector<float> zeros(sk.size(), 0.0f);
+
+    for (std::size_t m : {1, 4, 8}) {
+        const auto xv = normal(m * k, 10 + m);
+        auto run = [&](bool grouped, std::size_t* steps) {
+            ScopedEnv env("VELOMIND_GROUP_QMM", grouped ? "1" : "0");
+            Graph g;
+            auto x = g.input({(dim_t)m, (dim_t)k}, DataType::Float32);
+            auto in = [&](const auto& v, shape_t shape, DataType dt) {
+                auto t = g.input(shape, dt);
+                return std::pair{t, &v};
+            };
+            auto [tq, pq] = in(wq, {(dim_t)k / 2, (dim_t)nq}, DataType::Int8);
+            auto [tsq, psq] = in(sq, {(dim_t)k / 32, (dim_t)nq}, DataType::Float32);
+            auto [tk, pk] = in(wk, {(dim_t)k / 2, (dim_t)nkv}, DataType::Int8);
+            auto [tsk, psk] = in(sk, {(dim_t)k / 32, (dim_t)nkv}, DataType::Float32);
+            auto [tz, pz] = in(zeros, {(dim_t)k / 32, (dim_t)nkv}, DataType::Float32);
+            auto [tv, pv] = in(wv, {(dim_t)k / 2, (dim_t)nkv}, DataType::Int8);
+            auto [tsv, psv] = in(sv, {(dim_t)k / 32, (dim_t)nkv}, DataType::Float32);
+            auto [tg, pg] = in(wg, {(dim_t)k, (dim_t)ni}, DataType::Int8);
+            auto [tsg, psg] = in(sg, {(dim_t)ni}, DataType::Float32);
+            auto [tu, pu] = in(wu, {(dim_t)k, (dim_t)ni}, DataType::Int8);
+            auto [tsu, psu] = in(su, {(dim_t)ni}, DataType::Float32);
+            auto yq = g.op(OpDescriptor{Op::QuantizedMatMul, a4}, x, tq, tsq);
+            // tz holds zeros: tz + sk is sk exactly, produced by a node
+            // that follows q in the order
+            auto sk2 = g.op(Op::Add, tz, tsk);
+            auto yk = g.op(OpDescriptor{Op::QuantizedMatMul, a4}, x, tk, sk2);
+            auto yv = g.op(OpDescriptor{Op::QuantizedMatMul, a4}, x, tv, tsv);
+            auto yg = g.op(OpDescriptor{Op::QuantizedMatMul, a8}, x, tg, tsg);
+            auto yu = g.op(OpDescriptor{Op::QuantizedMatMul, a8}, x, tu, tsu);
+            g.mark_output(yq);
+            g.mark_output(yk);
+            g.mark_output(yv);
+            g.mark_output(yg);
+            g.mark_output(yu);
+            auto exec = g.build(DeviceType::HIP);
+            REQUIRE(exec->num_nodes() == 6);
+            *steps = exec->num_steps();
+            x.copy_from_host(as_bytes(xv));
+            tq.copy_from_host(as_bytes(*pq));
+            tsq.copy_from_host(as_bytes(*psq));
+            tk.copy_from_host(as_bytes(*pk));
+            tsk.copy_from_host(as_bytes(*psk));
+            tz.copy_from_host(as_bytes(*pz));
+            tv.copy_from_host(as_bytes(*pv));
+            tsv.copy_from_host(as_bytes(*psv));
+            tg.copy_from_host(as_bytes(*pg));
+            tsg.copy_from_host(as_bytes(*psg));
+            tu.copy_from_host(as_bytes(*pu));
+            tsu.copy_from_host(as_bytes(*psu));
+            exec->execute();
+            std::vector<std::vector<float>> out;
+            for (auto [t, n] : std::vector<std::pair<Tensor, std::size_t>>{{yq, nq}, {yk, nkv}, {yv, nkv}, {yg, ni}, {yu, ni}}) {
+                std::vector<float> o(m * n);
+                t.copy_to_host(as_writeable_bytes(o));
+                out.push_back(std::move(o));
+            }
+            return out;
+        };
+        std::size_t steps_grouped = 0, steps_single = 0;
+        const auto grouped = run(true, &steps_grouped);
+        const auto single = run(false, &steps_single);
+        REQUIRE(steps_single == 6);
+        // m <= 4: {q, v}, add, {gate, up}, k; m = 8: nothing grouped
+        REQUIRE(steps_grouped == (m <= 4 ? 4 : 6));
+        const std::vector<std::tuple<const std::vector<std::int8_t>*, const std::vector<float>*, std::size_t, int>>
+            mats{{&wq, &sq, nq, 2}, {&wk, &sk, nkv, 2}, {&wv, &sv, nkv, 2}, {&wg, &sg, ni, 1}, {&wu, &su, ni, 1}};
+        for (std::size_t i = 0; i < mats.size(); ++i) {
+            const auto& [w, s, n, qt] = mats[i];
+            std::vector<float> ref(m * n);
+            vmo_qmm_2d_f32(xv.data(), w->data(), s->data(), ref.data(), m, k, n, qt, qt == 2 ? 32 : 0);
+            const float bound = (m <= 4 ? 1e-5f : 1e-3f) * max_abs(ref);
+            REQUIRE(max_abs_diff(grouped[i], ref) <= bound);
+            REQUIRE(max_abs_diff(grouped[i], single[i]) <= 1e-6f * max_abs(single[i]));
+        }
+    }
+}

@@ -31,7 +31,8 @@ public:
         KernelFn kernel = nullptr;
         std::vector<pConstTensorStorage> inputs;
         std::vector<pTensorStorage> outputs;
-        std::shared_ptr<const void> attrs;  // the node's OpDescriptor
+        std::shared_ptr<const void> attrs;  // the node's OpDescriptor (fused > 1: the group's attrs)
+        std::size_t fused = 1;              // graph nodes this step runs (sibling QuantizedMatMuls)
     };
 
     // A storage the plan reads or writes, with the metadata it had at build
@@ -53,7 +54,8 @@ public:
         pConstGraph graph = nullptr;
         std::weak_ptr<void> graph_lifetime;
         DeviceType device = DeviceType::CPU;
-        std::vector<CompiledNode> topo;
+        std::vector<CompiledNode> topo;         // the steps, in order
+        std::size_t node_count = 0;              // graph nodes the steps run
         std::vector<WatchedStorage> watched;
         std::vector<IndexGuard> index_guards;   // ascending node order
         MemoryPlanStats plan_stats;
@@ -79,6 +81,9 @@ public:
     auto output(Tensor tensor) const -> pConstTensorStorage;
     auto memory_plan_stats() const noexcept -> const MemoryPlanStats&;
     auto num_nodes() const -> std::size_t;
+    // Kernel steps a run enqueues: num_nodes() less the nodes that run
+    // grouped with a sibling.
+    auto num_steps() const -> std::size_t;
     auto empty() const -> bool { return num_nodes() == 0; }
 
 private:

@@ -68,7 +68,56 @@ void quantized_matmul_hip_impl(const pConstTensorStorage* in, const pTensorStora
     }
 }
 
+// Sibling fp32 QuantizedMatMul nodes sharing A, compiled into one step by
+// the graph compiler: inputs [A, B_1, S_1, .., B_g, S_g], outputs
+// [C_1, .., C_g].  Each member is checked as a single node is; then one
+// vm_hip_qmm_group_f32 call (one GEMV launch for rows <= 4).
+void quantized_matmul_group_hip(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const auto& grp = *static_cast<const internal::QmmGroupAttrs*>(attrs);
+    const auto& qa = std::get<QuantizedMatMulAttrs>(grp.desc.attrs);
+    const auto* a = in[0];
+    if (!a || grp.members < 1 || grp.members > VM_HIP_QMM_GROUP_MAX)
+        throw std::runtime_error("quantized_matmul group hip: bad group");
+    if (!a->is_contiguous())
+        throw std::invalid_argument(error_context(Op::QuantizedMatMul, *out[0], "launch") +
+                                    ": strided operands are not supported on HIP");
+    const std::size_t rank = a->shape.size();
+    const std::int64_t k = a->shape[rank - 1];
+    std::int64_t rows = 1;
+    for (std::size_t i = 0; i + 1 < rank; ++i) rows *= a->shape[i];
+    const int qt = qa.quant_type == QuantType::Int4 ? VM_HIP_QUANT_INT4 : VM_HIP_QUANT_INT8;
+    const std::int64_t bs = (qt == VM_HIP_QUANT_INT4 && qa.block_size <= 0) ? 32 : qa.block_size;
+    const std::int64_t nblk = bs > 0 ? (k + bs - 1) / bs : 1;
+    vm_hip_qmm_member members[VM_HIP_QMM_GROUP_MAX];
+    for (std::size_t g = 0; g < grp.members; ++g) {
+        const auto* w = in[1 + 2 * g];
+        const auto* s = in[2 + 2 * g];
+        auto* c = out[g];
+        if (!w || !s || !c) throw std::runtime_error("quantized_matmul group hip: null storage");
+        if (!w->is_contiguous() || !s->is_contiguous() || !c->is_contiguous())
+            throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") +
+                                        ": strided operands are not supported on HIP");
+        const std::int64_t n = w->shape[1];
+        const std::uint64_t need_scales = static_cast<std::uint64_t>(k > 0 ? nblk : 0) * static_cast<std::uint64_t>(n);
+        if (storage_numel(*s) < need_scales)
+            throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") + ": scales hold " +
+                                        std::to_string(storage_numel(*s)) + " values, the kernel reads " +
+                                        std::to_string(need_scales));
+        members[g] = vm_hip_qmm_member{static_cast<const std::int8_t*>(w->data), static_cast<const float*>(s->data),
+                                       static_cast<float*>(c->data), n};
+    }
+    const int status = vm_hip_qmm_group_f32(static_cast<const float*>(a->data), rows, k, members,
+                                            static_cast<int>(grp.members), qt, qa.block_size, current_stream());
+    if (status != VM_HIP_OK) {
+        const std::string last = vm_hip_last_error();
+        const char* stage = last.find(" at sync") != std::string::npos ? "sync" : "launch";
+        throw_status(status, error_context(Op::QuantizedMatMul, *out[0], stage));
+    }
+}
+
 }  // namespace
+
+VELOMIND_REGISTER_QMM_GROUP(::velomind::DeviceType::HIP, quantized_matmul_group_hip)
 
 VELOMIND_REGISTER_QUANTIZED_MATMUL(::velomind::DeviceType::HIP, ::velomind::DataType::Float32,
                                    ::velomind::DataType::Float32, ::velomind::DataType::Float32,

@@ -98,6 +98,7 @@ void Executable::Impl::derive_run_plan() {
         const CompiledNode& cn = topo[i];
         for (pConstTensorStorage s : cn.inputs) watch(s);
         for (pConstTensorStorage s : cn.outputs) watch(s);
+        if (cn.fused > 1) continue;   // grouped QuantizedMatMuls: no index guard
         const auto& desc = *static_cast<const OpDescriptor*>(cn.attrs.get());
         if (desc.op == Op::Embedding && cn.inputs.size() >= 2)
             index_guards.push_back(IndexGuard{i, cn.inputs[1], cn.inputs[0]->shape.empty() ? 0 : cn.inputs[0]->shape[0]});
@@ -155,7 +156,9 @@ auto Executable::output(Tensor t) const -> pConstTensorStorage {
     return _impl->graph->tensor_storage_at(t.index());
 }
 
-auto Executable::num_nodes() const -> std::size_t { return _impl ? _impl->topo.size() : 0; }
+auto Executable::num_nodes() const -> std::size_t { return _impl ? _impl->node_count : 0; }
+
+auto Executable::num_steps() const -> std::size_t { return _impl ? _impl->topo.size() : 0; }
 
 auto Executable::memory_plan_stats() const noexcept -> const MemoryPlanStats& {
     static const MemoryPlanStats empty;

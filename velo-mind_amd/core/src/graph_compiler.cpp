@@ -92,6 +92,80 @@ std::size_t injected_failure_point() {
     return (end && *end == '\0') ? static_cast<std::size_t>(n) : 0;
 }
 
+// ---- steps -----------------------------------------------------------------
+// A compiled step runs one node, or (where the device registers a group
+// kernel) up to kMaxQmmGroup sibling QuantizedMatMul nodes that read the
+// same fp32 A with the same quantisation and have at most four rows of A:
+// decode projections such as q | k | v and gate | up then stream their
+// weights in one launch.  A sibling is pulled forward to the first
+// member's place only when every tensor it reads is already available
+// there; memory lifetimes are planned on the steps, so tensors the group
+// writes early never share arena space with anything still live.
+// VELOMIND_GROUP_QMM=0 keeps every node on its own.
+using Step = std::vector<pConstNode>;
+
+const QuantizedMatMulAttrs* qmm_attrs(pConstNode n) {
+    if (n->op().op != Op::QuantizedMatMul) return nullptr;
+    return std::get_if<QuantizedMatMulAttrs>(&n->op().attrs);
+}
+
+bool qmm_groupable(pConstNode n) {
+    const auto* qa = qmm_attrs(n);
+    if (!qa || qa->trans_b) return false;
+    const auto in = n->inputs();
+    const auto out = n->outputs();
+    if (in.size() != 3 || out.size() != 1) return false;
+    if (in[0]->dtype != DataType::Float32 || in[1]->dtype != DataType::Int8 || in[2]->dtype != DataType::Float32 ||
+        out[0]->dtype != DataType::Float32)
+        return false;
+    if (in[0]->shape.empty() || in[1]->shape.size() != 2) return false;
+    dim_t rows = 1;
+    for (std::size_t i = 0; i + 1 < in[0]->shape.size(); ++i) rows *= in[0]->shape[i];
+    return rows >= 1 && rows <= 4;
+}
+
+bool qmm_siblings(pConstNode a, pConstNode b) {
+    if (!qmm_groupable(b) || a->inputs()[0] != b->inputs()[0]) return false;
+    const auto* qa = qmm_attrs(a);
+    const auto* qb = qmm_attrs(b);
+    return qa->quant_type == qb->quant_type && qa->block_size == qb->block_size;
+}
+
+std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType device) {
+    const char* env = std::getenv("VELOMIND_GROUP_QMM");
+    const bool group = qmm_group_kernel(device) != nullptr && !(env && env[0] == '0');
+    std::unordered_map<pConstTensorStorage, std::size_t> producer;
+    for (std::size_t i = 0; i < order.size(); ++i)
+        for (auto* out : order[i]->outputs()) producer.emplace(out, i);
+    std::vector<bool> done(order.size(), false), taken(order.size(), false);
+    std::vector<Step> steps;
+    for (std::size_t i = 0; i < order.size(); ++i) {
+        if (taken[i]) continue;
+        std::vector<std::size_t> members{i};
+        taken[i] = true;
+        if (group && qmm_groupable(order[i])) {
+            for (std::size_t j = i + 1; j < order.size() && members.size() < kMaxQmmGroup; ++j) {
+                if (taken[j] || !qmm_siblings(order[i], order[j])) continue;
+                bool ready = true;
+                for (auto* in : order[j]->inputs()) {
+                    const auto it = producer.find(in);
+                    if (it != producer.end() && !done[it->second]) ready = false;
+                }
+                if (!ready) continue;
+                members.push_back(j);
+                taken[j] = true;
+            }
+        }
+        Step step;
+        for (std::size_t m : members) {
+            step.push_back(order[m]);
+            done[m] = true;
+        }
+        steps.push_back(std::move(step));
+    }
+    return steps;
+}
+
 std::shared_ptr<TensorStorage> allocate_checked(std::size_t bytes, DeviceType device) {
     auto s = TensorStorage::allocate(bytes, device);
     if (!s || s->device != device || s->size_bytes < bytes || (bytes > 0 && s->data == nullptr))
@@ -106,6 +180,7 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     if (graph._built) throw std::logic_error("Graph::build: graph is already built");
     graph.validate(device);
     const auto order = graph._topological_order();
+    const auto steps = plan_steps(order, device);
     const auto& tensors = graph._tensors;
 
     std::unordered_map<pConstTensorStorage, std::size_t> index_of;
@@ -115,20 +190,22 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     std::vector<bool> active(tensors.size(), false);
     std::vector<std::size_t> birth(tensors.size(), 0), death(tensors.size(), 0);
     std::vector<bool> born(tensors.size(), false);
-    for (std::size_t step = 0; step < order.size(); ++step) {
-        for (auto* in : order[step]->inputs()) {
-            const auto i = index_of.at(in);
-            active[i] = true;
-            death[i] = std::max(death[i], step);
-        }
-        for (auto* out : order[step]->outputs()) {
-            const auto i = index_of.at(out);
-            active[i] = true;
-            if (!born[i]) {
-                born[i] = true;
-                birth[i] = step;
+    for (std::size_t step = 0; step < steps.size(); ++step) {
+        for (const auto* node : steps[step]) {
+            for (auto* in : node->inputs()) {
+                const auto i = index_of.at(in);
+                active[i] = true;
+                death[i] = std::max(death[i], step);
             }
-            death[i] = std::max(death[i], step);
+            for (auto* out : node->outputs()) {
+                const auto i = index_of.at(out);
+                active[i] = true;
+                if (!born[i]) {
+                    born[i] = true;
+                    birth[i] = step;
+                }
+                death[i] = std::max(death[i], step);
+            }
         }
     }
     std::vector<bool> dedicated(tensors.size(), false);
@@ -230,8 +307,26 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     impl->device = device;
     impl->plan_stats = stats;
     if (auto create = get_device_context_hooks(device).create) impl->device_context = create();
-    impl->topo.reserve(order.size());
-    for (const auto* node : order) {
+    impl->node_count = order.size();
+    impl->topo.reserve(steps.size());
+    for (const auto& step : steps) {
+        if (step.size() > 1) {
+            // grouped QuantizedMatMul: [A, B_1, S_1, ..], [C_1, ..]
+            Executable::CompiledNode cn;
+            cn.inputs.push_back(remap.at(step.front()->inputs()[0]));
+            for (const auto* node : step) {
+                cn.inputs.push_back(remap.at(node->inputs()[1]));
+                cn.inputs.push_back(remap.at(node->inputs()[2]));
+                cn.outputs.push_back(remap.at(node->outputs()[0]));
+            }
+            cn.kernel = qmm_group_kernel(device);
+            auto* ga = new QmmGroupAttrs{step.front()->op(), step.size()};
+            cn.attrs = std::shared_ptr<const void>(ga, [](const void* p) { delete static_cast<const QmmGroupAttrs*>(p); });
+            cn.fused = step.size();
+            impl->topo.push_back(std::move(cn));
+            continue;
+        }
+        const auto* node = step.front();
         Executable::CompiledNode cn;
         std::vector<DataType> dtypes;
         for (auto* in : node->inputs()) {

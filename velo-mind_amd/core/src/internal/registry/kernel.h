@@ -40,6 +40,21 @@ auto resolve_op_kernel(Op op, std::span<const DataType> input_dtypes, DataType o
 
 auto register_op_kernel(DeviceType device, Op op, KernelDtypeKey key, Executable::KernelFn fn) -> void;
 
+// Grouped QuantizedMatMul: sibling fp32 QuantizedMatMul nodes that read the
+// same A (q | k | v, gate | up) run as one compiled step when the device
+// registers a group kernel.  Its inputs are [A, B_1, scales_1, B_2,
+// scales_2, ...], its outputs [C_1, C_2, ...], its attrs a QmmGroupAttrs.
+// No counterpart in the reference, which runs every node on its own.
+struct QmmGroupAttrs {
+    OpDescriptor desc;          // the members' common descriptor
+    std::size_t members = 0;    // 2 .. kMaxQmmGroup
+};
+inline constexpr std::size_t kMaxQmmGroup = 4;
+
+auto register_qmm_group_kernel(DeviceType device, Executable::KernelFn fn) -> void;
+// nullptr when the device has none (its QuantizedMatMul nodes run one by one)
+auto qmm_group_kernel(DeviceType device) -> Executable::KernelFn;
+
 template <DataType D> struct dtype_to_type;
 template <> struct dtype_to_type<DataType::Float32> { using type = float; };
 template <> struct dtype_to_type<DataType::Int32> { using type = std::int32_t; };
@@ -68,3 +83,10 @@ template <DataType D> using dtype_t = typename dtype_to_type<D>::type;
                                               3, (TC_DT)}),                                       \
         (&NAME<::velomind::internal::dtype_t<TA_DT>, ::velomind::internal::dtype_t<TSCALE_DT>,    \
                ::velomind::internal::dtype_t<TC_DT>>))
+
+// Registers FN as DEVICE's grouped QuantizedMatMul kernel.
+#define VELOMIND_REGISTER_QMM_GROUP(DEVICE, FN)                                                   \
+    [[maybe_unused]] static const bool VELOMIND_CONCAT_(_velomind_qg_, __LINE__) = [] {          \
+        ::velomind::internal::register_qmm_group_kernel((DEVICE), (FN));                         \
+        return true;                                                                             \
+    }();

@@ -48,6 +48,24 @@ auto resolve_op_kernel(Op op, std::span<const DataType> input_dtypes, DataType o
     return nullptr;
 }
 
+namespace {
+auto qmm_group_table() -> std::array<Executable::KernelFn, MAX_DEVICE_TYPES>& {
+    static std::array<Executable::KernelFn, MAX_DEVICE_TYPES> table{};
+    return table;
+}
+}  // namespace
+
+auto register_qmm_group_kernel(DeviceType device, Executable::KernelFn fn) -> void {
+    const auto idx = static_cast<std::size_t>(device);
+    if (idx >= MAX_DEVICE_TYPES) throw std::out_of_range("register_qmm_group_kernel: device index out of range");
+    qmm_group_table()[idx] = fn;
+}
+
+auto qmm_group_kernel(DeviceType device) -> Executable::KernelFn {
+    const auto idx = static_cast<std::size_t>(device);
+    return idx < MAX_DEVICE_TYPES ? qmm_group_table()[idx] : nullptr;
+}
+
 // ---- signatures and default attributes -----------------------------------
 
 auto signatures() -> std::array<OpSignatureFn, MAX_OPS>& {

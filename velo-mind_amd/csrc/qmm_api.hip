@@ -173,6 +173,43 @@ int vm_hip_qmm_f32(const float* a, const int8_t* wq, const float* scale, float* 
                         static_cast<hipStream_t>(stream));
 }
 
+int vm_hip_qmm_group_f32(const float* a, int64_t rows_m, int64_t k, const vm_hip_qmm_member* members, int count,
+                         int quant_type, int block_size, void* stream) {
+    clear_error();
+    if (!members || count < 1 || count > VM_HIP_QMM_GROUP_MAX)
+        return fail_inval("QuantizedMatMul group: 1 to VM_HIP_QMM_GROUP_MAX members");
+    for (int g = 0; g < count; ++g)
+        VM_TRY(validate_qmm(a, members[g].codes, members[g].scales, members[g].c, rows_m, k, members[g].n, quant_type,
+                            block_size));
+    VM_TRY(injected_failure("QuantizedMatMul", "launch"));
+    auto s = static_cast<hipStream_t>(stream);
+    const int bs = (quant_type == VM_HIP_QUANT_INT4 && block_size <= 0) ? 32 : block_size;
+    bool empty = rows_m == 0 || k == 0;
+    for (int g = 0; g < count; ++g) empty = empty || members[g].n == 0;
+    if (!empty && rows_m <= 4) {
+        const uint8_t* wq[VM_HIP_QMM_GROUP_MAX];
+        const float* sc[VM_HIP_QMM_GROUP_MAX];
+        float* c[VM_HIP_QMM_GROUP_MAX];
+        int n[VM_HIP_QMM_GROUP_MAX];
+        for (int g = 0; g < count; ++g) {
+            wq[g] = reinterpret_cast<const uint8_t*>(members[g].codes);
+            sc[g] = members[g].scales;
+            c[g] = members[g].c;
+            n[g] = static_cast<int>(members[g].n);
+        }
+        const int rc = gemv_qmm_group_f32(a, wq, sc, c, n, count, static_cast<int>(rows_m), static_cast<int>(k),
+                                          quant_type, bs, s);
+        if (rc != VM_HIP_EUNSUPPORTED) return rc;
+        clear_error();
+    }
+    // one launch per member (prefill rows, or a member the grouped GEMV
+    // does not cover)
+    for (int g = 0; g < count; ++g)
+        VM_TRY(qmm_f32_impl(a, members[g].codes, members[g].scales, members[g].c, rows_m, k, members[g].n, quant_type,
+                            block_size, s));
+    return 0;
+}
+
 int vm_hip_qmm(const void* a, int a_dtype, const int8_t* wq, const void* scale, int scale_dtype,
                void* c, int c_dtype, int64_t rows_m, int64_t k, int64_t n, int quant_type,
                int block_size, void* stream) {

@@ -89,6 +89,36 @@ __device__ __forceinline__ float swap_halves_add(float a, float b) {
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// The matrices one launch multiplies by the same activations (a group of
+// sibling projections such as q | k | v): their tiles are numbered one
+// after the other, member g owning tiles [tile_end[g-1], tile_end[g]), and
+// the split-K pair words index the members' columns side by side
+// (col_base[g] + column, n_total in all).  A single matrix is a group of
+// one.  Members are picked with selects on a workgroup-uniform index:
+// indexing the argument arrays would copy them to scratch memory.
+constexpr int kMaxMembers = 4;
+
+struct GemvMembers {
+    const uint8_t* wq[kMaxMembers];
+    const float* scale[kMaxMembers];
+    float* c[kMaxMembers];
+    int n[kMaxMembers];
+    int col_base[kMaxMembers];
+    int tile_end[kMaxMembers];
+    uint32_t code_bytes[kMaxMembers];
+    uint32_t scale_bytes[kMaxMembers];
+    int count;
+    int n_total;
+};
+
+template <class T>
+__device__ __forceinline__ T pick(const T (&v)[kMaxMembers], int g) {
+    T r = v[0];
+#pragma unroll
+    for (int i = 1; i < kMaxMembers; ++i) r = g == i ? v[i] : r;
+    return r;
+}
+
 // Codes and scales of one chunk for one lane.
 template <int KIND>
 struct Chunk {
@@ -98,12 +128,14 @@ struct Chunk {
 
 // KIND: 0 = INT8 per-column scale, 1 = INT8 blockwise, 2 = INT4 blockwise.
 // MR: activation rows (1, 2 or 4); L: lanes per row segment; W: waves.
-template <int KIND, int MR, int L, int W>
+// GROUPED: several members (one launch for sibling projections); a single
+// matrix runs the GROUPED = false copy, which reads member 0's fields only
+// (each argument it reads is a scalar load on the path to the first code
+// load: the member table costs ~0.6 us per launch when it is searched).
+template <int KIND, int MR, int L, int W, bool GROUPED>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
-    const float* __restrict__ a, const uint8_t* __restrict__ wq, const float* __restrict__ scale,
-    float* __restrict__ c, int m, int k, int n, int block_size, int chunks_per_split,
-    uint32_t code_bytes, uint32_t scale_bytes, uint32_t a_bytes, int a_vec, int blk_shift,
-    unsigned long long* __restrict__ pairs) {
+    const float* __restrict__ a, const GemvMembers mb, int m, int k, int block_size, int chunks_per_split,
+    uint32_t a_bytes, int a_vec, int blk_shift, unsigned long long* __restrict__ pairs) {
     using CS = ChunkShape<KIND>;
     constexpr int G = 64 / L;            // row groups per wave
     constexpr int RG = W * G;            // row groups per workgroup
@@ -127,6 +159,24 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         const int full = static_cast<int>(gridDim.x) & ~7;
         if (tile < full) tile = (tile & 7) * (full >> 3) + (tile >> 3);
     }
+    // the member this tile belongs to, and the tile within it
+    int member = 0;
+    if constexpr (GROUPED) {
+#pragma unroll
+        for (int g = 1; g < kMaxMembers; ++g) member += (g < mb.count && tile >= mb.tile_end[g - 1]) ? 1 : 0;
+        int first = 0;
+#pragma unroll
+        for (int g = 1; g < kMaxMembers; ++g) first = member == g ? mb.tile_end[g - 1] : first;
+        tile -= first;
+    }
+    const uint8_t* __restrict__ wq = pick(mb.wq, member);
+    const float* __restrict__ scale = pick(mb.scale, member);
+    float* __restrict__ c = pick(mb.c, member);
+    const int n = pick(mb.n, member);
+    const int col_base = pick(mb.col_base, member);
+    const uint32_t code_bytes = pick(mb.code_bytes, member);
+    const uint32_t scale_bytes = pick(mb.scale_bytes, member);
+    const int n_total = GROUPED ? mb.n_total : n;
     const int split = blockIdx.y;
     const int splits = gridDim.y;
     const int col0 = tile * kTileCols + (lane % L) * kVec;
@@ -394,7 +444,8 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
             // A lower half whose upper partner lies past the last split
             // moves up alone.
             if (half == 1 || ((2 * node + 1) << lvl) < splits) {
-                unsigned long long* word = pairs + level_base + (static_cast<int64_t>(node) * MR + i) * n + col;
+                unsigned long long* word =
+                    pairs + level_base + (static_cast<int64_t>(node) * MR + i) * n_total + col_base + col;
                 const unsigned enc = __float_as_uint(v + 0.0f) ^ 0x80000000u;
                 const unsigned long long mine = half ? static_cast<unsigned long long>(enc) << 32 : enc;
                 const unsigned long long old =
@@ -408,7 +459,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
                 const float po = __uint_as_float(other ^ 0x80000000u);
                 v = half ? po + v : v + po;
             }
-            level_base += static_cast<int64_t>((splits + (2 << lvl) - 1) >> (lvl + 1)) * MR * n;
+            level_base += static_cast<int64_t>((splits + (2 << lvl) - 1) >> (lvl + 1)) * MR * n_total;
         }
         if (!last) continue;
         if constexpr (KIND == 0) v *= scale[col];
@@ -581,20 +632,42 @@ GemvConfig choose_config(int kind, int m, int k, int n) {
     return cfg;
 }
 
+// One matrix of a group, as the launchers take it.
+struct Member {
+    const uint8_t* wq;
+    const float* scale;
+    float* c;
+    int n;
+};
+
 template <int KIND, int MR, int L, int W>
-int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
-               int block_size, const GemvConfig& cfg, hipStream_t stream) {
-    const int tiles = (n + kVec * L - 1) / (kVec * L);
+int launch_cfg(const float* a, const Member* members, int count, int m, int k, int block_size,
+               const GemvConfig& cfg, hipStream_t stream) {
+    const int64_t byte_rows = KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : k;
+    const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
+    GemvMembers mb{};
+    int tiles = 0, n_total = 0;
+    for (int g = 0; g < count; ++g) {
+        const int n = members[g].n;
+        mb.wq[g] = members[g].wq;
+        mb.scale[g] = members[g].scale;
+        mb.c[g] = members[g].c;
+        mb.n[g] = n;
+        mb.col_base[g] = n_total;
+        tiles += (n + kVec * L - 1) / (kVec * L);
+        mb.tile_end[g] = tiles;
+        mb.code_bytes[g] = static_cast<uint32_t>(byte_rows * n);
+        mb.scale_bytes[g] = static_cast<uint32_t>(KIND == 0 ? 0 : nblk * n * 4);
+        n_total += n;
+    }
+    mb.count = count;
+    mb.n_total = n_total;
     Workspace ws{};
     if (cfg.splits > 1)  // two 32-bit counter slots per pair word
-        VM_TRY(get_workspace(stream, 0, 2 * tree_words(cfg.splits, MR, n), &ws));
+        VM_TRY(get_workspace(stream, 0, 2 * tree_words(cfg.splits, MR, n_total), &ws));
     unsigned long long* pairs = reinterpret_cast<unsigned long long*>(ws.counters);
     const std::size_t lds = (static_cast<std::size_t>(MR) * cfg.chunks_per_split * kChunkK +
                              static_cast<std::size_t>(W) * MR * kVec * L + 4) * sizeof(float);
-    const int64_t byte_rows = KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : k;
-    const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
-    const uint32_t code_bytes = static_cast<uint32_t>(byte_rows * n);
-    const uint32_t scale_bytes = static_cast<uint32_t>(KIND == 0 ? 0 : nblk * n * 4);
     const uint32_t a_bytes = static_cast<uint32_t>(static_cast<int64_t>(m) * k * 4);
     const int a_vec = (k % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0) ? 1 : 0;
     // Chunk -> scale block is a shift when block_size / 8 is a power of two.
@@ -603,20 +676,23 @@ int launch_cfg(const float* a, const uint8_t* wq, const float* scale, float* c, 
         const int cpb = block_size / kChunkK;
         if ((cpb & (cpb - 1)) == 0) blk_shift = __builtin_ctz(static_cast<unsigned>(cpb));
     }
-    hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
-                       stream, a, wq, scale, c, m, k, n, block_size, cfg.chunks_per_split, code_bytes,
-                       scale_bytes, a_bytes, a_vec, blk_shift, pairs);
+    if (count == 1)
+        hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, false>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
+                           stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs);
+    else
+        hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, true>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
+                           stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs);
     return check_launch("QuantizedMatMul", stream);
 }
 
 template <int KIND, int MR>
-int launch_mr(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
-              int block_size, hipStream_t stream) {
-    const GemvConfig cfg = choose_config(KIND, m, k, n);
+int launch_mr(const float* a, const Member* members, int count, int m, int k, int n_total, int block_size,
+              hipStream_t stream) {
+    const GemvConfig cfg = choose_config(KIND, m, k, n_total);
 #define VM_GEMV_CASE(LL, WW)                                                                    \
     if constexpr (WW <= max_waves(KIND, MR))                                                    \
         if (cfg.L == LL && cfg.W == WW)                                                         \
-            return launch_cfg<KIND, MR, LL, WW>(a, wq, scale, c, m, k, n, block_size, cfg, stream);
+            return launch_cfg<KIND, MR, LL, WW>(a, members, count, m, k, block_size, cfg, stream);
     VM_GEMV_CASE(1, 4)
     VM_GEMV_CASE(2, 4)
     VM_GEMV_CASE(2, 8)
@@ -632,33 +708,56 @@ int launch_mr(const float* a, const uint8_t* wq, const float* scale, float* c, i
 }
 
 template <int KIND>
-int launch_kind(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
-                int block_size, hipStream_t stream) {
-    if (m == 1) return launch_mr<KIND, 1>(a, wq, scale, c, m, k, n, block_size, stream);
-    if (m == 2) return launch_mr<KIND, 2>(a, wq, scale, c, m, k, n, block_size, stream);
-    return launch_mr<KIND, 4>(a, wq, scale, c, m, k, n, block_size, stream);
+int launch_kind(const float* a, const Member* members, int count, int m, int k, int n_total, int block_size,
+                hipStream_t stream) {
+    if (m == 1) return launch_mr<KIND, 1>(a, members, count, m, k, n_total, block_size, stream);
+    if (m == 2) return launch_mr<KIND, 2>(a, members, count, m, k, n_total, block_size, stream);
+    return launch_mr<KIND, 4>(a, members, count, m, k, n_total, block_size, stream);
+}
+
+// One launch for `count` matrices sharing the activations; VM_HIP_EUNSUPPORTED
+// when any member needs another kernel.
+int gemv_group_f32(const float* a, const Member* members, int count, int m, int k, int quant_type,
+                   int block_size, hipStream_t stream) {
+    if (m < 1 || m > 4 || count < 1 || count > kMaxMembers) return VM_HIP_EUNSUPPORTED;
+    int64_t n_total = 0;
+    for (int g = 0; g < count; ++g) {
+        const Member& mm = members[g];
+        // Buffer offsets are 32-bit: codes and scales must stay below 2 GiB.
+        if (mm.n < 1 || static_cast<int64_t>(k) * mm.n >= (int64_t(1) << 31)) return VM_HIP_EUNSUPPORTED;
+        // 16-byte code loads need 16-byte aligned rows; scales are read as float4.
+        if (mm.n % kVec != 0 || reinterpret_cast<uintptr_t>(mm.wq) % 16 != 0 ||
+            reinterpret_cast<uintptr_t>(mm.scale) % 16 != 0)
+            return VM_HIP_EUNSUPPORTED;
+        n_total += mm.n;
+    }
+    if (n_total >= (int64_t(1) << 30)) return VM_HIP_EUNSUPPORTED;
+    const int nt = static_cast<int>(n_total);
+    if (quant_type == VM_HIP_QUANT_INT4) {
+        if (block_size <= 0 || block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
+        return launch_kind<2>(a, members, count, m, k, nt, block_size, stream);
+    }
+    if (block_size > 0) {
+        if (block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
+        return launch_kind<1>(a, members, count, m, k, nt, block_size, stream);
+    }
+    return launch_kind<0>(a, members, count, m, k, nt, 0, stream);
 }
 
 }  // namespace
 
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                  int n, int quant_type, int block_size, hipStream_t stream) {
-    if (m < 1 || m > 4) return VM_HIP_EUNSUPPORTED;
-    // Buffer offsets are 32-bit: codes and scales must stay below 2 GiB.
-    if (static_cast<int64_t>(k) * n >= (int64_t(1) << 31)) return VM_HIP_EUNSUPPORTED;
-    // 16-byte code loads need 16-byte aligned rows; scales are read as float4.
-    if (n % kVec != 0 || reinterpret_cast<uintptr_t>(wq) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(scale) % 16 != 0)
-        return VM_HIP_EUNSUPPORTED;
-    if (quant_type == VM_HIP_QUANT_INT4) {
-        if (block_size <= 0 || block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
-        return launch_kind<2>(a, wq, scale, c, m, k, n, block_size, stream);
-    }
-    if (block_size > 0) {
-        if (block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
-        return launch_kind<1>(a, wq, scale, c, m, k, n, block_size, stream);
-    }
-    return launch_kind<0>(a, wq, scale, c, m, k, n, 0, stream);
+    const Member one{wq, scale, c, n};
+    return gemv_group_f32(a, &one, 1, m, k, quant_type, block_size, stream);
+}
+
+int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* const* scale, float* const* c,
+                       const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream) {
+    if (count < 1 || count > kMaxMembers) return VM_HIP_EUNSUPPORTED;
+    Member members[kMaxMembers];
+    for (int g = 0; g < count; ++g) members[g] = Member{wq[g], scale[g], c[g], n[g]};
+    return gemv_group_f32(a, members, count, m, k, quant_type, block_size, stream);
 }
 
 }  // namespace vmhip

@@ -12,6 +12,12 @@ namespace vmhip {
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                  int n, int quant_type, int block_size, hipStream_t stream);
 
+// The same GEMV for `count` (<= 4) matrices sharing the activations, in one
+// launch (qmm_gemv.hip); VM_HIP_EUNSUPPORTED when a member needs another
+// kernel.
+int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* const* scale, float* const* c,
+                       const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream);
+
 // Prefill-shaped MFMA GEMM for m > 4 rows (qmm_gemm.hip).
 int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                  int n, int quant_type, int block_size, hipStream_t stream);

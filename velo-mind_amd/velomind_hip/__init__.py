@@ -44,6 +44,11 @@ class Prefetch(ctypes.Structure):
     _fields_ = [("ptr", c_void_p * 4), ("bytes", ctypes.c_uint64 * 4), ("count", c_int)]
 
 
+class QmmMember(ctypes.Structure):
+    """vm_hip_qmm_member (include/vm_hip.h)."""
+    _fields_ = [("codes", c_void_p), ("scales", c_void_p), ("c", c_void_p), ("n", c_int64)]
+
+
 def _declare(L: ctypes.CDLL) -> None:
     p = c_void_p
     sig = {
@@ -72,6 +77,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_graph_destroy": ([p], c_int),
         "vm_hip_qmm_f32": ([p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_qmm_f32_noalloc": ([p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
+        "vm_hip_qmm_group_f32": ([p, c_int64, c_int64, POINTER(QmmMember), c_int, c_int, c_int, p], c_int),
         "vm_hip_qmm": ([p, c_int, p, p, c_int, p, c_int, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_pack_int8": ([p, p, p, c_int64, c_int64, p], c_int),
         "vm_hip_pack_int4": ([p, p, p, c_int64, c_int64, c_int64, p], c_int),
@@ -129,7 +135,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_stream_destroy", "vm_hip_stream_synchronize", "vm_hip_event_create",
             "vm_hip_event_destroy", "vm_hip_event_record", "vm_hip_event_synchronize",
             "vm_hip_event_elapsed_ms", "vm_hip_stream_begin_capture", "vm_hip_stream_end_capture",
-            "vm_hip_graph_launch", "vm_hip_graph_destroy", "vm_hip_qmm_f32", "vm_hip_qmm_f32_noalloc", "vm_hip_qmm",
+            "vm_hip_graph_launch", "vm_hip_graph_destroy", "vm_hip_qmm_f32", "vm_hip_qmm_f32_noalloc", "vm_hip_qmm_group_f32", "vm_hip_qmm",
             "vm_hip_pack_int8",
             "vm_hip_pack_int4", "vm_hip_dequant_int8", "vm_hip_dequant_int4", "vm_hip_half_to_f32",
             "vm_hip_embedding_f32", "vm_hip_rmsnorm_f32", "vm_hip_rope_f32", "vm_hip_transpose_f32",
@@ -302,6 +308,12 @@ def qmm_f32(a: int, wq: int, scale: int, c: int, m: int, k: int, n: int, quant_t
             block_size: int, stream=None) -> None:
     """vm_hip_qmm_f32 on raw device addresses."""
     check(open_library().vm_hip_qmm_f32(a, wq, scale, c, m, k, n, quant_type, block_size, _h(stream)))
+
+
+def qmm_group_f32(a: int, m: int, k: int, members, quant_type: int, block_size: int, stream=None) -> None:
+    """vm_hip_qmm_group_f32: members = [(codes, scales, c, n), ...] device addresses."""
+    arr = (QmmMember * len(members))(*[QmmMember(w, s, c, n) for w, s, c, n in members])
+    check(open_library().vm_hip_qmm_group_f32(a, m, k, arr, len(members), quant_type, block_size, _h(stream)))
 
 
 def qmm_f32_noalloc(a: int, wq: int, scale: int, c: int, m: int, k: int, n: int, quant_type: int,
