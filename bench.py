@@ -405,6 +405,85 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph
     return out
 
 
+def decode_trace_report(tokens: int = 8) -> dict:
+    """Phase timing of the one-launch decode step (TinyLlama-1.1B INT4,
+    512-token prompt) from a library built with VELOMIND_DECODE_TRACE=1:
+    the timestamps of the last step's phases (decode_persistent.hip lists
+    the events), as medians over workgroups and layers, and the chain of
+    one middle layer relative to the moment the previous layer's last
+    down-projection slice was stored."""
+    import ctypes
+
+    import velomind_hip as H
+    from velomind_hip import llama as VL
+
+    spec = E2E_MODELS["tinyllama_1.1b_int4"]
+
+    class Cfg:
+        pass
+
+    cfg = Cfg()
+    for k, v in spec["cfg"].items():
+        setattr(cfg, k, v)
+    lib = H.open_library()
+    probe = np.zeros(1, np.uint64)
+    if lib.vm_hip_decode_trace_read(probe.ctypes.data, 0) != 0:
+        raise RuntimeError("--decode-trace needs libvmhip built with VELOMIND_DECODE_TRACE=1")
+    w = VL.Weights(cfg)
+    w.fill_synthetic(20240601, 0.02)
+    prev = os.environ.get("VELOMIND_DECODE_PERSISTENT")
+    os.environ["VELOMIND_DECODE_PERSISTENT"] = "1"
+    try:
+        sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"], max_seq=spec["prompt"] + tokens + 1)
+    finally:
+        if prev is None:
+            del os.environ["VELOMIND_DECODE_PERSISTENT"]
+        else:
+            os.environ["VELOMIND_DECODE_PERSISTENT"] = prev
+    if DECODE_PATHS[sess.decode_path()] != "persistent":
+        raise RuntimeError("the persistent decode step does not cover TinyLlama here")
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, spec["prompt"]).astype(np.int32)
+    _, (_, dec_s, nd) = sess.generate(prompt, tokens)
+    wgs, slots, events = 512, 34, 24
+    buf = np.zeros(wgs * slots * events, np.uint64)
+    H.check(lib.vm_hip_decode_trace_read(buf.ctypes.data, buf.nbytes))
+    sess.close()
+    w.close()
+    t = buf.reshape(wgs, slots, events).astype(np.int64)
+    L = cfg.num_layers
+    live = t[:, 0, 0] > 0
+    us = (t[live] - t[live, 0, 0].min()) / 100.0   # 100 MHz wall clock
+    phases = [("qkv_stage", 0, 1), ("qkv_compute", 1, 2), ("qkv_store", 2, 3), ("attention", 4, 5),
+              ("o_stage", 5, 6), ("o_compute", 6, 7), ("o_store", 7, 8), ("gate_up_stage", 8, 9),
+              ("gate_up_compute", 9, 10), ("gate_up_store", 10, 11), ("down_stage", 11, 12),
+              ("down_compute", 12, 13), ("down_store", 13, 14)]
+    per_phase = {n: round(float(np.median(np.median(us[:, :L, b] - us[:, :L, a], axis=0))), 2) for n, a, b in phases}
+    layer_us = np.median(us[:, 1:L, 0] - us[:, 0:L - 1, 0], axis=0)
+    mid = L // 2
+    z = us[:, mid - 1, 14].max()
+    u = us[:, mid, :] - z
+    att = u[:, 18] > -z   # workgroups that ran an attention item
+    red = np.arange(us.shape[0] - 40, us.shape[0])
+    chain = {"qkv_staged_median": float(np.median(u[:, 1])), "qkv_stored_max": float(u[:, 3].max()),
+             "reduce_done_median": float(np.median(u[red, 16])),
+             "attention_inputs_in_median": float(np.median(u[att, 17])),
+             "attention_records_out_median": float(np.median(u[att, 18])),
+             "o_staged_median": float(np.median(u[:, 6])), "o_stored_max": float(u[:, 8].max()),
+             "gate_up_staged_median": float(np.median(u[:, 9])), "gate_up_stored_max": float(u[:, 11].max()),
+             "down_staged_median": float(np.median(u[:, 12])), "down_stored_max": float(u[:, 14].max())}
+    gu = us[:, mid, 10] - us[:, mid, 9]
+    half = us.shape[0] // 2
+    return {"model": "tinyllama_1.1b_int4", "prompt": spec["prompt"], "tokens": tokens,
+            "decode_us_per_token": round(dec_s / nd * 1e6, 1), "workgroups": int(us.shape[0]),
+            "layer_us_median": round(float(np.median(layer_us)), 2),
+            "phase_us_median": per_phase,
+            "layer_chain_us": {k: round(v, 2) for k, v in chain.items()},
+            "gate_up_compute_us_by_workgroup_half": [round(float(np.median(gu[:half])), 2),
+                                                     round(float(np.median(gu[half:])), 2)],
+            "lm_head_us": round(float(np.median(us[:, L, 2] - us[:, L, 0])), 2),
+            "argmax_us": round(float(us[0, L, 4] - np.median(us[:, L, 2])), 2)}
+
+
 GEMM_K, GEMM_N = 2048, 5632
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -616,6 +695,9 @@ def main() -> int:
                          "the decode steps launch eagerly so that rocprofv3 can trace them)")
     ap.add_argument("--decode-persistent", action="store_true",
                     help="with --e2e-only: decode with the one-launch step (vm_hip_decode_step)")
+    ap.add_argument("--decode-trace", action="store_true",
+                    help="only the one-launch decode step's phase timestamps (library built with "
+                         "VELOMIND_DECODE_TRACE=1), printed as one JSON line")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg (config 3)")
     ap.add_argument("--no-large", action="store_true", help="skip the 70B-class decode GEMV leg")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg, printed as one JSON line")
@@ -652,6 +734,9 @@ def main() -> int:
             H.qmm_f32(a.addr, pa, sa, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
         stream.synchronize()
         log(f"bench: {reps} GEMM launches M={m} quant_type={qt} done, walking {rot.copies} weight copies")
+        return 0
+    if args.decode_trace:
+        print(json.dumps({"metric": METRIC, "decode_trace": decode_trace_report()}), flush=True)
         return 0
     if args.gemm_only:
         print(json.dumps({"metric": METRIC, "gemm": gemm_bench(H, stream)}), flush=True)

@@ -578,6 +578,11 @@ int vm_hip_decode_step(const vm_hip_decode_model* model, void* workspace, int64_
 /* Nonzero when a step since the last call timed out waiting for another
  * workgroup (results of that step are invalid); clears the flag. */
 int vm_hip_decode_status(void* workspace, int* failed, void* stream);
+/* Phase timestamps of the last steps (u64, 100 MHz wall clock, laid out
+ * [512 workgroups][34 slots][24 events]; see decode_persistent.hip), for
+ * profiling: only in a library built with VELOMIND_DECODE_TRACE=1, which
+ * compiles them in; VM_HIP_EUNSUPPORTED otherwise. */
+int vm_hip_decode_trace_read(void* host, int64_t bytes);
 
 #ifdef __cplusplus
 }

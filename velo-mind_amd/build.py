@@ -36,6 +36,9 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-result",
     f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}",
 ]
+# Phase timestamps in the one-launch decode step (profiling builds only).
+if os.environ.get("VELOMIND_DECODE_TRACE") == "1":
+    HIP_FLAGS.append("-DVM_DECODE_TRACE")
 CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-Wextra",
              f"-I{os.path.join(CORE, 'include')}", f"-I{os.path.join(CORE, 'src')}",
              f"-I{os.path.join(ROOT, 'include')}"]

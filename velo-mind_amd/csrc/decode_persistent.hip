@@ -68,6 +68,35 @@ namespace {
 
 typedef unsigned long long u64;
 
+// Phase timestamps, compiled in only with -DVM_DECODE_TRACE (build.py:
+// VELOMIND_DECODE_TRACE=1): thread 0 of each of the first kTraceWgs
+// workgroups stores the 100 MHz wall clock at the phase boundaries of every
+// layer (slot `layer`, event `ev`; the lm_head and argmax use slot
+// `layers`), read back with vm_hip_decode_trace_read.  Events per layer:
+//   0 QKV stage begins      1 staged       2 computed     3 stored
+//  15 reduce begins        16 reduce done (the last 40 workgroups)
+//   4 attention begins     17 first item's inputs in   18 its records out
+//   5 attention done        6 O staged     7 computed     8 stored
+//   9 gate|up staged       10 computed    11 stored
+//  12 down staged          13 computed    14 stored
+// and in slot `layers`: 0 final norm begins, 1 staged, 2 lm_head done,
+// 3 local argmax done, 4 workgroup 0's reduction done.
+constexpr int kTraceWgs = 512;
+constexpr int kTraceSlots = 34;
+constexpr int kTraceEvents = 24;
+#ifdef VM_DECODE_TRACE
+__device__ u64 g_decode_trace[kTraceWgs * kTraceSlots * kTraceEvents];
+#define VM_TRACE(slot, ev)                                                                         \
+    do {                                                                                           \
+        if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && (slot) < kTraceSlots)                    \
+            g_decode_trace[(blockIdx.x * kTraceSlots + (slot)) * kTraceEvents + (ev)] = wall_clock64(); \
+    } while (0)
+#else
+#define VM_TRACE(slot, ev) \
+    do {                   \
+    } while (0)
+#endif
+
 constexpr int kT = 256;          // threads per workgroup
 constexpr int kWaves = 4;
 constexpr int kTile = 256;       // columns per GEMV tile (16 lanes x 16 columns)
@@ -962,6 +991,7 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
     for (int layer = 0; layer < L; ++layer) {
         const vm_hip_decode_layer& ly = a.m.layer[layer];
         // ---- QKV: residual + RMSNorm staged, weights in wa
+        VM_TRACE(layer, 0);
         {
             const GemvView v = view_of(layer, kPhQkv);
             GemvSmem& sm = smem.g;
@@ -972,28 +1002,36 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
                 stage_normres(a, a.pq, kpr, hidden, w, sm, poll, nullptr, a.ha, tag_of(a, layer - 1, kPhGu), a.dn_sl,
                               a.pd.splits, tag_of(a, layer - 1, kPhDown), ly.attn_norm, a.hb, a.ss_attn,
                               tag_of(a, layer, kPhQkv));
+            VM_TRACE(layer, 1);
             if (w < att_items) att_prefetch(a, layer, w, nc, kv);
             zero_red(sm);
             __syncthreads();
             K::compute(v, a.pq, w, 0, wa, sm);
             __syncthreads();
+            VM_TRACE(layer, 2);
             gemv_store(a.pq, a.qkv_n, w, 0, sm, a.qkv_sl, tag_of(a, layer, kPhQkv));
             __syncthreads();
+            VM_TRACE(layer, 3);
         }
+        VM_TRACE(layer, 15);
         // ---- QKV reduction (one head per workgroup, counted from the
         // last workgroup so that they differ from the attention items')
         {
             const int head = G - 1 - w;
             if (head < a.qkv_n / kD) qkv_reduce(a, layer, head, p, smem.g, poll, scr.ss);
         }
+        VM_TRACE(layer, 16);
         // ---- attention: K/V chunk prefetched; O weights issued into wb
         // after the first item's records
+        VM_TRACE(layer, 4);
         {
             bool issued = false;
             for (int item = w; item < att_items; item += G) {
                 if (item != w) att_prefetch(a, layer, item, nc, kv);
                 att_load(a, layer, item, nc, p, kv, smem.a, poll);
+                if (item == w) VM_TRACE(layer, 17);
                 att_compute(a, layer, item, nc, p, smem.a);
+                if (item == w) VM_TRACE(layer, 18);
                 if (!issued) {
                     K::issue(view_of(layer, kPhO), a.po, w, 0, wb);
                     issued = true;
@@ -1001,17 +1039,21 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
             }
             if (!issued) K::issue(view_of(layer, kPhO), a.po, w, 0, wb);
         }
+        VM_TRACE(layer, 5);
         // ---- O: attention records merged while staging, weights in wb;
         // gate|up weights into wa after the stores
         {
             GemvSmem& sm = smem.g;
             stage_attn(a, a.po, kpr, w, nc, sm, poll, tag_of(a, layer, kPhAtt));
+            VM_TRACE(layer, 6);
             zero_red(sm);
             __syncthreads();
             K::compute(view_of(layer, kPhO), a.po, w, 0, wb, sm);
             __syncthreads();
+            VM_TRACE(layer, 7);
             gemv_store(a.po, hidden, w, 0, sm, a.o_sl, tag_of(a, layer, kPhO));
             __syncthreads();
+            VM_TRACE(layer, 8);
             K::issue(view_of(layer, kPhGu), a.pg, w, 0, wa);
         }
         // ---- gate|up: residual + RMSNorm staged, weights in wa; down
@@ -1020,12 +1062,15 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
             GemvSmem& sm = smem.g;
             stage_normres(a, a.pg, kpr, hidden, w, sm, poll, nullptr, a.hb, tag_of(a, layer, kPhQkv), a.o_sl,
                           a.po.splits, tag_of(a, layer, kPhO), ly.ffn_norm, a.ha, a.ss_ffn, tag_of(a, layer, kPhGu));
+            VM_TRACE(layer, 9);
             zero_red(sm);
             __syncthreads();
             K::compute(view_of(layer, kPhGu), a.pg, w, 0, wa, sm);
             __syncthreads();
+            VM_TRACE(layer, 10);
             gemv_store(a.pg, 2 * inter, w, 0, sm, a.gu_sl, tag_of(a, layer, kPhGu));
             __syncthreads();
+            VM_TRACE(layer, 11);
             K::issue(view_of(layer, kPhDown), a.pd, w, 0, wb);
         }
         // ---- down: SwiGLU staged, weights in wb; the next QKV (or
@@ -1034,12 +1079,15 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
             GemvSmem& sm = smem.g;
             stage_swiglu(a, a.pd, kpr, w, sm, poll, a.gu_sl, a.pg.splits, a.ss_ffn, a.pg.splits,
                          tag_of(a, layer, kPhGu), scr.ss);
+            VM_TRACE(layer, 12);
             zero_red(sm);
             __syncthreads();
             K::compute(view_of(layer, kPhDown), a.pd, w, 0, wb, sm);
             __syncthreads();
+            VM_TRACE(layer, 13);
             gemv_store(a.pd, hidden, w, 0, sm, a.dn_sl, tag_of(a, layer, kPhDown));
             __syncthreads();
+            VM_TRACE(layer, 14);
             if (layer + 1 < L)
                 K::issue(view_of(layer + 1, kPhQkv), a.pq, w, 0, wa);
             else
@@ -1049,12 +1097,14 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
 
     // ---- lm_head: final norm staged; rounds of kMaxItems items, weights
     // alternating wa / wb
+    VM_TRACE(L, 0);
     {
         GemvSmem& sm = smem.g;
         const uint32_t ltag = tag_of(a, L, kPhLm);
         stage_normres(a, a.pl, kpr, hidden, w, sm, poll, nullptr, a.ha, tag_of(a, L - 1, kPhGu), a.dn_sl, a.pd.splits,
                       tag_of(a, L - 1, kPhDown), a.m.final_norm, nullptr, a.ss_fin, ltag);
         const int V = static_cast<int>(a.m.vocab);
+        VM_TRACE(L, 1);
         for (int r0 = 0; r0 < a.pl.items; r0 += 2 * kMaxItems) {
             if (r0 + kMaxItems < a.pl.items) K::issue(lm_view, a.pl, w, r0 + kMaxItems, wb);
             zero_red(sm);
@@ -1074,6 +1124,7 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
         }
     }
 
+    VM_TRACE(L, 2);
     // ---- logits of this workgroup's vocabulary range (four per float4
     // group, the lm_head slices divided among parts), its argmax candidate
     {
@@ -1118,6 +1169,7 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
         }
         __syncthreads();
         ArgSmem& sm = smem.r;
+        VM_TRACE(L, 3);
         block_argmax(bv, bi, sm);
         if (threadIdx.x == 0) {
             put1(a.cand + 2 * w, bv, ctag);
@@ -1145,6 +1197,7 @@ __global__ __launch_bounds__(kT, 2) void decode_step_kernel(DecodeArgs a) {
                 }
             }
             block_argmax(cv, ci, sm);
+            VM_TRACE(L, 4);
             if (threadIdx.x == 0) {
                 a.m.token[0] = ci;
                 const int next = p + 1;
@@ -1360,6 +1413,23 @@ int vm_hip_decode_step(const vm_hip_decode_model* model, void* workspace, int64_
     VM_TRY_HIP(hipLaunchCooperativeKernel(fn, dim3(lay.G), dim3(kT), args, 0, static_cast<hipStream_t>(stream)),
                "DecodeStep on HIP at launch: hipLaunchCooperativeKernel");
     return check_launch("DecodeStep", static_cast<hipStream_t>(stream));
+}
+
+int vm_hip_decode_trace_read(void* host, int64_t bytes) {
+    clear_error();
+#ifdef VM_DECODE_TRACE
+    if (!host || bytes < 0) return fail_inval("vm_hip_decode_trace_read: bad argument");
+    const int64_t all = static_cast<int64_t>(sizeof(g_decode_trace));
+    VM_TRY_HIP(hipDeviceSynchronize(), "decode_trace: sync");
+    VM_TRY_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_decode_trace), static_cast<size_t>(std::min(bytes, all))),
+               "decode_trace: copy");
+    return 0;
+#else
+    (void)host;
+    (void)bytes;
+    set_error("vm_hip_decode_trace_read: libvmhip was built without VM_DECODE_TRACE (VELOMIND_DECODE_TRACE=1)");
+    return VM_HIP_EUNSUPPORTED;
+#endif
 }
 
 int vm_hip_decode_status(void* workspace, int* failed, void* stream) {
