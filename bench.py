@@ -374,7 +374,7 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph
         os.environ["VELOMIND_DECODE_PERSISTENT"] = "1" if persistent else "0"
         try:
             sess = VL.Session(w, VL.ENGINE_RESIDENT, spec["quant"], spec["block"],
-                              max_seq=spec["prompt"] + steps + 1)
+                              max_seq=spec["prompt"] + max(steps, 8) + 1)
         finally:
             if prev is None:
                 del os.environ["VELOMIND_DECODE_PERSISTENT"]
@@ -695,6 +695,10 @@ def main() -> int:
                          "the decode steps launch eagerly so that rocprofv3 can trace them)")
     ap.add_argument("--decode-persistent", action="store_true",
                     help="with --e2e-only: decode with the one-launch step (vm_hip_decode_step)")
+    ap.add_argument("--e2e-model", default="", choices=[""] + list(E2E_MODELS),
+                    help="with --e2e-only: only this model")
+    ap.add_argument("--e2e-steps", type=int, default=0,
+                    help="with --e2e-only: decode this many tokens instead of the config's (short profiling runs)")
     ap.add_argument("--decode-trace", action="store_true",
                     help="only the one-launch decode step's phase timestamps (library built with "
                          "VELOMIND_DECODE_TRACE=1), printed as one JSON line")
@@ -743,9 +747,10 @@ def main() -> int:
         return 0
     if args.e2e_only:
         e2e = {}
-        for name in E2E_MODELS:
+        for name in [args.e2e_model] if args.e2e_model else E2E_MODELS:
             log(f"bench: end-to-end {name}")
-            e2e[name] = e2e_bench(name, use_graph=not args.no_graph, persistent=args.decode_persistent)
+            e2e[name] = e2e_bench(name, use_graph=not args.no_graph, persistent=args.decode_persistent,
+                                  steps=args.e2e_steps)
             log(f"bench: {name}: prefill {e2e[name]['prefill_tokens_per_s']} tok/s, "
                 f"decode {e2e[name]['decode_tokens_per_s']} tok/s ({e2e[name]['decode_path']})")
         print(json.dumps({"metric": METRIC, "e2e": e2e}), flush=True)
