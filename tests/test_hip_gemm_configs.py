@@ -165,3 +165,46 @@ def test_activation_magnitudes(hip, kind, block, reps):
         # per-column INT8 stages nothing: fp32-equivalent against the reference loop
         bound = (2.0 ** -22 + 2 * k * 2.0 ** -24) * 1.01 * mag + 1e-300
         assert np.all(np.abs(out - ref) <= bound), f"worst ratio {np.max(np.abs(out - ref) / bound):.3e}"
+
+
+# Wide-tile variants (rows_m > 32), forced through VELOMIND_GEMM_WIDE="BM,BN,S,D".
+WIDE = [(128, 128, 2, 1), (128, 128, 2, 2), (128, 128, 4, 1), (64, 128, 2, 1), (64, 128, 4, 1), (128, 64, 2, 2), (64, 256, 2, 1)]
+
+
+@pytest.mark.parametrize("kind,block", [("int8", 0), ("int8_block", 32), ("int8_block", 96), ("int4", 32),
+                                        ("int4", 64)])
+@pytest.mark.parametrize("bm,bn,depth,groups", WIDE)
+@pytest.mark.parametrize("m", [40, 130])
+def test_forced_wide(hip, monkeypatch, bm, bn, depth, groups, kind, block, m):
+    # K = 224 = 3.5 steps of 64; N = 336 leaves partial tiles for every BN;
+    # m = 130 leaves a 2-row M tile after 128.
+    k, n = 224, 336
+    rng = np.random.default_rng(bm * 7 + bn + depth * 3 + groups * 5 + block + m)
+    q, s, qt, blk = _weights(kind, k, n, rng, block)
+    oq = O.QUANT_INT4 if qt == 2 else O.QUANT_INT8
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = O.qmm(x, q.view(np.int8), s, k, oq, blk)
+    for splits in (1, 2, 4):
+        monkeypatch.setenv("VELOMIND_GEMM_WIDE", f"{bm},{bn},{splits},{depth},{groups}")
+        print(f"case wide BM={bm} BN={bn} D={depth} G={groups} S={splits} kind={kind} block={block} m={m} k={k} n={n}",
+              flush=True)
+        out = hip.run_qmm(x, q, s, k, qt, blk)
+        _check(out, ref)
+    monkeypatch.delenv("VELOMIND_GEMM_WIDE")
+
+
+@pytest.mark.parametrize("kind,block", [("int8", 0), ("int4", 32)])
+def test_wide_long_k(hip, monkeypatch, kind, block):
+    # K = 2048: every ring stage wraps several times; the default rule's splits
+    m, k, n = 200, 2048, 512
+    rng = np.random.default_rng(91 + block)
+    q, s, qt, blk = _weights(kind, k, n, rng, block)
+    oq = O.QUANT_INT4 if qt == 2 else O.QUANT_INT8
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = O.qmm(x, q.view(np.int8), s, k, oq, blk)
+    print(f"case wide long-k default kind={kind} m={m} k={k} n={n}", flush=True)
+    _check(hip.run_qmm(x, q, s, k, qt, blk), ref)
+    monkeypatch.setenv("VELOMIND_GEMM_WIDE", "128,128,3,2,2")
+    print(f"case wide long-k 128,128,3,2,2 kind={kind}", flush=True)
+    _check(hip.run_qmm(x, q, s, k, qt, blk), ref)
+    monkeypatch.delenv("VELOMIND_GEMM_WIDE")

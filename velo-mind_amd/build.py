@@ -55,6 +55,12 @@ def _run(cmd: list[str]) -> None:
             sys.stderr.write(line + "\n")
 
 
+# Per-file additions.  qmm_gemm.hip: MFMA accumulators in ordinary VGPRs
+# (with AGPR accumulators the register allocator rotates the loop-carried
+# tiles through copies every iteration of the wide kernel's K loop).
+FILE_FLAGS = {"qmm_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def build_vmhip(jobs: int = 8) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -63,7 +69,7 @@ def build_vmhip(jobs: int = 8) -> str:
     for src in sources:
         obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
         objs.append(obj)
-        cmds.append([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        cmds.append([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     out = os.path.join(OUT_DIR, "libvmhip.so")

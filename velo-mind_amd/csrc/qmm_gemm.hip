@@ -61,6 +61,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;         // K rows per pipeline step
@@ -538,26 +539,86 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 // for an all-zero row, or one holding an infinity or NaN, which then
 // reaches the output as the reference's fp32 arithmetic would propagate
 // it); hi = fp16(a * 2^x_r) and lo = fp16(a * 2^x_r - hi), the difference
-// being exact in fp32.  hi at ah[r * k + c], lo at ah[m * k + r * k + c].
-// One workgroup per row.  Rows of up to kSplitHeld float4 groups per
-// thread stay in registers between the maximum and the split (one read of
-// A); longer rows are read a second time (from L2).
-constexpr int kSplitHeld = 6;   // k <= 6144 in one read
+// being exact in fp32.
+// FRAG = false: row-major, hi at ah[r * k + c], lo at ah[m * k + r * k + c]
+// (the small-tile kernel).
+// FRAG = true (the wide kernel): in the operand order of
+// v_mfma_f32_32x32x16_f16, so that one wave's operand for 32 rows and 16 k
+// is 1 KB of consecutive memory: the 16 bytes lane l of the wave loads for
+// row block b (rows 32b .. 32b + 31) and k block q (k 16q .. 16q + 15) --
+// row 32b + l % 32, k 16q + 8 (l / 32) + 0..7 -- sit at half offset
+// ((b * k / 16 + q) * 64 + l) * 8; lo follows hi after mp * k halves, mp =
+// m rounded up to 32.  Inside each 16-byte piece the halves are stored in
+// the order k = 0, 4, 1, 5, 2, 6, 3, 7, the order in which the wide
+// kernel's weight unpacking produces B (a dot product does not depend on
+// the order of its terms, so A and B only have to agree).
+//
+// Workgroups [0, m) split one row each; rows of up to kSplitHeld groups of
+// eight per thread stay in registers between the maximum and the split
+// (one read of A), longer rows are read a second time (from L2).
+// Workgroups [m, m + col_wgs) compute, for blockwise scales, the per-column
+// power of two the wide kernel stages B with: 2^e with max_b |s[b, j]| / 2^e
+// in [0.5, 1) over all of K (e = 0 for an all-zero or non-finite maximum),
+// written as col_pow[j] = 2^e and col_pow[n + j] = 2^-e; 256 columns each.
+constexpr int kSplitHeld = 3;   // k <= 6144 in one read
 
-__global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restrict__ a,
-                                                          _Float16* __restrict__ ah,
-                                                          int* __restrict__ row_exp, int m, int k, int vec) {
-    __shared__ float wmax[4];
-    const int row = blockIdx.x;
+template <bool FRAG>
+__global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict__ a, _Float16* __restrict__ ah,
+                                                        int* __restrict__ row_exp, int m, int k, int vec,
+                                                        const float* __restrict__ scale, float* __restrict__ col_pow,
+                                                        int n, int nblk) {
+    __shared__ float wmax[4 * 256];
     const int tid = threadIdx.x;
+    if (static_cast<int>(blockIdx.x) >= m) {
+        const int j0 = (static_cast<int>(blockIdx.x) - m) * 256 + 4 * (tid & 63);
+        const int bg = tid >> 6;
+        float mx[4] = {0.f, 0.f, 0.f, 0.f};
+        if (j0 < n) {
+            for (int b = bg; b < nblk; b += 4 * 4) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int bb = b + 4 * u;
+                    v[u] = bb < nblk ? *reinterpret_cast<const float4*>(scale + static_cast<int64_t>(bb) * n + j0)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    mx[0] = fmaxf(mx[0], fabsf(v[u].x));
+                    mx[1] = fmaxf(mx[1], fabsf(v[u].y));
+                    mx[2] = fmaxf(mx[2], fabsf(v[u].z));
+                    mx[3] = fmaxf(mx[3], fabsf(v[u].w));
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wmax[bg * 256 + 4 * (tid & 63) + e] = mx[e];
+        __syncthreads();
+        const int j = (static_cast<int>(blockIdx.x) - m) * 256 + tid;
+        if (j < n) {
+            float mm = fmaxf(fmaxf(wmax[tid], wmax[256 + tid]), fmaxf(wmax[512 + tid], wmax[768 + tid]));
+            int e = 0;
+            if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
+            col_pow[j] = ldexpf(1.0f, e);
+            col_pow[n + j] = ldexpf(1.0f, -e);
+        }
+        return;
+    }
+    const int row = blockIdx.x;
     const float* src = a + static_cast<int64_t>(row) * k;
-    const int vecs = k >> 2;   // k % 32 == 0 on this path
-    const bool held = vecs <= kSplitHeld * 256;
-    auto load4 = [&](int v) {
-        if (vec) return reinterpret_cast<const float4*>(src)[v];
-        return make_float4(src[4 * v], src[4 * v + 1], src[4 * v + 2], src[4 * v + 3]);
+    const int groups = k >> 3;   // k % 32 == 0 on this path
+    const bool held = groups <= kSplitHeld * 256;
+    auto load8 = [&](int g, float4& p, float4& q) {
+        if (vec) {
+            p = reinterpret_cast<const float4*>(src)[2 * g];
+            q = reinterpret_cast<const float4*>(src)[2 * g + 1];
+        } else {
+            const float* s8 = src + 8 * g;
+            p = make_float4(s8[0], s8[1], s8[2], s8[3]);
+            q = make_float4(s8[4], s8[5], s8[6], s8[7]);
+        }
     };
-    float4 keep[kSplitHeld];
+    float4 keep[kSplitHeld][2];
     float mx = 0.0f;
     bool special = false;
     auto scan = [&](const float4& x) {
@@ -569,13 +630,26 @@ __global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restric
     if (held) {
 #pragma unroll
         for (int r = 0; r < kSplitHeld; ++r) {
-            const int v = tid + r * 256;
-            keep[r] = v < vecs ? load4(v) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int g = tid + r * 256;
+            if (g < groups) {
+                load8(g, keep[r][0], keep[r][1]);
+            } else {
+                keep[r][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+                keep[r][1] = keep[r][0];
+            }
         }
 #pragma unroll
-        for (int r = 0; r < kSplitHeld; ++r) scan(keep[r]);
+        for (int r = 0; r < kSplitHeld; ++r) {
+            scan(keep[r][0]);
+            scan(keep[r][1]);
+        }
     } else {
-        for (int v = tid; v < vecs; v += 256) scan(load4(v));
+        for (int g = tid; g < groups; g += 256) {
+            float4 p, q;
+            load8(g, p, q);
+            scan(p);
+            scan(q);
+        }
     }
     // an infinity or NaN anywhere in the row disables the scaling
     if (special) mx = __builtin_inff();
@@ -590,30 +664,523 @@ __global__ __launch_bounds__(256) void a_split_f16_kernel(const float* __restric
         x = 15 - e;
     }
     if (tid == 0) row_exp[row] = x;
-    half4v* hi = reinterpret_cast<half4v*>(ah + static_cast<int64_t>(row) * k);
-    half4v* lo = reinterpret_cast<half4v*>(ah + (static_cast<int64_t>(m) + row) * k);
-    auto split = [&](int v, const float4& y) {
-        const float s0 = ldexpf(y.x, x), s1 = ldexpf(y.y, x), s2 = ldexpf(y.z, x), s3 = ldexpf(y.w, x);
-        const half4v h = {static_cast<_Float16>(s0), static_cast<_Float16>(s1), static_cast<_Float16>(s2),
-                          static_cast<_Float16>(s3)};
-        hi[v] = h;
-        // an infinite part (|a| beyond fp16 in an unscaled row) leaves lo at 0
-        auto rest = [](float s, _Float16 hh) {
-            const float d = s - static_cast<float>(hh);
-            return static_cast<_Float16>(d == d && fabsf(d) <= 65504.0f ? d : 0.0f);
-        };
-        lo[v] = half4v{rest(s0, h[0]), rest(s1, h[1]), rest(s2, h[2]), rest(s3, h[3])};
+    const int64_t mp = FRAG ? (static_cast<int64_t>(m) + 31) / 32 * 32 : m;
+    half8v* hi = reinterpret_cast<half8v*>(ah);
+    half8v* lo = reinterpret_cast<half8v*>(ah + mp * k);
+    // 16-byte piece index of the row's 8-group g
+    auto piece = [&](int g) -> int64_t {
+        if constexpr (FRAG)
+            return ((static_cast<int64_t>(row / 32) * (k / 16) + g / 2) * 64 + row % 32 + 32 * (g % 2));
+        return static_cast<int64_t>(row) * (k / 8) + g;
+    };
+    auto split = [&](int g, const float4& p, const float4& q) {
+        const float s[8] = {ldexpf(p.x, x), ldexpf(p.y, x), ldexpf(p.z, x), ldexpf(p.w, x),
+                            ldexpf(q.x, x), ldexpf(q.y, x), ldexpf(q.z, x), ldexpf(q.w, x)};
+        half8v h, l;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            // position i holds k = i (row-major) or k = i / 2 + 4 * (i % 2) (FRAG)
+            const int kk = FRAG ? (i >> 1) + 4 * (i & 1) : i;
+            const _Float16 hh = static_cast<_Float16>(s[kk]);
+            // an infinite part (|a| beyond fp16 in an unscaled row) leaves lo at 0
+            const float d = s[kk] - static_cast<float>(hh);
+            h[i] = hh;
+            l[i] = static_cast<_Float16>(d == d && fabsf(d) <= 65504.0f ? d : 0.0f);
+        }
+        hi[piece(g)] = h;
+        lo[piece(g)] = l;
     };
     if (held) {
 #pragma unroll
         for (int r = 0; r < kSplitHeld; ++r) {
-            const int v = tid + r * 256;
-            if (v < vecs) split(v, keep[r]);
+            const int g = tid + r * 256;
+            if (g < groups) split(g, keep[r][0], keep[r][1]);
         }
     } else {
-        for (int v = tid; v < vecs; v += 256) split(v, load4(v));
+        for (int g = tid; g < groups; g += 256) {
+            float4 p, q;
+            load8(g, p, q);
+            split(g, p, q);
+        }
     }
 }
+
+// ---------------------------------------------------------------------------
+// Wide-tile MFMA GEMM (rows_m > 32).  A BM x BN tile per workgroup of four
+// waves stacked in M (each wave BM/4 rows by all BN columns), K in steps of
+// 64 rows.
+//
+// A (hi and lo fp16 parts, laid out in operand order by
+// gemm_prep_kernel<true>) goes straight from global memory into MFMA
+// operand registers: one wave's operand for 32 rows and 16 k is one 1 KB
+// load of consecutive memory (rows scattered over 32 cache lines would
+// take the vector memory pipeline 4x the line lookups, which measured as
+// ~2000 cycles of load issue per step).  Each wave owns distinct rows, so
+// A is read once per workgroup and never passes through LDS (with both fp16
+// parts it is the larger operand: 4 bytes per element).
+//
+// B is unpacked once per tile and step and shared through LDS.  A thread
+// takes "units" of 4 columns x 8 K rows: INT4 four dword loads (byte
+// rows), INT8 eight, each a 128-byte run across 32 lanes.  v_perm_b32
+// transposes the unit to one dword per column (INT4: its 8 nibbles in K
+// order; INT8: rows {0,1,4,5} and {2,3,6,7}), the packed-half magic numbers
+// turn the codes into fp16 in the order k = 0, 4, 1, 5, 2, 6, 3, 7 (the
+// order A is stored in), and each column's 8 halves go to LDS as one
+// 16-byte write.  B sits in LDS column-major ([column][k], 64 + 8 halves
+// per row: 144-byte rows make both the writes and the fragment reads free
+// of bank conflicts), and tile column 4q + c is stored at LDS row c * BN/4
+// + q, so the 16 lanes of a write touch 16 consecutive rows; the epilogue
+// maps rows back to columns.
+//
+// Pipeline: a ring of D register stages, stage t holding A's fragments of
+// step t and B's raw codes of step t + 1; at step t the MFMAs use A(t) and
+// B(t) from LDS while B(t + 1) is unpacked into the other LDS buffer, then
+// stage t is refilled with step t + D.  One barrier per step.  The K loop
+// runs whole rounds of D steps (steps past the split multiply zeros), so
+// every iteration issues the same loads and the compiler's vmcnt waits
+// release each stage as soon as its own loads are in.
+namespace wide {
+
+#ifndef VM_WIDE_SCHED
+#define VM_WIDE_SCHED 1
+#endif
+#ifndef VM_WIDE_VALU
+#define VM_WIDE_VALU 5
+#endif
+
+constexpr int kRow = kBK + 8;   // halves per LDS row of B (one column): 144 bytes
+
+template <int KIND, int BM, int BN, int D, int G>
+struct Cfg {
+    static constexpr int kThreads = 256 * G;                          // G groups of four waves
+    static constexpr int WAVES_N = 128 / BM;                          // BM 128: 4 x 1 waves; BM 64: 2 x 2
+    static constexpr int WN = BN / WAVES_N;                           // columns per wave (32 rows each)
+    static constexpr int TN = WN / 32;                                // 32 x 32 MFMA tiles per wave
+    static constexpr int kQuads = BN / 4;
+    static constexpr int kUnits = kQuads * (kBK / 8);                 // 4 columns x 8 K rows
+    static constexpr int kBPer = (kUnits + 255) / 256;                // per thread of a group
+    static constexpr int kWords = KIND == 2 ? 4 : 8;                  // code dwords per unit
+    static constexpr bool kBlock = KIND != 0;
+    static constexpr int kLdsB = BN * kRow;                           // halves per buffer
+    static constexpr int kCRow = BN + 4;                              // epilogue tile row (floats)
+    static constexpr int kLdsBytes = (2 * G * kLdsB * 2 > BM * kCRow * 4) ? 2 * G * kLdsB * 2 : BM * kCRow * 4;
+    // Two workgroups per CU when two fit in LDS and the registers a thread
+    // holds (accumulators, D stages, B fragments, ~48 for addressing)
+    // stay within the 256 that two waves per SIMD leave each; otherwise one,
+    // with all 512.
+    static constexpr int kRegEstimate = TN * 16 + D * (32 + kBPer * (kWords + (kBlock ? 4 : 0))) + TN * 4 + 48;
+    static constexpr int kWavesPerEu = G == 2 ? 2 : (2 * kLdsBytes <= 160 * 1024 && kRegEstimate <= 256) ? 2 : 1;
+    static_assert((BM == 128 || BM == 64) && TN >= 1 && WN % 32 == 0, "32 x 32 MFMA tiles");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+template <int KIND, int BM, int BN, int D, int G>
+struct Raw {
+    using C = Cfg<KIND, BM, BN, D, G>;
+    half8v ah[4];   // A hi fragments of this step, one per 16-k sub-step
+    half8v al[4];   // A lo fragments
+    uint32_t w[C::kBPer][C::kWords];
+    u32x4 s[C::kBlock ? C::kBPer : 1];
+};
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// fp16 pair {v, v}, rounded to nearest even
+__device__ __forceinline__ uint32_t splat_f16(float v) {
+    const _Float16 h = static_cast<_Float16>(v);
+    return __builtin_bit_cast(uint32_t, half2v{h, h});
+}
+
+template <int KIND, int BM, int BN, int D, int G>
+__global__ __launch_bounds__(256 * G) __attribute__((amdgpu_waves_per_eu(Cfg<KIND, BM, BN, D, G>::kWavesPerEu,
+                                                                         Cfg<KIND, BM, BN, D, G>::kWavesPerEu)))
+void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict__ row_exp,
+                          const float* __restrict__ col_pow, const uint8_t* __restrict__ wq,
+                          const float* __restrict__ scale, float* __restrict__ c, int m, int k, int n,
+                          int block_size, int steps_per_split, int tiles_n, int tiles_m, uint32_t a_bytes,
+                          uint32_t lo_offset, uint32_t code_bytes, uint32_t scale_bytes, float* __restrict__ partials,
+                          unsigned* __restrict__ counters) {
+    using C = Cfg<KIND, BM, BN, D, G>;
+    using R = Raw<KIND, BM, BN, D, G>;
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    __shared__ unsigned ticket;
+
+    // G = 2: two groups of four waves take alternate K steps of the tile
+    // (group g the steps s with s % 2 == g), so each SIMD holds two waves and
+    // one wave's stalls on load issue leave the MFMA pipe to the other; the
+    // groups' accumulators are summed through LDS at the end.
+    const int tid = threadIdx.x;
+    const int grp = G == 2 ? tid >> 8 : 0;
+    const int gtid = tid & 255;   // thread within the group
+    const int lane = tid & 63;
+    const int wave = gtid >> 6;
+    const int wm = wave / C::WAVES_N;
+    const int wn = wave % C::WAVES_N;
+    int lin = blockIdx.x;
+    {
+        const int full = static_cast<int>(gridDim.x) & ~7;
+        if (lin < full) lin = (lin & 7) * (full >> 3) + (lin >> 3);
+    }
+    const int tile_x = lin % tiles_n;
+    const int tile_y = (lin / tiles_n) % tiles_m;
+    const int split = lin / (tiles_n * tiles_m);
+    const int splits = static_cast<int>(gridDim.x) / (tiles_n * tiles_m);
+    const int n0 = tile_x * BN;
+    const int m0 = tile_y * BM;
+    const int total_steps = (k + kBK - 1) / kBK;
+    const int step0 = split * steps_per_split;
+    const int nsteps = min(total_steps, step0 + steps_per_split) - step0;
+    const int k_end = min(k, (step0 + nsteps) * kBK);
+    const int fr = lane & 31;   // operand row (A) / column (B) of a 32 x 32 x 16 MFMA
+    const int fh = lane >> 5;   // which 8 of its 16 k
+
+    const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wq, code_bytes);
+    const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
+
+    // 2^-e of the unit columns (blockwise scales)
+    float inv[C::kBPer][4];
+    if constexpr (C::kBlock) {
+        const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(col_pow, static_cast<uint32_t>(n) * 8u);
+#pragma unroll
+        for (int p = 0; p < C::kBPer; ++p) {
+            const int u = gtid + p * 256;
+            const int col = n0 + 4 * (u % C::kQuads);
+            const u32x4 v = buffer_load16(prs, (u < C::kUnits && col < n) ? (static_cast<uint32_t>(n) + col) * 4u
+                                                                         : static_cast<uint32_t>(n) * 8u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) inv[p][e] = __uint_as_float(v[e]);
+        }
+    }
+
+    // Scale block of a unit: with the loaded step's first row k0 = q0 *
+    // block_size + r0, the unit's block is q0 + 0, 1 or 2 (block_size >= 32
+    // > the unit's offset of at most 56 rows), found with compares.  (q0,
+    // r0) advance by one step per load (each load fetches B for the step
+    // after the previous load's), so no division sits in the loop.
+    int q0 = 0, r0 = 0;
+    if constexpr (C::kBlock) {
+        const int kb = (step0 + G + grp) * kBK;   // the group's first load fetches B of its second step
+        q0 = kb / block_size;
+        r0 = kb - q0 * block_size;
+    }
+    // A pieces of this lane (out-of-range rows and steps read zeros): row
+    // block (m0 / 32 + wm), k block q: byte offset ((b * k/16 + q) * 64 + lane) * 16
+    const bool a_row_ok = m0 + wm * 32 + fr < m;
+    const uint32_t a_blk_off = (static_cast<uint32_t>(m0 / 32 + wm) * static_cast<uint32_t>(k / 16) * 64u + lane) * 16u;
+
+    // stage of the group's step t (K step G * t + grp): A of that step,
+    // B codes and scales of the group's step t + 1
+    auto load = [&](int t, R& r) {
+        const int k0 = (step0 + G * t + grp) * kBK;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int kq = k0 / 16 + q;
+            const bool ok = a_row_ok && 16 * kq < k_end;
+            const uint32_t off = a_blk_off + static_cast<uint32_t>(kq) * 1024u;
+            r.ah[q] = __builtin_bit_cast(half8v, buffer_load16(ars, ok ? off : a_bytes));
+            r.al[q] = __builtin_bit_cast(half8v, buffer_load16(ars, ok ? off + lo_offset : a_bytes));
+        }
+        const int kb0 = k0 + G * kBK;
+#pragma unroll
+        for (int p = 0; p < C::kBPer; ++p) {
+            const int u = gtid + p * 256;
+            const int q = u % C::kQuads;
+            const int kg = u / C::kQuads;
+            const int col = n0 + 4 * q;
+            const int klog = kb0 + 8 * kg;
+            const bool ok = u < C::kUnits && klog < k_end && col < n;
+            const uint32_t row0 = KIND == 2 ? static_cast<uint32_t>(klog) / 2u : static_cast<uint32_t>(klog);
+#pragma unroll
+            for (int i = 0; i < C::kWords; ++i)
+                r.w[p][i] = buffer_load4(wrs, ok ? (row0 + i) * static_cast<uint32_t>(n) + col : code_bytes);
+            if constexpr (C::kBlock) {
+                const int tt = r0 + 8 * kg;
+                const uint32_t blk = static_cast<uint32_t>(q0 + (tt >= block_size) + (tt >= 2 * block_size));
+                r.s[p] = buffer_load16(srs, ok ? (blk * static_cast<uint32_t>(n) + col) * 4u : scale_bytes);
+            }
+        }
+        if constexpr (C::kBlock) {   // r0 + 64 G < (2 G + 1) * block_size
+            r0 += G * kBK;
+#pragma unroll
+            for (int i = 0; i < 2 * G; ++i) {
+                const int c1 = r0 >= block_size ? 1 : 0;
+                r0 -= c1 * block_size;
+                q0 += c1;
+            }
+        }
+    };
+
+    // unit -> four columns of 8 fp16 weights (k order 0, 4, 1, 5, 2, 6, 3, 7)
+    auto unpack = [&](const R& r, int p, u32x4 (&out)[4]) {
+        uint32_t t[4][2];
+        const uint32_t* w = r.w[p];
+        if constexpr (KIND == 2) {
+            const uint32_t a01 = perm(w[1], w[0], 0x05010400u), b01 = perm(w[1], w[0], 0x07030602u);
+            const uint32_t a23 = perm(w[3], w[2], 0x05010400u), b23 = perm(w[3], w[2], 0x07030602u);
+            t[0][0] = perm(a23, a01, 0x05040100u);
+            t[1][0] = perm(a23, a01, 0x07060302u);
+            t[2][0] = perm(b23, b01, 0x05040100u);
+            t[3][0] = perm(b23, b01, 0x07060302u);
+        } else {
+            const uint32_t a01 = perm(w[1], w[0], 0x05010400u), b01 = perm(w[1], w[0], 0x07030602u);
+            const uint32_t a23 = perm(w[3], w[2], 0x05010400u), b23 = perm(w[3], w[2], 0x07030602u);
+            const uint32_t a45 = perm(w[5], w[4], 0x05010400u), b45 = perm(w[5], w[4], 0x07030602u);
+            const uint32_t a67 = perm(w[7], w[6], 0x05010400u), b67 = perm(w[7], w[6], 0x07030602u);
+            t[0][0] = perm(a45, a01, 0x05040100u);
+            t[1][0] = perm(a45, a01, 0x07060302u);
+            t[2][0] = perm(b45, b01, 0x05040100u);
+            t[3][0] = perm(b45, b01, 0x07060302u);
+            t[0][1] = perm(a67, a23, 0x05040100u);
+            t[1][1] = perm(a67, a23, 0x07060302u);
+            t[2][1] = perm(b67, b23, 0x05040100u);
+            t[3][1] = perm(b67, b23, 0x07060302u);
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            uint32_t sc = 0;
+            if constexpr (C::kBlock) sc = splat_f16(__uint_as_float(r.s[p][cc]) * inv[p][cc]);
+            if constexpr (KIND == 2) {
+                const uint32_t x = t[cc][0] ^ 0x88888888u;
+                const _Float16 bias = static_cast<_Float16>(1032.0f);
+                out[cc][0] = hmul2(hsub2((x & 0x000F000Fu) | 0x64006400u, bias), sc);
+                out[cc][1] = hmul2(hsub2(((x >> 4) & 0x000F000Fu) | 0x64006400u, bias), sc);
+                out[cc][2] = hmul2(hsub2(((x >> 8) & 0x000F000Fu) | 0x64006400u, bias), sc);
+                out[cc][3] = hmul2(hsub2(((x >> 12) & 0x000F000Fu) | 0x64006400u, bias), sc);
+            } else {
+                const _Float16 bias = static_cast<_Float16>(1152.0f);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t x = t[cc][h] ^ 0x80808080u;
+                    uint32_t e = hsub2((x & 0x00FF00FFu) | 0x64006400u, bias);
+                    uint32_t o = hsub2(((x >> 8) & 0x00FF00FFu) | 0x64006400u, bias);
+                    if constexpr (C::kBlock) {
+                        e = hmul2(e, sc);
+                        o = hmul2(o, sc);
+                    }
+                    out[cc][2 * h] = e;
+                    out[cc][2 * h + 1] = o;
+                }
+            }
+        }
+    };
+    // LDS B buffer `buf` (0, 1) of this group
+    auto lds_b = [&](int buf) { return lds + (grp * 2 + buf) * C::kLdsB; };
+    auto write_b = [&](const R& r, int buf) {
+        _Float16* b = lds_b(buf);
+#pragma unroll
+        for (int p = 0; p < C::kBPer; ++p) {
+            const int u = gtid + p * 256;
+            if (C::kUnits % 256 == 0 || u < C::kUnits) {
+                u32x4 out[4];
+                unpack(r, p, out);
+                const int q = u % C::kQuads;
+                const int kg = u / C::kQuads;
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc)
+                    *reinterpret_cast<u32x4*>(b + (cc * C::kQuads + q) * kRow + 8 * kg) = out[cc];
+            }
+        }
+    };
+
+    floatx16 acc[C::TN];
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+
+    // MFMAs of two 16-k sub-steps: every tile's hi product, then every
+    // tile's lo product (consecutive MFMAs rarely wait for each other's
+    // accumulator)
+    auto mfma_pair = [&](const R& r, int buf, int q0) {
+        const _Float16* b = lds_b(buf);
+#pragma unroll
+        for (int q = q0; q < q0 + 2; ++q) {
+            half8v bf[C::TN];
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j)
+                bf[j] = *reinterpret_cast<const half8v*>(b + (wn * C::WN + j * 32 + fr) * kRow + q * 16 + 8 * fh);
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.ah[q], bf[j], acc[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.al[q], bf[j], acc[j], 0, 0, 0);
+        }
+    };
+
+    // Instruction order inside a step (the compiler otherwise issues the
+    // loads, the MFMAs and the B unpacking as separate runs, leaving the
+    // MFMA pipe idle for more than half of the step): B fragment reads for
+    // the first two 16-k sub-steps, then every MFMA followed by a share of
+    // the VALU work and the loads, the remaining fragment reads halfway.
+    auto interleave = [&]() {
+#if VM_WIDE_SCHED
+        constexpr int kMfma = 4 * C::TN * 2;
+        constexpr int kLoads = 8 + C::kBPer * (C::kWords + (C::kBlock ? 1 : 0));
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::TN, 0);   // DS reads, sub-steps 0 and 1
+#pragma unroll
+        for (int i = 0; i < kMfma; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, VM_WIDE_VALU, 0);   // VALU
+            if (i < kLoads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+            if (i == kMfma / 2 - 2) __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::TN, 0);   // DS reads 2, 3
+        }
+#endif
+    };
+
+    // ---- pipeline.  B(0) is loaded and unpacked on its own; stage t then
+    // carries A(t) and B(t + 1).
+    {
+        R b0;
+        const int kk0 = (step0 + grp) * kBK;
+        // B of the group's first step: a stage whose B part is that step (its A part is unused)
+#pragma unroll
+        for (int p = 0; p < C::kBPer; ++p) {
+            const int u = gtid + p * 256;
+            const int q = u % C::kQuads;
+            const int kg = u / C::kQuads;
+            const int col = n0 + 4 * q;
+            const int klog = kk0 + 8 * kg;
+            const bool ok = u < C::kUnits && klog < k_end && col < n;
+            const uint32_t row0 = KIND == 2 ? static_cast<uint32_t>(klog) / 2u : static_cast<uint32_t>(klog);
+#pragma unroll
+            for (int i = 0; i < C::kWords; ++i)
+                b0.w[p][i] = buffer_load4(wrs, ok ? (row0 + i) * static_cast<uint32_t>(n) + col : code_bytes);
+            if constexpr (C::kBlock) {
+                const uint32_t blk = static_cast<uint32_t>(klog) / static_cast<uint32_t>(block_size);
+                b0.s[p] = buffer_load16(srs, ok ? (blk * static_cast<uint32_t>(n) + col) * 4u : scale_bytes);
+            }
+        }
+        write_b(b0, 0);
+    }
+    // Stage refills go into the stage of the previous step, at the start of
+    // a step: a load into registers that MFMAs issued just before still
+    // read waits for those MFMAs (measured: ~1800 cycles per step when the
+    // stage just consumed was refilled right after its MFMAs).  So D stages
+    // keep D - 1 steps in flight.  (The loader's scale-block state expects
+    // the steps in order: the prologue loads steps 0 .. D - 2, step s loads
+    // step s + D - 1.)
+    R st[D];
+#pragma unroll
+    for (int d = 0; d + 1 < D; ++d) load(d, st[d]);
+    __syncthreads();
+    const int nloc = (nsteps + G - 1) / G;   // steps per group
+    for (int s = 0; s < nloc; s += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int cur = u & 1;   // D is even: buffer parity is static
+            load(s + u + D - 1, st[(u + D - 1) % D]);
+            mfma_pair(st[u], cur, 0);
+            write_b(st[u], cur ^ 1);
+            mfma_pair(st[u], cur, 2);
+            interleave();
+            __syncthreads();
+        }
+    }
+
+    // ---- epilogue.  The tile goes through LDS (free after the loop's last
+    // barrier) so that C, or the split's partials, are written in whole
+    // 16-byte pieces of rows.  32 x 32 D layout: element v of lane l is row
+    // 8 * (v / 4) + 4 * (l / 32) + v % 4; its column is LDS B row rr = wn *
+    // WN + j * 32 + l % 32, i.e. tile column 4 * (rr % BN/4) + rr / (BN/4).
+    float* sc = reinterpret_cast<float*>(lds);
+    if constexpr (G == 2) {
+        // group 1's partial sums go through the tile (same positions as
+        // group 0's), group 0 adds them in fixed order
+        if (grp == 1) {
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j) {
+                const int rr = wn * C::WN + j * 32 + fr;
+                const int tc = 4 * (rr % C::kQuads) + rr / C::kQuads;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) sc[(wm * 32 + 8 * (v / 4) + 4 * fh + v % 4) * C::kCRow + tc] = acc[j][v];
+            }
+        }
+        __syncthreads();
+        if (grp == 0) {
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j) {
+                const int rr = wn * C::WN + j * 32 + fr;
+                const int tc = 4 * (rr % C::kQuads) + rr / C::kQuads;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[j][v] += sc[(wm * 32 + 8 * (v / 4) + 4 * fh + v % 4) * C::kCRow + tc];
+            }
+        }
+        __syncthreads();
+    }
+    if (grp == 0) {
+        const __amdgpu_buffer_rsrc_t crs = C::kBlock ? buffer_rsrc(col_pow, static_cast<uint32_t>(n) * 4u) : srs;
+        const uint32_t lim = C::kBlock ? static_cast<uint32_t>(n) * 4u : scale_bytes;
+        float colscale[C::TN];
+        int tcol[C::TN];
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) {
+            const int rr = wn * C::WN + j * 32 + fr;
+            tcol[j] = 4 * (rr % C::kQuads) + rr / C::kQuads;
+            const int col = n0 + tcol[j];
+            colscale[j] = __uint_as_float(buffer_load4(crs, col < n ? static_cast<uint32_t>(col) * 4u : lim));
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int trow = wm * 32 + 8 * (v / 4) + 4 * fh + v % 4;
+            const int row = m0 + trow;
+            const int nx = row < m ? -row_exp[row] : 0;   // 2^-x undoes the row's staging scale
+#pragma unroll
+            for (int j = 0; j < C::TN; ++j) sc[trow * C::kCRow + tcol[j]] = ldexpf(acc[j][v] * colscale[j], nx);
+        }
+    }
+    __syncthreads();
+    const uint32_t out_lim = static_cast<uint32_t>(min(static_cast<int64_t>(m) * n * 4, int64_t(0x7fffffff)));
+    const __amdgpu_buffer_rsrc_t out_rs =
+        buffer_rsrc(splits == 1 ? c : partials + static_cast<int64_t>(split) * m * n, out_lim);
+    for (int idx = tid; idx < BM * (BN / 4); idx += C::kThreads) {
+        const int trow = idx / (BN / 4);
+        const int tc = 4 * (idx % (BN / 4));
+        const int row = m0 + trow, col = n0 + tc;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(sc + trow * C::kCRow + tc);
+        const uint32_t off = (row < m && col < n) ? (static_cast<uint32_t>(row) * n + col) * 4u : out_lim;
+        if (splits == 1) buffer_store16(out_rs, off, v);
+        else coherent_store16(out_rs, off, v);   // read by another workgroup (XCD) after the ticket
+    }
+    if (splits == 1) return;
+
+    publish_partials();
+    __syncthreads();
+    const int tile = tile_y * tiles_n + tile_x;
+    if (tid == 0) ticket = ticket_take(&counters[tile], static_cast<unsigned>(splits));
+    __syncthreads();
+    if (ticket != static_cast<unsigned>(splits - 1)) return;
+    const int64_t stride = static_cast<int64_t>(m) * n;
+    const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(partials, 0x7fffffff);
+    const __amdgpu_buffer_rsrc_t crs = buffer_rsrc(c, out_lim);
+    for (int idx = tid; idx < BM * (BN / 4); idx += C::kThreads) {
+        const int row = m0 + idx / (BN / 4);
+        const int col = n0 + 4 * (idx % (BN / 4));
+        if (row >= m || col >= n) continue;
+        const int64_t base = static_cast<int64_t>(row) * n + col;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < splits; s0 += 4) {
+            u32x4 t[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t e = base + (s0 + u) * stride;
+                t[u] = s0 + u < splits ? coherent_load16(prs, static_cast<uint32_t>(e * 4)) : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] += __uint_as_float(t[u][q]);
+        }
+        buffer_store16(crs, static_cast<uint32_t>(base * 4),
+                       u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
+    }
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace wide
 
 struct GemmConfig {
     int bm = 128, bn = 128, splits = 1, deep = 0;
@@ -742,6 +1309,135 @@ int launch_kind(const _Float16* a, const int* row_exp, const uint8_t* wq, const 
     return launch<KIND, 64, 64, 2, 2>(a, row_exp, wq, scale, c, m, k, n, block_size, cfg.splits, stream);
 }
 
+// ---- wide kernel: tile and split choice, launch
+// Rows above this go to the wide kernel by default.
+constexpr int kWideMinRows = 64;
+
+// Which kernel takes rows_m > 4: the wide kernel above kWideMinRows rows;
+// VELOMIND_GEMM_WIDE=0 or a forced small-tile configuration
+// (VELOMIND_GEMM_CFG) keeps every shape on the small-tile kernel, a forced
+// wide configuration (VELOMIND_GEMM_WIDE="BM,BN,S,D[,G]") sends every
+// shape to the wide kernel (measurement sweeps and tests).
+// By default the wide kernel also needs a grid of at least kWideMinWgs
+// workgroups (tiles x K splits): short-K, narrow-N shapes such as
+// SmolLM2-360M's 960 x 960 projections at 128 rows (15 tiles, K too short
+// to split) keep the small-tile kernel's finer grid.
+constexpr long kWideMinWgs = 96;
+
+struct WideConfig;
+WideConfig choose_wide(int kind, int m, int k, int n);
+
+bool use_wide_kernel(int kind, int m, int k, int n);
+
+struct WideConfig {
+    int bm = 128, bn = 128, splits = 1, depth = 2, groups = 1;
+};
+
+// From sweeps on MI355X (config 3: K = 2048, N = 5632, M = 128 / 256 /
+// 512, INT8 and INT4, weights cold): 128-row tiles with two wave groups,
+// 128 columns for M >= 256 and 64 below, and K splits until the grid holds
+// at least ~150 workgroups while every group keeps at least four steps
+// (M = 512: 176 tiles, no split; M = 256: 88 tiles x 2; M = 128: 88 x 2).
+// A split costs a write and a read of the fp32 partial tile, so it only
+// pays where tiles alone leave most CUs idle.
+WideConfig choose_wide(int kind, int m, int k, int n) {
+    (void)kind;
+    WideConfig cfg;
+    const int steps = (k + kBK - 1) / kBK;
+    cfg.bm = 128;
+    cfg.bn = m >= 256 ? 128 : 64;
+    cfg.groups = 2;
+    const long tiles = static_cast<long>((m + cfg.bm - 1) / cfg.bm) * ((n + cfg.bn - 1) / cfg.bn);
+    int s = 1;
+    while (s * 2 <= kMaxSplits && tiles * s < 150 && steps / (s * 2 * cfg.groups) >= 4) s *= 2;
+    cfg.splits = s;
+    // Tuning override for measurement sweeps: VELOMIND_GEMM_WIDE="BM,BN,S,D[,G]"
+    if (const char* env = std::getenv("VELOMIND_GEMM_WIDE")) {
+        int bm = 0, bn = 0, sx = 0, d = 0, g = 1;
+        const int got = std::sscanf(env, "%d,%d,%d,%d,%d", &bm, &bn, &sx, &d, &g);
+        const bool known = (bm == 128 && bn == 128 && ((d == 2 && (g == 1 || g == 2)) || (d == 4 && g == 1))) ||
+                           (bm == 128 && bn == 64 && d == 2 && (g == 1 || g == 2)) ||
+                           (bm == 64 && bn == 128 && (d == 2 || d == 4) && g == 1) ||
+                           (bm == 64 && bn == 256 && d == 2 && g == 1);
+        if (got >= 4 && sx >= 1 && sx <= kMaxSplits && known) {
+            cfg.bm = bm;
+            cfg.bn = bn;
+            cfg.splits = sx;
+            cfg.depth = d;
+            cfg.groups = g;
+        }
+    }
+    // partial tiles are addressed with 32-bit byte offsets
+    while (cfg.splits > 1 && static_cast<int64_t>(cfg.splits) * m * n * 4 >= (int64_t(1) << 31)) cfg.splits /= 2;
+    return cfg;
+}
+
+bool use_wide_kernel(int kind, int m, int k, int n) {
+    if (std::getenv("VELOMIND_GEMM_CFG")) return false;
+    const char* env = std::getenv("VELOMIND_GEMM_WIDE");
+    if (env && env[0] == '0' && env[1] == '\0') return false;
+    if (env && env[0] != '\0') return true;
+    if (m <= kWideMinRows) return false;
+    const WideConfig cfg = choose_wide(kind, m, k, n);
+    const long tiles = static_cast<long>((m + cfg.bm - 1) / cfg.bm) * ((n + cfg.bn - 1) / cfg.bn);
+    return tiles * cfg.splits >= kWideMinWgs;
+}
+
+template <int KIND, int BM, int BN, int D, int G>
+int launch_wide(const _Float16* a, const int* row_exp, const float* col_pow, const uint8_t* wq, const float* scale,
+                float* c, int m, int k, int n, int block_size, int splits, hipStream_t stream) {
+    using C = wide::Cfg<KIND, BM, BN, D, G>;
+    auto kernel = wide::qmm_mfma_wide_kernel<KIND, BM, BN, D, G>;
+    static bool lds_set = false;   // per instantiation (LDS above the 64 KB default)
+    if (!lds_set) {
+        VM_TRY_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes),
+                   "QuantizedMatMul: hipFuncSetAttribute");
+        lds_set = true;
+    }
+    const int tiles_n = (n + BN - 1) / BN;
+    const int tiles_m = (m + BM - 1) / BM;
+    const int steps = (k + kBK - 1) / kBK;
+    const int sps = (steps + splits - 1) / splits;
+    splits = (steps + sps - 1) / sps;
+    Workspace ws{};
+    if (splits > 1) {
+        VM_TRY(get_workspace(stream, static_cast<std::size_t>(splits) * m * n,
+                             static_cast<std::size_t>(tiles_m) * tiles_n, &ws));
+    }
+    const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
+    // A in operand order: m rounded up to 32 rows per part
+    const uint32_t lo_offset = static_cast<uint32_t>((static_cast<int64_t>(m) + 31) / 32 * 32 * k * 2);
+    const uint32_t a_bytes = 2u * lo_offset;   // hi, then lo
+    const uint32_t code_bytes =
+        static_cast<uint32_t>((KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : static_cast<int64_t>(k)) * n);
+    const uint32_t scale_bytes = static_cast<uint32_t>((KIND == 0 ? 1 : nblk) * n * 4);
+    hipLaunchKernelGGL(kernel, dim3(tiles_n * tiles_m * splits), dim3(C::kThreads), C::kLdsBytes, stream, a, row_exp,
+                       col_pow, wq, scale, c, m, k, n, block_size, sps, tiles_n, tiles_m, a_bytes, lo_offset,
+                       code_bytes, scale_bytes, ws.partials, ws.counters);
+    return check_launch("QuantizedMatMul", stream);
+}
+
+template <int KIND>
+int launch_wide_kind(const _Float16* a, const int* row_exp, const float* col_pow, const uint8_t* wq,
+                     const float* scale, float* c, int m, int k, int n, int block_size, hipStream_t stream) {
+    const WideConfig cfg = choose_wide(KIND, m, k, n);
+#define VM_WIDE(BMX, BNX, DX, GX)                                                                              \
+    if (cfg.bm == BMX && cfg.bn == BNX && cfg.depth == DX && cfg.groups == GX)                                 \
+        return launch_wide<KIND, BMX, BNX, DX, GX>(a, row_exp, col_pow, wq, scale, c, m, k, n, block_size,      \
+                                                   cfg.splits, stream);
+    VM_WIDE(128, 128, 2, 1)
+    VM_WIDE(128, 128, 2, 2)
+    VM_WIDE(128, 128, 4, 1)
+    VM_WIDE(128, 64, 2, 1)
+    VM_WIDE(128, 64, 2, 2)
+    VM_WIDE(64, 128, 2, 1)
+    VM_WIDE(64, 128, 4, 1)
+    VM_WIDE(64, 256, 2, 1)
+#undef VM_WIDE
+    return VM_HIP_EUNSUPPORTED;
+}
+
 }  // namespace
 
 int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
@@ -750,7 +1446,8 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
     // whole 16-column groups; buffer offsets are 32-bit.
     if (k % 32 != 0 || n % 16 != 0) return VM_HIP_EUNSUPPORTED;
     // (A's two fp16 parts take m * k * 4 bytes, addressed with 32-bit offsets)
-    if (static_cast<int64_t>(m) * k * 4 >= (int64_t(1) << 31) || static_cast<int64_t>(k) * n >= (int64_t(1) << 31) ||
+    if ((static_cast<int64_t>(m) + 31) / 32 * 32 * k * 4 >= (int64_t(1) << 31) ||
+        static_cast<int64_t>(k) * n >= (int64_t(1) << 31) ||
         static_cast<int64_t>(m) * n * 4 * kMaxSplits >= (int64_t(1) << 40))
         return VM_HIP_EUNSUPPORTED;
     // one-dimensional grid of at most 2^30 workgroups
@@ -764,14 +1461,32 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
         if (block_size % 32 != 0) return VM_HIP_EUNSUPPORTED;
         kind = 1;
     }
-    // A's row-scaled fp16 parts (hi, lo) and row exponents, staged for this call.
-    const std::size_t half_bytes = (static_cast<std::size_t>(m) * k * 4 + 255) & ~std::size_t(255);
+    const bool use_wide = use_wide_kernel(kind, m, k, n);
+    // A's row-scaled fp16 parts (hi, lo), the row exponents and, for the
+    // wide kernel with blockwise scales, the per-column powers of two.
+    const std::size_t mp = use_wide ? (static_cast<std::size_t>(m) + 31) / 32 * 32 : static_cast<std::size_t>(m);
+    const std::size_t half_bytes = (mp * k * 4 + 255) & ~std::size_t(255);
+    const std::size_t exp_bytes = (static_cast<std::size_t>(m) * sizeof(int) + 255) & ~std::size_t(255);
+    const bool col_exps = use_wide && kind != 0;
+    const std::size_t pow_bytes = col_exps ? static_cast<std::size_t>(n) * 2 * sizeof(float) : 0;
     void* aux = nullptr;
-    VM_TRY(get_aux(stream, half_bytes + static_cast<std::size_t>(m) * sizeof(int), &aux));
+    VM_TRY(get_aux(stream, half_bytes + exp_bytes + pow_bytes, &aux));
     auto* ah = static_cast<_Float16*>(aux);
     auto* row_exp = reinterpret_cast<int*>(static_cast<char*>(aux) + half_bytes);
-    hipLaunchKernelGGL(a_split_f16_kernel, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k,
-                       reinterpret_cast<uintptr_t>(a) % 16 == 0 ? 1 : 0);
+    auto* col_pow = col_exps ? reinterpret_cast<float*>(static_cast<char*>(aux) + half_bytes + exp_bytes) : nullptr;
+    const int vec = reinterpret_cast<uintptr_t>(a) % 16 == 0 ? 1 : 0;
+    const int nblk = kind == 0 ? 1 : (k + block_size - 1) / block_size;
+    const int col_wgs = col_exps ? (n + 255) / 256 : 0;
+    if (use_wide) {
+        hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(m + col_wgs), dim3(256), 0, stream, a, ah, row_exp, m, k, vec,
+                           scale, col_pow, n, nblk);
+        VM_TRY(check_launch("QuantizedMatMul", stream));
+        if (kind == 2) return launch_wide_kind<2>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
+        if (kind == 1) return launch_wide_kind<1>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
+        return launch_wide_kind<0>(ah, row_exp, col_pow, wq, scale, c, m, k, n, 0, stream);
+    }
+    hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k, vec, scale,
+                       col_pow, n, nblk);
     VM_TRY(check_launch("QuantizedMatMul", stream));
     if (kind == 2) return launch_kind<2>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
     if (kind == 1) return launch_kind<1>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);

@@ -36,6 +36,28 @@ __device__ __forceinline__ void coherent_store(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), rsrc,
+                                           static_cast<int>(offset), 0, 0);
+}
+
+// 16-byte forms of coherent_store / coherent_load: the sc1 cache-policy bit
+// (16) on a buffer access is what the compiler emits for an agent-scope
+// relaxed atomic store or load on gfx950 (written through to, or read from,
+// the memory-side coherence point), for 16 bytes at a time.  Used for
+// split-K partial tiles.
+constexpr int kPolicySc1 = 16;
+
+__device__ __forceinline__ void coherent_store16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), rsrc,
+                                           static_cast<int>(offset), 0, kPolicySc1);
+}
+
+__device__ __forceinline__ u32x4 coherent_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset), 0,
+                                                                          kPolicySc1));
+}
+
 // Split-K ticket hand-off.  Each workgroup stores its partials with
 // agent-scope relaxed stores (coherent_store), every thread waits for its
 // own stores to be acknowledged (publish_partials), the workgroup meets at
