@@ -553,37 +553,42 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 // kernel's weight unpacking produces B (a dot product does not depend on
 // the order of its terms, so A and B only have to agree).
 //
-// Workgroups [0, m) split one row each; rows of up to kSplitHeld groups of
-// eight per thread stay in registers between the maximum and the split
-// (one read of A), longer rows are read a second time (from L2).
-// Workgroups [m, m + col_wgs) compute, for blockwise scales, the per-column
-// power of two the wide kernel stages B with: 2^e with max_b |s[b, j]| / 2^e
-// in [0.5, 1) over all of K (e = 0 for an all-zero or non-finite maximum),
-// written as col_pow[j] = 2^e and col_pow[n + j] = 2^-e; 256 columns each.
+// Workgroups [col_wgs, col_wgs + m) split one row each; rows of up to
+// kSplitHeld groups of eight per thread stay in registers between the
+// maximum and the split (one read of A), longer rows are read a second time
+// (from L2).  Workgroups [0, col_wgs) come first, so that they start before
+// the row workgroups: for blockwise scales they compute the per-column power
+// of two the wide kernel stages B with, 2^e with max_b |s[b, j]| / 2^e in
+// [0.5, 1) over all of K (e = 0 for an all-zero or non-finite maximum),
+// written as col_pow[j] = 2^e and col_pow[n + j] = 2^-e.  A column workgroup
+// takes 64 columns: 16 threads of float4 columns by 16 block groups, every
+// thread's scale loads in flight together (eight per batch).
 constexpr int kSplitHeld = 3;   // k <= 6144 in one read
+constexpr int kPrepCols = 64;   // columns per column workgroup
 
 template <bool FRAG>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict__ a, _Float16* __restrict__ ah,
                                                         int* __restrict__ row_exp, int m, int k, int vec,
                                                         const float* __restrict__ scale, float* __restrict__ col_pow,
-                                                        int n, int nblk) {
+                                                        int n, int nblk, int col_wgs) {
     __shared__ float wmax[4 * 256];
     const int tid = threadIdx.x;
-    if (static_cast<int>(blockIdx.x) >= m) {
-        const int j0 = (static_cast<int>(blockIdx.x) - m) * 256 + 4 * (tid & 63);
-        const int bg = tid >> 6;
+    if (static_cast<int>(blockIdx.x) < col_wgs) {
+        const int j0 = static_cast<int>(blockIdx.x) * kPrepCols + 4 * (tid & 15);
+        const int bg = tid >> 4;
         float mx[4] = {0.f, 0.f, 0.f, 0.f};
         if (j0 < n) {
-            for (int b = bg; b < nblk; b += 4 * 4) {
-                float4 v[4];
+            constexpr int kBatch = 8;
+            for (int b0 = bg; b0 < nblk; b0 += 16 * kBatch) {
+                float4 v[kBatch];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int bb = b + 4 * u;
+                for (int u = 0; u < kBatch; ++u) {
+                    const int bb = b0 + 16 * u;
                     v[u] = bb < nblk ? *reinterpret_cast<const float4*>(scale + static_cast<int64_t>(bb) * n + j0)
                                      : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < kBatch; ++u) {
                     mx[0] = fmaxf(mx[0], fabsf(v[u].x));
                     mx[1] = fmaxf(mx[1], fabsf(v[u].y));
                     mx[2] = fmaxf(mx[2], fabsf(v[u].z));
@@ -592,11 +597,12 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
             }
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) wmax[bg * 256 + 4 * (tid & 63) + e] = mx[e];
+        for (int e = 0; e < 4; ++e) wmax[bg * kPrepCols + 4 * (tid & 15) + e] = mx[e];
         __syncthreads();
-        const int j = (static_cast<int>(blockIdx.x) - m) * 256 + tid;
-        if (j < n) {
-            float mm = fmaxf(fmaxf(wmax[tid], wmax[256 + tid]), fmaxf(wmax[512 + tid], wmax[768 + tid]));
+        const int j = static_cast<int>(blockIdx.x) * kPrepCols + tid;
+        if (tid < kPrepCols && j < n) {
+            float mm = 0.0f;
+            for (int g = 0; g < 16; ++g) mm = fmaxf(mm, wmax[g * kPrepCols + tid]);
             int e = 0;
             if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
             col_pow[j] = ldexpf(1.0f, e);
@@ -604,7 +610,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
         }
         return;
     }
-    const int row = blockIdx.x;
+    const int row = static_cast<int>(blockIdx.x) - col_wgs;
     const float* src = a + static_cast<int64_t>(row) * k;
     const int groups = k >> 3;   // k % 32 == 0 on this path
     const bool held = groups <= kSplitHeld * 256;
@@ -1357,6 +1363,7 @@ WideConfig choose_wide(int kind, int m, int k, int n) {
         const int got = std::sscanf(env, "%d,%d,%d,%d,%d", &bm, &bn, &sx, &d, &g);
         const bool known = (bm == 128 && bn == 128 && ((d == 2 && (g == 1 || g == 2)) || (d == 4 && g == 1))) ||
                            (bm == 128 && bn == 64 && d == 2 && (g == 1 || g == 2)) ||
+
                            (bm == 64 && bn == 128 && (d == 2 || d == 4) && g == 1) ||
                            (bm == 64 && bn == 256 && d == 2 && g == 1);
         if (got >= 4 && sx >= 1 && sx <= kMaxSplits && known) {
@@ -1476,17 +1483,17 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
     auto* col_pow = col_exps ? reinterpret_cast<float*>(static_cast<char*>(aux) + half_bytes + exp_bytes) : nullptr;
     const int vec = reinterpret_cast<uintptr_t>(a) % 16 == 0 ? 1 : 0;
     const int nblk = kind == 0 ? 1 : (k + block_size - 1) / block_size;
-    const int col_wgs = col_exps ? (n + 255) / 256 : 0;
+    const int col_wgs = col_exps ? (n + kPrepCols - 1) / kPrepCols : 0;
     if (use_wide) {
         hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(m + col_wgs), dim3(256), 0, stream, a, ah, row_exp, m, k, vec,
-                           scale, col_pow, n, nblk);
+                           scale, col_pow, n, nblk, col_wgs);
         VM_TRY(check_launch("QuantizedMatMul", stream));
         if (kind == 2) return launch_wide_kind<2>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
         if (kind == 1) return launch_wide_kind<1>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
         return launch_wide_kind<0>(ah, row_exp, col_pow, wq, scale, c, m, k, n, 0, stream);
     }
     hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k, vec, scale,
-                       col_pow, n, nblk);
+                       col_pow, n, nblk, 0);
     VM_TRY(check_launch("QuantizedMatMul", stream));
     if (kind == 2) return launch_kind<2>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
     if (kind == 1) return launch_kind<1>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
