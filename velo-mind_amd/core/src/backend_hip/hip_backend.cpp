@@ -1,11 +1,32 @@
-// DeviceType::HIP registration: storage creator (one vm_hip_malloc per
+// DeviceType::HIP registration: storage creator (one device block per
 // storage, so a graph's arena is a single device allocation), synchronous
 // transfers on the thread's current stream, availability, and the
 // execution context (one non-blocking stream per Executable, made current
 // on the executing thread and synchronized at the end of execute()).
 // Replaces the reference's src/cuda/storage.cu and cuda_context.{h,cu}.
+//
+// The reference's engine builds a new Graph for every call
+// (llama_engine.cpp:395-455), so a decode token allocates and frees the
+// arena, the inputs and every layer's grown K/V cache, and creates and
+// destroys the Executable's stream.  On HIP those calls cost more than the
+// token's kernels (hipFree synchronizes the device; a stream creation
+// takes ~0.7 ms), so the backend keeps them:
+//   * storages come from a per-device block cache in size classes (eight
+//     per power of two, so a K/V cache that grows by a row usually keeps
+//     its class).  A freed block is parked, and becomes reusable only after
+//     a device-wide synchronization that began after it was freed -- the
+//     guarantee hipFree gives -- which the allocator performs itself when a
+//     request finds only parked blocks of its class;
+//   * Executable streams come from a per-device pool and return to it
+//     (synchronized) when the Executable is destroyed, keeping the
+//     stream's split-K and staging workspaces;
+//   * the device count is read once per process.
+#include <algorithm>
+#include <map>
 #include <memory>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "backend_hip/hip_runtime.h"
 #include "internal/registry/device_context.h"
@@ -18,30 +39,139 @@ namespace {
 
 thread_local void* t_current_stream = nullptr;
 
-struct HipContext {
-    void* stream = nullptr;
-    ~HipContext() {
-        if (stream) (void)vm_hip_stream_destroy(stream);
+int current_device_or_zero() {
+    int d = 0;
+    return vm_hip_get_device(&d) == VM_HIP_OK ? d : 0;
+}
+
+// ---- storage block cache
+constexpr std::size_t kMinClass = 256;
+constexpr std::size_t kMaxCachedBytes = std::size_t(8) << 30;   // parked + free, per process
+
+// Size class of a request: 256-byte multiples up to 2 KiB, then eight
+// classes per power of two.
+std::size_t size_class(std::size_t bytes) {
+    if (bytes <= 8 * kMinClass) return (bytes + kMinClass - 1) / kMinClass * kMinClass;
+    std::size_t p = 1;
+    while (p * 2 <= bytes) p *= 2;   // p <= bytes < 2p
+    const std::size_t step = p / 8;
+    return (bytes + step - 1) / step * step;
+}
+
+struct BlockCache {
+    struct PerDevice {
+        std::map<std::size_t, std::vector<void*>> ready;    // idle: reusable now
+        std::map<std::size_t, std::vector<void*>> parked;   // freed since the last device synchronization
+        std::size_t parked_count = 0;
+    };
+    std::mutex mu;
+    std::map<int, PerDevice> dev;
+    std::size_t cached_bytes = 0;
+
+    static BlockCache& get() {
+        static BlockCache* c = new BlockCache();   // outlives every storage (never destroyed)
+        return *c;
+    }
+
+    void* take(int d, std::size_t cls) {
+        std::lock_guard<std::mutex> lock(mu);
+        PerDevice& pd = dev[d];
+        auto it = pd.ready.find(cls);
+        if (it == pd.ready.end() || it->second.empty()) {
+            auto pk = pd.parked.find(cls);
+            if (pk == pd.parked.end() || pk->second.empty()) return nullptr;
+            // every parked block of this device becomes idle once the
+            // device has drained
+            if (vm_hip_device_synchronize() != VM_HIP_OK) return nullptr;
+            for (auto& [c, v] : pd.parked) {
+                auto& r = pd.ready[c];
+                r.insert(r.end(), v.begin(), v.end());
+            }
+            pd.parked.clear();
+            pd.parked_count = 0;
+            it = pd.ready.find(cls);
+        }
+        void* p = it->second.back();
+        it->second.pop_back();
+        cached_bytes -= cls;
+        return p;
+    }
+
+    // false: the cache is full, the caller frees the block itself
+    bool park(int d, std::size_t cls, void* p) {
+        std::lock_guard<std::mutex> lock(mu);
+        if (cached_bytes + cls > kMaxCachedBytes) return false;
+        PerDevice& pd = dev[d];
+        pd.parked[cls].push_back(p);
+        ++pd.parked_count;
+        cached_bytes += cls;
+        return true;
     }
 };
 
 std::shared_ptr<TensorStorage> hip_allocate(std::size_t bytes) {
-    void* dev = nullptr;
-    if (bytes > 0) {
-        const int rc = vm_hip_malloc(&dev, bytes);
-        if (rc != VM_HIP_OK) throw std::runtime_error(vm_hip_last_error());
+    void* block = nullptr;
+    const std::size_t cls = bytes > 0 ? size_class(bytes) : 0;
+    const int d = current_device_or_zero();
+    if (cls > 0) {
+        block = BlockCache::get().take(d, cls);
+        if (!block) {
+            const int rc = vm_hip_malloc(&block, cls);
+            if (rc != VM_HIP_OK) throw std::runtime_error(vm_hip_last_error());
+        }
     }
     // The deleter keeps the original pointer: bind_input may rebind data.
-    auto s = std::shared_ptr<TensorStorage>(new TensorStorage{}, [dev](TensorStorage* p) {
-        if (dev) (void)vm_hip_free(dev);
+    auto s = std::shared_ptr<TensorStorage>(new TensorStorage{}, [block, cls, d](TensorStorage* p) {
+        if (block && !BlockCache::get().park(d, cls, block)) (void)vm_hip_free(block);
         delete p;
     });
     s->size_bytes = bytes;
-    s->capacity_bytes = bytes;
+    s->capacity_bytes = cls;
     s->device = DeviceType::HIP;
-    s->data = dev;
+    s->data = block;
     return s;
 }
+
+// ---- Executable streams
+struct StreamPool {
+    std::mutex mu;
+    std::map<int, std::vector<void*>> idle;
+    static StreamPool& get() {
+        static StreamPool* p = new StreamPool();   // pooled streams live until the process ends
+        return *p;
+    }
+    void* take(int d) {
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            auto& v = idle[d];
+            if (!v.empty()) {
+                void* s = v.back();
+                v.pop_back();
+                return s;
+            }
+        }
+        void* s = nullptr;
+        const int rc = vm_hip_stream_create(&s);
+        if (rc != VM_HIP_OK) throw std::runtime_error(std::string("HIP context: ") + vm_hip_last_error());
+        return s;
+    }
+    void give(int d, void* s) {
+        if (vm_hip_stream_synchronize(s) != VM_HIP_OK) {
+            (void)vm_hip_stream_destroy(s);
+            return;
+        }
+        std::lock_guard<std::mutex> lock(mu);
+        idle[d].push_back(s);
+    }
+};
+
+struct HipContext {
+    void* stream = nullptr;
+    int device = 0;
+    ~HipContext() {
+        if (stream) StreamPool::get().give(device, stream);
+    }
+};
 
 void hip_h2d(void* dst, const void* src, std::size_t bytes) {
     const int rc = vm_hip_memcpy_h2d(dst, src, bytes, t_current_stream);
@@ -54,14 +184,17 @@ void hip_d2h(void* dst, const void* src, std::size_t bytes) {
 }
 
 bool hip_available() noexcept {
-    int n = 0;
-    return vm_hip_device_count(&n) == VM_HIP_OK && n > 0;
+    static const bool available = [] {
+        int n = 0;
+        return vm_hip_device_count(&n) == VM_HIP_OK && n > 0;
+    }();
+    return available;
 }
 
 std::shared_ptr<void> context_create() {
     auto ctx = std::make_shared<HipContext>();
-    const int rc = vm_hip_stream_create(&ctx->stream);
-    if (rc != VM_HIP_OK) throw std::runtime_error(std::string("HIP context: ") + vm_hip_last_error());
+    ctx->device = current_device_or_zero();
+    ctx->stream = StreamPool::get().take(ctx->device);
     return ctx;
 }
 
