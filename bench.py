@@ -59,6 +59,7 @@ Prints one JSON line.  Only --gpus 1 is supported (one GPU per box).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -484,6 +485,27 @@ def decode_trace_report(tokens: int = 8) -> dict:
             "argmax_us": round(float(us[0, L, 4] - np.median(us[:, L, 2])), 2)}
 
 
+def handoff_probe(H, stream, rounds: int = 2000) -> list:
+    """The platform diagnostic behind the one-launch decode step's limits
+    (vm_hip_diag_handoff): microseconds per all-to-all hand-off of tagged
+    words between workgroups (one per compute unit), alone, beside compute
+    units streaming HBM, after each workgroup streams a share of its own,
+    and with streaming waves on the same compute units."""
+    lib = H.open_library()
+    cases = [(0, 32, 0), (0, 128, 0), (0, 256, 0), (1, 224, 0), (1, 192, 0), (1, 128, 0),
+             (2, 256, 8), (2, 256, 16), (2, 256, 32), (2, 256, 64), (3, 256, 1), (3, 256, 2), (3, 256, 4)]
+    names = {0: "alone", 1: "other CUs stream HBM", 2: "each workgroup first streams kb KiB",
+             3: "kb waves of each workgroup stream HBM"}
+    out = []
+    for mode, parts, kb in cases:
+        us, gbs = ctypes.c_double(0.0), ctypes.c_double(0.0)
+        H.check(lib.vm_hip_diag_handoff(mode, parts, kb, rounds, ctypes.byref(us), ctypes.byref(gbs), stream.handle))
+        out.append({"mode": names[mode], "participants": parts, "kb": kb, "us_per_handoff": round(us.value, 3),
+                    "stream_GB_s": round(gbs.value, 1)})
+        log(f"bench: hand-off {names[mode]} P={parts} kb={kb}: {us.value:.3f} us, streaming {gbs.value:.0f} GB/s")
+    return out
+
+
 GEMM_K, GEMM_N = 2048, 5632
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -699,9 +721,15 @@ def main() -> int:
                     help="with --e2e-only: only this model")
     ap.add_argument("--e2e-steps", type=int, default=0,
                     help="with --e2e-only: decode this many tokens instead of the config's (short profiling runs)")
+    ap.add_argument("--e2e-layers", default="",
+                    help="with --e2e-only and --e2e-model: comma-separated layer counts to run instead of the "
+                         "config's (per-layer decode time with the weights resident in the 256 MB Infinity Cache "
+                         "at few layers, streamed from HBM at many)")
     ap.add_argument("--decode-trace", action="store_true",
                     help="only the one-launch decode step's phase timestamps (library built with "
                          "VELOMIND_DECODE_TRACE=1), printed as one JSON line")
+    ap.add_argument("--handoff-probe", action="store_true",
+                    help="only the platform hand-off diagnostic (vm_hip_diag_handoff), printed as one JSON line")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg (config 3)")
     ap.add_argument("--no-large", action="store_true", help="skip the 70B-class decode GEMV leg")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg, printed as one JSON line")
@@ -742,8 +770,29 @@ def main() -> int:
     if args.decode_trace:
         print(json.dumps({"metric": METRIC, "decode_trace": decode_trace_report()}), flush=True)
         return 0
+    if args.handoff_probe:
+        print(json.dumps({"metric": METRIC, "handoff_probe": handoff_probe(H, stream)}), flush=True)
+        return 0
     if args.gemm_only:
         print(json.dumps({"metric": METRIC, "gemm": gemm_bench(H, stream)}), flush=True)
+        return 0
+    if args.e2e_only and args.e2e_layers:
+        if not args.e2e_model:
+            log("bench: --e2e-layers needs --e2e-model")
+            return 2
+        base = E2E_MODELS[args.e2e_model]
+        rows = []
+        for layers in (int(v) for v in args.e2e_layers.split(",")):
+            name = f"{args.e2e_model}_{layers}_layers"
+            E2E_MODELS[name] = dict(base, cfg=dict(base["cfg"], num_layers=layers))
+            wb = decode_weight_bytes(E2E_MODELS[name]["cfg"], base["quant"], base["block"])
+            for persistent in (False, True):
+                r = e2e_bench(name, persistent=persistent, steps=args.e2e_steps or 48)
+                rows.append({"layers": layers, "decode_path": r["decode_path"], "weight_MB_per_token": round(wb / 1e6, 1),
+                             "decode_us_per_token": r["decode_us_per_token"],
+                             "us_per_layer": round(r["decode_us_per_token"] / layers, 2)})
+                log(f"bench: {name} {r['decode_path']}: {r['decode_us_per_token']} us/token")
+        print(json.dumps({"metric": METRIC, "e2e_layers": rows}), flush=True)
         return 0
     if args.e2e_only:
         e2e = {}

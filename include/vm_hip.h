@@ -584,6 +584,23 @@ int vm_hip_decode_status(void* workspace, int* failed, void* stream);
  * compiles them in; VM_HIP_EUNSUPPORTED otherwise. */
 int vm_hip_decode_trace_read(void* host, int64_t bytes);
 
+/* ---- Platform diagnostic (no reference counterpart) --------------------
+ * The cost of an all-to-all hand-off inside one launch, the primitive a
+ * one-launch decode step is built from (diag_handoff.hip): `participants`
+ * workgroups, one per compute unit, each store 8 tagged 64-bit words per
+ * round and poll everyone's words at agent scope.  Modes: ALONE; STREAM_CUS
+ * (the other compute units stream HBM meanwhile); STREAM_FIRST (each
+ * participant first streams `kb` KiB, then polls); STREAM_WAVES (`kb` = 1..4
+ * extra waves of each participant stream HBM continuously).  Writes
+ * microseconds per round (slowest participant) and the GB/s the streaming
+ * loads reached; allocates 1 GiB for the duration of the call. */
+#define VM_HIP_DIAG_ALONE        0
+#define VM_HIP_DIAG_STREAM_CUS   1
+#define VM_HIP_DIAG_STREAM_FIRST 2
+#define VM_HIP_DIAG_STREAM_WAVES 3
+int vm_hip_diag_handoff(int mode, int participants, int kb, int rounds, double* us_per_round, double* stream_gb_s,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,11 +4,13 @@
 // (:140-207 numerics, :310-374 cross-backend, :376-411 storage sizes,
 // :448-469 half-precision sources) and the concurrent build/execute stress
 // of tests/test_coverage_matrix.cpp:690-738.
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <stdexcept>
 #include <thread>
 
+#include "internal/registry/storage.h"
 #include "test_helpers.h"
 
 using namespace velomind;
@@ -231,6 +233,63 @@ TEST_CASE("HIP graph memory plan uses one device arena", "[gpu][memory]") {
     std::vector<float> out(256);
     h.copy_to_host(as_writeable_bytes(out));
     REQUIRE(max_abs_diff(out, xv) <= 1e-5f * max_abs(xv));
+}
+
+TEST_CASE("HIP storages of a rebuilt graph come from the block cache", "[gpu][memory]") {
+    REQUIRE_HIP();
+    // The reference engine rebuilds its graph per call: the second build
+    // of the same graph allocates from the blocks the first one freed and
+    // gives identical results.
+    const std::size_t k = 256;
+    const auto w = normal(k * k, 31, 0.02f);
+    std::vector<std::int8_t> q(k * k);
+    std::vector<float> s(k);
+    vmo_quantize_int8_per_channel(w.data(), q.data(), s.data(), k, k);
+    const auto a = normal(k, 32);
+    auto run = [&]() {
+        Graph g;
+        auto x = g.input({1, (dim_t)k}, DataType::Float32);
+        auto tw = g.input({(dim_t)k, (dim_t)k}, DataType::Int8);
+        auto ts = g.input({(dim_t)k}, DataType::Float32);
+        auto h = g.op(Op::QuantizedMatMul, x, tw, ts);
+        auto y = g.op(Op::QuantizedMatMul, h, tw, ts);
+        g.mark_output(y);
+        auto exec = g.build(DeviceType::HIP);
+        x.copy_from_host(as_bytes(a));
+        tw.copy_from_host(as_bytes(q));
+        ts.copy_from_host(as_bytes(s));
+        exec->execute();
+        REQUIRE(y.capacity_bytes() >= y.nbytes());
+        std::vector<float> out(k);
+        y.copy_to_host(as_writeable_bytes(out));
+        return out;
+    };
+    const auto o1 = run();
+    const auto o2 = run();
+    REQUIRE(std::memcmp(o1.data(), o2.data(), k * 4) == 0);
+    std::vector<float> h(k), ref(k);
+    vmo_qmm_2d_f32(a.data(), q.data(), s.data(), h.data(), 1, k, k, 1, 0);
+    vmo_qmm_2d_f32(h.data(), q.data(), s.data(), ref.data(), 1, k, k, 1, 0);
+    REQUIRE(max_abs_diff(o1, ref) <= 1e-5f * max_abs(ref));
+
+    // A freed block returns for the next request of its size class (a
+    // size no other test uses, so the class holds only this block), also
+    // for a request one K/V row larger; its contents survive the round trip.
+    const std::size_t bytes = 7654321;
+    auto st = internal::create_tensor_storage(bytes, DeviceType::HIP);
+    REQUIRE(st->capacity_bytes >= bytes);
+    const void* p = st->data;
+    std::vector<std::uint8_t> pattern(bytes), back(bytes);
+    for (std::size_t i = 0; i < bytes; ++i) pattern[i] = static_cast<std::uint8_t>(i * 7 + 3);
+    REQUIRE(vm_hip_memcpy_h2d(st->data, pattern.data(), bytes, nullptr) == 0);
+    st.reset();
+    auto again = internal::create_tensor_storage(bytes + 256, DeviceType::HIP);
+    REQUIRE(again->data == p);
+    REQUIRE(again->size_bytes == bytes + 256);
+    REQUIRE(vm_hip_memcpy_d2h(back.data(), again->data, bytes, nullptr) == 0);
+    REQUIRE(back == pattern);
+    auto other = internal::create_tensor_storage(bytes, DeviceType::HIP);   // the class is empty again
+    REQUIRE(other->data != p);
 }
 
 TEST_CASE("bind_input uses an external device buffer", "[gpu][api]") {

@@ -121,6 +121,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_attention_decode_slices_prefetch_f32": ([p, c_int64, p, c_int64, c_float, c_float, p, p, p, p, p, p,
                                                          c_int64, c_int64, c_int64, c_int64, c_float,
                                                          POINTER(Prefetch), p], c_int),
+        "vm_hip_diag_handoff": ([c_int, c_int, c_int, c_int, POINTER(ctypes.c_double), POINTER(ctypes.c_double), p],
+                                c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -149,7 +151,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_qmm_gemv_slices_src_f32", "vm_hip_attention_decode_chunks", "vm_hip_attention_decode_slices_f32",
             "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32",
             "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32", "vm_hip_decode_workspace_bytes",
-            "vm_hip_decode_step", "vm_hip_decode_status", "vm_hip_decode_trace_read"]
+            "vm_hip_decode_step", "vm_hip_decode_status", "vm_hip_decode_trace_read", "vm_hip_diag_handoff"]
 
 
 def open_library() -> ctypes.CDLL:
