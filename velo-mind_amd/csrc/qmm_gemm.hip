@@ -566,6 +566,77 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 constexpr int kSplitHeld = 3;   // k <= 6144 in one read
 constexpr int kPrepCols = 64;   // columns per column workgroup
 
+// Column workgroup `cw` of the prep: the per-column powers of two of 64
+// columns (16 threads of float4 columns by 16 block groups, every scale
+// load of a thread in flight together, eight per batch).
+__device__ void prep_col_pow(const float* __restrict__ scale, float* __restrict__ col_pow, int n, int nblk, int cw,
+                             float* wmax) {
+    const int tid = threadIdx.x;
+    const int j0 = cw * kPrepCols + 4 * (tid & 15);
+    const int bg = tid >> 4;
+    float mx[4] = {0.f, 0.f, 0.f, 0.f};
+    if (j0 < n) {
+        constexpr int kBatch = 8;
+        for (int b0 = bg; b0 < nblk; b0 += 16 * kBatch) {
+            float4 v[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int bb = b0 + 16 * u;
+                v[u] = bb < nblk ? *reinterpret_cast<const float4*>(scale + static_cast<int64_t>(bb) * n + j0)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                mx[0] = fmaxf(mx[0], fabsf(v[u].x));
+                mx[1] = fmaxf(mx[1], fabsf(v[u].y));
+                mx[2] = fmaxf(mx[2], fabsf(v[u].z));
+                mx[3] = fmaxf(mx[3], fabsf(v[u].w));
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wmax[bg * kPrepCols + 4 * (tid & 15) + e] = mx[e];
+    __syncthreads();
+    const int j = cw * kPrepCols + tid;
+    if (tid < kPrepCols && j < n) {
+        float mm = 0.0f;
+        for (int g = 0; g < 16; ++g) mm = fmaxf(mm, wmax[g * kPrepCols + tid]);
+        int e = 0;
+        if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
+        col_pow[j] = ldexpf(1.0f, e);
+        col_pow[n + j] = ldexpf(1.0f, -e);
+    }
+}
+
+// hi = fp16(a 2^x), lo = fp16(a 2^x - hi) of one 8-group, position i
+// holding k = i (row-major) or k = i / 2 + 4 (i % 2) (operand order); an
+// infinite part (|a| beyond fp16 in an unscaled row) leaves lo at 0.
+template <bool FRAG>
+__device__ __forceinline__ void split8(const float4& p, const float4& q, int x, half8v& h, half8v& l) {
+    const float s[8] = {ldexpf(p.x, x), ldexpf(p.y, x), ldexpf(p.z, x), ldexpf(p.w, x),
+                        ldexpf(q.x, x), ldexpf(q.y, x), ldexpf(q.z, x), ldexpf(q.w, x)};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int kk = FRAG ? (i >> 1) + 4 * (i & 1) : i;
+        const _Float16 hh = static_cast<_Float16>(s[kk]);
+        const float d = s[kk] - static_cast<float>(hh);
+        h[i] = hh;
+        l[i] = static_cast<_Float16>(d == d && fabsf(d) <= 65504.0f ? d : 0.0f);
+    }
+}
+
+// The row exponent x of a row with largest magnitude mx (x = 0 when the
+// row holds an infinity or NaN, or is all zeros): 2^x mx in [2^14, 2^15).
+__device__ __forceinline__ int row_exponent(float mx) {
+    int x = 0;
+    if (mx > 0.0f && mx <= 3.4028235e38f) {
+        int e = 0;
+        (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
+        x = 15 - e;
+    }
+    return x;
+}
+
 template <bool FRAG>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict__ a, _Float16* __restrict__ ah,
                                                         int* __restrict__ row_exp, int m, int k, int vec,
@@ -574,40 +645,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
     __shared__ float wmax[4 * 256];
     const int tid = threadIdx.x;
     if (static_cast<int>(blockIdx.x) < col_wgs) {
-        const int j0 = static_cast<int>(blockIdx.x) * kPrepCols + 4 * (tid & 15);
-        const int bg = tid >> 4;
-        float mx[4] = {0.f, 0.f, 0.f, 0.f};
-        if (j0 < n) {
-            constexpr int kBatch = 8;
-            for (int b0 = bg; b0 < nblk; b0 += 16 * kBatch) {
-                float4 v[kBatch];
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const int bb = b0 + 16 * u;
-                    v[u] = bb < nblk ? *reinterpret_cast<const float4*>(scale + static_cast<int64_t>(bb) * n + j0)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-#pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    mx[0] = fmaxf(mx[0], fabsf(v[u].x));
-                    mx[1] = fmaxf(mx[1], fabsf(v[u].y));
-                    mx[2] = fmaxf(mx[2], fabsf(v[u].z));
-                    mx[3] = fmaxf(mx[3], fabsf(v[u].w));
-                }
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wmax[bg * kPrepCols + 4 * (tid & 15) + e] = mx[e];
-        __syncthreads();
-        const int j = static_cast<int>(blockIdx.x) * kPrepCols + tid;
-        if (tid < kPrepCols && j < n) {
-            float mm = 0.0f;
-            for (int g = 0; g < 16; ++g) mm = fmaxf(mm, wmax[g * kPrepCols + tid]);
-            int e = 0;
-            if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
-            col_pow[j] = ldexpf(1.0f, e);
-            col_pow[n + j] = ldexpf(1.0f, -e);
-        }
+        prep_col_pow(scale, col_pow, n, nblk, static_cast<int>(blockIdx.x), wmax);
         return;
     }
     const int row = static_cast<int>(blockIdx.x) - col_wgs;
@@ -663,12 +701,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
     if ((tid & 63) == 0) wmax[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    int x = 0;
-    if (mx > 0.0f && mx <= 3.4028235e38f) {
-        int e = 0;
-        (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
-        x = 15 - e;
-    }
+    const int x = row_exponent(mx);
     if (tid == 0) row_exp[row] = x;
     const int64_t mp = FRAG ? (static_cast<int64_t>(m) + 31) / 32 * 32 : m;
     half8v* hi = reinterpret_cast<half8v*>(ah);
@@ -680,19 +713,8 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
         return static_cast<int64_t>(row) * (k / 8) + g;
     };
     auto split = [&](int g, const float4& p, const float4& q) {
-        const float s[8] = {ldexpf(p.x, x), ldexpf(p.y, x), ldexpf(p.z, x), ldexpf(p.w, x),
-                            ldexpf(q.x, x), ldexpf(q.y, x), ldexpf(q.z, x), ldexpf(q.w, x)};
         half8v h, l;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            // position i holds k = i (row-major) or k = i / 2 + 4 * (i % 2) (FRAG)
-            const int kk = FRAG ? (i >> 1) + 4 * (i & 1) : i;
-            const _Float16 hh = static_cast<_Float16>(s[kk]);
-            // an infinite part (|a| beyond fp16 in an unscaled row) leaves lo at 0
-            const float d = s[kk] - static_cast<float>(hh);
-            h[i] = hh;
-            l[i] = static_cast<_Float16>(d == d && fabsf(d) <= 65504.0f ? d : 0.0f);
-        }
+        split8<FRAG>(p, q, x, h, l);
         hi[piece(g)] = h;
         lo[piece(g)] = l;
     };
@@ -707,6 +729,101 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
             float4 p, q;
             load8(g, p, q);
             split(g, p, q);
+        }
+    }
+}
+
+
+// The wide kernel's prep for k <= 6144 (GT = ceil(k / 2048) groups of
+// eight per thread and row): R = 8 / GT rows per workgroup, held in
+// registers between their maxima and their split.  Operand order puts 32
+// rows side by side in every 1 KB piece, so one row alone writes 16 bytes
+// per 512-byte half-piece; R consecutive rows give each thread an R x
+// 16-byte run.  Column workgroups as in gemm_prep_kernel.
+template <int R, int GT>
+__global__ __launch_bounds__(256) void gemm_prep_frag_kernel(const float* __restrict__ a, _Float16* __restrict__ ah,
+                                                             int* __restrict__ row_exp, int m, int k, int vec,
+                                                             const float* __restrict__ scale,
+                                                             float* __restrict__ col_pow, int n, int nblk,
+                                                             int col_wgs) {
+    __shared__ float wmax[4 * 256];
+    const int tid = threadIdx.x;
+    if (static_cast<int>(blockIdx.x) < col_wgs) {
+        prep_col_pow(scale, col_pow, n, nblk, static_cast<int>(blockIdx.x), wmax);
+        return;
+    }
+    const int row0 = (static_cast<int>(blockIdx.x) - col_wgs) * R;
+    const int groups = k >> 3;
+    float4 v[R][GT][2];
+    float mx[R];
+    bool special[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float* src = a + static_cast<int64_t>(row0 + r) * k;
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            const int g = tid + u * 256;
+            if (row0 + r < m && g < groups) {
+                if (vec) {
+                    v[r][u][0] = reinterpret_cast<const float4*>(src)[2 * g];
+                    v[r][u][1] = reinterpret_cast<const float4*>(src)[2 * g + 1];
+                } else {
+                    const float* s8 = src + 8 * g;
+                    v[r][u][0] = make_float4(s8[0], s8[1], s8[2], s8[3]);
+                    v[r][u][1] = make_float4(s8[4], s8[5], s8[6], s8[7]);
+                }
+            } else {
+                v[r][u][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+                v[r][u][1] = v[r][u][0];
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        mx[r] = 0.0f;
+        special[r] = false;
+#pragma unroll
+        for (int u = 0; u < GT; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float4 x = v[r][u][h];
+                mx[r] = fmaxf(mx[r], fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+                special[r] = special[r] || !(fabsf(x.x) <= 3.4028235e38f) || !(fabsf(x.y) <= 3.4028235e38f) ||
+                             !(fabsf(x.z) <= 3.4028235e38f) || !(fabsf(x.w) <= 3.4028235e38f);
+            }
+        // an infinity or NaN anywhere in the row disables the scaling
+        if (special[r]) mx[r] = __builtin_inff();
+        for (int off = 32; off > 0; off >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off));
+    }
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int r = 0; r < R; ++r) wmax[(tid >> 6) * R + r] = mx[r];
+    __syncthreads();
+    int x[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        x[r] = row_exponent(fmaxf(fmaxf(wmax[r], wmax[R + r]), fmaxf(wmax[2 * R + r], wmax[3 * R + r])));
+    if (tid < R && row0 + tid < m) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (r == tid) row_exp[row0 + r] = x[r];
+    }
+    const int64_t mp = (static_cast<int64_t>(m) + 31) / 32 * 32;
+    half8v* hi = reinterpret_cast<half8v*>(ah);
+    half8v* lo = reinterpret_cast<half8v*>(ah + mp * k);
+#pragma unroll
+    for (int u = 0; u < GT; ++u) {
+        const int g = tid + u * 256;
+        if (g >= groups) break;
+        // rows row0 .. row0 + R - 1 (one 32-row block) are consecutive 16-byte pieces
+        const int64_t base = (static_cast<int64_t>(row0 / 32) * (k / 16) + g / 2) * 64 + row0 % 32 + 32 * (g % 2);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (row0 + r >= m) break;
+            half8v h, l;
+            split8<true>(v[r][u][0], v[r][u][1], x[r], h, l);
+            hi[base + r] = h;
+            lo[base + r] = l;
         }
     }
 }
@@ -1447,6 +1564,21 @@ int launch_wide_kind(const _Float16* a, const int* row_exp, const float* col_pow
 
 }  // namespace
 
+// Rows per workgroup of the operand-order prep: the most (up to 8 / GT,
+// a power of two) that still leave at least kPrepMinWgs row workgroups.
+// VELOMIND_PREP_MIN_WGS overrides the minimum (measurement sweeps).
+constexpr int kPrepMinWgs = 256;
+
+static int prep_rows_per_wg(int m, int gt) {
+    if (gt > 3) return 0;
+    int min_wgs = kPrepMinWgs;
+    if (const char* env = std::getenv("VELOMIND_PREP_MIN_WGS")) min_wgs = std::max(0, std::atoi(env));
+    int r = 8 / gt;
+    if (r == 8 / 3) r = 2;
+    while (r > 1 && (m + r - 1) / r < min_wgs) r /= 2;
+    return r;
+}
+
 int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
                  int quant_type, int block_size, hipStream_t stream) {
     // 64-row steps may end half-way (k % 32 == 0); 16-byte code pieces need
@@ -1485,8 +1617,18 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
     const int nblk = kind == 0 ? 1 : (k + block_size - 1) / block_size;
     const int col_wgs = col_exps ? (n + kPrepCols - 1) / kPrepCols : 0;
     if (use_wide) {
-        hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(m + col_wgs), dim3(256), 0, stream, a, ah, row_exp, m, k, vec,
-                           scale, col_pow, n, nblk, col_wgs);
+        const int gt = (k / 8 + 255) / 256;
+        const int rows_per_wg = prep_rows_per_wg(m, gt);
+#define VM_PREP(RX, GX)                                                                                           \
+    if (gt == GX && rows_per_wg == RX)                                                                            \
+        hipLaunchKernelGGL((gemm_prep_frag_kernel<RX, GX>), dim3(col_wgs + (m + RX - 1) / RX), dim3(256), 0,     \
+                           stream, a, ah, row_exp, m, k, vec, scale, col_pow, n, nblk, col_wgs);                  \
+    else
+        VM_PREP(8, 1) VM_PREP(4, 1) VM_PREP(2, 1) VM_PREP(1, 1) VM_PREP(4, 2) VM_PREP(2, 2) VM_PREP(1, 2)
+        VM_PREP(2, 3) VM_PREP(1, 3)
+#undef VM_PREP
+            hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(m + col_wgs), dim3(256), 0, stream, a, ah, row_exp, m, k,
+                               vec, scale, col_pow, n, nblk, col_wgs);
         VM_TRY(check_launch("QuantizedMatMul", stream));
         if (kind == 2) return launch_wide_kind<2>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
         if (kind == 1) return launch_wide_kind<1>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
