@@ -55,9 +55,11 @@ struct DevBuf {
     T* as() const { return static_cast<T*>(p); }
 };
 
-// One packed linear [k, n].
+// One packed linear [k, n]; col_pow: the per-column powers of two of
+// blockwise scales that the wide prefill GEMM stages them with (computed
+// once, for prompts whose activations the producers stage themselves).
 struct Packed {
-    DevBuf codes, scales;
+    DevBuf codes, scales, col_pow;
     std::int64_t k = 0, n = 0;
 };
 
@@ -318,6 +320,78 @@ struct HipLlamaDecoder::Impl {
               "quantized matmul");
     }
 
+    // ---- prompts: activations staged for the GEMM by their producer
+    // (vm_hip_qmm_a_layout), instead of a pre-pass inside every GEMM call.
+    // VELOMIND_STAGE_A=0 keeps the fp32 hand-over (comparisons).
+    bool stage_a = true;
+    DevBuf a_stage;
+
+    void prepare_staging() {
+        const char* env = std::getenv("VELOMIND_STAGE_A");
+        stage_a = !(env && env[0] == '0');
+        if (qt != VM_HIP_QUANT_INT4) return;   // per-column INT8 scales need no column powers
+        auto powers = [&](Packed& w) {
+            if (w.n % 16 != 0 || block % 32 != 0) return;
+            w.col_pow = DevBuf(static_cast<std::size_t>(w.n) * 8);
+            check(vm_hip_qmm_col_pow(w.scales.as<float>(), w.col_pow.as<float>(), w.k, w.n, qt, block, stream),
+                  "column powers");
+        };
+        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+            powers(qkv[l]);
+            powers(o[l]);
+            powers(gate_up[l]);
+            powers(down[l]);
+        }
+    }
+
+    // The layout the GEMM of `w` takes its `rows`-row activations in
+    // (VM_HIP_A_FP32 when staging is off or does not apply).
+    int stage_layout(const Packed& w, std::int64_t rows) {
+        int lay = VM_HIP_A_FP32;
+        std::int64_t bytes = 0;
+        if (!stage_a || rows <= 4) return lay;
+        check(vm_hip_qmm_a_layout(rows, w.k, w.n, qt, block_arg(), &lay, &bytes), "activation layout");
+        if (lay != VM_HIP_A_FP32 && a_stage.bytes < static_cast<std::size_t>(bytes)) {
+            check(vm_hip_stream_synchronize(stream), "staging buffer");
+            a_stage = DevBuf(static_cast<std::size_t>(bytes));
+        }
+        return lay;
+    }
+
+    void qmm_staged(const Packed& w, float* c, std::int64_t rows) {
+        check(vm_hip_qmm_staged_f32(a_stage.p, w.col_pow.p ? w.col_pow.as<float>() : nullptr,
+                                    static_cast<const std::int8_t*>(w.codes.p), w.scales.as<float>(), c, rows, w.k,
+                                    w.n, qt, block_arg(), stream),
+              "quantized matmul (staged activations)");
+    }
+
+    // h += delta, RMSNorm with weight nw, then the projection `w` of it.
+    void norm_qmm(float* hp, const float* delta, const float* nw, const Packed& w, float* out, std::int64_t rows) {
+        const float eps = cfg.rms_norm_eps;
+        const int lay = stage_layout(w, rows);
+        if (lay == VM_HIP_A_FP32) {
+            check(vm_hip_add_rmsnorm_f32(hp, delta, nw, hn.as<float>(), rows, hidden, eps, stream), "add_rmsnorm");
+            qmm(hn.as<float>(), w, out, rows);
+            return;
+        }
+        check(vm_hip_add_rmsnorm_stage_f32(hp, delta, nw, a_stage.p, lay, nullptr, rows, hidden, eps, stream),
+              "add_rmsnorm (staged)");
+        qmm_staged(w, out, rows);
+    }
+
+    // SiLU(gate) * up of the gate|up output, then the down projection.
+    void silu_qmm(const float* gate_up_out, const Packed& w, float* out, std::int64_t rows) {
+        const int lay = stage_layout(w, rows);
+        if (lay == VM_HIP_A_FP32) {
+            check(vm_hip_silu_mul_f32(gate_up_out, act.as<float>(), rows, inter, stream), "silu_mul");
+            qmm(act.as<float>(), w, out, rows);
+            return;
+        }
+        check(vm_hip_silu_mul_stage_f32(gate_up_out, a_stage.p, lay, nullptr, rows, inter, stream),
+              "silu_mul (staged)");
+        qmm_staged(w, out, rows);
+    }
+
     // Layers over `rows` tokens whose first position is *pos; leaves the
     // last row's logits in `logits`.
     void forward(std::int64_t rows) {
@@ -329,10 +403,8 @@ struct HipLlamaDecoder::Impl {
                                    rows == 1 ? token.as<std::int32_t>() : idx.as<std::int32_t>(), rows, hp, stream),
               "embedding");
         for (std::size_t l = 0; l < cfg.num_layers; ++l) {
-            check(vm_hip_add_rmsnorm_f32(hp, l == 0 ? nullptr : down_out.as<float>(),
-                                         static_cast<const float*>(attn_norm[l]->data), hnp, rows, hidden, eps, stream),
-                  "add_rmsnorm");
-            qmm(hnp, qkv[l], qkv_out.as<float>(), rows);
+            norm_qmm(hp, l == 0 ? nullptr : down_out.as<float>(), static_cast<const float*>(attn_norm[l]->data),
+                     qkv[l], qkv_out.as<float>(), rows);
             check(vm_hip_rope_kv_append_f32(qkv_out.as<float>(), rows, cos_t.as<float>(), sin_t.as<float>(), posp,
                                             q.as<float>(), kc(l), vc(l), H, Hk, D,
                                             static_cast<std::int64_t>(max_seq), stream),
@@ -346,12 +418,9 @@ struct HipLlamaDecoder::Impl {
                                                    static_cast<std::int64_t>(max_seq), 1.0f, stream),
                       "attention_prefill");
             qmm(ctx.as<float>(), o[l], attn_out.as<float>(), rows);
-            check(vm_hip_add_rmsnorm_f32(hp, attn_out.as<float>(), static_cast<const float*>(ffn_norm[l]->data), hnp,
-                                         rows, hidden, eps, stream),
-                  "add_rmsnorm");
-            qmm(hnp, gate_up[l], gu.as<float>(), rows);
-            check(vm_hip_silu_mul_f32(gu.as<float>(), act.as<float>(), rows, inter, stream), "silu_mul");
-            qmm(act.as<float>(), down[l], down_out.as<float>(), rows);
+            norm_qmm(hp, attn_out.as<float>(), static_cast<const float*>(ffn_norm[l]->data), gate_up[l],
+                     gu.as<float>(), rows);
+            silu_qmm(gu.as<float>(), down[l], down_out.as<float>(), rows);
         }
         // Only the last row reaches the head (slice_last_token, llama_graph.cpp:141-158).
         const std::int64_t last = (rows - 1) * hidden;
@@ -528,6 +597,7 @@ HipLlamaDecoder::HipLlamaDecoder(const LlamaWeightSet& weights, QuantType quant_
     m.pack(m.lm_head, static_cast<const float*>(weights.storage(W::LmHead)->data), m.hidden, m.vocab);
 
     m.allocate();
+    m.prepare_staging();
     m.setup_persistent();
 }
 
@@ -554,6 +624,7 @@ HipLlamaDecoder::HipLlamaDecoder(const PackedLlamaWeights& packed, std::size_t m
     m.assemble(m.lm_head, {&packed.linear(W::LmHead)});
     check(vm_hip_stream_synchronize(m.stream), "assemble");
     m.allocate();
+    m.prepare_staging();
     m.setup_persistent();
 }
 

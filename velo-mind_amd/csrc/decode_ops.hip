@@ -19,7 +19,9 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <string>
 
+#include "a_split.h"
 #include "decode_attn.h"
 #include "vm_device.h"
 #include "vm_hip.h"
@@ -1138,6 +1140,196 @@ int prefetch_plan(const vm_hip_prefetch* in, vm_hip_prefetch* out, int* wgs) {
     return 0;
 }
 
+// ---- Producers that stage the prefill GEMM's activations (a_split.h) in
+// the same pass: add + RMSNorm (the GEMM input of q|k|v and gate|up) and
+// SiLU(g) * u (the down projection's input).  A workgroup takes R rows;
+// thread t holds the 8-groups t + 256 u (u < GT) of each row in registers,
+// so a row's largest magnitude is known before its parts are written.  In
+// operand order R consecutive rows are R consecutive 16-byte pieces of a
+// thread's stores.  `out_f32` (optional) also receives the fp32 rows.
+template <int R>
+__device__ __forceinline__ void block_reduce_rows(float (&v)[R], float (*part)[kT / 64], bool is_max) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(v[r], off, 64);
+            v[r] = is_max ? fmaxf(v[r], o) : v[r] + o;
+        }
+        if ((threadIdx.x & 63) == 0) part[r][threadIdx.x >> 6] = v[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float t = part[r][0];
+#pragma unroll
+        for (int i = 1; i < kT / 64; ++i) t = is_max ? fmaxf(t, part[r][i]) : t + part[r][i];
+        v[r] = t;
+    }
+    __syncthreads();
+}
+
+template <int GT, int R, bool PIECES>
+__device__ __forceinline__ void stage_rows(float4 (&y)[R][GT][2], int row0, int m, int k, _Float16* ah,
+                                           int* row_exp, int64_t half_elems, float* out_f32,
+                                           float (*part)[kT / 64]) {
+    const int groups = k / 8;
+    float mx[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        mx[r] = 0.0f;
+        bool special = false;
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            a_scan4(y[r][u][0], mx[r], special);
+            a_scan4(y[r][u][1], mx[r], special);
+        }
+        // an infinity or NaN anywhere in the row disables the scaling
+        if (special) mx[r] = __builtin_inff();
+    }
+    block_reduce_rows<R>(mx, part, true);
+    half8_t* hi = reinterpret_cast<half8_t*>(ah);
+    half8_t* lo = reinterpret_cast<half8_t*>(ah + half_elems);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        if (row >= m) break;
+        const int x = a_row_exponent(mx[r]);
+        if (threadIdx.x == 0) row_exp[row] = x;
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            const int g = static_cast<int>(threadIdx.x) + u * kT;
+            if (g >= groups) break;
+            half8_t h, l;
+            a_split8<PIECES>(y[r][u][0], y[r][u][1], x, h, l);
+            const int64_t pc = a_piece<PIECES>(row, g, k);
+            hi[pc] = h;
+            lo[pc] = l;
+            if (out_f32) {
+                float4* o = reinterpret_cast<float4*>(out_f32 + static_cast<int64_t>(row) * k + 8 * g);
+                o[0] = y[r][u][0];
+                o[1] = y[r][u][1];
+            }
+        }
+    }
+}
+
+template <int GT, int R, bool PIECES>
+__global__ __launch_bounds__(kT) void add_rmsnorm_stage_kernel(float* __restrict__ h, const float* __restrict__ delta,
+                                                               const float* __restrict__ w, _Float16* __restrict__ ah,
+                                                               int* __restrict__ row_exp, int64_t half_elems,
+                                                               float* __restrict__ out_f32, int m, int dim, float eps) {
+    __shared__ float part[R][kT / 64];
+    const int row0 = static_cast<int>(blockIdx.x) * R;
+    const int groups = dim / 8;
+    float4 wv[GT][2];
+    float4 y[R][GT][2];
+#pragma unroll
+    for (int u = 0; u < GT; ++u) {
+        const int g = static_cast<int>(threadIdx.x) + u * kT;
+        const bool ok = g < groups;
+        wv[u][0] = ok ? reinterpret_cast<const float4*>(w)[2 * g] : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[u][1] = ok ? reinterpret_cast<const float4*>(w)[2 * g + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool in = ok && row0 + r < m;
+            const int64_t base = static_cast<int64_t>(row0 + r) * dim + 8 * g;
+            float4 a0 = in ? *reinterpret_cast<const float4*>(h + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 a1 = in ? *reinterpret_cast<const float4*>(h + base + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (delta && in) {
+                const float4 d0 = *reinterpret_cast<const float4*>(delta + base);
+                const float4 d1 = *reinterpret_cast<const float4*>(delta + base + 4);
+                a0 = make_float4(a0.x + d0.x, a0.y + d0.y, a0.z + d0.z, a0.w + d0.w);
+                a1 = make_float4(a1.x + d1.x, a1.y + d1.y, a1.z + d1.z, a1.w + d1.w);
+            }
+            y[r][u][0] = a0;
+            y[r][u][1] = a1;
+        }
+    }
+    float ss[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        ss[r] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < GT; ++u)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float4 v = y[r][u][q];
+                ss[r] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss[r]))));
+            }
+    }
+    block_reduce_rows<R>(ss, part, false);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float inv = 1.0f / sqrtf(ss[r] / static_cast<float>(dim) + eps);
+        const bool in = row0 + r < m;
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            const int g = static_cast<int>(threadIdx.x) + u * kT;
+            if (delta && in && g < groups) {
+                float4* hr = reinterpret_cast<float4*>(h + static_cast<int64_t>(row0 + r) * dim + 8 * g);
+                hr[0] = y[r][u][0];
+                hr[1] = y[r][u][1];
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float4 v = y[r][u][q], wq = wv[u][q];
+                y[r][u][q] = make_float4(v.x * inv * wq.x, v.y * inv * wq.y, v.z * inv * wq.z, v.w * inv * wq.w);
+            }
+        }
+    }
+    stage_rows<GT, R, PIECES>(y, row0, m, dim, ah, row_exp, half_elems, out_f32, part);
+}
+
+template <int GT, int R, bool PIECES>
+__global__ __launch_bounds__(kT) void silu_mul_stage_kernel(const float* __restrict__ gu, _Float16* __restrict__ ah,
+                                                            int* __restrict__ row_exp, int64_t half_elems,
+                                                            float* __restrict__ out_f32, int m, int inter) {
+    __shared__ float part[R][kT / 64];
+    const int row0 = static_cast<int>(blockIdx.x) * R;
+    const int groups = inter / 8;
+    float4 y[R][GT][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int u = 0; u < GT; ++u) {
+            const int g = static_cast<int>(threadIdx.x) + u * kT;
+            const bool in = g < groups && row0 + r < m;
+            const float* gr = gu + static_cast<int64_t>(row0 + r) * 2 * inter + 8 * g;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float4 gv = in ? *reinterpret_cast<const float4*>(gr + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 uv =
+                    in ? *reinterpret_cast<const float4*>(gr + inter + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+                // silu_mul_vec_kernel's arithmetic
+                y[r][u][q] = make_float4(((1.0f / (1.0f + expf(-gv.x))) * gv.x) * uv.x,
+                                         ((1.0f / (1.0f + expf(-gv.y))) * gv.y) * uv.y,
+                                         ((1.0f / (1.0f + expf(-gv.z))) * gv.z) * uv.z,
+                                         ((1.0f / (1.0f + expf(-gv.w))) * gv.w) * uv.w);
+            }
+        }
+    stage_rows<GT, R, PIECES>(y, row0, m, inter, ah, row_exp, half_elems, out_f32, part);
+}
+
+// Rows per workgroup: as many as the registers allow (4 / GT, at least
+// 1, at most 2 for GT = 3) while leaving at least 256 workgroups; one row
+// when the parts are row-major (a row's stores are contiguous already).
+int stage_rows_per_wg(int64_t rows, int gt, bool pieces) {
+    if (!pieces) return 1;
+    int r = gt == 1 ? 4 : 2;
+    while (r > 1 && (rows + r - 1) / r < 256) r /= 2;
+    return r;
+}
+
+int check_stage(const void* a_staged, int layout, int64_t rows, int64_t k, const char* who) {
+    if (layout != VM_HIP_A_ROWS && layout != VM_HIP_A_PIECES)
+        return fail_inval(std::string(who) + ": layout must be VM_HIP_A_ROWS or VM_HIP_A_PIECES");
+    if (!a_staged) return fail_inval(std::string(who) + ": null staged buffer");
+    if (k % 32 != 0 || k > 3 * 8 * kT) return fail_inval(std::string(who) + ": the row length must be a multiple of 32, at most 6144");
+    if (rows > 0x7fffffff / 2) return fail_inval(std::string(who) + ": too many rows");
+    if (!aligned16(a_staged)) return fail_inval(std::string(who) + ": the staged buffer must be 16-byte aligned");
+    return 0;
+}
+
 }  // namespace
 }  // namespace vmhip
 
@@ -1267,6 +1459,64 @@ int vm_hip_silu_mul_f32(const float* gate_up, float* out, int64_t rows, int64_t 
                            inter);
     }
     return check_launch("silu_mul", S(stream));
+}
+
+int vm_hip_add_rmsnorm_stage_f32(float* h, const float* delta, const float* w, void* a_staged, int layout,
+                                 float* hn_out, int64_t rows, int64_t dim, float eps, void* stream) {
+    clear_error();
+    if (rows < 0 || dim < 0) return fail_inval("add_rmsnorm_stage: negative size");
+    if (rows == 0 || dim == 0) return 0;
+    if (!h || !w) return fail_inval("add_rmsnorm_stage: null pointer");
+    VM_TRY(check_stage(a_staged, layout, rows, dim, "add_rmsnorm_stage"));
+    if (!aligned16(h) || !aligned16(w) || (delta && !aligned16(delta)) || (hn_out && !aligned16(hn_out)))
+        return fail_inval("add_rmsnorm_stage: operands must be 16-byte aligned");
+    const bool pieces = layout == VM_HIP_A_PIECES;
+    const int gt = static_cast<int>((dim / 8 + kT - 1) / kT);
+    const int r = stage_rows_per_wg(rows, gt, pieces);
+    const int64_t half_elems = static_cast<int64_t>(a_stage_rows(rows, pieces)) * dim;
+    auto* ah = static_cast<_Float16*>(a_staged);
+    auto* rexp = reinterpret_cast<int*>(static_cast<char*>(a_staged) + a_stage_half_bytes(rows, dim, pieces));
+    const dim3 grid(static_cast<unsigned>((rows + r - 1) / r));
+    const int m = static_cast<int>(rows), d = static_cast<int>(dim);
+#define VM_STAGE(GX, RX, PX)                                                                                     \
+    if (gt == GX && r == RX && pieces == PX)                                                                     \
+        hipLaunchKernelGGL((add_rmsnorm_stage_kernel<GX, RX, PX>), grid, dim3(kT), 0, S(stream), h, delta, w, ah, \
+                           rexp, half_elems, hn_out, m, d, eps);                                                 \
+    else
+    VM_STAGE(1, 1, false) VM_STAGE(2, 1, false) VM_STAGE(3, 1, false) VM_STAGE(1, 1, true) VM_STAGE(1, 2, true)
+    VM_STAGE(1, 4, true) VM_STAGE(2, 1, true) VM_STAGE(2, 2, true) VM_STAGE(3, 1, true) VM_STAGE(3, 2, true)
+#undef VM_STAGE
+    return fail_inval("add_rmsnorm_stage: internal error: no kernel for this row length");
+    return check_launch("add_rmsnorm_stage", S(stream));
+}
+
+int vm_hip_silu_mul_stage_f32(const float* gate_up, void* a_staged, int layout, float* out_f32, int64_t rows,
+                              int64_t inter, void* stream) {
+    clear_error();
+    if (rows < 0 || inter < 0) return fail_inval("silu_mul_stage: negative size");
+    if (rows == 0 || inter == 0) return 0;
+    if (!gate_up) return fail_inval("silu_mul_stage: null pointer");
+    VM_TRY(check_stage(a_staged, layout, rows, inter, "silu_mul_stage"));
+    if (!aligned16(gate_up) || (out_f32 && !aligned16(out_f32)))
+        return fail_inval("silu_mul_stage: operands must be 16-byte aligned");
+    const bool pieces = layout == VM_HIP_A_PIECES;
+    const int gt = static_cast<int>((inter / 8 + kT - 1) / kT);
+    const int r = stage_rows_per_wg(rows, gt, pieces);
+    const int64_t half_elems = static_cast<int64_t>(a_stage_rows(rows, pieces)) * inter;
+    auto* ah = static_cast<_Float16*>(a_staged);
+    auto* rexp = reinterpret_cast<int*>(static_cast<char*>(a_staged) + a_stage_half_bytes(rows, inter, pieces));
+    const dim3 grid(static_cast<unsigned>((rows + r - 1) / r));
+    const int m = static_cast<int>(rows), d = static_cast<int>(inter);
+#define VM_STAGE(GX, RX, PX)                                                                                     \
+    if (gt == GX && r == RX && pieces == PX)                                                                     \
+        hipLaunchKernelGGL((silu_mul_stage_kernel<GX, RX, PX>), grid, dim3(kT), 0, S(stream), gate_up, ah, rexp,  \
+                           half_elems, out_f32, m, d);                                                           \
+    else
+    VM_STAGE(1, 1, false) VM_STAGE(2, 1, false) VM_STAGE(3, 1, false) VM_STAGE(1, 1, true) VM_STAGE(1, 2, true)
+    VM_STAGE(1, 4, true) VM_STAGE(2, 1, true) VM_STAGE(2, 2, true) VM_STAGE(3, 1, true) VM_STAGE(3, 2, true)
+#undef VM_STAGE
+    return fail_inval("silu_mul_stage: internal error: no kernel for this row length");
+    return check_launch("silu_mul_stage", S(stream));
 }
 
 int vm_hip_argmax_f32(const float* x, int64_t n, int32_t* token_out, int32_t* pos, int32_t* tokens, int64_t max_seq,

@@ -50,6 +50,7 @@
 #include <cstdio>
 #include <cstdlib>
 
+#include "a_split.h"
 #include "qmm_kernels.h"
 #include "vm_device.h"
 #include "vm_internal.h"
@@ -608,35 +609,6 @@ __device__ void prep_col_pow(const float* __restrict__ scale, float* __restrict_
     }
 }
 
-// hi = fp16(a 2^x), lo = fp16(a 2^x - hi) of one 8-group, position i
-// holding k = i (row-major) or k = i / 2 + 4 (i % 2) (operand order); an
-// infinite part (|a| beyond fp16 in an unscaled row) leaves lo at 0.
-template <bool FRAG>
-__device__ __forceinline__ void split8(const float4& p, const float4& q, int x, half8v& h, half8v& l) {
-    const float s[8] = {ldexpf(p.x, x), ldexpf(p.y, x), ldexpf(p.z, x), ldexpf(p.w, x),
-                        ldexpf(q.x, x), ldexpf(q.y, x), ldexpf(q.z, x), ldexpf(q.w, x)};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int kk = FRAG ? (i >> 1) + 4 * (i & 1) : i;
-        const _Float16 hh = static_cast<_Float16>(s[kk]);
-        const float d = s[kk] - static_cast<float>(hh);
-        h[i] = hh;
-        l[i] = static_cast<_Float16>(d == d && fabsf(d) <= 65504.0f ? d : 0.0f);
-    }
-}
-
-// The row exponent x of a row with largest magnitude mx (x = 0 when the
-// row holds an infinity or NaN, or is all zeros): 2^x mx in [2^14, 2^15).
-__device__ __forceinline__ int row_exponent(float mx) {
-    int x = 0;
-    if (mx > 0.0f && mx <= 3.4028235e38f) {
-        int e = 0;
-        (void)frexpf(mx, &e);   // mx = f * 2^e, f in [0.5, 1)
-        x = 15 - e;
-    }
-    return x;
-}
-
 template <bool FRAG>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict__ a, _Float16* __restrict__ ah,
                                                         int* __restrict__ row_exp, int m, int k, int vec,
@@ -701,7 +673,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
     if ((tid & 63) == 0) wmax[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    const int x = row_exponent(mx);
+    const int x = a_row_exponent(mx);
     if (tid == 0) row_exp[row] = x;
     const int64_t mp = FRAG ? (static_cast<int64_t>(m) + 31) / 32 * 32 : m;
     half8v* hi = reinterpret_cast<half8v*>(ah);
@@ -714,7 +686,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
     };
     auto split = [&](int g, const float4& p, const float4& q) {
         half8v h, l;
-        split8<FRAG>(p, q, x, h, l);
+        a_split8<FRAG>(p, q, x, h, l);
         hi[piece(g)] = h;
         lo[piece(g)] = l;
     };
@@ -802,7 +774,7 @@ __global__ __launch_bounds__(256) void gemm_prep_frag_kernel(const float* __rest
     int x[R];
 #pragma unroll
     for (int r = 0; r < R; ++r)
-        x[r] = row_exponent(fmaxf(fmaxf(wmax[r], wmax[R + r]), fmaxf(wmax[2 * R + r], wmax[3 * R + r])));
+        x[r] = a_row_exponent(fmaxf(fmaxf(wmax[r], wmax[R + r]), fmaxf(wmax[2 * R + r], wmax[3 * R + r])));
     if (tid < R && row0 + tid < m) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -821,7 +793,7 @@ __global__ __launch_bounds__(256) void gemm_prep_frag_kernel(const float* __rest
         for (int r = 0; r < R; ++r) {
             if (row0 + r >= m) break;
             half8v h, l;
-            split8<true>(v[r][u][0], v[r][u][1], x[r], h, l);
+            a_split8<true>(v[r][u][0], v[r][u][1], x[r], h, l);
             hi[base + r] = h;
             lo[base + r] = l;
         }
@@ -1579,11 +1551,12 @@ static int prep_rows_per_wg(int m, int gt) {
     return r;
 }
 
-int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
-                 int quant_type, int block_size, hipStream_t stream) {
+// Which MFMA path a call takes and how it stages A (VM_HIP_EUNSUPPORTED:
+// another kernel takes the shape).
+int gemm_plan(int m, int k, int n, int quant_type, int block_size, GemmPlan* plan) {
     // 64-row steps may end half-way (k % 32 == 0); 16-byte code pieces need
     // whole 16-column groups; buffer offsets are 32-bit.
-    if (k % 32 != 0 || n % 16 != 0) return VM_HIP_EUNSUPPORTED;
+    if (m <= 4 || k % 32 != 0 || n % 16 != 0) return VM_HIP_EUNSUPPORTED;
     // (A's two fp16 parts take m * k * 4 bytes, addressed with 32-bit offsets)
     if ((static_cast<int64_t>(m) + 31) / 32 * 32 * k * 4 >= (int64_t(1) << 31) ||
         static_cast<int64_t>(k) * n >= (int64_t(1) << 31) ||
@@ -1600,23 +1573,54 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
         if (block_size % 32 != 0) return VM_HIP_EUNSUPPORTED;
         kind = 1;
     }
-    const bool use_wide = use_wide_kernel(kind, m, k, n);
-    // A's row-scaled fp16 parts (hi, lo), the row exponents and, for the
+    plan->kind = kind;
+    plan->pieces = use_wide_kernel(kind, m, k, n);
+    plan->col_pow = plan->pieces && kind != 0;
+    return 0;
+}
+
+// The per-column powers of two of blockwise scales for the wide kernel
+// (col_pow[j] = 2^e, col_pow[n + j] = 2^-e), alone: the prep's column
+// workgroups without rows.
+int gemm_col_pow(const float* scale, float* col_pow, int k, int n, int block_size, hipStream_t stream) {
+    const int nblk = (k + block_size - 1) / block_size;
+    const int col_wgs = (n + kPrepCols - 1) / kPrepCols;
+    hipLaunchKernelGGL((gemm_prep_frag_kernel<1, 1>), dim3(col_wgs), dim3(256), 0, stream, nullptr, nullptr, nullptr,
+                       0, k, 0, scale, col_pow, n, nblk, col_wgs);
+    return check_launch("QuantizedMatMul", stream);
+}
+
+int gemm_qmm_staged_f32(const GemmPlan& plan, const _Float16* ah, const int* row_exp, const float* col_pow,
+                        const uint8_t* wq, const float* scale, float* c, int m, int k, int n, int block_size,
+                        hipStream_t stream) {
+    if (plan.pieces) {
+        if (plan.kind == 2) return launch_wide_kind<2>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
+        if (plan.kind == 1) return launch_wide_kind<1>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
+        return launch_wide_kind<0>(ah, row_exp, col_pow, wq, scale, c, m, k, n, 0, stream);
+    }
+    if (plan.kind == 2) return launch_kind<2>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
+    if (plan.kind == 1) return launch_kind<1>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
+    return launch_kind<0>(ah, row_exp, wq, scale, c, m, k, n, 0, stream);
+}
+
+int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k, int n,
+                 int quant_type, int block_size, hipStream_t stream) {
+    GemmPlan plan;
+    VM_TRY(gemm_plan(m, k, n, quant_type, block_size, &plan));
+    // A's row-scaled fp16 parts (hi, lo) and row exponents, then, for the
     // wide kernel with blockwise scales, the per-column powers of two.
-    const std::size_t mp = use_wide ? (static_cast<std::size_t>(m) + 31) / 32 * 32 : static_cast<std::size_t>(m);
-    const std::size_t half_bytes = (mp * k * 4 + 255) & ~std::size_t(255);
-    const std::size_t exp_bytes = (static_cast<std::size_t>(m) * sizeof(int) + 255) & ~std::size_t(255);
-    const bool col_exps = use_wide && kind != 0;
-    const std::size_t pow_bytes = col_exps ? static_cast<std::size_t>(n) * 2 * sizeof(float) : 0;
+    const std::size_t half_bytes = a_stage_half_bytes(m, k, plan.pieces);
+    const std::size_t stage_bytes = a_stage_bytes(m, k, plan.pieces);
+    const std::size_t pow_bytes = plan.col_pow ? static_cast<std::size_t>(n) * 2 * sizeof(float) : 0;
     void* aux = nullptr;
-    VM_TRY(get_aux(stream, half_bytes + exp_bytes + pow_bytes, &aux));
+    VM_TRY(get_aux(stream, stage_bytes + pow_bytes, &aux));
     auto* ah = static_cast<_Float16*>(aux);
     auto* row_exp = reinterpret_cast<int*>(static_cast<char*>(aux) + half_bytes);
-    auto* col_pow = col_exps ? reinterpret_cast<float*>(static_cast<char*>(aux) + half_bytes + exp_bytes) : nullptr;
+    auto* col_pow = plan.col_pow ? reinterpret_cast<float*>(static_cast<char*>(aux) + stage_bytes) : nullptr;
     const int vec = reinterpret_cast<uintptr_t>(a) % 16 == 0 ? 1 : 0;
-    const int nblk = kind == 0 ? 1 : (k + block_size - 1) / block_size;
-    const int col_wgs = col_exps ? (n + kPrepCols - 1) / kPrepCols : 0;
-    if (use_wide) {
+    const int nblk = plan.kind == 0 ? 1 : (k + block_size - 1) / block_size;
+    const int col_wgs = plan.col_pow ? (n + kPrepCols - 1) / kPrepCols : 0;
+    if (plan.pieces) {
         const int gt = (k / 8 + 255) / 256;
         const int rows_per_wg = prep_rows_per_wg(m, gt);
 #define VM_PREP(RX, GX)                                                                                           \
@@ -1629,17 +1633,12 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
 #undef VM_PREP
             hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(m + col_wgs), dim3(256), 0, stream, a, ah, row_exp, m, k,
                                vec, scale, col_pow, n, nblk, col_wgs);
-        VM_TRY(check_launch("QuantizedMatMul", stream));
-        if (kind == 2) return launch_wide_kind<2>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
-        if (kind == 1) return launch_wide_kind<1>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
-        return launch_wide_kind<0>(ah, row_exp, col_pow, wq, scale, c, m, k, n, 0, stream);
+    } else {
+        hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k, vec, scale,
+                           col_pow, n, nblk, 0);
     }
-    hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k, vec, scale,
-                       col_pow, n, nblk, 0);
     VM_TRY(check_launch("QuantizedMatMul", stream));
-    if (kind == 2) return launch_kind<2>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
-    if (kind == 1) return launch_kind<1>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
-    return launch_kind<0>(ah, row_exp, wq, scale, c, m, k, n, 0, stream);
+    return gemm_qmm_staged_f32(plan, ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
 }
 
 }  // namespace vmhip
