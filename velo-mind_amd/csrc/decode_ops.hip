@@ -721,21 +721,27 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
 // groups); output row 4g + e fetches its factor from lane 4g + e.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int D>
-__global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __restrict__ q,
-                                                               const float* __restrict__ k_cache,
-                                                               const float* __restrict__ v_cache,
-                                                               const int32_t* __restrict__ pos,
-                                                               float* __restrict__ out, int rows, int heads,
-                                                               int kv_heads, int max_seq, float scale) {
+template <int D, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attention_prefill_kernel(const float* __restrict__ q,
+                                                                       const float* __restrict__ k_cache,
+                                                                       const float* __restrict__ v_cache,
+                                                                       const int32_t* __restrict__ pos,
+                                                                       float* __restrict__ out, int rows, int heads,
+                                                                       int kv_heads, int max_seq, float scale) {
     static_assert(D == 64, "one 16-dim slab per lane group");
     constexpr int KT = 64;          // keys per tile
     constexpr int PITCH = D + 4;    // LDS row pitch in floats (conflict-free 16-byte reads)
+    constexpr int NT = 64 * WAVES;  // threads
+    constexpr int QR = 16 * WAVES;  // query rows per workgroup
     __shared__ __align__(16) float sk[KT * PITCH];
     __shared__ __align__(16) float sv[KT * PITCH];
-    const int h = blockIdx.y;
+    // One-dimensional grid, the query tiles with the most keys first (all
+    // heads' last tile, then the one before, ...), so that the workgroups
+    // dispatched last are the short ones.
+    const int tiles = (rows + QR - 1) / QR;
+    const int h = static_cast<int>(blockIdx.x) % heads;
     const int hk = h / (heads / kv_heads);
-    const int r0 = blockIdx.x * 64;
+    const int r0 = (tiles - 1 - static_cast<int>(blockIdx.x) / heads) * QR;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -758,7 +764,7 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
             qf[4 * c + 3] = v.w;
         }
     }
-    const int wg_end = min(p0 + min(r0 + 64, rows), n_keys);   // keys < wg_end reach some row of the tile
+    const int wg_end = min(p0 + min(r0 + QR, rows), n_keys);   // keys < wg_end reach some row of the tile
     const float* kb = k_cache + static_cast<int64_t>(hk) * max_seq * D;
     const float* vb = v_cache + static_cast<int64_t>(hk) * max_seq * D;
     f32x4 acc[4];   // O[row 4 lg + e][dim 16 db + lr]
@@ -769,13 +775,13 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
     // K/V tiles pass through registers one tile ahead: the next tile's
     // loads are issued as soon as the current one is in LDS, so they are in
     // flight during its scores and p . V.
-    constexpr int kU = KT * D / 4 / kT;   // float4s of K (and of V) per thread per tile
+    constexpr int kU = KT * D / 4 / NT;   // float4s of K (and of V) per thread per tile
     float4 nk_reg[kU], nv_reg[kU];
     auto load_tile = [&](int t0) {
         const int nkt = min(KT, n_keys - t0);
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int e = tid + u * kT;
+            const int e = tid + u * NT;
             const int j = e / (D / 4), c = e - j * (D / 4);
             nk_reg[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             nv_reg[u] = nk_reg[u];
@@ -790,7 +796,7 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
         __syncthreads();   // the previous tile is consumed
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int e = tid + u * kT;
+            const int e = tid + u * NT;
             const int j = e / (D / 4), c = e - j * (D / 4);
             *reinterpret_cast<float4*>(sk + j * PITCH + 4 * c) = nk_reg[u];
             *reinterpret_cast<float4*>(sv + j * PITCH + 4 * c) = nv_reg[u];
@@ -1435,11 +1441,15 @@ int vm_hip_attention_prefill_f32(const float* q, const float* k_cache, const flo
     }
     if (rows == 0) return 0;
     if (!q || !k_cache || !v_cache || !pos || !out) return fail_inval("attention_prefill: null pointer");
-    if (rows > max_seq || heads > 65535 || max_seq > (1 << 24)) return fail_inval("attention_prefill: too large");
+    if (rows > max_seq || heads > 65535 || max_seq > (1 << 24) || (rows + 15) / 16 * heads > INT32_MAX)
+        return fail_inval("attention_prefill: too large");
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
-    const dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(heads));
-    hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(kT), 0, S(stream), q, k_cache, v_cache, pos, out,
-                       static_cast<int>(rows), static_cast<int>(heads), static_cast<int>(kv_heads),
+    // Four waves (64 query rows) per workgroup: measured 33.0 us at 512 rows and
+    // 32 heads against 41.2 us with two waves and 41.3 us with one (more,
+    // smaller workgroups re-stage every K/V tile for fewer rows).
+    const unsigned wgs = static_cast<unsigned>(((rows + 63) / 64) * heads);
+    hipLaunchKernelGGL((attention_prefill_kernel<64, 4>), dim3(wgs), dim3(256), 0, S(stream), q, k_cache, v_cache,
+                       pos, out, static_cast<int>(rows), static_cast<int>(heads), static_cast<int>(kv_heads),
                        static_cast<int>(max_seq), sc);
     return check_launch("attention_prefill", S(stream));
 }

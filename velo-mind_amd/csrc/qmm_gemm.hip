@@ -1429,22 +1429,42 @@ struct WideConfig {
 };
 
 // From sweeps on MI355X (config 3: K = 2048, N = 5632, M = 128 / 256 /
-// 512, INT8 and INT4, weights cold): 128-row tiles with two wave groups,
-// 128 columns for M >= 256 and 64 below, and K splits until the grid holds
-// at least ~150 workgroups while every group keeps at least four steps
-// (M = 512: 176 tiles, no split; M = 256: 88 tiles x 2; M = 128: 88 x 2).
-// A split costs a write and a read of the fp32 partial tile, so it only
-// pays where tiles alone leave most CUs idle.
+// 512, INT8 and INT4, and the TinyLlama prefill projections at M = 512,
+// INT4; weights cold): 128-row tiles with two wave groups, 128 columns for
+// M >= 256 and 64 below, and K splits until the grid holds at least ~150
+// workgroups while every group keeps at least four steps (M = 512: 176
+// tiles, no split; M = 256: 88 tiles x 2; M = 128: 88 x 2).  A split costs
+// a write and a read of the fp32 partial tile, so it only pays where tiles
+// alone leave most CUs idle.  Two refinements:
+//   * when 128 columns would need splits that leave a group fewer than
+//     eight steps, 64 columns with fewer splits (K = 2048, N = 2048:
+//     27.6 us vs 29.8 with 128 columns and four splits);
+//   * more tiles than CUs: one wave group per workgroup, so that two
+//     workgroups share a CU and the whole grid is resident at once instead
+//     of a second, partial round (K = 2048, N = 11264: 352 tiles, 66.1 us vs
+//     75.0 with two groups).
 WideConfig choose_wide(int kind, int m, int k, int n) {
     (void)kind;
     WideConfig cfg;
     const int steps = (k + kBK - 1) / kBK;
     cfg.bm = 128;
-    cfg.bn = m >= 256 ? 128 : 64;
     cfg.groups = 2;
-    const long tiles = static_cast<long>((m + cfg.bm - 1) / cfg.bm) * ((n + cfg.bn - 1) / cfg.bn);
-    int s = 1;
-    while (s * 2 <= kMaxSplits && tiles * s < 150 && steps / (s * 2 * cfg.groups) >= 4) s *= 2;
+    auto tiles_of = [&](int bn) { return static_cast<long>((m + cfg.bm - 1) / cfg.bm) * ((n + bn - 1) / bn); };
+    auto splits_of = [&](long tiles) {
+        int s = 1;
+        while (s * 2 <= kMaxSplits && tiles * s < 150 && steps / (s * 2 * cfg.groups) >= 4) s *= 2;
+        return s;
+    };
+    cfg.bn = m >= 256 ? 128 : 64;
+    int s = splits_of(tiles_of(cfg.bn));
+    if (cfg.bn == 128 && steps / (s * cfg.groups) < 8) {
+        const int s64 = splits_of(tiles_of(64));
+        if (s64 < s) {
+            cfg.bn = 64;
+            s = s64;
+        }
+    }
+    if (s == 1 && tiles_of(cfg.bn) > 256 && cfg.bn == 128) cfg.groups = 1;
     cfg.splits = s;
     // Tuning override for measurement sweeps: VELOMIND_GEMM_WIDE="BM,BN,S,D[,G]"
     if (const char* env = std::getenv("VELOMIND_GEMM_WIDE")) {
