@@ -185,11 +185,14 @@ def test_rope_kv_append(hip):
 
 
 # (512, 0, ...) is TinyLlama's 512-token prefill (eight 64-key tiles for the
-# last query rows); (256, 300, ...) continues a cached prefix.
+# last query rows); (256, 300, ...) continues a cached prefix.  Grids of at
+# most 512 64-row tiles split each workgroup's keys over two wave pairs;
+# (600, 0, 64, ...) has 640 tiles and runs the one-group form.
 @pytest.mark.parametrize("rows,p0,heads,kv_heads,max_seq", [(19, 0, 8, 2, 96), (64, 0, 8, 2, 96), (70, 10, 8, 2, 96),
                                                         (200, 0, 32, 4, 256), (130, 77, 15, 5, 256),
                                                         (1, 40, 8, 8, 64), (512, 0, 32, 4, 768),
-                                                        (256, 300, 16, 4, 768)])
+                                                        (256, 300, 16, 4, 768), (33, 0, 4, 1, 40),
+                                                        (600, 0, 64, 8, 640), (600, 30, 64, 8, 640)])
 def test_attention_prefill(hip, rows, p0, heads, kv_heads, max_seq):
     d = 64
     rng = np.random.default_rng(rows + p0)

@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 #include "a_split.h"
@@ -707,8 +708,14 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
 // ---- Prefill attention over the resident cache with fp32 matrix cores:
 // q [H, S, D] rows at positions *pos + i see keys 0 .. *pos + i (causal);
 // out [S, H, D] (token-major, the layout the output projection reads).
-// Grid (ceil(S/64), H), four waves; wave w owns query rows r0 + 16w .. +15
-// and walks 64-key tiles staged in LDS with an online softmax.
+// A workgroup of four waves takes QR = 16 RW query rows of one head: wave w
+// owns rows 16 (w % RW) .. +15 and key group w / RW of KS.  The keys go by
+// in steps of KS 64-key tiles staged in LDS; group g runs its online
+// softmax over tile g of each step, and the groups' (max, sum, output)
+// triples are merged through LDS at the end.  Splitting the keys cuts the
+// longest chain of dependent MFMAs (the last query rows see every key) by
+// KS; the grid is one-dimensional with the query tiles that see the most
+// keys first, so the workgroups dispatched last are the short ones.
 //
 // v_mfma_f32_16x16x4_f32 (fp32 inputs and accumulation, so no precision is
 // given up against the fp32 reference) holds A[i][k] in lane i + 16k,
@@ -721,35 +728,36 @@ __global__ __launch_bounds__(kT) void attention_decode_slices_kernel(
 // groups); output row 4g + e fetches its factor from lane 4g + e.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int D, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void attention_prefill_kernel(const float* __restrict__ q,
-                                                                       const float* __restrict__ k_cache,
-                                                                       const float* __restrict__ v_cache,
-                                                                       const int32_t* __restrict__ pos,
-                                                                       float* __restrict__ out, int rows, int heads,
-                                                                       int kv_heads, int max_seq, float scale) {
+template <int D, int RW, int KS>
+__global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __restrict__ q,
+                                                                const float* __restrict__ k_cache,
+                                                                const float* __restrict__ v_cache,
+                                                                const int32_t* __restrict__ pos,
+                                                                float* __restrict__ out, int rows, int heads,
+                                                                int kv_heads, int max_seq, float scale) {
     static_assert(D == 64, "one 16-dim slab per lane group");
-    constexpr int KT = 64;          // keys per tile
+    static_assert(RW * KS == 4, "four waves");
+    constexpr int KT = 64;          // keys per tile (one key group's share of a step)
+    constexpr int ST = KT * KS;     // keys per step
     constexpr int PITCH = D + 4;    // LDS row pitch in floats (conflict-free 16-byte reads)
-    constexpr int NT = 64 * WAVES;  // threads
-    constexpr int QR = 16 * WAVES;  // query rows per workgroup
-    __shared__ __align__(16) float sk[KT * PITCH];
-    __shared__ __align__(16) float sv[KT * PITCH];
-    // One-dimensional grid, the query tiles with the most keys first (all
-    // heads' last tile, then the one before, ...), so that the workgroups
-    // dispatched last are the short ones.
+    constexpr int QR = 16 * RW;     // query rows per workgroup
+    __shared__ __align__(16) float sk[ST * PITCH];
+    __shared__ __align__(16) float sv[ST * PITCH];
     const int tiles = (rows + QR - 1) / QR;
     const int h = static_cast<int>(blockIdx.x) % heads;
     const int hk = h / (heads / kv_heads);
     const int r0 = (tiles - 1 - static_cast<int>(blockIdx.x) / heads) * QR;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
+    const int wr = wave % RW, kg = wave / RW;   // row block, key group
     const int lr = lane & 15, lg = lane >> 4;
     const int p0 = pos[0];
     const int n_keys = min(p0 + rows, max_seq);
-    const int qrow = r0 + 16 * wave + lr;     // the query row whose Q this lane holds
+    const int qrow = r0 + 16 * wr + lr;       // the query row whose Q this lane holds
     const bool row_ok = qrow < rows;
     const int my_last = p0 + qrow;            // keys <= my_last are visible to row qrow
+    // keys past this are masked for every row of the wave
+    const int wave_last = r0 + 16 * wr < rows ? p0 + min(r0 + 16 * wr + 15, rows - 1) : -1;
 
     // Q fragment: Q[qrow][16 lg + s], s = 0..15.
     float qf[16];
@@ -772,16 +780,16 @@ __global__ __launch_bounds__(64 * WAVES) void attention_prefill_kernel(const flo
     for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;   // statistics of row lr of this wave
 
-    // K/V tiles pass through registers one tile ahead: the next tile's
+    // K/V steps pass through registers one step ahead: the next step's
     // loads are issued as soon as the current one is in LDS, so they are in
     // flight during its scores and p . V.
-    constexpr int kU = KT * D / 4 / NT;   // float4s of K (and of V) per thread per tile
+    constexpr int kU = ST * D / 4 / 256;   // float4s of K (and of V) per thread per step
     float4 nk_reg[kU], nv_reg[kU];
-    auto load_tile = [&](int t0) {
-        const int nkt = min(KT, n_keys - t0);
+    auto load_step = [&](int t0) {
+        const int nkt = min(ST, n_keys - t0);
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int e = tid + u * NT;
+            const int e = tid + u * 256;
             const int j = e / (D / 4), c = e - j * (D / 4);
             nk_reg[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             nv_reg[u] = nk_reg[u];
@@ -791,24 +799,31 @@ __global__ __launch_bounds__(64 * WAVES) void attention_prefill_kernel(const flo
             }
         }
     };
-    if (wg_end > 0) load_tile(0);
-    for (int k0 = 0; k0 < wg_end; k0 += KT) {
-        __syncthreads();   // the previous tile is consumed
+    if (wg_end > 0) load_step(0);
+    for (int s0 = 0; s0 < wg_end; s0 += ST) {
+        __syncthreads();   // the previous step is consumed
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int e = tid + u * NT;
+            const int e = tid + u * 256;
             const int j = e / (D / 4), c = e - j * (D / 4);
             *reinterpret_cast<float4*>(sk + j * PITCH + 4 * c) = nk_reg[u];
             *reinterpret_cast<float4*>(sv + j * PITCH + 4 * c) = nv_reg[u];
         }
-        if (k0 + KT < wg_end) load_tile(k0 + KT);
+        if (s0 + ST < wg_end) load_step(s0 + ST);
         __syncthreads();
+
+        const int k0 = s0 + kg * KT;   // this key group's tile
+        // a tile wholly past the wave's last visible key (or past the keys)
+        // changes nothing
+        if (k0 > wave_last || k0 >= n_keys) continue;
+        const float* skt = sk + kg * KT * PITCH;
+        const float* svt = sv + kg * KT * PITCH;
 
         // S^T = K Q^T for the four 16-key blocks.
         f32x4 st[4];
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
-            const float* krow = sk + (16 * nb + lr) * PITCH + 16 * lg;
+            const float* krow = skt + (16 * nb + lr) * PITCH + 16 * lg;
             float ka[16];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -865,8 +880,63 @@ __global__ __launch_bounds__(64 * WAVES) void attention_prefill_kernel(const flo
 #pragma unroll
             for (int s = 0; s < 16; ++s) {
                 const int key = 16 * (s / 4) + 4 * lg + (s % 4);
-                const float bv = sv[key * PITCH + 16 * db + lr];
+                const float bv = svt[key * PITCH + 16 * db + lr];
                 acc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[s / 4][s % 4], bv, acc[db], 0, 0, 0);
+            }
+        }
+    }
+
+    // Merge the key groups' triples into group 0 (fixed order: group 0, 1,
+    // ..): m = max m_g, l = sum l_g e^(m_g - m), O = sum O_g e^(m_g - m).
+    if constexpr (KS > 1) {
+        __syncthreads();   // every wave is past its last LDS read
+        float* so = sk;                         // [KS - 1][RW][16 rows][D]
+        float* sst = sv;                        // [KS - 1][RW][16 rows][2]
+        if (kg > 0) {
+            float* o = so + ((kg - 1) * RW + wr) * 16 * D;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) o[(4 * lg + e) * D + 16 * db + lr] = acc[db][e];
+            if (lg == 0) {
+                float* t = sst + (((kg - 1) * RW + wr) * 16 + lr) * 2;
+                t[0] = m_run;
+                t[1] = l_run;
+            }
+        }
+        __syncthreads();
+        if (kg > 0) return;
+        float mg[KS], lgs[KS];
+        mg[0] = m_run;
+        lgs[0] = l_run;
+#pragma unroll
+        for (int g = 1; g < KS; ++g) {
+            const float* t = sst + (((g - 1) * RW + wr) * 16 + lr) * 2;
+            mg[g] = t[0];
+            lgs[g] = t[1];
+        }
+        float m = mg[0];
+#pragma unroll
+        for (int g = 1; g < KS; ++g) m = fmaxf(m, mg[g]);
+        float fg[KS];
+        float l = 0.0f;
+#pragma unroll
+        for (int g = 0; g < KS; ++g) {
+            fg[g] = mg[g] > -INFINITY ? expf(mg[g] - m) : 0.0f;
+            l += lgs[g] * fg[g];
+        }
+        l_run = l;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float f0 = __shfl(fg[0], 4 * lg + e, 64);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db][e] *= f0;
+#pragma unroll
+            for (int g = 1; g < KS; ++g) {
+                const float fe = __shfl(fg[g], 4 * lg + e, 64);
+                const float* o = so + ((g - 1) * RW + wr) * 16 * D;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) acc[db][e] += o[(4 * lg + e) * D + 16 * db + lr] * fe;
             }
         }
     }
@@ -874,7 +944,7 @@ __global__ __launch_bounds__(64 * WAVES) void attention_prefill_kernel(const flo
     for (int e = 0; e < 4; ++e) {
         const float le = __shfl(l_run, 4 * lg + e, 64);
         const float inv = le > 0.0f ? 1.0f / le : 0.0f;
-        const int row = r0 + 16 * wave + 4 * lg + e;
+        const int row = r0 + 16 * wr + 4 * lg + e;
         if (row < rows) {
             float* o = out + (static_cast<int64_t>(row) * heads + h) * D + lr;
 #pragma unroll
@@ -1429,6 +1499,22 @@ int vm_hip_attention_decode_f32(const float* q, const float* k_cache, const floa
     return check_launch("attention_decode", S(stream));
 }
 
+// Key groups per prefill-attention workgroup (64 / split query rows each).
+// Two when one-group workgroups would number at most 512 (512 rows x 32
+// heads: 25.3 us vs 33.7 with one group; 128 rows x 15 heads: 7.2 vs 10.0),
+// one for longer prompts, whose grid already spreads (2048 x 32: 219.5 us
+// vs 225.0 with two); four groups (139 KB of LDS, one workgroup per CU) were
+// slower everywhere.  VELOMIND_ATTN_SPLIT = 1 or 2 overrides (sweeps).
+static int attention_prefill_split(int64_t rows, int64_t heads) {
+    static const int forced = [] {
+        const char* e = std::getenv("VELOMIND_ATTN_SPLIT");
+        const int v = e ? std::atoi(e) : 0;
+        return (v == 1 || v == 2) ? v : 0;
+    }();
+    if (forced) return forced;
+    return (rows + 63) / 64 * heads <= 512 ? 2 : 1;
+}
+
 int vm_hip_attention_prefill_f32(const float* q, const float* k_cache, const float* v_cache, const int32_t* pos,
                                  float* out, int64_t rows, int64_t heads, int64_t kv_heads, int64_t head_dim,
                                  int64_t max_seq, float scale, void* stream) {
@@ -1444,13 +1530,17 @@ int vm_hip_attention_prefill_f32(const float* q, const float* k_cache, const flo
     if (rows > max_seq || heads > 65535 || max_seq > (1 << 24) || (rows + 15) / 16 * heads > INT32_MAX)
         return fail_inval("attention_prefill: too large");
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
-    // Four waves (64 query rows) per workgroup: measured 33.0 us at 512 rows and
-    // 32 heads against 41.2 us with two waves and 41.3 us with one (more,
-    // smaller workgroups re-stage every K/V tile for fewer rows).
-    const unsigned wgs = static_cast<unsigned>(((rows + 63) / 64) * heads);
-    hipLaunchKernelGGL((attention_prefill_kernel<64, 4>), dim3(wgs), dim3(256), 0, S(stream), q, k_cache, v_cache,
-                       pos, out, static_cast<int>(rows), static_cast<int>(heads), static_cast<int>(kv_heads),
-                       static_cast<int>(max_seq), sc);
+    const int split = attention_prefill_split(rows, heads);
+    const int r = static_cast<int>(rows), hd = static_cast<int>(heads), kvh = static_cast<int>(kv_heads),
+              ms = static_cast<int>(max_seq);
+    const int qr = 64 / split;   // query rows per workgroup
+    const dim3 grid(static_cast<unsigned>(((rows + qr - 1) / qr) * heads));
+    if (split == 1)
+        hipLaunchKernelGGL((attention_prefill_kernel<64, 4, 1>), grid, dim3(256), 0, S(stream), q, k_cache, v_cache,
+                           pos, out, r, hd, kvh, ms, sc);
+    else
+        hipLaunchKernelGGL((attention_prefill_kernel<64, 2, 2>), grid, dim3(256), 0, S(stream), q, k_cache, v_cache,
+                           pos, out, r, hd, kvh, ms, sc);
     return check_launch("attention_prefill", S(stream));
 }
 
