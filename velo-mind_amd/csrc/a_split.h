@@ -66,6 +66,16 @@ __device__ __forceinline__ void a_split8(const float4& p, const float4& q, int x
     }
 }
 
+// Workgroup b of a staging grid as a linear index whose runs of grid / 8
+// are dispatched to one XCD (workgroups go to the 8 XCDs round-robin by id):
+// the rows of a 128-byte line of operand-order pieces (8 rows x 16 bytes)
+// are then written by workgroups of one XCD, whose L2 merges the partial
+// lines, instead of being written back in pieces from several XCDs.
+__device__ __forceinline__ int a_stage_wg(int b, int grid) {
+    const int full = grid & ~7;
+    return b < full ? (b & 7) * (full >> 3) + (b >> 3) : b;
+}
+
 // 16-byte piece index of (row, 8-group g) in a buffer of k columns.
 template <bool PIECES>
 __device__ __forceinline__ int64_t a_piece(int64_t row, int g, int k) {

@@ -720,11 +720,12 @@ __global__ __launch_bounds__(256) void gemm_prep_frag_kernel(const float* __rest
                                                              int col_wgs) {
     __shared__ float wmax[4 * 256];
     const int tid = threadIdx.x;
-    if (static_cast<int>(blockIdx.x) < col_wgs) {
-        prep_col_pow(scale, col_pow, n, nblk, static_cast<int>(blockIdx.x), wmax);
+    const int wg = a_stage_wg(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+    if (wg < col_wgs) {
+        prep_col_pow(scale, col_pow, n, nblk, wg, wmax);
         return;
     }
-    const int row0 = (static_cast<int>(blockIdx.x) - col_wgs) * R;
+    const int row0 = (wg - col_wgs) * R;
     const int groups = k >> 3;
     float4 v[R][GT][2];
     float mx[R];
