@@ -104,6 +104,10 @@ private:
     auto _op_impl(OpDescriptor desc, std::vector<pConstTensorStorage> inputs) -> Tensor;
     auto _compute_required_nodes() const -> std::vector<bool>;
     auto _topological_order() const -> std::vector<pConstNode>;
+    auto _topological_order(const std::vector<bool>& req) const -> std::vector<pConstNode>;
+    // validate()'s checks; returns the topological order of the required
+    // nodes (the build's order, computed once).
+    auto _validated_order(DeviceType device) const -> std::vector<pConstNode>;
 
     friend struct GraphTestAccess;
     friend class internal::GraphCompiler;

@@ -167,8 +167,9 @@ auto Graph::_compute_required_nodes() const -> std::vector<bool> {
 
 // Kahn's algorithm over the required nodes, in insertion order among ready
 // nodes; throws on a cycle.
-auto Graph::_topological_order() const -> std::vector<pConstNode> {
-    const auto req = _compute_required_nodes();
+auto Graph::_topological_order() const -> std::vector<pConstNode> { return _topological_order(_compute_required_nodes()); }
+
+auto Graph::_topological_order(const std::vector<bool>& req) const -> std::vector<pConstNode> {
     std::unordered_map<pConstTensorStorage, std::size_t> producer;
     for (std::size_t i = 0; i < _nodes.size(); ++i)
         for (auto* o : _nodes[i].outputs()) producer[o] = i;
@@ -204,7 +205,9 @@ auto Graph::_topological_order() const -> std::vector<pConstNode> {
     return order;
 }
 
-auto Graph::validate(DeviceType device) const -> void {
+auto Graph::validate(DeviceType device) const -> void { (void)_validated_order(device); }
+
+auto Graph::_validated_order(DeviceType device) const -> std::vector<pConstNode> {
     if (_built) throw std::logic_error("Graph::validate: graph is already built");
     if (static_cast<std::size_t>(device) >= MAX_DEVICE_TYPES) throw std::invalid_argument("Graph::validate: invalid device");
     for (const auto& s : _tensors) {
@@ -227,7 +230,7 @@ auto Graph::validate(DeviceType device) const -> void {
         if (!internal::resolve_op_kernel(n.op().op, dtypes, out->dtype, device))
             throw std::invalid_argument(std::string("Graph::validate: unsupported kernel for ") + op_name(n.op().op));
     }
-    (void)_topological_order();
+    return _topological_order(req);
 }
 
 auto Graph::build(DeviceType device) -> std::unique_ptr<Executable> {

@@ -18,6 +18,7 @@
 #include "internal/graph_compiler.h"
 
 #include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <stdexcept>
 #include <string>
@@ -48,7 +49,12 @@ bool lifetimes_overlap(const Interval& a, const Interval& b) {
     return std::max(a.birth, b.birth) <= std::min(a.death, b.death);
 }
 
-// Places intervals; returns the arena size.
+// Places intervals; returns the arena size.  Lifetimes are inclusive
+// ranges of step indices, so two intersect exactly when they share a step:
+// the placed intervals alive at each step are kept in per-step lists, and
+// an interval's conflicts are gathered from the steps it spans instead of
+// from every interval placed before it (the scan over all earlier
+// intervals made a ~1000-node decode graph's plan quadratic).
 std::size_t plan_arena(std::vector<Interval>& items) {
     std::sort(items.begin(), items.end(), [](const Interval& a, const Interval& b) {
         if (a.bytes != b.bytes) return a.bytes > b.bytes;
@@ -57,13 +63,23 @@ std::size_t plan_arena(std::vector<Interval>& items) {
         if (a.birth != b.birth) return a.birth < b.birth;
         return a.tensor < b.tensor;
     });
+    std::size_t steps = 0;
+    for (const auto& it : items) steps = std::max(steps, it.death + 1);
+    std::vector<std::vector<std::size_t>> alive(steps);   // placed intervals per step
+    std::vector<std::size_t> seen(items.size(), SIZE_MAX);
+    std::vector<const Interval*> live;
+    std::vector<std::size_t> candidates;
     std::size_t total = 0;
     for (std::size_t i = 0; i < items.size(); ++i) {
         Interval& cur = items[i];
-        std::vector<const Interval*> live;
-        for (std::size_t j = 0; j < i; ++j)
-            if (lifetimes_overlap(items[j], cur)) live.push_back(&items[j]);
-        std::vector<std::size_t> candidates{0};
+        live.clear();
+        for (std::size_t st = cur.birth; st <= cur.death; ++st)
+            for (std::size_t j : alive[st])
+                if (seen[j] != i) {
+                    seen[j] = i;
+                    live.push_back(&items[j]);
+                }
+        candidates.assign(1, 0);
         for (const auto* p : live) candidates.push_back(p->offset + p->slot);
         std::sort(candidates.begin(), candidates.end());
         cur.offset = candidates.back();
@@ -80,6 +96,7 @@ std::size_t plan_arena(std::vector<Interval>& items) {
             }
         }
         total = std::max(total, cur.offset + cur.slot);
+        for (std::size_t st = cur.birth; st <= cur.death; ++st) alive[st].push_back(i);
     }
     return total;
 }
@@ -137,6 +154,11 @@ std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType de
     std::unordered_map<pConstTensorStorage, std::size_t> producer;
     for (std::size_t i = 0; i < order.size(); ++i)
         for (auto* out : order[i]->outputs()) producer.emplace(out, i);
+    // groupable nodes by the A they read, in order (siblings share A)
+    std::unordered_map<pConstTensorStorage, std::vector<std::size_t>> by_a;
+    if (group)
+        for (std::size_t i = 0; i < order.size(); ++i)
+            if (qmm_groupable(order[i])) by_a[order[i]->inputs()[0]].push_back(i);
     std::vector<bool> done(order.size(), false), taken(order.size(), false);
     std::vector<Step> steps;
     for (std::size_t i = 0; i < order.size(); ++i) {
@@ -144,8 +166,9 @@ std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType de
         std::vector<std::size_t> members{i};
         taken[i] = true;
         if (group && qmm_groupable(order[i])) {
-            for (std::size_t j = i + 1; j < order.size() && members.size() < kMaxQmmGroup; ++j) {
-                if (taken[j] || !qmm_siblings(order[i], order[j])) continue;
+            for (const std::size_t j : by_a.at(order[i]->inputs()[0])) {
+                if (members.size() >= kMaxQmmGroup) break;
+                if (j <= i || taken[j] || !qmm_siblings(order[i], order[j])) continue;
                 bool ready = true;
                 for (auto* in : order[j]->inputs()) {
                     const auto it = producer.find(in);
@@ -178,8 +201,7 @@ std::shared_ptr<TensorStorage> allocate_checked(std::size_t bytes, DeviceType de
 
 auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<Executable> {
     if (graph._built) throw std::logic_error("Graph::build: graph is already built");
-    graph.validate(device);
-    const auto order = graph._topological_order();
+    const auto order = graph._validated_order(device);
     const auto steps = plan_steps(order, device);
     const auto& tensors = graph._tensors;
 
