@@ -6,6 +6,7 @@
 // of tests/test_coverage_matrix.cpp:690-738.
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <thread>
@@ -290,6 +291,56 @@ TEST_CASE("HIP storages of a rebuilt graph come from the block cache", "[gpu][me
     REQUIRE(back == pattern);
     auto other = internal::create_tensor_storage(bytes, DeviceType::HIP);   // the class is empty again
     REQUIRE(other->data != p);
+}
+
+TEST_CASE("byte-preserving Reshape and Transpose steps view their input", "[gpu][memory]") {
+    REQUIRE_HIP();
+    // x + y -> Transpose moving a unit axis -> Reshape -> (+ itself), and a
+    // Transpose that does reorder bytes; results equal with the views on
+    // and off (VELOMIND_GRAPH_ALIAS=0), and an intermediate's bytes stay
+    // valid while a view of them is read later in the plan.
+    const auto a = normal(6 * 4, 41);
+    const auto b = normal(6 * 4, 42);
+    auto run = [&]() {
+        Graph g;
+        auto x = g.input({1, 6, 4}, DataType::Float32);
+        auto y = g.input({1, 6, 4}, DataType::Float32);
+        auto t1 = g.op(Op::Add, x, y);
+        auto t2 = g.op(OpDescriptor{Op::Transpose, TransposeAttrs{{1, 0, 2}}}, t1);    // [6, 1, 4], same bytes
+        auto t3 = g.op(OpDescriptor{Op::Reshape, ReshapeAttrs{shape_t{24}}}, t2);
+        auto t4 = g.op(OpDescriptor{Op::Transpose, TransposeAttrs{{0, 2, 1}}}, t1);    // [1, 4, 6], reordered
+        auto t5 = g.op(OpDescriptor{Op::Reshape, ReshapeAttrs{shape_t{24}}}, t4);
+        auto u = g.op(Op::Mul, x, y);   // more intermediates in flight
+        auto u2 = g.op(OpDescriptor{Op::Reshape, ReshapeAttrs{shape_t{24}}}, u);
+        auto o1 = g.op(Op::Add, t3, u2);
+        auto o2 = g.op(Op::Add, t5, t3);
+        g.mark_output(o1);
+        g.mark_output(o2);
+        auto exec = g.build(DeviceType::HIP);
+        x.copy_from_host(as_bytes(a));
+        y.copy_from_host(as_bytes(b));
+        exec->execute();
+        std::vector<float> r1(24), r2(24);
+        o1.copy_to_host(as_writeable_bytes(r1));
+        o2.copy_to_host(as_writeable_bytes(r2));
+        return std::make_pair(r1, r2);
+    };
+    const auto on = run();
+    ::setenv("VELOMIND_GRAPH_ALIAS", "0", 1);
+    const auto off = run();
+    ::unsetenv("VELOMIND_GRAPH_ALIAS");
+    REQUIRE(std::memcmp(on.first.data(), off.first.data(), 24 * 4) == 0);
+    REQUIRE(std::memcmp(on.second.data(), off.second.data(), 24 * 4) == 0);
+    for (int e = 0; e < 24; ++e) {
+        volatile float sum = a[e] + b[e], prod = a[e] * b[e];   // rounded as the device rounds them
+        REQUIRE(on.first[e] == sum + prod);
+    }
+    for (int j = 0; j < 4; ++j)
+        for (int i = 0; i < 6; ++i) {
+            const float t4 = a[i * 4 + j] + b[i * 4 + j];          // t1[i][j] at t4[j][i]
+            const float t3 = a[j * 6 + i] + b[j * 6 + i];          // t3 flat index j * 6 + i
+            REQUIRE(on.second[j * 6 + i] == t4 + t3);
+        }
 }
 
 TEST_CASE("bind_input uses an external device buffer", "[gpu][api]") {

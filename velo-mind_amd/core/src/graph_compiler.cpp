@@ -189,6 +189,38 @@ std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType de
     return steps;
 }
 
+// ---- byte-preserving nodes --------------------------------------------------
+// A Reshape, or a Transpose that keeps the order of every axis longer than
+// one, writes its input's bytes unchanged.  When input and output are both
+// arena intermediates, the output becomes a view of the input's bytes (the
+// input's lifetime extended over the output's) and the step launches
+// nothing: decode graphs of the reference's LLaMA layer hold ~110 such
+// Reshapes and ~140 such Transposes per token.  VELOMIND_GRAPH_ALIAS=0
+// keeps the copies.
+bool keeps_bytes(pConstNode n) {
+    const auto& op = n->op();
+    if (n->inputs().size() != 1 || n->outputs().size() != 1) return false;
+    const auto* in = n->inputs()[0];
+    const auto* out = n->outputs()[0];
+    if (in->dtype != out->dtype || in->size_bytes != out->size_bytes || !in->is_contiguous() ||
+        !out->is_contiguous())
+        return false;
+    if (op.op == Op::Reshape) return true;
+    if (op.op != Op::Transpose) return false;
+    const auto* ta = std::get_if<TransposeAttrs>(&op.attrs);
+    if (!ta || ta->perm.size() != in->shape.size()) return false;
+    int last = -1;
+    for (int axis : ta->perm) {
+        if (axis < 0 || static_cast<std::size_t>(axis) >= in->shape.size()) return false;
+        if (in->shape[static_cast<std::size_t>(axis)] == 1) continue;
+        if (axis < last) return false;
+        last = axis;
+    }
+    return true;
+}
+
+void no_launch(const pConstTensorStorage*, const pTensorStorage*, const void*) {}
+
 std::shared_ptr<TensorStorage> allocate_checked(std::size_t bytes, DeviceType device) {
     auto s = TensorStorage::allocate(bytes, device);
     if (!s || s->device != device || s->size_bytes < bytes || (bytes > 0 && s->data == nullptr))
@@ -246,9 +278,29 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     for (std::size_t i = 0; i < tensors.size(); ++i)
         if (tensors[i]->data != nullptr || graph.is_input_tensor(i)) dedicated[i] = true;
 
+    // Byte-preserving steps between arena intermediates: the output views
+    // its root's bytes, whose lifetime covers the output's.
+    std::vector<std::size_t> root(tensors.size());
+    for (std::size_t i = 0; i < tensors.size(); ++i) root[i] = i;
+    std::vector<bool> alias_step(steps.size(), false);
+    {
+        const char* env = std::getenv("VELOMIND_GRAPH_ALIAS");
+        if (!(env && env[0] == '0')) {
+            for (std::size_t step = 0; step < steps.size(); ++step) {
+                if (steps[step].size() != 1 || !keeps_bytes(steps[step].front())) continue;
+                const auto in = root[index_of.at(steps[step].front()->inputs()[0])];
+                const auto out = index_of.at(steps[step].front()->outputs()[0]);
+                if (dedicated[in] || dedicated[out] || tensors[in]->size_bytes == 0) continue;
+                root[out] = in;
+                death[in] = std::max(death[in], death[out]);
+                alias_step[step] = true;
+            }
+        }
+    }
+
     std::vector<Interval> arena_items;
     for (std::size_t i = 0; i < tensors.size(); ++i) {
-        if (!active[i] || dedicated[i] || tensors[i]->size_bytes == 0) continue;
+        if (!active[i] || dedicated[i] || root[i] != i || tensors[i]->size_bytes == 0) continue;
         arena_items.push_back(Interval{i, birth[i], std::max(birth[i], death[i]), tensors[i]->size_bytes,
                                        align_up(tensors[i]->size_bytes, kArenaAlignment), 0});
     }
@@ -304,6 +356,23 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         staged[i] = std::move(buf);
     }
 
+    for (std::size_t i = 0; i < tensors.size(); ++i) {
+        if (root[i] == i) continue;
+        const auto& src = *tensors[i];
+        const auto& base = staged[root[i]];
+        auto view = std::make_shared<TensorStorage>();
+        view->shape = src.shape;
+        view->strides = src.strides.empty() ? default_strides(src.shape) : src.strides;
+        view->dtype = src.dtype;
+        view->device = device;
+        view->size_bytes = src.size_bytes;
+        view->offset_bytes = base->offset_bytes;
+        view->capacity_bytes = base->capacity_bytes;
+        view->data = base->data;
+        view->external_owner = base->external_owner ? base->external_owner : std::shared_ptr<void>(base);
+        staged[i] = std::move(view);
+    }
+
     stats.peak_bytes = arena_bytes + dedicated_bytes;
     stats.intermediate_tensor_count = arena_items.size();
     std::size_t unshared = 0;
@@ -350,6 +419,7 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         }
         const auto* node = step.front();
         Executable::CompiledNode cn;
+        const bool aliased = alias_step[static_cast<std::size_t>(&step - steps.data())];
         std::vector<DataType> dtypes;
         for (auto* in : node->inputs()) {
             auto* s = remap.at(in);
@@ -361,7 +431,7 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
             cn.outputs.push_back(s);
         }
         if (cn.outputs.empty()) throw std::runtime_error("velomind: op node has no outputs");
-        cn.kernel = resolve_op_kernel(node->op().op, dtypes, node->outputs().front()->dtype, device);
+        cn.kernel = aliased ? &no_launch : resolve_op_kernel(node->op().op, dtypes, node->outputs().front()->dtype, device);
         if (!cn.kernel) throw std::runtime_error(std::string("velomind: no kernel for op=") + op_name(node->op().op));
         cn.attrs = std::shared_ptr<const void>(new OpDescriptor(node->op()),
                                                [](const void* p) { delete static_cast<const OpDescriptor*>(p); });
