@@ -15,6 +15,7 @@
 // per token; the argmax writes the next token where the embedding reads it
 // and advances the position.
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <stdexcept>
@@ -101,7 +102,9 @@ struct HipLlamaDecoder::Impl {
     // consumers add (vm_hip_qmm_gemv_slices_f32); counts per projection.
     bool sliced = false;
     int s_qkv = 0, s_o = 0, s_gu = 0, s_down = 0, s_lm = 0;
-    int lm_max = kMaxLm;   // slice limit of lm_head (VELOMIND_LM_SLICES overrides, sweeps)
+    // slice limits of q|k|v, o, gate|up, down, lm_head (the kMax* values;
+    // VELOMIND_SLICES_MAX="qkv,o,gu,down,lm" overrides them for sweeps)
+    int qkv_max = kMaxQkv, o_max = kMaxO, gu_max = kMaxGu, down_max = kMaxDown, lm_max = kMaxLm;
     DevBuf qkv_sl, o_sl, gu_sl, down_sl, lm_sl;
     DevBuf h2, ss_attn, ss_ffn, ss_final, att_part;   // second residual buffer, norm partials, attention records
     int att_chunk = 0, att_chunks = 0;
@@ -218,7 +221,7 @@ struct HipLlamaDecoder::Impl {
         attn_src.max_seq = static_cast<int>(max_seq);
         for (std::size_t l = 0; l < cfg.num_layers; ++l) {
             gemv_src(normres(ha, down_sl.as<float>(), l == 0 ? 0 : s_down, attn_norm[l]->data, hb, ss_attn.as<float>()),
-                     qkv[l], qkv_sl.as<float>(), kMaxQkv);
+                     qkv[l], qkv_sl.as<float>(), qkv_max);
             // Attention leaves most CUs idle: its extra workgroups read the
             // output and gate|up projections' weights into the Infinity
             // Cache for the two launches after it (measured on MI355X:
@@ -239,9 +242,9 @@ struct HipLlamaDecoder::Impl {
                       sin_t.as<float>(), posp, kc(l), vc(l), att_part.as<float>(), H, Hk, D,
                       static_cast<std::int64_t>(max_seq), 1.0f, &pf, stream),
                   "attention_decode");
-            gemv_src(attn_src, o[l], o_sl.as<float>(), kMaxO);
+            gemv_src(attn_src, o[l], o_sl.as<float>(), o_max);
             gemv_src(normres(hb, o_sl.as<float>(), s_o, ffn_norm[l]->data, ha, ss_ffn.as<float>()), gate_up[l],
-                     gu_sl.as<float>(), kMaxGu);
+                     gu_sl.as<float>(), gu_max);
             vm_hip_gemv_src sw{};
             sw.kind = VM_HIP_GEMV_SRC_SWIGLU;
             sw.act = gu_sl.as<float>();
@@ -250,7 +253,7 @@ struct HipLlamaDecoder::Impl {
             sw.ss_count = s_gu;
             sw.ss_dim = dim;
             sw.eps = eps;
-            gemv_src(sw, down[l], down_sl.as<float>(), kMaxDown);
+            gemv_src(sw, down[l], down_sl.as<float>(), down_max);
         }
         gemv_src(normres(ha, down_sl.as<float>(), s_down, final_norm->data, nullptr, ss_final.as<float>()), lm_head,
                  lm_sl.as<float>(), lm_max);
@@ -495,12 +498,29 @@ void HipLlamaDecoder::Impl::allocate() {
     m.token = DevBuf(4);
     m.pos = DevBuf(4);
     m.tokens = DevBuf(rows * 4);
-    m.s_qkv = m.slices_for(m.qkv[0], Impl::kMaxQkv);
-    m.s_o = m.slices_for(m.o[0], Impl::kMaxO);
-    m.s_gu = m.slices_for(m.gate_up[0], Impl::kMaxGu);
-    m.s_down = m.slices_for(m.down[0], Impl::kMaxDown);
-    m.lm_max = Impl::kMaxLm;
-    if (const char* e = std::getenv("VELOMIND_LM_SLICES")) m.lm_max = std::max(1, std::min(32, std::atoi(e)));
+    if (const char* e = std::getenv("VELOMIND_SLICES_MAX")) {
+        int v[5] = {m.qkv_max, m.o_max, m.gu_max, m.down_max, m.lm_max};
+        if (std::sscanf(e, "%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4]) == 5 &&
+            std::all_of(v, v + 5, [](int x) { return x >= 1 && x <= 64; })) {
+            m.qkv_max = v[0];
+            m.o_max = v[1];
+            m.gu_max = v[2];
+            m.down_max = v[3];
+            m.lm_max = v[4];
+        }
+    }
+    m.s_qkv = m.slices_for(m.qkv[0], m.qkv_max);
+    m.s_o = m.slices_for(m.o[0], m.o_max);
+    m.s_gu = m.slices_for(m.gate_up[0], m.gu_max);
+    // down: twice the slices (four-wave workgroups instead of eight) while
+    // the grid stays within one workgroup per CU (SmolLM2-360M, N = 960: 80
+    // -> 160 workgroups, decode 891.7 -> 850.2 us/token; TinyLlama's 176
+    // would become 352 and slow down, 687.8 -> 699.6).
+    if (!std::getenv("VELOMIND_SLICES_MAX")) {
+        const int wide = m.slices_for(m.down[0], 2 * m.down_max);
+        if (wide > 0 && static_cast<std::int64_t>(wide) * ((m.down[0].n + 255) / 256) <= 256) m.down_max *= 2;
+    }
+    m.s_down = m.slices_for(m.down[0], m.down_max);
     m.s_lm = m.slices_for(m.lm_head, m.lm_max);
     m.sliced = m.s_qkv && m.s_o && m.s_gu && m.s_down && m.s_lm && m.hidden % 4 == 0 && m.inter % 4 == 0 &&
                m.H * m.D == m.hidden &&
