@@ -4,6 +4,8 @@
 // test_helpers.cpp).  Cases mirror the reference's
 // tests/test_quantization.cpp:57-98 and :413-478, tests/test_basic.cpp:139-145
 // and tests/test_validation.cpp:133-167.
+#include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 #include <variant>
 
@@ -218,6 +220,51 @@ TEST_CASE("memory plan: intermediates share one arena", "[core][memory]") {
     for (std::size_t i = 0; i < g.tensor_count(); ++i)
         if (g.tensor_storage_at(i)->is_alias()) ++aliases;
     REQUIRE(aliases == 5);
+}
+
+TEST_CASE("a Reshape between intermediates is a view of its input", "[core][memory]") {
+    // QMM -> Reshape -> QMM -> Reshape -> QMM: the Reshapes' outputs point at
+    // their inputs' bytes (and take no arena slot) unless
+    // VELOMIND_GRAPH_ALIAS=0; results are identical either way.
+    const std::size_t k = 64;
+    const auto w = normal(k * k, 51, 0.05f);
+    std::vector<std::int8_t> q(k * k);
+    std::vector<float> sc(k);
+    vmo_quantize_int8_per_channel(w.data(), q.data(), sc.data(), k, k);
+    const auto a = normal(k, 52);
+    auto run = [&](bool views) {
+        if (!views) ::setenv("VELOMIND_GRAPH_ALIAS", "0", 1);
+        Graph g;
+        auto x = g.input({1, (dim_t)k}, DataType::Float32);
+        auto tw = g.input({(dim_t)k, (dim_t)k}, DataType::Int8);
+        auto ts = g.input({(dim_t)k}, DataType::Float32);
+        auto h1 = g.op(Op::QuantizedMatMul, x, tw, ts);
+        auto r1 = g.op(OpDescriptor{Op::Reshape, ReshapeAttrs{shape_t{1, 1, (dim_t)k}}}, h1);
+        auto h2 = g.op(Op::QuantizedMatMul, r1, tw, ts);
+        auto r2 = g.op(OpDescriptor{Op::Reshape, ReshapeAttrs{shape_t{1, (dim_t)k}}}, h2);
+        auto y = g.op(Op::QuantizedMatMul, r2, tw, ts);
+        g.mark_output(y);
+        auto exec = g.build(DeviceType::CPU);
+        ::unsetenv("VELOMIND_GRAPH_ALIAS");
+        REQUIRE((g.tensor_storage_at(r1.index())->data == g.tensor_storage_at(h1.index())->data) == views);
+        REQUIRE((g.tensor_storage_at(r2.index())->data == g.tensor_storage_at(h2.index())->data) == views);
+        REQUIRE(exec->memory_plan_stats().intermediate_tensor_count == (views ? 2u : 4u));
+        x.copy_from_host(as_bytes(a));
+        tw.copy_from_host(as_bytes(q));
+        ts.copy_from_host(as_bytes(sc));
+        exec->execute();
+        std::vector<float> out(k);
+        y.copy_to_host(as_writeable_bytes(out));
+        return out;
+    };
+    const auto on = run(true);
+    const auto off = run(false);
+    REQUIRE(std::memcmp(on.data(), off.data(), k * 4) == 0);
+    std::vector<float> h(k), h2(k), ref(k);
+    vmo_qmm_2d_f32(a.data(), q.data(), sc.data(), h.data(), 1, k, k, 1, 0);
+    vmo_qmm_2d_f32(h.data(), q.data(), sc.data(), h2.data(), 1, k, k, 1, 0);
+    vmo_qmm_2d_f32(h2.data(), q.data(), sc.data(), ref.data(), 1, k, k, 1, 0);
+    REQUIRE(std::memcmp(on.data(), ref.data(), k * 4) == 0);
 }
 
 TEST_CASE("dead nodes are eliminated when outputs are marked", "[core][memory]") {

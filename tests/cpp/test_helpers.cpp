@@ -1,6 +1,7 @@
 // Registers the oracle as the CPU QuantizedMatMul kernel of the test binary.
 #include "test_helpers.h"
 
+#include <cstring>
 #include <variant>
 
 #include "internal/registry/kernel.h"
@@ -20,7 +21,17 @@ void oracle_qmm_cpu(const velomind::pConstTensorStorage* in, const velomind::pTe
                    static_cast<int>(qa.quant_type), qa.block_size);
 }
 
+// Reshape on the host: a byte copy into the output's shape.
+void copy_reshape_cpu(const velomind::pConstTensorStorage* in, const velomind::pTensorStorage* out, const void*) {
+    std::memcpy(out[0]->data, in[0]->data, in[0]->size_bytes);
+}
+
 }  // namespace
+
+VELOMIND_REGISTER_OP_KERNEL(::velomind::DeviceType::CPU, ::velomind::Op::Reshape,
+                            (::velomind::internal::KernelDtypeKey{{::velomind::DataType::Float32}, 1,
+                                                                  ::velomind::DataType::Float32}),
+                            &copy_reshape_cpu)
 
 VELOMIND_REGISTER_OP_KERNEL(::velomind::DeviceType::CPU, ::velomind::Op::QuantizedMatMul,
                             (::velomind::internal::KernelDtypeKey{
