@@ -485,27 +485,6 @@ def decode_trace_report(tokens: int = 8) -> dict:
             "argmax_us": round(float(us[0, L, 4] - np.median(us[:, L, 2])), 2)}
 
 
-def handoff_probe(H, stream, rounds: int = 2000) -> list:
-    """The platform diagnostic behind the one-launch decode step's limits
-    (vm_hip_diag_handoff): microseconds per all-to-all hand-off of tagged
-    words between workgroups (one per compute unit), alone, beside compute
-    units streaming HBM, after each workgroup streams a share of its own,
-    and with streaming waves on the same compute units."""
-    lib = H.open_library()
-    cases = [(0, 32, 0), (0, 128, 0), (0, 256, 0), (1, 224, 0), (1, 192, 0), (1, 128, 0),
-             (2, 256, 8), (2, 256, 16), (2, 256, 32), (2, 256, 64), (3, 256, 1), (3, 256, 2), (3, 256, 4)]
-    names = {0: "alone", 1: "other CUs stream HBM", 2: "each workgroup first streams kb KiB",
-             3: "kb waves of each workgroup stream HBM"}
-    out = []
-    for mode, parts, kb in cases:
-        us, gbs = ctypes.c_double(0.0), ctypes.c_double(0.0)
-        H.check(lib.vm_hip_diag_handoff(mode, parts, kb, rounds, ctypes.byref(us), ctypes.byref(gbs), stream.handle))
-        out.append({"mode": names[mode], "participants": parts, "kb": kb, "us_per_handoff": round(us.value, 3),
-                    "stream_GB_s": round(gbs.value, 1)})
-        log(f"bench: hand-off {names[mode]} P={parts} kb={kb}: {us.value:.3f} us, streaming {gbs.value:.0f} GB/s")
-    return out
-
-
 GEMM_K, GEMM_N = 2048, 5632
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -728,8 +707,6 @@ def main() -> int:
     ap.add_argument("--decode-trace", action="store_true",
                     help="only the one-launch decode step's phase timestamps (library built with "
                          "VELOMIND_DECODE_TRACE=1), printed as one JSON line")
-    ap.add_argument("--handoff-probe", action="store_true",
-                    help="only the platform hand-off diagnostic (vm_hip_diag_handoff), printed as one JSON line")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg (config 3)")
     ap.add_argument("--no-large", action="store_true", help="skip the 70B-class decode GEMV leg")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg, printed as one JSON line")
@@ -769,9 +746,6 @@ def main() -> int:
         return 0
     if args.decode_trace:
         print(json.dumps({"metric": METRIC, "decode_trace": decode_trace_report()}), flush=True)
-        return 0
-    if args.handoff_probe:
-        print(json.dumps({"metric": METRIC, "handoff_probe": handoff_probe(H, stream)}), flush=True)
         return 0
     if args.gemm_only:
         print(json.dumps({"metric": METRIC, "gemm": gemm_bench(H, stream)}), flush=True)

@@ -591,7 +591,8 @@ int vm_hip_decode_trace_read(void* host, int64_t bytes);
  * significant bits), row-major or in the wide MFMA kernel's operand order.
  * A producer that holds whole rows can write that layout itself instead:
  * vm_hip_qmm_a_layout says which layout (VM_HIP_A_FP32: the shape takes
- * fp32 A only) and how many bytes the staged buffer needs for a call;
+ * fp32 A only, as every row longer than 6144 does, the producers' limit)
+ * and how many bytes the staged buffer needs for a call;
  * vm_hip_add_rmsnorm_stage_f32 (vm_hip_add_rmsnorm_f32's arithmetic) and
  * vm_hip_silu_mul_stage_f32 (vm_hip_silu_mul_f32's) write it, with the fp32
  * rows too when hn_out / out_f32 is given; vm_hip_qmm_staged_f32 runs the
@@ -612,23 +613,6 @@ int vm_hip_add_rmsnorm_stage_f32(float* h, const float* delta, const float* w, v
                                  float* hn_out, int64_t rows, int64_t dim, float eps, void* stream);
 int vm_hip_silu_mul_stage_f32(const float* gate_up, void* a_staged, int layout, float* out_f32, int64_t rows,
                               int64_t inter, void* stream);
-
-/* ---- Platform diagnostic (no reference counterpart) --------------------
- * The cost of an all-to-all hand-off inside one launch, the primitive a
- * one-launch decode step is built from (diag_handoff.hip): `participants`
- * workgroups, one per compute unit, each store 8 tagged 64-bit words per
- * round and poll everyone's words at agent scope.  Modes: ALONE; STREAM_CUS
- * (the other compute units stream HBM meanwhile); STREAM_FIRST (each
- * participant first streams `kb` KiB, then polls); STREAM_WAVES (`kb` = 1..4
- * extra waves of each participant stream HBM continuously).  Writes
- * microseconds per round (slowest participant) and the GB/s the streaming
- * loads reached; allocates 1 GiB for the duration of the call. */
-#define VM_HIP_DIAG_ALONE        0
-#define VM_HIP_DIAG_STREAM_CUS   1
-#define VM_HIP_DIAG_STREAM_FIRST 2
-#define VM_HIP_DIAG_STREAM_WAVES 3
-int vm_hip_diag_handoff(int mode, int participants, int kb, int rounds, double* us_per_round, double* stream_gb_s,
-                        void* stream);
 
 #ifdef __cplusplus
 }

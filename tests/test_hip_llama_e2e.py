@@ -52,9 +52,9 @@ def _toy():
     return cfg, L.load_toy_llama(load_file(os.path.join(GOLDEN, "model.safetensors")), cfg)
 
 
-def _gqa(seed=11):
+def _gqa(seed=11, intermediate=384):
     # head_dim 64 (the resident decoder's fast path), 4 query heads per KV head.
-    cfg = L.LlamaConfig(vocab_size=300, hidden_size=512, intermediate_size=384, num_layers=2, num_heads=8,
+    cfg = L.LlamaConfig(vocab_size=300, hidden_size=512, intermediate_size=intermediate, num_layers=2, num_heads=8,
                         num_kv_heads=2, rms_norm_eps=1e-5, rope_theta=10000.0)
     rng = np.random.default_rng(seed)
     n = lambda *s: (rng.standard_normal(s) * 0.05).astype(np.float32)  # noqa: E731
@@ -127,6 +127,22 @@ def test_resident_decoder_matches_oracle(llama, qt, block):
     prompt = list(range(7, 7 + 70, 3))[:19]
     ref, _ = L.prefill(cfg, ow, prompt, last_only=True)
     _close(s.prefill(prompt), ref[0], 1e-4, "prefill 19")
+
+
+@pytest.mark.parametrize("qt,block", QUANTS[1:])
+def test_resident_prefill_rows_beyond_the_staging_limit(llama, qt, block):
+    """An intermediate size above the 6144 the activation-staging producers
+    take: the down projection's prompt GEMM gets fp32 activations instead
+    (vm_hip_qmm_a_layout reports VM_HIP_A_FP32), and prompts long enough
+    for the GEMM path still match the oracle."""
+    cfg, w = _gqa(seed=13, intermediate=6400)
+    ow = _oracle_weights(w, qt, block)
+    s = llama.Session(llama.Weights.from_oracle(cfg, w), llama.ENGINE_RESIDENT, qt, block, max_seq=64)
+    print(f"case resident intermediate 6400 qt={qt}", flush=True)
+    prompt = list(range(11, 11 + 19))
+    ref, kv = L.prefill(cfg, ow, prompt, last_only=True)
+    _close(s.prefill(prompt), ref[0], 1e-4, "prefill 19")
+    _close(s.forward_step(3, 19), L.decode(cfg, ow, 3, 19, kv)[0], 1e-4, "decode pos 19")
 
 
 @pytest.mark.parametrize("qt,block", QUANTS[1:])

@@ -89,10 +89,14 @@ def test_noalloc_refuses_scratch_beyond_its_array(hip):
     dw = hip.DeviceBuffer(k // 2 * n)
     ds = hip.DeviceBuffer(k // 32 * n * 4)
     dc = hip.DeviceBuffer(m * n * 4)
+    sentinel = np.full((m, n), 7.25, np.float32)
+    dc.upload(sentinel)
     with pytest.raises(hip.VmHipError) as info:
         hip.qmm_f32_noalloc(da.addr, dw.addr, ds.addr, dc.addr, m, k, n, O.QUANT_INT4, 32)
     assert info.value.status == hip.EINVAL
     assert "static scratch" in str(info.value)
     hip.synchronize()
+    # a refused call leaves the output unwritten
+    assert np.array_equal(dc.download(np.float32, (m, n)), sentinel)
     # the entry point keeps working after a refusal
     _check(hip, 31, 16, 2048, 5632, O.QUANT_INT4)

@@ -11,12 +11,11 @@
 // destroys the Executable's stream.  On HIP those calls cost more than the
 // token's kernels (hipFree synchronizes the device; a stream creation
 // takes ~0.7 ms), so the backend keeps them:
-//   * storages come from a per-device block cache in size classes (eight
-//     per power of two, so a K/V cache that grows by a row usually keeps
-//     its class).  A freed block is parked, and becomes reusable only after
-//     a device-wide synchronization that began after it was freed -- the
-//     guarantee hipFree gives -- which the allocator performs itself when a
-//     request finds only parked blocks of its class;
+//   * storages come from a per-device block cache in size classes
+//     (block_cache.h): a freed block is parked, and becomes reusable only
+//     after a device-wide synchronization that began after it was freed --
+//     the guarantee hipFree gives; when the device allocator fails, the
+//     cache gives its blocks back and the allocation is tried again;
 //   * Executable streams come from a per-device pool and return to it
 //     (synchronized) when the Executable is destroyed, keeping the
 //     stream's split-K and staging workspaces;
@@ -28,6 +27,7 @@
 #include <string>
 #include <vector>
 
+#include "backend_hip/block_cache.h"
 #include "backend_hip/hip_runtime.h"
 #include "internal/registry/device_context.h"
 #include "internal/registry/memory_transfer.h"
@@ -44,85 +44,28 @@ int current_device_or_zero() {
     return vm_hip_get_device(&d) == VM_HIP_OK ? d : 0;
 }
 
-// ---- storage block cache
-constexpr std::size_t kMinClass = 256;
-constexpr std::size_t kMaxCachedBytes = std::size_t(8) << 30;   // parked + free, per process
+// ---- storage block cache (block_cache.h)
+constexpr std::size_t kMaxCachedBytes = std::size_t(8) << 30;   // parked + idle, per process
 
-// Size class of a request: 256-byte multiples up to 2 KiB, then eight
-// classes per power of two.
-std::size_t size_class(std::size_t bytes) {
-    if (bytes <= 8 * kMinClass) return (bytes + kMinClass - 1) / kMinClass * kMinClass;
-    std::size_t p = 1;
-    while (p * 2 <= bytes) p *= 2;   // p <= bytes < 2p
-    const std::size_t step = p / 8;
-    return (bytes + step - 1) / step * step;
+BlockCache& block_cache() {
+    static BlockCache* c = new BlockCache(   // outlives every storage (never destroyed)
+        BlockOps{[](void** p, std::size_t n) { return vm_hip_malloc(p, n); }, [](void* p) { return vm_hip_free(p); },
+                 [] { return vm_hip_device_synchronize(); }},
+        kMaxCachedBytes);
+    return *c;
 }
-
-struct BlockCache {
-    struct PerDevice {
-        std::map<std::size_t, std::vector<void*>> ready;    // idle: reusable now
-        std::map<std::size_t, std::vector<void*>> parked;   // freed since the last device synchronization
-        std::size_t parked_count = 0;
-    };
-    std::mutex mu;
-    std::map<int, PerDevice> dev;
-    std::size_t cached_bytes = 0;
-
-    static BlockCache& get() {
-        static BlockCache* c = new BlockCache();   // outlives every storage (never destroyed)
-        return *c;
-    }
-
-    void* take(int d, std::size_t cls) {
-        std::lock_guard<std::mutex> lock(mu);
-        PerDevice& pd = dev[d];
-        auto it = pd.ready.find(cls);
-        if (it == pd.ready.end() || it->second.empty()) {
-            auto pk = pd.parked.find(cls);
-            if (pk == pd.parked.end() || pk->second.empty()) return nullptr;
-            // every parked block of this device becomes idle once the
-            // device has drained
-            if (vm_hip_device_synchronize() != VM_HIP_OK) return nullptr;
-            for (auto& [c, v] : pd.parked) {
-                auto& r = pd.ready[c];
-                r.insert(r.end(), v.begin(), v.end());
-            }
-            pd.parked.clear();
-            pd.parked_count = 0;
-            it = pd.ready.find(cls);
-        }
-        void* p = it->second.back();
-        it->second.pop_back();
-        cached_bytes -= cls;
-        return p;
-    }
-
-    // false: the cache is full, the caller frees the block itself
-    bool park(int d, std::size_t cls, void* p) {
-        std::lock_guard<std::mutex> lock(mu);
-        if (cached_bytes + cls > kMaxCachedBytes) return false;
-        PerDevice& pd = dev[d];
-        pd.parked[cls].push_back(p);
-        ++pd.parked_count;
-        cached_bytes += cls;
-        return true;
-    }
-};
 
 std::shared_ptr<TensorStorage> hip_allocate(std::size_t bytes) {
     void* block = nullptr;
-    const std::size_t cls = bytes > 0 ? size_class(bytes) : 0;
+    const std::size_t cls = bytes > 0 ? block_size_class(bytes) : 0;
     const int d = current_device_or_zero();
     if (cls > 0) {
-        block = BlockCache::get().take(d, cls);
-        if (!block) {
-            const int rc = vm_hip_malloc(&block, cls);
-            if (rc != VM_HIP_OK) throw std::runtime_error(vm_hip_last_error());
-        }
+        block = block_cache().allocate(d, cls);
+        if (!block) throw std::runtime_error(vm_hip_last_error());
     }
     // The deleter keeps the original pointer: bind_input may rebind data.
     auto s = std::shared_ptr<TensorStorage>(new TensorStorage{}, [block, cls, d](TensorStorage* p) {
-        if (block && !BlockCache::get().park(d, cls, block)) (void)vm_hip_free(block);
+        if (block) (void)block_cache().park(d, cls, block);
         delete p;
     });
     s->size_bytes = bytes;

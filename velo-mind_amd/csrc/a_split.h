@@ -23,6 +23,10 @@ namespace vmhip {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
+// Longest row the staging producers write (three 8-groups per thread of a
+// 256-thread workgroup holding the whole row).
+constexpr int64_t kStageMaxK = 6144;
+
 // Rows padded for the layout, and the staged buffer's parts.
 inline int64_t a_stage_rows(int64_t m, bool pieces) { return pieces ? (m + 31) / 32 * 32 : m; }
 inline std::size_t a_stage_half_bytes(int64_t m, int64_t k, bool pieces) {

@@ -1408,7 +1408,8 @@ int check_stage(const void* a_staged, int layout, int64_t rows, int64_t k, const
     if (layout != VM_HIP_A_ROWS && layout != VM_HIP_A_PIECES)
         return fail_inval(std::string(who) + ": layout must be VM_HIP_A_ROWS or VM_HIP_A_PIECES");
     if (!a_staged) return fail_inval(std::string(who) + ": null staged buffer");
-    if (k % 32 != 0 || k > 3 * 8 * kT) return fail_inval(std::string(who) + ": the row length must be a multiple of 32, at most 6144");
+    static_assert(3 * 8 * kT == kStageMaxK, "staging row limit");
+    if (k % 32 != 0 || k > kStageMaxK) return fail_inval(std::string(who) + ": the row length must be a multiple of 32, at most 6144");
     if (rows > 0x7fffffff / 2) return fail_inval(std::string(who) + ": too many rows");
     if (!aligned16(a_staged)) return fail_inval(std::string(who) + ": the staged buffer must be 16-byte aligned");
     return 0;

@@ -1266,8 +1266,8 @@ struct Layout {
 };
 
 int cooperative_grid(int* G) {
-    static std::mutex mu;
-    static std::map<int, int> cache;
+    static std::mutex& mu = *new std::mutex;            // never destroyed (usable during exit)
+    static std::map<int, int>& cache = *new std::map<int, int>;
     int dev = 0;
     VM_TRY_HIP(hipGetDevice(&dev), "decode_step: hipGetDevice");
     std::lock_guard<std::mutex> lock(mu);

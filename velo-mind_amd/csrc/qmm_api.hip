@@ -183,6 +183,9 @@ int vm_hip_qmm_a_layout(int64_t rows_m, int64_t k, int64_t n, int quant_type, in
     *layout = VM_HIP_A_FP32;
     *bytes = 0;
     if (rows_m > INT32_MAX) return 0;
+    // Staged layouts only for rows the staging producers take (the two
+    // fp16 parts of a whole row held by one workgroup: k <= 6144).
+    if (k > kStageMaxK) return 0;
     const int bs = (quant_type == VM_HIP_QUANT_INT4 && block_size <= 0) ? 32 : block_size;
     GemmPlan plan;
     if (gemm_plan(static_cast<int>(rows_m), static_cast<int>(k), static_cast<int>(n), quant_type, bs, &plan) != 0) {

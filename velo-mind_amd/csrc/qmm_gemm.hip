@@ -1490,6 +1490,9 @@ WideConfig choose_wide(int kind, int m, int k, int n) {
 }
 
 bool use_wide_kernel(int kind, int m, int k, int n) {
+    // The wide kernel writes C with 32-bit byte offsets (the small-tile
+    // kernel addresses it with 64-bit pointers), whatever the overrides say.
+    if (static_cast<int64_t>(m) * n * 4 >= (int64_t(1) << 31)) return false;
     if (std::getenv("VELOMIND_GEMM_CFG")) return false;
     const char* env = std::getenv("VELOMIND_GEMM_WIDE");
     if (env && env[0] == '0' && env[1] == '\0') return false;

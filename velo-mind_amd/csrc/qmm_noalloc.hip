@@ -16,7 +16,10 @@
 // address, until the process ends.  Every call on one GPU shares it: calls
 // that overlap on one GPU (different streams, or host threads) race and
 // must be serialized by the caller.  Shapes whose scratch would exceed the
-// array are rejected with VM_HIP_EINVAL before anything is launched.
+// array are rejected with VM_HIP_EINVAL and leave the output unwritten; a
+// refused MFMA GEMM call (more than 4 rows) may already have launched its
+// A-staging kernel into the array's staging area, whose contents no call
+// relies on (every call stages its own A before reading it).
 #include <hip/hip_runtime.h>
 
 #include <cstddef>

@@ -28,15 +28,12 @@ struct WsEntry {
     std::vector<void*> retired;
 };
 
-std::mutex g_ws_mutex;
-std::map<std::pair<int, hipStream_t>, WsEntry> g_ws;
 
 struct StagingEntry {
     void*       base = nullptr;
     std::size_t bytes = 0;
     std::vector<void*> retired;
 };
-std::map<std::pair<int, hipStream_t>, StagingEntry> g_staging;
 
 thread_local FixedRegion* t_fixed = nullptr;
 
@@ -45,7 +42,23 @@ struct AuxEntry {
     std::size_t bytes = 0;
     std::vector<void*> retired;
 };
-std::map<std::pair<int, hipStream_t>, AuxEntry> g_aux;
+// The per-(device, stream) buffers and their lock, created on first use and
+// never destroyed: streams can be destroyed from finalizers that run while
+// the process exits (Python objects, static destructors of other
+// libraries), after namespace-scope objects of this library would already
+// be gone.  The buffers themselves are freed with their stream, and the
+// driver reclaims whatever is left at exit.
+struct Registries {
+    std::mutex mutex;
+    std::map<std::pair<int, hipStream_t>, WsEntry> ws;
+    std::map<std::pair<int, hipStream_t>, StagingEntry> staging;
+    std::map<std::pair<int, hipStream_t>, AuxEntry> aux;
+};
+
+Registries& registries() {
+    static Registries* r = new Registries;
+    return *r;
+}
 
 int current_device() {
     int dev = 0;
@@ -125,8 +138,9 @@ int get_workspace(hipStream_t stream, std::size_t partial_floats, std::size_t co
         return 0;
     }
     const int dev = current_device();
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    WsEntry& e = g_ws[{dev, stream}];
+    Registries& reg = registries();
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    WsEntry& e = reg.ws[{dev, stream}];
     if (e.base == nullptr || e.partial_floats < partial_floats || e.counter_slots < counter_slots) {
         if (stream != nullptr) {
             hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -178,8 +192,9 @@ int get_aux(hipStream_t stream, std::size_t bytes, void** out) {
         return 0;
     }
     const int dev = current_device();
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    AuxEntry& e = g_aux[{dev, stream}];
+    Registries& reg = registries();
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    AuxEntry& e = reg.aux[{dev, stream}];
     if (e.base == nullptr || e.bytes < bytes) {
         if (stream != nullptr) {
             hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -201,24 +216,25 @@ int get_aux(hipStream_t stream, std::size_t bytes, void** out) {
 
 void release_workspace(hipStream_t stream) {
     const int dev = current_device();
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    auto it = g_ws.find({dev, stream});
-    if (it != g_ws.end()) {
+    Registries& reg = registries();
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    auto it = reg.ws.find({dev, stream});
+    if (it != reg.ws.end()) {
         if (it->second.base) (void)hipFree(it->second.base);
         for (void* p : it->second.retired) (void)hipFree(p);
-        g_ws.erase(it);
+        reg.ws.erase(it);
     }
-    auto ax = g_aux.find({dev, stream});
-    if (ax != g_aux.end()) {
+    auto ax = reg.aux.find({dev, stream});
+    if (ax != reg.aux.end()) {
         if (ax->second.base) (void)hipFree(ax->second.base);
         for (void* p : ax->second.retired) (void)hipFree(p);
-        g_aux.erase(ax);
+        reg.aux.erase(ax);
     }
-    auto st = g_staging.find({dev, stream});
-    if (st != g_staging.end()) {
+    auto st = reg.staging.find({dev, stream});
+    if (st != reg.staging.end()) {
         if (st->second.base) (void)hipFree(st->second.base);
         for (void* p : st->second.retired) (void)hipFree(p);
-        g_staging.erase(st);
+        reg.staging.erase(st);
     }
 }
 
@@ -226,8 +242,9 @@ int get_staging(hipStream_t stream, std::size_t bytes, void** out) {
     if (const FixedRegion* f = t_fixed)
         return fail_inval(std::string(f->who) + ": dtype staging would allocate; only fp32 operands are accepted");
     const int dev = current_device();
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    StagingEntry& e = g_staging[{dev, stream}];
+    Registries& reg = registries();
+    std::lock_guard<std::mutex> lock(reg.mutex);
+    StagingEntry& e = reg.staging[{dev, stream}];
     if (e.base == nullptr || e.bytes < bytes) {
         if (stream != nullptr) {
             hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -248,8 +265,9 @@ int get_staging(hipStream_t stream, std::size_t bytes, void** out) {
 }
 
 int cu_count() {
-    static std::mutex m;
-    static std::map<int, int> cache;
+    // never destroyed, like the buffer registries (usable during exit)
+    static std::mutex& m = *new std::mutex;
+    static std::map<int, int>& cache = *new std::map<int, int>;
     const int dev = current_device();
     std::lock_guard<std::mutex> lock(m);
     auto it = cache.find(dev);

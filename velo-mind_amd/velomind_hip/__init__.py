@@ -21,6 +21,7 @@ QUANT_INT8 = 1
 QUANT_INT4 = 2
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 4, 5
 EINVAL, EUNSUPPORTED, EINJECTED, ENODEVICE = -1, -2, -3, -4
+A_FP32, A_ROWS, A_PIECES = 0, 1, 2   # prefill GEMM activation layouts (vm_hip_qmm_a_layout)
 
 _lib: ctypes.CDLL | None = None
 
@@ -121,8 +122,6 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_attention_decode_slices_prefetch_f32": ([p, c_int64, p, c_int64, c_float, c_float, p, p, p, p, p, p,
                                                          c_int64, c_int64, c_int64, c_int64, c_float,
                                                          POINTER(Prefetch), p], c_int),
-        "vm_hip_diag_handoff": ([c_int, c_int, c_int, c_int, POINTER(ctypes.c_double), POINTER(ctypes.c_double), p],
-                                c_int),
         "vm_hip_qmm_a_layout": ([c_int64, c_int64, c_int64, c_int, c_int, POINTER(c_int), POINTER(c_int64)], c_int),
         "vm_hip_qmm_col_pow": ([p, p, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_qmm_staged_f32": ([p, p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
@@ -156,7 +155,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_qmm_gemv_slices_src_f32", "vm_hip_attention_decode_chunks", "vm_hip_attention_decode_slices_f32",
             "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32",
             "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32", "vm_hip_decode_workspace_bytes",
-            "vm_hip_decode_step", "vm_hip_decode_status", "vm_hip_decode_trace_read", "vm_hip_diag_handoff",
+            "vm_hip_decode_step", "vm_hip_decode_status", "vm_hip_decode_trace_read",
             "vm_hip_qmm_a_layout", "vm_hip_qmm_col_pow", "vm_hip_qmm_staged_f32", "vm_hip_add_rmsnorm_stage_f32",
             "vm_hip_silu_mul_stage_f32"]
 
