@@ -67,28 +67,6 @@ __device__ __forceinline__ float dpp_row_ror(float v, int off) {
     return __int_as_float(r);
 }
 
-// v_permlane16_swap_b32 exchanges the odd 16-lane rows of `a` with the even
-// rows of `b`; the sum of the two results holds, in even rows, a's row pair
-// sum and, in odd rows, b's.  (The results are read through memcpy: element
-// access on the builtin's returned pair reads the first element twice with
-// this compiler.)
-__device__ __forceinline__ float swap_rows_add(float a, float b) {
-    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    unsigned q[2];
-    __builtin_memcpy(q, &p, sizeof q);
-    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
-
-// v_permlane32_swap_b32: the upper 32 lanes of `a` trade places with the
-// lower 32 lanes of `b`; the sum holds a's half sum in lanes 0..31 and b's
-// in lanes 32..63.
-__device__ __forceinline__ float swap_halves_add(float a, float b) {
-    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    unsigned q[2];
-    __builtin_memcpy(q, &p, sizeof q);
-    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
-
 // The matrices one launch multiplies by the same activations (a group of
 // sibling projections such as q | k | v): their tiles are numbered one
 // after the other, member g owning tiles [tile_end[g-1], tile_end[g]), and

@@ -63,20 +63,6 @@ constexpr int kGemvSrcSwiglu = VM_HIP_GEMV_SRC_SWIGLU;
 constexpr int kGemvSrcNormRes = VM_HIP_GEMV_SRC_NORMRES;
 constexpr int kGemvSrcAttn = VM_HIP_GEMV_SRC_ATTN;
 
-__device__ __forceinline__ float swap_rows_add(float a, float b) {
-    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    unsigned q[2];
-    __builtin_memcpy(q, &p, sizeof q);
-    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
-
-__device__ __forceinline__ float swap_halves_add(float a, float b) {
-    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    unsigned q[2];
-    __builtin_memcpy(q, &p, sizeof q);
-    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
-
 __device__ __forceinline__ float silu_mul(float g, float u) {
     const float sig = 1.0f / (1.0f + expf(-g));
     return (sig * g) * u;

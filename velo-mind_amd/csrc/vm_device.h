@@ -26,6 +26,27 @@ __device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t rsrc, ui
     return __builtin_amdgcn_raw_buffer_load_b32(rsrc, static_cast<int>(offset), 0, 0);
 }
 
+// v_permlane16_swap_b32 exchanges the odd 16-lane rows of `a` with the even
+// rows of `b`; the sum of the two results holds, in even rows, a's row pair
+// sum and, in odd rows, b's.  v_permlane32_swap_b32: the upper 32 lanes of
+// `a` trade places with the lower 32 lanes of `b`; the sum holds a's half
+// sum in lanes 0..31 and b's in lanes 32..63.  (The results are read through
+// memcpy: element access on the builtin's returned pair reads the first
+// element twice with this compiler.)
+__device__ __forceinline__ float swap_rows_add(float a, float b) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    unsigned q[2];
+    __builtin_memcpy(q, &p, sizeof q);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+__device__ __forceinline__ float swap_halves_add(float a, float b) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    unsigned q[2];
+    __builtin_memcpy(q, &p, sizeof q);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // Agent-scope relaxed accesses: coherent across the XCDs' L2s (sc1), used
 // for split-K partials that another workgroup reads after a ticket.
 __device__ __forceinline__ float coherent_load(const float* p) {
