@@ -596,19 +596,14 @@ int vm_hip_decode_trace_read(void* host, int64_t bytes);
  * vm_hip_add_rmsnorm_stage_f32 (vm_hip_add_rmsnorm_f32's arithmetic) and
  * vm_hip_silu_mul_stage_f32 (vm_hip_silu_mul_f32's) write it, with the fp32
  * rows too when hn_out / out_f32 is given; vm_hip_qmm_staged_f32 runs the
- * GEMM on it, equal bit for bit to vm_hip_qmm_f32 on the fp32 rows.  With
- * VM_HIP_A_PIECES and blockwise scales the GEMM also takes the per-column
- * powers of two of the scales ([2n] floats), which depend only on the
- * weights: vm_hip_qmm_col_pow computes them once. */
+ * GEMM on it, equal bit for bit to vm_hip_qmm_f32 on the fp32 rows. */
 #define VM_HIP_A_FP32   0
 #define VM_HIP_A_ROWS   1
 #define VM_HIP_A_PIECES 2
 int vm_hip_qmm_a_layout(int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size, int* layout,
                         int64_t* bytes);
-int vm_hip_qmm_col_pow(const float* scale, float* col_pow, int64_t k, int64_t n, int quant_type, int block_size,
-                       void* stream);
-int vm_hip_qmm_staged_f32(const void* a_staged, const float* col_pow, const int8_t* wq, const float* scale, float* c,
-                          int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size, void* stream);
+int vm_hip_qmm_staged_f32(const void* a_staged, const int8_t* wq, const float* scale, float* c, int64_t rows_m,
+                          int64_t k, int64_t n, int quant_type, int block_size, void* stream);
 int vm_hip_add_rmsnorm_stage_f32(float* h, const float* delta, const float* w, void* a_staged, int layout,
                                  float* hn_out, int64_t rows, int64_t dim, float eps, void* stream);
 int vm_hip_silu_mul_stage_f32(const float* gate_up, void* a_staged, int layout, float* out_f32, int64_t rows,

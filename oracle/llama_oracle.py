@@ -33,6 +33,7 @@ it.  How each is pinned (tests/test_oracle_llama.py):
 from __future__ import annotations
 
 import math
+import os
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -204,23 +205,15 @@ class LlamaConfig:
         return self.hidden_size // self.num_heads
 
 
-# ------------------------------------------- linears: exact, dense, GPU-rounded
+# ------------------------------------------- linears: exact and dense
 
 # How a packed Linear computes (Linear.mode):
 #   LINEAR_EXACT  the C oracle's QuantizedMatMul (quantized_matmul.cpp:48-267,
-#                 the reference's own loop order; slow, the default)
+#                 the reference's own arithmetic; the default)
 #   LINEAR_DENSE  dequantized weights (quant.cpp:106-123, :177-209) times x
-#                 with fp32 BLAS: the same sum in another order, for models
-#                 too large for the scalar loop
-#   LINEAR_HIP    LINEAR_DENSE, except that products with more than
-#                 HIP_GEMV_MAX_ROWS rows use the weights as the HIP MFMA path
-#                 stages them (round_block_weights: blockwise weights rounded
-#                 to fp16 once, a fixed function of the weights).  That path
-#                 takes the activations at fp32-equivalent precision
-#                 (split_rows_fp16), so nothing activation-dependent is
-#                 rounded and GPU results can be held to fp32-summation bounds
-LINEAR_EXACT, LINEAR_DENSE, LINEAR_HIP = "exact", "dense", "hip"
-HIP_GEMV_MAX_ROWS = 4
+#                 with fp32 BLAS: the same sum in another order, for the
+#                 many decode steps of full-size models
+LINEAR_EXACT, LINEAR_DENSE = "exact", "dense"
 
 
 def split_rows_fp16(x: np.ndarray) -> np.ndarray:
@@ -245,26 +238,29 @@ def split_rows_fp16(x: np.ndarray) -> np.ndarray:
     return np.ldexp(total, -xr[..., None])
 
 
-def round_block_weights(codes: np.ndarray, scales: np.ndarray, block: int) -> np.ndarray:
-    """numpy restatement of the C oracle's vmo_hip_block_weights (which
-    Linear.gemm_weights uses for speed; the two are checked against each
-    other).  The HIP MFMA path's blockwise weights: with 2^e per column (max scale
-    / 2^e in [0.5, 1)), w = fp16(code * fp16(s / 2^e)) * 2^e, both roundings
-    to nearest even.  (The kernel takes e over each workgroup's K range; the
-    roundings are relative and so independent of e while s / 2^e stays in
-    fp16's normal range, as it does unless a block scale is 2^14 times
-    smaller than its column's largest.)  codes: [K, N] integers; scales:
-    [ceil(K / block), N].  Returns fp32 [K, N] (exact)."""
-    k = codes.shape[0]
-    sc = np.ascontiguousarray(scales, f32)
-    smax = sc.max(axis=0)
-    _, e = np.frexp(np.where(smax > 0, smax, 1).astype(np.float64))
-    e = np.where(smax > 0, e, 0).astype(np.int64)
-    s16 = np.ldexp(sc.astype(np.float64), -e[None, :]).astype(np.float16).astype(f32)
-    rows = np.repeat(s16, block, axis=0)[:k]
-    prod = codes.astype(f32) * rows                      # exact in fp32
-    prod16 = prod.astype(np.float16).astype(f32)
-    return np.ldexp(prod16, e[None, :].astype(np.int32)).astype(f32)
+def _oracle_threads() -> int:
+    try:
+        return max(1, min(16, len(os.sched_getaffinity(0))))
+    except AttributeError:
+        return max(1, min(16, os.cpu_count() or 1))
+
+
+def _qmm_rows_parallel(x2, q, s, k, quant_type, block):
+    """Q.qmm over row chunks on several threads (the C call releases the
+    GIL).  The reference loop computes every row of an M > 1 product on its
+    own, so splitting into chunks of at least two rows changes no bit of the
+    result (a one-row call would take the M = 1 streaming path instead)."""
+    m = x2.shape[0]
+    chunks = min(_oracle_threads(), m // 2)
+    if chunks < 2:
+        return Q.qmm(x2, q, s, k, quant_type, block)
+    from concurrent.futures import ThreadPoolExecutor
+
+    edges = np.linspace(0, m, chunks + 1).astype(int)
+    with ThreadPoolExecutor(chunks) as ex:
+        parts = list(ex.map(lambda lo_hi: Q.qmm(x2[lo_hi[0]:lo_hi[1]], q, s, k, quant_type, block),
+                            zip(edges[:-1], edges[1:])))
+    return np.concatenate(parts, axis=0)
 
 
 @dataclass
@@ -280,7 +276,6 @@ class Linear:
     block: int = 0
     mode: str = LINEAR_EXACT
     _dense: np.ndarray | None = field(default=None, repr=False)
-    _gemm: np.ndarray | None = field(default=None, repr=False)
 
     def codes(self) -> np.ndarray:
         """Integer codes [K, N] (INT4 nibbles sign-extended, quant.cpp:17-22)."""
@@ -300,21 +295,16 @@ class Linear:
         if self.quant_type == Q.QUANT_NONE:
             return self.w
         if self._dense is None:
-            if self.quant_type == Q.QUANT_INT8:
+            if self.quant_type == Q.QUANT_INT8 and self.block > 0:
+                # blockwise INT8 (QuantizedMatMulAttrs.block_size > 0, no
+                # quant.cpp packer): code * the scale of its K block, exact
+                rows = np.repeat(np.asarray(self.s, f32).reshape(-1, self.n), self.block, axis=0)[: self.k]
+                self._dense = (self.q.view(np.int8).astype(f32) * rows).astype(f32)
+            elif self.quant_type == Q.QUANT_INT8:
                 self._dense = Q.dequantize_int8(self.q.view(np.int8), self.s)
             else:
                 self._dense = Q.dequantize_int4(self.q.view(np.uint8), self.s, self.k, self.block)
         return self._dense
-
-    def gemm_weights(self) -> np.ndarray:
-        """W as the HIP MFMA path stages it: INT8 per-column codes are exact
-        (the scale multiplies the fp32 result), blockwise weights are
-        round_block_weights()."""
-        if self.quant_type == Q.QUANT_INT8 and self.block == 0:
-            return self.dense()
-        if self._gemm is None:
-            self._gemm = Q.hip_block_weights(self.q, self.s.reshape(-1, self.n), self.k, self.block, self.quant_type)
-        return self._gemm
 
     def __call__(self, x: np.ndarray) -> np.ndarray:
         """llama_graph.cpp:30-44 (apply_linear): QuantizedMatMul when the
@@ -323,9 +313,7 @@ class Linear:
         if self.quant_type == Q.QUANT_NONE:
             y = (x2 @ self.w.astype(f32)).astype(f32)
         elif self.mode == LINEAR_EXACT:
-            y = Q.qmm(x2, self.q.view(np.int8), self.s, self.k, self.quant_type, self.block)
-        elif self.mode == LINEAR_HIP and x2.shape[0] > HIP_GEMV_MAX_ROWS:
-            y = (x2 @ self.gemm_weights()).astype(f32)
+            y = _qmm_rows_parallel(x2, self.q.view(np.int8), self.s, self.k, self.quant_type, self.block)
         else:
             y = (x2 @ self.dense()).astype(f32)
         return y.reshape(x.shape[:-1] + (y.shape[-1],))

@@ -50,9 +50,6 @@ def lib() -> ctypes.CDLL:
         L.vmo_f32_to_bf16.argtypes = [c_float]
         L.vmo_f32_to_bf16.restype = c_uint16
         L.vmo_cpu_has_avx2_fma.restype = c_int
-        L.vmo_round_f16.argtypes = [c_float]
-        L.vmo_round_f16.restype = c_float
-        L.vmo_hip_block_weights.argtypes = [p, p, p, c_size_t, c_size_t, c_size_t, c_int]
         _lib = L
     return _lib
 
@@ -173,19 +170,3 @@ def has_avx2_fma() -> bool:
     return bool(lib().vmo_cpu_has_avx2_fma())
 
 
-def round_f16(x: np.ndarray) -> np.ndarray:
-    """vmo_round_f16 elementwise (binary16 rounding, ties to even)."""
-    x = np.ascontiguousarray(x, np.float32)
-    f = lib().vmo_round_f16
-    return np.array([f(float(v)) for v in x.ravel()], np.float32).reshape(x.shape)
-
-
-def hip_block_weights(wq: np.ndarray, s: np.ndarray, rows: int, block: int, quant_type: int) -> np.ndarray:
-    """vmo_hip_block_weights: the MFMA path's staged blockwise weights,
-    fp32 [rows, cols]."""
-    wq = np.ascontiguousarray(wq).view(np.int8)
-    s = np.ascontiguousarray(s, np.float32)
-    cols = wq.shape[1]
-    out = np.empty((rows, cols), np.float32)
-    lib().vmo_hip_block_weights(_ptr(wq), _ptr(s), _ptr(out), rows, cols, block, quant_type)
-    return out

@@ -289,12 +289,67 @@ int vmo_qmm_decode_int8(const float* a, const int8_t* b_q, const float* scale, f
     return 1;
 }
 
+/* The scalar reference's arithmetic (quantized_matmul.cpp:48-141) for
+ * contiguous fp32 operands, in row-major order: for each row of A (and each
+ * block), the K loop runs outside the column loop, so every output element
+ * sees exactly the sequence of fp32 operations of qmm_scalar_generic (a
+ * block's products added in K order, times the block scale, added to the
+ * element's total; per-channel INT8: products added in K order, then times
+ * the column scale), with no contraction (-ffp-contract=off), while the
+ * codes are read a row at a time and the column loop vectorizes.  Pinned
+ * bit for bit against vmo_qmm_scalar_f32 (tests/test_oracle_qmm.py). */
+__attribute__((optimize("O3")))
+static void qmm_rows_f32(const float* a, const int8_t* b_q, const float* scale, float* c, size_t m, size_t k,
+                         size_t n, int quant_type, int block_size) {
+    const int int4 = quant_type == VMO_QUANT_INT4;
+    size_t bs = 0;
+    if (int4) bs = block_size > 0 ? (size_t)block_size : 32;
+    else if (block_size > 0) bs = (size_t)block_size;
+    float* code = (float*)malloc((n ? n : 1) * 3 * sizeof(float));
+    if (!code) abort();
+    float* part = code + n;
+    float* total = part + n;
+    for (size_t i = 0; i < m; ++i) {
+        const float* ai = a + i * k;
+        for (size_t j = 0; j < n; ++j) total[j] = 0.0f;
+        const size_t step = bs ? bs : (k ? k : 1);
+        for (size_t p0 = 0; p0 < k; p0 += step) {
+            const size_t p1 = (p0 + step < k) ? p0 + step : k;
+            float* acc = bs ? part : total;
+            if (bs)
+                for (size_t j = 0; j < n; ++j) part[j] = 0.0f;
+            for (size_t p = p0; p < p1; ++p) {
+                if (int4) {
+                    const uint8_t* row = (const uint8_t*)b_q + (p / 2) * n;
+                    if (p & 1u)
+                        for (size_t j = 0; j < n; ++j) code[j] = (float)nib_to_int(row[j] >> 4);
+                    else
+                        for (size_t j = 0; j < n; ++j) code[j] = (float)nib_to_int(row[j]);
+                } else {
+                    const int8_t* row = b_q + p * n;
+                    for (size_t j = 0; j < n; ++j) code[j] = (float)row[j];
+                }
+                const float av = ai[p];
+                for (size_t j = 0; j < n; ++j) acc[j] += av * code[j];
+            }
+            if (bs) {
+                const float* s = scale + (p0 / bs) * n;
+                for (size_t j = 0; j < n; ++j) total[j] += part[j] * s[j];
+            }
+        }
+        if (!bs)
+            for (size_t j = 0; j < n; ++j) total[j] = total[j] * scale[j];
+        for (size_t j = 0; j < n; ++j) c[i * n + j] = total[j];
+    }
+    free(code);
+}
+
 void vmo_qmm_2d_f32(const float* a, const int8_t* b_q, const float* scale, float* c,
                     size_t m, size_t k, size_t n, int quant_type, int block_size) {
     /* quantized_matmul.cpp:254-266: M=1 tries the streaming decode first. */
     if (m == 1 && vmo_qmm_decode_int8(a, b_q, scale, c, k, n, 1, n, 1, quant_type, block_size))
         return;
-    vmo_qmm_scalar_f32(a, b_q, scale, c, m, k, n, k, 1, n, 1, n, 1, quant_type, block_size);
+    qmm_rows_f32(a, b_q, scale, c, m, k, n, quant_type, block_size);
 }
 
 /* ---- dtype.h restatement: half-precision conversions -------------------- */
@@ -354,60 +409,3 @@ uint16_t vmo_f32_to_bf16(float f) {
     return (uint16_t)(x >> 16);
 }
 
-/* ---- model of the HIP MFMA path's roundings (see qmm_oracle.h) ---- */
-
-float vmo_round_f16(float x) {
-    uint32_t u;
-    memcpy(&u, &x, sizeof u);
-    const uint32_t a = u & 0x7FFFFFFFu;
-    if (a > 0x7F800000u) return x;                           /* NaN */
-    if (a >= 0x477FF000u) return (u >> 31) ? -INFINITY : INFINITY;   /* >= 65520 */
-    if (a < 0x38800000u) {                                   /* below 2^-14: subnormal grid 2^-24 */
-        const double r = nearbyint((double)x * 0x1p24) * 0x1p-24;
-        return (float)r;
-    }
-    /* normal range: keep 11 significant bits, ties to even */
-    u = (u + 0xFFFu + ((u >> 13) & 1u)) & ~0x1FFFu;
-    float r;
-    memcpy(&r, &u, sizeof r);
-    return r;
-}
-
-void vmo_hip_block_weights(const int8_t* b_q, const float* scale, float* dst, size_t rows, size_t cols,
-                           size_t block_size, int quant_type) {
-    if (!b_q || !scale || !dst || rows == 0 || cols == 0 || block_size == 0) return;
-    const size_t nblk = (rows + block_size - 1) / block_size;
-    int* ex = (int*)malloc(cols * sizeof(int));
-    float* s16 = (float*)malloc(cols * sizeof(float));
-    if (!ex || !s16) {
-        free(ex);
-        free(s16);
-        return;
-    }
-    for (size_t c = 0; c < cols; ++c) {
-        float smax = 0.0f;
-        for (size_t b = 0; b < nblk; ++b)
-            if (fabsf(scale[b * cols + c]) > smax) smax = fabsf(scale[b * cols + c]);
-        ex[c] = 0;
-        if (smax > 0.0f && smax <= 3.0e38f) (void)frexpf(smax, &ex[c]);
-    }
-    for (size_t b = 0; b < nblk; ++b) {
-        for (size_t c = 0; c < cols; ++c) s16[c] = vmo_round_f16(ldexpf(scale[b * cols + c], -ex[c]));
-        const size_t r1 = (b + 1) * block_size < rows ? (b + 1) * block_size : rows;
-        for (size_t r = b * block_size; r < r1; ++r) {
-            float* out = dst + r * cols;
-            for (size_t c = 0; c < cols; ++c) {
-                int code;
-                if (quant_type == VMO_QUANT_INT4) {
-                    const unsigned byte = (uint8_t)b_q[(r / 2) * cols + c];
-                    code = nib_to_int((r & 1) ? byte >> 4 : byte);
-                } else {
-                    code = b_q[r * cols + c];
-                }
-                out[c] = ldexpf(vmo_round_f16((float)code * s16[c]), ex[c]);
-            }
-        }
-    }
-    free(ex);
-    free(s16);
-}

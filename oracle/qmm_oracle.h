@@ -91,21 +91,6 @@ uint16_t vmo_f32_to_f16(float f);
 float    vmo_bf16_to_f32(uint16_t b);
 uint16_t vmo_f32_to_bf16(float f);
 
-/* Model of the HIP MFMA path's deliberate roundings (no reference
- * counterpart: the reference's CPU path has none).
- *
- * vmo_round_f16: x rounded to the nearest binary16 value, ties to even,
- * subnormals included, |x| >= 65520 to infinity (IEEE 754 binary16, as the
- * GPU's v_cvt_f16_f32 and fp16 multiply round), returned as a float.
- *
- * vmo_hip_block_weights: the blockwise weights [rows, cols] as the MFMA
- * path stages them, w = round_f16(code * round_f16(s / 2^e)) * 2^e with 2^e
- * per column (the column's largest scale / 2^e in [0.5, 1)); b_q holds
- * INT8 codes [rows, cols] or INT4 packed [(rows+1)/2, cols] (quant.cpp's
- * layout), scale [ceil(rows/block), cols]. */
-float vmo_round_f16(float x);
-void vmo_hip_block_weights(const int8_t* b_q, const float* scale, float* dst, size_t rows, size_t cols,
-                           size_t block_size, int quant_type);
 
 /* 1 when the running CPU has AVX2+FMA (quantized_matmul.cpp:36-43). */
 int vmo_cpu_has_avx2_fma(void);

@@ -6,7 +6,7 @@ Covers INT8 per column and INT4 block 32, grouped-query attention, decode
 positions that cross the 32-key attention chunks, greedy generation, and a
 context long enough that the attention items outnumber the workgroups (each
 workgroup then takes several).  Bound: 1e-4 of max |logit| against the
-oracle (LINEAR_HIP mode; decode steps are fp32 GEMVs), 1e-5 against the
+oracle (LINEAR_DENSE mode; decode steps are fp32 GEMVs), 1e-5 against the
 other step (the same arithmetic, summed in another grouping).
 """
 from __future__ import annotations
@@ -68,7 +68,7 @@ def _sessions(llama, monkeypatch, dev, qt, block, max_seq):
 @pytest.mark.parametrize("qt,block", [(1, 0), (2, 32)])
 def test_persistent_step_matches_oracle_and_slices(llama, monkeypatch, qt, block):
     cfg, w = _model(11, hidden=512, heads=8, kv_heads=2, inter=384, vocab=320, layers=2)
-    ow = L.set_linear_mode(L.quantize_linears(w, qt, block), L.LINEAR_HIP)
+    ow = L.set_linear_mode(L.quantize_linears(w, qt, block), L.LINEAR_DENSE)
     dev = llama.Weights.from_oracle(cfg, w)
     sp, ss = _sessions(llama, monkeypatch, dev, qt, block, max_seq=80)
     prompt = [3, 1, 4]
@@ -92,7 +92,7 @@ def test_persistent_step_matches_oracle_and_slices(llama, monkeypatch, qt, block
 @pytest.mark.parametrize("qt,block", [(1, 0), (2, 32)])
 def test_persistent_generate_is_greedy(llama, monkeypatch, qt, block):
     cfg, w = _model(5, hidden=512, heads=8, kv_heads=2, inter=384, vocab=320, layers=2)
-    ow = L.set_linear_mode(L.quantize_linears(w, qt, block), L.LINEAR_HIP)
+    ow = L.set_linear_mode(L.quantize_linears(w, qt, block), L.LINEAR_DENSE)
     dev = llama.Weights.from_oracle(cfg, w)
     sp, ss = _sessions(llama, monkeypatch, dev, qt, block, max_seq=64)
     prompt = [2, 7, 1, 8, 2, 8]
@@ -108,7 +108,7 @@ def test_persistent_long_context_several_items_per_workgroup(llama, monkeypatch)
     # 8 KV heads x 33 key chunks at position 1040: more attention items than
     # the 256 workgroups of an MI355X
     cfg, w = _model(3, hidden=512, heads=8, kv_heads=8, inter=256, vocab=256, layers=1)
-    ow = L.set_linear_mode(L.quantize_linears(w, 2, 32), L.LINEAR_HIP)
+    ow = L.set_linear_mode(L.quantize_linears(w, 2, 32), L.LINEAR_DENSE)
     dev = llama.Weights.from_oracle(cfg, w)
     sp, ss = _sessions(llama, monkeypatch, dev, 2, 32, max_seq=1100)
     prompt = list(np.random.default_rng(4).integers(0, cfg.vocab_size, 1040))

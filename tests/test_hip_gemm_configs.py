@@ -1,13 +1,15 @@
 """Every MFMA GEMM tile variant (rows_m > 4), forced through the tuning
-override VELOMIND_GEMM_CFG="BM,BN,S" (or "BM,BN,S,D" for the variants
-that keep all D K-steps of a split in flight), against the oracle.
+overrides (VELOMIND_GEMM_CFG="BM,BN,S[,D]" for the small-tile kernel,
+VELOMIND_GEMM_WIDE="BM,BN,S,D,G" for the wide one), against the oracle.
 
-Covers the three weight kinds, K splits 1/2/4 (deterministic split-K
+Per-column INT8 takes either kernel; blockwise weights (INT4, INT8 with
+blocks) always take the wide kernel, which multiplies each 32-row chunk's
+fp32 sum by its block scale (codes exact in fp16), in its tile shapes with
+two 32 x 32 tiles per wave.  Covers K splits 1/2/4 (deterministic split-K
 reduction), partial M and N tiles, K ending half-way through a 64-row step,
-INT8 blocks of 32 and 96 rows, and block scales from 1e-7 to 1e3 (the
-per-column power-of-two normalisation keeps fp16 weights in range).
-Bound: the north-star 1e-3 * max|ref|; test_activation_magnitudes also
-holds the path to fp32 summation bounds against a model of its staging.
+INT8 blocks of 32 and 96 rows, and block scales from 1e-7 to 1e3.  Bound:
+the north-star 1e-3 * max|ref|; test_activation_magnitudes also holds every
+kind to fp32 summation bounds against the reference loop.
 """
 from __future__ import annotations
 
@@ -43,8 +45,7 @@ def _weights(kind, k, n, rng, block):
     return q, s, 2, block
 
 
-@pytest.mark.parametrize("kind,block", [("int8", 0), ("int8_block", 32), ("int8_block", 96), ("int4", 32),
-                                        ("int4", 64)])
+@pytest.mark.parametrize("kind,block", [("int8", 0)])
 @pytest.mark.parametrize("bm,bn", TILES)
 def test_forced_tile(hip, monkeypatch, bm, bn, kind, block):
     m, k, n = 40, 224, 336        # partial M and N tiles; 224 = 3.5 steps of 64
@@ -61,8 +62,7 @@ def test_forced_tile(hip, monkeypatch, bm, bn, kind, block):
     monkeypatch.delenv("VELOMIND_GEMM_CFG")
 
 
-@pytest.mark.parametrize("kind,block", [("int8", 0), ("int8_block", 32), ("int8_block", 96), ("int4", 32),
-                                        ("int4", 64)])
+@pytest.mark.parametrize("kind,block", [("int8", 0)])
 @pytest.mark.parametrize("bm,deep", [(16, 4), (16, 8), (32, 4), (32, 8)])
 @pytest.mark.parametrize("m", [5, 16, 40])
 def test_forced_deep(hip, monkeypatch, bm, deep, kind, block, m):
@@ -116,7 +116,7 @@ def test_split_k_deterministic(hip, monkeypatch):
     rng = np.random.default_rng(5)
     q, s = O.quantize_int4((rng.standard_normal((k, n)) * 0.02).astype(np.float32), 32)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    monkeypatch.setenv("VELOMIND_GEMM_CFG", "32,128,8")
+    monkeypatch.setenv("VELOMIND_GEMM_WIDE", "64,128,8,2,1")   # eight K splits of the blockwise kernel
     outs = [hip.run_qmm(x, q, s, k, hip.QUANT_INT4, 32) for _ in range(3)]
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
@@ -153,28 +153,31 @@ def test_activation_magnitudes(hip, kind, block, reps):
     err = np.abs(out - ref).max(axis=1)
     assert np.all(err <= TOL * rowmax), f"worst row ratio {np.max(err / rowmax):.3e}"
     # Against the model of what the MFMAs multiply (A split into two fp16
-    # parts, blockwise weights staged in fp16) the only difference left is
-    # fp32 summation of 2k products: |err| <= 2k * 2^-24 * sum_k |a * w|.
-    lin = LO.Linear(q=q, s=s, k=k, n=n, quant_type=oq, block=blk, mode=LO.LINEAR_HIP)
-    wh = lin.gemm_weights().astype(np.float64)
-    model = LO.split_rows_fp16(x) @ wh
-    mag = np.abs(x.astype(np.float64)) @ np.abs(wh)
+    # parts, the exact weights) the only difference left is fp32 summation
+    # of 2k products and the chunk sums' scaling: |err| <= 2k * 2^-24 *
+    # sum_k |a * w|.
+    lin = LO.Linear(q=q, s=s, k=k, n=n, quant_type=oq, block=blk, mode=LO.LINEAR_DENSE)
+    wd = lin.dense().astype(np.float64)
+    model = LO.split_rows_fp16(x) @ wd
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wd)
     bound = 2 * k * 2.0 ** -24 * 1.01 * mag + 1e-300
     assert np.all(np.abs(out - model) <= bound), f"worst ratio {np.max(np.abs(out - model) / bound):.3e}"
-    if kind == "int8":
-        # per-column INT8 stages nothing: fp32-equivalent against the reference loop
-        bound = (2.0 ** -22 + 2 * k * 2.0 ** -24) * 1.01 * mag + 1e-300
-        assert np.all(np.abs(out - ref) <= bound), f"worst ratio {np.max(np.abs(out - ref) / bound):.3e}"
+    # every kind is fp32-equivalent against the reference loop itself
+    bound = (2.0 ** -22 + 4 * k * 2.0 ** -24) * 1.01 * mag + 1e-300
+    assert np.all(np.abs(out - ref) <= bound), f"worst ratio {np.max(np.abs(out - ref) / bound):.3e}"
 
 
-# Wide-tile variants (rows_m > 32), forced through VELOMIND_GEMM_WIDE="BM,BN,S,D".
-WIDE = [(128, 128, 2, 1), (128, 128, 2, 2), (128, 128, 4, 1), (64, 128, 2, 1), (64, 128, 4, 1), (128, 64, 2, 2), (64, 256, 2, 1)]
+# Wide-tile variants, forced through VELOMIND_GEMM_WIDE="BM,BN,S,D,G": per-column
+# INT8 takes all of them, blockwise weights the ones with two 32 x 32 tiles per wave.
+WIDE_INT8 = [(128, 128, 2, 1), (128, 128, 2, 2), (128, 128, 4, 1), (64, 128, 2, 1), (64, 128, 4, 1), (128, 64, 2, 1),
+             (128, 64, 2, 2), (64, 256, 2, 1)]
+WIDE_BLOCK = [(128, 64, 2, 1), (128, 64, 2, 2), (64, 128, 2, 1)]
+WIDE_CASES = ([("int8", 0) + t for t in WIDE_INT8] +
+              [kb + t for kb in (("int8_block", 32), ("int8_block", 96), ("int4", 32), ("int4", 64)) for t in WIDE_BLOCK])
 
 
-@pytest.mark.parametrize("kind,block", [("int8", 0), ("int8_block", 32), ("int8_block", 96), ("int4", 32),
-                                        ("int4", 64)])
-@pytest.mark.parametrize("bm,bn,depth,groups", WIDE)
-@pytest.mark.parametrize("m", [40, 130])
+@pytest.mark.parametrize("kind,block,bm,bn,depth,groups", WIDE_CASES)
+@pytest.mark.parametrize("m", [6, 40, 130])
 def test_forced_wide(hip, monkeypatch, bm, bn, depth, groups, kind, block, m):
     # K = 224 = 3.5 steps of 64; N = 336 leaves partial tiles for every BN;
     # m = 130 leaves a 2-row M tile after 128.
@@ -204,7 +207,8 @@ def test_wide_long_k(hip, monkeypatch, kind, block):
     ref = O.qmm(x, q.view(np.int8), s, k, oq, blk)
     print(f"case wide long-k default kind={kind} m={m} k={k} n={n}", flush=True)
     _check(hip.run_qmm(x, q, s, k, qt, blk), ref)
-    monkeypatch.setenv("VELOMIND_GEMM_WIDE", "128,128,3,2,2")
-    print(f"case wide long-k 128,128,3,2,2 kind={kind}", flush=True)
+    forced = "128,128,3,2,2" if kind == "int8" else "128,64,3,2,2"
+    monkeypatch.setenv("VELOMIND_GEMM_WIDE", forced)
+    print(f"case wide long-k {forced} kind={kind}", flush=True)
     _check(hip.run_qmm(x, q, s, k, qt, blk), ref)
     monkeypatch.delenv("VELOMIND_GEMM_WIDE")

@@ -296,7 +296,10 @@ def test_gemv_slices_residual_norm_source(hip, k, n, qt, block, delta_slices):
     _close(out.sum(axis=0, dtype=np.float64) * inv, ref, TOL, "normed projection")
 
 
-@pytest.mark.parametrize("heads,kv_heads,d,max_seq,p,slices", [(32, 4, 64, 584, 530, 16),
+@pytest.mark.parametrize("heads,kv_heads,d,max_seq,p,slices", [(32, 4, 64, 769, 767, 16),   # TinyLlama, bench's last
+                                                                (32, 4, 64, 776, 775, 16),   # last row of the cache
+                                                                (15, 5, 64, 257, 255, 15),   # SmolLM2, bench's last
+                                                                (32, 4, 64, 584, 530, 16),
                                                                 (32, 4, 64, 584, 0, 16),
                                                                 (32, 4, 64, 584, 63, 3),
                                                                 (15, 5, 64, 264, 200, 15),

@@ -8,11 +8,10 @@ positions, HIP-graph decode steps).
 
 Tolerance: 1e-4 of max |logit| of the oracle, everywhere.  Quantized runs
 compare against the oracle's quantized model (the same quant.cpp packing)
-in its LINEAR_HIP mode: projections of more than 4 rows use the blockwise
-weights as the MFMA path stages them in fp16 (round_block_weights, pinned
-in tests/test_oracle_llama.py); that path takes activations at
-fp32-equivalent precision, so what is left is fp32 summation order and the
-bound measures the kernels, not quantization or fp16.
+in its LINEAR_DENSE mode (exact codes and scales); the GPU's GEMM path takes
+activations at fp32-equivalent precision and applies block scales in fp32,
+so what is left is fp32 summation order and the bound measures the kernels,
+not quantization or fp16.
 """
 from __future__ import annotations
 
@@ -78,7 +77,7 @@ QUANTS = [(0, 0), (1, 0), (2, 32)]   # (quant_type, block): fp32, INT8 per colum
 
 
 def _oracle_weights(w, qt, block):
-    return w if qt == 0 else L.set_linear_mode(L.quantize_linears(w, qt, block), L.LINEAR_HIP)
+    return w if qt == 0 else L.set_linear_mode(L.quantize_linears(w, qt, block), L.LINEAR_DENSE)
 
 
 @pytest.mark.parametrize("fused", [False, True])

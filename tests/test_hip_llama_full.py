@@ -10,8 +10,9 @@
 Weights are synthetic N(0, 0.02) (norms N(1, 0.02)), generated and packed
 on the GPU, saved as a pre-packed safetensors file and read back with the
 safetensors library: the oracle (oracle/llama_oracle.py) runs on exactly
-those codes and scales, in its LINEAR_HIP mode (the blockwise weights as
-the MFMA path stages them, pinned in tests/test_oracle_llama.py).
+those codes and scales, in its LINEAR_DENSE mode (the dequantized weights
+times x in fp32, the reference QuantizedMatMul's sum in another order,
+pinned against LINEAR_EXACT in tests/test_oracle_llama.py).
 
 Tolerance.  At these depths the synthetic networks amplify fp32 rounding:
 perturbing the oracle's embedding by 2^-24 relative noise moves its
@@ -21,6 +22,18 @@ each comparison is held to TOL_FACTOR times the spread the oracle itself
 shows under two such perturbations (never below 1e-4 of max|logit|), plus
 the reference's own end-to-end criteria, cosine > 0.999 and the same
 argmax (tests/test_quantization.cpp:480-546).
+
+Late positions: the bench decodes TinyLlama at positions 512..767 and
+SmolLM2 at 128..255; a prompt that ends LATE_STEPS positions before the
+last, followed by LATE_STEPS teacher-forced decode steps on the resident
+decoder (the kernels of the bench's decode step, with its max_seq),
+reaches the same last positions, and each step's logits are held to the
+oracle as above.
+
+Reference arithmetic: the prompt logits are also compared with the oracle
+in its LINEAR_EXACT mode (the reference CPU QuantizedMatMul's own loop,
+exact codes and scales) under the reference's end-to-end criteria, cosine >
+0.999, rmse < 0.15 and the same argmax (tests/test_quantization.cpp:537-545).
 
 Both engines are checked: the resident decoder, and the graph engine (the
 reference engine's loop, a Graph on DeviceType::HIP per call,
@@ -46,16 +59,17 @@ TOL_FACTOR = 4.0
 PERTURB = 2.0 ** -24
 STEPS = 16
 LOGIT_STEPS = 3
+LATE_STEPS = 8
 
 MODELS = {
     "tinyllama_1.1b_int4": dict(
         cfg=L.LlamaConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632, num_layers=22, num_heads=32,
                           num_kv_heads=4, rms_norm_eps=1e-5, rope_theta=10000.0),
-        quant=2, block=32, prompt=512, tied=False, seed=20240601),
+        quant=2, block=32, prompt=512, decode=256, tied=False, seed=20240601),
     "smollm2_360m_int8": dict(
         cfg=L.LlamaConfig(vocab_size=49152, hidden_size=960, intermediate_size=2560, num_layers=32, num_heads=15,
                           num_kv_heads=5, rms_norm_eps=1e-5, rope_theta=100000.0, tie_word_embeddings=True),
-        quant=1, block=0, prompt=128, tied=True, seed=20240602),
+        quant=1, block=0, prompt=128, decode=128, tied=True, seed=20240602),
 }
 
 
@@ -125,7 +139,7 @@ def model(request, hip, tmp_path_factory):
     path = tmp_path_factory.mktemp(name) / "packed.safetensors"
     packed.save(str(path))
     packed.close()
-    ow = L.set_linear_mode(L.load_packed(load_file(str(path)), cfg, spec["quant"], spec["block"]), L.LINEAR_HIP)
+    ow = L.set_linear_mode(L.load_packed(load_file(str(path)), cfg, spec["quant"], spec["block"]), L.LINEAR_DENSE)
     path.unlink()
     if spec["tied"]:
         # the tie is real: the packed lm_head is quant.cpp's INT8 packing of
@@ -136,7 +150,7 @@ def model(request, hip, tmp_path_factory):
     print(f"case {name}: oracle prefill of {spec['prompt']} tokens, and of two perturbed copies", flush=True)
     ref = OracleRun(cfg, ow, prompt)
     perturbed = [OracleRun(cfg, _perturbed(ow, seed), prompt) for seed in (1, 2)]
-    return dict(name=name, spec=spec, cfg=cfg, dev=dev, prompt=prompt, ref=ref, perturbed=perturbed)
+    return dict(name=name, spec=spec, cfg=cfg, dev=dev, prompt=prompt, ref=ref, perturbed=perturbed, ow=ow)
 
 
 def _bound(model, ref_z, pert_z) -> float:
@@ -204,6 +218,69 @@ def test_graph_engine_full_size(llama_module, model):
         _run_engine(model, s)
     finally:
         s.close()
+
+
+@pytest.mark.timeout(900)
+def test_resident_decoder_late_positions(llama_module, model):
+    """The bench's last decode positions (TinyLlama 760..767 of max_seq 769,
+    SmolLM2 248..255 of 257): teacher-forced steps against the oracle, and
+    the HIP-graph generation of the same tokens."""
+    import dataclasses
+
+    spec, cfg, name = model["spec"], model["cfg"], model["name"]
+    end = spec["prompt"] + spec["decode"]
+    n = end - LATE_STEPS
+    prompt = np.random.default_rng(spec["seed"] % 997).integers(0, cfg.vocab_size, n).astype(np.int32)
+    print(f"case {name}: late positions {n}..{end - 1}, oracle prefill of {n} tokens (and two perturbed)", flush=True)
+    ow = model["ow"]
+    ref = OracleRun(cfg, ow, prompt)
+    pert = [OracleRun(cfg, _perturbed(ow, seed), prompt) for seed in (3, 4)]
+    s = llama_module.Session(model["dev"], llama_module.ENGINE_RESIDENT, spec["quant"], spec["block"], max_seq=end + 1)
+    try:
+        z = s.prefill(prompt)
+        _close(z, ref.logits, _bound(model, ref.logits, [p.logits for p in pert]), f"{name} prompt of {n}")
+        toks = [int(np.argmax(z))]
+        for i in range(LATE_STEPS):
+            zi = s.forward_step(toks[-1], n + i)
+            zr = ref.decode(toks)[-1]
+            _close(zi, zr, _bound(model, zr, [p.decode(toks)[-1] for p in pert]), f"{name} decode at {n + i}")
+            toks.append(int(np.argmax(zi)))
+        gen, _ = s.generate(prompt, LATE_STEPS - 1)
+        assert [int(t) for t in gen] == toks[:LATE_STEPS]
+    finally:
+        s.close()
+
+
+@pytest.mark.timeout(900)
+def test_prompt_logits_meet_the_reference_criteria_exactly(llama_module, model):
+    """Prompt logits of the resident decoder against the oracle run with the
+    reference CPU QuantizedMatMul's own arithmetic (LINEAR_EXACT: exact
+    codes and scales, no fp16 staging) under the reference's end-to-end
+    criteria."""
+    import dataclasses
+
+    spec, cfg, name = model["spec"], model["cfg"], model["name"]
+    ow = model["ow"]
+    exact = lambda lin: dataclasses.replace(lin, mode=L.LINEAR_EXACT, _dense=None)  # noqa: E731
+    ex = L.LlamaWeights(embed=ow.embed, final_norm=ow.final_norm, lm_head=exact(ow.lm_head), attn_norm=ow.attn_norm,
+                        ffn_norm=ow.ffn_norm, wq=[exact(x) for x in ow.wq], wk=[exact(x) for x in ow.wk],
+                        wv=[exact(x) for x in ow.wv], wo=[exact(x) for x in ow.wo], gate=[exact(x) for x in ow.gate],
+                        up=[exact(x) for x in ow.up], down=[exact(x) for x in ow.down])
+    print(f"case {name}: oracle prefill with the reference's QuantizedMatMul arithmetic", flush=True)
+    ref, _ = L.prefill(cfg, ex, model["prompt"], last_only=True)
+    ref = ref[0]
+    s = llama_module.Session(model["dev"], llama_module.ENGINE_RESIDENT, spec["quant"], spec["block"],
+                             max_seq=spec["prompt"] + 8)
+    try:
+        z = s.prefill(model["prompt"])
+    finally:
+        s.close()
+    max_diff, rmse, _, cos = Q.metrics(ref, z)
+    print(f"  {name}: cosine {cos:.6f}, rmse {rmse:.3e}, max diff {max_diff:.3e}, "
+          f"max|logit| {float(np.abs(ref).max()):.3e}", flush=True)
+    assert cos > 0.999
+    assert rmse < 0.15
+    assert int(np.argmax(z)) == int(np.argmax(ref))
 
 
 @pytest.fixture(scope="module")

@@ -2,10 +2,14 @@
 algorithm), through the C ABI.
 
 Contract: max|C_hip - C_ref| <= 1e-3 * max|C_ref| (fp32 accumulation).  The
-fp32 GEMV path (rows_m <= 4) is held to 1e-5 * max|C_ref| as well, which a
-dropped term, wrong nibble or wrong scale index would break.
+fp32 GEMV path (rows_m <= 4) and the config-3 GEMMs (activations at 22
+significant bits, codes exact, scales applied in fp32) are held to
+1e-5 * max|C_ref| as well, which a dropped term, wrong nibble or wrong
+scale index would break.
 """
 from __future__ import annotations
+
+import ctypes
 
 import numpy as np
 import pytest
@@ -92,6 +96,35 @@ def test_config3_prefill(hip, m, qt):
                       32 if qt == "int4" else 0)
         _check(ref_o, ref, 1e-5)
     _check(out, ref, TOL)
+    _check(out, ref, 1e-5)
+
+
+@pytest.mark.parametrize("qt", ["int4", "int8"])
+def test_output_of_more_than_2gib(hip, qt):
+    """A 4100 x 131072 fp32 output (2.05 GiB) on the wide MFMA kernel, which
+    addresses C from a 64-bit base per 128-row tile: rows on both sides of
+    the 2 GiB mark match the reference loop."""
+    m, k, n = 4100, 32, 131072
+    x = _normal((m, k), 71)
+    if qt == "int4":
+        q, s = _int4(k, n, 72)
+        hq, oq, blk = hip.QUANT_INT4, O.QUANT_INT4, 32
+    else:
+        q, s = _int8(k, n, 73)
+        hq, oq, blk = hip.QUANT_INT8, O.QUANT_INT8, 0
+    da = hip.DeviceBuffer.from_array(x)
+    dw = hip.DeviceBuffer.from_array(np.ascontiguousarray(q).view(np.int8))
+    ds = hip.DeviceBuffer.from_array(s)
+    dc = hip.DeviceBuffer(m * n * 4)
+    print(f"case qmm output {m}x{n} ({m * n * 4 / 2**30:.2f} GiB) qt={qt}", flush=True)
+    hip.qmm_f32(da.addr, dw.addr, ds.addr, dc.addr, m, k, n, hq, blk)
+    hip.synchronize()
+    lib = hip.open_library()
+    for r0 in (0, 2047, 4094):   # row 4096 starts at 2 GiB
+        rows = np.empty((6 if r0 == 4094 else 2, n), np.float32)
+        hip.check(lib.vm_hip_memcpy_d2h(rows.ctypes.data, ctypes.c_void_p(dc.addr + r0 * n * 4), rows.nbytes, None))
+        ref = O.qmm(x[r0:r0 + rows.shape[0]], q.view(np.int8), s, k, oq, blk)
+        _check(rows, ref, 1e-5)
 
 
 @pytest.mark.parametrize("m", [1, 4, 16])

@@ -41,13 +41,8 @@ def _layout(lib, rows, k, n, qt, blk):
 
 def _gemm_both(H, lib, staged, a32, q, s, rows, k, n, qt, blk, layout):
     dq, ds = H.DeviceBuffer.from_array(q), H.DeviceBuffer.from_array(s)
-    cp = None
-    if layout == A_PIECES and blk > 0:
-        cp = H.DeviceBuffer(n * 8)
-        H.check(lib.vm_hip_qmm_col_pow(ds.ptr, cp.ptr, k, n, qt, blk, None))
     c1, c2 = H.DeviceBuffer(rows * n * 4), H.DeviceBuffer(rows * n * 4)
-    H.check(lib.vm_hip_qmm_staged_f32(staged.ptr, cp.ptr if cp else None, dq.ptr, ds.ptr, c1.ptr, rows, k, n, qt, blk,
-                                      None))
+    H.check(lib.vm_hip_qmm_staged_f32(staged.ptr, dq.ptr, ds.ptr, c1.ptr, rows, k, n, qt, blk, None))
     H.qmm_f32(a32.addr, dq.addr, ds.addr, c2.addr, rows, k, n, qt, blk)
     return c1.download(np.float32, (rows, n)), c2.download(np.float32, (rows, n))
 
@@ -55,6 +50,8 @@ def _gemm_both(H, lib, staged, a32, q, s, rows, k, n, qt, blk, layout):
 @pytest.mark.parametrize("rows,n,want", [(24, 1024, A_ROWS), (130, 2048, A_PIECES), (512, 2048, A_PIECES)])
 @pytest.mark.parametrize("kind", ["int8", "int8_block", "int4"])
 def test_add_rmsnorm_stage(hip, rows, n, want, kind):
+    if kind != "int8":
+        want = A_PIECES   # blockwise scales always take the wide kernel's operand order
     H, lib = hip, hip.open_library()
     k = 2048
     rng = np.random.default_rng(rows + n + len(kind))
@@ -83,6 +80,8 @@ def test_add_rmsnorm_stage(hip, rows, n, want, kind):
                                                (512, 5632, 2048, A_PIECES)])
 @pytest.mark.parametrize("kind", ["int8", "int4"])
 def test_silu_mul_stage(hip, rows, inter, n, want, kind):
+    if kind != "int8":
+        want = A_PIECES   # blockwise scales always take the wide kernel's operand order
     H, lib = hip, hip.open_library()
     rng = np.random.default_rng(rows + inter + len(kind))
     gu = rng.standard_normal((rows, 2 * inter)).astype(np.float32) * 3
@@ -135,7 +134,6 @@ def test_stage_arguments(hip):
     q = H.DeviceBuffer(2048 * 2048)
     s = H.DeviceBuffer(64 * 2048 * 4)
     c = H.DeviceBuffer(512 * 2048 * 4)
-    # rows the GEMM does not take, and a pieces shape with blockwise scales but no column powers
-    assert lib.vm_hip_qmm_staged_f32(buf.ptr, None, q.ptr, s.ptr, c.ptr, 3, 2048, 2048, 2, 32, None) == H.EINVAL
-    assert lib.vm_hip_qmm_staged_f32(buf.ptr, None, q.ptr, s.ptr, c.ptr, 512, 2048, 2048, 2, 32, None) == H.EINVAL
-    assert lib.vm_hip_qmm_col_pow(s.ptr, c.ptr, 2048, 2048, 1, 0, None) == H.EINVAL   # per-column INT8
+    # rows the GEMM does not take, and a null staged buffer
+    assert lib.vm_hip_qmm_staged_f32(buf.ptr, q.ptr, s.ptr, c.ptr, 3, 2048, 2048, 2, 32, None) == H.EINVAL
+    assert lib.vm_hip_qmm_staged_f32(None, q.ptr, s.ptr, c.ptr, 512, 2048, 2048, 2, 32, None) == H.EINVAL

@@ -23,13 +23,16 @@ def test_wide_kernel_taken_at_prefill_shapes():
     assert _layout(512, 2048, 5632, H.QUANT_INT8, 0)[0] == H.A_PIECES
 
 
-def test_outputs_of_2gib_or_more_stay_off_the_wide_kernel():
-    # The wide kernel writes C with 32-bit byte offsets: a 4096 x 131072 fp32
-    # output (2 GiB) must take the small-tile kernel (64-bit addressing).
-    lay, _ = _layout(4096, 2048, 131072)
-    assert lay != H.A_PIECES
-    lay, _ = _layout(4096, 2048, 131072 - 16)
-    assert lay == H.A_PIECES
+def test_blockwise_weights_always_take_the_wide_kernel():
+    # Only the wide kernel applies block scales to each chunk's fp32 sum;
+    # it addresses C from a 64-bit base per 128-row tile, so outputs of
+    # 2 GiB and more stay on it too (tests/test_hip_qmm.py writes one).
+    for rows in (5, 16, 64, 512, 4096):
+        assert _layout(rows, 2048, 5632)[0] == H.A_PIECES
+    assert _layout(4096, 2048, 131072)[0] == H.A_PIECES
+    assert _layout(16, 2048, 5632, H.QUANT_INT8, 32)[0] == H.A_PIECES
+    # per-column INT8 keeps the small-tile kernel for few rows
+    assert _layout(16, 2048, 5632, H.QUANT_INT8, 0)[0] == H.A_ROWS
 
 
 def test_rows_longer_than_the_producers_limit_take_fp32():

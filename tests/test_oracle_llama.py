@@ -218,7 +218,7 @@ def test_layout_ops_against_numpy():
         L.embedding(x[0], np.array([4], np.int32))
 
 
-# ------------------------------------------- linear modes (dense, HIP-rounded)
+# ------------------------------------------- linear modes (exact, dense)
 
 def _packed_linear(rng, k, n, qt, mode):
     w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
@@ -227,6 +227,19 @@ def _packed_linear(rng, k, n, qt, mode):
         return L.Linear(q=q, s=s, k=k, n=n, quant_type=qt, block=0, mode=mode)
     q, s = Q.quantize_int4(w, 32)
     return L.Linear(q=q, s=s, k=k, n=n, quant_type=qt, block=32, mode=mode)
+
+
+def test_dense_blockwise_int8_matches_the_scalar_oracle():
+    # INT8 codes with block scales (QuantizedMatMulAttrs.block_size > 0)
+    rng = np.random.default_rng(3)
+    k, n, block = 100, 24, 32
+    q = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    s = (rng.random((-(-k // block), n)) * 10.0 ** rng.uniform(-3, 1, (-(-k // block), n))).astype(np.float32)
+    lin = L.Linear(q=q, s=s, k=k, n=n, quant_type=Q.QUANT_INT8, block=block, mode=L.LINEAR_EXACT)
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    exact = lin(x)
+    lin.mode = L.LINEAR_DENSE
+    assert np.abs(lin(x) - exact).max() <= 1e-5 * np.abs(exact).max()
 
 
 @pytest.mark.parametrize("qt", [Q.QUANT_INT8, Q.QUANT_INT4])
@@ -240,14 +253,6 @@ def test_dense_mode_matches_the_scalar_oracle(qt, m):
     lin.mode = L.LINEAR_DENSE
     dense = lin(x)
     assert np.abs(dense - exact).max() <= 1e-5 * np.abs(exact).max()
-    lin.mode = L.LINEAR_HIP
-    hipr = lin(x)
-    if m <= L.HIP_GEMV_MAX_ROWS or qt == Q.QUANT_INT8:
-        # the GEMV path, and INT8 per-column weights on the MFMA path, are fp32
-        assert np.abs(hipr - exact).max() <= 1e-5 * np.abs(exact).max()
-    else:
-        err = np.abs(hipr - exact).max() / np.abs(exact).max()
-        assert 0 < err <= 1e-3                       # the fp16 staging of blockwise weights, bounded
 
 
 def test_codes_unpack_to_the_dequantized_weights():
@@ -285,23 +290,6 @@ def test_split_rows_fp16_closed_forms():
     assert r[0].tolist() == [0.0, 0.0] and r[1, 0] == np.inf and r[1, 1] == 1.0
 
 
-def test_round_block_weights_closed_forms():
-    codes = np.array([[7, -3], [1, 5], [-7, 0], [2, 7]], np.int8)
-    # power-of-two scales: every rounding is exact
-    s = np.array([[2.0 ** -6, 2.0 ** -9], [2.0 ** -20, 0.5]], np.float32)
-    w = L.round_block_weights(codes, s, 2)
-    assert np.array_equal(w, codes.astype(np.float32) * np.repeat(s, 2, axis=0))
-    # scale 1 + 2^-12 rounds to 1 in fp16; 1 + 2^-10 is exact, but
-    # 7 * (1 + 2^-10) = 7 + 1.75 ulp rounds to 7 + 2 ulp = 7 + 2^-7
-    s = np.array([[1 + 2.0 ** -12, 1 + 2.0 ** -10]], np.float32)
-    w = L.round_block_weights(np.array([[3, 7]], np.int8), s, 32)
-    assert w.tolist() == [[3.0, 7 + 2.0 ** -7]]
-    # the column normalisation keeps tiny scales in fp16's normal range
-    s = np.array([[1.5 * 2.0 ** -20]], np.float32)
-    w = L.round_block_weights(np.array([[7]], np.int8), s, 32)
-    assert w[0, 0] == np.float32(7 * 1.5 * 2.0 ** -20)
-
-
 def test_load_packed_reads_the_packed_layout():
     rng = np.random.default_rng(5)
     cfg = L.LlamaConfig(vocab_size=40, hidden_size=64, intermediate_size=96, num_layers=2, num_heads=4,
@@ -331,32 +319,3 @@ def test_load_packed_reads_the_packed_layout():
     L.set_linear_mode(w, L.LINEAR_DENSE)
     logits_dense, _ = L.prefill(cfg, w, [3, 1, 4, 1, 5, 9], last_only=True)
     assert np.abs(logits_dense - logits_exact).max() <= 1e-5 * np.abs(logits_exact).max()
-
-
-def test_c_rounding_model_matches_numpy():
-    """vmo_round_f16 against numpy's float32 -> float16 conversion (IEEE
-    binary16, ties to even) over normals, ties, subnormals, overflow; and
-    vmo_hip_block_weights against the numpy restatement."""
-    rng = np.random.default_rng(13)
-    x = np.concatenate([
-        (rng.standard_normal(20000) * 10.0 ** rng.uniform(-9, 5, 20000)).astype(np.float32),
-        np.array([65504, 65519.99, 65520, 1e6, 2.0 ** -14, 2.0 ** -24, 3 * 2.0 ** -26, 2.0 ** -25,
-                  1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -(1 + 2.0 ** -11), 0.0, -0.0], np.float32),
-        ((np.arange(4096, dtype=np.float32) + 0.5) * np.float32(2.0 ** -12)),   # exact ties
-    ])
-    with np.errstate(over="ignore"):
-        ref = x.astype(np.float16).astype(np.float32)
-    got = Q.round_f16(x)
-    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
-    for qt in (Q.QUANT_INT8, Q.QUANT_INT4):
-        k, n, block = 96, 40, 32
-        w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
-        if qt == Q.QUANT_INT4:
-            q, s = Q.quantize_int4(w, block)
-        else:
-            q = rng.integers(-127, 128, (k, n), dtype=np.int8)
-            s = (rng.random((k // block, n)) * 10.0 ** rng.uniform(-3, 1, (k // block, n))).astype(np.float32)
-        lin = L.Linear(q=q, s=s, k=k, n=n, quant_type=qt, block=block)
-        c_model = Q.hip_block_weights(q, s, k, block, qt)
-        np_model = L.round_block_weights(lin.codes(), s.reshape(-1, n), block)
-        assert np.array_equal(c_model, np_model)

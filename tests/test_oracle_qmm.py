@@ -35,6 +35,29 @@ def test_reference_int8_qmm_vs_dequant_matmul(m, k, n):
     assert np.abs(out - ref).max() < 1e-4
 
 
+@pytest.mark.parametrize("quant,block", [(O.QUANT_INT8, 0), (O.QUANT_INT8, 32), (O.QUANT_INT8, 7),
+                                         (O.QUANT_INT4, 32), (O.QUANT_INT4, 0), (O.QUANT_INT4, 2), (O.QUANT_INT4, 64)])
+@pytest.mark.parametrize("m,k,n", [(2, 64, 16), (3, 101, 37), (5, 576, 1536), (2, 2048, 96), (4, 0, 8), (3, 33, 1)])
+def test_row_major_loop_is_the_scalar_reference_bit_for_bit(quant, block, m, k, n):
+    """vmo_qmm_2d_f32 runs the scalar reference's per-element arithmetic in
+    row-major order (the loop the full-size exact oracle needs); every
+    element must come out bit-identical to the reference's column loop,
+    including odd K, tails of blocks, per-channel INT8 and values of every
+    magnitude (an fp32 reassociation or a contraction would show)."""
+    rng = np.random.default_rng(m * 1000 + k + n + block)
+    if quant == O.QUANT_INT4:
+        q = rng.integers(0, 256, ((k + 1) // 2, n), dtype=np.uint8).view(np.int8)
+        nb = -(-k // (block if block > 0 else 32))
+    else:
+        q = rng.integers(-128, 128, (k, n), dtype=np.int8)
+        nb = -(-k // block) if block > 0 else 1
+    s = (np.exp2(rng.integers(-20, 20, (max(nb, 1), n))) * rng.uniform(0.5, 1.0, (max(nb, 1), n))).astype(np.float32)
+    a = (rng.standard_normal((m, k)) * np.exp2(rng.integers(-30, 30, (m, k)))).astype(np.float32)
+    fast = O.qmm(a, q, s, k, quant, block)
+    ref = O.qmm_scalar(a, q, s, k, quant, block)
+    assert np.array_equal(fast.view(np.uint32), ref.view(np.uint32))
+
+
 def test_reference_avx2_decode_vs_scalar():
     # tests/test_quantization.cpp:209-241
     k, n = 576, 1536

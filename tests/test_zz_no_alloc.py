@@ -81,18 +81,21 @@ def test_noalloc_on_a_stream_then_null_stream(hip):
     _check(hip, 23, 1, 576, 1536, O.QUANT_INT8)
 
 
-def test_noalloc_refuses_scratch_beyond_its_array(hip):
-    # 32 rows INT4 at K=2048 takes eight K splits of 32 x 32768 fp32
-    # partials (32 MiB), more than the 14 MiB the static array holds.
-    m, k, n = 32, 2048, 32768
+def test_noalloc_refuses_scratch_beyond_its_array(hip, monkeypatch):
+    # 130 rows INT4 at K=4096 forced to sixteen K splits of the wide kernel
+    # (the tuning override) take 16 x 130 x 8192 fp32 partials (65 MiB),
+    # more than the 14 MiB the static array holds.
+    m, k, n = 130, 4096, 8192
     da = hip.DeviceBuffer(m * k * 4)
     dw = hip.DeviceBuffer(k // 2 * n)
     ds = hip.DeviceBuffer(k // 32 * n * 4)
     dc = hip.DeviceBuffer(m * n * 4)
     sentinel = np.full((m, n), 7.25, np.float32)
     dc.upload(sentinel)
+    monkeypatch.setenv("VELOMIND_GEMM_WIDE", "128,64,16,2,1")
     with pytest.raises(hip.VmHipError) as info:
         hip.qmm_f32_noalloc(da.addr, dw.addr, ds.addr, dc.addr, m, k, n, O.QUANT_INT4, 32)
+    monkeypatch.delenv("VELOMIND_GEMM_WIDE")
     assert info.value.status == hip.EINVAL
     assert "static scratch" in str(info.value)
     hip.synchronize()

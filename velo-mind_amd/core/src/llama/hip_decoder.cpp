@@ -56,11 +56,9 @@ struct DevBuf {
     T* as() const { return static_cast<T*>(p); }
 };
 
-// One packed linear [k, n]; col_pow: the per-column powers of two of
-// blockwise scales that the wide prefill GEMM stages them with (computed
-// once, for prompts whose activations the producers stage themselves).
+// One packed linear [k, n].
 struct Packed {
-    DevBuf codes, scales, col_pow;
+    DevBuf codes, scales;
     std::int64_t k = 0, n = 0;
 };
 
@@ -335,19 +333,6 @@ struct HipLlamaDecoder::Impl {
     void prepare_staging() {
         const char* env = std::getenv("VELOMIND_STAGE_A");
         stage_a = !(env && env[0] == '0');
-        if (qt != VM_HIP_QUANT_INT4) return;   // per-column INT8 scales need no column powers
-        auto powers = [&](Packed& w) {
-            if (w.n % 16 != 0 || block % 32 != 0) return;
-            w.col_pow = DevBuf(static_cast<std::size_t>(w.n) * 8);
-            check(vm_hip_qmm_col_pow(w.scales.as<float>(), w.col_pow.as<float>(), w.k, w.n, qt, block, stream),
-                  "column powers");
-        };
-        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
-            powers(qkv[l]);
-            powers(o[l]);
-            powers(gate_up[l]);
-            powers(down[l]);
-        }
     }
 
     // The layout the GEMM of `w` takes its `rows`-row activations in
@@ -365,9 +350,8 @@ struct HipLlamaDecoder::Impl {
     }
 
     void qmm_staged(const Packed& w, float* c, std::int64_t rows) {
-        check(vm_hip_qmm_staged_f32(a_stage.p, w.col_pow.p ? w.col_pow.as<float>() : nullptr,
-                                    static_cast<const std::int8_t*>(w.codes.p), w.scales.as<float>(), c, rows, w.k,
-                                    w.n, qt, block_arg(), stream),
+        check(vm_hip_qmm_staged_f32(a_stage.p, static_cast<const std::int8_t*>(w.codes.p), w.scales.as<float>(), c,
+                                    rows, w.k, w.n, qt, block_arg(), stream),
               "quantized matmul (staged activations)");
     }
 

@@ -197,20 +197,8 @@ int vm_hip_qmm_a_layout(int64_t rows_m, int64_t k, int64_t n, int quant_type, in
     return 0;
 }
 
-int vm_hip_qmm_col_pow(const float* scale, float* col_pow, int64_t k, int64_t n, int quant_type, int block_size,
-                       void* stream) {
-    clear_error();
-    if (quant_type != VM_HIP_QUANT_INT4 && !(quant_type == VM_HIP_QUANT_INT8 && block_size > 0))
-        return fail_inval("vm_hip_qmm_col_pow: only blockwise scales (INT4, or INT8 with block_size > 0)");
-    if (k <= 0 || n <= 0 || k > INT32_MAX || n > INT32_MAX) return fail_inval("vm_hip_qmm_col_pow: bad shape");
-    if (!scale || !col_pow) return fail_inval("vm_hip_qmm_col_pow: null pointer");
-    const int bs = (quant_type == VM_HIP_QUANT_INT4 && block_size <= 0) ? 32 : block_size;
-    if (bs % 32 != 0 || n % 16 != 0) return fail_inval("vm_hip_qmm_col_pow: block_size % 32 and n % 16 must be 0");
-    return gemm_col_pow(scale, col_pow, static_cast<int>(k), static_cast<int>(n), bs, static_cast<hipStream_t>(stream));
-}
-
-int vm_hip_qmm_staged_f32(const void* a_staged, const float* col_pow, const int8_t* wq, const float* scale, float* c,
-                          int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size, void* stream) {
+int vm_hip_qmm_staged_f32(const void* a_staged, const int8_t* wq, const float* scale, float* c, int64_t rows_m,
+                          int64_t k, int64_t n, int quant_type, int block_size, void* stream) {
     clear_error();
     VM_TRY(validate_qmm(a_staged, wq, scale, c, rows_m, k, n, quant_type, block_size));
     VM_TRY(injected_failure("QuantizedMatMul", "launch"));
@@ -219,13 +207,10 @@ int vm_hip_qmm_staged_f32(const void* a_staged, const float* col_pow, const int8
     GemmPlan plan;
     if (gemm_plan(static_cast<int>(rows_m), static_cast<int>(k), static_cast<int>(n), quant_type, bs, &plan) != 0)
         return fail_inval("vm_hip_qmm_staged_f32: the shape does not take staged A (vm_hip_qmm_a_layout)");
-    if (plan.col_pow && !col_pow)
-        return fail_inval("vm_hip_qmm_staged_f32: this shape needs the per-column powers of two (vm_hip_qmm_col_pow)");
     const auto* ah = static_cast<const _Float16*>(a_staged);
     const auto* row_exp = reinterpret_cast<const int*>(static_cast<const char*>(a_staged) +
                                                        a_stage_half_bytes(rows_m, k, plan.pieces));
-    return gemm_qmm_staged_f32(plan, ah, row_exp, plan.col_pow ? col_pow : nullptr,
-                               reinterpret_cast<const uint8_t*>(wq), scale, c, static_cast<int>(rows_m),
+    return gemm_qmm_staged_f32(plan, ah, row_exp, reinterpret_cast<const uint8_t*>(wq), scale, c, static_cast<int>(rows_m),
                                static_cast<int>(k), static_cast<int>(n), bs, static_cast<hipStream_t>(stream));
 }
 

@@ -1,43 +1,45 @@
-// Prefill-shaped (rows_m > 4) quantized matmul on gfx950 MFMA
-// (v_mfma_f32_16x16x32_f16, fp32 accumulation).
+// Prefill-shaped (rows_m > 4) quantized matmul on gfx950 MFMA, fp32
+// accumulation.
 //
 // C[M, N] = A[M, K] * W[K, N] with W given as the reference's codes (INT8
 // [K, N] or INT4 packed [(K+1)/2, N], N contiguous) and fp32 scales.
 //
-// A is first split once per call (a_split_f16_kernel): each row r is
-// multiplied by 2^x_r, the power of two that puts its largest magnitude in
-// [2^14, 2^15), and written as two fp16 parts hi = fp16(a * 2^x_r) and
-// lo = fp16(a * 2^x_r - hi), so that hi + lo carries 22 significant bits of
-// any finite fp32 row without overflow or underflow.  Both parts go through
-// the MFMAs (products with the exact fp16 codes are exact, accumulation is
-// fp32), and the epilogue multiplies by 2^-x_r, which is exact: the
-// activations are used at fp32-equivalent precision.
+// A is first split once per call (the prep kernels, or its producer, see
+// a_split.h): each row r is multiplied by 2^x_r, the power of two that puts
+// its largest magnitude in [2^14, 2^15), and written as two fp16 parts
+// hi = fp16(a * 2^x_r) and lo = fp16(a * 2^x_r - hi), so that hi + lo
+// carries 22 significant bits of any finite fp32 row without overflow or
+// underflow.  Both parts go through the MFMAs (products with the exact fp16
+// codes are exact, accumulation is fp32), and the epilogue multiplies by
+// 2^-x_r, which is exact: the activations are used at fp32-equivalent
+// precision.
 //
-// Pipeline (per workgroup: a BM x BN output tile, four waves, K in steps of
-// 64 rows):
+// B: codes -> fp16 with packed-half magic numbers (0x6400 | (code ^ 0x80..)
+// is 1024 + 128 + code), exact.  Scales: INT8 per column multiplies each
+// fp32 result in the epilogue; blockwise scales (INT4, INT8 with block_size
+// > 0) multiply each 32-row chunk's fp32 sum, which the wide kernel keeps in
+// an accumulator of its own (the reference's per-block sum times the block
+// scale, quantized_matmul.cpp:76-90).  Beyond fp32 accumulation the only
+// rounding is A's split (relative 2^-22).
+//
+// Two kernels:
+//   qmm_mfma_kernel (small tiles, v_mfma_f32_16x16x32_f16) takes per-column
+//     INT8 with few rows;
+//   wide::qmm_mfma_wide_kernel (v_mfma_f32_32x32x16_f16) takes more rows
+//     and every blockwise call.
+// Small-tile pipeline (per workgroup: a BM x BN output tile, four waves, K
+// in steps of 64 rows):
 //   global -> registers  raw buffer loads (zeros past the end), two steps
 //                        ahead of the MFMAs;
 //   registers -> LDS     A: the hi and lo parts as loaded, row-major [BM][64];
-//                        B: codes -> fp16 with packed-half magic numbers
-//                        (0x6400 | (code ^ 0x80..) is 1024 + 128 + code),
-//                        times the block scale, stored in the codes' own
-//                        layout [64][BN] (N contiguous, 16-byte writes);
+//                        B: fp16 codes in the codes' own layout [64][BN]
+//                        (N contiguous, 16-byte writes);
 //   LDS -> MFMA          A operand: ds_read_b128 of 8 consecutive k;
 //                        B operand: two ds_read_b64_tr_b16 transposed reads
 //                        give each lane 8 consecutive k of one column.
 // Columns are kept in the order (c0, c2, c1, c3) inside every group of four
 // in LDS (the order the magic-number unpacking produces); the epilogue
 // writes each result to its true column.
-//
-// Scales.  INT8 per column: applied in the epilogue (fp32).  Blockwise
-// (INT4, INT8 with block_size > 0): B is staged as fp16(code * s / 2^e),
-// where 2^e is a per-column power of two with max_s / 2^e in [0.5, 1) over
-// the workgroup's K range, and the fp32 result is multiplied by 2^e (exact).
-// The normalisation keeps every staged weight inside fp16's normal range
-// whatever the scales' magnitude.  Beyond fp32 accumulation the only
-// rounding is then (code * s / 2^e) -> fp16 for blockwise weights (relative
-// 2^-11, a fixed function of the weights) and A's split (relative 2^-22);
-// INT8 per-column codes are exact and their scales apply in fp32.
 //
 // Split-K for small M: each split stores its scaled partial tile
 // with agent-scope stores, the last split of a tile (atomic ticket) adds
@@ -83,24 +85,14 @@ __device__ __forceinline__ half4v lds_read_tr16(const _Float16* p) {
     return __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(lp));
 }
 
-__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
-    const half2v h = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
-    return __builtin_bit_cast(uint32_t, h);
-}
-
-__device__ __forceinline__ uint32_t hmul2(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) * __builtin_bit_cast(half2v, b));
-}
-
 __device__ __forceinline__ uint32_t hsub2(uint32_t a, _Float16 b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) - half2v{b, b});
 }
 
-// KIND: 0 = INT8 per-column, 1 = INT8 blockwise, 2 = INT4 blockwise.
+// KIND: 0 = INT8 per-column (the only kind this kernel takes).
 template <int KIND, int BM, int BN, int WAVES_M, int WAVES_N>
 struct Tile {
-    static constexpr bool kInt4 = KIND == 2;
-    static constexpr bool kBlock = KIND != 0;
+    static_assert(KIND == 0, "the small-tile kernel takes per-column INT8 (blockwise scales: the wide kernel)");
     static constexpr int WM = BM / WAVES_M;
     static constexpr int WN = BN / WAVES_N;
     static constexpr int TM = WM / 16;
@@ -109,11 +101,10 @@ struct Tile {
     static constexpr int kBrow = BN + kBpad;                   // halves per B k-row
     static constexpr int kAPieces = BM * (kBK / 8);            // 8 halves (16 bytes) each
     static constexpr int kAPass = (kAPieces + kThreads - 1) / kThreads;
-    static constexpr int kBRows = kInt4 ? kBK / 2 : kBK;       // code byte rows per step
+    static constexpr int kBRows = kBK;                         // code byte rows per step
     static constexpr int kBPieces = kBRows * (BN / 16);        // 16 bytes each
     static constexpr int kBPass = (kBPieces + kThreads - 1) / kThreads;
     static constexpr int kQB = BN / 4;                         // column quads
-    static constexpr int kRedRows = kThreads / kQB;
     static_assert(WAVES_M * WAVES_N == 4, "four waves");
     static_assert(TM >= 1 && TN >= 1 && WM % 16 == 0 && WN % 16 == 0, "16x16 MFMA tiles");
     static_assert(BN % 16 == 0 && kThreads % kQB == 0, "tile shape");
@@ -125,7 +116,6 @@ struct Stage {
     u32x4 a[T::kAPass];
     u32x4 al[T::kAPass];
     u32x4 b[T::kBPass];
-    u32x4 s[T::kBlock ? T::kBPass : 1][T::kBlock ? 4 : 1];
 };
 
 // DEEP = 0: a two-step register pipeline over the split's K steps.
@@ -145,12 +135,6 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * T::kArow];
     __shared__ __attribute__((aligned(16))) _Float16 sAl[2][BM * T::kArow];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][kBK * T::kBrow];
-    __shared__ float sPow[T::kBlock ? BN : 1];   // 2^e per column (physical order)
-    __shared__ float sInv[T::kBlock ? BN : 1];   // 2^-e
-    // The scale-normalisation scratch lives in the second B buffer: it is
-    // used (and released by a barrier) before any B step is written there.
-    float* sRed = reinterpret_cast<float*>(sB[1]);
-    static_assert(!T::kBlock || T::kRedRows * BN * 4 <= kBK * T::kBrow * 2, "sRed fits in a B buffer");
     __shared__ unsigned ticket;
 
     const int tid = threadIdx.x;
@@ -183,43 +167,6 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wq, code_bytes);
     const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
 
-    // ---- per-column normalisation of block scales over this split's K range
-    auto normalise_scales = [&]() {
-        if constexpr (T::kBlock) {
-            const int b0 = k_begin / block_size;
-            const int b1 = (k_end + block_size - 1) / block_size;
-            const int q = tid % T::kQB;
-            float mx[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int b = b0 + tid / T::kQB; b < b1; b += 4 * T::kRedRows) {
-                u32x4 v[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int bb = b + u * T::kRedRows;
-                    const uint32_t off = bb < b1 ? (static_cast<uint32_t>(bb) * n + n0 + 4 * q) * 4u : scale_bytes;
-                    v[u] = buffer_load16(srs, off);
-                }
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], fabsf(__uint_as_float(v[u][e])));
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sRed[(tid / T::kQB) * BN + 4 * q + e] = mx[e];
-            __syncthreads();
-            if (tid < BN) {
-                float mm = 0.f;
-#pragma unroll
-                for (int r = 0; r < T::kRedRows; ++r) mm = fmaxf(mm, sRed[r * BN + tid]);
-                int e = 0;
-                if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
-                sPow[tid] = ldexpf(1.0f, e);
-                sInv[tid] = ldexpf(1.0f, -e);
-            }
-            __syncthreads();
-        }
-    };
-    if constexpr (DEEP == 0) normalise_scales();
-
     // ---- global -> registers for one step
     auto load_step = [&](int s, S& st) {
         const int k0 = (step0 + s) * kBK;
@@ -238,16 +185,9 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
             const int piece = tid + p * kThreads;
             const int row = piece / (BN / 16);            // code byte row within the step
             const int col = n0 + 16 * (piece % (BN / 16));
-            const int krow = T::kInt4 ? k0 / 2 + row : k0 + row;
-            const int klog = T::kInt4 ? k0 + 2 * row : k0 + row;   // first logical K row of the piece
-            const bool ok = piece < T::kBPieces && klog < k_end;
+            const int krow = k0 + row;
+            const bool ok = piece < T::kBPieces && krow < k_end;
             st.b[p] = buffer_load16(wrs, ok ? static_cast<uint32_t>(krow) * n + col : code_bytes);
-            if constexpr (T::kBlock) {
-                const uint32_t blk = static_cast<uint32_t>(klog) / static_cast<uint32_t>(block_size);
-                const uint32_t soff = ok ? (blk * n + col) * 4u : scale_bytes;
-#pragma unroll
-                for (int qd = 0; qd < 4; ++qd) st.s[p][qd] = buffer_load16(srs, soff + 16u * qd);
-            }
         }
     };
 
@@ -255,7 +195,7 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
     struct Packed {
         u32x4 a[T::kAPass];
         u32x4 al[T::kAPass];
-        u32x4 b[T::kBPass][T::kInt4 ? 4 : 2];
+        u32x4 b[T::kBPass][2];
     };
     auto convert_step = [&](const S& st, Packed& pk) {
 #pragma unroll
@@ -265,42 +205,12 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
         }
 #pragma unroll
         for (int p = 0; p < T::kBPass; ++p) {
-            const int piece = tid + p * kThreads;
-            const int cl = 16 * (piece % (BN / 16));      // local column of the piece
-            // normalised scales, paired in (c0, c2), (c1, c3) order per quad
-            uint32_t sn[8];
-            if constexpr (T::kBlock) {
-#pragma unroll
-                for (int qd = 0; qd < 4; ++qd) {
-                    const float* inv = sInv + cl + 4 * qd;
-                    sn[2 * qd] = pk_f16(__uint_as_float(st.s[p][qd][0]) * inv[0], __uint_as_float(st.s[p][qd][2]) * inv[2]);
-                    sn[2 * qd + 1] = pk_f16(__uint_as_float(st.s[p][qd][1]) * inv[1], __uint_as_float(st.s[p][qd][3]) * inv[3]);
-                }
-            }
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                if constexpr (T::kInt4) {
-                    const uint32_t x = st.b[p][d] ^ 0x88888888u;
-                    uint32_t e02 = hsub2((x & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
-                    uint32_t e13 = hsub2(((x >> 8) & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
-                    uint32_t o02 = hsub2(((x >> 4) & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
-                    uint32_t o13 = hsub2(((x >> 12) & 0x000F000Fu) | 0x64006400u, static_cast<_Float16>(1032.0f));
-                    // b[p][0..1]: even K row, 16 columns; b[p][2..3]: odd K row
-                    pk.b[p][d / 2][2 * (d % 2)] = hmul2(e02, sn[2 * d]);
-                    pk.b[p][d / 2][2 * (d % 2) + 1] = hmul2(e13, sn[2 * d + 1]);
-                    pk.b[p][2 + d / 2][2 * (d % 2)] = hmul2(o02, sn[2 * d]);
-                    pk.b[p][2 + d / 2][2 * (d % 2) + 1] = hmul2(o13, sn[2 * d + 1]);
-                } else {
-                    const uint32_t x = st.b[p][d] ^ 0x80808080u;
-                    uint32_t e02 = hsub2((x & 0x00FF00FFu) | 0x64006400u, static_cast<_Float16>(1152.0f));
-                    uint32_t e13 = hsub2(((x >> 8) & 0x00FF00FFu) | 0x64006400u, static_cast<_Float16>(1152.0f));
-                    if constexpr (T::kBlock) {
-                        e02 = hmul2(e02, sn[2 * d]);
-                        e13 = hmul2(e13, sn[2 * d + 1]);
-                    }
-                    pk.b[p][d / 2][2 * (d % 2)] = e02;
-                    pk.b[p][d / 2][2 * (d % 2) + 1] = e13;
-                }
+                const uint32_t x = st.b[p][d] ^ 0x80808080u;
+                pk.b[p][d / 2][2 * (d % 2)] = hsub2((x & 0x00FF00FFu) | 0x64006400u, static_cast<_Float16>(1152.0f));
+                pk.b[p][d / 2][2 * (d % 2) + 1] =
+                    hsub2(((x >> 8) & 0x00FF00FFu) | 0x64006400u, static_cast<_Float16>(1152.0f));
             }
         }
     };
@@ -324,18 +234,9 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
             if (piece >= T::kBPieces) continue;
             const int row = piece / (BN / 16);
             const int cl = 16 * (piece % (BN / 16));
-            if constexpr (T::kInt4) {
-                _Float16* r0 = lb + (2 * row) * T::kBrow + cl;
-                _Float16* r1 = r0 + T::kBrow;
-                *reinterpret_cast<u32x4*>(r0) = pk.b[p][0];
-                *reinterpret_cast<u32x4*>(r0 + 8) = pk.b[p][1];
-                *reinterpret_cast<u32x4*>(r1) = pk.b[p][2];
-                *reinterpret_cast<u32x4*>(r1 + 8) = pk.b[p][3];
-            } else {
-                _Float16* r0 = lb + row * T::kBrow + cl;
-                *reinterpret_cast<u32x4*>(r0) = pk.b[p][0];
-                *reinterpret_cast<u32x4*>(r0 + 8) = pk.b[p][1];
-            }
+            _Float16* r0 = lb + row * T::kBrow + cl;
+            *reinterpret_cast<u32x4*>(r0) = pk.b[p][0];
+            *reinterpret_cast<u32x4*>(r0 + 8) = pk.b[p][1];
         }
     };
     auto store_step = [&](const S& st, int buf) {
@@ -411,7 +312,6 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
         S st[DEEP];
 #pragma unroll
         for (int s = 0; s < DEEP; ++s) load_step(s, st[s]);
-        normalise_scales();   // its scale loads queue behind the steps' loads
         store_step(st[0], 0);
         __syncthreads();
 #pragma unroll
@@ -461,11 +361,7 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < T::TN; ++j) {
         const int cp = col_of(j);
-        if constexpr (T::kBlock) {
-            colscale[j] = sPow[cp];
-        } else {
-            colscale[j] = __uint_as_float(buffer_load4(srs, (n0 + cp < n) ? static_cast<uint32_t>(n0 + cp) * 4u : scale_bytes));
-        }
+        colscale[j] = __uint_as_float(buffer_load4(srs, (n0 + cp < n) ? static_cast<uint32_t>(n0 + cp) * 4u : scale_bytes));
     }
 
     // 2^-x of each of the lane's rows undoes the staging scale (exact).
@@ -554,73 +450,17 @@ __global__ __launch_bounds__(kThreads, BM >= 128 ? 1 : 2) void qmm_mfma_kernel(
 // kernel's weight unpacking produces B (a dot product does not depend on
 // the order of its terms, so A and B only have to agree).
 //
-// Workgroups [col_wgs, col_wgs + m) split one row each; rows of up to
-// kSplitHeld groups of eight per thread stay in registers between the
-// maximum and the split (one read of A), longer rows are read a second time
-// (from L2).  Workgroups [0, col_wgs) come first, so that they start before
-// the row workgroups: for blockwise scales they compute the per-column power
-// of two the wide kernel stages B with, 2^e with max_b |s[b, j]| / 2^e in
-// [0.5, 1) over all of K (e = 0 for an all-zero or non-finite maximum),
-// written as col_pow[j] = 2^e and col_pow[n + j] = 2^-e.  A column workgroup
-// takes 64 columns: 16 threads of float4 columns by 16 block groups, every
-// thread's scale loads in flight together (eight per batch).
+// Workgroup r splits row r; rows of up to kSplitHeld groups of eight per
+// thread stay in registers between the maximum and the split (one read of
+// A), longer rows are read a second time (from L2).
 constexpr int kSplitHeld = 3;   // k <= 6144 in one read
-constexpr int kPrepCols = 64;   // columns per column workgroup
-
-// Column workgroup `cw` of the prep: the per-column powers of two of 64
-// columns (16 threads of float4 columns by 16 block groups, every scale
-// load of a thread in flight together, eight per batch).
-__device__ void prep_col_pow(const float* __restrict__ scale, float* __restrict__ col_pow, int n, int nblk, int cw,
-                             float* wmax) {
-    const int tid = threadIdx.x;
-    const int j0 = cw * kPrepCols + 4 * (tid & 15);
-    const int bg = tid >> 4;
-    float mx[4] = {0.f, 0.f, 0.f, 0.f};
-    if (j0 < n) {
-        constexpr int kBatch = 8;
-        for (int b0 = bg; b0 < nblk; b0 += 16 * kBatch) {
-            float4 v[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int bb = b0 + 16 * u;
-                v[u] = bb < nblk ? *reinterpret_cast<const float4*>(scale + static_cast<int64_t>(bb) * n + j0)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                mx[0] = fmaxf(mx[0], fabsf(v[u].x));
-                mx[1] = fmaxf(mx[1], fabsf(v[u].y));
-                mx[2] = fmaxf(mx[2], fabsf(v[u].z));
-                mx[3] = fmaxf(mx[3], fabsf(v[u].w));
-            }
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) wmax[bg * kPrepCols + 4 * (tid & 15) + e] = mx[e];
-    __syncthreads();
-    const int j = cw * kPrepCols + tid;
-    if (tid < kPrepCols && j < n) {
-        float mm = 0.0f;
-        for (int g = 0; g < 16; ++g) mm = fmaxf(mm, wmax[g * kPrepCols + tid]);
-        int e = 0;
-        if (mm > 0.f && mm <= 3.0e38f) (void)frexpf(mm, &e);
-        col_pow[j] = ldexpf(1.0f, e);
-        col_pow[n + j] = ldexpf(1.0f, -e);
-    }
-}
 
 template <bool FRAG>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict__ a, _Float16* __restrict__ ah,
-                                                        int* __restrict__ row_exp, int m, int k, int vec,
-                                                        const float* __restrict__ scale, float* __restrict__ col_pow,
-                                                        int n, int nblk, int col_wgs) {
-    __shared__ float wmax[4 * 256];
+                                                        int* __restrict__ row_exp, int m, int k, int vec) {
+    __shared__ float wmax[4];
     const int tid = threadIdx.x;
-    if (static_cast<int>(blockIdx.x) < col_wgs) {
-        prep_col_pow(scale, col_pow, n, nblk, static_cast<int>(blockIdx.x), wmax);
-        return;
-    }
-    const int row = static_cast<int>(blockIdx.x) - col_wgs;
+    const int row = static_cast<int>(blockIdx.x);
     const float* src = a + static_cast<int64_t>(row) * k;
     const int groups = k >> 3;   // k % 32 == 0 on this path
     const bool held = groups <= kSplitHeld * 256;
@@ -711,21 +551,14 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const float* __restrict_
 // registers between their maxima and their split.  Operand order puts 32
 // rows side by side in every 1 KB piece, so one row alone writes 16 bytes
 // per 512-byte half-piece; R consecutive rows give each thread an R x
-// 16-byte run.  Column workgroups as in gemm_prep_kernel.
+// 16-byte run.
 template <int R, int GT>
 __global__ __launch_bounds__(256) void gemm_prep_frag_kernel(const float* __restrict__ a, _Float16* __restrict__ ah,
-                                                             int* __restrict__ row_exp, int m, int k, int vec,
-                                                             const float* __restrict__ scale,
-                                                             float* __restrict__ col_pow, int n, int nblk,
-                                                             int col_wgs) {
-    __shared__ float wmax[4 * 256];
+                                                             int* __restrict__ row_exp, int m, int k, int vec) {
+    __shared__ float wmax[4 * R];
     const int tid = threadIdx.x;
     const int wg = a_stage_wg(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
-    if (wg < col_wgs) {
-        prep_col_pow(scale, col_pow, n, nblk, wg, wmax);
-        return;
-    }
-    const int row0 = (wg - col_wgs) * R;
+    const int row0 = wg * R;
     const int groups = k >> 3;
     float4 v[R][GT][2];
     float mx[R];
@@ -859,12 +692,17 @@ struct Cfg {
     static constexpr bool kBlock = KIND != 0;
     static constexpr int kLdsB = BN * kRow;                           // halves per buffer
     static constexpr int kCRow = BN + 4;                              // epilogue tile row (floats)
-    static constexpr int kLdsBytes = (2 * G * kLdsB * 2 > BM * kCRow * 4) ? 2 * G * kLdsB * 2 : BM * kCRow * 4;
+    // blockwise scales of a step: [2 chunks of 32 K rows][BN] floats per
+    // buffer, indexed like B's LDS rows, after the B buffers
+    static constexpr int kLdsS = kBlock ? 2 * BN : 0;
+    static constexpr int kLoopBytes = 2 * G * kLdsB * 2 + 2 * G * kLdsS * 4;
+    static constexpr int kLdsBytes = kLoopBytes > BM * kCRow * 4 ? kLoopBytes : BM * kCRow * 4;
     // Two workgroups per CU when two fit in LDS and the registers a thread
     // holds (accumulators, D stages, B fragments, ~48 for addressing)
     // stay within the 256 that two waves per SIMD leave each; otherwise one,
     // with all 512.
-    static constexpr int kRegEstimate = TN * 16 + D * (32 + kBPer * (kWords + (kBlock ? 4 : 0))) + TN * 4 + 48;
+    static constexpr int kRegEstimate =
+        TN * 16 + (kBlock ? 32 : 0) + D * (32 + kBPer * (kWords + (kBlock ? 4 : 0))) + TN * 4 + 48;
     static constexpr int kWavesPerEu = G == 2 ? 2 : (2 * kLdsBytes <= 160 * 1024 && kRegEstimate <= 256) ? 2 : 1;
     static_assert((BM == 128 || BM == 64) && TN >= 1 && WN % 32 == 0, "32 x 32 MFMA tiles");
     static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -883,17 +721,11 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// fp16 pair {v, v}, rounded to nearest even
-__device__ __forceinline__ uint32_t splat_f16(float v) {
-    const _Float16 h = static_cast<_Float16>(v);
-    return __builtin_bit_cast(uint32_t, half2v{h, h});
-}
 
 template <int KIND, int BM, int BN, int D, int G>
 __global__ __launch_bounds__(256 * G) __attribute__((amdgpu_waves_per_eu(Cfg<KIND, BM, BN, D, G>::kWavesPerEu,
                                                                          Cfg<KIND, BM, BN, D, G>::kWavesPerEu)))
-void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict__ row_exp,
-                          const float* __restrict__ col_pow, const uint8_t* __restrict__ wq,
+void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict__ row_exp, const uint8_t* __restrict__ wq,
                           const float* __restrict__ scale, float* __restrict__ c, int m, int k, int n,
                           int block_size, int steps_per_split, int tiles_n, int tiles_m, uint32_t a_bytes,
                           uint32_t lo_offset, uint32_t code_bytes, uint32_t scale_bytes, float* __restrict__ partials,
@@ -935,21 +767,6 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
     const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
     const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wq, code_bytes);
     const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(scale, scale_bytes);
-
-    // 2^-e of the unit columns (blockwise scales)
-    float inv[C::kBPer][4];
-    if constexpr (C::kBlock) {
-        const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(col_pow, static_cast<uint32_t>(n) * 8u);
-#pragma unroll
-        for (int p = 0; p < C::kBPer; ++p) {
-            const int u = gtid + p * 256;
-            const int col = n0 + 4 * (u % C::kQuads);
-            const u32x4 v = buffer_load16(prs, (u < C::kUnits && col < n) ? (static_cast<uint32_t>(n) + col) * 4u
-                                                                         : static_cast<uint32_t>(n) * 8u);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) inv[p][e] = __uint_as_float(v[e]);
-        }
-    }
 
     // Scale block of a unit: with the loaded step's first row k0 = q0 *
     // block_size + r0, the unit's block is q0 + 0, 1 or 2 (block_size >= 32
@@ -1034,36 +851,33 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
             t[2][1] = perm(b67, b23, 0x05040100u);
             t[3][1] = perm(b67, b23, 0x07060302u);
         }
+        // exact fp16 codes (the block scales multiply each 32-row chunk's
+        // fp32 sum, see mfma_pair)
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
-            uint32_t sc = 0;
-            if constexpr (C::kBlock) sc = splat_f16(__uint_as_float(r.s[p][cc]) * inv[p][cc]);
             if constexpr (KIND == 2) {
                 const uint32_t x = t[cc][0] ^ 0x88888888u;
                 const _Float16 bias = static_cast<_Float16>(1032.0f);
-                out[cc][0] = hmul2(hsub2((x & 0x000F000Fu) | 0x64006400u, bias), sc);
-                out[cc][1] = hmul2(hsub2(((x >> 4) & 0x000F000Fu) | 0x64006400u, bias), sc);
-                out[cc][2] = hmul2(hsub2(((x >> 8) & 0x000F000Fu) | 0x64006400u, bias), sc);
-                out[cc][3] = hmul2(hsub2(((x >> 12) & 0x000F000Fu) | 0x64006400u, bias), sc);
+                out[cc][0] = hsub2((x & 0x000F000Fu) | 0x64006400u, bias);
+                out[cc][1] = hsub2(((x >> 4) & 0x000F000Fu) | 0x64006400u, bias);
+                out[cc][2] = hsub2(((x >> 8) & 0x000F000Fu) | 0x64006400u, bias);
+                out[cc][3] = hsub2(((x >> 12) & 0x000F000Fu) | 0x64006400u, bias);
             } else {
                 const _Float16 bias = static_cast<_Float16>(1152.0f);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const uint32_t x = t[cc][h] ^ 0x80808080u;
-                    uint32_t e = hsub2((x & 0x00FF00FFu) | 0x64006400u, bias);
-                    uint32_t o = hsub2(((x >> 8) & 0x00FF00FFu) | 0x64006400u, bias);
-                    if constexpr (C::kBlock) {
-                        e = hmul2(e, sc);
-                        o = hmul2(o, sc);
-                    }
-                    out[cc][2 * h] = e;
-                    out[cc][2 * h + 1] = o;
+                    out[cc][2 * h] = hsub2((x & 0x00FF00FFu) | 0x64006400u, bias);
+                    out[cc][2 * h + 1] = hsub2(((x >> 8) & 0x00FF00FFu) | 0x64006400u, bias);
                 }
             }
         }
     };
-    // LDS B buffer `buf` (0, 1) of this group
+    // LDS B buffer `buf` (0, 1) of this group, and its chunk scales
     auto lds_b = [&](int buf) { return lds + (grp * 2 + buf) * C::kLdsB; };
+    auto lds_s = [&](int buf) {
+        return reinterpret_cast<float*>(lds + 2 * G * C::kLdsB) + (grp * 2 + buf) * C::kLdsS;
+    };
     auto write_b = [&](const R& r, int buf) {
         _Float16* b = lds_b(buf);
 #pragma unroll
@@ -1077,6 +891,14 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
 #pragma unroll
                 for (int cc = 0; cc < 4; ++cc)
                     *reinterpret_cast<u32x4*>(b + (cc * C::kQuads + q) * kRow + 8 * kg) = out[cc];
+                if constexpr (C::kBlock) {
+                    // the first unit of each 32-row chunk holds the chunk's block scales
+                    if (kg % 4 == 0) {
+                        float* ss = lds_s(buf) + (kg / 4) * BN;
+#pragma unroll
+                        for (int cc = 0; cc < 4; ++cc) ss[cc * C::kQuads + q] = __uint_as_float(r.s[p][cc]);
+                    }
+                }
             }
         }
     };
@@ -1087,23 +909,61 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
 
-    // MFMAs of two 16-k sub-steps: every tile's hi product, then every
-    // tile's lo product (consecutive MFMAs rarely wait for each other's
-    // accumulator)
+    // MFMAs of two 16-k sub-steps (one 32-row chunk of K): every tile's hi
+    // product, then every tile's lo product (consecutive MFMAs rarely wait
+    // for each other's accumulator).  Blockwise scales: the chunk lies in
+    // one scale block, so its products go to a fresh accumulator that is
+    // then multiplied by the block scale of its column and added to the
+    // total in fp32 (quantized_matmul.cpp:76-90: a block's sum times its
+    // scale), the codes themselves being exact in fp16.
     auto mfma_pair = [&](const R& r, int buf, int q0) {
         const _Float16* b = lds_b(buf);
+        if constexpr (C::kBlock) {
+            // tiles two at a time, so that two chunk accumulators are live
+            constexpr int kPair = C::TN >= 2 ? 2 : 1;
+            const float* ss = lds_s(buf) + (q0 / 2) * BN;
 #pragma unroll
-        for (int q = q0; q < q0 + 2; ++q) {
-            half8v bf[C::TN];
+            for (int j0 = 0; j0 < C::TN; j0 += kPair) {
+                floatx16 blk[kPair];
 #pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-                bf[j] = *reinterpret_cast<const half8v*>(b + (wn * C::WN + j * 32 + fr) * kRow + q * 16 + 8 * fh);
+                for (int jj = 0; jj < kPair; ++jj)
 #pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.ah[q], bf[j], acc[j], 0, 0, 0);
+                    for (int e = 0; e < 16; ++e) blk[jj][e] = 0.f;
 #pragma unroll
-            for (int j = 0; j < C::TN; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.al[q], bf[j], acc[j], 0, 0, 0);
+                for (int q = q0; q < q0 + 2; ++q) {
+                    half8v bf[kPair];
+#pragma unroll
+                    for (int jj = 0; jj < kPair; ++jj)
+                        bf[jj] = *reinterpret_cast<const half8v*>(b + (wn * C::WN + (j0 + jj) * 32 + fr) * kRow +
+                                                                  q * 16 + 8 * fh);
+#pragma unroll
+                    for (int jj = 0; jj < kPair; ++jj)
+                        blk[jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.ah[q], bf[jj], blk[jj], 0, 0, 0);
+#pragma unroll
+                    for (int jj = 0; jj < kPair; ++jj)
+                        blk[jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.al[q], bf[jj], blk[jj], 0, 0, 0);
+                }
+#pragma unroll
+                for (int jj = 0; jj < kPair; ++jj) {
+                    const float sj = ss[wn * C::WN + (j0 + jj) * 32 + fr];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[j0 + jj][e] = fmaf(blk[jj][e], sj, acc[j0 + jj][e]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int q = q0; q < q0 + 2; ++q) {
+                half8v bf[C::TN];
+#pragma unroll
+                for (int j = 0; j < C::TN; ++j)
+                    bf[j] = *reinterpret_cast<const half8v*>(b + (wn * C::WN + j * 32 + fr) * kRow + q * 16 + 8 * fh);
+#pragma unroll
+                for (int j = 0; j < C::TN; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.ah[q], bf[j], acc[j], 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < C::TN; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r.al[q], bf[j], acc[j], 0, 0, 0);
+            }
         }
     };
 
@@ -1114,6 +974,9 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
     // the VALU work and the loads, the remaining fragment reads halfway.
     auto interleave = [&]() {
 #if VM_WIDE_SCHED
+        // (per-column INT8 only: the blockwise loop's chunk accumulators
+        // leave no registers for hoisting every fragment read)
+        if constexpr (C::kBlock) return;
         constexpr int kMfma = 4 * C::TN * 2;
         constexpr int kLoads = 8 + C::kBPer * (C::kWords + (C::kBlock ? 1 : 0));
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::TN, 0);   // DS reads, sub-steps 0 and 1
@@ -1208,8 +1071,8 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
         __syncthreads();
     }
     if (grp == 0) {
-        const __amdgpu_buffer_rsrc_t crs = C::kBlock ? buffer_rsrc(col_pow, static_cast<uint32_t>(n) * 4u) : srs;
-        const uint32_t lim = C::kBlock ? static_cast<uint32_t>(n) * 4u : scale_bytes;
+        // per-column INT8 scales multiply the fp32 sums here; blockwise
+        // scales were applied chunk by chunk
         float colscale[C::TN];
         int tcol[C::TN];
 #pragma unroll
@@ -1217,7 +1080,9 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
             const int rr = wn * C::WN + j * 32 + fr;
             tcol[j] = 4 * (rr % C::kQuads) + rr / C::kQuads;
             const int col = n0 + tcol[j];
-            colscale[j] = __uint_as_float(buffer_load4(crs, col < n ? static_cast<uint32_t>(col) * 4u : lim));
+            colscale[j] = C::kBlock ? 1.0f
+                                    : __uint_as_float(buffer_load4(srs, col < n ? static_cast<uint32_t>(col) * 4u
+                                                                                : scale_bytes));
         }
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -1229,15 +1094,18 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
         }
     }
     __syncthreads();
-    const uint32_t out_lim = static_cast<uint32_t>(min(static_cast<int64_t>(m) * n * 4, int64_t(0x7fffffff)));
+    // The tile's rows of C (or of the split's partials) from a 64-bit base:
+    // byte offsets within BM rows stay 32-bit for any C (gemm_plan bounds n).
+    const uint32_t out_lim = static_cast<uint32_t>(static_cast<int64_t>(min(BM, m - m0)) * n * 4);
     const __amdgpu_buffer_rsrc_t out_rs =
-        buffer_rsrc(splits == 1 ? c : partials + static_cast<int64_t>(split) * m * n, out_lim);
+        buffer_rsrc((splits == 1 ? c : partials + static_cast<int64_t>(split) * m * n) + static_cast<int64_t>(m0) * n,
+                    out_lim);
     for (int idx = tid; idx < BM * (BN / 4); idx += C::kThreads) {
         const int trow = idx / (BN / 4);
         const int tc = 4 * (idx % (BN / 4));
         const int row = m0 + trow, col = n0 + tc;
         const u32x4 v = *reinterpret_cast<const u32x4*>(sc + trow * C::kCRow + tc);
-        const uint32_t off = (row < m && col < n) ? (static_cast<uint32_t>(row) * n + col) * 4u : out_lim;
+        const uint32_t off = (row < m && col < n) ? (static_cast<uint32_t>(trow) * n + col) * 4u : out_lim;
         if (splits == 1) buffer_store16(out_rs, off, v);
         else coherent_store16(out_rs, off, v);   // read by another workgroup (XCD) after the ticket
     }
@@ -1249,9 +1117,10 @@ void qmm_mfma_wide_kernel(const _Float16* __restrict__ a, const int* __restrict_
     if (tid == 0) ticket = ticket_take(&counters[tile], static_cast<unsigned>(splits));
     __syncthreads();
     if (ticket != static_cast<unsigned>(splits - 1)) return;
+    // (split calls keep splits * m * n * 4 below 2^31, choose_wide)
     const int64_t stride = static_cast<int64_t>(m) * n;
     const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(partials, 0x7fffffff);
-    const __amdgpu_buffer_rsrc_t crs = buffer_rsrc(c, out_lim);
+    const __amdgpu_buffer_rsrc_t crs = buffer_rsrc(c, static_cast<uint32_t>(min(stride * 4, int64_t(0x7fffffff))));
     for (int idx = tid; idx < BM * (BN / 4); idx += C::kThreads) {
         const int row = m0 + idx / (BN / 4);
         const int col = n0 + 4 * (idx % (BN / 4));
@@ -1445,7 +1314,6 @@ struct WideConfig {
 //     of a second, partial round (K = 2048, N = 11264: 352 tiles, 66.1 us vs
 //     75.0 with two groups).
 WideConfig choose_wide(int kind, int m, int k, int n) {
-    (void)kind;
     WideConfig cfg;
     const int steps = (k + kBK - 1) / kBK;
     cfg.bm = 128;
@@ -1456,7 +1324,9 @@ WideConfig choose_wide(int kind, int m, int k, int n) {
         while (s * 2 <= kMaxSplits && tiles * s < 150 && steps / (s * 2 * cfg.groups) >= 4) s *= 2;
         return s;
     };
-    cfg.bn = m >= 256 ? 128 : 64;
+    // blockwise scales: 64-column tiles (two 32 x 32 tiles per wave, see
+    // the kernel's chunk accumulators)
+    cfg.bn = m >= 256 && kind == 0 ? 128 : 64;
     int s = splits_of(tiles_of(cfg.bn));
     if (cfg.bn == 128 && steps / (s * cfg.groups) < 8) {
         const int s64 = splits_of(tiles_of(64));
@@ -1465,17 +1335,27 @@ WideConfig choose_wide(int kind, int m, int k, int n) {
             s = s64;
         }
     }
-    if (s == 1 && tiles_of(cfg.bn) > 256 && cfg.bn == 128) cfg.groups = 1;
+    if (s == 1 && tiles_of(cfg.bn) > 256) cfg.groups = 1;
+    if (kind != 0 && (m <= 64 || m >= 256)) {
+        // blockwise scales, few or many rows: 64 x 128 tiles, one wave
+        // group (M = 512, K = 2048, N = 5632, INT4: 49.3 us, against 51.5
+        // with 128 x 64 and 61.9 with 128 x 64 in two groups; M = 128 keeps
+        // 128 x 64 in two groups with K splits, 25.8 against 28.0 us)
+        cfg.bm = 64;
+        cfg.bn = 128;
+        cfg.groups = 1;
+        s = splits_of(tiles_of(cfg.bn));
+    }
     cfg.splits = s;
     // Tuning override for measurement sweeps: VELOMIND_GEMM_WIDE="BM,BN,S,D[,G]"
     if (const char* env = std::getenv("VELOMIND_GEMM_WIDE")) {
         int bm = 0, bn = 0, sx = 0, d = 0, g = 1;
         const int got = std::sscanf(env, "%d,%d,%d,%d,%d", &bm, &bn, &sx, &d, &g);
-        const bool known = (bm == 128 && bn == 128 && ((d == 2 && (g == 1 || g == 2)) || (d == 4 && g == 1))) ||
+        const bool wide_ok = kind == 0;   // four tiles per wave, four stages: per-column INT8 only
+        const bool known = (bm == 128 && bn == 128 && wide_ok && ((d == 2 && (g == 1 || g == 2)) || (d == 4 && g == 1))) ||
                            (bm == 128 && bn == 64 && d == 2 && (g == 1 || g == 2)) ||
-
-                           (bm == 64 && bn == 128 && (d == 2 || d == 4) && g == 1) ||
-                           (bm == 64 && bn == 256 && d == 2 && g == 1);
+                           (bm == 64 && bn == 128 && (d == 2 || (d == 4 && wide_ok)) && g == 1) ||
+                           (bm == 64 && bn == 256 && d == 2 && g == 1 && wide_ok);
         if (got >= 4 && sx >= 1 && sx <= kMaxSplits && known) {
             cfg.bm = bm;
             cfg.bn = bn;
@@ -1490,9 +1370,10 @@ WideConfig choose_wide(int kind, int m, int k, int n) {
 }
 
 bool use_wide_kernel(int kind, int m, int k, int n) {
-    // The wide kernel writes C with 32-bit byte offsets (the small-tile
-    // kernel addresses it with 64-bit pointers), whatever the overrides say.
-    if (static_cast<int64_t>(m) * n * 4 >= (int64_t(1) << 31)) return false;
+    // Blockwise scales: only the wide kernel applies them to each 32-row
+    // chunk's fp32 sum (the small-tile kernel folds them into fp16 weights,
+    // 2^-11 relative rounding per weight), so it takes every such call.
+    if (kind != 0) return true;
     if (std::getenv("VELOMIND_GEMM_CFG")) return false;
     const char* env = std::getenv("VELOMIND_GEMM_WIDE");
     if (env && env[0] == '0' && env[1] == '\0') return false;
@@ -1504,7 +1385,7 @@ bool use_wide_kernel(int kind, int m, int k, int n) {
 }
 
 template <int KIND, int BM, int BN, int D, int G>
-int launch_wide(const _Float16* a, const int* row_exp, const float* col_pow, const uint8_t* wq, const float* scale,
+int launch_wide(const _Float16* a, const int* row_exp, const uint8_t* wq, const float* scale,
                 float* c, int m, int k, int n, int block_size, int splits, hipStream_t stream) {
     using C = wide::Cfg<KIND, BM, BN, D, G>;
     auto kernel = wide::qmm_mfma_wide_kernel<KIND, BM, BN, D, G>;
@@ -1533,27 +1414,32 @@ int launch_wide(const _Float16* a, const int* row_exp, const float* col_pow, con
         static_cast<uint32_t>((KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : static_cast<int64_t>(k)) * n);
     const uint32_t scale_bytes = static_cast<uint32_t>((KIND == 0 ? 1 : nblk) * n * 4);
     hipLaunchKernelGGL(kernel, dim3(tiles_n * tiles_m * splits), dim3(C::kThreads), C::kLdsBytes, stream, a, row_exp,
-                       col_pow, wq, scale, c, m, k, n, block_size, sps, tiles_n, tiles_m, a_bytes, lo_offset,
+                       wq, scale, c, m, k, n, block_size, sps, tiles_n, tiles_m, a_bytes, lo_offset,
                        code_bytes, scale_bytes, ws.partials, ws.counters);
     return check_launch("QuantizedMatMul", stream);
 }
 
 template <int KIND>
-int launch_wide_kind(const _Float16* a, const int* row_exp, const float* col_pow, const uint8_t* wq,
+int launch_wide_kind(const _Float16* a, const int* row_exp, const uint8_t* wq,
                      const float* scale, float* c, int m, int k, int n, int block_size, hipStream_t stream) {
     const WideConfig cfg = choose_wide(KIND, m, k, n);
 #define VM_WIDE(BMX, BNX, DX, GX)                                                                              \
     if (cfg.bm == BMX && cfg.bn == BNX && cfg.depth == DX && cfg.groups == GX)                                 \
-        return launch_wide<KIND, BMX, BNX, DX, GX>(a, row_exp, col_pow, wq, scale, c, m, k, n, block_size,      \
+        return launch_wide<KIND, BMX, BNX, DX, GX>(a, row_exp, wq, scale, c, m, k, n, block_size,               \
                                                    cfg.splits, stream);
-    VM_WIDE(128, 128, 2, 1)
-    VM_WIDE(128, 128, 2, 2)
-    VM_WIDE(128, 128, 4, 1)
     VM_WIDE(128, 64, 2, 1)
     VM_WIDE(128, 64, 2, 2)
     VM_WIDE(64, 128, 2, 1)
-    VM_WIDE(64, 128, 4, 1)
-    VM_WIDE(64, 256, 2, 1)
+    // four 32 x 32 tiles per wave, and four register stages: per-column
+    // INT8 only (blockwise scales hold a chunk accumulator per tile pair,
+    // which leaves no registers for them)
+    if constexpr (KIND == 0) {
+        VM_WIDE(128, 128, 2, 1)
+        VM_WIDE(128, 128, 2, 2)
+        VM_WIDE(64, 256, 2, 1)
+        VM_WIDE(128, 128, 4, 1)
+        VM_WIDE(64, 128, 4, 1)
+    }
 #undef VM_WIDE
     return VM_HIP_EUNSUPPORTED;
 }
@@ -1583,7 +1469,7 @@ int gemm_plan(int m, int k, int n, int quant_type, int block_size, GemmPlan* pla
     if (m <= 4 || k % 32 != 0 || n % 16 != 0) return VM_HIP_EUNSUPPORTED;
     // (A's two fp16 parts take m * k * 4 bytes, addressed with 32-bit offsets)
     if ((static_cast<int64_t>(m) + 31) / 32 * 32 * k * 4 >= (int64_t(1) << 31) ||
-        static_cast<int64_t>(k) * n >= (int64_t(1) << 31) ||
+        static_cast<int64_t>(k) * n >= (int64_t(1) << 31) || static_cast<int64_t>(n) * 128 * 4 >= (int64_t(1) << 31) ||
         static_cast<int64_t>(m) * n * 4 * kMaxSplits >= (int64_t(1) << 40))
         return VM_HIP_EUNSUPPORTED;
     // one-dimensional grid of at most 2^30 workgroups
@@ -1599,31 +1485,19 @@ int gemm_plan(int m, int k, int n, int quant_type, int block_size, GemmPlan* pla
     }
     plan->kind = kind;
     plan->pieces = use_wide_kernel(kind, m, k, n);
-    plan->col_pow = plan->pieces && kind != 0;
     return 0;
 }
 
-// The per-column powers of two of blockwise scales for the wide kernel
-// (col_pow[j] = 2^e, col_pow[n + j] = 2^-e), alone: the prep's column
-// workgroups without rows.
-int gemm_col_pow(const float* scale, float* col_pow, int k, int n, int block_size, hipStream_t stream) {
-    const int nblk = (k + block_size - 1) / block_size;
-    const int col_wgs = (n + kPrepCols - 1) / kPrepCols;
-    hipLaunchKernelGGL((gemm_prep_frag_kernel<1, 1>), dim3(col_wgs), dim3(256), 0, stream, nullptr, nullptr, nullptr,
-                       0, k, 0, scale, col_pow, n, nblk, col_wgs);
-    return check_launch("QuantizedMatMul", stream);
-}
-
-int gemm_qmm_staged_f32(const GemmPlan& plan, const _Float16* ah, const int* row_exp, const float* col_pow,
+int gemm_qmm_staged_f32(const GemmPlan& plan, const _Float16* ah, const int* row_exp,
                         const uint8_t* wq, const float* scale, float* c, int m, int k, int n, int block_size,
                         hipStream_t stream) {
     if (plan.pieces) {
-        if (plan.kind == 2) return launch_wide_kind<2>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
-        if (plan.kind == 1) return launch_wide_kind<1>(ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
-        return launch_wide_kind<0>(ah, row_exp, col_pow, wq, scale, c, m, k, n, 0, stream);
+        if (plan.kind == 2) return launch_wide_kind<2>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
+        if (plan.kind == 1) return launch_wide_kind<1>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
+        return launch_wide_kind<0>(ah, row_exp, wq, scale, c, m, k, n, 0, stream);
     }
-    if (plan.kind == 2) return launch_kind<2>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
-    if (plan.kind == 1) return launch_kind<1>(ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
+    // (blockwise scales always take the wide kernel, gemm_plan)
+    if (plan.kind != 0) return VM_HIP_EUNSUPPORTED;
     return launch_kind<0>(ah, row_exp, wq, scale, c, m, k, n, 0, stream);
 }
 
@@ -1631,38 +1505,30 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
                  int quant_type, int block_size, hipStream_t stream) {
     GemmPlan plan;
     VM_TRY(gemm_plan(m, k, n, quant_type, block_size, &plan));
-    // A's row-scaled fp16 parts (hi, lo) and row exponents, then, for the
-    // wide kernel with blockwise scales, the per-column powers of two.
+    // A's row-scaled fp16 parts (hi, lo) and row exponents
     const std::size_t half_bytes = a_stage_half_bytes(m, k, plan.pieces);
-    const std::size_t stage_bytes = a_stage_bytes(m, k, plan.pieces);
-    const std::size_t pow_bytes = plan.col_pow ? static_cast<std::size_t>(n) * 2 * sizeof(float) : 0;
     void* aux = nullptr;
-    VM_TRY(get_aux(stream, stage_bytes + pow_bytes, &aux));
+    VM_TRY(get_aux(stream, a_stage_bytes(m, k, plan.pieces), &aux));
     auto* ah = static_cast<_Float16*>(aux);
     auto* row_exp = reinterpret_cast<int*>(static_cast<char*>(aux) + half_bytes);
-    auto* col_pow = plan.col_pow ? reinterpret_cast<float*>(static_cast<char*>(aux) + stage_bytes) : nullptr;
     const int vec = reinterpret_cast<uintptr_t>(a) % 16 == 0 ? 1 : 0;
-    const int nblk = plan.kind == 0 ? 1 : (k + block_size - 1) / block_size;
-    const int col_wgs = plan.col_pow ? (n + kPrepCols - 1) / kPrepCols : 0;
     if (plan.pieces) {
         const int gt = (k / 8 + 255) / 256;
         const int rows_per_wg = prep_rows_per_wg(m, gt);
 #define VM_PREP(RX, GX)                                                                                           \
     if (gt == GX && rows_per_wg == RX)                                                                            \
-        hipLaunchKernelGGL((gemm_prep_frag_kernel<RX, GX>), dim3(col_wgs + (m + RX - 1) / RX), dim3(256), 0,     \
-                           stream, a, ah, row_exp, m, k, vec, scale, col_pow, n, nblk, col_wgs);                  \
+        hipLaunchKernelGGL((gemm_prep_frag_kernel<RX, GX>), dim3((m + RX - 1) / RX), dim3(256), 0, stream, a, ah, \
+                           row_exp, m, k, vec);                                                                   \
     else
         VM_PREP(8, 1) VM_PREP(4, 1) VM_PREP(2, 1) VM_PREP(1, 1) VM_PREP(4, 2) VM_PREP(2, 2) VM_PREP(1, 2)
         VM_PREP(2, 3) VM_PREP(1, 3)
 #undef VM_PREP
-            hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(m + col_wgs), dim3(256), 0, stream, a, ah, row_exp, m, k,
-                               vec, scale, col_pow, n, nblk, col_wgs);
+            hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k, vec);
     } else {
-        hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k, vec, scale,
-                           col_pow, n, nblk, 0);
+        hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(m), dim3(256), 0, stream, a, ah, row_exp, m, k, vec);
     }
     VM_TRY(check_launch("QuantizedMatMul", stream));
-    return gemm_qmm_staged_f32(plan, ah, row_exp, col_pow, wq, scale, c, m, k, n, block_size, stream);
+    return gemm_qmm_staged_f32(plan, ah, row_exp, wq, scale, c, m, k, n, block_size, stream);
 }
 
 }  // namespace vmhip

@@ -24,21 +24,17 @@ int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
 
 // How the GEMM takes a shape: kind 0 = INT8 per column, 1 = INT8 blockwise,
 // 2 = INT4; `pieces`: A staged in the wide kernel's operand order (else
-// row-major, a_split.h); `col_pow`: the wide kernel needs the per-column
-// powers of two of blockwise scales.  VM_HIP_EUNSUPPORTED when the GEMM does
-// not take the shape (rows <= 4, K % 32, N % 16, sizes past 32-bit offsets).
+// row-major, a_split.h; blockwise scales always take the wide kernel).
+// VM_HIP_EUNSUPPORTED when the GEMM does not take the shape (rows <= 4,
+// K % 32, N % 16, sizes past 32-bit offsets).
 struct GemmPlan {
     int kind = 0;
     bool pieces = false;
-    bool col_pow = false;
 };
 int gemm_plan(int m, int k, int n, int quant_type, int block_size, GemmPlan* plan);
 // The GEMM on A staged by its producer (a_split.h layout for the plan).
-int gemm_qmm_staged_f32(const GemmPlan& plan, const _Float16* ah, const int* row_exp, const float* col_pow,
-                        const uint8_t* wq, const float* scale, float* c, int m, int k, int n, int block_size,
-                        hipStream_t stream);
-// The per-column powers of two ([2n] floats) of blockwise scales.
-int gemm_col_pow(const float* scale, float* col_pow, int k, int n, int block_size, hipStream_t stream);
+int gemm_qmm_staged_f32(const GemmPlan& plan, const _Float16* ah, const int* row_exp, const uint8_t* wq,
+                        const float* scale, float* c, int m, int k, int n, int block_size, hipStream_t stream);
 
 // Any-shape reference-order kernel used for layouts the fast kernels do
 // not cover (odd N, block sizes that are not multiples of 32).

@@ -123,8 +123,7 @@ def _declare(L: ctypes.CDLL) -> None:
                                                          c_int64, c_int64, c_int64, c_int64, c_float,
                                                          POINTER(Prefetch), p], c_int),
         "vm_hip_qmm_a_layout": ([c_int64, c_int64, c_int64, c_int, c_int, POINTER(c_int), POINTER(c_int64)], c_int),
-        "vm_hip_qmm_col_pow": ([p, p, c_int64, c_int64, c_int, c_int, p], c_int),
-        "vm_hip_qmm_staged_f32": ([p, p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
+        "vm_hip_qmm_staged_f32": ([p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_add_rmsnorm_stage_f32": ([p, p, p, p, c_int, p, c_int64, c_int64, c_float, p], c_int),
         "vm_hip_silu_mul_stage_f32": ([p, p, c_int, p, c_int64, c_int64, p], c_int),
     }
@@ -156,7 +155,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32",
             "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32", "vm_hip_decode_workspace_bytes",
             "vm_hip_decode_step", "vm_hip_decode_status", "vm_hip_decode_trace_read",
-            "vm_hip_qmm_a_layout", "vm_hip_qmm_col_pow", "vm_hip_qmm_staged_f32", "vm_hip_add_rmsnorm_stage_f32",
+            "vm_hip_qmm_a_layout", "vm_hip_qmm_staged_f32", "vm_hip_add_rmsnorm_stage_f32",
             "vm_hip_silu_mul_stage_f32"]
 
 
