@@ -489,6 +489,73 @@ GEMM_K, GEMM_N = 2048, 5632
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
+GEMV_TRACE_PHASES = ("entry_to_first_load", "first_load_to_staged", "chunk_reduce", "waves_summed",
+                     "outputs_done")
+
+
+def gemv_trace_report(H, stream, reps: int = 10) -> dict:
+    """Phase timing of the decode GEMV (qmm_gemv.hip lists the events) from a
+    library built with VELOMIND_GEMV_TRACE=1: for each TinyLlama-1.1B INT4
+    decode shape and config 1's INT8 shape, one HIP graph of cold launches
+    over a Rotation, replayed `reps` times; the last launch's timestamps as
+    medians over its workgroups, the spread of their starts, the last
+    workgroup's end, and the replay's time per launch (the rest of which is
+    spent between kernels)."""
+    lib = H.open_library()
+    probe = np.zeros(1, np.uint64)
+    if lib.vm_hip_gemv_trace_read(probe.ctypes.data, 0) != 0:
+        raise RuntimeError("--gemv-trace needs libvmhip built with VELOMIND_GEMV_TRACE=1")
+    wgs, events = 4096, 8
+
+    def trace(launch_all, copies):
+        launch_all()
+        stream.synchronize()
+        us = timed_replay(H, stream, launch_all, reps) * 1e3 / copies
+        buf = np.zeros(wgs * events, np.uint64)
+        H.check(lib.vm_hip_gemv_trace_read(buf.ctypes.data, buf.nbytes))
+        t = buf.reshape(wgs, events)[:, :6].astype(np.int64)
+        # workgroup 0 runs in every launch; slots past this grid hold older launches
+        t = t[np.abs(t[:, 0] - t[0, 0]) < 2000]
+        rel = (t - t[:, 0].min()) * 0.01   # us
+        d = np.diff(rel, axis=1)
+        end = float(rel[:, 5].max())
+        return {"us_per_launch": round(us, 3), "workgroups": int(len(t)),
+                "start_spread_us": round(float(rel[:, 0].max()), 2),
+                "phases_us_median": {name: round(float(np.median(d[:, i])), 2)
+                                     for i, name in enumerate(GEMV_TRACE_PHASES)},
+                "last_done_us": round(end, 2), "between_kernels_us": round(us - end, 2)}
+
+    out = {}
+    wl = Workload(H, stream)
+    for (k, n), (mp, ms) in sorted(wl.masters.items()):
+        rot = Rotation(H, mp, ms, stream)
+
+        def launch_all(rot=rot, k=k, n=n):
+            for pa, sa in rot.addrs:
+                H.qmm_f32(wl.x[k].addr, pa, sa, wl.out[n].addr, 1, k, n, H.QUANT_INT4, BLOCK, stream)
+
+        out[f"int4_{k}x{n}"] = trace(launch_all, rot.copies)
+        rot.close()
+    k, n = CONFIG1_K, CONFIG1_N
+    rng = np.random.default_rng(3)
+    dw = H.DeviceBuffer.from_array((rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)))
+    p, s = H.DeviceBuffer(k * n), H.DeviceBuffer(n * 4)
+    H.pack_int8(dw.addr, p.addr, s.addr, k, n)
+    H.synchronize()
+    dx, dc = H.DeviceBuffer.from_array(rng.standard_normal(k, dtype=np.float32)), H.DeviceBuffer(n * 4)
+    rot = Rotation(H, p, s, stream)
+
+    def launch_int8():
+        for pa, sa in rot.addrs:
+            H.qmm_f32(dx.addr, pa, sa, dc.addr, 1, k, n, H.QUANT_INT8, 0, stream)
+
+    out[f"int8_{k}x{n}"] = trace(launch_int8, rot.copies)
+    rot.close()
+    for b in (dw, p, s, dx, dc):
+        b.close()
+    return out
+
+
 def gemm_setup(H):
     """BASELINE config 3 operands: W [2048, 5632] N(0, 0.02) packed on the
     GPU as INT8 (per column) and INT4 (block 32); A [512, 2048] N(0, 1)."""
@@ -704,6 +771,8 @@ def main() -> int:
                     help="with --e2e-only and --e2e-model: comma-separated layer counts to run instead of the "
                          "config's (per-layer decode time with the weights resident in the 256 MB Infinity Cache "
                          "at few layers, streamed from HBM at many)")
+    ap.add_argument("--gemv-trace", action="store_true",
+                    help="phase timestamps of the decode GEMV per shape (library built with VELOMIND_GEMV_TRACE=1)")
     ap.add_argument("--decode-trace", action="store_true",
                     help="only the one-launch decode step's phase timestamps (library built with "
                          "VELOMIND_DECODE_TRACE=1), printed as one JSON line")
@@ -746,6 +815,9 @@ def main() -> int:
         return 0
     if args.decode_trace:
         print(json.dumps({"metric": METRIC, "decode_trace": decode_trace_report()}), flush=True)
+        return 0
+    if args.gemv_trace:
+        print(json.dumps({"metric": METRIC, "gemv_trace": gemv_trace_report(H, stream)}), flush=True)
         return 0
     if args.gemm_only:
         print(json.dumps({"metric": METRIC, "gemm": gemm_bench(H, stream)}), flush=True)

@@ -583,6 +583,11 @@ int vm_hip_decode_status(void* workspace, int* failed, void* stream);
  * profiling: only in a library built with VELOMIND_DECODE_TRACE=1, which
  * compiles them in; VM_HIP_EUNSUPPORTED otherwise. */
 int vm_hip_decode_trace_read(void* host, int64_t bytes);
+/* Phase timestamps of the last decode GEMV launch (u64, 100 MHz wall clock,
+ * laid out [4096 workgroups][8 events], workgroup y * gridDim.x + x; see
+ * qmm_gemv.hip), for profiling: only in a library built with
+ * VELOMIND_GEMV_TRACE=1; VM_HIP_EUNSUPPORTED otherwise. */
+int vm_hip_gemv_trace_read(void* host, int64_t bytes);
 
 /* ---- Prefill GEMM activations staged by their producer (no reference
  * counterpart; the resident decoder's prompts) ---------------------------

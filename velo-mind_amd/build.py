@@ -39,6 +39,9 @@ HIP_FLAGS = [
 # Phase timestamps in the one-launch decode step (profiling builds only).
 if os.environ.get("VELOMIND_DECODE_TRACE") == "1":
     HIP_FLAGS.append("-DVM_DECODE_TRACE")
+# Phase timestamps in the decode GEMV (profiling builds only).
+if os.environ.get("VELOMIND_GEMV_TRACE") == "1":
+    HIP_FLAGS.append("-DVM_GEMV_TRACE")
 CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-Wextra",
              f"-I{os.path.join(CORE, 'include')}", f"-I{os.path.join(CORE, 'src')}",
              f"-I{os.path.join(ROOT, 'include')}"]

@@ -26,8 +26,9 @@
 // Dequantization: INT8 codes are sign-extended bytes (v_cvt_f32_i32 with an
 // SDWA byte select).  An INT4 byte holds the even K row in its low nibble;
 // moving each nibble to the top of a byte ((w << 4) & 0xF0.. and w & 0xF0..)
-// makes the signed byte equal 16*code, so the same SDWA convert applies and
-// the factor 1/16 is folded (exactly) into the scale.
+// makes the signed byte equal 16*code, so the same SDWA convert applies; the
+// sums then carry a factor 16, taken out (exactly, a power of two) once per
+// output when the waves' sums are added, not once per chunk and column.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -46,6 +47,43 @@ constexpr int kChunkK = 8;    // logical K rows per chunk
 constexpr int kVec = 16;      // columns per lane
 constexpr int kMaxSplits = 32;
 constexpr int kStageBatch = 4;  // activation loads in flight per thread while staging
+
+// Phase timestamps, compiled in only with -DVM_GEMV_TRACE (build.py:
+// VELOMIND_GEMV_TRACE=1): thread 0 of each of the first kGemvTraceWgs
+// workgroups (linear id y * gridDim.x + x) keeps the 100 MHz wall clock at
+//   0 kernel entry          1 first weight load issued
+//   2 chunk and activations in (after the staging barrier)
+//   3 its wave's chunks reduced   4 the waves' sums in LDS (barrier)
+//   5 done: outputs or its pair words written and complete
+// in registers and stores them when it ends (each launch overwrites the
+// previous one's), read back with vm_hip_gemv_trace_read.  The traced
+// build waits for its stores before the last mark.
+constexpr int kGemvTraceWgs = 4096;
+constexpr int kGemvTraceEvents = 8;
+#ifdef VM_GEMV_TRACE
+__device__ unsigned long long g_gemv_trace[kGemvTraceWgs * kGemvTraceEvents];
+#define VM_GEMV_MARKS unsigned long long gemv_ts[kGemvTraceEvents] = {}
+#define VM_GEMV_MARK(ev) gemv_ts[ev] = wall_clock64()
+#define VM_GEMV_END()                                                                               \
+    do {                                                                                            \
+        __builtin_amdgcn_s_waitcnt(0);                                                              \
+        __syncthreads();                                                                            \
+        gemv_ts[5] = wall_clock64();                                                                \
+        const unsigned wg_ = blockIdx.y * gridDim.x + blockIdx.x;                                   \
+        if (threadIdx.x == 0 && wg_ < kGemvTraceWgs)                                                \
+            for (int e_ = 0; e_ < kGemvTraceEvents; ++e_) g_gemv_trace[wg_ * kGemvTraceEvents + e_] = gemv_ts[e_]; \
+    } while (0)
+#else
+#define VM_GEMV_MARKS \
+    do {              \
+    } while (0)
+#define VM_GEMV_MARK(ev) \
+    do {                 \
+    } while (0)
+#define VM_GEMV_END() \
+    do {              \
+    } while (0)
+#endif
 
 template <int KIND>
 struct ChunkShape {
@@ -114,6 +152,8 @@ template <int KIND, int MR, int L, int W, bool GROUPED>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const GemvMembers mb, int m, int k, int block_size, int chunks_per_split,
     uint32_t a_bytes, int a_vec, int blk_shift, unsigned long long* __restrict__ pairs) {
+    VM_GEMV_MARKS;
+    VM_GEMV_MARK(0);
     using CS = ChunkShape<KIND>;
     constexpr int G = 64 / L;            // row groups per wave
     constexpr int RG = W * G;            // row groups per workgroup
@@ -124,6 +164,16 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const int xs_len = chunks_per_split * kChunkK;
     float* red = smem + MR * xs_len;                      // [W][MR][kTileCols]
     float* spare = red + W * MR * kTileCols;              // [4], write-only
+
+    // Every argument on the path to the first weight load, requested in one
+    // batch of scalar loads: left to itself the compiler issues a second,
+    // dependent batch after the tile renumbering below, one more kernel-
+    // argument round trip (0.1-0.3 us when the weight stream has evicted the
+    // arguments from L2) before any weight is requested.
+    if constexpr (!GROUPED)
+        asm volatile("" ::"s"(mb.wq[0]), "s"(mb.scale[0]), "s"(mb.n[0]), "s"(mb.code_bytes[0]),
+                     "s"(mb.scale_bytes[0]), "s"(k), "s"(block_size), "s"(chunks_per_split), "s"(blk_shift),
+                     "s"(gridDim.x));
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -241,12 +291,11 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         }
 
         if constexpr (CS::kScaled) {
-            const float f = CS::kInt4 ? 0.0625f : 1.0f;  // INT4 accumulated 16*code
             float sv[kVec];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) sv[4 * q + e] = __uint_as_float(cur.s[q][e]) * f;
+                for (int e = 0; e < 4; ++e) sv[4 * q + e] = __uint_as_float(cur.s[q][e]);
 #pragma unroll
             for (int i = 0; i < MR; ++i)
 #pragma unroll
@@ -267,6 +316,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     // all lie inside one row; otherwise each covers one element.
     Chunk<KIND> ca, cb;
     int ch = c_begin + rg;
+    VM_GEMV_MARK(1);
     load_chunk(ch, ca);
 
     {
@@ -322,6 +372,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         }
     }
     __syncthreads();
+    VM_GEMV_MARK(2);
 
     float total[MR][kVec];
 #pragma unroll
@@ -341,6 +392,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         ch += 2 * RG;
     }
     if (iters & 1) compute_chunk(ca, ch, total);
+    VM_GEMV_MARK(3);
 
     // Row groups of a wave (lanes that agree in lane % L) are summed with
     // VALU cross-lane operations, then each wave leaves one copy of its
@@ -378,6 +430,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         }
     }
     __syncthreads();
+    VM_GEMV_MARK(4);
 
     const int tile_col0 = tile * kTileCols;
     if (splits == 1) {
@@ -389,10 +442,12 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
                 float v = 0.0f;
 #pragma unroll
                 for (int w = 0; w < W; ++w) v += red[(w * MR + i) * kTileCols + cc];
+                if constexpr (CS::kInt4) v *= 0.0625f;  // INT4 sums carry 16 * code
                 if constexpr (KIND == 0) v *= scale[col];
                 c[static_cast<int64_t>(i) * n + col] = v;
             }
         }
+        VM_GEMV_END();
         return;
     }
 
@@ -414,6 +469,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; ++w) v += red[(w * MR + i) * kTileCols + cc];
+        if constexpr (CS::kInt4) v *= 0.0625f;
         bool last = true;
         int64_t level_base = 0;
         for (int lvl = 0; (1 << lvl) < splits; ++lvl) {
@@ -443,6 +499,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         if constexpr (KIND == 0) v *= scale[col];
         c[static_cast<int64_t>(i) * n + col] = v;
     }
+    VM_GEMV_END();
 }
 
 // Pair words of every level of the split tree (level l has
@@ -739,3 +796,22 @@ int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* co
 }
 
 }  // namespace vmhip
+
+using namespace vmhip;
+
+extern "C" int vm_hip_gemv_trace_read(void* host, int64_t bytes) {
+    clear_error();
+#ifdef VM_GEMV_TRACE
+    if (!host || bytes < 0) return fail_inval("vm_hip_gemv_trace_read: bad argument");
+    const int64_t all = static_cast<int64_t>(sizeof(g_gemv_trace));
+    VM_TRY_HIP(hipDeviceSynchronize(), "gemv_trace: sync");
+    VM_TRY_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gemv_trace), static_cast<size_t>(std::min(bytes, all))),
+               "gemv_trace: copy");
+    return 0;
+#else
+    (void)host;
+    (void)bytes;
+    set_error("vm_hip_gemv_trace_read: libvmhip was built without VM_GEMV_TRACE (VELOMIND_GEMV_TRACE=1)");
+    return VM_HIP_EUNSUPPORTED;
+#endif
+}
