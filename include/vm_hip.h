@@ -142,6 +142,21 @@ int vm_hip_qmm_f32(const float* a, const int8_t* wq, const float* scale, float* 
                    void* stream);
 
 /*
+ * C = addend + A x W: a QuantizedMatMul followed by the residual Add that
+ * consumes it (the reference LLaMA layer's h + o_proj(ctx) and
+ * h + down(act), llama_graph.cpp:122, :139), with the Add's one fp32
+ * addition applied to each output after the product's last rounding, so C
+ * equals vm_hip_qmm_f32 then an elementwise Add bit for bit.  rows_m <= 4:
+ * one GEMV launch; otherwise the product and the addition as two launches.
+ * addend [rows_m, n] may not alias C's rows being written by another call.
+ * No counterpart in the reference (the graph compiler on DeviceType::HIP
+ * fuses such pairs).
+ */
+int vm_hip_qmm_add_f32(const float* a, const int8_t* wq, const float* scale, const float* addend,
+                       float* c, int64_t rows_m, int64_t k, int64_t n, int quant_type,
+                       int block_size, void* stream);
+
+/*
  * Sibling quantized matmuls sharing A: for every member g,
  * C_g[rows_m, n_g] = A[rows_m, k] x W_g (codes_g, scales_g), all with the
  * same quant_type and block_size.  No counterpart in the reference, whose
@@ -281,10 +296,15 @@ int vm_hip_repeat_kv_f32(const float* x, float* y, int64_t outer, int64_t kv_hea
                          int64_t repeats, int64_t inner, void* stream);
 
 /* Elementwise y = a + b, a * b or sigmoid(a) over n elements.  Replace
- * src/cpu/ops/add.cpp:16-26, mul.cpp:16-26 and sigmoid.cpp:17-27. */
-#define VM_HIP_EW_ADD     0
-#define VM_HIP_EW_MUL     1
-#define VM_HIP_EW_SIGMOID 2
+ * src/cpu/ops/add.cpp:16-26, mul.cpp:16-26 and sigmoid.cpp:17-27.
+ * VM_HIP_EW_SILU_MUL: y = (sigmoid(a) * a) * b, the reference LLaMA MLP's
+ * Mul(Mul(Sigmoid(gate), gate), up) (llama_graph.cpp:136) with the same
+ * roundings in the same order, in one pass (the graph compiler's fused
+ * step on DeviceType::HIP). */
+#define VM_HIP_EW_ADD      0
+#define VM_HIP_EW_MUL      1
+#define VM_HIP_EW_SIGMOID  2
+#define VM_HIP_EW_SILU_MUL 3
 int vm_hip_elementwise_f32(int op, const float* a, const float* b, float* y, int64_t n,
                            void* stream);
 
@@ -307,6 +327,19 @@ int vm_hip_matmul_f32(const float* a, const float* b, float* c, int64_t batch, i
 int vm_hip_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t batch,
                          int64_t hq, int64_t hk, int64_t sq, int64_t sk, int64_t d, int64_t dv,
                          float scale, int causal, void* stream);
+
+/* Decode attention of the reference LLaMA graph's unfused chain
+ * (llama_graph.cpp:95-107: RepeatKV on K and V, Transpose of K, MatMul,
+ * Softmax, MatMul) in one launch: q [hq, 1, d], k [hkv, s, d], v [hkv, s,
+ * dv] -> o [hq, 1, dv]; query head h reads kv head h / (hq / hkv).  Bit for
+ * bit the chain's result on this library's MatMul and Softmax kernels (the
+ * same fp32 operations in the same order), without the repeated K/V, the
+ * transposed K and the score rows.  No mask and no scale (the chain has
+ * none at one query row).  s + d <= 16384.  The graph compiler on
+ * DeviceType::HIP runs matching chains through it. */
+int vm_hip_attention_decode_chain_f32(const float* q, const float* k, const float* v, float* o,
+                                      int64_t hq, int64_t hkv, int64_t s, int64_t d, int64_t dv,
+                                      void* stream);
 
 /* ---- the resident decoder (velomind::examples::llama::HipLlamaDecoder) ---
  * Fused forms of reference graph nodes for a decoder that keeps its KV

@@ -87,8 +87,10 @@ TEST_CASE("block cache reuses a freed block only after a device synchronization"
     CHECK(dev.mallocs == 2);
     REQUIRE(cache.park(0, 4096, b));
     REQUIRE(cache.park(1, 8192, c));     // another device's blocks stay apart
-    CHECK(cache.allocate(0, 8192) != c);
+    void* d = cache.allocate(0, 8192);
+    CHECK(d != c);
     CHECK(cache.cached_bytes() == 4096 + 8192);
+    REQUIRE(cache.park(0, 8192, d));
     cache.release_device(0);
     cache.release_device(1);
     CHECK(cache.cached_bytes() == 0);

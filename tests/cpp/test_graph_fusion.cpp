@@ -1,0 +1,257 @@
+// The graph compiler's fused chains (graph_compiler.cpp fuse_steps), checked
+// on the CPU: host kernels for the chain's operators and host fused kernels
+// that keep the same arithmetic order are registered for DeviceType::CPU in
+// this binary, so the pass itself -- which chains it takes, what it leaves
+// unallocated, what it refuses -- is exercised without a GPU.  The HIP
+// fused kernels are checked against the unfused chains on the GPU
+// (tests/test_hip_graph_fusion.py).
+#include <cmath>
+#include <cstring>
+#include <variant>
+
+#include "internal/registry/kernel.h"
+#include "test_helpers.h"
+
+using namespace velomind;
+using namespace vmtest;
+
+namespace {
+
+const float* cin(const pConstTensorStorage* in, int i) { return static_cast<const float*>(in[i]->data); }
+float* cout0(const pTensorStorage* out) { return static_cast<float*>(out[0]->data); }
+std::size_t numel(const TensorStorage& t) { return storage_numel(t); }
+
+float sigmoid_host(float x) { return 1.0f / (1.0f + std::exp(-x)); }
+
+void add_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    for (std::size_t e = 0; e < numel(*out[0]); ++e) cout0(out)[e] = cin(in, 0)[e] + cin(in, 1)[e];
+}
+void mul_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    for (std::size_t e = 0; e < numel(*out[0]); ++e) cout0(out)[e] = cin(in, 0)[e] * cin(in, 1)[e];
+}
+void sigmoid_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    for (std::size_t e = 0; e < numel(*out[0]); ++e) cout0(out)[e] = sigmoid_host(cin(in, 0)[e]);
+}
+// [B, M, K] x [B, K, N], each output an fma chain over k from 0.
+void matmul_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    const auto& a = in[0]->shape;
+    const auto& c = out[0]->shape;
+    const std::size_t b = static_cast<std::size_t>(c[0]), m = static_cast<std::size_t>(a[1]),
+                      k = static_cast<std::size_t>(a[2]), n = static_cast<std::size_t>(c[2]);
+    for (std::size_t z = 0; z < b; ++z)
+        for (std::size_t i = 0; i < m; ++i)
+            for (std::size_t j = 0; j < n; ++j) {
+                float acc = 0.0f;
+                for (std::size_t t = 0; t < k; ++t)
+                    acc = std::fma(cin(in, 0)[(z * m + i) * k + t], cin(in, 1)[(z * k + t) * n + j], acc);
+                cout0(out)[(z * m + i) * n + j] = acc;
+            }
+}
+// last axis
+void softmax_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    const std::size_t cols = static_cast<std::size_t>(in[0]->shape.back());
+    const std::size_t rows = numel(*in[0]) / cols;
+    for (std::size_t r = 0; r < rows; ++r) {
+        const float* x = cin(in, 0) + r * cols;
+        float mx = -INFINITY, sum = 0.0f;
+        for (std::size_t j = 0; j < cols; ++j) mx = std::fmax(mx, x[j]);
+        for (std::size_t j = 0; j < cols; ++j) sum += std::exp(x[j] - mx);
+        for (std::size_t j = 0; j < cols; ++j) cout0(out)[r * cols + j] = std::exp(x[j] - mx) / sum;
+    }
+}
+// [A, B, C] -> [A, C, B] (the only permutation these tests use)
+void transpose_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    const auto& s = in[0]->shape;
+    for (dim_t a = 0; a < s[0]; ++a)
+        for (dim_t b = 0; b < s[1]; ++b)
+            for (dim_t c = 0; c < s[2]; ++c) cout0(out)[(a * s[2] + c) * s[1] + b] = cin(in, 0)[(a * s[1] + b) * s[2] + c];
+}
+// axis 0: head h of the output is head h / repeats of the input
+void repeat_kv_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const int r = std::get<RepeatKVAttrs>(static_cast<const OpDescriptor*>(attrs)->attrs).repeats;
+    const auto& s = in[0]->shape;
+    const std::size_t inner = static_cast<std::size_t>(s[1] * s[2]);
+    for (std::size_t h = 0; h < static_cast<std::size_t>(s[0]) * r; ++h)
+        std::memcpy(cout0(out) + h * inner, cin(in, 0) + (h / r) * inner, inner * 4);
+}
+
+// fused: the same operations in the same order as the chains above
+void silu_mul_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    for (std::size_t e = 0; e < numel(*out[0]); ++e) {
+        const float g = cin(in, 0)[e];
+        cout0(out)[e] = (sigmoid_host(g) * g) * cin(in, 1)[e];
+    }
+}
+void qmm_add_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const auto& qa = std::get<QuantizedMatMulAttrs>(static_cast<const OpDescriptor*>(attrs)->attrs);
+    const std::size_t k = static_cast<std::size_t>(in[0]->shape.back()), n = static_cast<std::size_t>(in[1]->shape[1]);
+    const std::size_t rows = numel(*out[0]) / n;
+    vmo_qmm_2d_f32(cin(in, 0), static_cast<const std::int8_t*>(in[1]->data), cin(in, 2), cout0(out), rows, k, n,
+                   static_cast<int>(qa.quant_type), qa.block_size);
+    for (std::size_t e = 0; e < rows * n; ++e) cout0(out)[e] = cin(in, 3)[e] + cout0(out)[e];
+}
+void attention_decode_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    const auto& q = in[0]->shape;
+    const auto& k = in[1]->shape;
+    const std::size_t H = q[0], D = q[2], Hkv = k[0], S = k[1], Dv = in[2]->shape[2];
+    std::vector<float> p(S);
+    for (std::size_t h = 0; h < H; ++h) {
+        const std::size_t kv = h / (H / Hkv);
+        float mx = -INFINITY, sum = 0.0f;
+        for (std::size_t s = 0; s < S; ++s) {
+            float acc = 0.0f;
+            for (std::size_t t = 0; t < D; ++t) acc = std::fma(cin(in, 0)[h * D + t], cin(in, 1)[(kv * S + s) * D + t], acc);
+            p[s] = acc;
+        }
+        for (std::size_t s = 0; s < S; ++s) mx = std::fmax(mx, p[s]);
+        for (std::size_t s = 0; s < S; ++s) sum += std::exp(p[s] - mx);
+        for (std::size_t s = 0; s < S; ++s) p[s] = std::exp(p[s] - mx) / sum;
+        for (std::size_t t = 0; t < Dv; ++t) {
+            float acc = 0.0f;
+            for (std::size_t s = 0; s < S; ++s) acc = std::fma(p[s], cin(in, 2)[(kv * S + s) * Dv + t], acc);
+            cout0(out)[h * Dv + t] = acc;
+        }
+    }
+}
+
+constexpr DataType F32 = DataType::Float32;
+#define CPU_F32(OP, N, FN) \
+    VELOMIND_REGISTER_OP_KERNEL(DeviceType::CPU, OP, (internal::KernelDtypeKey{{F32, F32, F32, F32}, N, F32}), &FN)
+CPU_F32(Op::Add, 2, add_cpu)
+CPU_F32(Op::Mul, 2, mul_cpu)
+CPU_F32(Op::Sigmoid, 1, sigmoid_cpu)
+CPU_F32(Op::MatMul, 2, matmul_cpu)
+CPU_F32(Op::Softmax, 1, softmax_cpu)
+CPU_F32(Op::Transpose, 1, transpose_cpu)
+CPU_F32(Op::RepeatKV, 1, repeat_kv_cpu)
+VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::SiluMul, &silu_mul_fused_cpu)
+VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::QmmAdd, &qmm_add_fused_cpu)
+VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::AttentionDecode, &attention_decode_fused_cpu)
+
+struct QmmWeights {
+    std::vector<std::int8_t> q;
+    std::vector<float> s;
+};
+QmmWeights int8_weights(std::size_t k, std::size_t n, unsigned seed) {
+    const auto w = normal(k * n, seed, 0.05f);
+    QmmWeights r{std::vector<std::int8_t>(k * n), std::vector<float>(n)};
+    vmo_quantize_int8_per_channel(w.data(), r.q.data(), r.s.data(), k, n);
+    return r;
+}
+
+// An MLP block with its residual: out = h + down(silu(gate(x)) * up(x)).
+struct MlpRun {
+    std::vector<float> out;
+    std::size_t steps = 0, nodes = 0;
+    bool inner_unallocated = false;
+};
+MlpRun run_mlp(bool fuse, bool keep_sigmoid) {
+    const std::size_t d = 64, f = 96;
+    static const auto wg = int8_weights(d, f, 61), wu = int8_weights(d, f, 62), wd = int8_weights(f, d, 63);
+    static const auto x = normal(d, 64), h = normal(d, 65);
+    ScopedEnv env("VELOMIND_GRAPH_FUSE", fuse ? "1" : "0");
+    Graph g;
+    auto tx = g.input({1, (dim_t)d}, F32), th = g.input({1, (dim_t)d}, F32);
+    auto tg = g.input({(dim_t)d, (dim_t)f}, DataType::Int8), tgs = g.input({(dim_t)f}, F32);
+    auto tu = g.input({(dim_t)d, (dim_t)f}, DataType::Int8), tus = g.input({(dim_t)f}, F32);
+    auto td = g.input({(dim_t)f, (dim_t)d}, DataType::Int8), tds = g.input({(dim_t)d}, F32);
+    auto gate = g.op(Op::QuantizedMatMul, tx, tg, tgs);
+    auto up = g.op(Op::QuantizedMatMul, tx, tu, tus);
+    auto sg = g.op(Op::Sigmoid, gate);
+    auto t = g.op(Op::Mul, sg, gate);
+    auto act = g.op(Op::Mul, t, up);
+    auto y = g.op(Op::QuantizedMatMul, act, td, tds);
+    auto out = g.op(Op::Add, th, y);
+    g.mark_output(out);
+    if (keep_sigmoid) g.mark_output(sg);
+    auto exec = g.build(DeviceType::CPU);
+    MlpRun r;
+    r.steps = exec->num_steps();
+    r.nodes = exec->num_nodes();
+    r.inner_unallocated = g.tensor_storage_at(t.index())->data == nullptr && g.tensor_storage_at(y.index())->data == nullptr;
+    tx.copy_from_host(as_bytes(x));
+    th.copy_from_host(as_bytes(h));
+    tg.copy_from_host(as_bytes(wg.q));
+    tgs.copy_from_host(as_bytes(wg.s));
+    tu.copy_from_host(as_bytes(wu.q));
+    tus.copy_from_host(as_bytes(wu.s));
+    td.copy_from_host(as_bytes(wd.q));
+    tds.copy_from_host(as_bytes(wd.s));
+    exec->execute();
+    r.out.resize(d);
+    out.copy_to_host(as_writeable_bytes(r.out));
+    return r;
+}
+
+// Decode attention of the reference layer at one query row.
+struct AttnRun {
+    std::vector<float> ctx;
+    std::size_t steps = 0;
+};
+AttnRun run_attention(bool fuse, bool keep_scores, std::size_t hq, std::size_t hkv) {
+    const std::size_t s = 37, dh = 16;
+    const auto q = normal(hq * dh, 71), k = normal(hkv * s * dh, 72), v = normal(hkv * s * dh, 73);
+    ScopedEnv env("VELOMIND_GRAPH_FUSE", fuse ? "1" : "0");
+    Graph g;
+    auto tq = g.input({(dim_t)hq, 1, (dim_t)dh}, F32);
+    auto tk = g.input({(dim_t)hkv, (dim_t)s, (dim_t)dh}, F32);
+    auto tv = g.input({(dim_t)hkv, (dim_t)s, (dim_t)dh}, F32);
+    Tensor ka = tk, va = tv;
+    if (hq != hkv) {
+        const int rep = static_cast<int>(hq / hkv);
+        ka = g.op(OpDescriptor{Op::RepeatKV, RepeatKVAttrs{rep, 0}}, tk);
+        va = g.op(OpDescriptor{Op::RepeatKV, RepeatKVAttrs{rep, 0}}, tv);
+    }
+    auto kt = g.op(OpDescriptor{Op::Transpose, TransposeAttrs{{0, 2, 1}}}, ka);
+    auto scores = g.op(Op::MatMul, tq, kt);
+    auto ctx = g.op(Op::MatMul, g.op(Op::Softmax, scores), va);
+    g.mark_output(ctx);
+    if (keep_scores) g.mark_output(scores);
+    auto exec = g.build(DeviceType::CPU);
+    AttnRun r;
+    r.steps = exec->num_steps();
+    tq.copy_from_host(as_bytes(q));
+    tk.copy_from_host(as_bytes(k));
+    tv.copy_from_host(as_bytes(v));
+    exec->execute();
+    r.ctx.resize(hq * dh);
+    ctx.copy_to_host(as_writeable_bytes(r.ctx));
+    return r;
+}
+
+}  // namespace
+
+TEST_CASE("fusion: SwiGLU chain and QuantizedMatMul + residual Add run as single steps", "[core][fusion]") {
+    const auto off = run_mlp(false, false);
+    const auto on = run_mlp(true, false);
+    REQUIRE(off.nodes == 7);
+    REQUIRE(off.steps == 7);
+    // gate, up, SiluMul (3 nodes), QmmAdd (2 nodes)
+    REQUIRE(on.nodes == 7);
+    REQUIRE(on.steps == 4);
+    REQUIRE(on.inner_unallocated);
+    REQUIRE(!off.inner_unallocated);
+    REQUIRE(std::memcmp(on.out.data(), off.out.data(), on.out.size() * 4) == 0);
+}
+
+TEST_CASE("fusion: a kept inner tensor keeps its chain unfused", "[core][fusion]") {
+    // the Sigmoid's output is requested: SiluMul is not formed, QmmAdd still is
+    const auto on = run_mlp(true, true);
+    const auto off = run_mlp(false, true);
+    REQUIRE(on.steps == 6);
+    REQUIRE(std::memcmp(on.out.data(), off.out.data(), on.out.size() * 4) == 0);
+}
+
+TEST_CASE("fusion: decode attention chain runs as one step, with and without RepeatKV", "[core][fusion]") {
+    for (auto [hq, hkv] : {std::pair<std::size_t, std::size_t>{6, 2}, {4, 4}}) {
+        const auto off = run_attention(false, false, hq, hkv);
+        const auto on = run_attention(true, false, hq, hkv);
+        REQUIRE(off.steps == (hq != hkv ? 6u : 4u));
+        REQUIRE(on.steps == 1);
+        REQUIRE(std::memcmp(on.ctx.data(), off.ctx.data(), on.ctx.size() * 4) == 0);
+        // scores requested: the chain is kept
+        const auto kept = run_attention(true, true, hq, hkv);
+        REQUIRE(kept.steps == off.steps);
+        REQUIRE(std::memcmp(kept.ctx.data(), off.ctx.data(), off.ctx.size() * 4) == 0);
+    }
+}

@@ -18,6 +18,7 @@
 // examples/tinyllama/model_loader.cpp:65-202).
 #pragma once
 
+#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <memory>
@@ -81,6 +82,11 @@ public:
     // One token at position `pos` (== tokens processed so far).
     auto forward_step(std::int32_t token, std::size_t pos) -> std::vector<float>;
     auto seq_len() const noexcept -> std::size_t { return _seq_len; }
+    // Host seconds spent by the decode steps since the last prefill, summed:
+    // [0] building each step's Graph (nodes, shapes, bound weights), [1]
+    // Graph::build on HIP, [2] Executable::execute (launches and the final
+    // drain), [3] reading the logits back; [4] the number of steps.
+    auto step_timing() const noexcept -> const std::array<double, 5>& { return _timing; }
 
 private:
     void bind(Graph& g, ForwardWeights& w) const;
@@ -92,6 +98,7 @@ private:
     std::vector<std::shared_ptr<TensorStorage>> _lin, _scale;  // [7 * layers + 1]
     std::vector<std::shared_ptr<TensorStorage>> _k, _v;        // per layer, [Hkv, S, D]
     std::size_t _seq_len = 0;
+    std::array<double, 5> _timing{};
 };
 
 class PackedLlamaWeights;

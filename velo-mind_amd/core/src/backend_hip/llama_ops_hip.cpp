@@ -177,6 +177,28 @@ void fused_attention_hip(const pConstTensorStorage* in, const pTensorStorage* ou
                                 current_stream()));
 }
 
+// ---- fused steps (kernel.h FusedKind; the graph compiler checks shapes
+// and dtypes before it forms one)
+
+// Mul(Mul(Sigmoid(g), g), u): inputs [g, u].
+void silu_mul_fused_hip(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    require_contiguous(Op::Mul, in, 2, *out[0]);
+    finish(Op::Mul, *out[0],
+           vm_hip_elementwise_f32(VM_HIP_EW_SILU_MUL, fin(in, 0), fin(in, 1), fout(out),
+                                  static_cast<std::int64_t>(storage_numel(*out[0])), current_stream()));
+}
+
+// RepeatKV / Transpose / MatMul / Softmax / MatMul at one query row:
+// inputs [q [H, 1, D], K [Hkv, S, D], V [Hkv, S, Dv]], outputs [ctx [H, 1, Dv]].
+void attention_decode_fused_hip(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    require_contiguous(Op::MatMul, in, 3, *out[0]);
+    const auto& q = in[0]->shape;
+    const auto& k = in[1]->shape;
+    finish(Op::MatMul, *out[0],
+           vm_hip_attention_decode_chain_f32(fin(in, 0), fin(in, 1), fin(in, 2), fout(out), q[0], k[0], k[1], q[2],
+                                             in[2]->shape[2], current_stream()));
+}
+
 }  // namespace
 
 #define VM_HIP_F32_KERNEL(OP, N_IN, FN)                                                                  \
@@ -198,5 +220,11 @@ VM_HIP_F32_KERNEL(Op::Sigmoid, 1, (elementwise_hip<VM_HIP_EW_SIGMOID, Op::Sigmoi
 VM_HIP_F32_KERNEL(Op::Softmax, 1, softmax_hip)
 VM_HIP_F32_KERNEL(Op::MatMul, 2, matmul_hip)
 VM_HIP_F32_KERNEL(Op::FusedAttention, 3, fused_attention_hip)
+
+VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, internal::FusedKind::SiluMul, &silu_mul_fused_hip)
+VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, internal::FusedKind::AttentionDecode, &attention_decode_fused_hip)
+// vm_hip_attention_f32 maps query head h to kv head h / (hq / hk) itself,
+// so FusedAttention reads K/V as they were before RepeatKV.
+VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, internal::FusedKind::AttentionGqa, &fused_attention_hip)
 
 }  // namespace velomind::backend::hip

@@ -19,11 +19,10 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <span>
 #include <cstdlib>
 #include <stdexcept>
 #include <string>
-#include <unordered_map>
-#include <unordered_set>
 #include <vector>
 
 #include "internal/registry/device_context.h"
@@ -109,17 +108,65 @@ std::size_t injected_failure_point() {
     return (end && *end == '\0') ? static_cast<std::size_t>(n) : 0;
 }
 
+// Tensor storage -> index into Graph::_tensors: a flat open-addressing
+// table over the graph's storages (a decode graph holds ~1600; hashing them
+// into a node-based map took a third of the build).
+class TensorIndex {
+public:
+    static constexpr std::size_t npos = SIZE_MAX;
+    explicit TensorIndex(const std::vector<std::shared_ptr<TensorStorage>>& tensors) {
+        while (_cap < 2 * tensors.size()) _cap <<= 1;
+        _keys.assign(_cap, nullptr);
+        _vals.assign(_cap, 0);
+        for (std::size_t i = 0; i < tensors.size(); ++i) {
+            std::size_t h = slot(tensors[i].get());
+            while (_keys[h] && _keys[h] != tensors[i].get()) h = (h + 1) & (_cap - 1);
+            _keys[h] = tensors[i].get();
+            _vals[h] = i;
+        }
+    }
+    std::size_t find(pConstTensorStorage t) const {
+        for (std::size_t h = slot(t);; h = (h + 1) & (_cap - 1)) {
+            if (_keys[h] == t) return _vals[h];
+            if (!_keys[h]) return npos;
+        }
+    }
+    std::size_t at(pConstTensorStorage t) const {
+        const std::size_t i = find(t);
+        if (i == npos) throw std::out_of_range("velomind: node operand is not a tensor of its graph");
+        return i;
+    }
+
+private:
+    std::size_t slot(pConstTensorStorage t) const {
+        auto x = static_cast<std::uint64_t>(reinterpret_cast<std::uintptr_t>(t));
+        x ^= x >> 29;
+        x *= 0x9E3779B97F4A7C15ull;
+        return static_cast<std::size_t>(x >> 32) & (_cap - 1);
+    }
+    std::size_t _cap = 16;
+    std::vector<pConstTensorStorage> _keys;
+    std::vector<std::size_t> _vals;
+};
+
 // ---- steps -----------------------------------------------------------------
-// A compiled step runs one node, or (where the device registers a group
+// A compiled step runs one node; or (where the device registers a group
 // kernel) up to kMaxQmmGroup sibling QuantizedMatMul nodes that read the
 // same fp32 A with the same quantisation and have at most four rows of A:
 // decode projections such as q | k | v and gate | up then stream their
-// weights in one launch.  A sibling is pulled forward to the first
-// member's place only when every tensor it reads is already available
-// there; memory lifetimes are planned on the steps, so tensors the group
-// writes early never share arena space with anything still live.
-// VELOMIND_GROUP_QMM=0 keeps every node on its own.
-using Step = std::vector<pConstNode>;
+// weights in one launch; or (where the device registers the kernel) a
+// fused chain of nodes (kernel.h FusedKind, matched by fuse_steps below).
+// A sibling is pulled forward to the first member's place only when every
+// tensor it reads is already available there; memory lifetimes are planned
+// on the steps, so tensors the group writes early never share arena space
+// with anything still live.  VELOMIND_GROUP_QMM=0 keeps every node on its own.
+struct Step {
+    std::vector<pConstNode> nodes;            // graph nodes the step runs
+    int fused = -1;                           // FusedKind, or -1
+    std::vector<pConstTensorStorage> ins;     // fused: the chain's external operands
+    std::vector<pConstTensorStorage> outs;
+    const OpDescriptor* desc = nullptr;       // fused: descriptor the kernel takes, if any
+};
 
 const QuantizedMatMulAttrs* qmm_attrs(pConstNode n) {
     if (n->op().op != Op::QuantizedMatMul) return nullptr;
@@ -148,45 +195,216 @@ bool qmm_siblings(pConstNode a, pConstNode b) {
     return qa->quant_type == qb->quant_type && qa->block_size == qb->block_size;
 }
 
-std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType device) {
+std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType device, const TensorIndex& index,
+                             std::size_t tensor_count) {
     const char* env = std::getenv("VELOMIND_GROUP_QMM");
     const bool group = qmm_group_kernel(device) != nullptr && !(env && env[0] == '0');
-    std::unordered_map<pConstTensorStorage, std::size_t> producer;
-    for (std::size_t i = 0; i < order.size(); ++i)
-        for (auto* out : order[i]->outputs()) producer.emplace(out, i);
-    // groupable nodes by the A they read, in order (siblings share A)
-    std::unordered_map<pConstTensorStorage, std::vector<std::size_t>> by_a;
-    if (group)
-        for (std::size_t i = 0; i < order.size(); ++i)
-            if (qmm_groupable(order[i])) by_a[order[i]->inputs()[0]].push_back(i);
-    std::vector<bool> done(order.size(), false), taken(order.size(), false);
     std::vector<Step> steps;
+    steps.reserve(order.size());
+    if (!group) {
+        for (auto* n : order) steps.push_back(Step{{n}});
+        return steps;
+    }
+    std::vector<std::size_t> producer(tensor_count, SIZE_MAX);
+    for (std::size_t i = 0; i < order.size(); ++i)
+        for (auto* out : order[i]->outputs()) {
+            auto& p = producer[index.at(out)];
+            if (p == SIZE_MAX) p = i;
+        }
+    // groupable nodes by the A they read, in order (siblings share A)
+    std::vector<std::vector<std::size_t>> by_a(tensor_count);
+    for (std::size_t i = 0; i < order.size(); ++i)
+        if (qmm_groupable(order[i])) by_a[index.at(order[i]->inputs()[0])].push_back(i);
+    std::vector<bool> done(order.size(), false), taken(order.size(), false);
     for (std::size_t i = 0; i < order.size(); ++i) {
         if (taken[i]) continue;
-        std::vector<std::size_t> members{i};
+        Step step;
+        step.nodes.push_back(order[i]);
         taken[i] = true;
-        if (group && qmm_groupable(order[i])) {
-            for (const std::size_t j : by_a.at(order[i]->inputs()[0])) {
-                if (members.size() >= kMaxQmmGroup) break;
+        done[i] = true;
+        if (qmm_groupable(order[i])) {
+            for (const std::size_t j : by_a[index.at(order[i]->inputs()[0])]) {
+                if (step.nodes.size() >= kMaxQmmGroup) break;
                 if (j <= i || taken[j] || !qmm_siblings(order[i], order[j])) continue;
                 bool ready = true;
                 for (auto* in : order[j]->inputs()) {
-                    const auto it = producer.find(in);
-                    if (it != producer.end() && !done[it->second]) ready = false;
+                    const auto p = producer[index.at(in)];
+                    if (p != SIZE_MAX && !done[p]) ready = false;
                 }
                 if (!ready) continue;
-                members.push_back(j);
+                step.nodes.push_back(order[j]);
                 taken[j] = true;
+                done[j] = true;
             }
-        }
-        Step step;
-        for (std::size_t m : members) {
-            step.push_back(order[m]);
-            done[m] = true;
         }
         steps.push_back(std::move(step));
     }
     return steps;
+}
+
+// ---- fused chains -------------------------------------------------------------
+// Chains of single-node steps that the device runs as one launch
+// (kernel.h FusedKind).  A chain's inner tensors must have exactly one
+// consumer and must not be kept (requested outputs, graph inputs, tensors
+// that own data): they are then never allocated.  The fused step takes the
+// place of the chain's last node, where every operand it reads exists.
+//   SiluMul          y = Mul(Mul(Sigmoid(g), g), u)      (either operand order)
+//   QmmAdd           C = Add(h, QuantizedMatMul(A, ..))  (at most 4 rows of A, fp32, either order)
+//   AttentionDecode  ctx = MatMul(Softmax(MatMul(q, Transpose(RepeatKV(K)))), RepeatKV(V))
+//                    with q [H, 1, D], K [Hkv, S, D], V [Hkv, S, Dv], the
+//                    Transpose swapping the last two axes, the Softmax on the
+//                    last one (RepeatKV absent when H == Hkv)
+//   AttentionGqa     o = FusedAttention(q, RepeatKV(K), RepeatKV(V))
+// VELOMIND_GRAPH_FUSE=0 keeps every chain as separate launches.
+void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& index,
+                const std::vector<bool>& kept) {
+    const char* env = std::getenv("VELOMIND_GRAPH_FUSE");
+    if (env && env[0] == '0') return;
+    Executable::KernelFn kernels[kFusedKinds];
+    bool any = false;
+    for (std::size_t k = 0; k < kFusedKinds; ++k) {
+        kernels[k] = fused_kernel(device, static_cast<FusedKind>(k));
+        any = any || kernels[k];
+    }
+    if (!any) return;
+    const std::size_t nt = kept.size();
+    std::vector<std::uint32_t> consumers(nt, 0);
+    std::vector<std::size_t> producer(nt, SIZE_MAX);   // single-node step producing the tensor
+    for (std::size_t s = 0; s < steps.size(); ++s)
+        for (auto* n : steps[s].nodes) {
+            for (auto* in : n->inputs()) ++consumers[index.at(in)];
+            if (steps[s].nodes.size() == 1)
+                for (auto* out : n->outputs()) producer[index.at(out)] = s;
+        }
+    std::vector<bool> dead(steps.size(), false);
+    // the step producing t when it is a live, unfused single node of op `op` with one output
+    auto single = [&](pConstTensorStorage t, Op op) -> std::size_t {
+        const std::size_t s = producer[index.at(t)];
+        if (s == SIZE_MAX || dead[s] || steps[s].fused >= 0) return SIZE_MAX;
+        const auto* n = steps[s].nodes.front();
+        return (n->op().op == op && n->outputs().size() == 1) ? s : SIZE_MAX;
+    };
+    auto inner = [&](pConstTensorStorage t) {
+        const std::size_t i = index.at(t);
+        return consumers[i] == 1 && !kept[i];
+    };
+    auto f32 = [](pConstTensorStorage t) { return t->dtype == DataType::Float32; };
+    auto node_of = [&](std::size_t s) { return steps[s].nodes.front(); };
+    auto is_kv_repeat = [&](std::size_t s) {
+        if (s == SIZE_MAX) return false;
+        const auto* a = std::get_if<RepeatKVAttrs>(&node_of(s)->op().attrs);
+        return a && (a->axis == 0 || a->axis == -3) && node_of(s)->inputs()[0]->shape.size() == 3;
+    };
+    // K or V as the chain reads it: before its RepeatKV when that is inner
+    auto unrepeat = [&](pConstTensorStorage t, std::vector<std::size_t>& absorbed) -> pConstTensorStorage {
+        const std::size_t s = single(t, Op::RepeatKV);
+        if (!is_kv_repeat(s) || !inner(t)) return t;
+        absorbed.push_back(s);
+        return node_of(s)->inputs()[0];
+    };
+    auto make = [&](std::size_t at, FusedKind kind, std::vector<std::size_t> absorbed,
+                    std::vector<pConstTensorStorage> ins, const OpDescriptor* desc) {
+        Step f;
+        std::sort(absorbed.begin(), absorbed.end());
+        for (std::size_t s : absorbed) {
+            f.nodes.push_back(node_of(s));
+            dead[s] = true;
+        }
+        f.nodes.push_back(node_of(at));
+        f.fused = static_cast<int>(kind);
+        f.ins = std::move(ins);
+        f.outs = {node_of(at)->outputs()[0]};
+        f.desc = desc;
+        steps[at] = std::move(f);
+    };
+
+    for (std::size_t j = 0; j < steps.size(); ++j) {
+        if (dead[j] || steps[j].fused >= 0 || steps[j].nodes.size() != 1) continue;
+        const auto* n = node_of(j);
+        const auto ins = n->inputs();
+        if (n->outputs().size() != 1) continue;
+        const auto* out = n->outputs()[0];
+        const Op op = n->op().op;
+
+        if (op == Op::Mul && kernels[static_cast<int>(FusedKind::SiluMul)] && ins.size() == 2) {
+            bool done = false;
+            for (int ti = 0; ti < 2 && !done; ++ti) {
+                const auto* t = ins[ti];
+                const auto* u = ins[1 - ti];
+                const std::size_t st = single(t, Op::Mul);
+                if (st == SIZE_MAX || !inner(t)) continue;
+                const auto m1 = node_of(st)->inputs();
+                for (int si = 0; si < 2 && !done; ++si) {
+                    const auto* sg = m1[si];
+                    const auto* g = m1[1 - si];
+                    const std::size_t ss = single(sg, Op::Sigmoid);
+                    if (ss == SIZE_MAX || !inner(sg) || node_of(ss)->inputs()[0] != g) continue;
+                    if (!(f32(g) && f32(u) && f32(out) && f32(t) && f32(sg)) || g->shape != u->shape ||
+                        g->shape != out->shape || g->shape != t->shape || g->shape != sg->shape)
+                        continue;
+                    make(j, FusedKind::SiluMul, {ss, st}, {g, u}, nullptr);
+                    done = true;
+                }
+            }
+            continue;
+        }
+        if (op == Op::Add && kernels[static_cast<int>(FusedKind::QmmAdd)] && ins.size() == 2) {
+            for (int yi = 1; yi >= 0; --yi) {
+                const auto* y = ins[yi];
+                const auto* h = ins[1 - yi];
+                const std::size_t sq = single(y, Op::QuantizedMatMul);
+                if (sq == SIZE_MAX || !inner(y) || !qmm_groupable(node_of(sq))) continue;
+                if (!f32(h) || !f32(out) || h->shape != y->shape || out->shape != y->shape) continue;
+                const auto q = node_of(sq)->inputs();
+                make(j, FusedKind::QmmAdd, {sq}, {q[0], q[1], q[2], h}, &node_of(sq)->op());
+                break;
+            }
+            continue;
+        }
+        if (op == Op::MatMul && kernels[static_cast<int>(FusedKind::AttentionDecode)] && ins.size() == 2) {
+            const std::size_t sp = single(ins[0], Op::Softmax);
+            if (sp == SIZE_MAX || !inner(ins[0])) continue;
+            const auto* scores = node_of(sp)->inputs()[0];
+            const auto* sa = std::get_if<SoftmaxAttrs>(&node_of(sp)->op().attrs);
+            if (!sa || !(sa->axis == -1 || sa->axis == 2)) continue;
+            const std::size_t sm = single(scores, Op::MatMul);
+            if (sm == SIZE_MAX || !inner(scores)) continue;
+            const auto* q = node_of(sm)->inputs()[0];
+            const auto* kt = node_of(sm)->inputs()[1];
+            const std::size_t st = single(kt, Op::Transpose);
+            if (st == SIZE_MAX || !inner(kt)) continue;
+            const auto* ta = std::get_if<TransposeAttrs>(&node_of(st)->op().attrs);
+            if (!ta || ta->perm != std::vector<int>{0, 2, 1}) continue;
+            std::vector<std::size_t> absorbed{sp, sm, st};
+            const auto* k = unrepeat(node_of(st)->inputs()[0], absorbed);
+            const auto* v = unrepeat(ins[1], absorbed);
+            if (q->shape.size() != 3 || k->shape.size() != 3 || v->shape.size() != 3 || out->shape.size() != 3) continue;
+            const dim_t H = q->shape[0], D = q->shape[2], Hkv = k->shape[0], S = k->shape[1], Dv = v->shape[2];
+            // K and V both before their RepeatKV (Hkv heads) or both without one (H heads)
+            const bool shapes = q->shape[1] == 1 && k->shape[2] == D && v->shape[0] == Hkv && v->shape[1] == S &&
+                                Hkv > 0 && H % Hkv == 0 && S > 0 && S + D <= 16384 &&
+                                out->shape == shape_t{H, 1, Dv};
+            if (!shapes) continue;
+            if (!(f32(q) && f32(k) && f32(v) && f32(out))) continue;
+            make(j, FusedKind::AttentionDecode, absorbed, {q, k, v}, nullptr);
+            continue;
+        }
+        if (op == Op::FusedAttention && kernels[static_cast<int>(FusedKind::AttentionGqa)] && ins.size() == 3) {
+            std::vector<std::size_t> absorbed;
+            const auto* k = unrepeat(ins[1], absorbed);
+            const auto* v = unrepeat(ins[2], absorbed);
+            if (absorbed.size() != 2 || k->shape[0] != v->shape[0]) continue;
+            make(j, FusedKind::AttentionGqa, absorbed, {ins[0], k, v}, &n->op());
+            continue;
+        }
+    }
+    std::size_t w = 0;
+    for (std::size_t s = 0; s < steps.size(); ++s) {
+        if (dead[s]) continue;
+        if (w != s) steps[w] = std::move(steps[s]);
+        ++w;
+    }
+    steps.resize(w);
 }
 
 // ---- byte-preserving nodes --------------------------------------------------
@@ -234,38 +452,16 @@ std::shared_ptr<TensorStorage> allocate_checked(std::size_t bytes, DeviceType de
 auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<Executable> {
     if (graph._built) throw std::logic_error("Graph::build: graph is already built");
     const auto order = graph._validated_order(device);
-    const auto steps = plan_steps(order, device);
     const auto& tensors = graph._tensors;
+    const TensorIndex index(tensors);
 
-    std::unordered_map<pConstTensorStorage, std::size_t> index_of;
-    for (std::size_t i = 0; i < tensors.size(); ++i) index_of[tensors[i].get()] = i;
-
-    // Activity and lifetimes.
+    // Dedicated allocations: requested outputs (every tensor when none were
+    // marked), graph inputs and tensors that already own data.
     std::vector<bool> active(tensors.size(), false);
-    std::vector<std::size_t> birth(tensors.size(), 0), death(tensors.size(), 0);
-    std::vector<bool> born(tensors.size(), false);
-    for (std::size_t step = 0; step < steps.size(); ++step) {
-        for (const auto* node : steps[step]) {
-            for (auto* in : node->inputs()) {
-                const auto i = index_of.at(in);
-                active[i] = true;
-                death[i] = std::max(death[i], step);
-            }
-            for (auto* out : node->outputs()) {
-                const auto i = index_of.at(out);
-                active[i] = true;
-                if (!born[i]) {
-                    born[i] = true;
-                    birth[i] = step;
-                }
-                death[i] = std::max(death[i], step);
-            }
-        }
-    }
     std::vector<bool> dedicated(tensors.size(), false);
     if (graph._has_explicit_outputs) {
         for (auto* s : graph._explicit_outputs) {
-            const auto i = index_of.at(s);
+            const auto i = index.at(s);
             active[i] = true;
             dedicated[i] = true;
         }
@@ -278,6 +474,40 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     for (std::size_t i = 0; i < tensors.size(); ++i)
         if (tensors[i]->data != nullptr || graph.is_input_tensor(i)) dedicated[i] = true;
 
+    auto steps = plan_steps(order, device, index, tensors.size());
+    fuse_steps(steps, device, index, dedicated);
+
+    // Activity and lifetimes (a fused step touches its chain's external
+    // operands only).
+    std::vector<std::size_t> birth(tensors.size(), 0), death(tensors.size(), 0);
+    std::vector<bool> born(tensors.size(), false);
+    auto read = [&](pConstTensorStorage t, std::size_t step) {
+        const auto i = index.at(t);
+        active[i] = true;
+        death[i] = std::max(death[i], step);
+    };
+    auto write = [&](pConstTensorStorage t, std::size_t step) {
+        const auto i = index.at(t);
+        active[i] = true;
+        if (!born[i]) {
+            born[i] = true;
+            birth[i] = step;
+        }
+        death[i] = std::max(death[i], step);
+    };
+    for (std::size_t step = 0; step < steps.size(); ++step) {
+        const Step& st = steps[step];
+        if (st.fused >= 0) {
+            for (auto* in : st.ins) read(in, step);
+            for (auto* out : st.outs) write(out, step);
+            continue;
+        }
+        for (const auto* node : st.nodes) {
+            for (auto* in : node->inputs()) read(in, step);
+            for (auto* out : node->outputs()) write(out, step);
+        }
+    }
+
     // Byte-preserving steps between arena intermediates: the output views
     // its root's bytes, whose lifetime covers the output's.
     std::vector<std::size_t> root(tensors.size());
@@ -287,9 +517,10 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         const char* env = std::getenv("VELOMIND_GRAPH_ALIAS");
         if (!(env && env[0] == '0')) {
             for (std::size_t step = 0; step < steps.size(); ++step) {
-                if (steps[step].size() != 1 || !keeps_bytes(steps[step].front())) continue;
-                const auto in = root[index_of.at(steps[step].front()->inputs()[0])];
-                const auto out = index_of.at(steps[step].front()->outputs()[0]);
+                if (steps[step].fused >= 0 || steps[step].nodes.size() != 1 || !keeps_bytes(steps[step].nodes.front()))
+                    continue;
+                const auto in = root[index.at(steps[step].nodes.front()->inputs()[0])];
+                const auto out = index.at(steps[step].nodes.front()->outputs()[0]);
                 if (dedicated[in] || dedicated[out] || tensors[in]->size_bytes == 0) continue;
                 root[out] = in;
                 death[in] = std::max(death[in], death[out]);
@@ -388,8 +619,9 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     }
     stats.bytes_saved = unshared > arena_bytes ? unshared - arena_bytes : 0;
 
-    std::unordered_map<pConstTensorStorage, pTensorStorage> remap;
-    for (std::size_t i = 0; i < tensors.size(); ++i) remap[tensors[i].get()] = staged[i].get();
+    std::vector<pTensorStorage> staged_ptr(tensors.size());
+    for (std::size_t i = 0; i < tensors.size(); ++i) staged_ptr[i] = staged[i].get();
+    auto remap = [&](pConstTensorStorage t) { return staged_ptr[index.at(t)]; };
 
     // Kernels and the executable.
     auto impl = std::make_unique<Executable::Impl>();
@@ -401,37 +633,52 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     impl->node_count = order.size();
     impl->topo.reserve(steps.size());
     for (const auto& step : steps) {
-        if (step.size() > 1) {
-            // grouped QuantizedMatMul: [A, B_1, S_1, ..], [C_1, ..]
+        if (step.fused >= 0) {
+            // fused chain: its external operands, in the order its kind lists them
             Executable::CompiledNode cn;
-            cn.inputs.push_back(remap.at(step.front()->inputs()[0]));
-            for (const auto* node : step) {
-                cn.inputs.push_back(remap.at(node->inputs()[1]));
-                cn.inputs.push_back(remap.at(node->inputs()[2]));
-                cn.outputs.push_back(remap.at(node->outputs()[0]));
-            }
-            cn.kernel = qmm_group_kernel(device);
-            auto* ga = new QmmGroupAttrs{step.front()->op(), step.size()};
-            cn.attrs = std::shared_ptr<const void>(ga, [](const void* p) { delete static_cast<const QmmGroupAttrs*>(p); });
-            cn.fused = step.size();
+            for (auto* in : step.ins) cn.inputs.push_back(remap(in));
+            for (auto* out : step.outs) cn.outputs.push_back(remap(out));
+            cn.kernel = fused_kernel(device, static_cast<FusedKind>(step.fused));
+            if (step.desc)
+                cn.attrs = std::shared_ptr<const void>(new OpDescriptor(*step.desc), [](const void* p) {
+                    delete static_cast<const OpDescriptor*>(p);
+                });
+            cn.fused = step.nodes.size();
             impl->topo.push_back(std::move(cn));
             continue;
         }
-        const auto* node = step.front();
+        if (step.nodes.size() > 1) {
+            // grouped QuantizedMatMul: [A, B_1, S_1, ..], [C_1, ..]
+            Executable::CompiledNode cn;
+            cn.inputs.push_back(remap(step.nodes.front()->inputs()[0]));
+            for (const auto* node : step.nodes) {
+                cn.inputs.push_back(remap(node->inputs()[1]));
+                cn.inputs.push_back(remap(node->inputs()[2]));
+                cn.outputs.push_back(remap(node->outputs()[0]));
+            }
+            cn.kernel = qmm_group_kernel(device);
+            auto* ga = new QmmGroupAttrs{step.nodes.front()->op(), step.nodes.size()};
+            cn.attrs = std::shared_ptr<const void>(ga, [](const void* p) { delete static_cast<const QmmGroupAttrs*>(p); });
+            cn.fused = step.nodes.size();
+            impl->topo.push_back(std::move(cn));
+            continue;
+        }
+        const auto* node = step.nodes.front();
         Executable::CompiledNode cn;
         const bool aliased = alias_step[static_cast<std::size_t>(&step - steps.data())];
-        std::vector<DataType> dtypes;
+        DataType dtypes[4];
+        std::size_t n_in = 0;
         for (auto* in : node->inputs()) {
-            auto* s = remap.at(in);
-            cn.inputs.push_back(s);
-            dtypes.push_back(in->dtype);
+            cn.inputs.push_back(remap(in));
+            if (n_in < 4) dtypes[n_in] = in->dtype;
+            ++n_in;
         }
-        for (auto* out : node->outputs()) {
-            auto* s = remap.at(out);
-            cn.outputs.push_back(s);
-        }
+        for (auto* out : node->outputs()) cn.outputs.push_back(remap(out));
         if (cn.outputs.empty()) throw std::runtime_error("velomind: op node has no outputs");
-        cn.kernel = aliased ? &no_launch : resolve_op_kernel(node->op().op, dtypes, node->outputs().front()->dtype, device);
+        cn.kernel = aliased ? &no_launch
+                            : (n_in > 4 ? nullptr
+                                        : resolve_op_kernel(node->op().op, std::span<const DataType>(dtypes, n_in),
+                                                            node->outputs().front()->dtype, device));
         if (!cn.kernel) throw std::runtime_error(std::string("velomind: no kernel for op=") + op_name(node->op().op));
         cn.attrs = std::shared_ptr<const void>(new OpDescriptor(node->op()),
                                                [](const void* p) { delete static_cast<const OpDescriptor*>(p); });
@@ -442,10 +689,10 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     // Commit.
     graph._tensors.swap(staged);
     for (auto& node : graph._nodes) {
-        for (auto*& in : node._inputs) in = remap.at(in);
-        for (auto*& out : node._outputs) out = remap.at(out);
+        for (auto*& in : node._inputs) in = remap(in);
+        for (auto*& out : node._outputs) out = remap(out);
     }
-    for (auto*& out : graph._explicit_outputs) out = remap.at(out);
+    for (auto*& out : graph._explicit_outputs) out = remap(out);
     graph._built = true;
     graph._bound_device = device;
     graph._plan_stats = stats;

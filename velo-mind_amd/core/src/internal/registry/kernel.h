@@ -55,6 +55,27 @@ auto register_qmm_group_kernel(DeviceType device, Executable::KernelFn fn) -> vo
 // nullptr when the device has none (its QuantizedMatMul nodes run one by one)
 auto qmm_group_kernel(DeviceType device) -> Executable::KernelFn;
 
+// Fused steps: a chain of graph nodes that a device runs as one launch,
+// the chain's intermediates never materialised.  A device registers one
+// kernel per kind; the graph compiler matches the chains
+// (graph_compiler.cpp) and hands the kernel the chain's external operands.
+// No counterpart in the reference, which runs every node on its own.
+enum class FusedKind : int {
+    SiluMul = 0,          // Mul(Mul(Sigmoid(g), g), u): inputs [g, u], outputs [y]
+    QmmAdd = 1,           // Add(h, QuantizedMatMul(A, B, S)): inputs [A, B, S, h], outputs [C];
+                          // attrs the QuantizedMatMul's OpDescriptor
+    AttentionDecode = 2,  // one query row per head: RepeatKV(K), RepeatKV(V), Transpose(K),
+                          // MatMul, Softmax, MatMul: inputs [q, K, V] (K/V before RepeatKV),
+                          // outputs [ctx]
+    AttentionGqa = 3,     // FusedAttention on RepeatKV(K), RepeatKV(V): inputs [q, K, V]
+                          // (before RepeatKV), outputs [o]; attrs the FusedAttention's OpDescriptor
+};
+inline constexpr std::size_t kFusedKinds = 4;
+
+auto register_fused_kernel(DeviceType device, FusedKind kind, Executable::KernelFn fn) -> void;
+// nullptr when the device does not run that chain fused
+auto fused_kernel(DeviceType device, FusedKind kind) -> Executable::KernelFn;
+
 template <DataType D> struct dtype_to_type;
 template <> struct dtype_to_type<DataType::Float32> { using type = float; };
 template <> struct dtype_to_type<DataType::Int32> { using type = std::int32_t; };
@@ -83,6 +104,13 @@ template <DataType D> using dtype_t = typename dtype_to_type<D>::type;
                                               3, (TC_DT)}),                                       \
         (&NAME<::velomind::internal::dtype_t<TA_DT>, ::velomind::internal::dtype_t<TSCALE_DT>,    \
                ::velomind::internal::dtype_t<TC_DT>>))
+
+// Registers FN as DEVICE's kernel for the fused chain KIND.
+#define VELOMIND_REGISTER_FUSED(DEVICE, KIND, FN)                                                  \
+    [[maybe_unused]] static const bool VELOMIND_CONCAT_(_velomind_fz_, __LINE__) = [] {          \
+        ::velomind::internal::register_fused_kernel((DEVICE), (KIND), (FN));                     \
+        return true;                                                                             \
+    }();
 
 // Registers FN as DEVICE's grouped QuantizedMatMul kernel.
 #define VELOMIND_REGISTER_QMM_GROUP(DEVICE, FN)                                                   \

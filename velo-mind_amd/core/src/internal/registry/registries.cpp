@@ -66,6 +66,27 @@ auto qmm_group_kernel(DeviceType device) -> Executable::KernelFn {
     return idx < MAX_DEVICE_TYPES ? qmm_group_table()[idx] : nullptr;
 }
 
+namespace {
+auto fused_table() -> std::array<std::array<Executable::KernelFn, kFusedKinds>, MAX_DEVICE_TYPES>& {
+    static std::array<std::array<Executable::KernelFn, kFusedKinds>, MAX_DEVICE_TYPES> table{};
+    return table;
+}
+}  // namespace
+
+auto register_fused_kernel(DeviceType device, FusedKind kind, Executable::KernelFn fn) -> void {
+    const auto idx = static_cast<std::size_t>(device);
+    const auto k = static_cast<std::size_t>(kind);
+    if (idx >= MAX_DEVICE_TYPES || k >= kFusedKinds)
+        throw std::out_of_range("register_fused_kernel: device or kind out of range");
+    fused_table()[idx][k] = fn;
+}
+
+auto fused_kernel(DeviceType device, FusedKind kind) -> Executable::KernelFn {
+    const auto idx = static_cast<std::size_t>(device);
+    const auto k = static_cast<std::size_t>(kind);
+    return (idx < MAX_DEVICE_TYPES && k < kFusedKinds) ? fused_table()[idx][k] : nullptr;
+}
+
 // ---- signatures and default attributes -----------------------------------
 
 auto signatures() -> std::array<OpSignatureFn, MAX_OPS>& {

@@ -1,4 +1,5 @@
 // LlamaWeightSet and GraphLlamaSession (see velomind/llama/llama_hip.h).
+#include <chrono>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -196,6 +197,7 @@ auto GraphLlamaSession::prefill(std::span<const std::int32_t> tokens) -> std::ve
         _v.push_back(kv.v[l].shared_storage());
     }
     _seq_len = tokens.size();
+    _timing = {};
     std::vector<float> out(cfg.vocab_size);
     logits.copy_to_host(std::as_writable_bytes(std::span(out)));
     return out;
@@ -207,6 +209,8 @@ auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std
         return prefill(one);
     }
     if (pos != _seq_len) throw std::invalid_argument("GraphLlamaSession::forward_step: pos must equal the cache length");
+    using clock = std::chrono::steady_clock;
+    const auto t0 = clock::now();
     const auto& cfg = _weights->config();
     const auto half = static_cast<dim_t>(cfg.head_dim() / 2);
     Graph g;
@@ -221,6 +225,7 @@ auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std
         kv_in.v.push_back(g.input(_v[l]));
     }
     auto logits = build_forward_graph_decode(g, cfg, tok, w, kv_in, &kv_out);
+    const auto t1 = clock::now();
     auto exec = g.build(DeviceType::HIP);
     const std::int32_t one[1] = {token};
     tok.copy_from_host(std::as_bytes(std::span(one)));
@@ -228,7 +233,9 @@ auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std
     compute_rope_cache(1, cfg.head_dim(), cfg.rope_theta, c, sn, pos);
     w.cos_cache.copy_from_host(std::as_bytes(std::span(c)));
     w.sin_cache.copy_from_host(std::as_bytes(std::span(sn)));
+    const auto t2 = clock::now();
     exec->execute();
+    const auto t3 = clock::now();
     for (std::size_t l = 0; l < cfg.num_layers; ++l) {
         _k[l] = kv_out.k[l].shared_storage();
         _v[l] = kv_out.v[l].shared_storage();
@@ -236,6 +243,13 @@ auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std
     _seq_len = pos + 1;
     std::vector<float> out(cfg.vocab_size);
     logits.copy_to_host(std::as_writable_bytes(std::span(out)));
+    const auto t4 = clock::now();
+    auto sec = [](clock::time_point a, clock::time_point b) { return std::chrono::duration<double>(b - a).count(); };
+    _timing[0] += sec(t0, t1);
+    _timing[1] += sec(t1, t2);
+    _timing[2] += sec(t2, t3);
+    _timing[3] += sec(t3, t4);
+    _timing[4] += 1.0;
     return out;
 }
 

@@ -131,7 +131,11 @@ __global__ void repeat_kv_kernel(const float* __restrict__ x, float* __restrict_
     }
 }
 
-// ---- Elementwise Add / Mul / Sigmoid (add.cpp, mul.cpp, sigmoid.cpp).
+// ---- Elementwise Add / Mul / Sigmoid (add.cpp, mul.cpp, sigmoid.cpp), and
+// the SwiGLU chain Mul(Mul(Sigmoid(a), a), b) in one pass with the same
+// three roundings in the same order (the graph compiler's fused step).
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 __global__ void elementwise_kernel(int op, const float* __restrict__ a, const float* __restrict__ b,
                                    float* __restrict__ y, int64_t n) {
     for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < n;
@@ -140,7 +144,8 @@ __global__ void elementwise_kernel(int op, const float* __restrict__ a, const fl
         float r;
         if (op == VM_HIP_EW_ADD) r = x + b[e];
         else if (op == VM_HIP_EW_MUL) r = x * b[e];
-        else r = 1.0f / (1.0f + expf(-x));
+        else if (op == VM_HIP_EW_SILU_MUL) r = (sigmoid_f32(x) * x) * b[e];
+        else r = sigmoid_f32(x);
         y[e] = r;
     }
 }
@@ -299,6 +304,66 @@ __global__ __launch_bounds__(64) void attention_kernel(const float* __restrict__
     }
 }
 
+// ---- Decode attention as the reference graph's unfused chain computes it
+// (llama_graph.cpp:95-107: RepeatKV on K and V, Transpose of K, MatMul,
+// Softmax, MatMul) for one query row per head, in one launch: one
+// workgroup per query head h reads kv head h / (hq / hkv) directly.  Every
+// value follows the fp32 operations of the kernels the chain launches, in
+// their order: a score is matmul_f32_kernel's FMA chain over d from 0 (its
+// zero padding of K to a multiple of 16 included), the softmax is
+// softmax_rows_kernel's (64 lane-strided partial max and sum, xor
+// butterflies, exp(x - max) / sum), the context is matmul_f32_kernel's FMA
+// chain over the positions (padding included).  The result equals the
+// chain's bit for bit, without the repeated K/V, the transposed K and the
+// score rows in memory.
+__global__ __launch_bounds__(kT) void attention_decode_chain_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o,
+    int64_t hq, int64_t hkv, int64_t s, int64_t d, int64_t dv) {
+    extern __shared__ float sh[];
+    float* qs = sh;        // [d]
+    float* sc = sh + d;    // [s]: scores, then probabilities
+    __shared__ float stat[2];
+    const int64_t h = blockIdx.x;
+    const int64_t kvh = h / (hq / hkv);
+    const float* kb = k + kvh * s * d;
+    const float* vb = v + kvh * s * dv;
+    for (int64_t t = threadIdx.x; t < d; t += kT) qs[t] = q[h * d + t];
+    __syncthreads();
+    const int64_t dpad = (d + 15) / 16 * 16;
+    for (int64_t j = threadIdx.x; j < s; j += kT) {
+        const float* kr = kb + j * d;
+        float acc = 0.0f;
+        for (int64_t t = 0; t < d; ++t) acc = fmaf(qs[t], kr[t], acc);
+        for (int64_t t = d; t < dpad; ++t) acc = fmaf(0.0f, 0.0f, acc);
+        sc[j] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float mx = -INFINITY;
+        for (int64_t j = lane; j < s; j += 64) mx = fmaxf(mx, sc[j]);
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float sum = 0.0f;
+        for (int64_t j = lane; j < s; j += 64) sum += expf(sc[j] - mx);
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (lane == 0) {
+            stat[0] = mx;
+            stat[1] = sum;
+        }
+    }
+    __syncthreads();
+    const float mx = stat[0], sum = stat[1];
+    for (int64_t j = threadIdx.x; j < s; j += kT) sc[j] = expf(sc[j] - mx) / sum;
+    __syncthreads();
+    const int64_t spad = (s + 15) / 16 * 16;
+    for (int64_t t = threadIdx.x; t < dv; t += kT) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < s; ++j) acc = fmaf(sc[j], vb[j * dv + t], acc);
+        for (int64_t j = s; j < spad; ++j) acc = fmaf(0.0f, 0.0f, acc);
+        o[h * dv + t] = acc;
+    }
+}
+
 }  // namespace
 }  // namespace vmhip
 
@@ -420,12 +485,17 @@ int vm_hip_repeat_kv_f32(const float* x, float* y, int64_t outer, int64_t kv_hea
 
 int vm_hip_elementwise_f32(int op, const float* a, const float* b, float* y, int64_t n, void* stream) {
     clear_error();
-    if (op != VM_HIP_EW_ADD && op != VM_HIP_EW_MUL && op != VM_HIP_EW_SIGMOID) return fail_inval("elementwise: bad op");
+    if (op != VM_HIP_EW_ADD && op != VM_HIP_EW_MUL && op != VM_HIP_EW_SIGMOID && op != VM_HIP_EW_SILU_MUL)
+        return fail_inval("elementwise: bad op");
     if (n < 0) return fail_inval("elementwise: negative size");
     if (n == 0) return 0;
     if (!a || !y || (op != VM_HIP_EW_SIGMOID && !b)) return fail_inval("elementwise: null pointer");
     hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(n)), dim3(kT), 0, S(stream), op, a, b, y, n);
-    return check_launch(op == VM_HIP_EW_ADD ? "Add" : op == VM_HIP_EW_MUL ? "Mul" : "Sigmoid", S(stream));
+    return check_launch(op == VM_HIP_EW_ADD   ? "Add"
+                        : op == VM_HIP_EW_MUL ? "Mul"
+                        : op == VM_HIP_EW_SIGMOID ? "Sigmoid"
+                                                  : "SiluMul",
+                        S(stream));
 }
 
 int vm_hip_softmax_f32(const float* x, float* y, int64_t outer, int64_t cols, int64_t inner, void* stream) {
@@ -457,6 +527,20 @@ int vm_hip_matmul_f32(const float* a, const float* b, float* c, int64_t batch, i
                                                static_cast<unsigned>(batch)),
                        dim3(kT), 0, S(stream), a, b, c, m, k, n);
     return check_launch("MatMul", S(stream));
+}
+
+int vm_hip_attention_decode_chain_f32(const float* q, const float* k, const float* v, float* o, int64_t hq,
+                                      int64_t hkv, int64_t s, int64_t d, int64_t dv, void* stream) {
+    clear_error();
+    if (hq < 1 || hkv < 1 || hq % hkv != 0 || s < 1 || d < 1 || dv < 1)
+        return fail_inval("AttentionDecodeChain: bad shape");
+    if (s + d > 16384) return fail_inval("AttentionDecodeChain: S + D exceeds 16384 on this kernel");
+    if (hq > 0x7fffffff) return fail_inval("AttentionDecodeChain: too many heads");
+    if (!q || !k || !v || !o) return fail_inval("AttentionDecodeChain: null pointer");
+    const size_t lds = static_cast<size_t>(d + s) * sizeof(float);
+    hipLaunchKernelGGL(attention_decode_chain_kernel, dim3(static_cast<unsigned>(hq)), dim3(kT), lds, S(stream), q, k,
+                       v, o, hq, hkv, s, d, dv);
+    return check_launch("AttentionDecodeChain", S(stream));
 }
 
 int vm_hip_attention_f32(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t hq,

@@ -174,6 +174,25 @@ int vm_hip_qmm_f32(const float* a, const int8_t* wq, const float* scale, float* 
                         static_cast<hipStream_t>(stream));
 }
 
+int vm_hip_qmm_add_f32(const float* a, const int8_t* wq, const float* scale, const float* addend, float* c,
+                       int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size, void* stream) {
+    clear_error();
+    VM_TRY(validate_qmm(a, wq, scale, c, rows_m, k, n, quant_type, block_size));
+    if (rows_m == 0 || n == 0) return 0;
+    if (!addend) return fail_inval("QuantizedMatMul+Add: null addend");
+    VM_TRY(injected_failure("QuantizedMatMul", "launch"));
+    auto s = static_cast<hipStream_t>(stream);
+    if (rows_m <= 4 && k > 0) {
+        const int bs = (quant_type == VM_HIP_QUANT_INT4 && block_size <= 0) ? 32 : block_size;
+        const int rc = gemv_qmm_f32(a, reinterpret_cast<const uint8_t*>(wq), scale, c, static_cast<int>(rows_m),
+                                    static_cast<int>(k), static_cast<int>(n), quant_type, bs, s, addend);
+        if (rc != VM_HIP_EUNSUPPORTED) return rc;
+    }
+    // Shapes the GEMV does not take: the product, then the addition.
+    VM_TRY(qmm_f32_impl(a, wq, scale, c, rows_m, k, n, quant_type, block_size, s));
+    return vm_hip_elementwise_f32(VM_HIP_EW_ADD, addend, c, c, rows_m * n, stream);
+}
+
 int vm_hip_qmm_a_layout(int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size, int* layout,
                         int64_t* bytes) {
     clear_error();

@@ -151,7 +151,8 @@ struct Chunk {
 template <int KIND, int MR, int L, int W, bool GROUPED>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const GemvMembers mb, int m, int k, int block_size, int chunks_per_split,
-    uint32_t a_bytes, int a_vec, int blk_shift, unsigned long long* __restrict__ pairs) {
+    uint32_t a_bytes, int a_vec, int blk_shift, unsigned long long* __restrict__ pairs,
+    const float* __restrict__ addend) {
     VM_GEMV_MARKS;
     VM_GEMV_MARK(0);
     using CS = ChunkShape<KIND>;
@@ -444,6 +445,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
                 for (int w = 0; w < W; ++w) v += red[(w * MR + i) * kTileCols + cc];
                 if constexpr (CS::kInt4) v *= 0.0625f;  // INT4 sums carry 16 * code
                 if constexpr (KIND == 0) v *= scale[col];
+                if (addend) v = addend[static_cast<int64_t>(i) * n + col] + v;
                 c[static_cast<int64_t>(i) * n + col] = v;
             }
         }
@@ -497,6 +499,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         }
         if (!last) continue;
         if constexpr (KIND == 0) v *= scale[col];
+        if (addend) v = addend[static_cast<int64_t>(i) * n + col] + v;
         c[static_cast<int64_t>(i) * n + col] = v;
     }
     VM_GEMV_END();
@@ -673,6 +676,7 @@ struct Member {
     const float* scale;
     float* c;
     int n;
+    const float* addend = nullptr;  // [m, n] added to C (a launch of one matrix only)
 };
 
 template <int KIND, int MR, int L, int W>
@@ -713,10 +717,12 @@ int launch_cfg(const float* a, const Member* members, int count, int m, int k, i
     }
     if (count == 1)
         hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, false>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
-                           stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs);
+                           stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs,
+                           members[0].addend);
     else
         hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, true>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
-                           stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs);
+                           stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs,
+                           nullptr);
     return check_launch("QuantizedMatMul", stream);
 }
 
@@ -782,8 +788,8 @@ int gemv_group_f32(const float* a, const Member* members, int count, int m, int 
 }  // namespace
 
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
-                 int n, int quant_type, int block_size, hipStream_t stream) {
-    const Member one{wq, scale, c, n};
+                 int n, int quant_type, int block_size, hipStream_t stream, const float* addend) {
+    const Member one{wq, scale, c, n, addend};
     return gemv_group_f32(a, &one, 1, m, k, quant_type, block_size, stream);
 }
 

@@ -81,6 +81,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_qmm_group_f32": ([p, c_int64, c_int64, POINTER(QmmMember), c_int, c_int, c_int, p], c_int),
         "vm_hip_decode_trace_read": ([p, c_int64], c_int),
         "vm_hip_gemv_trace_read": ([p, c_int64], c_int),
+        "vm_hip_qmm_add_f32": ([p, p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
+        "vm_hip_attention_decode_chain_f32": ([p, p, p, p, c_int64, c_int64, c_int64, c_int64, c_int64, p], c_int),
         "vm_hip_qmm": ([p, c_int, p, p, c_int, p, c_int, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_pack_int8": ([p, p, p, c_int64, c_int64, p], c_int),
         "vm_hip_pack_int4": ([p, p, p, c_int64, c_int64, c_int64, p], c_int),
@@ -156,6 +158,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_slices_sum_scaled_f32", "vm_hip_attention_decode_slices_prefetch_f32",
             "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32", "vm_hip_decode_workspace_bytes",
             "vm_hip_decode_step", "vm_hip_decode_status", "vm_hip_decode_trace_read", "vm_hip_gemv_trace_read",
+            "vm_hip_qmm_add_f32", "vm_hip_attention_decode_chain_f32",
             "vm_hip_qmm_a_layout", "vm_hip_qmm_staged_f32", "vm_hip_add_rmsnorm_stage_f32",
             "vm_hip_silu_mul_stage_f32"]
 
@@ -397,7 +400,7 @@ def run_pack_int4(w: np.ndarray, block: int = 32):
 
 # ---- LLaMA graph operators, numpy level (one call each, null stream) ----
 
-EW_ADD, EW_MUL, EW_SIGMOID = 0, 1, 2
+EW_ADD, EW_MUL, EW_SIGMOID, EW_SILU_MUL = 0, 1, 2, 3
 GEMV_SRC_PLAIN, GEMV_SRC_SLICES, GEMV_SRC_SWIGLU, GEMV_SRC_NORMRES, GEMV_SRC_ATTN = 0, 1, 2, 3, 4
 
 

@@ -52,11 +52,13 @@ def lib() -> ctypes.CDLL:
         L.vm_llama_packed_destroy.restype = None
         L.vm_llama_session_create_packed.argtypes = [p, c_int64, POINTER(c_void_p)]
         L.vm_llama_session_decode_path.argtypes = [p, POINTER(c_int)]
+        L.vm_llama_session_step_timing.argtypes = [p, p]
         for name in ("vm_llama_weights_create", "vm_llama_weights_set", "vm_llama_weights_fill_synthetic",
                      "vm_llama_weights_tie_lm_head",
                      "vm_llama_session_create", "vm_llama_prefill", "vm_llama_forward_step", "vm_llama_generate",
                      "vm_llama_pack", "vm_llama_packed_save", "vm_llama_packed_config", "vm_llama_packed_load",
-                     "vm_llama_session_create_packed", "vm_llama_session_decode_path"):
+                     "vm_llama_session_create_packed", "vm_llama_session_decode_path",
+                     "vm_llama_session_step_timing"):
             getattr(L, name).restype = c_int
         _lib = L
     return _lib
@@ -200,6 +202,15 @@ class Session:
         _check(lib().vm_llama_generate(self.handle, t.ctypes.data, t.size, steps, int(use_hip_graph),
                                        out.ctypes.data, timing.ctypes.data))
         return out, (float(timing[0]), float(timing[1]), int(timing[2]))
+
+    def step_timing(self) -> dict:
+        """Graph engine: host seconds per decode step since the last prefill,
+        split into graph construction, Graph::build, execute and readback."""
+        t = np.zeros(5, np.float64)
+        _check(lib().vm_llama_session_step_timing(self.handle, t.ctypes.data))
+        n = max(1.0, t[4])
+        return {"steps": int(t[4]), "construct_ms": t[0] / n * 1e3, "build_ms": t[1] / n * 1e3,
+                "execute_ms": t[2] / n * 1e3, "readback_ms": t[3] / n * 1e3}
 
     def decode_path(self) -> int:
         """DECODE_GRAPH / _PER_OP / _SLICES / _PERSISTENT."""
