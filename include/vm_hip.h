@@ -328,6 +328,19 @@ int vm_hip_attention_f32(const float* q, const float* k, const float* v, float* 
                          int64_t hq, int64_t hk, int64_t sq, int64_t sk, int64_t d, int64_t dv,
                          float scale, int causal, void* stream);
 
+/* One decode position's attention inputs of the reference LLaMA layer in one
+ * launch (llama_graph.cpp:79-84, :296-305): q_out = RoPE(q) [hq, 1, d];
+ * k_out = Concat(k_past, RoPE(k)) and v_out = Concat(v_past, v) on the
+ * sequence axis, k [hkv, 1, d], v [hkv, 1, dv], the pasts [hkv, s_past, .],
+ * the outputs [hkv, s_past + 1, .].  cos/sin [1, d / 2] (the position's
+ * row).  Bit for bit what vm_hip_rope_f32 and vm_hip_concat_f32 produce.
+ * No counterpart in the reference (the graph compiler on DeviceType::HIP
+ * fuses these four nodes). */
+int vm_hip_rope_append_f32(const float* q, const float* k, const float* v, const float* k_past,
+                           const float* v_past, const float* cos_table, const float* sin_table,
+                           float* q_out, float* k_out, float* v_out, int64_t hq, int64_t hkv,
+                           int64_t s_past, int64_t d, int64_t dv, void* stream);
+
 /* Decode attention of the reference LLaMA graph's unfused chain
  * (llama_graph.cpp:95-107: RepeatKV on K and V, Transpose of K, MatMul,
  * Softmax, MatMul) in one launch: q [hq, 1, d], k [hkv, s, d], v [hkv, s,

@@ -75,6 +75,28 @@ void repeat_kv_cpu(const pConstTensorStorage* in, const pTensorStorage* out, con
         std::memcpy(cout0(out) + h * inner, cin(in, 0) + (h / r) * inner, inner * 4);
 }
 
+// RoPE over rows of the last axis with one cos/sin row
+void rope_rotate(float a, float b, float c, float s, float* y0, float* y1) {
+    *y0 = a * c - b * s;
+    *y1 = b * c + a * s;
+}
+void rope_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    const std::size_t d = static_cast<std::size_t>(in[0]->shape.back()), half = d / 2, rows = numel(*in[0]) / d;
+    for (std::size_t r = 0; r < rows; ++r)
+        for (std::size_t j = 0; j < half; ++j)
+            rope_rotate(cin(in, 0)[r * d + j], cin(in, 0)[r * d + j + half], cin(in, 1)[j], cin(in, 2)[j],
+                        cout0(out) + r * d + j, cout0(out) + r * d + j + half);
+}
+// axis 1 of rank-3 tensors
+void concat_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    const auto& a = in[0]->shape;
+    const std::size_t ab = static_cast<std::size_t>(a[1] * a[2]), bb = numel(*in[1]) / static_cast<std::size_t>(a[0]);
+    for (std::size_t o = 0; o < static_cast<std::size_t>(a[0]); ++o) {
+        std::memcpy(cout0(out) + o * (ab + bb), cin(in, 0) + o * ab, ab * 4);
+        std::memcpy(cout0(out) + o * (ab + bb) + ab, cin(in, 1) + o * bb, bb * 4);
+    }
+}
+
 // fused: the same operations in the same order as the chains above
 void silu_mul_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
     for (std::size_t e = 0; e < numel(*out[0]); ++e) {
@@ -114,6 +136,22 @@ void attention_decode_fused_cpu(const pConstTensorStorage* in, const pTensorStor
     }
 }
 
+// inputs [q, k, v, K_past, V_past, cos, sin], outputs [q', K, V]
+void rope_append_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    const pConstTensorStorage rq[3] = {in[0], in[5], in[6]};
+    const pConstTensorStorage rk[3] = {in[1], in[5], in[6]};
+    rope_cpu(rq, out, nullptr);
+    std::vector<float> kr(numel(*in[1]));
+    TensorStorage tmp = *in[1];
+    tmp.data = kr.data();
+    const pTensorStorage ko[1] = {&tmp};
+    rope_cpu(rk, ko, nullptr);
+    const pConstTensorStorage ck[2] = {in[3], &tmp};
+    const pConstTensorStorage cv[2] = {in[4], in[2]};
+    concat_cpu(ck, out + 1, nullptr);
+    concat_cpu(cv, out + 2, nullptr);
+}
+
 constexpr DataType F32 = DataType::Float32;
 #define CPU_F32(OP, N, FN) \
     VELOMIND_REGISTER_OP_KERNEL(DeviceType::CPU, OP, (internal::KernelDtypeKey{{F32, F32, F32, F32}, N, F32}), &FN)
@@ -124,9 +162,12 @@ CPU_F32(Op::MatMul, 2, matmul_cpu)
 CPU_F32(Op::Softmax, 1, softmax_cpu)
 CPU_F32(Op::Transpose, 1, transpose_cpu)
 CPU_F32(Op::RepeatKV, 1, repeat_kv_cpu)
+CPU_F32(Op::RotaryEmbedding, 3, rope_cpu)
+CPU_F32(Op::Concat, 2, concat_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::SiluMul, &silu_mul_fused_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::QmmAdd, &qmm_add_fused_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::AttentionDecode, &attention_decode_fused_cpu)
+VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::RopeAppend, &rope_append_fused_cpu)
 
 struct QmmWeights {
     std::vector<std::int8_t> q;
@@ -254,4 +295,68 @@ TEST_CASE("fusion: decode attention chain runs as one step, with and without Rep
         REQUIRE(kept.steps == off.steps);
         REQUIRE(std::memcmp(kept.ctx.data(), off.ctx.data(), off.ctx.size() * 4) == 0);
     }
+}
+
+namespace {
+// One decode position of the reference layer's attention: RoPE on q and k,
+// the KV caches grown by Concat, then the attention chain; K and V kept.
+struct LayerAttnRun {
+    std::vector<float> ctx, kc, vc;
+    std::size_t steps = 0;
+};
+LayerAttnRun run_layer_attention(bool fuse, bool keep_rotated_q) {
+    const std::size_t hq = 6, hkv = 2, s = 9, dh = 8, half = dh / 2;
+    const auto q = normal(hq * dh, 81), k = normal(hkv * dh, 82), v = normal(hkv * dh, 83);
+    const auto pk = normal(hkv * s * dh, 84), pv = normal(hkv * s * dh, 85), c = normal(half, 86), sn = normal(half, 87);
+    ScopedEnv env("VELOMIND_GRAPH_FUSE", fuse ? "1" : "0");
+    Graph g;
+    auto tq = g.input({(dim_t)hq, 1, (dim_t)dh}, F32), tk = g.input({(dim_t)hkv, 1, (dim_t)dh}, F32);
+    auto tv = g.input({(dim_t)hkv, 1, (dim_t)dh}, F32);
+    auto tpk = g.input({(dim_t)hkv, (dim_t)s, (dim_t)dh}, F32), tpv = g.input({(dim_t)hkv, (dim_t)s, (dim_t)dh}, F32);
+    auto tc = g.input({1, (dim_t)half}, F32), ts = g.input({1, (dim_t)half}, F32);
+    auto qr = g.op(Op::RotaryEmbedding, tq, tc, ts);
+    auto kr = g.op(Op::RotaryEmbedding, tk, tc, ts);
+    auto kc = g.op(OpDescriptor{Op::Concat, ConcatAttrs{1}}, tpk, kr);
+    auto vc = g.op(OpDescriptor{Op::Concat, ConcatAttrs{1}}, tpv, tv);
+    auto ka = g.op(OpDescriptor{Op::RepeatKV, RepeatKVAttrs{3, 0}}, kc);
+    auto va = g.op(OpDescriptor{Op::RepeatKV, RepeatKVAttrs{3, 0}}, vc);
+    auto kt = g.op(OpDescriptor{Op::Transpose, TransposeAttrs{{0, 2, 1}}}, ka);
+    auto ctx = g.op(Op::MatMul, g.op(Op::Softmax, g.op(Op::MatMul, qr, kt)), va);
+    g.mark_output(ctx);
+    g.mark_output(kc);
+    g.mark_output(vc);
+    if (keep_rotated_q) g.mark_output(qr);
+    auto exec = g.build(DeviceType::CPU);
+    LayerAttnRun r;
+    r.steps = exec->num_steps();
+    tq.copy_from_host(as_bytes(q));
+    tk.copy_from_host(as_bytes(k));
+    tv.copy_from_host(as_bytes(v));
+    tpk.copy_from_host(as_bytes(pk));
+    tpv.copy_from_host(as_bytes(pv));
+    tc.copy_from_host(as_bytes(c));
+    ts.copy_from_host(as_bytes(sn));
+    exec->execute();
+    r.ctx.resize(hq * dh);
+    r.kc.resize(hkv * (s + 1) * dh);
+    r.vc.resize(hkv * (s + 1) * dh);
+    ctx.copy_to_host(as_writeable_bytes(r.ctx));
+    kc.copy_to_host(as_writeable_bytes(r.kc));
+    vc.copy_to_host(as_writeable_bytes(r.vc));
+    return r;
+}
+}  // namespace
+
+TEST_CASE("fusion: RoPE on q and k with the KV appends run as one step", "[core][fusion]") {
+    const auto off = run_layer_attention(false, false);
+    const auto on = run_layer_attention(true, false);
+    REQUIRE(off.steps == 10);
+    REQUIRE(on.steps == 2);   // RopeAppend, AttentionDecode
+    REQUIRE(std::memcmp(on.ctx.data(), off.ctx.data(), on.ctx.size() * 4) == 0);
+    REQUIRE(std::memcmp(on.kc.data(), off.kc.data(), on.kc.size() * 4) == 0);
+    REQUIRE(std::memcmp(on.vc.data(), off.vc.data(), on.vc.size() * 4) == 0);
+    // a requested rotated q is an output of the fused step, which still forms
+    const auto kept = run_layer_attention(true, true);
+    REQUIRE(kept.steps == 2);
+    REQUIRE(std::memcmp(kept.ctx.data(), off.ctx.data(), off.ctx.size() * 4) == 0);
 }

@@ -36,10 +36,17 @@ public:
     };
 
     // A storage the plan reads or writes, with the metadata it had at build
-    // time.  Each storage appears once, however many nodes touch it.
+    // time (the fields a run re-checks).  Each storage appears once, however
+    // many nodes touch it.
+    struct FrozenLayout {
+        shape_t shape;
+        DataType dtype = DataType::Float32;
+        DeviceType device = DeviceType::CPU;
+        std::size_t size_bytes = 0;
+    };
     struct WatchedStorage {
         pConstTensorStorage live = nullptr;
-        TensorStorage frozen;
+        FrozenLayout frozen;
     };
 
     // Embedding node whose device-resident indices are read back and range

@@ -199,6 +199,23 @@ void attention_decode_fused_hip(const pConstTensorStorage* in, const pTensorStor
                                              in[2]->shape[2], current_stream()));
 }
 
+// RoPE(q), Concat(K_past, RoPE(k)), Concat(V_past, v) at one position:
+// inputs [q [H, 1, D], k [Hkv, 1, D], v [Hkv, 1, Dv], K_past [Hkv, S, D],
+// V_past [Hkv, S, Dv], cos, sin], outputs [q', K [Hkv, S + 1, D], V].
+void rope_append_fused_hip(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
+    require_contiguous(Op::Concat, in, 7, *out[1]);
+    for (int i = 0; i < 3; ++i)
+        if (!out[i]->is_contiguous())
+            throw std::invalid_argument(error_context(Op::Concat, *out[i], "launch") + ": strided output is not supported on HIP");
+    const auto& q = in[0]->shape;
+    const auto& kp = in[3]->shape;
+    finish(Op::Concat, *out[1],
+           vm_hip_rope_append_f32(fin(in, 0), fin(in, 1), fin(in, 2), fin(in, 3), fin(in, 4), fin(in, 5), fin(in, 6),
+                                  static_cast<float*>(out[0]->data), static_cast<float*>(out[1]->data),
+                                  static_cast<float*>(out[2]->data), q[0], kp[0], kp[1], q[2], in[4]->shape[2],
+                                  current_stream()));
+}
+
 }  // namespace
 
 #define VM_HIP_F32_KERNEL(OP, N_IN, FN)                                                                  \
@@ -223,6 +240,7 @@ VM_HIP_F32_KERNEL(Op::FusedAttention, 3, fused_attention_hip)
 
 VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, internal::FusedKind::SiluMul, &silu_mul_fused_hip)
 VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, internal::FusedKind::AttentionDecode, &attention_decode_fused_hip)
+VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, internal::FusedKind::RopeAppend, &rope_append_fused_hip)
 // vm_hip_attention_f32 maps query head h to kv head h / (hq / hk) itself,
 // so FusedAttention reads K/V as they were before RepeatKV.
 VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, internal::FusedKind::AttentionGqa, &fused_attention_hip)

@@ -45,7 +45,7 @@ void require_live(const Executable::Impl* impl, const char* who) {
     if (impl->graph_lifetime.expired()) throw std::logic_error(std::string(who) + ": owning graph has been destroyed");
 }
 
-bool same_layout(const TensorStorage& a, const TensorStorage& b) {
+bool same_layout(const TensorStorage& a, const Executable::FrozenLayout& b) {
     return a.shape == b.shape && a.dtype == b.dtype && a.device == b.device && a.size_bytes == b.size_bytes;
 }
 
@@ -91,8 +91,10 @@ void Executable::Impl::derive_run_plan() {
     watched.clear();
     index_guards.clear();
     std::unordered_set<pConstTensorStorage> seen;
+    seen.reserve(4 * topo.size() + 16);
+    watched.reserve(2 * topo.size() + 16);
     auto watch = [&](pConstTensorStorage s) {
-        if (seen.insert(s).second) watched.push_back(WatchedStorage{s, *s});
+        if (seen.insert(s).second) watched.push_back(WatchedStorage{s, FrozenLayout{s->shape, s->dtype, s->device, s->size_bytes}});
     };
     for (std::size_t i = 0; i < topo.size(); ++i) {
         const CompiledNode& cn = topo[i];

@@ -3,13 +3,13 @@
 #include "velomind/graph.h"
 
 #include <algorithm>
-#include <queue>
+#include <span>
 #include <stdexcept>
-#include <unordered_map>
 
 #include "internal/graph_compiler.h"
 #include "internal/registry/kernel.h"
 #include "internal/registry/shape.h"
+#include "internal/tensor_index.h"
 #include "velomind/executable.h"
 
 namespace velomind {
@@ -136,73 +136,107 @@ auto Graph::outputs() const -> std::vector<Tensor> {
     return res;
 }
 
-// Nodes reachable backwards from the explicit outputs (all nodes if none).
-auto Graph::_compute_required_nodes() const -> std::vector<bool> {
-    if (!_has_explicit_outputs) return std::vector<bool>(_nodes.size(), true);
-    std::unordered_map<pConstTensorStorage, std::size_t> producer;
-    for (std::size_t i = 0; i < _nodes.size(); ++i)
-        for (auto* o : _nodes[i].outputs()) producer[o] = i;
-    std::vector<bool> req(_nodes.size(), false);
-    std::vector<std::size_t> stack;
-    for (auto* s : _explicit_outputs) {
-        auto it = producer.find(s);
-        if (it != producer.end() && !req[it->second]) {
-            req[it->second] = true;
-            stack.push_back(it->second);
+namespace {
+
+// The node writing each tensor (by index into the tensor list; the last
+// writer when several do), SIZE_MAX for tensors no node writes.
+std::vector<std::size_t> producers_of(const std::vector<Node>& nodes, const internal::TensorIndex& index,
+                                      std::size_t tensors) {
+    std::vector<std::size_t> p(tensors, SIZE_MAX);
+    for (std::size_t i = 0; i < nodes.size(); ++i)
+        for (auto* o : nodes[i].outputs()) {
+            const std::size_t t = index.find(o);
+            if (t != internal::TensorIndex::npos) p[t] = i;
         }
-    }
+    return p;
+}
+
+std::size_t producer_of(pConstTensorStorage s, const internal::TensorIndex& index,
+                        const std::vector<std::size_t>& producer) {
+    const std::size_t t = index.find(s);
+    return t == internal::TensorIndex::npos ? SIZE_MAX : producer[t];
+}
+
+// Nodes reachable backwards from the explicit outputs.
+std::vector<bool> required_nodes(const std::vector<Node>& nodes, const std::vector<pConstTensorStorage>& outputs,
+                                 const internal::TensorIndex& index, const std::vector<std::size_t>& producer) {
+    std::vector<bool> req(nodes.size(), false);
+    std::vector<std::size_t> stack;
+    auto reach = [&](pConstTensorStorage s) {
+        const std::size_t p = producer_of(s, index, producer);
+        if (p != SIZE_MAX && !req[p]) {
+            req[p] = true;
+            stack.push_back(p);
+        }
+    };
+    for (auto* s : outputs) reach(s);
     while (!stack.empty()) {
         const std::size_t u = stack.back();
         stack.pop_back();
-        for (auto* in : _nodes[u].inputs()) {
-            auto it = producer.find(in);
-            if (it != producer.end() && !req[it->second]) {
-                req[it->second] = true;
-                stack.push_back(it->second);
-            }
-        }
+        for (auto* in : nodes[u].inputs()) reach(in);
     }
     return req;
 }
 
 // Kahn's algorithm over the required nodes, in insertion order among ready
-// nodes; throws on a cycle.
-auto Graph::_topological_order() const -> std::vector<pConstNode> { return _topological_order(_compute_required_nodes()); }
-
-auto Graph::_topological_order(const std::vector<bool>& req) const -> std::vector<pConstNode> {
-    std::unordered_map<pConstTensorStorage, std::size_t> producer;
-    for (std::size_t i = 0; i < _nodes.size(); ++i)
-        for (auto* o : _nodes[i].outputs()) producer[o] = i;
-    std::vector<std::size_t> indeg(_nodes.size(), 0);
-    std::vector<std::vector<std::size_t>> users(_nodes.size());
+// nodes (FIFO); throws on a cycle.
+std::vector<pConstNode> topological(const std::vector<Node>& nodes, const std::vector<bool>& req,
+                                    const internal::TensorIndex& index, const std::vector<std::size_t>& producer) {
+    const std::size_t n = nodes.size();
+    std::vector<std::size_t> indeg(n, 0), deps, edge_u, edge_v;
     std::size_t active = 0;
-    for (std::size_t v = 0; v < _nodes.size(); ++v) {
+    for (std::size_t v = 0; v < n; ++v) {
         if (!req[v]) continue;
         ++active;
-        std::vector<std::size_t> deps;
-        for (auto* in : _nodes[v].inputs()) {
-            auto it = producer.find(in);
-            if (it != producer.end() && req[it->second]) deps.push_back(it->second);
+        deps.clear();
+        for (auto* in : nodes[v].inputs()) {
+            const std::size_t p = producer_of(in, index, producer);
+            if (p != SIZE_MAX && req[p]) deps.push_back(p);
         }
         std::sort(deps.begin(), deps.end());
         deps.erase(std::unique(deps.begin(), deps.end()), deps.end());
         indeg[v] = deps.size();
-        for (std::size_t u : deps) users[u].push_back(v);
+        for (std::size_t u : deps) {
+            edge_u.push_back(u);
+            edge_v.push_back(v);
+        }
     }
-    std::queue<std::size_t> ready;
-    for (std::size_t v = 0; v < _nodes.size(); ++v)
-        if (req[v] && indeg[v] == 0) ready.push(v);
+    // users of each node in ascending order, as compressed rows
+    std::vector<std::size_t> first(n + 1, 0), users(edge_u.size());
+    for (std::size_t u : edge_u) ++first[u + 1];
+    for (std::size_t i = 0; i < n; ++i) first[i + 1] += first[i];
+    std::vector<std::size_t> fill(first.begin(), first.end() - 1);
+    for (std::size_t e = 0; e < edge_u.size(); ++e) users[fill[edge_u[e]]++] = edge_v[e];
+    std::vector<std::size_t> ready;
+    ready.reserve(active);
+    for (std::size_t v = 0; v < n; ++v)
+        if (req[v] && indeg[v] == 0) ready.push_back(v);
     std::vector<pConstNode> order;
     order.reserve(active);
-    while (!ready.empty()) {
-        const std::size_t u = ready.front();
-        ready.pop();
-        order.push_back(&_nodes[u]);
-        for (std::size_t v : users[u])
-            if (--indeg[v] == 0) ready.push(v);
+    for (std::size_t head = 0; head < ready.size(); ++head) {
+        const std::size_t u = ready[head];
+        order.push_back(&nodes[u]);
+        for (std::size_t e = first[u]; e < first[u + 1]; ++e)
+            if (--indeg[users[e]] == 0) ready.push_back(users[e]);
     }
     if (order.size() != active) throw std::invalid_argument("Graph::build: cycle detected in graph");
     return order;
+}
+
+}  // namespace
+
+// Nodes reachable backwards from the explicit outputs (all nodes if none).
+auto Graph::_compute_required_nodes() const -> std::vector<bool> {
+    if (!_has_explicit_outputs) return std::vector<bool>(_nodes.size(), true);
+    const internal::TensorIndex index(_tensors);
+    return required_nodes(_nodes, _explicit_outputs, index, producers_of(_nodes, index, _tensors.size()));
+}
+
+auto Graph::_topological_order() const -> std::vector<pConstNode> { return _topological_order(_compute_required_nodes()); }
+
+auto Graph::_topological_order(const std::vector<bool>& req) const -> std::vector<pConstNode> {
+    const internal::TensorIndex index(_tensors);
+    return topological(_nodes, req, index, producers_of(_nodes, index, _tensors.size()));
 }
 
 auto Graph::validate(DeviceType device) const -> void { (void)_validated_order(device); }
@@ -215,7 +249,10 @@ auto Graph::_validated_order(DeviceType device) const -> std::vector<pConstNode>
         if (s->data != nullptr && s->device != device)
             throw std::invalid_argument("Graph::validate: populated storage belongs to another device");
     }
-    const auto req = _compute_required_nodes();
+    const internal::TensorIndex index(_tensors);
+    const auto producer = producers_of(_nodes, index, _tensors.size());
+    const auto req = _has_explicit_outputs ? required_nodes(_nodes, _explicit_outputs, index, producer)
+                                           : std::vector<bool>(_nodes.size(), true);
     for (std::size_t i = 0; i < _nodes.size(); ++i) {
         if (!req[i]) continue;
         const auto& n = _nodes[i];
@@ -225,12 +262,15 @@ auto Graph::_validated_order(DeviceType device) const -> std::vector<pConstNode>
         const auto* out = n.outputs().front();
         if (sig.shape != out->shape || sig.dtype != out->dtype)
             throw std::invalid_argument("Graph::validate: output metadata no longer matches signature");
-        std::vector<DataType> dtypes;
-        for (auto* in : n.inputs()) dtypes.push_back(in->dtype);
-        if (!internal::resolve_op_kernel(n.op().op, dtypes, out->dtype, device))
+        DataType dtypes[4];
+        const auto ins = n.inputs();
+        const bool keyed = ins.size() <= 4;
+        for (std::size_t j = 0; keyed && j < ins.size(); ++j) dtypes[j] = ins[j]->dtype;
+        if (!keyed || !internal::resolve_op_kernel(n.op().op, std::span<const DataType>(dtypes, ins.size()), out->dtype,
+                                                   device))
             throw std::invalid_argument(std::string("Graph::validate: unsupported kernel for ") + op_name(n.op().op));
     }
-    return _topological_order(req);
+    return topological(_nodes, req, index, producer);
 }
 
 auto Graph::build(DeviceType device) -> std::unique_ptr<Executable> {

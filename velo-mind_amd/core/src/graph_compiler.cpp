@@ -26,6 +26,7 @@
 #include <vector>
 
 #include "internal/registry/device_context.h"
+#include "internal/tensor_index.h"
 #include "internal/registry/kernel.h"
 #include "internal/registry/storage.h"
 
@@ -107,47 +108,6 @@ std::size_t injected_failure_point() {
     const unsigned long long n = std::strtoull(v, &end, 10);
     return (end && *end == '\0') ? static_cast<std::size_t>(n) : 0;
 }
-
-// Tensor storage -> index into Graph::_tensors: a flat open-addressing
-// table over the graph's storages (a decode graph holds ~1600; hashing them
-// into a node-based map took a third of the build).
-class TensorIndex {
-public:
-    static constexpr std::size_t npos = SIZE_MAX;
-    explicit TensorIndex(const std::vector<std::shared_ptr<TensorStorage>>& tensors) {
-        while (_cap < 2 * tensors.size()) _cap <<= 1;
-        _keys.assign(_cap, nullptr);
-        _vals.assign(_cap, 0);
-        for (std::size_t i = 0; i < tensors.size(); ++i) {
-            std::size_t h = slot(tensors[i].get());
-            while (_keys[h] && _keys[h] != tensors[i].get()) h = (h + 1) & (_cap - 1);
-            _keys[h] = tensors[i].get();
-            _vals[h] = i;
-        }
-    }
-    std::size_t find(pConstTensorStorage t) const {
-        for (std::size_t h = slot(t);; h = (h + 1) & (_cap - 1)) {
-            if (_keys[h] == t) return _vals[h];
-            if (!_keys[h]) return npos;
-        }
-    }
-    std::size_t at(pConstTensorStorage t) const {
-        const std::size_t i = find(t);
-        if (i == npos) throw std::out_of_range("velomind: node operand is not a tensor of its graph");
-        return i;
-    }
-
-private:
-    std::size_t slot(pConstTensorStorage t) const {
-        auto x = static_cast<std::uint64_t>(reinterpret_cast<std::uintptr_t>(t));
-        x ^= x >> 29;
-        x *= 0x9E3779B97F4A7C15ull;
-        return static_cast<std::size_t>(x >> 32) & (_cap - 1);
-    }
-    std::size_t _cap = 16;
-    std::vector<pConstTensorStorage> _keys;
-    std::vector<std::size_t> _vals;
-};
 
 // ---- steps -----------------------------------------------------------------
 // A compiled step runs one node; or (where the device registers a group
@@ -255,6 +215,10 @@ std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType de
 //                    Transpose swapping the last two axes, the Softmax on the
 //                    last one (RepeatKV absent when H == Hkv)
 //   AttentionGqa     o = FusedAttention(q, RepeatKV(K), RepeatKV(V))
+//   RopeAppend       q' = RoPE(q), K = Concat(K_past, RoPE(k)), V = Concat(V_past, v)
+//                    at one position (new rows [., 1, .], one cos/sin row), the
+//                    four nodes within a few steps of each other and q', K read
+//                    by nothing before the fused step's place
 // VELOMIND_GRAPH_FUSE=0 keeps every chain as separate launches.
 void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& index,
                 const std::vector<bool>& kept) {
@@ -270,9 +234,14 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
     const std::size_t nt = kept.size();
     std::vector<std::uint32_t> consumers(nt, 0);
     std::vector<std::size_t> producer(nt, SIZE_MAX);   // single-node step producing the tensor
+    std::vector<std::size_t> first_use(nt, SIZE_MAX);  // earliest step reading the tensor
     for (std::size_t s = 0; s < steps.size(); ++s)
         for (auto* n : steps[s].nodes) {
-            for (auto* in : n->inputs()) ++consumers[index.at(in)];
+            for (auto* in : n->inputs()) {
+                const std::size_t i = index.at(in);
+                ++consumers[i];
+                first_use[i] = std::min(first_use[i], s);
+            }
             if (steps[s].nodes.size() == 1)
                 for (auto* out : n->outputs()) producer[index.at(out)] = s;
         }
@@ -303,7 +272,8 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
         return node_of(s)->inputs()[0];
     };
     auto make = [&](std::size_t at, FusedKind kind, std::vector<std::size_t> absorbed,
-                    std::vector<pConstTensorStorage> ins, const OpDescriptor* desc) {
+                    std::vector<pConstTensorStorage> ins, const OpDescriptor* desc,
+                    std::vector<pConstTensorStorage> outs = {}) {
         Step f;
         std::sort(absorbed.begin(), absorbed.end());
         for (std::size_t s : absorbed) {
@@ -313,7 +283,7 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
         f.nodes.push_back(node_of(at));
         f.fused = static_cast<int>(kind);
         f.ins = std::move(ins);
-        f.outs = {node_of(at)->outputs()[0]};
+        f.outs = outs.empty() ? std::vector<pConstTensorStorage>{node_of(at)->outputs()[0]} : std::move(outs);
         f.desc = desc;
         steps[at] = std::move(f);
     };
@@ -387,6 +357,66 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
             if (!shapes) continue;
             if (!(f32(q) && f32(k) && f32(v) && f32(out))) continue;
             make(j, FusedKind::AttentionDecode, absorbed, {q, k, v}, nullptr);
+            continue;
+        }
+        if (op == Op::Concat && kernels[static_cast<int>(FusedKind::RopeAppend)] && ins.size() == 2) {
+            // the later of the two appends; the other and the two RoPEs come a few steps before it
+            auto seq_append = [&](pConstNode c) {
+                const auto* a = std::get_if<ConcatAttrs>(&c->op().attrs);
+                const auto* p = c->inputs()[0];
+                const auto* x = c->inputs()[1];
+                return c->outputs().size() == 1 && a && (a->axis == 1 || a->axis == -2) && p->shape.size() == 3 &&
+                       x->shape.size() == 3 && x->shape[1] == 1 && x->shape[0] == p->shape[0] &&
+                       x->shape[2] == p->shape[2] && f32(p) && f32(x) && f32(c->outputs()[0]);
+            };
+            auto near_single = [&](std::size_t from, auto&& want) {
+                for (std::size_t b = from; b-- > 0 && from - b <= 8;)
+                    if (!dead[b] && steps[b].fused < 0 && steps[b].nodes.size() == 1 && want(b)) return b;
+                return SIZE_MAX;
+            };
+            if (!seq_append(n)) continue;
+            const auto* past = ins[0];
+            const std::size_t so = near_single(j, [&](std::size_t b) {
+                const auto* c = node_of(b);
+                return c->op().op == Op::Concat && seq_append(c) && c->inputs()[0]->shape[0] == past->shape[0] &&
+                       c->inputs()[0]->shape[1] == past->shape[1];
+            });
+            if (so == SIZE_MAX) continue;
+            // the key append is the one whose new row is an inner RoPE output
+            auto roped = [&](pConstNode c) {
+                const std::size_t r = single(c->inputs()[1], Op::RotaryEmbedding);
+                return (r != SIZE_MAX && inner(c->inputs()[1])) ? r : SIZE_MAX;
+            };
+            const std::size_t r_here = roped(n), r_other = roped(node_of(so));
+            if ((r_here == SIZE_MAX) == (r_other == SIZE_MAX)) continue;
+            const auto* kcat = r_here != SIZE_MAX ? n : node_of(so);
+            const auto* vcat = r_here != SIZE_MAX ? node_of(so) : n;
+            const std::size_t sb = r_here != SIZE_MAX ? r_here : r_other;
+            if (sb > j) continue;
+            const auto* kr = kcat->inputs()[1];
+            const auto* k = node_of(sb)->inputs()[0];
+            const auto* cs = node_of(sb)->inputs()[1];
+            const auto* sn = node_of(sb)->inputs()[2];
+            if (cs->shape.size() != 2 || cs->shape[0] != 1 || sn->shape != cs->shape || k->shape != kr->shape) continue;
+            const std::size_t sa = near_single(j, [&](std::size_t b) {
+                const auto* a = node_of(b);
+                return b != sb && a->op().op == Op::RotaryEmbedding && a->outputs().size() == 1 &&
+                       a->inputs()[1] == cs && a->inputs()[2] == sn;
+            });
+            if (sa == SIZE_MAX) continue;
+            const auto* q = node_of(sa)->inputs()[0];
+            const auto* qr = node_of(sa)->outputs()[0];
+            const auto* kc = kcat->outputs()[0];
+            const auto* vc = vcat->outputs()[0];
+            const dim_t D = k->shape[2];
+            if (q->shape.size() != 3 || q->shape[1] != 1 || q->shape[2] != D || qr->shape != q->shape || D % 2 != 0 ||
+                cs->shape[1] != D / 2 || !f32(q) || !f32(qr) || !f32(cs) || !f32(sn))
+                continue;
+            // q' and the other append's cache are computed at step j: nothing may read them before it
+            const auto* early = r_here != SIZE_MAX ? vc : kc;
+            if (first_use[index.at(qr)] <= j || first_use[index.at(early)] <= j) continue;
+            make(j, FusedKind::RopeAppend, {sa, sb, so},
+                 {q, k, vcat->inputs()[1], kcat->inputs()[0], vcat->inputs()[0], cs, sn}, nullptr, {qr, kc, vc});
             continue;
         }
         if (op == Op::FusedAttention && kernels[static_cast<int>(FusedKind::AttentionGqa)] && ins.size() == 3) {
@@ -471,8 +501,16 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
             dedicated[i] = true;
         }
     }
+    // graph inputs: the tensors no node writes (Graph::is_input_tensor, for
+    // every tensor at once)
+    std::vector<bool> produced(tensors.size(), false);
+    for (const auto& node : graph._nodes)
+        for (auto* out : node.outputs()) {
+            const auto i = index.find(out);
+            if (i != TensorIndex::npos) produced[i] = true;
+        }
     for (std::size_t i = 0; i < tensors.size(); ++i)
-        if (tensors[i]->data != nullptr || graph.is_input_tensor(i)) dedicated[i] = true;
+        if (tensors[i]->data != nullptr || !produced[i]) dedicated[i] = true;
 
     auto steps = plan_steps(order, device, index, tensors.size());
     fuse_steps(steps, device, index, dedicated);

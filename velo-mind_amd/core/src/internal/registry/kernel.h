@@ -69,8 +69,10 @@ enum class FusedKind : int {
                           // outputs [ctx]
     AttentionGqa = 3,     // FusedAttention on RepeatKV(K), RepeatKV(V): inputs [q, K, V]
                           // (before RepeatKV), outputs [o]; attrs the FusedAttention's OpDescriptor
+    RopeAppend = 4,       // one decode position: RoPE(q), Concat(K_past, RoPE(k)), Concat(V_past, v):
+                          // inputs [q, k, v, K_past, V_past, cos, sin], outputs [q', K, V]
 };
-inline constexpr std::size_t kFusedKinds = 4;
+inline constexpr std::size_t kFusedKinds = 5;
 
 auto register_fused_kernel(DeviceType device, FusedKind kind, Executable::KernelFn fn) -> void;
 // nullptr when the device does not run that chain fused

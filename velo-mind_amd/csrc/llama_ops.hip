@@ -61,7 +61,13 @@ __global__ __launch_bounds__(kT) void rmsnorm_kernel(const float* __restrict__ x
 
 // ---- Rotary embedding on rows of head_dim (rotary_embedding.cpp:17-45):
 // the first and second halves rotate by (cos, sin) of position
-// row % cos_rows.
+// row % cos_rows.  One rotation, shared by every kernel that applies it so
+// that they round alike.
+__device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, float* y0, float* y1) {
+    *y0 = a * c - b * s;
+    *y1 = b * c + a * s;
+}
+
 __global__ void rope_kernel(const float* __restrict__ x, const float* __restrict__ cs, const float* __restrict__ sn,
                             float* __restrict__ y, int64_t rows, int64_t head_dim, int64_t cos_rows) {
     const int64_t half = head_dim / 2;
@@ -75,8 +81,46 @@ __global__ void rope_kernel(const float* __restrict__ x, const float* __restrict
         const float b = x[r * head_dim + j + half];
         const float c = cs[pos * half + j];
         const float s = sn[pos * half + j];
-        y[r * head_dim + j] = a * c - b * s;
-        y[r * head_dim + j + half] = b * c + a * s;
+        rope_rotate(a, b, c, s, y + r * head_dim + j, y + r * head_dim + j + half);
+    }
+}
+
+// ---- One decode position's attention inputs in one launch: RoPE on the
+// query [hq, 1, d] and on the new key [hkv, 1, d], each appended to its
+// cache as Concat(past, new) on the sequence axis (llama_graph.cpp:79-84,
+// :296-305), and the new value appended to its cache: q_out [hq, 1, d],
+// k_out [hkv, s + 1, d], v_out [hkv, s + 1, dv].  cos/sin hold one row
+// (the position).  Elements equal the RoPE and Concat kernels' bit for bit.
+__global__ void rope_append_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                   const float* __restrict__ v, const float* __restrict__ pk,
+                                   const float* __restrict__ pv, const float* __restrict__ cs,
+                                   const float* __restrict__ sn, float* __restrict__ q_out, float* __restrict__ k_out,
+                                   float* __restrict__ v_out, int64_t hq, int64_t hkv, int64_t s, int64_t d,
+                                   int64_t dv) {
+    const int64_t half = d / 2;
+    const int64_t n_q = hq * half;               // rotated pairs of the query
+    const int64_t n_kn = hkv * half;             // rotated pairs of the new key
+    const int64_t n_kp = hkv * s * d;            // cached key elements
+    const int64_t n_v = hkv * (s + 1) * dv;      // value cache with the new row
+    const int64_t total = n_q + n_kn + n_kp + n_v;
+    for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < total;
+         e += static_cast<int64_t>(gridDim.x) * kT) {
+        if (e < n_q + n_kn) {
+            const bool is_q = e < n_q;
+            const int64_t p = is_q ? e : e - n_q;
+            const int64_t r = p / half, j = p - r * half;
+            const float* x = is_q ? q + r * d : k + r * d;
+            float* y = is_q ? q_out + r * d : k_out + (r * (s + 1) + s) * d;
+            rope_rotate(x[j], x[j + half], cs[j], sn[j], y + j, y + j + half);
+        } else if (e < n_q + n_kn + n_kp) {
+            const int64_t p = e - n_q - n_kn;
+            const int64_t h = p / (s * d), t = p - h * s * d;
+            k_out[h * (s + 1) * d + t] = pk[p];
+        } else {
+            const int64_t p = e - n_q - n_kn - n_kp;
+            const int64_t h = p / ((s + 1) * dv), t = p - h * (s + 1) * dv;
+            v_out[p] = t < s * dv ? pv[h * s * dv + t] : v[h * dv + (t - s * dv)];
+        }
     }
 }
 
@@ -407,6 +451,19 @@ int vm_hip_rope_f32(const float* x, const float* cos_table, const float* sin_tab
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(rows * head_dim / 2)), dim3(kT), 0, S(stream), x, cos_table,
                        sin_table, y, rows, head_dim, cos_rows);
     return check_launch("RotaryEmbedding", S(stream));
+}
+
+int vm_hip_rope_append_f32(const float* q, const float* k, const float* v, const float* k_past, const float* v_past,
+                           const float* cos_table, const float* sin_table, float* q_out, float* k_out, float* v_out,
+                           int64_t hq, int64_t hkv, int64_t s_past, int64_t d, int64_t dv, void* stream) {
+    clear_error();
+    if (hq < 1 || hkv < 1 || s_past < 0 || d < 2 || d % 2 != 0 || dv < 1) return fail_inval("RopeAppend: bad shape");
+    if (!q || !k || !v || !cos_table || !sin_table || !q_out || !k_out || !v_out || (s_past > 0 && (!k_past || !v_past)))
+        return fail_inval("RopeAppend: null pointer");
+    const int64_t total = hq * (d / 2) + hkv * (d / 2) + hkv * s_past * d + hkv * (s_past + 1) * dv;
+    hipLaunchKernelGGL(rope_append_kernel, dim3(grid_for(total)), dim3(kT), 0, S(stream), q, k, v, k_past, v_past,
+                       cos_table, sin_table, q_out, k_out, v_out, hq, hkv, s_past, d, dv);
+    return check_launch("RopeAppend", S(stream));
 }
 
 int vm_hip_transpose_f32(const float* x, float* y, int rank, const int64_t* in_shape, const int* perm, void* stream) {
