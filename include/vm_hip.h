@@ -183,6 +183,21 @@ int vm_hip_qmm_group_f32(const float* a, int64_t rows_m, int64_t k, const vm_hip
                          int count, int quant_type, int block_size, void* stream);
 
 /*
+ * vm_hip_qmm_group_f32 on RMSNorm(A): each row of A [rows_m, k] is first
+ * normalized as RMSNorm over its k values with weight norm_w [k] and
+ * epsilon eps (src/cpu/ops/rmsnorm.cpp:17-60; the same arithmetic as
+ * vm_hip_rmsnorm_f32, bit for bit), then multiplied by every member.  The
+ * reference LLaMA layer's RMSNorm feeding q | k | v and gate | up
+ * (llama_graph.cpp:53-56, :125-136); the graph compiler on DeviceType::HIP
+ * fuses the pair.  rows_m <= 4: one GEMV launch that normalizes while it
+ * stages A; otherwise the normalized rows go to a per-stream buffer first.
+ * No counterpart in the reference.
+ */
+int vm_hip_qmm_norm_group_f32(const float* a, const float* norm_w, float eps, int64_t rows_m,
+                              int64_t k, const vm_hip_qmm_member* members, int count,
+                              int quant_type, int block_size, void* stream);
+
+/*
  * vm_hip_qmm_f32 without any device allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -97,6 +97,21 @@ void concat_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const 
     }
 }
 
+// RMSNorm over the last axis
+void rmsnorm_rows(const float* x, const float* w, float* y, std::size_t rows, std::size_t d, float eps) {
+    for (std::size_t r = 0; r < rows; ++r) {
+        float ss = 0.0f;
+        for (std::size_t i = 0; i < d; ++i) ss = std::fma(x[r * d + i], x[r * d + i], ss);
+        const float inv = 1.0f / std::sqrt(ss / static_cast<float>(d) + eps);
+        for (std::size_t i = 0; i < d; ++i) y[r * d + i] = (x[r * d + i] * inv) * w[i];
+    }
+}
+void rmsnorm_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const float eps = std::get<RMSNormAttrs>(static_cast<const OpDescriptor*>(attrs)->attrs).epsilon;
+    const std::size_t d = static_cast<std::size_t>(in[0]->shape.back());
+    rmsnorm_rows(cin(in, 0), cin(in, 1), cout0(out), numel(*in[0]) / d, d, eps);
+}
+
 // fused: the same operations in the same order as the chains above
 void silu_mul_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
     for (std::size_t e = 0; e < numel(*out[0]); ++e) {
@@ -152,6 +167,19 @@ void rope_append_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* 
     concat_cpu(cv, out + 2, nullptr);
 }
 
+// inputs [x, w, B_1, S_1, ..], outputs [C_1, ..]
+void norm_qmm_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const auto& na = *static_cast<const internal::NormQmmAttrs*>(attrs);
+    const auto& qa = std::get<QuantizedMatMulAttrs>(na.desc.attrs);
+    const std::size_t k = static_cast<std::size_t>(in[0]->shape.back()), rows = numel(*in[0]) / k;
+    std::vector<float> hn(rows * k);
+    rmsnorm_rows(cin(in, 0), cin(in, 1), hn.data(), rows, k, na.epsilon);
+    for (std::size_t g = 0; g < na.members; ++g)
+        vmo_qmm_2d_f32(hn.data(), static_cast<const std::int8_t*>(in[2 + 2 * g]->data), cin(in, 3 + 2 * g),
+                       static_cast<float*>(out[g]->data), rows, k, static_cast<std::size_t>(in[2 + 2 * g]->shape[1]),
+                       static_cast<int>(qa.quant_type), qa.block_size);
+}
+
 constexpr DataType F32 = DataType::Float32;
 #define CPU_F32(OP, N, FN) \
     VELOMIND_REGISTER_OP_KERNEL(DeviceType::CPU, OP, (internal::KernelDtypeKey{{F32, F32, F32, F32}, N, F32}), &FN)
@@ -164,10 +192,12 @@ CPU_F32(Op::Transpose, 1, transpose_cpu)
 CPU_F32(Op::RepeatKV, 1, repeat_kv_cpu)
 CPU_F32(Op::RotaryEmbedding, 3, rope_cpu)
 CPU_F32(Op::Concat, 2, concat_cpu)
+CPU_F32(Op::RMSNorm, 2, rmsnorm_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::SiluMul, &silu_mul_fused_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::QmmAdd, &qmm_add_fused_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::AttentionDecode, &attention_decode_fused_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::RopeAppend, &rope_append_fused_cpu)
+VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::NormQmm, &norm_qmm_fused_cpu)
 
 struct QmmWeights {
     std::vector<std::int8_t> q;
@@ -359,4 +389,53 @@ TEST_CASE("fusion: RoPE on q and k with the KV appends run as one step", "[core]
     const auto kept = run_layer_attention(true, true);
     REQUIRE(kept.steps == 2);
     REQUIRE(std::memcmp(kept.ctx.data(), off.ctx.data(), off.ctx.size() * 4) == 0);
+}
+
+namespace {
+// y = QMM(RMSNorm(x)); with `second`, another QMM reads the norm too.
+struct NormRun {
+    std::vector<float> y;
+    std::size_t steps = 0;
+};
+NormRun run_norm_qmm(bool fuse, bool second) {
+    const std::size_t d = 64, n = 48;
+    static const auto w1 = int8_weights(d, n, 91), w2 = int8_weights(d, n, 92);
+    static const auto x = normal(2 * d, 93), nw = normal(d, 94);
+    ScopedEnv env("VELOMIND_GRAPH_FUSE", fuse ? "1" : "0");
+    Graph g;
+    auto tx = g.input({2, (dim_t)d}, F32), tw = g.input({(dim_t)d}, F32);
+    auto b1 = g.input({(dim_t)d, (dim_t)n}, DataType::Int8), s1 = g.input({(dim_t)n}, F32);
+    auto b2 = g.input({(dim_t)d, (dim_t)n}, DataType::Int8), s2 = g.input({(dim_t)n}, F32);
+    auto hn = g.op(OpDescriptor{Op::RMSNorm, RMSNormAttrs{1e-5f, -1}}, tx, tw);
+    auto y = g.op(Op::QuantizedMatMul, hn, b1, s1);
+    g.mark_output(y);
+    if (second) g.mark_output(g.op(Op::QuantizedMatMul, hn, b2, s2));
+    auto exec = g.build(DeviceType::CPU);
+    NormRun r;
+    r.steps = exec->num_steps();
+    tx.copy_from_host(as_bytes(x));
+    tw.copy_from_host(as_bytes(nw));
+    b1.copy_from_host(as_bytes(w1.q));
+    s1.copy_from_host(as_bytes(w1.s));
+    if (second) {
+        b2.copy_from_host(as_bytes(w2.q));
+        s2.copy_from_host(as_bytes(w2.s));
+    }
+    exec->execute();
+    r.y.resize(2 * n);
+    y.copy_to_host(as_writeable_bytes(r.y));
+    return r;
+}
+}  // namespace
+
+TEST_CASE("fusion: RMSNorm read only by a QuantizedMatMul step runs inside it", "[core][fusion]") {
+    const auto off = run_norm_qmm(false, false);
+    const auto on = run_norm_qmm(true, false);
+    REQUIRE(off.steps == 2);
+    REQUIRE(on.steps == 1);
+    REQUIRE(std::memcmp(on.y.data(), off.y.data(), on.y.size() * 4) == 0);
+    // read by two separate steps (no group kernel here): the norm stays its own step
+    const auto two = run_norm_qmm(true, true);
+    REQUIRE(two.steps == 3);
+    REQUIRE(std::memcmp(two.y.data(), off.y.data(), off.y.size() * 4) == 0);
 }

@@ -4,7 +4,8 @@ fuse_steps, kernel.h FusedKind).
 Each fused kernel is compared with the chain of single-operator launches it
 replaces, bit for bit, through the C ABI: the decode attention chain
 (RepeatKV, Transpose, MatMul, Softmax, MatMul), QuantizedMatMul followed by
-its residual Add, and the SwiGLU Mul(Mul(Sigmoid(g), g), u).  Then the graph
+its residual Add, RMSNorm feeding sibling QuantizedMatMuls, RoPE with the
+KV-cache appends, and the SwiGLU Mul(Mul(Sigmoid(g), g), u).  Then the graph
 engine (the reference engine's loop, a Graph per call) decodes with fusion
 on (the default) and with VELOMIND_GRAPH_FUSE=0, and the logits must be
 identical, for both attention forms of the reference layer and every
@@ -92,6 +93,66 @@ def test_qmm_add_matches_qmm_then_add(hip, m, k, n, qt, blk):
         x = out.download(np.float32, (m, n))
         y = ref.download(np.float32, (m, n))
         assert x.tobytes() == y.tobytes(), f"max diff {np.abs(x - y).max():.3e}"
+
+
+@pytest.mark.parametrize("m,k,ns,qt,blk", [
+    (1, 960, (960, 320, 320), 1, 0), (1, 2048, (2048, 256, 256), 2, 32), (2, 2048, (5632, 5632), 2, 32),
+    (3, 576, (1536,), 1, 0), (4, 960, (2560, 2560), 1, 32), (1, 5632, (2048,), 2, 32),
+    (8, 960, (960, 320), 1, 0), (1, 64, (40, 48), 2, 32)])
+def test_norm_group_matches_rmsnorm_then_group(hip, m, k, ns, qt, blk):
+    H = hip
+    lib = H.open_library()
+    print(f"case norm group m={m} k={k} ns={ns} qt={qt} blk={blk}", flush=True)
+    rng = np.random.default_rng(m * 131 + k + len(ns))
+    rows = (k + 1) // 2 if qt == 2 else k
+    nb = (k + blk - 1) // blk if blk > 0 else 1
+    a = (rng.standard_normal((m, k), dtype=np.float32) * 3).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(k, dtype=np.float32)).astype(np.float32)
+    da, dnw = _dev(H, a), _dev(H, nw)
+    hn = H.DeviceBuffer(m * k * 4)
+    keep, ref_m, out_m = [], (H.QmmMember * len(ns))(), (H.QmmMember * len(ns))()
+    for g, n in enumerate(ns):
+        codes = _dev(H, rng.integers(-128, 128, size=(rows, n), dtype=np.int8))
+        scales = _dev(H, (rng.random((nb, n), dtype=np.float32) * 0.02).astype(np.float32))
+        ref, out = H.DeviceBuffer(m * n * 4), H.DeviceBuffer(m * n * 4)
+        keep += [codes, scales, ref, out]
+        ref_m[g] = H.QmmMember(codes.addr, scales.addr, ref.addr, n)
+        out_m[g] = H.QmmMember(codes.addr, scales.addr, out.addr, n)
+    eps = 1e-5
+    for _ in range(2):
+        H.check(lib.vm_hip_rmsnorm_f32(da.ptr, dnw.ptr, hn.ptr, m, k, ctypes.c_float(eps), None))
+        H.check(lib.vm_hip_qmm_group_f32(hn.ptr, m, k, ref_m, len(ns), qt, blk, None))
+        H.check(lib.vm_hip_qmm_norm_group_f32(da.ptr, dnw.ptr, ctypes.c_float(eps), m, k, out_m, len(ns), qt, blk,
+                                              None))
+        H.synchronize()
+        for g, n in enumerate(ns):
+            x = keep[4 * g + 3].download(np.float32, (m, n))
+            y = keep[4 * g + 2].download(np.float32, (m, n))
+            assert np.all(np.isfinite(y))
+            assert x.tobytes() == y.tobytes(), f"member {g}: max diff {np.abs(x - y).max():.3e}"
+
+
+@pytest.mark.parametrize("hq,hkv,s,d", [(15, 5, 128, 64), (32, 4, 767, 64), (4, 4, 1, 16), (6, 2, 9, 8)])
+def test_rope_append_matches_rope_and_concat(hip, hq, hkv, s, d):
+    H = hip
+    lib = H.open_library()
+    print(f"case rope append hq={hq} hkv={hkv} s={s} d={d}", flush=True)
+    rng = np.random.default_rng(s + d)
+    arrs = [rng.standard_normal(sh, dtype=np.float32) for sh in
+            ((hq, 1, d), (hkv, 1, d), (hkv, 1, d), (hkv, s, d), (hkv, s, d), (1, d // 2), (1, d // 2))]
+    q, k, v, pk, pv, cs, sn = (_dev(H, x) for x in arrs)
+    qr, kr = H.DeviceBuffer(hq * d * 4), H.DeviceBuffer(hkv * d * 4)
+    kc, vc = H.DeviceBuffer(hkv * (s + 1) * d * 4), H.DeviceBuffer(hkv * (s + 1) * d * 4)
+    fq, fk, fv = H.DeviceBuffer(hq * d * 4), H.DeviceBuffer(hkv * (s + 1) * d * 4), H.DeviceBuffer(hkv * (s + 1) * d * 4)
+    H.check(lib.vm_hip_rope_f32(q.ptr, cs.ptr, sn.ptr, qr.ptr, hq, d, 1, None))
+    H.check(lib.vm_hip_rope_f32(k.ptr, cs.ptr, sn.ptr, kr.ptr, hkv, d, 1, None))
+    H.check(lib.vm_hip_concat_f32(pk.ptr, kr.ptr, kc.ptr, hkv, s * d, d, None))
+    H.check(lib.vm_hip_concat_f32(pv.ptr, v.ptr, vc.ptr, hkv, s * d, d, None))
+    H.check(lib.vm_hip_rope_append_f32(q.ptr, k.ptr, v.ptr, pk.ptr, pv.ptr, cs.ptr, sn.ptr, fq.ptr, fk.ptr, fv.ptr,
+                                       hq, hkv, s, d, d, None))
+    H.synchronize()
+    for got, ref, size in ((fq, qr, hq * d), (fk, kc, hkv * (s + 1) * d), (fv, vc, hkv * (s + 1) * d)):
+        assert got.download(np.float32, (size,)).tobytes() == ref.download(np.float32, (size,)).tobytes()
 
 
 def test_silu_mul_matches_sigmoid_mul_mul(hip):

@@ -153,9 +153,58 @@ void quantized_matmul_group_hip(const pConstTensorStorage* in, const pTensorStor
     }
 }
 
+// RMSNorm feeding QuantizedMatMul(s), fused by the graph compiler: inputs
+// [x, w, B_1, S_1, .., B_g, S_g], outputs [C_1, .., C_g], attrs a
+// NormQmmAttrs.  Each member is checked as a single node is.
+void quantized_matmul_norm_group_hip(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const auto& na = *static_cast<const internal::NormQmmAttrs*>(attrs);
+    const auto& qa = std::get<QuantizedMatMulAttrs>(na.desc.attrs);
+    const auto* x = in[0];
+    const auto* nw = in[1];
+    if (!x || !nw || na.members < 1 || na.members > VM_HIP_QMM_GROUP_MAX)
+        throw std::runtime_error("quantized_matmul norm group hip: bad group");
+    if (!x->is_contiguous() || !nw->is_contiguous())
+        throw std::invalid_argument(error_context(Op::RMSNorm, *out[0], "launch") +
+                                    ": strided operands are not supported on HIP");
+    const std::int64_t k = x->shape.back();
+    std::int64_t rows = 1;
+    for (std::size_t i = 0; i + 1 < x->shape.size(); ++i) rows *= x->shape[i];
+    const int qt = qa.quant_type == QuantType::Int4 ? VM_HIP_QUANT_INT4 : VM_HIP_QUANT_INT8;
+    const std::int64_t bs = (qt == VM_HIP_QUANT_INT4 && qa.block_size <= 0) ? 32 : qa.block_size;
+    const std::int64_t nblk = bs > 0 ? (k + bs - 1) / bs : 1;
+    vm_hip_qmm_member members[VM_HIP_QMM_GROUP_MAX];
+    for (std::size_t g = 0; g < na.members; ++g) {
+        const auto* w = in[2 + 2 * g];
+        const auto* s = in[3 + 2 * g];
+        auto* c = out[g];
+        if (!w || !s || !c) throw std::runtime_error("quantized_matmul norm group hip: null storage");
+        if (!w->is_contiguous() || !s->is_contiguous() || !c->is_contiguous())
+            throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") +
+                                        ": strided operands are not supported on HIP");
+        const std::int64_t n = w->shape[1];
+        const std::uint64_t need_scales = static_cast<std::uint64_t>(k > 0 ? nblk : 0) * static_cast<std::uint64_t>(n);
+        if (storage_numel(*s) < need_scales)
+            throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") + ": scales hold " +
+                                        std::to_string(storage_numel(*s)) + " values, the kernel reads " +
+                                        std::to_string(need_scales));
+        members[g] = vm_hip_qmm_member{static_cast<const std::int8_t*>(w->data), static_cast<const float*>(s->data),
+                                       static_cast<float*>(c->data), n};
+    }
+    const int status = vm_hip_qmm_norm_group_f32(static_cast<const float*>(x->data), static_cast<const float*>(nw->data),
+                                                 na.epsilon, rows, k, members, static_cast<int>(na.members), qt,
+                                                 qa.block_size, current_stream());
+    if (status != VM_HIP_OK) {
+        const std::string last = vm_hip_last_error();
+        const char* stage = last.find(" at sync") != std::string::npos ? "sync" : "launch";
+        throw_status(status, error_context(Op::QuantizedMatMul, *out[0], stage));
+    }
+}
+
 }  // namespace
 
 VELOMIND_REGISTER_QMM_GROUP(::velomind::DeviceType::HIP, quantized_matmul_group_hip)
+VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, ::velomind::internal::FusedKind::NormQmm,
+                        &quantized_matmul_norm_group_hip)
 VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, ::velomind::internal::FusedKind::QmmAdd,
                         &quantized_matmul_add_hip)
 

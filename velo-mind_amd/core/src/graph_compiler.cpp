@@ -125,8 +125,12 @@ struct Step {
     int fused = -1;                           // FusedKind, or -1
     std::vector<pConstTensorStorage> ins;     // fused: the chain's external operands
     std::vector<pConstTensorStorage> outs;
-    const OpDescriptor* desc = nullptr;       // fused: descriptor the kernel takes, if any
+    std::shared_ptr<const void> attrs;        // fused: what the kernel takes as attrs, if anything
 };
+
+std::shared_ptr<const void> desc_copy(const OpDescriptor& d) {
+    return std::shared_ptr<const void>(new OpDescriptor(d), [](const void* p) { delete static_cast<const OpDescriptor*>(p); });
+}
 
 const QuantizedMatMulAttrs* qmm_attrs(pConstNode n) {
     if (n->op().op != Op::QuantizedMatMul) return nullptr;
@@ -215,6 +219,8 @@ std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType de
 //                    Transpose swapping the last two axes, the Softmax on the
 //                    last one (RepeatKV absent when H == Hkv)
 //   AttentionGqa     o = FusedAttention(q, RepeatKV(K), RepeatKV(V))
+//   NormQmm          C_g = QuantizedMatMul(RMSNorm(x, w), ..) for the members of one step
+//                    (a single node or a sibling group) that are the norm's only readers
 //   RopeAppend       q' = RoPE(q), K = Concat(K_past, RoPE(k)), V = Concat(V_past, v)
 //                    at one position (new rows [., 1, .], one cos/sin row), the
 //                    four nodes within a few steps of each other and q', K read
@@ -272,7 +278,7 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
         return node_of(s)->inputs()[0];
     };
     auto make = [&](std::size_t at, FusedKind kind, std::vector<std::size_t> absorbed,
-                    std::vector<pConstTensorStorage> ins, const OpDescriptor* desc,
+                    std::vector<pConstTensorStorage> ins, std::shared_ptr<const void> attrs,
                     std::vector<pConstTensorStorage> outs = {}) {
         Step f;
         std::sort(absorbed.begin(), absorbed.end());
@@ -284,12 +290,50 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
         f.fused = static_cast<int>(kind);
         f.ins = std::move(ins);
         f.outs = outs.empty() ? std::vector<pConstTensorStorage>{node_of(at)->outputs()[0]} : std::move(outs);
-        f.desc = desc;
+        f.attrs = std::move(attrs);
         steps[at] = std::move(f);
     };
 
+    // RMSNorm read only by the QuantizedMatMul(s) of step j: NormQmm
+    auto norm_qmm = [&](std::size_t j) {
+        const auto& members = steps[j].nodes;
+        if (!kernels[static_cast<int>(FusedKind::NormQmm)] || !qmm_groupable(members.front())) return false;
+        const auto* hn = members.front()->inputs()[0];
+        const std::size_t sr = single(hn, Op::RMSNorm);
+        if (sr == SIZE_MAX) return false;
+        const std::size_t i = index.at(hn);
+        if (kept[i] || consumers[i] != members.size()) return false;
+        const auto* norm = node_of(sr);
+        const auto* na = std::get_if<RMSNormAttrs>(&norm->op().attrs);
+        const auto* x = norm->inputs()[0];
+        const auto* w = norm->inputs()[1];
+        const dim_t k = hn->shape.back();
+        if (!na || !(na->axis == -1 || na->axis == static_cast<int>(hn->shape.size()) - 1) || x->shape != hn->shape ||
+            w->shape != shape_t{k} || !f32(x) || !f32(w))
+            return false;
+        Step f;
+        f.nodes.push_back(norm);
+        f.ins = {x, w};
+        for (auto* mnode : members) {
+            f.nodes.push_back(mnode);
+            f.ins.push_back(mnode->inputs()[1]);
+            f.ins.push_back(mnode->inputs()[2]);
+            f.outs.push_back(mnode->outputs()[0]);
+        }
+        f.fused = static_cast<int>(FusedKind::NormQmm);
+        auto* a = new NormQmmAttrs{members.front()->op(), members.size(), na->epsilon};
+        f.attrs = std::shared_ptr<const void>(a, [](const void* p) { delete static_cast<const NormQmmAttrs*>(p); });
+        dead[sr] = true;
+        steps[j] = std::move(f);
+        return true;
+    };
+
     for (std::size_t j = 0; j < steps.size(); ++j) {
-        if (dead[j] || steps[j].fused >= 0 || steps[j].nodes.size() != 1) continue;
+        if (dead[j] || steps[j].fused >= 0) continue;
+        if (steps[j].nodes.size() > 1) {   // a sibling QuantizedMatMul group
+            norm_qmm(j);
+            continue;
+        }
         const auto* n = node_of(j);
         const auto ins = n->inputs();
         if (n->outputs().size() != 1) continue;
@@ -326,9 +370,13 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
                 if (sq == SIZE_MAX || !inner(y) || !qmm_groupable(node_of(sq))) continue;
                 if (!f32(h) || !f32(out) || h->shape != y->shape || out->shape != y->shape) continue;
                 const auto q = node_of(sq)->inputs();
-                make(j, FusedKind::QmmAdd, {sq}, {q[0], q[1], q[2], h}, &node_of(sq)->op());
+                make(j, FusedKind::QmmAdd, {sq}, {q[0], q[1], q[2], h}, desc_copy(node_of(sq)->op()));
                 break;
             }
+            continue;
+        }
+        if (op == Op::QuantizedMatMul) {
+            norm_qmm(j);
             continue;
         }
         if (op == Op::MatMul && kernels[static_cast<int>(FusedKind::AttentionDecode)] && ins.size() == 2) {
@@ -424,7 +472,7 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
             const auto* k = unrepeat(ins[1], absorbed);
             const auto* v = unrepeat(ins[2], absorbed);
             if (absorbed.size() != 2 || k->shape[0] != v->shape[0]) continue;
-            make(j, FusedKind::AttentionGqa, absorbed, {ins[0], k, v}, &n->op());
+            make(j, FusedKind::AttentionGqa, absorbed, {ins[0], k, v}, desc_copy(n->op()));
             continue;
         }
     }
@@ -677,10 +725,7 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
             for (auto* in : step.ins) cn.inputs.push_back(remap(in));
             for (auto* out : step.outs) cn.outputs.push_back(remap(out));
             cn.kernel = fused_kernel(device, static_cast<FusedKind>(step.fused));
-            if (step.desc)
-                cn.attrs = std::shared_ptr<const void>(new OpDescriptor(*step.desc), [](const void* p) {
-                    delete static_cast<const OpDescriptor*>(p);
-                });
+            cn.attrs = step.attrs;
             cn.fused = step.nodes.size();
             impl->topo.push_back(std::move(cn));
             continue;

@@ -71,8 +71,16 @@ enum class FusedKind : int {
                           // (before RepeatKV), outputs [o]; attrs the FusedAttention's OpDescriptor
     RopeAppend = 4,       // one decode position: RoPE(q), Concat(K_past, RoPE(k)), Concat(V_past, v):
                           // inputs [q, k, v, K_past, V_past, cos, sin], outputs [q', K, V]
+    NormQmm = 5,          // QuantizedMatMul(s) of RMSNorm(x, w): inputs [x, w, B_1, S_1, ..],
+                          // outputs [C_1, ..]; attrs a NormQmmAttrs
 };
-inline constexpr std::size_t kFusedKinds = 5;
+inline constexpr std::size_t kFusedKinds = 6;
+
+struct NormQmmAttrs {
+    OpDescriptor desc;          // the QuantizedMatMuls' common descriptor
+    std::size_t members = 0;    // 1 .. kMaxQmmGroup
+    float epsilon = 0.0f;       // the RMSNorm's
+};
 
 auto register_fused_kernel(DeviceType device, FusedKind kind, Executable::KernelFn fn) -> void;
 // nullptr when the device does not run that chain fused

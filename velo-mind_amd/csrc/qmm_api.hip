@@ -233,9 +233,16 @@ int vm_hip_qmm_staged_f32(const void* a_staged, const int8_t* wq, const float* s
                                static_cast<int>(k), static_cast<int>(n), bs, static_cast<hipStream_t>(stream));
 }
 
-int vm_hip_qmm_group_f32(const float* a, int64_t rows_m, int64_t k, const vm_hip_qmm_member* members, int count,
-                         int quant_type, int block_size, void* stream) {
-    clear_error();
+}  // extern "C"
+
+namespace {
+
+// Sibling quantized matmuls sharing A, optionally RMS-normalizing A first
+// (norm_w non-null): one GEMV launch for rows_m <= 4 where it covers every
+// member; otherwise the normalized rows go to the stream's staging buffer
+// (the separate RMSNorm kernel) and each member runs on its own.
+int qmm_group_impl(const float* a, const float* norm_w, float norm_eps, int64_t rows_m, int64_t k,
+                   const vm_hip_qmm_member* members, int count, int quant_type, int block_size, void* stream) {
     if (!members || count < 1 || count > VM_HIP_QMM_GROUP_MAX)
         return fail_inval("QuantizedMatMul group: 1 to VM_HIP_QMM_GROUP_MAX members");
     for (int g = 0; g < count; ++g)
@@ -258,16 +265,41 @@ int vm_hip_qmm_group_f32(const float* a, int64_t rows_m, int64_t k, const vm_hip
             n[g] = static_cast<int>(members[g].n);
         }
         const int rc = gemv_qmm_group_f32(a, wq, sc, c, n, count, static_cast<int>(rows_m), static_cast<int>(k),
-                                          quant_type, bs, s);
+                                          quant_type, bs, s, norm_w, norm_eps);
         if (rc != VM_HIP_EUNSUPPORTED) return rc;
         clear_error();
+    }
+    const float* x = a;
+    if (norm_w && rows_m > 0 && k > 0) {
+        void* staged = nullptr;
+        VM_TRY(get_staging(s, static_cast<std::size_t>(rows_m) * static_cast<std::size_t>(k) * sizeof(float), &staged));
+        VM_TRY(vm_hip_rmsnorm_f32(a, norm_w, static_cast<float*>(staged), rows_m, k, norm_eps, stream));
+        x = static_cast<const float*>(staged);
     }
     // one launch per member (prefill rows, or a member the grouped GEMV
     // does not cover)
     for (int g = 0; g < count; ++g)
-        VM_TRY(qmm_f32_impl(a, members[g].codes, members[g].scales, members[g].c, rows_m, k, members[g].n, quant_type,
+        VM_TRY(qmm_f32_impl(x, members[g].codes, members[g].scales, members[g].c, rows_m, k, members[g].n, quant_type,
                             block_size, s));
     return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vm_hip_qmm_group_f32(const float* a, int64_t rows_m, int64_t k, const vm_hip_qmm_member* members, int count,
+                         int quant_type, int block_size, void* stream) {
+    clear_error();
+    return qmm_group_impl(a, nullptr, 0.0f, rows_m, k, members, count, quant_type, block_size, stream);
+}
+
+int vm_hip_qmm_norm_group_f32(const float* a, const float* norm_w, float eps, int64_t rows_m, int64_t k,
+                              const vm_hip_qmm_member* members, int count, int quant_type, int block_size,
+                              void* stream) {
+    clear_error();
+    if (!norm_w && rows_m > 0 && k > 0) return fail_inval("QuantizedMatMul group: null RMSNorm weight");
+    return qmm_group_impl(a, norm_w, eps, rows_m, k, members, count, quant_type, block_size, stream);
 }
 
 int vm_hip_qmm(const void* a, int a_dtype, const int8_t* wq, const void* scale, int scale_dtype,

@@ -152,7 +152,7 @@ template <int KIND, int MR, int L, int W, bool GROUPED>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const GemvMembers mb, int m, int k, int block_size, int chunks_per_split,
     uint32_t a_bytes, int a_vec, int blk_shift, unsigned long long* __restrict__ pairs,
-    const float* __restrict__ addend) {
+    const float* __restrict__ addend, const float* __restrict__ norm_w, float norm_eps) {
     VM_GEMV_MARKS;
     VM_GEMV_MARK(0);
     using CS = ChunkShape<KIND>;
@@ -373,6 +373,45 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         }
     }
     __syncthreads();
+
+    // RMSNorm of each activation row before the product (norm_w non-null):
+    // the row's sum of squares over all k with rmsnorm_kernel's arithmetic
+    // (256 threads striding the row with an fma chain, xor butterflies, the
+    // four waves' sums in order), then the staged slice scaled as that
+    // kernel scales it, (x * inv) * w.  Bit for bit the separate RMSNorm.
+    if (norm_w) {
+        __shared__ float norm_part[MR][4];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            if (r >= m) break;
+            float sq = 0.0f;
+            if (threadIdx.x < 256)
+                for (int i = threadIdx.x; i < k; i += 256) {
+                    const float v = a[static_cast<int64_t>(r) * k + i];
+                    sq = fmaf(v, v, sq);
+                }
+            for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+            if (threadIdx.x < 256 && lane == 0) norm_part[r][wave] = sq;
+        }
+        __syncthreads();
+        float inv[MR];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            float tot = 0.0f;
+            if (r < m)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) tot += norm_part[r][w];
+            inv[r] = 1.0f / sqrtf(tot / static_cast<float>(k) + norm_eps);
+        }
+        for (int e = threadIdx.x; e < MR * xs_len; e += W * 64) {
+            int r = 0;
+#pragma unroll
+            for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
+            const int kk = k_begin + (e - r * xs_len);
+            if (r < m && kk < k) xs[e] = (xs[e] * inv[r]) * norm_w[kk];
+        }
+        __syncthreads();
+    }
     VM_GEMV_MARK(2);
 
     float total[MR][kVec];
@@ -679,9 +718,15 @@ struct Member {
     const float* addend = nullptr;  // [m, n] added to C (a launch of one matrix only)
 };
 
+// RMSNorm applied to A before the product (GemvNorm::w non-null).
+struct GemvNorm {
+    const float* w = nullptr;
+    float eps = 0.0f;
+};
+
 template <int KIND, int MR, int L, int W>
 int launch_cfg(const float* a, const Member* members, int count, int m, int k, int block_size,
-               const GemvConfig& cfg, hipStream_t stream) {
+               const GemvConfig& cfg, const GemvNorm& norm, hipStream_t stream) {
     const int64_t byte_rows = KIND == 2 ? (static_cast<int64_t>(k) + 1) / 2 : k;
     const int64_t nblk = KIND == 0 ? 1 : (static_cast<int64_t>(k) + block_size - 1) / block_size;
     GemvMembers mb{};
@@ -718,22 +763,22 @@ int launch_cfg(const float* a, const Member* members, int count, int m, int k, i
     if (count == 1)
         hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, false>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
                            stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs,
-                           members[0].addend);
+                           members[0].addend, norm.w, norm.eps);
     else
         hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, true>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
                            stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs,
-                           nullptr);
+                           nullptr, norm.w, norm.eps);
     return check_launch("QuantizedMatMul", stream);
 }
 
 template <int KIND, int MR>
 int launch_mr(const float* a, const Member* members, int count, int m, int k, int n_total, int block_size,
-              hipStream_t stream) {
+              const GemvNorm& norm, hipStream_t stream) {
     const GemvConfig cfg = choose_config(KIND, m, k, n_total);
 #define VM_GEMV_CASE(LL, WW)                                                                    \
     if constexpr (WW <= max_waves(KIND, MR))                                                    \
         if (cfg.L == LL && cfg.W == WW)                                                         \
-            return launch_cfg<KIND, MR, LL, WW>(a, members, count, m, k, block_size, cfg, stream);
+            return launch_cfg<KIND, MR, LL, WW>(a, members, count, m, k, block_size, cfg, norm, stream);
     VM_GEMV_CASE(1, 4)
     VM_GEMV_CASE(2, 4)
     VM_GEMV_CASE(2, 8)
@@ -750,16 +795,16 @@ int launch_mr(const float* a, const Member* members, int count, int m, int k, in
 
 template <int KIND>
 int launch_kind(const float* a, const Member* members, int count, int m, int k, int n_total, int block_size,
-                hipStream_t stream) {
-    if (m == 1) return launch_mr<KIND, 1>(a, members, count, m, k, n_total, block_size, stream);
-    if (m == 2) return launch_mr<KIND, 2>(a, members, count, m, k, n_total, block_size, stream);
-    return launch_mr<KIND, 4>(a, members, count, m, k, n_total, block_size, stream);
+                const GemvNorm& norm, hipStream_t stream) {
+    if (m == 1) return launch_mr<KIND, 1>(a, members, count, m, k, n_total, block_size, norm, stream);
+    if (m == 2) return launch_mr<KIND, 2>(a, members, count, m, k, n_total, block_size, norm, stream);
+    return launch_mr<KIND, 4>(a, members, count, m, k, n_total, block_size, norm, stream);
 }
 
 // One launch for `count` matrices sharing the activations; VM_HIP_EUNSUPPORTED
 // when any member needs another kernel.
 int gemv_group_f32(const float* a, const Member* members, int count, int m, int k, int quant_type,
-                   int block_size, hipStream_t stream) {
+                   int block_size, const GemvNorm& norm, hipStream_t stream) {
     if (m < 1 || m > 4 || count < 1 || count > kMaxMembers) return VM_HIP_EUNSUPPORTED;
     int64_t n_total = 0;
     for (int g = 0; g < count; ++g) {
@@ -776,13 +821,13 @@ int gemv_group_f32(const float* a, const Member* members, int count, int m, int 
     const int nt = static_cast<int>(n_total);
     if (quant_type == VM_HIP_QUANT_INT4) {
         if (block_size <= 0 || block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
-        return launch_kind<2>(a, members, count, m, k, nt, block_size, stream);
+        return launch_kind<2>(a, members, count, m, k, nt, block_size, norm, stream);
     }
     if (block_size > 0) {
         if (block_size % kChunkK != 0) return VM_HIP_EUNSUPPORTED;
-        return launch_kind<1>(a, members, count, m, k, nt, block_size, stream);
+        return launch_kind<1>(a, members, count, m, k, nt, block_size, norm, stream);
     }
-    return launch_kind<0>(a, members, count, m, k, nt, 0, stream);
+    return launch_kind<0>(a, members, count, m, k, nt, 0, norm, stream);
 }
 
 }  // namespace
@@ -790,15 +835,16 @@ int gemv_group_f32(const float* a, const Member* members, int count, int m, int 
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                  int n, int quant_type, int block_size, hipStream_t stream, const float* addend) {
     const Member one{wq, scale, c, n, addend};
-    return gemv_group_f32(a, &one, 1, m, k, quant_type, block_size, stream);
+    return gemv_group_f32(a, &one, 1, m, k, quant_type, block_size, GemvNorm{}, stream);
 }
 
 int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* const* scale, float* const* c,
-                       const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream) {
+                       const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream,
+                       const float* norm_w, float norm_eps) {
     if (count < 1 || count > kMaxMembers) return VM_HIP_EUNSUPPORTED;
     Member members[kMaxMembers];
     for (int g = 0; g < count; ++g) members[g] = Member{wq[g], scale[g], c[g], n[g]};
-    return gemv_group_f32(a, members, count, m, k, quant_type, block_size, stream);
+    return gemv_group_f32(a, members, count, m, k, quant_type, block_size, GemvNorm{norm_w, norm_eps}, stream);
 }
 
 }  // namespace vmhip

@@ -17,8 +17,11 @@ int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c
 // The same GEMV for `count` (<= 4) matrices sharing the activations, in one
 // launch (qmm_gemv.hip); VM_HIP_EUNSUPPORTED when a member needs another
 // kernel.
+// With a non-null norm_w, each row of A is first RMS-normalized (the
+// separate RMSNorm kernel's arithmetic, bit for bit): C_g = RMSNorm(A) x W_g.
 int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* const* scale, float* const* c,
-                       const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream);
+                       const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream,
+                       const float* norm_w = nullptr, float norm_eps = 0.0f);
 
 // Prefill-shaped MFMA GEMM for m > 4 rows (qmm_gemm.hip).
 int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
