@@ -157,6 +157,21 @@ int vm_hip_qmm_add_f32(const float* a, const int8_t* wq, const float* scale, con
                        int block_size, void* stream);
 
 /*
+ * C = addend + SwiGLU(gate, up) x W: the reference LLaMA MLP's
+ * Mul(Mul(Sigmoid(gate), gate), up) (llama_graph.cpp:136) as the
+ * activations of a QuantizedMatMul, and the residual Add after it
+ * (:139); addend may be NULL (no Add).  Each activation is rounded as
+ * vm_hip_elementwise_f32's VM_HIP_EW_SILU_MUL rounds it, so C equals the
+ * separate launches bit for bit.  rows_m <= 4: one GEMV launch that forms
+ * the activations while it stages them; otherwise they go to a per-stream
+ * buffer first.  gate and up are [rows_m, k].  No counterpart in the
+ * reference (the graph compiler on DeviceType::HIP fuses the chain).
+ */
+int vm_hip_qmm_swiglu_add_f32(const float* gate, const float* up, const int8_t* wq,
+                              const float* scale, const float* addend, float* c, int64_t rows_m,
+                              int64_t k, int64_t n, int quant_type, int block_size, void* stream);
+
+/*
  * Sibling quantized matmuls sharing A: for every member g,
  * C_g[rows_m, n_g] = A[rows_m, k] x W_g (codes_g, scales_g), all with the
  * same quant_type and block_size.  No counterpart in the reference, whose

@@ -167,6 +167,18 @@ void rope_append_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* 
     concat_cpu(cv, out + 2, nullptr);
 }
 
+// inputs [g, u, B, S, h], outputs [C]
+void swiglu_qmm_add_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const auto& qa = std::get<QuantizedMatMulAttrs>(static_cast<const OpDescriptor*>(attrs)->attrs);
+    const std::size_t k = static_cast<std::size_t>(in[0]->shape.back()), n = static_cast<std::size_t>(in[2]->shape[1]);
+    const std::size_t rows = numel(*in[0]) / k;
+    std::vector<float> act(rows * k);
+    for (std::size_t e = 0; e < act.size(); ++e) act[e] = (sigmoid_host(cin(in, 0)[e]) * cin(in, 0)[e]) * cin(in, 1)[e];
+    vmo_qmm_2d_f32(act.data(), static_cast<const std::int8_t*>(in[2]->data), cin(in, 3), cout0(out), rows, k, n,
+                   static_cast<int>(qa.quant_type), qa.block_size);
+    for (std::size_t e = 0; e < rows * n; ++e) cout0(out)[e] = cin(in, 4)[e] + cout0(out)[e];
+}
+
 // inputs [x, w, B_1, S_1, ..], outputs [C_1, ..]
 void norm_qmm_fused_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
     const auto& na = *static_cast<const internal::NormQmmAttrs*>(attrs);
@@ -198,6 +210,7 @@ VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::QmmAdd, &qmm_add_f
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::AttentionDecode, &attention_decode_fused_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::RopeAppend, &rope_append_fused_cpu)
 VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::NormQmm, &norm_qmm_fused_cpu)
+VELOMIND_REGISTER_FUSED(DeviceType::CPU, internal::FusedKind::SwigluQmmAdd, &swiglu_qmm_add_fused_cpu)
 
 struct QmmWeights {
     std::vector<std::int8_t> q;
@@ -216,7 +229,7 @@ struct MlpRun {
     std::size_t steps = 0, nodes = 0;
     bool inner_unallocated = false;
 };
-MlpRun run_mlp(bool fuse, bool keep_sigmoid) {
+MlpRun run_mlp(bool fuse, bool keep_sigmoid, bool keep_act = false) {
     const std::size_t d = 64, f = 96;
     static const auto wg = int8_weights(d, f, 61), wu = int8_weights(d, f, 62), wd = int8_weights(f, d, 63);
     static const auto x = normal(d, 64), h = normal(d, 65);
@@ -235,11 +248,14 @@ MlpRun run_mlp(bool fuse, bool keep_sigmoid) {
     auto out = g.op(Op::Add, th, y);
     g.mark_output(out);
     if (keep_sigmoid) g.mark_output(sg);
+    if (keep_act) g.mark_output(act);
     auto exec = g.build(DeviceType::CPU);
     MlpRun r;
     r.steps = exec->num_steps();
     r.nodes = exec->num_nodes();
-    r.inner_unallocated = g.tensor_storage_at(t.index())->data == nullptr && g.tensor_storage_at(y.index())->data == nullptr;
+    r.inner_unallocated = g.tensor_storage_at(t.index())->data == nullptr &&
+                          g.tensor_storage_at(y.index())->data == nullptr &&
+                          (keep_act || g.tensor_storage_at(act.index())->data == nullptr);
     tx.copy_from_host(as_bytes(x));
     th.copy_from_host(as_bytes(h));
     tg.copy_from_host(as_bytes(wg.q));
@@ -292,17 +308,22 @@ AttnRun run_attention(bool fuse, bool keep_scores, std::size_t hq, std::size_t h
 
 }  // namespace
 
-TEST_CASE("fusion: SwiGLU chain and QuantizedMatMul + residual Add run as single steps", "[core][fusion]") {
+TEST_CASE("fusion: SwiGLU chain, its QuantizedMatMul and the residual Add run as one step", "[core][fusion]") {
     const auto off = run_mlp(false, false);
     const auto on = run_mlp(true, false);
     REQUIRE(off.nodes == 7);
     REQUIRE(off.steps == 7);
-    // gate, up, SiluMul (3 nodes), QmmAdd (2 nodes)
+    // gate, up, SwigluQmmAdd (5 nodes)
     REQUIRE(on.nodes == 7);
-    REQUIRE(on.steps == 4);
+    REQUIRE(on.steps == 3);
     REQUIRE(on.inner_unallocated);
     REQUIRE(!off.inner_unallocated);
     REQUIRE(std::memcmp(on.out.data(), off.out.data(), on.out.size() * 4) == 0);
+    // the SwiGLU output requested: SiluMul and QmmAdd form apart
+    const auto kept = run_mlp(true, false, true);
+    REQUIRE(kept.steps == 4);
+    REQUIRE(kept.inner_unallocated);
+    REQUIRE(std::memcmp(kept.out.data(), off.out.data(), off.out.size() * 4) == 0);
 }
 
 TEST_CASE("fusion: a kept inner tensor keeps its chain unfused", "[core][fusion]") {

@@ -155,6 +155,37 @@ def test_rope_append_matches_rope_and_concat(hip, hq, hkv, s, d):
         assert got.download(np.float32, (size,)).tobytes() == ref.download(np.float32, (size,)).tobytes()
 
 
+@pytest.mark.parametrize("m,k,n,qt,blk,with_add", [
+    (1, 2560, 960, 1, 0, True), (1, 5632, 2048, 2, 32, True), (2, 5632, 2048, 2, 32, False),
+    (4, 2560, 960, 1, 32, True), (8, 2560, 960, 1, 0, True), (1, 64, 40, 2, 32, True)])
+def test_qmm_swiglu_add_matches_the_separate_launches(hip, m, k, n, qt, blk, with_add):
+    H = hip
+    lib = H.open_library()
+    print(f"case swiglu qmm m={m} k={k} n={n} qt={qt} blk={blk} add={with_add}", flush=True)
+    rng = np.random.default_rng(m * 17 + k + n)
+    rows = (k + 1) // 2 if qt == 2 else k
+    nb = (k + blk - 1) // blk if blk > 0 else 1
+    g = (rng.standard_normal((m, k), dtype=np.float32) * 3).astype(np.float32)
+    u = rng.standard_normal((m, k), dtype=np.float32)
+    h = rng.standard_normal((m, n), dtype=np.float32)
+    dg, du, dh = _dev(H, g), _dev(H, u), _dev(H, h)
+    dw = _dev(H, rng.integers(-128, 128, size=(rows, n), dtype=np.int8))
+    ds = _dev(H, (rng.random((nb, n), dtype=np.float32) * 0.02).astype(np.float32))
+    act, ref, out = H.DeviceBuffer(m * k * 4), H.DeviceBuffer(m * n * 4), H.DeviceBuffer(m * n * 4)
+    for _ in range(2):
+        H.check(lib.vm_hip_elementwise_f32(H.EW_SILU_MUL, dg.ptr, du.ptr, act.ptr, m * k, None))
+        H.check(lib.vm_hip_qmm_f32(act.ptr, dw.ptr, ds.ptr, ref.ptr, m, k, n, qt, blk, None))
+        if with_add:
+            H.check(lib.vm_hip_elementwise_f32(H.EW_ADD, dh.ptr, ref.ptr, ref.ptr, m * n, None))
+        H.check(lib.vm_hip_qmm_swiglu_add_f32(dg.ptr, du.ptr, dw.ptr, ds.ptr, dh.ptr if with_add else None,
+                                              out.ptr, m, k, n, qt, blk, None))
+        H.synchronize()
+        x = out.download(np.float32, (m, n))
+        y = ref.download(np.float32, (m, n))
+        assert np.all(np.isfinite(y))
+        assert x.tobytes() == y.tobytes(), f"max diff {np.abs(x - y).max():.3e}"
+
+
 def test_silu_mul_matches_sigmoid_mul_mul(hip):
     H = hip
     lib = H.open_library()

@@ -106,6 +106,45 @@ void quantized_matmul_add_hip(const pConstTensorStorage* in, const pTensorStorag
     }
 }
 
+// Add(h, QuantizedMatMul(SiluMul(g, u))) fused by the graph compiler:
+// inputs [gate, up, B, scales, addend], outputs [C]; attrs the
+// QuantizedMatMul's descriptor.
+void quantized_matmul_swiglu_add_hip(const pConstTensorStorage* in, const pTensorStorage* out, const void* attrs) {
+    const auto* g = in[0];
+    const auto* u = in[1];
+    const auto* w = in[2];
+    const auto* s = in[3];
+    const auto* h = in[4];
+    auto* c = out[0];
+    if (!g || !u || !w || !s || !h || !c) throw std::runtime_error("quantized_matmul swiglu hip: null storage");
+    const auto& qa = std::get<QuantizedMatMulAttrs>(static_cast<const OpDescriptor*>(attrs)->attrs);
+    if (!g->is_contiguous() || !u->is_contiguous() || !w->is_contiguous() || !s->is_contiguous() ||
+        !h->is_contiguous() || !c->is_contiguous())
+        throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") +
+                                    ": strided operands are not supported on HIP");
+    const std::int64_t k = g->shape.back();
+    const std::int64_t n = w->shape[1];
+    std::int64_t rows = 1;
+    for (std::size_t i = 0; i + 1 < c->shape.size(); ++i) rows *= c->shape[i];
+    const int qt = qa.quant_type == QuantType::Int4 ? VM_HIP_QUANT_INT4 : VM_HIP_QUANT_INT8;
+    const std::int64_t bs = (qt == VM_HIP_QUANT_INT4 && qa.block_size <= 0) ? 32 : qa.block_size;
+    const std::int64_t nblk = bs > 0 ? (k + bs - 1) / bs : 1;
+    const std::uint64_t need_scales = static_cast<std::uint64_t>(k > 0 ? nblk : 0) * static_cast<std::uint64_t>(n);
+    if (storage_numel(*s) < need_scales)
+        throw std::invalid_argument(error_context(Op::QuantizedMatMul, *c, "launch") + ": scales hold " +
+                                    std::to_string(storage_numel(*s)) + " values, the kernel reads " +
+                                    std::to_string(need_scales));
+    const int status = vm_hip_qmm_swiglu_add_f32(
+        static_cast<const float*>(g->data), static_cast<const float*>(u->data), static_cast<const std::int8_t*>(w->data),
+        static_cast<const float*>(s->data), static_cast<const float*>(h->data), static_cast<float*>(c->data), rows, k, n,
+        qt, qa.block_size, current_stream());
+    if (status != VM_HIP_OK) {
+        const std::string last = vm_hip_last_error();
+        const char* stage = last.find(" at sync") != std::string::npos ? "sync" : "launch";
+        throw_status(status, error_context(Op::QuantizedMatMul, *c, stage));
+    }
+}
+
 // Sibling fp32 QuantizedMatMul nodes sharing A, compiled into one step by
 // the graph compiler: inputs [A, B_1, S_1, .., B_g, S_g], outputs
 // [C_1, .., C_g].  Each member is checked as a single node is; then one
@@ -205,6 +244,8 @@ void quantized_matmul_norm_group_hip(const pConstTensorStorage* in, const pTenso
 VELOMIND_REGISTER_QMM_GROUP(::velomind::DeviceType::HIP, quantized_matmul_group_hip)
 VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, ::velomind::internal::FusedKind::NormQmm,
                         &quantized_matmul_norm_group_hip)
+VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, ::velomind::internal::FusedKind::SwigluQmmAdd,
+                        &quantized_matmul_swiglu_add_hip)
 VELOMIND_REGISTER_FUSED(::velomind::DeviceType::HIP, ::velomind::internal::FusedKind::QmmAdd,
                         &quantized_matmul_add_hip)
 

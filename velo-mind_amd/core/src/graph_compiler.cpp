@@ -219,21 +219,29 @@ std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType de
 //                    Transpose swapping the last two axes, the Softmax on the
 //                    last one (RepeatKV absent when H == Hkv)
 //   AttentionGqa     o = FusedAttention(q, RepeatKV(K), RepeatKV(V))
+//   SwigluQmmAdd     C = Add(h, QuantizedMatMul(SiluMul(g, u), ..)): a QmmAdd whose
+//                    activations are a fused SiluMul's inner output
 //   NormQmm          C_g = QuantizedMatMul(RMSNorm(x, w), ..) for the members of one step
 //                    (a single node or a sibling group) that are the norm's only readers
 //   RopeAppend       q' = RoPE(q), K = Concat(K_past, RoPE(k)), V = Concat(V_past, v)
 //                    at one position (new rows [., 1, .], one cos/sin row), the
 //                    four nodes within a few steps of each other and q', K read
 //                    by nothing before the fused step's place
-// VELOMIND_GRAPH_FUSE=0 keeps every chain as separate launches.
+// VELOMIND_GRAPH_FUSE=0 keeps every chain as separate launches;
+// VELOMIND_GRAPH_FUSE_OFF lists kinds (their numbers) to leave out.
 void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& index,
                 const std::vector<bool>& kept) {
     const char* env = std::getenv("VELOMIND_GRAPH_FUSE");
     if (env && env[0] == '0') return;
+    // VELOMIND_GRAPH_FUSE_OFF="k,k,.." leaves the listed kinds out (measurements)
+    bool off[kFusedKinds] = {};
+    if (const char* list = std::getenv("VELOMIND_GRAPH_FUSE_OFF"))
+        for (const char* c = list; *c; ++c)
+            if (*c >= '0' && *c <= '9' && static_cast<std::size_t>(*c - '0') < kFusedKinds) off[*c - '0'] = true;
     Executable::KernelFn kernels[kFusedKinds];
     bool any = false;
     for (std::size_t k = 0; k < kFusedKinds; ++k) {
-        kernels[k] = fused_kernel(device, static_cast<FusedKind>(k));
+        kernels[k] = off[k] ? nullptr : fused_kernel(device, static_cast<FusedKind>(k));
         any = any || kernels[k];
     }
     if (!any) return;
@@ -370,6 +378,23 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
                 if (sq == SIZE_MAX || !inner(y) || !qmm_groupable(node_of(sq))) continue;
                 if (!f32(h) || !f32(out) || h->shape != y->shape || out->shape != y->shape) continue;
                 const auto q = node_of(sq)->inputs();
+                // activations from a fused SiluMul read by this product alone: one launch for all
+                const std::size_t sa = producer[index.at(q[0])];
+                if (kernels[static_cast<int>(FusedKind::SwigluQmmAdd)] && sa != SIZE_MAX && !dead[sa] &&
+                    steps[sa].fused == static_cast<int>(FusedKind::SiluMul) && inner(q[0])) {
+                    Step f;
+                    f.nodes = steps[sa].nodes;
+                    f.nodes.push_back(node_of(sq));
+                    f.nodes.push_back(n);
+                    f.fused = static_cast<int>(FusedKind::SwigluQmmAdd);
+                    f.ins = {steps[sa].ins[0], steps[sa].ins[1], q[1], q[2], h};
+                    f.outs = {out};
+                    f.attrs = desc_copy(node_of(sq)->op());
+                    dead[sa] = true;
+                    dead[sq] = true;
+                    steps[j] = std::move(f);
+                    break;
+                }
                 make(j, FusedKind::QmmAdd, {sq}, {q[0], q[1], q[2], h}, desc_copy(node_of(sq)->op()));
                 break;
             }

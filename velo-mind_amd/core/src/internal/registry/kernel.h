@@ -73,8 +73,10 @@ enum class FusedKind : int {
                           // inputs [q, k, v, K_past, V_past, cos, sin], outputs [q', K, V]
     NormQmm = 5,          // QuantizedMatMul(s) of RMSNorm(x, w): inputs [x, w, B_1, S_1, ..],
                           // outputs [C_1, ..]; attrs a NormQmmAttrs
+    SwigluQmmAdd = 6,     // Add(h, QuantizedMatMul(Mul(Mul(Sigmoid(g), g), u), B, S)): inputs
+                          // [g, u, B, S, h], outputs [C]; attrs the QuantizedMatMul's OpDescriptor
 };
-inline constexpr std::size_t kFusedKinds = 6;
+inline constexpr std::size_t kFusedKinds = 7;
 
 struct NormQmmAttrs {
     OpDescriptor desc;          // the QuantizedMatMuls' common descriptor

@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdint>
 
+#include "vm_device.h"
 #include "vm_hip.h"
 #include "vm_internal.h"
 
@@ -178,8 +179,6 @@ __global__ void repeat_kv_kernel(const float* __restrict__ x, float* __restrict_
 // ---- Elementwise Add / Mul / Sigmoid (add.cpp, mul.cpp, sigmoid.cpp), and
 // the SwiGLU chain Mul(Mul(Sigmoid(a), a), b) in one pass with the same
 // three roundings in the same order (the graph compiler's fused step).
-__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
-
 __global__ void elementwise_kernel(int op, const float* __restrict__ a, const float* __restrict__ b,
                                    float* __restrict__ y, int64_t n) {
     for (int64_t e = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; e < n;
@@ -188,7 +187,7 @@ __global__ void elementwise_kernel(int op, const float* __restrict__ a, const fl
         float r;
         if (op == VM_HIP_EW_ADD) r = x + b[e];
         else if (op == VM_HIP_EW_MUL) r = x * b[e];
-        else if (op == VM_HIP_EW_SILU_MUL) r = (sigmoid_f32(x) * x) * b[e];
+        else if (op == VM_HIP_EW_SILU_MUL) r = silu_mul_f32(x, b[e]);
         else r = sigmoid_f32(x);
         y[e] = r;
     }

@@ -193,6 +193,34 @@ int vm_hip_qmm_add_f32(const float* a, const int8_t* wq, const float* scale, con
     return vm_hip_elementwise_f32(VM_HIP_EW_ADD, addend, c, c, rows_m * n, stream);
 }
 
+int vm_hip_qmm_swiglu_add_f32(const float* gate, const float* up, const int8_t* wq, const float* scale,
+                              const float* addend, float* c, int64_t rows_m, int64_t k, int64_t n, int quant_type,
+                              int block_size, void* stream) {
+    clear_error();
+    VM_TRY(validate_qmm(gate, wq, scale, c, rows_m, k, n, quant_type, block_size));
+    if (rows_m == 0 || n == 0) return 0;
+    if (k > 0 && !up) return fail_inval("QuantizedMatMul SwiGLU: null up");
+    VM_TRY(injected_failure("QuantizedMatMul", "launch"));
+    auto s = static_cast<hipStream_t>(stream);
+    if (rows_m <= 4 && k > 0) {
+        const int bs = (quant_type == VM_HIP_QUANT_INT4 && block_size <= 0) ? 32 : block_size;
+        const int rc = gemv_qmm_f32(gate, reinterpret_cast<const uint8_t*>(wq), scale, c, static_cast<int>(rows_m),
+                                    static_cast<int>(k), static_cast<int>(n), quant_type, bs, s, addend, up);
+        if (rc != VM_HIP_EUNSUPPORTED) return rc;
+    }
+    // Shapes the GEMV does not take: the SwiGLU product in the stream's
+    // staging buffer, the product, then the addition.
+    const float* x = gate;
+    if (k > 0) {
+        void* staged = nullptr;
+        VM_TRY(get_staging(s, static_cast<std::size_t>(rows_m) * static_cast<std::size_t>(k) * sizeof(float), &staged));
+        VM_TRY(vm_hip_elementwise_f32(VM_HIP_EW_SILU_MUL, gate, up, static_cast<float*>(staged), rows_m * k, stream));
+        x = static_cast<const float*>(staged);
+    }
+    VM_TRY(qmm_f32_impl(x, wq, scale, c, rows_m, k, n, quant_type, block_size, s));
+    return addend ? vm_hip_elementwise_f32(VM_HIP_EW_ADD, addend, c, c, rows_m * n, stream) : 0;
+}
+
 int vm_hip_qmm_a_layout(int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size, int* layout,
                         int64_t* bytes) {
     clear_error();

@@ -152,7 +152,8 @@ template <int KIND, int MR, int L, int W, bool GROUPED>
 __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     const float* __restrict__ a, const GemvMembers mb, int m, int k, int block_size, int chunks_per_split,
     uint32_t a_bytes, int a_vec, int blk_shift, unsigned long long* __restrict__ pairs,
-    const float* __restrict__ addend, const float* __restrict__ norm_w, float norm_eps) {
+    const float* __restrict__ addend, const float* __restrict__ norm_w, float norm_eps,
+    const float* __restrict__ a_up) {
     VM_GEMV_MARKS;
     VM_GEMV_MARK(0);
     using CS = ChunkShape<KIND>;
@@ -321,13 +322,17 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
     load_chunk(ch, ca);
 
     {
+        // With a_up the staged activation is the SwiGLU product of a (gate)
+        // and a_up, silu_mul_f32 per element (the elementwise kernels'
+        // rounding); out-of-range reads give zeros for both, hence 0.
         const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
+        const __amdgpu_buffer_rsrc_t urs = buffer_rsrc(a_up ? a_up : a, a_bytes);
         constexpr int T = W * 64;
         if (a_vec) {
             const int q_per_row = xs_len / 4;  // xs_len is a multiple of 8
             const int q_total = MR * q_per_row;
             for (int q0 = threadIdx.x; q0 < q_total; q0 += kStageBatch * T) {
-                u32x4 t[kStageBatch];
+                u32x4 t[kStageBatch], tu[kStageBatch];
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
                     const int q = q0 + u * T;
@@ -339,7 +344,14 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
                                              ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u
                                              : a_bytes;
                     t[u] = buffer_load16(ars, off);
+                    if (a_up) tu[u] = buffer_load16(urs, off);
                 }
+                if (a_up)
+#pragma unroll
+                    for (int u = 0; u < kStageBatch; ++u)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            t[u][c] = __float_as_uint(silu_mul_f32(__uint_as_float(t[u][c]), __uint_as_float(tu[u][c])));
                 // Unconditional writes (surplus ones go to a spare LDS slot)
                 // keep the compiler from sinking loads into per-write branches.
 #pragma unroll
@@ -351,7 +363,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
         } else {
             const int e_total = MR * xs_len;
             for (int e0 = threadIdx.x; e0 < e_total; e0 += kStageBatch * T) {
-                uint32_t t[kStageBatch];
+                uint32_t t[kStageBatch], tu[kStageBatch];
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
                     const int e = e0 + u * T;
@@ -363,7 +375,12 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_kernel(
                                              ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u
                                              : a_bytes;
                     t[u] = __builtin_amdgcn_raw_buffer_load_b32(ars, static_cast<int>(off), 0, 0);
+                    if (a_up) tu[u] = __builtin_amdgcn_raw_buffer_load_b32(urs, static_cast<int>(off), 0, 0);
                 }
+                if (a_up)
+#pragma unroll
+                    for (int u = 0; u < kStageBatch; ++u)
+                        t[u] = __float_as_uint(silu_mul_f32(__uint_as_float(t[u]), __uint_as_float(tu[u])));
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
                     const int e = e0 + u * T;
@@ -718,10 +735,13 @@ struct Member {
     const float* addend = nullptr;  // [m, n] added to C (a launch of one matrix only)
 };
 
-// RMSNorm applied to A before the product (GemvNorm::w non-null).
+// What the kernel does to A before the product: RMSNorm (w non-null), or
+// the SwiGLU product with a second matrix (up non-null; A is the gate).
+// Not both.
 struct GemvNorm {
     const float* w = nullptr;
     float eps = 0.0f;
+    const float* up = nullptr;
 };
 
 template <int KIND, int MR, int L, int W>
@@ -763,11 +783,11 @@ int launch_cfg(const float* a, const Member* members, int count, int m, int k, i
     if (count == 1)
         hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, false>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
                            stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs,
-                           members[0].addend, norm.w, norm.eps);
+                           members[0].addend, norm.w, norm.eps, norm.up);
     else
         hipLaunchKernelGGL((qmm_gemv_kernel<KIND, MR, L, W, true>), dim3(tiles, cfg.splits), dim3(W * 64), lds,
                            stream, a, mb, m, k, block_size, cfg.chunks_per_split, a_bytes, a_vec, blk_shift, pairs,
-                           nullptr, norm.w, norm.eps);
+                           nullptr, norm.w, norm.eps, norm.up);
     return check_launch("QuantizedMatMul", stream);
 }
 
@@ -833,9 +853,9 @@ int gemv_group_f32(const float* a, const Member* members, int count, int m, int 
 }  // namespace
 
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
-                 int n, int quant_type, int block_size, hipStream_t stream, const float* addend) {
+                 int n, int quant_type, int block_size, hipStream_t stream, const float* addend, const float* a_up) {
     const Member one{wq, scale, c, n, addend};
-    return gemv_group_f32(a, &one, 1, m, k, quant_type, block_size, GemvNorm{}, stream);
+    return gemv_group_f32(a, &one, 1, m, k, quant_type, block_size, GemvNorm{nullptr, 0.0f, a_up}, stream);
 }
 
 int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* const* scale, float* const* c,
@@ -844,7 +864,7 @@ int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* co
     if (count < 1 || count > kMaxMembers) return VM_HIP_EUNSUPPORTED;
     Member members[kMaxMembers];
     for (int g = 0; g < count; ++g) members[g] = Member{wq[g], scale[g], c[g], n[g]};
-    return gemv_group_f32(a, members, count, m, k, quant_type, block_size, GemvNorm{norm_w, norm_eps}, stream);
+    return gemv_group_f32(a, members, count, m, k, quant_type, block_size, GemvNorm{norm_w, norm_eps, nullptr}, stream);
 }
 
 }  // namespace vmhip

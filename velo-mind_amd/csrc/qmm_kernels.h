@@ -10,9 +10,11 @@ namespace vmhip {
 // Decode-shaped GEMV for 1 <= m <= 4 rows (qmm_gemv.hip).  Returns
 // VM_HIP_EUNSUPPORTED when the shape/alignment needs another kernel.  A
 // non-null `addend` [m, n] is added to each output (addend + A x W, one fp32
-// addition after the product's last rounding).
+// addition after the product's last rounding).  A non-null `a_up` [m, k]
+// makes the activations the SwiGLU product silu_mul_f32(a, a_up).
 int gemv_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
-                 int n, int quant_type, int block_size, hipStream_t stream, const float* addend = nullptr);
+                 int n, int quant_type, int block_size, hipStream_t stream, const float* addend = nullptr,
+                 const float* a_up = nullptr);
 
 // The same GEMV for `count` (<= 4) matrices sharing the activations, in one
 // launch (qmm_gemv.hip); VM_HIP_EUNSUPPORTED when a member needs another

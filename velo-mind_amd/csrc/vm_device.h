@@ -114,4 +114,11 @@ __device__ __forceinline__ unsigned ticket_take(unsigned* counter, unsigned /*co
     return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The reference LLaMA MLP's activation: Sigmoid(g), then Mul by g, then
+// Mul by u (llama_graph.cpp:136), as the elementwise kernels round it.
+// Every kernel that computes it in one pass uses this so that they agree
+// bit for bit.
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_mul_f32(float g, float u) { return (sigmoid_f32(g) * g) * u; }
+
 }  // namespace vmhip

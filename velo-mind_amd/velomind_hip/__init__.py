@@ -84,6 +84,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_qmm_add_f32": ([p, p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_attention_decode_chain_f32": ([p, p, p, p, c_int64, c_int64, c_int64, c_int64, c_int64, p], c_int),
         "vm_hip_rope_append_f32": ([p] * 10 + [c_int64] * 5 + [p], c_int),
+        "vm_hip_qmm_swiglu_add_f32": ([p, p, p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
         "vm_hip_qmm_norm_group_f32": ([p, p, c_float, c_int64, c_int64, POINTER(QmmMember), c_int, c_int, c_int, p],
                                       c_int),
         "vm_hip_qmm": ([p, c_int, p, p, c_int, p, c_int, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
@@ -162,7 +163,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_argmax_workspace_bytes", "vm_hip_argmax_slices_ws_f32", "vm_hip_decode_workspace_bytes",
             "vm_hip_decode_step", "vm_hip_decode_status", "vm_hip_decode_trace_read", "vm_hip_gemv_trace_read",
             "vm_hip_qmm_add_f32", "vm_hip_attention_decode_chain_f32", "vm_hip_rope_append_f32",
-            "vm_hip_qmm_norm_group_f32",
+            "vm_hip_qmm_norm_group_f32", "vm_hip_qmm_swiglu_add_f32",
             "vm_hip_qmm_a_layout", "vm_hip_qmm_staged_f32", "vm_hip_add_rmsnorm_stage_f32",
             "vm_hip_silu_mul_stage_f32"]
 
