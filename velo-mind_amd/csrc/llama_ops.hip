@@ -373,11 +373,29 @@ __global__ __launch_bounds__(kT) void attention_decode_chain_kernel(
     for (int64_t t = threadIdx.x; t < d; t += kT) qs[t] = q[h * d + t];
     __syncthreads();
     const int64_t dpad = (d + 15) / 16 * 16;
+    // Each score's fma chain runs in order over d; the K row is loaded ahead
+    // in batches of 16 float4 (16-byte aligned rows) so the chain does not
+    // wait on one load per step.
+    const bool vec = d % 4 == 0 && reinterpret_cast<uintptr_t>(kb) % 16 == 0;
     for (int64_t j = threadIdx.x; j < s; j += kT) {
         const float* kr = kb + j * d;
         float acc = 0.0f;
-        for (int64_t t = 0; t < d; ++t) acc = fmaf(qs[t], kr[t], acc);
-        for (int64_t t = d; t < dpad; ++t) acc = fmaf(0.0f, 0.0f, acc);
+        int64_t t = 0;
+        if (vec)
+            for (; t + 64 <= d; t += 64) {
+                float4 r[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) r[u] = *reinterpret_cast<const float4*>(kr + t + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    acc = fmaf(qs[t + 4 * u], r[u].x, acc);
+                    acc = fmaf(qs[t + 4 * u + 1], r[u].y, acc);
+                    acc = fmaf(qs[t + 4 * u + 2], r[u].z, acc);
+                    acc = fmaf(qs[t + 4 * u + 3], r[u].w, acc);
+                }
+            }
+        for (; t < d; ++t) acc = fmaf(qs[t], kr[t], acc);
+        for (t = d; t < dpad; ++t) acc = fmaf(0.0f, 0.0f, acc);
         sc[j] = acc;
     }
     __syncthreads();
@@ -401,8 +419,16 @@ __global__ __launch_bounds__(kT) void attention_decode_chain_kernel(
     const int64_t spad = (s + 15) / 16 * 16;
     for (int64_t t = threadIdx.x; t < dv; t += kT) {
         float acc = 0.0f;
-        for (int64_t j = 0; j < s; ++j) acc = fmaf(sc[j], vb[j * dv + t], acc);
-        for (int64_t j = s; j < spad; ++j) acc = fmaf(0.0f, 0.0f, acc);
+        int64_t j = 0;
+        for (; j + 32 <= s; j += 32) {   // 32 V rows' loads ahead of the in-order chain
+            float vv[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) vv[u] = vb[(j + u) * dv + t];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) acc = fmaf(sc[j + u], vv[u], acc);
+        }
+        for (; j < s; ++j) acc = fmaf(sc[j], vb[j * dv + t], acc);
+        for (j = s; j < spad; ++j) acc = fmaf(0.0f, 0.0f, acc);
         o[h * dv + t] = acc;
     }
 }
