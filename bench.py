@@ -52,7 +52,10 @@ fraction of HBM peak.  ``persistent_step`` is the same decode with the
 one-launch step vm_hip_decode_step (slower than the default captured
 launch-per-projection step on this GPU, so reported beside it).  For
 config 4, ``graph_engine`` is the drop-in path: the reference engine's loop
-over a Graph on DeviceType::HIP per call (32 decode steps).
+over a Graph on DeviceType::HIP per call, over config 4's 128 decode tokens,
+with the reference layer's default attention chain and with its
+use_fused_attention form, and the host time per step split into graph
+construction, Graph::build, execute and the logits' readback.
 
 Prints one JSON line.  Only --gpus 1 is supported (one GPU per box).
 """
@@ -306,9 +309,10 @@ def cpu_baseline(target_s: float) -> dict:
             "tokens_per_s": round(sweeps / dt, 4)}
 
 
-# The drop-in path (graph engine) is timed on config 4, with its decode
-# steps capped so that the leg stays within seconds.
-GRAPH_ENGINE_E2E = {"smollm2_360m_int8": 32}
+# The drop-in path (graph engine) is timed on config 4's full workload
+# (128-token prompt, 128 decode tokens), with the reference layer's default
+# attention chain and with its use_fused_attention form.
+GRAPH_ENGINE_E2E = {"smollm2_360m_int8": 128}
 
 E2E_MODELS = {
     # TinyLlama-1.1B shapes, synthetic INT4 weights,
@@ -345,7 +349,7 @@ DECODE_PATHS = {0: "graph", 1: "per-op", 2: "slices", 3: "persistent"}
 
 
 def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph_engine: bool = False,
-              steps: int = 0) -> dict:
+              steps: int = 0, fused_attention: bool = False) -> dict:
     """Greedy generation on the resident HIP decoder (HIP-graph decode
     steps, or with persistent=True the one-launch step vm_hip_decode_step;
     device-event timing of the prefill and of the decode steps), or with
@@ -369,7 +373,7 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph
         w.tie_lm_head()
     steps = steps or spec["steps"]
     if graph_engine:
-        sess = VL.Session(w, VL.ENGINE_GRAPH, spec["quant"], spec["block"])
+        sess = VL.Session(w, VL.ENGINE_GRAPH, spec["quant"], spec["block"], fused_attention=fused_attention)
     else:
         prev = os.environ.get("VELOMIND_DECODE_PERSISTENT")
         os.environ["VELOMIND_DECODE_PERSISTENT"] = "1" if persistent else "0"
@@ -387,6 +391,7 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph
     prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, spec["prompt"]).astype(np.int32)
     sess.generate(prompt, 8 if not graph_engine else 2, use_hip_graph=use_graph)  # warm-up (sizes workspaces)
     _, (pf_s, dec_s, nd) = sess.generate(prompt, steps, use_hip_graph=use_graph)
+    step_ms = sess.step_timing() if graph_engine else None
     wb = decode_weight_bytes(spec["cfg"], spec["quant"], spec["block"])
     dec_tps = nd / dec_s
     out = {"prompt_tokens": spec["prompt"], "decode_tokens": steps, "decode_steps_timed": nd,
@@ -401,6 +406,10 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph
                       "host wall-clock timing" if graph_engine else
                       "resident HIP decoder, " + ("HIP-graph" if use_graph else "eager") +
                       " decode steps, greedy argmax on device")}
+    if step_ms is not None:
+        out["host_ms_per_step"] = {k: round(v, 3) for k, v in step_ms.items() if k != "steps"}
+        out["attention"] = "FusedAttention (use_fused_attention)" if fused_attention else \
+            "MatMul / Softmax / MatMul chain (the reference default)"
     sess.close()
     w.close()
     return out
@@ -771,6 +780,8 @@ def main() -> int:
                     help="with --e2e-only and --e2e-model: comma-separated layer counts to run instead of the "
                          "config's (per-layer decode time with the weights resident in the 256 MB Infinity Cache "
                          "at few layers, streamed from HBM at many)")
+    ap.add_argument("--graph-engine", action="store_true",
+                    help="only the drop-in graph-engine decode of config 4 (both attention forms)")
     ap.add_argument("--gemv-trace", action="store_true",
                     help="phase timestamps of the decode GEMV per shape (library built with VELOMIND_GEMV_TRACE=1)")
     ap.add_argument("--decode-trace", action="store_true",
@@ -839,6 +850,14 @@ def main() -> int:
                              "us_per_layer": round(r["decode_us_per_token"] / layers, 2)})
                 log(f"bench: {name} {r['decode_path']}: {r['decode_us_per_token']} us/token")
         print(json.dumps({"metric": METRIC, "e2e_layers": rows}), flush=True)
+        return 0
+    if args.graph_engine:
+        out = {}
+        for name, steps in GRAPH_ENGINE_E2E.items():
+            for fa in (False, True):
+                out[f"{name}{'_fused_attention' if fa else ''}"] = e2e_bench(name, graph_engine=True, steps=steps,
+                                                                              fused_attention=fa)
+        print(json.dumps({"metric": METRIC, "graph_engine": out}), flush=True)
         return 0
     if args.e2e_only:
         e2e = {}
@@ -971,11 +990,15 @@ def main() -> int:
                 f"decode {e2e[name]['decode_tokens_per_s']} tok/s ({e2e[name]['decode_path']}), "
                 f"persistent step {pers['decode_tokens_per_s']} tok/s")
             if name in GRAPH_ENGINE_E2E:
+                keys = ("prefill_tokens_per_s", "prefill_ms", "decode_tokens", "decode_tokens_per_s",
+                        "decode_us_per_token", "host_ms_per_step", "attention", "engine")
                 ge = e2e_bench(name, graph_engine=True, steps=GRAPH_ENGINE_E2E[name])
-                e2e[name]["graph_engine"] = {k: ge[k] for k in ("prefill_tokens_per_s", "prefill_ms", "decode_tokens",
-                                                                "decode_tokens_per_s", "decode_us_per_token", "engine")}
+                gf = e2e_bench(name, graph_engine=True, steps=GRAPH_ENGINE_E2E[name], fused_attention=True)
+                e2e[name]["graph_engine"] = {k: ge[k] for k in keys}
+                e2e[name]["graph_engine"]["fused_attention"] = {k: gf[k] for k in keys if k != "engine"}
                 log(f"bench: {name} graph engine: prefill {ge['prefill_tokens_per_s']} tok/s, "
-                    f"decode {ge['decode_tokens_per_s']} tok/s")
+                    f"decode {ge['decode_tokens_per_s']} tok/s; use_fused_attention: "
+                    f"decode {gf['decode_tokens_per_s']} tok/s")
 
     gemm = None
     if not args.no_gemm and not args.only_shape:
