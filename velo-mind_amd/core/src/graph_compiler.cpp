@@ -45,10 +45,6 @@ struct Interval {
 
 std::size_t align_up(std::size_t v, std::size_t a) { return (v + a - 1) / a * a; }
 
-bool lifetimes_overlap(const Interval& a, const Interval& b) {
-    return std::max(a.birth, b.birth) <= std::min(a.death, b.death);
-}
-
 // Places intervals; returns the arena size.  Lifetimes are inclusive
 // ranges of step indices, so two intersect exactly when they share a step:
 // the placed intervals alive at each step are kept in per-step lists, and
@@ -166,7 +162,11 @@ std::vector<Step> plan_steps(const std::vector<pConstNode>& order, DeviceType de
     std::vector<Step> steps;
     steps.reserve(order.size());
     if (!group) {
-        for (auto* n : order) steps.push_back(Step{{n}});
+        for (auto* n : order) {
+            Step st;
+            st.nodes.push_back(n);
+            steps.push_back(std::move(st));
+        }
         return steps;
     }
     std::vector<std::size_t> producer(tensor_count, SIZE_MAX);

@@ -81,10 +81,10 @@ typedef unsigned long long u64;
 //  12 down staged          13 computed    14 stored
 // and in slot `layers`: 0 final norm begins, 1 staged, 2 lm_head done,
 // 3 local argmax done, 4 workgroup 0's reduction done.
+#ifdef VM_DECODE_TRACE
 constexpr int kTraceWgs = 512;
 constexpr int kTraceSlots = 34;
 constexpr int kTraceEvents = 24;
-#ifdef VM_DECODE_TRACE
 __device__ u64 g_decode_trace[kTraceWgs * kTraceSlots * kTraceEvents];
 #define VM_TRACE(slot, ev)                                                                         \
     do {                                                                                           \

@@ -25,6 +25,13 @@ int gemv_qmm_group_f32(const float* a, const uint8_t* const* wq, const float* co
                        const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream,
                        const float* norm_w = nullptr, float norm_eps = 0.0f);
 
+// The kernels with fused extras (qmm_gemv_fx.hip), reached through the two
+// functions above when an extra is non-null: addend (one matrix only),
+// norm_w or a_up (not both).
+int gemv_qmm_fx_f32(const float* a, const uint8_t* const* wq, const float* const* scale, float* const* c,
+                    const int* n, int count, int m, int k, int quant_type, int block_size, hipStream_t stream,
+                    const float* addend, const float* norm_w, float norm_eps, const float* a_up);
+
 // Prefill-shaped MFMA GEMM for m > 4 rows (qmm_gemm.hip).
 int gemm_qmm_f32(const float* a, const uint8_t* wq, const float* scale, float* c, int m, int k,
                  int n, int quant_type, int block_size, hipStream_t stream);
