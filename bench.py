@@ -634,6 +634,21 @@ def gemm_bench(H, stream, reps: int = 5) -> dict:
 CONFIG1_K, CONFIG1_N = 576, 1536
 
 
+def config1_setup(H):
+    """Config 1's operands: x [576] and W [576, 1536] ~ N(0, 0.02), W packed
+    on the GPU (INT8 per column).  Returns x and the device buffers."""
+    rng = np.random.default_rng(3)
+    k, n = CONFIG1_K, CONFIG1_N
+    w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal(k, dtype=np.float32)
+    dw = H.DeviceBuffer.from_array(w)
+    p, s = H.DeviceBuffer(k * n), H.DeviceBuffer(n * 4)
+    H.pack_int8(dw.addr, p.addr, s.addr, k, n)
+    H.synchronize()
+    dw.close()
+    return x, p, s, H.DeviceBuffer.from_array(x), H.DeviceBuffer(n * 4)
+
+
 def config1_bench(H, stream, reps: int = 10, cpu_seconds: float = 3.0) -> dict:
     """the INT8 per-column decode GEMV (M=1), K 576 x
     N 1536 (quantized_matmul.cpp:190-235's streaming decode shape).  W
@@ -644,16 +659,8 @@ def config1_bench(H, stream, reps: int = 10, cpu_seconds: float = 3.0) -> dict:
     on one pinned core, on the same codes (cache-resident: 0.9 MB)."""
     import oracle as O
 
-    rng = np.random.default_rng(3)
     k, n = CONFIG1_K, CONFIG1_N
-    w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-    x = rng.standard_normal(k, dtype=np.float32)
-    dw = H.DeviceBuffer.from_array(w)
-    p, s = H.DeviceBuffer(k * n), H.DeviceBuffer(n * 4)
-    H.pack_int8(dw.addr, p.addr, s.addr, k, n)
-    H.synchronize()
-    dw.close()
-    dx, dc = H.DeviceBuffer.from_array(x), H.DeviceBuffer(n * 4)
+    x, p, s, dx, dc = config1_setup(H)
     rot = Rotation(H, p, s, stream)
 
     def launch_all():
@@ -793,6 +800,9 @@ def main() -> int:
     ap.add_argument("--gemm-profile", default="",
                     help="M,QT,REPS: only REPS eager launches of one config-3 GEMM, each on the next weight copy "
                          "of a >= 512 MB rotation (rocprofv3 counter passes)")
+    ap.add_argument("--config1-profile", type=int, default=0,
+                    help="REPS: only REPS eager launches of config 1's INT8 GEMV, each on the next weight copy "
+                         "of a >= 512 MB rotation (rocprofv3 counter passes)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (rocprofv3 counter calibration)")
     args = ap.parse_args()
@@ -823,6 +833,15 @@ def main() -> int:
             H.qmm_f32(a.addr, pa, sa, c.addr, m, GEMM_K, GEMM_N, qt, blk, stream)
         stream.synchronize()
         log(f"bench: {reps} GEMM launches M={m} quant_type={qt} done, walking {rot.copies} weight copies")
+        return 0
+    if args.config1_profile:
+        _, p, s, dx, dc = config1_setup(H)
+        rot = Rotation(H, p, s, stream)
+        for i in range(args.config1_profile):
+            pa, sa = rot.addrs[i % rot.copies]
+            H.qmm_f32(dx.addr, pa, sa, dc.addr, 1, CONFIG1_K, CONFIG1_N, H.QUANT_INT8, 0, stream)
+        stream.synchronize()
+        log(f"bench: {args.config1_profile} config-1 GEMV launches done, walking {rot.copies} weight copies")
         return 0
     if args.decode_trace:
         print(json.dumps({"metric": METRIC, "decode_trace": decode_trace_report()}), flush=True)

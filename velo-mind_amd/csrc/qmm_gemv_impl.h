@@ -336,6 +336,42 @@ __device__ __forceinline__ void gemv_body(
     VM_GEMV_MARK(1);
     load_chunk(ch, ca);
 
+    // RMSNorm operands (fx.norm_w non-null), requested together with the
+    // staging loads so that the norm adds no memory round trip: the first
+    // kNormRegs elements of this thread's stride of each row (the sum of
+    // squares) and of norm_w for the first kNormRegs staged elements it
+    // scales.  Rows longer than that load the rest after the barrier.
+    constexpr int kNormRegs = 8;
+    float nv[MR][kNormRegs];
+    float nwv[kNormRegs];
+    if constexpr (FX) {
+        if (fx.norm_w) {
+            const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
+            const uint32_t w_bytes = static_cast<uint32_t>(k) * 4u;
+            const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(fx.norm_w, w_bytes);
+#pragma unroll
+            for (int r = 0; r < MR; ++r)
+#pragma unroll
+                for (int j = 0; j < kNormRegs; ++j) {
+                    const int i = static_cast<int>(threadIdx.x) + 256 * j;
+                    const uint32_t off = (threadIdx.x < 256 && r < m && i < k)
+                                             ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + i) * 4u
+                                             : a_bytes;
+                    nv[r][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ars, static_cast<int>(off), 0, 0));
+                }
+#pragma unroll
+            for (int j = 0; j < kNormRegs; ++j) {
+                const int e = static_cast<int>(threadIdx.x) + j * W * 64;
+                int r = 0;
+#pragma unroll
+                for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
+                const int kk = k_begin + (e - r * xs_len);
+                const uint32_t off = (e < MR * xs_len && kk < k) ? static_cast<uint32_t>(kk) * 4u : w_bytes;
+                nwv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, static_cast<int>(off), 0, 0));
+            }
+        }
+    }
+
     {
         // With a_up the staged activation is the SwiGLU product of a (gate)
         // and a_up, silu_mul_f32 per element (the elementwise kernels'
@@ -417,11 +453,15 @@ __device__ __forceinline__ void gemv_body(
         for (int r = 0; r < MR; ++r) {
             if (r >= m) break;
             float sq = 0.0f;
-            if (threadIdx.x < 256)
-                for (int i = threadIdx.x; i < k; i += 256) {
+            if (threadIdx.x < 256) {
+#pragma unroll
+                for (int j = 0; j < kNormRegs; ++j)
+                    if (static_cast<int>(threadIdx.x) + 256 * j < k) sq = fmaf(nv[r][j], nv[r][j], sq);
+                for (int i = threadIdx.x + 256 * kNormRegs; i < k; i += 256) {
                     const float v = a[static_cast<int64_t>(r) * k + i];
                     sq = fmaf(v, v, sq);
                 }
+            }
             for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
             if (threadIdx.x < 256 && lane == 0) norm_part[r][wave] = sq;
         }
@@ -435,12 +475,27 @@ __device__ __forceinline__ void gemv_body(
                 for (int w = 0; w < 4; ++w) tot += norm_part[r][w];
             inv[r] = 1.0f / sqrtf(tot / static_cast<float>(k) + fx.norm_eps);
         }
-        for (int e = threadIdx.x; e < MR * xs_len; e += W * 64) {
+        auto scale_one = [&](int e, float wv) {
             int r = 0;
 #pragma unroll
             for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
             const int kk = k_begin + (e - r * xs_len);
-            if (r < m && kk < k) xs[e] = (xs[e] * inv[r]) * fx.norm_w[kk];
+            float rinv = inv[0];
+#pragma unroll
+            for (int i = 1; i < MR; ++i) rinv = r == i ? inv[i] : rinv;
+            if (r < m && kk < k) xs[e] = (xs[e] * rinv) * wv;
+        };
+#pragma unroll
+        for (int j = 0; j < kNormRegs; ++j) {
+            const int e = static_cast<int>(threadIdx.x) + j * W * 64;
+            if (e < MR * xs_len) scale_one(e, nwv[j]);
+        }
+        for (int e = threadIdx.x + kNormRegs * W * 64; e < MR * xs_len; e += W * 64) {
+            int r = 0;
+#pragma unroll
+            for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
+            const int kk = k_begin + (e - r * xs_len);
+            scale_one(e, kk < k ? fx.norm_w[kk] : 0.0f);
         }
         __syncthreads();
     }
