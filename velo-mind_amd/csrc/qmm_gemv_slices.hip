@@ -14,8 +14,8 @@
 //             row) x 4 row-lanes (the wave's four 16-lane DPP rows) = 4R
 //             byte rows, all inside one scale block
 //   workgroup W waves stacked in K (4RW byte rows), on one 256-column tile
-//   grid      (tiles, splits); tiles are renumbered so that each XCD owns a
-//             contiguous run of columns
+//   grid      (tiles, splits), renumbered so that each XCD owns a
+//             contiguous run of splits (K ranges)
 // The four row-lanes of a wave are reduced first with the gfx950
 // permlane16/32 swaps (each lane is left with 4 of its 16 columns), so the
 // block scale is one 16-byte load per lane and four FMAs; the waves of a
@@ -99,12 +99,22 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
     const int wave = threadIdx.x >> 6;
     const int cl = lane & 15;   // column lane
     const int rl = lane >> 4;   // row lane (DPP row)
+    // Workgroups are dealt to the 8 XCDs round-robin by linear id; each XCD
+    // takes a contiguous run of (split, tile) pairs in split-major order, so
+    // the workgroups that stage one K range of the activations share an L2
+    // (tiles share no weight lines: a tile is whole 128-byte lines).
     int tile = blockIdx.x;
+    int split = blockIdx.y;
     {
-        const int full = static_cast<int>(gridDim.x) & ~7;
-        if (tile < full) tile = (tile & 7) * (full >> 3) + (tile >> 3);
+        const int gx = static_cast<int>(gridDim.x);
+        const int lin = static_cast<int>(blockIdx.y) * gx + tile;
+        const int full = (gx * static_cast<int>(gridDim.y)) & ~7;
+        if (lin < full) {
+            const int p = (lin & 7) * (full >> 3) + (lin >> 3);
+            split = p / gx;
+            tile = p - split * gx;
+        }
     }
-    const int split = blockIdx.y;
     const int col0 = tile * kTileCols + cl * 16;
     const bool col_ok = col0 < n;                          // n % 16 == 0: all 16 columns or none
     const int wg_row0 = split * kRowsWg;
@@ -337,7 +347,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
                 }
                 if constexpr (kNorm) {
                     if (ok) {
-                        if (src.h_out && blockIdx.x == 0) *reinterpret_cast<float4*>(src.h_out + kk) = g;
+                        if (src.h_out && tile == 0) *reinterpret_cast<float4*>(src.h_out + kk) = g;
                         ss_part = fmaf(g.x, g.x, fmaf(g.y, g.y, fmaf(g.z, g.z, g.w * g.w)));
                         g = make_float4(g.x * __uint_as_float(nwv[0]), g.y * __uint_as_float(nwv[1]),
                                         g.z * __uint_as_float(nwv[2]), g.w * __uint_as_float(nwv[3]));
@@ -354,7 +364,7 @@ __global__ __launch_bounds__(W * 64) void qmm_gemv_slices_kernel(
         }
         __syncthreads();
         if constexpr (kNorm) {
-            if (src.ss_out && blockIdx.x == 0 && threadIdx.x == 0) {
+            if (src.ss_out && tile == 0 && threadIdx.x == 0) {
                 float t = 0.0f;
 #pragma unroll
                 for (int ww = 0; ww < W; ++ww) t += ssp[ww];
