@@ -29,8 +29,12 @@ def _dev(H, a):
     return H.DeviceBuffer.from_array(np.ascontiguousarray(a))
 
 
-@pytest.mark.parametrize("hq,hkv,s,d", [(8, 2, 37, 64), (15, 5, 129, 64), (32, 4, 775, 64), (4, 4, 1, 16),
-                                         (6, 3, 17, 20), (2, 1, 1000, 128)])
+# V copied into LDS (s * d fits: s = 1 ... 400, partial last 1 KiB blocks
+# included) and V read from global memory (s = 775 and 1000 overflow LDS;
+# d = 18 is not a multiple of 4).
+@pytest.mark.parametrize("hq,hkv,s,d", [(8, 2, 37, 64), (15, 5, 129, 64), (15, 5, 256, 64), (15, 5, 400, 64),
+                                         (32, 4, 775, 64), (4, 4, 1, 16), (6, 3, 17, 20), (4, 2, 33, 18),
+                                         (2, 1, 1000, 128)])
 def test_attention_decode_chain_matches_the_unfused_chain(hip, hq, hkv, s, d):
     H = hip
     lib = H.open_library()

@@ -359,17 +359,37 @@ __global__ __launch_bounds__(64) void attention_kernel(const float* __restrict__
 // chain over the positions (padding included).  The result equals the
 // chain's bit for bit, without the repeated K/V, the transposed K and the
 // score rows in memory.
+//
+// VLDS (the head's V fits in LDS beside the scores): V is copied into LDS
+// by direct global-to-LDS loads issued at entry, before the scores -- its
+// rows are independent of them -- so the copy overlaps the score phase and
+// the context chain reads LDS instead of waiting on global loads one batch
+// at a time.  Layout [V: s * dv][q: d][scores: s][max, sum].
+template <bool VLDS>
 __global__ __launch_bounds__(kT) void attention_decode_chain_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ o,
     int64_t hq, int64_t hkv, int64_t s, int64_t d, int64_t dv) {
+    // No static LDS: the dynamic block starts at LDS address 0, so V's copy
+    // (16 bytes per lane) lands 16-byte aligned.
     extern __shared__ float sh[];
-    float* qs = sh;        // [d]
-    float* sc = sh + d;    // [s]: scores, then probabilities
-    __shared__ float stat[2];
+    float* vs = sh;                       // [s * dv] (VLDS)
+    float* qs = VLDS ? sh + s * dv : sh;  // [d]
+    float* sc = qs + d;                   // [s]: scores, then probabilities
+    float* stat = sc + s;                 // [2]: max, sum
     const int64_t h = blockIdx.x;
     const int64_t kvh = h / (hq / hkv);
     const float* kb = k + kvh * s * d;
     const float* vb = v + kvh * s * dv;
+    if constexpr (VLDS) {
+        // Wave w copies 1 KiB blocks w, w + 4, ...: lane l moves float4
+        // 64 * block + l (16 bytes to LDS at the block's base + 16 l).
+        const int n4 = static_cast<int>(s * dv / 4);   // dv % 4 == 0, v 16-byte aligned
+        const int lane = threadIdx.x & 63;
+        for (int blk = threadIdx.x >> 6; blk * 64 < n4; blk += kT / 64)
+            if (blk * 64 + lane < n4)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(vb + 4 * (blk * 64 + lane)),
+                                                 (__attribute__((address_space(3))) void*)(vs + 256 * blk), 16, 0, 0);
+    }
     for (int64_t t = threadIdx.x; t < d; t += kT) qs[t] = q[h * d + t];
     __syncthreads();
     const int64_t dpad = (d + 15) / 16 * 16;
@@ -398,6 +418,9 @@ __global__ __launch_bounds__(kT) void attention_decode_chain_kernel(
         for (t = d; t < dpad; ++t) acc = fmaf(0.0f, 0.0f, acc);
         sc[j] = acc;
     }
+    // VLDS: the LDS copy of V is complete once this wave's loads are, and
+    // visible to every wave after the barrier.
+    if constexpr (VLDS) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
@@ -420,14 +443,25 @@ __global__ __launch_bounds__(kT) void attention_decode_chain_kernel(
     for (int64_t t = threadIdx.x; t < dv; t += kT) {
         float acc = 0.0f;
         int64_t j = 0;
-        for (; j + 32 <= s; j += 32) {   // 32 V rows' loads ahead of the in-order chain
-            float vv[32];
+        if constexpr (VLDS) {
+            for (; j + 16 <= s; j += 16) {   // LDS reads of 16 V rows ahead of the in-order chain
+                float vv[16];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) vv[u] = vb[(j + u) * dv + t];
+                for (int u = 0; u < 16; ++u) vv[u] = vs[(j + u) * dv + t];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) acc = fmaf(sc[j + u], vv[u], acc);
+                for (int u = 0; u < 16; ++u) acc = fmaf(sc[j + u], vv[u], acc);
+            }
+            for (; j < s; ++j) acc = fmaf(sc[j], vs[j * dv + t], acc);
+        } else {
+            for (; j + 32 <= s; j += 32) {   // 32 V rows' loads ahead of the in-order chain
+                float vv[32];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) vv[u] = vb[(j + u) * dv + t];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) acc = fmaf(sc[j + u], vv[u], acc);
+            }
+            for (; j < s; ++j) acc = fmaf(sc[j], vb[j * dv + t], acc);
         }
-        for (; j < s; ++j) acc = fmaf(sc[j], vb[j * dv + t], acc);
         for (j = s; j < spad; ++j) acc = fmaf(0.0f, 0.0f, acc);
         o[h * dv + t] = acc;
     }
@@ -441,6 +475,8 @@ using namespace vmhip;
 namespace {
 
 hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+constexpr size_t kChainMaxLds = 160 * 1024;   // dynamic LDS of the V-staging chain kernel (no static LDS)
 
 }  // namespace
 
@@ -619,9 +655,29 @@ int vm_hip_attention_decode_chain_f32(const float* q, const float* k, const floa
     if (s + d > 16384) return fail_inval("AttentionDecodeChain: S + D exceeds 16384 on this kernel");
     if (hq > 0x7fffffff) return fail_inval("AttentionDecodeChain: too many heads");
     if (!q || !k || !v || !o) return fail_inval("AttentionDecodeChain: null pointer");
-    const size_t lds = static_cast<size_t>(d + s) * sizeof(float);
-    hipLaunchKernelGGL(attention_decode_chain_kernel, dim3(static_cast<unsigned>(hq)), dim3(kT), lds, S(stream), q, k,
-                       v, o, hq, hkv, s, d, dv);
+    // V staged in LDS when it fits (gfx950: 160 KiB per workgroup) and
+    // loads as float4.
+    const size_t lds = static_cast<size_t>(d + s + 2) * sizeof(float);
+    const size_t lds_v = lds + static_cast<size_t>(s * dv) * sizeof(float);
+    // The dynamic LDS limit is raised once per process (a refusal, cleared
+    // here, keeps every launch on the global-memory form).
+    static const bool big_lds = [] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_decode_chain_kernel<true>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kChainMaxLds));
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_decode_chain_kernel<false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kChainMaxLds));
+        if (e != hipSuccess) (void)hipGetLastError();
+        return e == hipSuccess;
+    }();
+    const bool vlds = big_lds && dv % 4 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && lds_v <= kChainMaxLds;
+    if (vlds) {
+        hipLaunchKernelGGL(attention_decode_chain_kernel<true>, dim3(static_cast<unsigned>(hq)), dim3(kT), lds_v,
+                           S(stream), q, k, v, o, hq, hkv, s, d, dv);
+    } else {
+        hipLaunchKernelGGL(attention_decode_chain_kernel<false>, dim3(static_cast<unsigned>(hq)), dim3(kT), lds,
+                           S(stream), q, k, v, o, hq, hkv, s, d, dv);
+    }
     return check_launch("AttentionDecodeChain", S(stream));
 }
 
