@@ -135,3 +135,24 @@ def test_attention(hip, hq, hk, sq, sk, d, dv, scale, causal):
     v = rng.standard_normal((2, hk, sk, dv)).astype(np.float32)
     print(f"case attention hq={hq} hk={hk} sq={sq} sk={sk} d={d} dv={dv} causal={causal}", flush=True)
     _close(hip.run_attention(q, k, v, scale, causal), L.attention(q, k, v, scale, causal), 1e-5)
+
+
+@pytest.mark.parametrize("hq,hk,sk,d,dv", [
+    (15, 5, 129, 64, 64),    # SmolLM2 decode, V copied into LDS
+    (32, 4, 256, 64, 64),    # TinyLlama heads, V in LDS
+    (32, 4, 700, 64, 64),    # V read from global memory (does not fit LDS)
+    (8, 2, 5, 32, 24),       # Dv != D
+    (4, 2, 33, 18, 18),      # D not a multiple of 4 (scalar loads, V from global)
+])
+def test_attention_single_row_kernel_matches_the_row_kernel(hip, hq, hk, sk, d, dv):
+    """Sq = 1 runs attention_row_kernel (four waves per row); the same row
+    inside a two-row non-causal call runs attention_kernel.  Both follow one
+    fp32 operation order, so the outputs agree bit for bit."""
+    rng = np.random.default_rng(hq * 7 + sk)
+    q = rng.standard_normal((2, hq, 1, d)).astype(np.float32) * 0.5
+    k = rng.standard_normal((2, hk, sk, d)).astype(np.float32) * 0.5
+    v = rng.standard_normal((2, hk, sk, dv)).astype(np.float32)
+    print(f"case attention row hq={hq} hk={hk} sk={sk} d={d} dv={dv}", flush=True)
+    one = hip.run_attention(q, k, v, 0.0, True)
+    two = hip.run_attention(np.concatenate([q, q], axis=2), k, v, 0.0, False)
+    assert one.tobytes() == np.ascontiguousarray(two[:, :, :1, :]).tobytes()

@@ -347,6 +347,110 @@ __global__ __launch_bounds__(64) void attention_kernel(const float* __restrict__
     }
 }
 
+// ---- The same attention for one query row per (batch, head) (decode,
+// Sq = 1), one 256-thread workgroup per row: the scores' fma chains run on
+// all four waves (each in attention_kernel's order, its float4 loads
+// batched), wave 0 reduces max and sum over the same lane-strided partials
+// and butterflies as attention_kernel, and the value chain runs as there.
+// Every value equals attention_kernel's bit for bit.  VLDS: the head's V is
+// copied into LDS by direct global-to-LDS loads issued at entry, so the
+// copy overlaps the scores.  Layout [V: sk * dv][q: d][scores: sk][max, sum].
+template <bool VLDS>
+__global__ __launch_bounds__(kT) void attention_row_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ v, float* __restrict__ o,
+                                                           int64_t hq, int64_t hk, int64_t sk, int64_t d, int64_t dv,
+                                                           float scale) {
+    extern __shared__ float sh[];   // no static LDS: V's copy lands 16-byte aligned
+    float* vs = sh;
+    float* qs = VLDS ? sh + sk * dv : sh;
+    float* sc = qs + d;
+    float* stat = sc + sk;
+    const int64_t row = blockIdx.x;   // (batch, head)
+    const int64_t h = row % hq;
+    const int64_t bidx = row / hq;
+    const int64_t hkv = h / (hq / hk);
+    const float* kb = k + (bidx * hk + hkv) * sk * d;
+    const float* vb = v + (bidx * hk + hkv) * sk * dv;
+    if constexpr (VLDS) {
+        const int n4 = static_cast<int>(sk * dv / 4);   // dv % 4 == 0, v 16-byte aligned
+        const int lane = threadIdx.x & 63;
+        for (int blk = threadIdx.x >> 6; blk * 64 < n4; blk += kT / 64)
+            if (blk * 64 + lane < n4)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(vb + 4 * (blk * 64 + lane)),
+                                                 (__attribute__((address_space(3))) void*)(vs + 256 * blk), 16, 0, 0);
+    }
+    for (int64_t t = threadIdx.x; t < d; t += kT) qs[t] = q[row * d + t];
+    __syncthreads();
+    const bool vec = d % 4 == 0 && reinterpret_cast<uintptr_t>(kb) % 16 == 0;
+    for (int64_t j = threadIdx.x; j < sk; j += kT) {
+        const float* kr = kb + j * d;
+        float dot = 0.0f;
+        int64_t t = 0;
+        if (vec)
+            for (; t + 64 <= d; t += 64) {
+                float4 r[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) r[u] = *reinterpret_cast<const float4*>(kr + t + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    dot = fmaf(qs[t + 4 * u], r[u].x, dot);
+                    dot = fmaf(qs[t + 4 * u + 1], r[u].y, dot);
+                    dot = fmaf(qs[t + 4 * u + 2], r[u].z, dot);
+                    dot = fmaf(qs[t + 4 * u + 3], r[u].w, dot);
+                }
+            }
+        for (; t < d; ++t) dot = fmaf(qs[t], kr[t], dot);
+        sc[j] = dot * scale;
+    }
+    if constexpr (VLDS) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float mx = -INFINITY;
+        for (int64_t j = lane; j < sk; j += 64) mx = fmaxf(mx, sc[j]);
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        if (lane == 0) stat[0] = mx;
+    }
+    __syncthreads();
+    const float mx = stat[0];
+    for (int64_t j = threadIdx.x; j < sk; j += kT) sc[j] = expf(sc[j] - mx);
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float sum = 0.0f;
+        for (int64_t j = lane; j < sk; j += 64) sum += sc[j];
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (lane == 0) stat[1] = sum;
+    }
+    __syncthreads();
+    const float sum = stat[1];
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    for (int64_t t = threadIdx.x; t < dv; t += kT) {
+        float acc = 0.0f;
+        int64_t j = 0;
+        if constexpr (VLDS) {
+            for (; j + 16 <= sk; j += 16) {
+                float vv[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) vv[u] = vs[(j + u) * dv + t];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) acc = fmaf(sc[j + u], vv[u], acc);
+            }
+            for (; j < sk; ++j) acc = fmaf(sc[j], vs[j * dv + t], acc);
+        } else {
+            for (; j + 32 <= sk; j += 32) {
+                float vv[32];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) vv[u] = vb[(j + u) * dv + t];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) acc = fmaf(sc[j + u], vv[u], acc);
+            }
+            for (; j < sk; ++j) acc = fmaf(sc[j], vb[j * dv + t], acc);
+        }
+        o[row * dv + t] = acc * inv;
+    }
+}
+
 // ---- Decode attention as the reference graph's unfused chain computes it
 // (llama_graph.cpp:95-107: RepeatKV on K and V, Transpose of K, MatMul,
 // Softmax, MatMul) for one query row per head, in one launch: one
@@ -476,7 +580,18 @@ namespace {
 
 hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 
-constexpr size_t kChainMaxLds = 160 * 1024;   // dynamic LDS of the V-staging chain kernel (no static LDS)
+constexpr size_t kChainMaxLds = 160 * 1024;   // dynamic LDS of the V-staging attention kernels (no static LDS)
+
+// Raises both kernels' dynamic LDS limit to kChainMaxLds; false (the error
+// cleared) when the runtime refuses, which keeps launches on their
+// global-memory forms.
+bool raise_lds_limit(const void* a, const void* b) {
+    hipError_t e = hipFuncSetAttribute(a, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kChainMaxLds));
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(b, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kChainMaxLds));
+    if (e != hipSuccess) (void)hipGetLastError();
+    return e == hipSuccess;
+}
 
 }  // namespace
 
@@ -661,15 +776,8 @@ int vm_hip_attention_decode_chain_f32(const float* q, const float* k, const floa
     const size_t lds_v = lds + static_cast<size_t>(s * dv) * sizeof(float);
     // The dynamic LDS limit is raised once per process (a refusal, cleared
     // here, keeps every launch on the global-memory form).
-    static const bool big_lds = [] {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_decode_chain_kernel<true>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kChainMaxLds));
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_decode_chain_kernel<false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kChainMaxLds));
-        if (e != hipSuccess) (void)hipGetLastError();
-        return e == hipSuccess;
-    }();
+    static const bool big_lds = raise_lds_limit(reinterpret_cast<const void*>(&attention_decode_chain_kernel<true>),
+                                                reinterpret_cast<const void*>(&attention_decode_chain_kernel<false>));
     const bool vlds = big_lds && dv % 4 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && lds_v <= kChainMaxLds;
     if (vlds) {
         hipLaunchKernelGGL(attention_decode_chain_kernel<true>, dim3(static_cast<unsigned>(hq)), dim3(kT), lds_v,
@@ -695,6 +803,20 @@ int vm_hip_attention_f32(const float* q, const float* k, const float* v, float* 
     if (lds > 64 * 1024) return fail_inval("FusedAttention: Sk + D exceeds 16384 on this kernel");
     if (rows > 0x7fffffff) return fail_inval("FusedAttention: too many rows");
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(d));
+    if (sq == 1 && sk > 0) {
+        // One query row per head: four waves per row, V in LDS when it fits.
+        static const bool big_lds = raise_lds_limit(reinterpret_cast<const void*>(&attention_row_kernel<true>),
+                                                    reinterpret_cast<const void*>(&attention_row_kernel<false>));
+        const size_t row_lds = static_cast<size_t>(d + sk + 2) * sizeof(float);
+        const size_t row_lds_v = row_lds + static_cast<size_t>(sk * dv) * sizeof(float);
+        if (big_lds && dv % 4 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && row_lds_v <= kChainMaxLds)
+            hipLaunchKernelGGL(attention_row_kernel<true>, dim3(static_cast<unsigned>(rows)), dim3(kT), row_lds_v,
+                               S(stream), q, k, v, o, hq, hk, sk, d, dv, sc);
+        else
+            hipLaunchKernelGGL(attention_row_kernel<false>, dim3(static_cast<unsigned>(rows)), dim3(kT), row_lds,
+                               S(stream), q, k, v, o, hq, hk, sk, d, dv, sc);
+        return check_launch("FusedAttention", S(stream));
+    }
     hipLaunchKernelGGL(attention_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), static_cast<size_t>(lds),
                        S(stream), q, k, v, o, hq, hk, sq, sk, d, dv, sc, causal ? 1 : 0);
     return check_launch("FusedAttention", S(stream));
