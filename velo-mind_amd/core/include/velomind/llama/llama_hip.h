@@ -86,7 +86,7 @@ public:
     // [0] building each step's Graph (nodes, shapes, bound weights), [1]
     // Graph::build on HIP, [2] Executable::execute (launches and the final
     // drain), [3] reading the logits back; [4] the number of steps.
-    auto step_timing() const noexcept -> const std::array<double, 5>& { return _timing; }
+    auto step_timing() const noexcept -> const std::array<double, 6>& { return _timing; }
 
 private:
     void bind(Graph& g, ForwardWeights& w) const;
@@ -98,7 +98,7 @@ private:
     std::vector<std::shared_ptr<TensorStorage>> _lin, _scale;  // [7 * layers + 1]
     std::vector<std::shared_ptr<TensorStorage>> _k, _v;        // per layer, [Hkv, S, D]
     std::size_t _seq_len = 0;
-    std::array<double, 5> _timing{};
+    std::array<double, 6> _timing{};
 };
 
 class PackedLlamaWeights;

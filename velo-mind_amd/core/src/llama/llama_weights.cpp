@@ -213,43 +213,48 @@ auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std
     const auto t0 = clock::now();
     const auto& cfg = _weights->config();
     const auto half = static_cast<dim_t>(cfg.head_dim() / 2);
-    Graph g;
-    auto tok = g.input({1}, DataType::Int32);
-    ForwardWeights w;
-    bind(g, w);
-    w.cos_cache = g.input({1, half}, DataType::Float32);
-    w.sin_cache = g.input({1, half}, DataType::Float32);
-    KVCacheHandles kv_in, kv_out;
-    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
-        kv_in.k.push_back(g.input(_k[l]));
-        kv_in.v.push_back(g.input(_v[l]));
-    }
-    auto logits = build_forward_graph_decode(g, cfg, tok, w, kv_in, &kv_out);
-    const auto t1 = clock::now();
-    auto exec = g.build(DeviceType::HIP);
-    const std::int32_t one[1] = {token};
-    tok.copy_from_host(std::as_bytes(std::span(one)));
-    std::vector<float> c, sn;
-    compute_rope_cache(1, cfg.head_dim(), cfg.rope_theta, c, sn, pos);
-    w.cos_cache.copy_from_host(std::as_bytes(std::span(c)));
-    w.sin_cache.copy_from_host(std::as_bytes(std::span(sn)));
-    const auto t2 = clock::now();
-    exec->execute();
-    const auto t3 = clock::now();
-    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
-        _k[l] = kv_out.k[l].shared_storage();
-        _v[l] = kv_out.v[l].shared_storage();
-    }
-    _seq_len = pos + 1;
     std::vector<float> out(cfg.vocab_size);
-    logits.copy_to_host(std::as_writable_bytes(std::span(out)));
-    const auto t4 = clock::now();
+    clock::time_point t1, t2, t3, t4;
+    {
+        Graph g;
+        auto tok = g.input({1}, DataType::Int32);
+        ForwardWeights w;
+        bind(g, w);
+        w.cos_cache = g.input({1, half}, DataType::Float32);
+        w.sin_cache = g.input({1, half}, DataType::Float32);
+        KVCacheHandles kv_in, kv_out;
+        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+            kv_in.k.push_back(g.input(_k[l]));
+            kv_in.v.push_back(g.input(_v[l]));
+        }
+        auto logits = build_forward_graph_decode(g, cfg, tok, w, kv_in, &kv_out);
+        t1 = clock::now();
+        auto exec = g.build(DeviceType::HIP);
+        const std::int32_t one[1] = {token};
+        tok.copy_from_host(std::as_bytes(std::span(one)));
+        std::vector<float> c, sn;
+        compute_rope_cache(1, cfg.head_dim(), cfg.rope_theta, c, sn, pos);
+        w.cos_cache.copy_from_host(std::as_bytes(std::span(c)));
+        w.sin_cache.copy_from_host(std::as_bytes(std::span(sn)));
+        t2 = clock::now();
+        exec->execute();
+        t3 = clock::now();
+        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+            _k[l] = kv_out.k[l].shared_storage();
+            _v[l] = kv_out.v[l].shared_storage();
+        }
+        _seq_len = pos + 1;
+        logits.copy_to_host(std::as_writable_bytes(std::span(out)));
+        t4 = clock::now();
+    }   // the step's Executable and Graph are destroyed here
+    const auto t5 = clock::now();
     auto sec = [](clock::time_point a, clock::time_point b) { return std::chrono::duration<double>(b - a).count(); };
     _timing[0] += sec(t0, t1);
     _timing[1] += sec(t1, t2);
     _timing[2] += sec(t2, t3);
     _timing[3] += sec(t3, t4);
     _timing[4] += 1.0;
+    _timing[5] += sec(t4, t5);
     return out;
 }
 
