@@ -340,10 +340,13 @@ __device__ __forceinline__ void gemv_body(
     // staging loads so that the norm adds no memory round trip: the first
     // kNormRegs elements of this thread's stride of each row (the sum of
     // squares) and of norm_w for the first kNormRegs staged elements it
-    // scales.  Rows longer than that load the rest after the barrier.
-    constexpr int kNormRegs = 8;
-    float nv[MR][kNormRegs];
-    float nwv[kNormRegs];
+    // scales (one row's worth, shared by the rows).  Rows longer than that
+    // load the rest after the barrier.
+    // 1024-thread workgroups (at most 128 VGPRs) keep no such registers:
+    // they would spill, so they load everything after the barrier.
+    constexpr int kNormRegs = W >= 16 ? 0 : 8;
+    float nv[MR][kNormRegs > 0 ? kNormRegs : 1];
+    float nwv[kNormRegs > 0 ? kNormRegs : 1];
     if constexpr (FX) {
         if (fx.norm_w) {
             const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
@@ -361,12 +364,9 @@ __device__ __forceinline__ void gemv_body(
                 }
 #pragma unroll
             for (int j = 0; j < kNormRegs; ++j) {
-                const int e = static_cast<int>(threadIdx.x) + j * W * 64;
-                int r = 0;
-#pragma unroll
-                for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
-                const int kk = k_begin + (e - r * xs_len);
-                const uint32_t off = (e < MR * xs_len && kk < k) ? static_cast<uint32_t>(kk) * 4u : w_bytes;
+                const int e = static_cast<int>(threadIdx.x) + j * W * 64;   // element of a staged row
+                const int kk = k_begin + e;
+                const uint32_t off = (e < xs_len && kk < k) ? static_cast<uint32_t>(kk) * 4u : w_bytes;
                 nwv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, static_cast<int>(off), 0, 0));
             }
         }
@@ -451,9 +451,8 @@ __device__ __forceinline__ void gemv_body(
         __shared__ float norm_part[MR][4];
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
-            if (r >= m) break;
             float sq = 0.0f;
-            if (threadIdx.x < 256) {
+            if (r < m && threadIdx.x < 256) {
 #pragma unroll
                 for (int j = 0; j < kNormRegs; ++j)
                     if (static_cast<int>(threadIdx.x) + 256 * j < k) sq = fmaf(nv[r][j], nv[r][j], sq);
@@ -463,7 +462,7 @@ __device__ __forceinline__ void gemv_body(
                 }
             }
             for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
-            if (threadIdx.x < 256 && lane == 0) norm_part[r][wave] = sq;
+            if (r < m && threadIdx.x < 256 && lane == 0) norm_part[r][wave] = sq;
         }
         __syncthreads();
         float inv[MR];
@@ -475,27 +474,18 @@ __device__ __forceinline__ void gemv_body(
                 for (int w = 0; w < 4; ++w) tot += norm_part[r][w];
             inv[r] = 1.0f / sqrtf(tot / static_cast<float>(k) + fx.norm_eps);
         }
-        auto scale_one = [&](int e, float wv) {
-            int r = 0;
+        // Row by row, so that each row's 1/rms is a register.
 #pragma unroll
-            for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
-            const int kk = k_begin + (e - r * xs_len);
-            float rinv = inv[0];
+        for (int r = 0; r < MR; ++r) {
+            if (r >= m) continue;
+            float* xr = xs + r * xs_len;
 #pragma unroll
-            for (int i = 1; i < MR; ++i) rinv = r == i ? inv[i] : rinv;
-            if (r < m && kk < k) xs[e] = (xs[e] * rinv) * wv;
-        };
-#pragma unroll
-        for (int j = 0; j < kNormRegs; ++j) {
-            const int e = static_cast<int>(threadIdx.x) + j * W * 64;
-            if (e < MR * xs_len) scale_one(e, nwv[j]);
-        }
-        for (int e = threadIdx.x + kNormRegs * W * 64; e < MR * xs_len; e += W * 64) {
-            int r = 0;
-#pragma unroll
-            for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
-            const int kk = k_begin + (e - r * xs_len);
-            scale_one(e, kk < k ? fx.norm_w[kk] : 0.0f);
+            for (int j = 0; j < kNormRegs; ++j) {
+                const int e = static_cast<int>(threadIdx.x) + j * W * 64;
+                if (e < xs_len && k_begin + e < k) xr[e] = (xr[e] * inv[r]) * nwv[j];
+            }
+            for (int e = threadIdx.x + kNormRegs * W * 64; e < xs_len; e += W * 64)
+                if (k_begin + e < k) xr[e] = (xr[e] * inv[r]) * fx.norm_w[k_begin + e];
         }
         __syncthreads();
     }
