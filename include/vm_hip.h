@@ -133,9 +133,10 @@ int vm_hip_graph_destroy(void* graph_exec);
  * Accumulation is fp32.  rows_m <= 4 runs the HBM-bound GEMV kernels;
  * larger rows_m runs the MFMA GEMM, which carries each row of A as two
  * fp16 parts under a power-of-two row scale (22 significant bits for any
- * finite fp32 A; INT8 codes are exact in fp16, per-column scales apply in
- * fp32, blockwise weights are staged as fp16(code * scale / 2^e)).  k == 0
- * writes zeros; rows_m == 0 or n == 0 is a no-op.
+ * finite fp32 A); codes are exact in fp16, per-column scales multiply each
+ * fp32 result and blockwise scales each 32-row chunk's fp32 sum, as the
+ * reference does (quantized_matmul.cpp:76-90).  k == 0 writes zeros;
+ * rows_m == 0 or n == 0 is a no-op.
  */
 int vm_hip_qmm_f32(const float* a, const int8_t* wq, const float* scale, float* c,
                    int64_t rows_m, int64_t k, int64_t n, int quant_type, int block_size,
