@@ -26,6 +26,7 @@ namespace velomind {
 class Executable;
 namespace internal {
 class GraphCompiler;
+class TensorIndex;
 }
 
 template <typename T>
@@ -108,6 +109,8 @@ private:
     // validate()'s checks; returns the topological order of the required
     // nodes (the build's order, computed once).
     auto _validated_order(DeviceType device) const -> std::vector<pConstNode>;
+    // The same with the caller's index of _tensors (the build reuses it).
+    auto _validated_order(DeviceType device, const internal::TensorIndex& index) const -> std::vector<pConstNode>;
 
     friend struct GraphTestAccess;
     friend class internal::GraphCompiler;

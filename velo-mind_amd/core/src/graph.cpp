@@ -157,23 +157,44 @@ std::size_t producer_of(pConstTensorStorage s, const internal::TensorIndex& inde
     return t == internal::TensorIndex::npos ? SIZE_MAX : producer[t];
 }
 
+// The producing node of every node input (SIZE_MAX: nothing writes it), as
+// compressed rows: node v's inputs are node[first[v] .. first[v + 1]).
+// Found once, for the passes that walk the graph's edges.
+struct InputProducers {
+    std::vector<std::size_t> first, node;
+};
+
+InputProducers input_producers(const std::vector<Node>& nodes, const internal::TensorIndex& index,
+                               const std::vector<std::size_t>& producer) {
+    InputProducers ip;
+    ip.first.resize(nodes.size() + 1, 0);
+    std::size_t edges = 0;
+    for (std::size_t v = 0; v < nodes.size(); ++v) edges += nodes[v].inputs().size();
+    ip.node.reserve(edges);
+    for (std::size_t v = 0; v < nodes.size(); ++v) {
+        for (auto* in : nodes[v].inputs()) ip.node.push_back(producer_of(in, index, producer));
+        ip.first[v + 1] = ip.node.size();
+    }
+    return ip;
+}
+
 // Nodes reachable backwards from the explicit outputs.
 std::vector<bool> required_nodes(const std::vector<Node>& nodes, const std::vector<pConstTensorStorage>& outputs,
-                                 const internal::TensorIndex& index, const std::vector<std::size_t>& producer) {
+                                 const internal::TensorIndex& index, const std::vector<std::size_t>& producer,
+                                 const InputProducers& ip) {
     std::vector<bool> req(nodes.size(), false);
     std::vector<std::size_t> stack;
-    auto reach = [&](pConstTensorStorage s) {
-        const std::size_t p = producer_of(s, index, producer);
+    auto reach = [&](std::size_t p) {
         if (p != SIZE_MAX && !req[p]) {
             req[p] = true;
             stack.push_back(p);
         }
     };
-    for (auto* s : outputs) reach(s);
+    for (auto* s : outputs) reach(producer_of(s, index, producer));
     while (!stack.empty()) {
         const std::size_t u = stack.back();
         stack.pop_back();
-        for (auto* in : nodes[u].inputs()) reach(in);
+        for (std::size_t e = ip.first[u]; e < ip.first[u + 1]; ++e) reach(ip.node[e]);
     }
     return req;
 }
@@ -181,7 +202,7 @@ std::vector<bool> required_nodes(const std::vector<Node>& nodes, const std::vect
 // Kahn's algorithm over the required nodes, in insertion order among ready
 // nodes (FIFO); throws on a cycle.
 std::vector<pConstNode> topological(const std::vector<Node>& nodes, const std::vector<bool>& req,
-                                    const internal::TensorIndex& index, const std::vector<std::size_t>& producer) {
+                                    const InputProducers& ip) {
     const std::size_t n = nodes.size();
     std::vector<std::size_t> indeg(n, 0), deps, edge_u, edge_v;
     std::size_t active = 0;
@@ -189,8 +210,8 @@ std::vector<pConstNode> topological(const std::vector<Node>& nodes, const std::v
         if (!req[v]) continue;
         ++active;
         deps.clear();
-        for (auto* in : nodes[v].inputs()) {
-            const std::size_t p = producer_of(in, index, producer);
+        for (std::size_t e = ip.first[v]; e < ip.first[v + 1]; ++e) {
+            const std::size_t p = ip.node[e];
             if (p != SIZE_MAX && req[p]) deps.push_back(p);
         }
         std::sort(deps.begin(), deps.end());
@@ -229,19 +250,25 @@ std::vector<pConstNode> topological(const std::vector<Node>& nodes, const std::v
 auto Graph::_compute_required_nodes() const -> std::vector<bool> {
     if (!_has_explicit_outputs) return std::vector<bool>(_nodes.size(), true);
     const internal::TensorIndex index(_tensors);
-    return required_nodes(_nodes, _explicit_outputs, index, producers_of(_nodes, index, _tensors.size()));
+    const auto producer = producers_of(_nodes, index, _tensors.size());
+    return required_nodes(_nodes, _explicit_outputs, index, producer, input_producers(_nodes, index, producer));
 }
 
 auto Graph::_topological_order() const -> std::vector<pConstNode> { return _topological_order(_compute_required_nodes()); }
 
 auto Graph::_topological_order(const std::vector<bool>& req) const -> std::vector<pConstNode> {
     const internal::TensorIndex index(_tensors);
-    return topological(_nodes, req, index, producers_of(_nodes, index, _tensors.size()));
+    return topological(_nodes, req, input_producers(_nodes, index, producers_of(_nodes, index, _tensors.size())));
 }
 
 auto Graph::validate(DeviceType device) const -> void { (void)_validated_order(device); }
 
 auto Graph::_validated_order(DeviceType device) const -> std::vector<pConstNode> {
+    if (_built) throw std::logic_error("Graph::validate: graph is already built");
+    return _validated_order(device, internal::TensorIndex(_tensors));
+}
+
+auto Graph::_validated_order(DeviceType device, const internal::TensorIndex& index) const -> std::vector<pConstNode> {
     if (_built) throw std::logic_error("Graph::validate: graph is already built");
     if (static_cast<std::size_t>(device) >= MAX_DEVICE_TYPES) throw std::invalid_argument("Graph::validate: invalid device");
     for (const auto& s : _tensors) {
@@ -249,9 +276,9 @@ auto Graph::_validated_order(DeviceType device) const -> std::vector<pConstNode>
         if (s->data != nullptr && s->device != device)
             throw std::invalid_argument("Graph::validate: populated storage belongs to another device");
     }
-    const internal::TensorIndex index(_tensors);
     const auto producer = producers_of(_nodes, index, _tensors.size());
-    const auto req = _has_explicit_outputs ? required_nodes(_nodes, _explicit_outputs, index, producer)
+    const auto ip = input_producers(_nodes, index, producer);
+    const auto req = _has_explicit_outputs ? required_nodes(_nodes, _explicit_outputs, index, producer, ip)
                                            : std::vector<bool>(_nodes.size(), true);
     for (std::size_t i = 0; i < _nodes.size(); ++i) {
         if (!req[i]) continue;
@@ -270,7 +297,7 @@ auto Graph::_validated_order(DeviceType device) const -> std::vector<pConstNode>
                                                    device))
             throw std::invalid_argument(std::string("Graph::validate: unsupported kernel for ") + op_name(n.op().op));
     }
-    return topological(_nodes, req, index, producer);
+    return topological(_nodes, req, ip);
 }
 
 auto Graph::build(DeviceType device) -> std::unique_ptr<Executable> {

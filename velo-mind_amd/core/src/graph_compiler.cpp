@@ -554,9 +554,9 @@ std::shared_ptr<TensorStorage> allocate_checked(std::size_t bytes, DeviceType de
 
 auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<Executable> {
     if (graph._built) throw std::logic_error("Graph::build: graph is already built");
-    const auto order = graph._validated_order(device);
     const auto& tensors = graph._tensors;
     const TensorIndex index(tensors);
+    const auto order = graph._validated_order(device, index);
 
     // Dedicated allocations: requested outputs (every tensor when none were
     // marked), graph inputs and tensors that already own data.
