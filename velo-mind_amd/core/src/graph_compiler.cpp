@@ -124,8 +124,13 @@ struct Step {
     std::shared_ptr<const void> attrs;        // fused: what the kernel takes as attrs, if anything
 };
 
-std::shared_ptr<const void> desc_copy(const OpDescriptor& d) {
-    return std::shared_ptr<const void>(new OpDescriptor(d), [](const void* p) { delete static_cast<const OpDescriptor*>(p); });
+// A node's descriptor as kernel attributes, without a copy: the executable
+// runs only while its graph lives (Executable::execute checks the graph's
+// lifetime first) and a built graph's nodes never move, so the pointer
+// into the node stays valid for every run (an aliasing shared_ptr that owns
+// nothing).
+std::shared_ptr<const void> node_desc(const OpDescriptor& d) {
+    return std::shared_ptr<const void>(std::shared_ptr<const void>{}, &d);
 }
 
 const QuantizedMatMulAttrs* qmm_attrs(pConstNode n) {
@@ -389,13 +394,13 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
                     f.fused = static_cast<int>(FusedKind::SwigluQmmAdd);
                     f.ins = {steps[sa].ins[0], steps[sa].ins[1], q[1], q[2], h};
                     f.outs = {out};
-                    f.attrs = desc_copy(node_of(sq)->op());
+                    f.attrs = node_desc(node_of(sq)->op());
                     dead[sa] = true;
                     dead[sq] = true;
                     steps[j] = std::move(f);
                     break;
                 }
-                make(j, FusedKind::QmmAdd, {sq}, {q[0], q[1], q[2], h}, desc_copy(node_of(sq)->op()));
+                make(j, FusedKind::QmmAdd, {sq}, {q[0], q[1], q[2], h}, node_desc(node_of(sq)->op()));
                 break;
             }
             continue;
@@ -497,7 +502,7 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
             const auto* k = unrepeat(ins[1], absorbed);
             const auto* v = unrepeat(ins[2], absorbed);
             if (absorbed.size() != 2 || k->shape[0] != v->shape[0]) continue;
-            make(j, FusedKind::AttentionGqa, absorbed, {ins[0], k, v}, desc_copy(n->op()));
+            make(j, FusedKind::AttentionGqa, absorbed, {ins[0], k, v}, node_desc(n->op()));
             continue;
         }
     }
@@ -747,6 +752,8 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         if (step.fused >= 0) {
             // fused chain: its external operands, in the order its kind lists them
             Executable::CompiledNode cn;
+            cn.inputs.reserve(step.ins.size());
+            cn.outputs.reserve(step.outs.size());
             for (auto* in : step.ins) cn.inputs.push_back(remap(in));
             for (auto* out : step.outs) cn.outputs.push_back(remap(out));
             cn.kernel = fused_kernel(device, static_cast<FusedKind>(step.fused));
@@ -758,6 +765,8 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         if (step.nodes.size() > 1) {
             // grouped QuantizedMatMul: [A, B_1, S_1, ..], [C_1, ..]
             Executable::CompiledNode cn;
+            cn.inputs.reserve(1 + 2 * step.nodes.size());
+            cn.outputs.reserve(step.nodes.size());
             cn.inputs.push_back(remap(step.nodes.front()->inputs()[0]));
             for (const auto* node : step.nodes) {
                 cn.inputs.push_back(remap(node->inputs()[1]));
@@ -776,6 +785,8 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         const bool aliased = alias_step[static_cast<std::size_t>(&step - steps.data())];
         DataType dtypes[4];
         std::size_t n_in = 0;
+        cn.inputs.reserve(node->inputs().size());
+        cn.outputs.reserve(node->outputs().size());
         for (auto* in : node->inputs()) {
             cn.inputs.push_back(remap(in));
             if (n_in < 4) dtypes[n_in] = in->dtype;
@@ -788,8 +799,7 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
                                         : resolve_op_kernel(node->op().op, std::span<const DataType>(dtypes, n_in),
                                                             node->outputs().front()->dtype, device));
         if (!cn.kernel) throw std::runtime_error(std::string("velomind: no kernel for op=") + op_name(node->op().op));
-        cn.attrs = std::shared_ptr<const void>(new OpDescriptor(node->op()),
-                                               [](const void* p) { delete static_cast<const OpDescriptor*>(p); });
+        cn.attrs = node_desc(node->op());
         impl->topo.push_back(std::move(cn));
     }
     impl->derive_run_plan();
