@@ -5,6 +5,7 @@
 // tests/test_quantization.cpp:57-98 and :413-478, tests/test_basic.cpp:139-145
 // and tests/test_validation.cpp:133-167.
 #include <cstdlib>
+#include <memory>
 #include <cstring>
 #include <stdexcept>
 #include <variant>
@@ -318,6 +319,23 @@ TEST_CASE("CPU graph runs the oracle kernel end to end", "[core][oracle]") {
     vmo_qmm_2d_f32(a.data(), q.data(), s.data(), ref.data(), m, k, n, 1, 0);
     REQUIRE(max_abs_diff(out, ref) == 0.0f);
     REQUIRE_THROWS_AS(tc.copy_to_host(std::span<std::byte>()), std::runtime_error);
+}
+
+TEST_CASE("an executable whose graph is gone refuses to run", "[core][lifetime]") {
+    // Compiled nodes refer to their graph's operator descriptors, so running
+    // after the graph is destroyed must fail before any kernel reads them
+    // (the reference's executable.cpp contract).
+    std::unique_ptr<Executable> exec;
+    {
+        Graph g;
+        auto ta = g.input({2, 64}, DataType::Float32);
+        auto tw = g.input({64, 32}, DataType::Int8);
+        auto ts = g.input({32}, DataType::Float32);
+        (void)g.op(Op::QuantizedMatMul, ta, tw, ts);
+        exec = g.build(DeviceType::CPU);
+        REQUIRE_NOTHROW(exec->execute());
+    }
+    REQUIRE_THROWS_AS(exec->execute(), std::logic_error);
 }
 
 TEST_CASE("compute_quantization_metrics edge cases", "[core][metrics]") {
