@@ -584,6 +584,20 @@ int vm_hip_attention_decode_slices_prefetch_f32(const float* qkv, int64_t qkv_sl
                                                 int64_t head_dim, int64_t max_seq, float scale,
                                                 const vm_hip_prefetch* prefetch, void* stream);
 
+/* Asynchronous strided copy of one logical tensor of `rank` (1..8)
+ * dimensions `shape` whose elements are elem_bytes (1, 2 or 4) wide: the
+ * element at coordinates x goes from src + sum(x[d] * src_strides[d]) to
+ * dst + sum(x[d] * dst_strides[d]) (strides in elements, not negative).
+ * Gathers a strided view into a contiguous buffer or scatters one back; the
+ * caller guarantees both extents lie inside their allocations.  Backs the
+ * HIP QuantizedMatMul on strided operands, which the reference's CPU kernel
+ * honours (src/cpu/ops/quantized_matmul.cpp:306-315).  Overlapping
+ * destinations (a zero stride over a dimension longer than one) are the
+ * caller's to avoid. */
+#define VM_HIP_COPY_MAX_RANK 8
+int vm_hip_copy_strided(void* dst, const int64_t* dst_strides, const void* src, const int64_t* src_strides,
+                        const int64_t* shape, int rank, int elem_bytes, void* stream);
+
 /* Asynchronous 2-D device copy: `rows` rows of `width` bytes from src
  * (row pitch spitch) to dst (row pitch dpitch).  Used to assemble fused
  * weight matrices column block by column block. */

@@ -7,6 +7,7 @@
 // (tests/test_hip_graph_fusion.py).
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <variant>
 
 #include "internal/registry/kernel.h"
@@ -23,8 +24,20 @@ std::size_t numel(const TensorStorage& t) { return storage_numel(t); }
 
 float sigmoid_host(float x) { return 1.0f / (1.0f + std::exp(-x)); }
 
+// element e (row-major order of its shape) of an operand that may be strided
+float elem(const TensorStorage& t, std::size_t e) {
+    const auto st = t.effective_strides();
+    std::size_t off = 0;
+    for (std::size_t d = t.shape.size(); d-- > 0;) {
+        const auto extent = static_cast<std::size_t>(t.shape[d]);
+        off += (e % extent) * static_cast<std::size_t>(st[d]);
+        e /= extent;
+    }
+    return static_cast<const float*>(t.data)[off];
+}
+
 void add_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
-    for (std::size_t e = 0; e < numel(*out[0]); ++e) cout0(out)[e] = cin(in, 0)[e] + cin(in, 1)[e];
+    for (std::size_t e = 0; e < numel(*out[0]); ++e) cout0(out)[e] = elem(*in[0], e) + elem(*in[1], e);
 }
 void mul_cpu(const pConstTensorStorage* in, const pTensorStorage* out, const void*) {
     for (std::size_t e = 0; e < numel(*out[0]); ++e) cout0(out)[e] = cin(in, 0)[e] * cin(in, 1)[e];
@@ -229,13 +242,25 @@ struct MlpRun {
     std::size_t steps = 0, nodes = 0;
     bool inner_unallocated = false;
 };
-MlpRun run_mlp(bool fuse, bool keep_sigmoid, bool keep_act = false) {
+// strided_h: the residual is every other float of a host buffer (a view
+// input, as the reference's strided TensorStorage views are).
+MlpRun run_mlp(bool fuse, bool keep_sigmoid, bool keep_act = false, bool strided_h = false) {
     const std::size_t d = 64, f = 96;
     static const auto wg = int8_weights(d, f, 61), wu = int8_weights(d, f, 62), wd = int8_weights(f, d, 63);
     static const auto x = normal(d, 64), h = normal(d, 65);
     ScopedEnv env("VELOMIND_GRAPH_FUSE", fuse ? "1" : "0");
     Graph g;
-    auto tx = g.input({1, (dim_t)d}, F32), th = g.input({1, (dim_t)d}, F32);
+    std::vector<float> h_pitched(2 * d, -1.0f);
+    for (std::size_t j = 0; j < d; ++j) h_pitched[2 * j] = h[j];
+    auto h_view = std::make_shared<TensorStorage>();
+    h_view->shape = {1, (dim_t)d};
+    h_view->strides = {(dim_t)(2 * d), 2};
+    h_view->dtype = F32;
+    h_view->data = h_pitched.data();
+    h_view->size_bytes = d * 4;
+    h_view->capacity_bytes = h_pitched.size() * 4;
+    auto tx = g.input({1, (dim_t)d}, F32);
+    auto th = strided_h ? g.input(h_view) : g.input({1, (dim_t)d}, F32);
     auto tg = g.input({(dim_t)d, (dim_t)f}, DataType::Int8), tgs = g.input({(dim_t)f}, F32);
     auto tu = g.input({(dim_t)d, (dim_t)f}, DataType::Int8), tus = g.input({(dim_t)f}, F32);
     auto td = g.input({(dim_t)f, (dim_t)d}, DataType::Int8), tds = g.input({(dim_t)d}, F32);
@@ -257,7 +282,7 @@ MlpRun run_mlp(bool fuse, bool keep_sigmoid, bool keep_act = false) {
                           g.tensor_storage_at(y.index())->data == nullptr &&
                           (keep_act || g.tensor_storage_at(act.index())->data == nullptr);
     tx.copy_from_host(as_bytes(x));
-    th.copy_from_host(as_bytes(h));
+    if (!strided_h) th.copy_from_host(as_bytes(h));
     tg.copy_from_host(as_bytes(wg.q));
     tgs.copy_from_host(as_bytes(wg.s));
     tu.copy_from_host(as_bytes(wu.q));
@@ -324,6 +349,17 @@ TEST_CASE("fusion: SwiGLU chain, its QuantizedMatMul and the residual Add run as
     REQUIRE(kept.steps == 4);
     REQUIRE(kept.inner_unallocated);
     REQUIRE(std::memcmp(kept.out.data(), off.out.data(), off.out.size() * 4) == 0);
+}
+
+TEST_CASE("fusion: a chain with a strided external operand runs node by node", "[core][fusion]") {
+    // The fused kernels take dense operands: with the residual a strided
+    // view, SwigluQmmAdd splits back into its five nodes, with the same result.
+    const auto off = run_mlp(false, false);
+    const auto on = run_mlp(true, false, false, true);
+    REQUIRE(on.nodes == 7);
+    REQUIRE(on.steps == 7);
+    REQUIRE(!on.inner_unallocated);
+    REQUIRE(std::memcmp(on.out.data(), off.out.data(), on.out.size() * 4) == 0);
 }
 
 TEST_CASE("fusion: a kept inner tensor keeps its chain unfused", "[core][fusion]") {

@@ -8,9 +8,12 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
+#include <span>
 #include <stdexcept>
 #include <thread>
 
+#include "internal/registry/kernel.h"
 #include "internal/registry/storage.h"
 #include "test_helpers.h"
 
@@ -533,4 +536,260 @@ TEST_CASE("sibling QuantizedMatMuls sharing A run as one grouped step", "[gpu][q
             REQUIRE(max_abs_diff(grouped[i], single[i]) <= 1e-6f * max_abs(single[i]));
         }
     }
+}
+
+namespace {
+
+// A device copy of `v` with `pad_bytes` of zeros after it.
+std::shared_ptr<TensorStorage> device_copy(std::span<const std::byte> v, std::size_t pad_bytes = 0) {
+    auto s = TensorStorage::allocate(v.size() + pad_bytes, DeviceType::HIP);
+    REQUIRE(s);
+    std::vector<std::byte> host(v.begin(), v.end());
+    host.resize(v.size() + pad_bytes, std::byte{0});
+    REQUIRE(vm_hip_memcpy_h2d(s->data, host.data(), host.size(), nullptr) == 0);
+    return s;
+}
+
+// A strided view of `base` starting `offset` bytes in.
+std::shared_ptr<TensorStorage> view_of(const std::shared_ptr<TensorStorage>& base, shape_t shape, stride_t strides,
+                                       DataType dt, std::size_t offset = 0) {
+    auto v = std::make_shared<TensorStorage>();
+    v->shape = std::move(shape);
+    v->strides = std::move(strides);
+    v->dtype = dt;
+    v->device = DeviceType::HIP;
+    v->offset_bytes = base->offset_bytes + offset;
+    v->capacity_bytes = base->capacity_bytes ? base->capacity_bytes : base->size_bytes;
+    v->data = static_cast<std::byte*>(base->data) + offset;
+    v->size_bytes = storage_nbytes(*v);
+    v->external_owner = base;
+    return v;
+}
+
+template <typename T>
+std::vector<T> to_host(const TensorStorage& s, std::size_t count) {
+    std::vector<T> out(count);
+    REQUIRE(vm_hip_device_synchronize() == 0);
+    REQUIRE(vm_hip_memcpy_d2h(out.data(), s.data, count * sizeof(T), nullptr) == 0);
+    return out;
+}
+
+}  // namespace
+
+TEST_CASE("strided A, B and C on HIP match the contiguous operands bit for bit", "[gpu][quantization][strided]") {
+    // The reference's CPU kernel reads A and B through their strides and
+    // writes C through its strides (quantized_matmul.cpp:306-315); here
+    // the adapter gathers and scatters around the contiguous kernels.
+    REQUIRE_HIP();
+    const std::vector<DataType> key{DataType::Float32, DataType::Int8, DataType::Float32};
+    const auto fn = internal::resolve_op_kernel(Op::QuantizedMatMul, key, DataType::Float32, DeviceType::HIP);
+    REQUIRE(fn != nullptr);
+    const std::size_t k = 256, n = 192, pad = 16;
+    for (const int qt : {1, 2}) {
+        const int block = qt == 2 ? 32 : 0;
+        const OpDescriptor desc{Op::QuantizedMatMul,
+                                QuantizedMatMulAttrs{.quant_type = qt == 2 ? QuantType::Int4 : QuantType::Int8,
+                                                     .block_size = block}};
+        const std::size_t qrows = qt == 2 ? k / 2 : k;
+        const auto w = normal(k * n, 90 + qt, 0.05f);
+        std::vector<std::int8_t> q(qrows * n);
+        std::vector<float> s(qt == 2 ? (k / 32) * n : n);
+        if (qt == 2)
+            vmo_quantize_int4_block(w.data(), reinterpret_cast<std::uint8_t*>(q.data()), s.data(), k, n, 32);
+        else
+            vmo_quantize_int8_per_channel(w.data(), q.data(), s.data(), k, n);
+        // B padded to n + pad columns
+        std::vector<std::int8_t> q_pitched(qrows * (n + pad), 0);
+        for (std::size_t r = 0; r < qrows; ++r)
+            std::memcpy(q_pitched.data() + r * (n + pad), q.data() + r * n, n);
+        const auto dq = device_copy(as_bytes(q));
+        const auto dq_pitched = device_copy(as_bytes(q_pitched));
+        const auto ds = device_copy(as_bytes(s));
+        const auto wq_dense = view_of(dq, {(dim_t)qrows, (dim_t)n}, {}, DataType::Int8);
+        const auto wq_strided = view_of(dq_pitched, {(dim_t)qrows, (dim_t)n}, {(dim_t)(n + pad), 1}, DataType::Int8);
+        const auto sc = view_of(ds, {(dim_t)(s.size() / n), (dim_t)n}, {}, DataType::Float32);
+
+        for (std::size_t m : {1, 3, 16}) {
+            const auto a = normal(m * k, 100 + m);
+            auto call = [&](const std::shared_ptr<TensorStorage>& ta, const std::shared_ptr<TensorStorage>& tw,
+                            const std::shared_ptr<TensorStorage>& tc) {
+                const pConstTensorStorage ins[3] = {ta.get(), tw.get(), sc.get()};
+                const pTensorStorage outs[1] = {tc.get()};
+                fn(ins, outs, &desc);
+            };
+            // contiguous operands: the baseline, checked against the oracle
+            const auto da = device_copy(as_bytes(a));
+            const auto a_dense = view_of(da, {(dim_t)m, (dim_t)k}, {}, DataType::Float32);
+            auto dc = TensorStorage::allocate(m * n * 4, DeviceType::HIP);
+            const auto c_dense = view_of(dc, {(dim_t)m, (dim_t)n}, {}, DataType::Float32);
+            call(a_dense, wq_dense, c_dense);
+            const auto base = to_host<float>(*c_dense, m * n);
+            std::vector<float> ref(m * n);
+            vmo_qmm_2d_f32(a.data(), q.data(), s.data(), ref.data(), m, k, n, qt, block);
+            REQUIRE(max_abs_diff(base, ref) <= (m <= 4 ? 1e-5f : 1e-3f) * max_abs(ref));
+
+            auto same = [&](const std::vector<float>& got) {
+                REQUIRE(got.size() == base.size());
+                REQUIRE(std::memcmp(got.data(), base.data(), base.size() * 4) == 0);
+            };
+            // A with a row pitch of k + 8, 4 floats into its allocation
+            {
+                std::vector<float> a_pitched(4 + m * (k + 8), 9.0f);
+                for (std::size_t r = 0; r < m; ++r)
+                    std::memcpy(a_pitched.data() + 4 + r * (k + 8), a.data() + r * k, k * 4);
+                const auto d = device_copy(as_bytes(a_pitched));
+                const auto av = view_of(d, {(dim_t)m, (dim_t)k}, {(dim_t)(k + 8), 1}, DataType::Float32, 16);
+                REQUIRE(m == 1 || !av->is_contiguous());   // one row: any pitch is dense
+                auto dc2 = TensorStorage::allocate(m * n * 4, DeviceType::HIP);
+                const auto c2 = view_of(dc2, {(dim_t)m, (dim_t)n}, {}, DataType::Float32);
+                call(av, wq_dense, c2);
+                same(to_host<float>(*c2, m * n));
+            }
+            // A transposed: the [k, m] array read as [m, k] with strides {1, m}
+            if (m > 1) {
+                std::vector<float> at(k * m);
+                for (std::size_t r = 0; r < m; ++r)
+                    for (std::size_t j = 0; j < k; ++j) at[j * m + r] = a[r * k + j];
+                const auto d = device_copy(as_bytes(at));
+                const auto av = view_of(d, {(dim_t)m, (dim_t)k}, {1, (dim_t)m}, DataType::Float32);
+                auto dc2 = TensorStorage::allocate(m * n * 4, DeviceType::HIP);
+                const auto c2 = view_of(dc2, {(dim_t)m, (dim_t)n}, {}, DataType::Float32);
+                call(av, wq_dense, c2);
+                same(to_host<float>(*c2, m * n));
+            }
+            // B with a row pitch of n + pad
+            {
+                auto dc2 = TensorStorage::allocate(m * n * 4, DeviceType::HIP);
+                const auto c2 = view_of(dc2, {(dim_t)m, (dim_t)n}, {}, DataType::Float32);
+                call(a_dense, wq_strided, c2);
+                same(to_host<float>(*c2, m * n));
+            }
+            // C written into columns [0, n) of an [m, n + pad] array: the
+            // pad columns keep their values
+            {
+                const std::vector<float> sentinel(m * (n + pad), 7.0f);
+                const auto d = device_copy(as_bytes(sentinel));
+                const auto cv = view_of(d, {(dim_t)m, (dim_t)n}, {(dim_t)(n + pad), 1}, DataType::Float32);
+                call(a_dense, wq_dense, cv);
+                const auto all = to_host<float>(*d, m * (n + pad));
+                std::vector<float> got(m * n);
+                for (std::size_t r = 0; r < m; ++r) {
+                    std::memcpy(got.data() + r * n, all.data() + r * (n + pad), n * 4);
+                    for (std::size_t j = n; j < n + pad; ++j) REQUIRE(all[r * (n + pad) + j] == 7.0f);
+                }
+                same(got);
+            }
+            // A as [2, m, k] batches with a gap of one row between them
+            // (rows 0..m-1 then m+1..2m): C [2, m, n] against the dense call
+            // on the gathered rows
+            {
+                const auto a2 = normal(2 * m * k, 200 + m);
+                std::vector<float> a_gap((2 * m + 1) * k, 5.0f);
+                for (std::size_t b = 0; b < 2; ++b)
+                    std::memcpy(a_gap.data() + b * (m + 1) * k, a2.data() + b * m * k, m * k * 4);
+                const auto dg = device_copy(as_bytes(a_gap));
+                const auto av = view_of(dg, {2, (dim_t)m, (dim_t)k}, {(dim_t)((m + 1) * k), (dim_t)k, 1},
+                                        DataType::Float32);
+                const auto dd = device_copy(as_bytes(a2));
+                const auto ad = view_of(dd, {2, (dim_t)m, (dim_t)k}, {}, DataType::Float32);
+                auto c_gap = TensorStorage::allocate(2 * m * n * 4, DeviceType::HIP);
+                auto c_ref = TensorStorage::allocate(2 * m * n * 4, DeviceType::HIP);
+                const auto cg = view_of(c_gap, {2, (dim_t)m, (dim_t)n}, {}, DataType::Float32);
+                const auto cr = view_of(c_ref, {2, (dim_t)m, (dim_t)n}, {}, DataType::Float32);
+                call(ad, wq_dense, cr);
+                call(av, wq_dense, cg);
+                const auto want = to_host<float>(*cr, 2 * m * n);
+                const auto got = to_host<float>(*cg, 2 * m * n);
+                REQUIRE(std::memcmp(got.data(), want.data(), want.size() * 4) == 0);
+            }
+        }
+    }
+}
+
+TEST_CASE("strided operands that overlap or overrun are refused before any launch", "[gpu][quantization][strided]") {
+    REQUIRE_HIP();
+    const std::vector<DataType> key{DataType::Float32, DataType::Int8, DataType::Float32};
+    const auto fn = internal::resolve_op_kernel(Op::QuantizedMatMul, key, DataType::Float32, DeviceType::HIP);
+    REQUIRE(fn != nullptr);
+    const std::size_t m = 2, k = 64, n = 32;
+    const OpDescriptor desc{Op::QuantizedMatMul, QuantizedMatMulAttrs{.quant_type = QuantType::Int8, .block_size = 0}};
+    const auto da = device_copy(as_bytes(normal(m * k, 1)));
+    const auto dw = device_copy(as_bytes(std::vector<std::int8_t>(k * n, 1)));
+    const auto ds = device_copy(as_bytes(std::vector<float>(n, 0.5f)));
+    const auto dc = device_copy(as_bytes(std::vector<float>(m * n, 0.0f)));
+    const auto a = view_of(da, {(dim_t)m, (dim_t)k}, {}, DataType::Float32);
+    const auto w = view_of(dw, {(dim_t)k, (dim_t)n}, {}, DataType::Int8);
+    const auto s = view_of(ds, {(dim_t)n}, {}, DataType::Float32);
+    auto call = [&](const std::shared_ptr<TensorStorage>& ta, const std::shared_ptr<TensorStorage>& tc) {
+        const pConstTensorStorage ins[3] = {ta.get(), w.get(), s.get()};
+        const pTensorStorage outs[1] = {tc.get()};
+        fn(ins, outs, &desc);
+    };
+    // both rows of C on the same addresses
+    REQUIRE_THROWS_AS(call(a, view_of(dc, {(dim_t)m, (dim_t)n}, {0, 1}, DataType::Float32)), std::invalid_argument);
+    // rows half a row apart: row 1 overlaps row 0
+    REQUIRE_THROWS_AS(call(a, view_of(dc, {(dim_t)m, (dim_t)n}, {(dim_t)(n / 2), 1}, DataType::Float32)),
+                      std::invalid_argument);
+    // A's row pitch reaching past its allocation (declared as exactly m * k floats)
+    auto overrun = view_of(da, {(dim_t)m, (dim_t)k}, {(dim_t)(k + 1), 1}, DataType::Float32);
+    overrun->capacity_bytes = m * k * 4;
+    REQUIRE_THROWS_AS(call(overrun, view_of(dc, {(dim_t)m, (dim_t)n}, {}, DataType::Float32)), std::invalid_argument);
+    // a repeated A row (stride 0) is a legal read
+    call(view_of(da, {(dim_t)m, (dim_t)k}, {0, 1}, DataType::Float32),
+         view_of(dc, {(dim_t)m, (dim_t)n}, {}, DataType::Float32));
+    const auto c = to_host<float>(*dc, m * n);
+    REQUIRE(std::memcmp(c.data(), c.data() + n, n * 4) == 0);
+}
+
+TEST_CASE("a graph on a strided input view keeps its QuantizedMatMul + Add unfused", "[gpu][quantization][strided]") {
+    // x is every other row of a device array: the residual Add stays out
+    // of the second product's launch (the fused kernel takes dense operands
+    // only), and both outputs equal the dense graph's bit for bit.
+    REQUIRE_HIP();
+    const std::size_t m = 2, k = 128, n = 128;
+    const auto xv = normal(m * k, 301), hv = normal(m * n, 302);
+    const auto w1 = normal(k * n, 303, 0.05f), w2 = normal(k * n, 304, 0.05f);
+    std::vector<std::int8_t> q1(k * n), q2(k * n);
+    std::vector<float> s1(n), s2(n);
+    vmo_quantize_int8_per_channel(w1.data(), q1.data(), s1.data(), k, n);
+    vmo_quantize_int8_per_channel(w2.data(), q2.data(), s2.data(), k, n);
+    std::vector<float> x_gapped(2 * m * k, 3.0f);
+    for (std::size_t r = 0; r < m; ++r) std::memcpy(x_gapped.data() + 2 * r * k, xv.data() + r * k, k * 4);
+    const auto dx = device_copy(as_bytes(x_gapped));
+    auto run = [&](bool strided, std::size_t* steps) {
+        ScopedEnv env("VELOMIND_GROUP_QMM", "0");
+        Graph g;
+        auto x = strided ? g.input(view_of(dx, {(dim_t)m, (dim_t)k}, {(dim_t)(2 * k), 1}, DataType::Float32))
+                         : g.input({(dim_t)m, (dim_t)k}, DataType::Float32);
+        auto h = g.input({(dim_t)m, (dim_t)n}, DataType::Float32);
+        auto t1 = g.input({(dim_t)k, (dim_t)n}, DataType::Int8), ts1 = g.input({(dim_t)n}, DataType::Float32);
+        auto t2 = g.input({(dim_t)k, (dim_t)n}, DataType::Int8), ts2 = g.input({(dim_t)n}, DataType::Float32);
+        auto y1 = g.op(Op::QuantizedMatMul, x, t1, ts1);
+        auto y2 = g.op(Op::Add, h, g.op(Op::QuantizedMatMul, x, t2, ts2));
+        g.mark_output(y1);
+        g.mark_output(y2);
+        auto exec = g.build(DeviceType::HIP);
+        *steps = exec->num_steps();
+        if (!strided) x.copy_from_host(as_bytes(xv));
+        h.copy_from_host(as_bytes(hv));
+        t1.copy_from_host(as_bytes(q1));
+        ts1.copy_from_host(as_bytes(s1));
+        t2.copy_from_host(as_bytes(q2));
+        ts2.copy_from_host(as_bytes(s2));
+        exec->execute();
+        std::vector<float> o1(m * n), o2(m * n);
+        y1.copy_to_host(as_writeable_bytes(o1));
+        y2.copy_to_host(as_writeable_bytes(o2));
+        return std::pair{o1, o2};
+    };
+    std::size_t dense_steps = 0, strided_steps = 0;
+    const auto dense = run(false, &dense_steps);
+    const auto strided = run(true, &strided_steps);
+    REQUIRE(dense_steps == 2);     // product, product + Add fused
+    REQUIRE(strided_steps == 3);   // product, product, Add
+    REQUIRE(std::memcmp(dense.first.data(), strided.first.data(), m * n * 4) == 0);
+    REQUIRE(std::memcmp(dense.second.data(), strided.second.data(), m * n * 4) == 0);
+    std::vector<float> ref(m * n);
+    vmo_qmm_2d_f32(xv.data(), q1.data(), s1.data(), ref.data(), m, k, n, 1, 0);
+    REQUIRE(max_abs_diff(strided.first, ref) <= 1e-5f * max_abs(ref));
 }

@@ -148,6 +148,9 @@ bool qmm_groupable(pConstNode n) {
         out[0]->dtype != DataType::Float32)
         return false;
     if (in[0]->shape.empty() || in[1]->shape.size() != 2) return false;
+    for (auto* t : in)
+        if (!t->is_contiguous()) return false;
+    if (!out[0]->is_contiguous()) return false;
     dim_t rows = 1;
     for (std::size_t i = 0; i + 1 < in[0]->shape.size(); ++i) rows *= in[0]->shape[i];
     return rows >= 1 && rows <= 4;
@@ -515,6 +518,38 @@ void fuse_steps(std::vector<Step>& steps, DeviceType device, const TensorIndex& 
     steps.resize(w);
 }
 
+// Fused and grouped launches take dense operands only (a single node's
+// kernel gathers and scatters strided ones itself): a step that would hand
+// such a launch a strided operand runs its nodes one by one instead, at the
+// step's place, where every operand of every member exists.  Only a fused
+// chain's external operands count; its inner tensors are never allocated.
+void split_strided(std::vector<Step>& steps) {
+    auto dense = [](const auto& ts) {
+        return std::all_of(ts.begin(), ts.end(), [](pConstTensorStorage t) { return t->is_contiguous(); });
+    };
+    auto launchable = [&](const Step& st) {
+        if (st.fused >= 0) return dense(st.ins) && dense(st.outs);
+        if (st.nodes.size() < 2) return true;
+        return std::all_of(st.nodes.begin(), st.nodes.end(),
+                           [&](pConstNode n) { return dense(n->inputs()) && dense(n->outputs()); });
+    };
+    if (std::all_of(steps.begin(), steps.end(), launchable)) return;
+    std::vector<Step> out;
+    out.reserve(steps.size());
+    for (auto& st : steps) {
+        if (launchable(st)) {
+            out.push_back(std::move(st));
+            continue;
+        }
+        for (auto* n : st.nodes) {
+            Step one;
+            one.nodes.push_back(n);
+            out.push_back(std::move(one));
+        }
+    }
+    steps = std::move(out);
+}
+
 // ---- byte-preserving nodes --------------------------------------------------
 // A Reshape, or a Transpose that keeps the order of every axis longer than
 // one, writes its input's bytes unchanged.  When input and output are both
@@ -592,6 +627,7 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
 
     auto steps = plan_steps(order, device, index, tensors.size());
     fuse_steps(steps, device, index, dedicated);
+    split_strided(steps);
 
     // Activity and lifetimes (a fused step touches its chain's external
     // operands only).

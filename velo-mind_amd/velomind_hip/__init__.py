@@ -82,6 +82,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "vm_hip_decode_trace_read": ([p, c_int64], c_int),
         "vm_hip_gemv_trace_read": ([p, c_int64], c_int),
         "vm_hip_qmm_add_f32": ([p, p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
+        "vm_hip_copy_strided": ([p, p, p, p, p, c_int, c_int, p], c_int),
         "vm_hip_attention_decode_chain_f32": ([p, p, p, p, c_int64, c_int64, c_int64, c_int64, c_int64, p], c_int),
         "vm_hip_rope_append_f32": ([p] * 10 + [c_int64] * 5 + [p], c_int),
         "vm_hip_qmm_swiglu_add_f32": ([p, p, p, p, p, p, c_int64, c_int64, c_int64, c_int, c_int, p], c_int),
@@ -165,7 +166,7 @@ def exported_symbols() -> list[str]:
             "vm_hip_qmm_add_f32", "vm_hip_attention_decode_chain_f32", "vm_hip_rope_append_f32",
             "vm_hip_qmm_norm_group_f32", "vm_hip_qmm_swiglu_add_f32",
             "vm_hip_qmm_a_layout", "vm_hip_qmm_staged_f32", "vm_hip_add_rmsnorm_stage_f32",
-            "vm_hip_silu_mul_stage_f32"]
+            "vm_hip_silu_mul_stage_f32", "vm_hip_copy_strided"]
 
 
 def open_library() -> ctypes.CDLL:
