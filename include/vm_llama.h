@@ -120,11 +120,13 @@ int vm_llama_session_decode_path(const vm_llama_session* s, int* path);
 /* Graph engine only: host seconds of the decode steps since the last
  * prefill, summed over steps -- out[0] building each step's Graph, out[1]
  * Graph::build on DeviceType::HIP, out[2] Executable::execute (launches and
- * the final drain), out[3] reading the logits back, out[5] destroying the
- * step's Executable and Graph -- and out[4] the number of steps.  No
- * counterpart in the reference (its engine times whole steps,
- * llama_engine.cpp:395-455); -1 for a resident session. */
-int vm_llama_session_step_timing(const vm_llama_session* s, double* out6);
+ * the final drain), out[3] reading the logits back, out[5] destroying a
+ * step's Executable and Graph, out[6] waiting for the helper thread that
+ * builds the next step's Graph while a step runs (out[0], out[1] and out[5]
+ * are then that thread's time, overlapped with out[2]) -- and out[4] the
+ * number of steps.  No counterpart in the reference (its engine times whole
+ * steps, llama_engine.cpp:395-455); -1 for a resident session. */
+int vm_llama_session_step_timing(const vm_llama_session* s, double* out7);
 
 /* Greedy decoding: prefill, then `steps` decode steps; out_tokens receives
  * steps + 1 tokens (the first from the prompt's logits).  timing (may be

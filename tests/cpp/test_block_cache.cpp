@@ -96,6 +96,29 @@ TEST_CASE("block cache reuses a freed block only after a device synchronization"
     CHECK(cache.cached_bytes() == 0);
 }
 
+TEST_CASE("block cache reclaim makes parked blocks reusable with one synchronization", "[core][memory]") {
+    FakeDevice dev;
+    dev.capacity = 1 << 20;
+    g_dev = &dev;
+    BlockCache cache(fake_ops(), 1 << 20);
+    cache.reclaim(0);                    // nothing parked: no synchronization
+    CHECK(dev.syncs == 0);
+    void* a = cache.allocate(0, 4096);
+    void* b = cache.allocate(0, 8192);
+    REQUIRE(cache.park(0, 4096, a));
+    REQUIRE(cache.park(0, 8192, b));
+    cache.reclaim(0);
+    CHECK(dev.syncs == 1);
+    CHECK(cache.allocate(0, 8192) == b);  // both classes reusable without another synchronization
+    CHECK(cache.allocate(0, 4096) == a);
+    CHECK(dev.syncs == 1);
+    CHECK(dev.mallocs == 2);
+    REQUIRE(cache.park(0, 4096, a));
+    REQUIRE(cache.park(0, 8192, b));
+    cache.release_device(0);
+    CHECK(dev.live.empty());
+}
+
 TEST_CASE("block cache gives idle blocks back when the device allocator fails", "[core][memory]") {
     FakeDevice dev;
     dev.capacity = 64 << 10;

@@ -111,6 +111,34 @@ def test_graph_engine_gqa(llama, qt, block):
     _close(s.forward_step(9, 2), L.decode(cfg, ow, 9, 2, kv, True)[0], 1e-4, "decode")
 
 
+def test_graph_engine_helper_thread_changes_no_result(llama, monkeypatch):
+    """Each decode step's Graph built on the helper thread while the previous
+    step runs (the default) against every step built, run and destroyed in
+    turn (VELOMIND_GRAPH_PIPELINE=0): the same logits bit for bit, across a
+    new prompt that discards the prebuilt step."""
+    cfg, w = _gqa()
+    dev = llama.Weights.from_oracle(cfg, w)
+    outs = {}
+    for pipe in ("1", "0"):
+        monkeypatch.setenv("VELOMIND_GRAPH_PIPELINE", pipe)
+        print(f"case graph engine pipeline={pipe}", flush=True)
+        s = llama.Session(dev, llama.ENGINE_GRAPH, 2, 32, True)
+        try:
+            got = [s.prefill([5, 7])]
+            for pos, tok in ((2, 9), (3, 4), (4, 11), (5, 2)):
+                got.append(s.forward_step(tok, pos))
+            t = s.step_timing()
+            assert t["steps"] == 4
+            got.append(s.prefill([3, 1, 4]))
+            got.append(s.forward_step(1, 3))
+            got.append(s.forward_step(8, 4))
+        finally:
+            s.close()
+        outs[pipe] = got
+    for i, (a, b) in enumerate(zip(outs["1"], outs["0"])):
+        assert np.array_equal(a, b), f"output {i} differs"
+
+
 @pytest.mark.parametrize("qt,block", QUANTS[1:])
 def test_resident_decoder_matches_oracle(llama, qt, block):
     # (toy_llama has head_dim 16; the resident decoder runs head_dim 64 or 128.)

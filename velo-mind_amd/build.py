@@ -42,7 +42,7 @@ if os.environ.get("VELOMIND_DECODE_TRACE") == "1":
 # Phase timestamps in the decode GEMV (profiling builds only).
 if os.environ.get("VELOMIND_GEMV_TRACE") == "1":
     HIP_FLAGS.append("-DVM_GEMV_TRACE")
-CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-Wextra",
+CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-pthread", "-Wall", "-Wextra",
              f"-I{os.path.join(CORE, 'include')}", f"-I{os.path.join(CORE, 'src')}",
              f"-I{os.path.join(ROOT, 'include')}"]
 
@@ -98,7 +98,7 @@ def build_core(jobs: int = 8) -> str | None:
         list(ex.map(_run, cmds))
     out = os.path.join(OUT_DIR, "libvelomind.so")
     tmp = out + ".tmp"
-    _run([CXX, "-shared", "-fPIC", *objs, "-o", tmp, f"-L{OUT_DIR}", "-lvmhip",
+    _run([CXX, "-shared", "-fPIC", "-pthread", *objs, "-o", tmp, f"-L{OUT_DIR}", "-lvmhip",
           "-Wl,-rpath,$ORIGIN", "-Wl,-soname,libvelomind.so"])
     os.replace(tmp, out)
     return out

@@ -21,6 +21,7 @@
 #include <array>
 #include <cstddef>
 #include <cstdint>
+#include <future>
 #include <memory>
 #include <span>
 #include <vector>
@@ -73,10 +74,19 @@ private:
     auto slot(LlamaWeight kind, std::size_t layer) const -> std::size_t;
 };
 
+// Decode steps overlap host and device work: while step t's graph runs,
+// a helper thread builds the graph of position t + 1 (it depends on the
+// position and on step t's K/V tensors, not on the next token's value) and
+// destroys step t - 1's.  Every step still builds, runs and destroys its
+// own Graph, with the same results as one after another;
+// VELOMIND_GRAPH_PIPELINE=0 runs them one after another.
 class VELOMIND_CORE_EXPORT GraphLlamaSession {
 public:
     GraphLlamaSession(std::shared_ptr<const LlamaWeightSet> weights, QuantType quant_type, int block_size,
                       bool use_fused_attention);
+    ~GraphLlamaSession();
+    GraphLlamaSession(const GraphLlamaSession&) = delete;
+    GraphLlamaSession& operator=(const GraphLlamaSession&) = delete;
     // Prompt at positions 0..n-1; returns the last position's logits.
     auto prefill(std::span<const std::int32_t> tokens) -> std::vector<float>;
     // One token at position `pos` (== tokens processed so far).
@@ -85,20 +95,34 @@ public:
     // Host seconds spent by the decode steps since the last prefill, summed:
     // [0] building each step's Graph (nodes, shapes, bound weights), [1]
     // Graph::build on HIP, [2] Executable::execute (launches and the final
-    // drain), [3] reading the logits back; [4] the number of steps.
-    auto step_timing() const noexcept -> const std::array<double, 6>& { return _timing; }
+    // drain), [3] reading the logits back, [5] destroying a step's
+    // Executable and Graph, [6] waiting for the helper thread to finish the
+    // step's Graph; [4] the number of steps.  With the helper thread, [0],
+    // [1] and [5] are its time, overlapped with [2].
+    auto step_timing() const noexcept -> const std::array<double, 7>& { return _timing; }
 
 private:
+    struct DecodeStep;
+    struct Helper;
     void bind(Graph& g, ForwardWeights& w) const;
+    // The graph of the decode step at `pos` reading K/V `k`, `v`, built on HIP.
+    auto make_step(std::size_t pos, std::vector<std::shared_ptr<TensorStorage>> k,
+                   std::vector<std::shared_ptr<TensorStorage>> v) const -> std::unique_ptr<DecodeStep>;
+    // Waits for the helper thread and discards what it built.
+    void drop_prebuilt() noexcept;
     std::shared_ptr<const LlamaWeightSet> _weights;
     QuantType _qt;
     int _block;
     bool _fused;
+    bool _pipeline = true;
     // Packed linears (or the fp32 ones when unquantized), shared by every step's graph.
     std::vector<std::shared_ptr<TensorStorage>> _lin, _scale;  // [7 * layers + 1]
     std::vector<std::shared_ptr<TensorStorage>> _k, _v;        // per layer, [Hkv, S, D]
     std::size_t _seq_len = 0;
-    std::array<double, 6> _timing{};
+    std::array<double, 7> _timing{};
+    std::unique_ptr<DecodeStep> _retired;                  // the last step run, destroyed by the helper
+    std::future<std::unique_ptr<DecodeStep>> _prebuilt;    // the next position's step, from the helper
+    std::unique_ptr<Helper> _helper;                       // the helper thread (started on first use)
 };
 
 class PackedLlamaWeights;

@@ -94,6 +94,27 @@ public:
         return freed;
     }
 
+    // Makes every block parked on device d reusable, after one device-wide
+    // synchronization (none when nothing is parked).  Called where the device
+    // is idle anyway, it spares a later take() that synchronization while
+    // other work runs.
+    void reclaim(int d) {
+        Lists parked;
+        {
+            std::lock_guard<std::mutex> lock(_mu);
+            auto it = _dev.find(d);
+            if (it == _dev.end() || it->second.parked.empty()) return;
+            parked.swap(it->second.parked);
+        }
+        const bool drained = _ops.synchronize() == 0;
+        std::lock_guard<std::mutex> lock(_mu);
+        PerDevice& pd = _dev[d];
+        Lists& dst = drained ? pd.ready : pd.parked;
+        for (auto& [c, v] : parked) {
+            auto& r = dst[c];
+            r.insert(r.end(), v.begin(), v.end());
+        }
+    }
     std::size_t cached_bytes() {
         std::lock_guard<std::mutex> lock(_mu);
         return _cached;

@@ -158,6 +158,8 @@ void context_synchronize(void* ctx) {
 
 void* current_stream() noexcept { return t_current_stream; }
 
+void reclaim_freed_blocks() { block_cache().reclaim(current_device_or_zero()); }
+
 std::string error_context(Op op, const TensorStorage& output, const char* stage) {
     std::string msg = std::string(op_name(op)) + " on HIP output shape=[";
     for (std::size_t i = 0; i < output.shape.size(); ++i) {

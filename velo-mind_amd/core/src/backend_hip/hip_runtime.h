@@ -13,6 +13,12 @@ namespace velomind::backend::hip {
 // Stream of the HIP context active on this thread (nullptr = null stream).
 void* current_stream() noexcept;
 
+// Makes the storage blocks freed so far on the current device reusable (one
+// device-wide synchronization when any are waiting).  For callers that know
+// the device is idle and are about to allocate from another thread while
+// new work runs: the allocations then need no synchronization of their own.
+void reclaim_freed_blocks();
+
 // "<op> on HIP output shape=[a,b] at <stage>" (the reference's CUDA
 // message format, src/cuda/ops/backend_error.h:15-23).
 std::string error_context(Op op, const TensorStorage& output, const char* stage);

@@ -160,12 +160,12 @@ int vm_llama_session_decode_path(const vm_llama_session* s, int* path) {
     });
 }
 
-int vm_llama_session_step_timing(const vm_llama_session* s, double* out6) {
+int vm_llama_session_step_timing(const vm_llama_session* s, double* out7) {
     return guarded([&] {
-        if (!s || !out6) throw std::invalid_argument("vm_llama_session_step_timing: null argument");
+        if (!s || !out7) throw std::invalid_argument("vm_llama_session_step_timing: null argument");
         if (!s->graph) throw std::invalid_argument("vm_llama_session_step_timing: not a graph-engine session");
         const auto& t = s->graph->step_timing();
-        std::copy(t.begin(), t.end(), out6);
+        std::copy(t.begin(), t.end(), out7);
     });
 }
 

@@ -1,9 +1,14 @@
 // LlamaWeightSet and GraphLlamaSession (see velomind/llama/llama_hip.h).
 #include <chrono>
+#include <condition_variable>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <thread>
 #include <stdexcept>
 #include <string>
 
+#include "backend_hip/hip_runtime.h"
 #include "velomind/executable.h"
 #include "velomind/llama/llama_hip.h"
 #include "vm_hip.h"
@@ -122,6 +127,8 @@ GraphLlamaSession::GraphLlamaSession(std::shared_ptr<const LlamaWeightSet> weigh
     if (_qt == QuantType::Int8 && _block > 0)
         throw std::invalid_argument("GraphLlamaSession: INT8 weights are packed per column (block_size 0)");
     if (_qt == QuantType::Int4 && _block <= 0) _block = 32;  // the packer's block (quant.h:89)
+    const char* pipe = std::getenv("VELOMIND_GRAPH_PIPELINE");
+    _pipeline = !(pipe && pipe[0] == '0');
     const auto& cfg = _weights->config();
     const std::size_t n = 7 * cfg.num_layers + 1;
     _lin.resize(n);
@@ -167,6 +174,7 @@ void GraphLlamaSession::bind(Graph& g, ForwardWeights& w) const {
 
 auto GraphLlamaSession::prefill(std::span<const std::int32_t> tokens) -> std::vector<float> {
     if (tokens.empty()) throw std::invalid_argument("GraphLlamaSession::prefill: tokens is empty");
+    drop_prebuilt();
     const auto& cfg = _weights->config();
     const auto s = static_cast<dim_t>(tokens.size());
     const auto half = static_cast<dim_t>(cfg.head_dim() / 2);
@@ -203,6 +211,112 @@ auto GraphLlamaSession::prefill(std::span<const std::int32_t> tokens) -> std::ve
     return out;
 }
 
+struct GraphLlamaSession::DecodeStep {
+    std::size_t pos = 0;
+    std::vector<std::shared_ptr<TensorStorage>> k_in, v_in;   // the K/V tensors the graph reads
+    std::unique_ptr<Graph> graph;
+    std::unique_ptr<Executable> exec;                          // destroyed before its graph
+    Tensor tok, cos, sin, logits;
+    KVCacheHandles kv_out;
+    double construct_s = 0.0, build_s = 0.0;
+    double teardown_s = 0.0;   // of the step the helper destroyed after building this one
+};
+
+auto GraphLlamaSession::make_step(std::size_t pos, std::vector<std::shared_ptr<TensorStorage>> k,
+                                  std::vector<std::shared_ptr<TensorStorage>> v) const
+    -> std::unique_ptr<DecodeStep> {
+    using clock = std::chrono::steady_clock;
+    const auto t0 = clock::now();
+    const auto& cfg = _weights->config();
+    const auto half = static_cast<dim_t>(cfg.head_dim() / 2);
+    auto st = std::make_unique<DecodeStep>();
+    st->pos = pos;
+    st->graph = std::make_unique<Graph>();
+    Graph& g = *st->graph;
+    st->tok = g.input({1}, DataType::Int32);
+    ForwardWeights w;
+    bind(g, w);
+    w.cos_cache = g.input({1, half}, DataType::Float32);
+    w.sin_cache = g.input({1, half}, DataType::Float32);
+    KVCacheHandles kv_in;
+    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+        kv_in.k.push_back(g.input(k[l]));
+        kv_in.v.push_back(g.input(v[l]));
+    }
+    st->logits = build_forward_graph_decode(g, cfg, st->tok, w, kv_in, &st->kv_out);
+    st->cos = w.cos_cache;
+    st->sin = w.sin_cache;
+    const auto t1 = clock::now();
+    st->exec = g.build(DeviceType::HIP);
+    const auto t2 = clock::now();
+    st->construct_s = std::chrono::duration<double>(t1 - t0).count();
+    st->build_s = std::chrono::duration<double>(t2 - t1).count();
+    st->k_in = std::move(k);
+    st->v_in = std::move(v);
+    return st;
+}
+
+// The helper: one thread for the session's life, running one job at a
+// time.  Every prebuilt step is built and destroyed on it, so its allocator
+// state stays warm (a fresh thread per step made construction and teardown
+// 2-2.5x slower).
+struct GraphLlamaSession::Helper {
+    using Job = std::packaged_task<std::unique_ptr<DecodeStep>()>;
+    std::mutex mu;
+    std::condition_variable cv;
+    Job job;
+    bool has_job = false, stop = false;
+    std::thread th{[this] { run(); }};   // last: starts after the fields above exist
+
+    ~Helper() {
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            stop = true;
+        }
+        cv.notify_one();
+        th.join();
+    }
+    auto post(Job j) -> std::future<std::unique_ptr<DecodeStep>> {
+        auto f = j.get_future();
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            job = std::move(j);
+            has_job = true;
+        }
+        cv.notify_one();
+        return f;
+    }
+    void run() {
+        for (;;) {
+            Job j;
+            {
+                std::unique_lock<std::mutex> lock(mu);
+                cv.wait(lock, [&] { return has_job || stop; });
+                if (!has_job) return;
+                j = std::move(job);
+                has_job = false;
+            }
+            j();
+        }
+    }
+};
+
+void GraphLlamaSession::drop_prebuilt() noexcept {
+    if (_prebuilt.valid()) {
+        try {
+            (void)_prebuilt.get();
+        } catch (...) {
+            // a step nobody will run: its failure is nobody's to report
+        }
+    }
+    _retired.reset();
+}
+
+GraphLlamaSession::~GraphLlamaSession() {
+    drop_prebuilt();
+    _helper.reset();
+}
+
 auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std::vector<float> {
     if (_seq_len == 0) {
         const std::int32_t one[1] = {token};
@@ -210,51 +324,79 @@ auto GraphLlamaSession::forward_step(std::int32_t token, std::size_t pos) -> std
     }
     if (pos != _seq_len) throw std::invalid_argument("GraphLlamaSession::forward_step: pos must equal the cache length");
     using clock = std::chrono::steady_clock;
+    auto sec = [](clock::time_point a, clock::time_point b) { return std::chrono::duration<double>(b - a).count(); };
     const auto t0 = clock::now();
     const auto& cfg = _weights->config();
-    const auto half = static_cast<dim_t>(cfg.head_dim() / 2);
+    // The step prebuilt for this position over the current K/V, when there is
+    // one (get() rethrows a failure of its build here, at its own step).
+    std::unique_ptr<DecodeStep> step;
+    if (_prebuilt.valid()) {
+        step = _prebuilt.get();
+        if (step && (step->pos != pos || step->k_in != _k || step->v_in != _v)) step.reset();
+    }
+    const auto t1 = clock::now();
+    double teardown = 0.0;
+    if (step) {
+        teardown = step->teardown_s;
+    } else {
+        _retired.reset();
+        step = make_step(pos, _k, _v);
+    }
+    if (_pipeline) {
+        // The next position's graph reads this step's K/V outputs, which
+        // exist from this build on.  The device is idle here, so blocks freed
+        // by earlier steps become reusable now, without the helper having to
+        // synchronize while this step runs.
+        backend::hip::reclaim_freed_blocks();
+        std::vector<std::shared_ptr<TensorStorage>> k_next, v_next;
+        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+            k_next.push_back(step->kv_out.k[l].shared_storage());
+            v_next.push_back(step->kv_out.v[l].shared_storage());
+        }
+        int device = 0;
+        check(vm_hip_get_device(&device), "GraphLlamaSession: current device");
+        if (!_helper) _helper = std::make_unique<Helper>();
+        _prebuilt = _helper->post(Helper::Job([this, pos, device, k = std::move(k_next), v = std::move(v_next),
+                                               old = std::move(_retired)]() mutable {
+            check(vm_hip_set_device(device), "GraphLlamaSession: helper device");
+            auto next = make_step(pos + 1, std::move(k), std::move(v));
+            const auto td = clock::now();
+            old.reset();
+            next->teardown_s = std::chrono::duration<double>(clock::now() - td).count();
+            return next;
+        }));
+    }
+    const std::int32_t one[1] = {token};
+    step->tok.copy_from_host(std::as_bytes(std::span(one)));
+    std::vector<float> c, sn;
+    compute_rope_cache(1, cfg.head_dim(), cfg.rope_theta, c, sn, pos);
+    step->cos.copy_from_host(std::as_bytes(std::span(c)));
+    step->sin.copy_from_host(std::as_bytes(std::span(sn)));
+    const auto t2 = clock::now();
+    step->exec->execute();
+    const auto t3 = clock::now();
+    for (std::size_t l = 0; l < cfg.num_layers; ++l) {
+        _k[l] = step->kv_out.k[l].shared_storage();
+        _v[l] = step->kv_out.v[l].shared_storage();
+    }
+    _seq_len = pos + 1;
     std::vector<float> out(cfg.vocab_size);
-    clock::time_point t1, t2, t3, t4;
-    {
-        Graph g;
-        auto tok = g.input({1}, DataType::Int32);
-        ForwardWeights w;
-        bind(g, w);
-        w.cos_cache = g.input({1, half}, DataType::Float32);
-        w.sin_cache = g.input({1, half}, DataType::Float32);
-        KVCacheHandles kv_in, kv_out;
-        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
-            kv_in.k.push_back(g.input(_k[l]));
-            kv_in.v.push_back(g.input(_v[l]));
-        }
-        auto logits = build_forward_graph_decode(g, cfg, tok, w, kv_in, &kv_out);
-        t1 = clock::now();
-        auto exec = g.build(DeviceType::HIP);
-        const std::int32_t one[1] = {token};
-        tok.copy_from_host(std::as_bytes(std::span(one)));
-        std::vector<float> c, sn;
-        compute_rope_cache(1, cfg.head_dim(), cfg.rope_theta, c, sn, pos);
-        w.cos_cache.copy_from_host(std::as_bytes(std::span(c)));
-        w.sin_cache.copy_from_host(std::as_bytes(std::span(sn)));
-        t2 = clock::now();
-        exec->execute();
-        t3 = clock::now();
-        for (std::size_t l = 0; l < cfg.num_layers; ++l) {
-            _k[l] = kv_out.k[l].shared_storage();
-            _v[l] = kv_out.v[l].shared_storage();
-        }
-        _seq_len = pos + 1;
-        logits.copy_to_host(std::as_writable_bytes(std::span(out)));
-        t4 = clock::now();
-    }   // the step's Executable and Graph are destroyed here
-    const auto t5 = clock::now();
-    auto sec = [](clock::time_point a, clock::time_point b) { return std::chrono::duration<double>(b - a).count(); };
-    _timing[0] += sec(t0, t1);
-    _timing[1] += sec(t1, t2);
+    step->logits.copy_to_host(std::as_writable_bytes(std::span(out)));
+    const auto t4 = clock::now();
+    const double construct = step->construct_s, build = step->build_s;
+    if (_pipeline) {
+        _retired = std::move(step);   // destroyed by the helper while the next step runs
+    } else {
+        step.reset();
+        teardown = sec(t4, clock::now());
+    }
+    _timing[0] += construct;
+    _timing[1] += build;
     _timing[2] += sec(t2, t3);
     _timing[3] += sec(t3, t4);
     _timing[4] += 1.0;
-    _timing[5] += sec(t4, t5);
+    _timing[5] += teardown;
+    _timing[6] += sec(t0, t1);
     return out;
 }
 

@@ -204,14 +204,18 @@ class Session:
         return out, (float(timing[0]), float(timing[1]), int(timing[2]))
 
     def step_timing(self) -> dict:
-        """Graph engine: host seconds per decode step since the last prefill,
-        split into graph construction, Graph::build, execute, readback and
-        teardown (destroying the step's Executable and Graph)."""
-        t = np.zeros(6, np.float64)
+        """Graph engine: host milliseconds per decode step since the last
+        prefill, split into graph construction, Graph::build, execute,
+        readback, teardown (destroying a step's Executable and Graph) and the
+        wait for the helper thread that builds the next step's Graph while a
+        step runs (construction, build and teardown are then its time,
+        overlapped with execute)."""
+        t = np.zeros(7, np.float64)
         _check(lib().vm_llama_session_step_timing(self.handle, t.ctypes.data))
         n = max(1.0, t[4])
         return {"steps": int(t[4]), "construct_ms": t[0] / n * 1e3, "build_ms": t[1] / n * 1e3,
-                "execute_ms": t[2] / n * 1e3, "readback_ms": t[3] / n * 1e3, "teardown_ms": t[5] / n * 1e3}
+                "execute_ms": t[2] / n * 1e3, "readback_ms": t[3] / n * 1e3, "teardown_ms": t[5] / n * 1e3,
+                "wait_ms": t[6] / n * 1e3}
 
     def decode_path(self) -> int:
         """DECODE_GRAPH / _PER_OP / _SLICES / _PERSISTENT."""
