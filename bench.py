@@ -178,11 +178,11 @@ class Rotation:
     ROTATION_BYTES, so that every launch streams its weights from HBM rather
     than from the Infinity Cache of the previous replay."""
 
-    def __init__(self, H, codes, scales, stream, min_copies: int = 1):
+    def __init__(self, H, codes, scales, stream, min_copies: int = 1, copies: int = 0):
         lib = H.open_library()
         self.cb, self.sb = codes.nbytes, scales.nbytes
         self.stride = (self.cb + self.sb + 255) // 256 * 256
-        self.copies = max(min_copies, -(-ROTATION_BYTES // (self.cb + self.sb)))
+        self.copies = copies or max(min_copies, -(-ROTATION_BYTES // (self.cb + self.sb)))
         self.buf = H.DeviceBuffer(self.copies * self.stride)
         base = self.buf.addr
         for i in range(self.copies):
@@ -703,6 +703,109 @@ def config1_bench(H, stream, reps: int = 10, cpu_seconds: float = 3.0) -> dict:
     return out
 
 
+def fused_gemv_bench(H, stream, reps: int = 10) -> dict:
+    """The graph engine's fused decode GEMVs (kernel.h FusedKind: NormQmm,
+    QmmAdd, SwigluQmmAdd) beside the plain launches of the same products,
+    at SmolLM2-360M INT8 shapes (M = 1): q|k|v and gate|up as sibling groups
+    with and without the RMSNorm in their staging, o with and without the
+    residual addend, down with and without the SwiGLU staging and addend.
+    Each case is launched once per weight copy of Rotations walking >= 512 MB
+    (cold HBM), as one HIP graph replayed `reps` times; microseconds per
+    launch."""
+    import ctypes
+
+    lib = H.load()
+    rng = np.random.default_rng(11)
+    hid, kvd, inter = 960, 320, 2560
+
+    def packed(k, n):
+        w = (rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        dw = H.DeviceBuffer.from_array(w)
+        p, sc = H.DeviceBuffer(k * n), H.DeviceBuffer(n * 4)
+        H.pack_int8(dw.addr, p.addr, sc.addr, k, n)
+        H.synchronize()
+        dw.close()
+        return p, sc
+
+    vec = lambda n: H.DeviceBuffer.from_array(rng.standard_normal(n, dtype=np.float32))   # noqa: E731
+    x, g, h = vec(inter), vec(inter), vec(inter)
+    nw = H.DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(hid)).astype(np.float32))
+    outs = [H.DeviceBuffer(inter * 4) for _ in range(3)]
+
+    def rotations(shapes):
+        mats = [packed(k, n) for k, n in shapes]
+        copies = -(-ROTATION_BYTES // sum(k * n + n * 4 for k, n in shapes))
+        rots = [Rotation(H, p, sc, stream, copies=copies) for p, sc in mats]
+        for p, sc in mats:
+            p.close()
+            sc.close()
+        return rots, copies
+
+    def members(rots, shapes, i):
+        arr = (H.QmmMember * len(rots))()
+        for j, (r, (_, n)) in enumerate(zip(rots, shapes)):
+            arr[j].codes, arr[j].scales = r.addrs[i]
+            arr[j].c, arr[j].n = outs[j].addr, n
+        return arr
+
+    def time_case(rots, copies, launch_one) -> float:
+        args = [launch_one(i) for i in range(copies)]   # ctypes arguments built outside the capture
+        def launch_all():
+            for f in args:
+                f()
+        launch_all()   # eager first: sizes any split-K workspace before the capture
+        stream.synchronize()
+        return timed_replay(H, stream, launch_all, reps) * 1e3 / copies
+
+    eps = ctypes.c_float(1e-5)
+    out = {}
+    for name, shapes in (("q|k|v", ((hid, hid), (hid, kvd), (hid, kvd))), ("gate|up", ((hid, inter), (hid, inter)))):
+        rots, copies = rotations(shapes)
+        cnt = len(shapes)
+
+        def plain(i, rots=rots, shapes=shapes, cnt=cnt):
+            m = members(rots, shapes, i)
+            return lambda: H.check(lib.vm_hip_qmm_group_f32(x.addr, 1, hid, m, cnt, H.QUANT_INT8, 0, stream.handle))
+
+        def normed(i, rots=rots, shapes=shapes, cnt=cnt):
+            m = members(rots, shapes, i)
+            return lambda: H.check(lib.vm_hip_qmm_norm_group_f32(x.addr, nw.addr, eps, 1, hid, m, cnt, H.QUANT_INT8,
+                                                                 0, stream.handle))
+
+        a, b = time_case(rots, copies, plain), time_case(rots, copies, normed)
+        out[name] = {"KxN": f"{hid}x{'|'.join(str(n) for _, n in shapes)}", "plain_group_us": round(a, 3),
+                     "with_rmsnorm_us": round(b, 3), "copies": copies}
+        for r in rots:
+            r.close()
+    for name, (k, n), fused, what in (("o", (hid, hid), "qmm_add", "with_addend_us"),
+                                      ("down", (inter, hid), "swiglu_add", "with_swiglu_and_addend_us")):
+        rots, copies = rotations(((k, n),))
+        r = rots[0]
+
+        def plain(i, k=k, n=n, r=r):
+            pa, sa = r.addrs[i]
+            return lambda: H.check(lib.vm_hip_qmm_f32(x.addr, pa, sa, outs[0].addr, 1, k, n, H.QUANT_INT8, 0,
+                                                      stream.handle))
+
+        def add(i, k=k, n=n, r=r):
+            pa, sa = r.addrs[i]
+            return lambda: H.check(lib.vm_hip_qmm_add_f32(x.addr, pa, sa, h.addr, outs[0].addr, 1, k, n,
+                                                          H.QUANT_INT8, 0, stream.handle))
+
+        def swiglu(i, k=k, n=n, r=r):
+            pa, sa = r.addrs[i]
+            return lambda: H.check(lib.vm_hip_qmm_swiglu_add_f32(g.addr, x.addr, pa, sa, h.addr, outs[0].addr, 1, k,
+                                                                 n, H.QUANT_INT8, 0, stream.handle))
+
+        a = time_case(rots, copies, plain)
+        b = time_case(rots, copies, add if fused == "qmm_add" else swiglu)
+        out[name] = {"KxN": f"{k}x{n}", "plain_us": round(a, 3), what: round(b, 3), "copies": copies}
+        r.close()
+    for buf in (x, g, h, nw, *outs):
+        buf.close()
+    return out
+
+
 LARGE_SHAPES = ((8192, 28672), (28672, 8192), (8192, 128256))
 
 
@@ -787,6 +890,8 @@ def main() -> int:
                     help="with --e2e-only and --e2e-model: comma-separated layer counts to run instead of the "
                          "config's (per-layer decode time with the weights resident in the 256 MB Infinity Cache "
                          "at few layers, streamed from HBM at many)")
+    ap.add_argument("--fused-gemv", action="store_true",
+                    help="only the graph engine's fused decode GEMVs beside the plain ones (SmolLM2 INT8 shapes)")
     ap.add_argument("--graph-engine", action="store_true",
                     help="only the drop-in graph-engine decode of config 4 (both attention forms)")
     ap.add_argument("--gemv-trace", action="store_true",
@@ -869,6 +974,9 @@ def main() -> int:
                              "us_per_layer": round(r["decode_us_per_token"] / layers, 2)})
                 log(f"bench: {name} {r['decode_path']}: {r['decode_us_per_token']} us/token")
         print(json.dumps({"metric": METRIC, "e2e_layers": rows}), flush=True)
+        return 0
+    if args.fused_gemv:
+        print(json.dumps({"metric": METRIC, "fused_gemv": fused_gemv_bench(H, stream)}), flush=True)
         return 0
     if args.graph_engine:
         out = {}

@@ -325,33 +325,36 @@ __device__ __forceinline__ void gemv_body(
         }
     };
 
-    // Issue the first chunk's loads, then stage this split's activations
-    // with kStageBatch buffer loads in flight per thread before the first
-    // LDS write (one memory round trip for up to 4 * 4 * W * 64 elements).  Loads outside a row's
+    // Memory requests in the order their results are needed: the RMSNorm
+    // operands and the first batch of this split's activations (one batch of
+    // kStageBatch buffer loads per thread covers 4 * 4 * W * 64 elements),
+    // then the first chunk's codes and scales.  Loads complete in issue
+    // order, so the staging, the norm and their barriers wait only for the
+    // activations (an L2 hit when the producer just wrote them) and run while
+    // the weights are still in flight from HBM.  Loads outside a row's
     // [0, k) use an offset past the buffer and read zeros.  With k % 4 == 0
     // and a 16-byte aligned A (a_vec) each load covers four elements that
     // all lie inside one row; otherwise each covers one element.
     Chunk<KIND> ca, cb;
     int ch = c_begin + rg;
     VM_GEMV_MARK(1);
-    load_chunk(ch, ca);
 
-    // RMSNorm operands (fx.norm_w non-null), requested together with the
-    // staging loads so that the norm adds no memory round trip: the first
-    // kNormRegs elements of this thread's stride of each row (the sum of
-    // squares) and of norm_w for the first kNormRegs staged elements it
-    // scales (one row's worth, shared by the rows).  Rows longer than that
-    // load the rest after the barrier.
+    // RMSNorm (fx.norm_w non-null): the row's sum of squares over all k
+    // with rmsnorm_kernel's arithmetic (256 threads striding the row with an
+    // fma chain, xor butterflies, the four waves' sums in order), then each
+    // staged element scaled as that kernel scales it, (x * inv) * w: bit for
+    // bit the separate RMSNorm.  The first kNormRegs elements of this
+    // thread's stride of each row are requested before everything else, the
+    // sum is reduced while the weights are in flight, and the staging stores
+    // write the scaled values (norm_w is loaded beside the activations).
     // 1024-thread workgroups (at most 128 VGPRs) keep no such registers:
-    // they would spill, so they load everything after the barrier.
+    // they would spill, so they read the row in the sum's loop.
     constexpr int kNormRegs = W >= 16 ? 0 : 8;
+    const bool norm = FX && fx.norm_w != nullptr;
     float nv[MR][kNormRegs > 0 ? kNormRegs : 1];
-    float nwv[kNormRegs > 0 ? kNormRegs : 1];
     if constexpr (FX) {
-        if (fx.norm_w) {
+        if (norm) {
             const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
-            const uint32_t w_bytes = static_cast<uint32_t>(k) * 4u;
-            const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(fx.norm_w, w_bytes);
 #pragma unroll
             for (int r = 0; r < MR; ++r)
 #pragma unroll
@@ -362,15 +365,46 @@ __device__ __forceinline__ void gemv_body(
                                              : a_bytes;
                     nv[r][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ars, static_cast<int>(off), 0, 0));
                 }
-#pragma unroll
-            for (int j = 0; j < kNormRegs; ++j) {
-                const int e = static_cast<int>(threadIdx.x) + j * W * 64;   // element of a staged row
-                const int kk = k_begin + e;
-                const uint32_t off = (e < xs_len && kk < k) ? static_cast<uint32_t>(kk) * 4u : w_bytes;
-                nwv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, static_cast<int>(off), 0, 0));
-            }
         }
     }
+    __shared__ float norm_part[FX ? MR : 1][4];
+    // Each row's 1/rms once the waves' partial sums are in norm_part, in a
+    // vector register: rows picked at run time read it without the array
+    // going to scratch.
+    float __attribute__((ext_vector_type(4))) inv = {0.0f, 0.0f, 0.0f, 0.0f};
+    static_assert(MR <= 4, "one 1/rms lane per row");
+    auto norm_sum = [&] {
+        if constexpr (FX) {
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                float sq = 0.0f;
+                if (r < m && threadIdx.x < 256) {
+#pragma unroll
+                    for (int j = 0; j < kNormRegs; ++j)
+                        if (static_cast<int>(threadIdx.x) + 256 * j < k) sq = fmaf(nv[r][j], nv[r][j], sq);
+                    for (int i = threadIdx.x + 256 * kNormRegs; i < k; i += 256) {
+                        const float v = a[static_cast<int64_t>(r) * k + i];
+                        sq = fmaf(v, v, sq);
+                    }
+                }
+                for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+                if (r < m && threadIdx.x < 256 && lane == 0) norm_part[r][wave] = sq;
+            }
+        }
+    };
+    auto norm_inv = [&] {
+        if constexpr (FX) {
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                float tot = 0.0f;
+                if (r < m)
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) tot += norm_part[r][w];
+                inv[r] = 1.0f / sqrtf(tot / static_cast<float>(k) + fx.norm_eps);
+            }
+        }
+    };
+    auto inv_of = [&](int r) { return MR == 1 ? inv[0] : inv[r]; };
 
     {
         // With a_up the staged activation is the SwiGLU product of a (gate)
@@ -378,31 +412,62 @@ __device__ __forceinline__ void gemv_body(
         // rounding); out-of-range reads give zeros for both, hence 0.
         const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(a, a_bytes);
         const __amdgpu_buffer_rsrc_t urs = buffer_rsrc(FX && fx.a_up ? fx.a_up : a, a_bytes);
+        // The second operand of each staged element, at most one: a_up (same
+        // offset as a) or norm_w (the element's column).  One load from a
+        // resource chosen here keeps the two from looking like competing
+        // writes of one register, which would cost a wait for every load.
+        const uint32_t nw_bytes = static_cast<uint32_t>(k) * 4u;
+        const bool up = FX && fx.a_up;
+        const bool two = up || norm;
+        const __amdgpu_buffer_rsrc_t rs2 = norm ? buffer_rsrc(fx.norm_w, nw_bytes) : urs;
         constexpr int T = W * 64;
+        // Prologue shared by both layouts: the weights requested after the
+        // first batch, the norm's partial sums published with one barrier
+        // and each row's 1/rms computed before any staged value is written.
+        auto after_first_issue = [&] {
+            load_chunk(ch, ca);
+            if (norm) {
+                norm_sum();
+                __syncthreads();
+                norm_inv();
+            }
+        };
         if (a_vec) {
             const int q_per_row = xs_len / 4;  // xs_len is a multiple of 8
             const int q_total = MR * q_per_row;
-            for (int q0 = threadIdx.x; q0 < q_total; q0 += kStageBatch * T) {
-                u32x4 t[kStageBatch], tu[kStageBatch];
+            u32x4 t[kStageBatch], tu[kStageBatch];
+            int row[kStageBatch];
+            auto issue = [&](int q0) {
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
                     const int q = q0 + u * T;
                     int r = 0;  // q / q_per_row for MR <= 4, without a division
 #pragma unroll
                     for (int i = 1; i < MR; ++i) r += q >= i * q_per_row ? 1 : 0;
+                    row[u] = r;
                     const int kk = k_begin + 4 * (q - r * q_per_row);
-                    const uint32_t off = (q < q_total && r < m && kk < k)
-                                             ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u
-                                             : a_bytes;
+                    const bool in = q < q_total && r < m && kk < k;
+                    const uint32_t off =
+                        in ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u : a_bytes;
                     t[u] = buffer_load16(ars, off);
-                    if (FX && fx.a_up) tu[u] = buffer_load16(urs, off);
+                    if (two) tu[u] = buffer_load16(rs2, norm ? (in ? static_cast<uint32_t>(kk) * 4u : nw_bytes) : off);
                 }
-                if (FX && fx.a_up)
+            };
+            auto store = [&](int q0) {
+                if (up)
 #pragma unroll
                     for (int u = 0; u < kStageBatch; ++u)
 #pragma unroll
                         for (int c = 0; c < 4; ++c)
                             t[u][c] = __float_as_uint(silu_mul_f32(__uint_as_float(t[u][c]), __uint_as_float(tu[u][c])));
+                if (norm)
+#pragma unroll
+                    for (int u = 0; u < kStageBatch; ++u) {
+                        const float ir = inv_of(row[u]);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            t[u][c] = __float_as_uint((__uint_as_float(t[u][c]) * ir) * __uint_as_float(tu[u][c]));
+                    }
                 // Unconditional writes (surplus ones go to a spare LDS slot)
                 // keep the compiler from sinking loads into per-write branches.
 #pragma unroll
@@ -410,85 +475,61 @@ __device__ __forceinline__ void gemv_body(
                     const int q = q0 + u * T;
                     *reinterpret_cast<u32x4*>(q < q_total ? xs + 4 * q : spare) = t[u];
                 }
+            };
+            issue(threadIdx.x);
+            after_first_issue();
+            store(threadIdx.x);
+            for (int q0 = threadIdx.x + kStageBatch * T; q0 < q_total; q0 += kStageBatch * T) {
+                issue(q0);
+                store(q0);
             }
         } else {
             const int e_total = MR * xs_len;
-            for (int e0 = threadIdx.x; e0 < e_total; e0 += kStageBatch * T) {
-                uint32_t t[kStageBatch], tu[kStageBatch];
+            uint32_t t[kStageBatch], tu[kStageBatch];
+            int row[kStageBatch];
+            auto issue = [&](int e0) {
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
                     const int e = e0 + u * T;
                     int r = 0;
 #pragma unroll
                     for (int i = 1; i < MR; ++i) r += e >= i * xs_len ? 1 : 0;
+                    row[u] = r;
                     const int kk = k_begin + (e - r * xs_len);
-                    const uint32_t off = (e < e_total && r < m && kk < k)
-                                             ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u
-                                             : a_bytes;
+                    const bool in = e < e_total && r < m && kk < k;
+                    const uint32_t off =
+                        in ? (static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + kk) * 4u : a_bytes;
                     t[u] = __builtin_amdgcn_raw_buffer_load_b32(ars, static_cast<int>(off), 0, 0);
-                    if (FX && fx.a_up) tu[u] = __builtin_amdgcn_raw_buffer_load_b32(urs, static_cast<int>(off), 0, 0);
+                    if (two)
+                        tu[u] = __builtin_amdgcn_raw_buffer_load_b32(
+                            rs2, static_cast<int>(norm ? (in ? static_cast<uint32_t>(kk) * 4u : nw_bytes) : off), 0, 0);
                 }
-                if (FX && fx.a_up)
+            };
+            auto store = [&](int e0) {
+                if (up)
 #pragma unroll
                     for (int u = 0; u < kStageBatch; ++u)
                         t[u] = __float_as_uint(silu_mul_f32(__uint_as_float(t[u]), __uint_as_float(tu[u])));
+                if (norm)
+#pragma unroll
+                    for (int u = 0; u < kStageBatch; ++u)
+                        t[u] = __float_as_uint((__uint_as_float(t[u]) * inv_of(row[u])) * __uint_as_float(tu[u]));
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
                     const int e = e0 + u * T;
                     *(e < e_total ? xs + e : spare) = __uint_as_float(t[u]);
                 }
+            };
+            issue(threadIdx.x);
+            after_first_issue();
+            store(threadIdx.x);
+            for (int e0 = threadIdx.x + kStageBatch * T; e0 < e_total; e0 += kStageBatch * T) {
+                issue(e0);
+                store(e0);
             }
         }
     }
     __syncthreads();
-
-    // RMSNorm of each activation row before the product (fx.norm_w non-null):
-    // the row's sum of squares over all k with rmsnorm_kernel's arithmetic
-    // (256 threads striding the row with an fma chain, xor butterflies, the
-    // four waves' sums in order), then the staged slice scaled as that
-    // kernel scales it, (x * inv) * w.  Bit for bit the separate RMSNorm.
-    if constexpr (FX) if (fx.norm_w) {
-        __shared__ float norm_part[MR][4];
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            float sq = 0.0f;
-            if (r < m && threadIdx.x < 256) {
-#pragma unroll
-                for (int j = 0; j < kNormRegs; ++j)
-                    if (static_cast<int>(threadIdx.x) + 256 * j < k) sq = fmaf(nv[r][j], nv[r][j], sq);
-                for (int i = threadIdx.x + 256 * kNormRegs; i < k; i += 256) {
-                    const float v = a[static_cast<int64_t>(r) * k + i];
-                    sq = fmaf(v, v, sq);
-                }
-            }
-            for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
-            if (r < m && threadIdx.x < 256 && lane == 0) norm_part[r][wave] = sq;
-        }
-        __syncthreads();
-        float inv[MR];
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            float tot = 0.0f;
-            if (r < m)
-#pragma unroll
-                for (int w = 0; w < 4; ++w) tot += norm_part[r][w];
-            inv[r] = 1.0f / sqrtf(tot / static_cast<float>(k) + fx.norm_eps);
-        }
-        // Row by row, so that each row's 1/rms is a register.
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            if (r >= m) continue;
-            float* xr = xs + r * xs_len;
-#pragma unroll
-            for (int j = 0; j < kNormRegs; ++j) {
-                const int e = static_cast<int>(threadIdx.x) + j * W * 64;
-                if (e < xs_len && k_begin + e < k) xr[e] = (xr[e] * inv[r]) * nwv[j];
-            }
-            for (int e = threadIdx.x + kNormRegs * W * 64; e < xs_len; e += W * 64)
-                if (k_begin + e < k) xr[e] = (xr[e] * inv[r]) * fx.norm_w[k_begin + e];
-        }
-        __syncthreads();
-    }
     VM_GEMV_MARK(2);
 
     float total[MR][kVec];
@@ -843,7 +884,12 @@ int launch_cfg(const float* a, const Member* members, int count, int m, int k, i
     const std::size_t lds = (static_cast<std::size_t>(MR) * cfg.chunks_per_split * kChunkK +
                              static_cast<std::size_t>(W) * MR * kVec * L + 4) * sizeof(float);
     const uint32_t a_bytes = static_cast<uint32_t>(static_cast<int64_t>(m) * k * 4);
-    const int a_vec = (k % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0) ? 1 : 0;
+    // 16-byte activation loads: rows of a multiple of 4 elements and 16-byte
+    // aligned operands (a_up and norm_w are read at the same offsets).
+    const int a_vec = (k % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(fx.a_up) % 16 == 0 && reinterpret_cast<uintptr_t>(fx.norm_w) % 16 == 0)
+                          ? 1
+                          : 0;
     // Chunk -> scale block is a shift when block_size / 8 is a power of two.
     int blk_shift = -1;
     if (KIND != 0) {
