@@ -408,6 +408,10 @@ def e2e_bench(name: str, use_graph: bool = True, persistent: bool = False, graph
                       " decode steps, greedy argmax on device")}
     if step_ms is not None:
         out["host_ms_per_step"] = {k: round(v, 3) for k, v in step_ms.items() if k != "steps"}
+        # Each step's graph is built on a helper thread while the previous
+        # step executes: the main thread waiting for it means the host's
+        # construction + build + teardown, not the device, set the rate.
+        out["bound"] = "host (graph construction and build)" if step_ms["wait_ms"] > 0.05 else "device"
         out["attention"] = "FusedAttention (use_fused_attention)" if fused_attention else \
             "MatMul / Softmax / MatMul chain (the reference default)"
     sess.close()
@@ -1118,7 +1122,7 @@ def main() -> int:
                 f"persistent step {pers['decode_tokens_per_s']} tok/s")
             if name in GRAPH_ENGINE_E2E:
                 keys = ("prefill_tokens_per_s", "prefill_ms", "decode_tokens", "decode_tokens_per_s",
-                        "decode_us_per_token", "host_ms_per_step", "attention", "engine")
+                        "decode_us_per_token", "host_ms_per_step", "bound", "attention", "engine")
                 ge = e2e_bench(name, graph_engine=True, steps=GRAPH_ENGINE_E2E[name])
                 gf = e2e_bench(name, graph_engine=True, steps=GRAPH_ENGINE_E2E[name], fused_attention=True)
                 e2e[name]["graph_engine"] = {k: ge[k] for k in keys}
