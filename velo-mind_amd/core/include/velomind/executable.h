@@ -5,6 +5,7 @@
 #pragma once
 
 #include <cstddef>
+#include <array>
 #include <memory>
 #include <vector>
 
@@ -39,6 +40,11 @@ public:
     // time (the fields a run re-checks).  Each storage appears once, however
     // many nodes touch it.
     struct FrozenLayout {
+        // The shape: inline up to kInlineRank dimensions (no allocation per
+        // watched storage and build), else in `shape`.
+        static constexpr std::size_t kInlineRank = 6;
+        std::array<dim_t, kInlineRank> dims{};
+        std::size_t rank = 0;
         shape_t shape;
         DataType dtype = DataType::Float32;
         DeviceType device = DeviceType::CPU;

@@ -16,7 +16,7 @@
 
 #include <cstdint>
 #include <stdexcept>
-#include <unordered_set>
+#include <algorithm>
 #include <vector>
 
 #include "internal/registry/device_context.h"
@@ -45,8 +45,27 @@ void require_live(const Executable::Impl* impl, const char* who) {
     if (impl->graph_lifetime.expired()) throw std::logic_error(std::string(who) + ": owning graph has been destroyed");
 }
 
+Executable::FrozenLayout freeze(const TensorStorage& s) {
+    Executable::FrozenLayout f;
+    f.rank = s.shape.size();
+    if (f.rank <= f.dims.size())
+        std::copy(s.shape.begin(), s.shape.end(), f.dims.begin());
+    else
+        f.shape = s.shape;
+    f.dtype = s.dtype;
+    f.device = s.device;
+    f.size_bytes = s.size_bytes;
+    return f;
+}
+
+bool same_shape(const shape_t& a, const Executable::FrozenLayout& b) {
+    if (a.size() != b.rank) return false;
+    if (b.rank > b.dims.size()) return a == b.shape;
+    return std::equal(a.begin(), a.end(), b.dims.begin());
+}
+
 bool same_layout(const TensorStorage& a, const Executable::FrozenLayout& b) {
-    return a.shape == b.shape && a.dtype == b.dtype && a.device == b.device && a.size_bytes == b.size_bytes;
+    return same_shape(a.shape, b) && a.dtype == b.dtype && a.device == b.device && a.size_bytes == b.size_bytes;
 }
 
 void verify_watched(const Executable::WatchedStorage& w) {
@@ -90,11 +109,24 @@ const char* bind_violation(const TensorStorage& slot, const ExternalBuffer& buf,
 void Executable::Impl::derive_run_plan() {
     watched.clear();
     index_guards.clear();
-    std::unordered_set<pConstTensorStorage> seen;
-    seen.reserve(4 * topo.size() + 16);
-    watched.reserve(2 * topo.size() + 16);
+    // Storages already watched: an open-addressing set of pointers in one
+    // array (a node-based set allocated once per storage and build).
+    std::size_t operands = 16;
+    for (const auto& cn : topo) operands += cn.inputs.size() + cn.outputs.size();
+    std::size_t cap = 16;
+    while (cap < 2 * operands) cap <<= 1;
+    std::vector<pConstTensorStorage> seen(cap, nullptr);
+    watched.reserve(operands);
     auto watch = [&](pConstTensorStorage s) {
-        if (seen.insert(s).second) watched.push_back(WatchedStorage{s, FrozenLayout{s->shape, s->dtype, s->device, s->size_bytes}});
+        std::size_t h = (reinterpret_cast<std::uintptr_t>(s) >> 4) * 0x9E3779B97F4A7C15ull;
+        for (std::size_t i = h & (cap - 1);; i = (i + 1) & (cap - 1)) {
+            if (seen[i] == s) return;
+            if (seen[i] == nullptr) {
+                seen[i] = s;
+                break;
+            }
+        }
+        watched.push_back(WatchedStorage{s, freeze(*s)});
     };
     for (std::size_t i = 0; i < topo.size(); ++i) {
         const CompiledNode& cn = topo[i];

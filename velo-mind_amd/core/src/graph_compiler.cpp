@@ -10,9 +10,10 @@
 // lifetime intersects its own, slots rounded up to 256 bytes.  On HIP the
 // arena is a single device allocation.
 //
-// Everything is staged on copies of the graph's storage list and only
-// committed after the last allocation, so a failed build leaves the graph
-// unchanged and buildable again.  VELOMIND_FAIL_GRAPH_BUILD_AFTER_ALLOCATIONS=N
+// Allocations are staged on a copy of the graph's storage list (arena
+// placements written into the graph's own storages only after the last
+// step that can fail, and undone if one does), so a failed build leaves the
+// graph unchanged and buildable again.  VELOMIND_FAIL_GRAPH_BUILD_AFTER_ALLOCATIONS=N
 // injects a failure after the N-th allocation (the reference's hook of the
 // same name, src/internal/graph_compiler.cpp:563-568).
 #include "internal/graph_compiler.h"
@@ -47,10 +48,10 @@ std::size_t align_up(std::size_t v, std::size_t a) { return (v + a - 1) / a * a;
 
 // Places intervals; returns the arena size.  Lifetimes are inclusive
 // ranges of step indices, so two intersect exactly when they share a step:
-// the placed intervals alive at each step are kept in per-step lists, and
-// an interval's conflicts are gathered from the steps it spans instead of
-// from every interval placed before it (the scan over all earlier
-// intervals made a ~1000-node decode graph's plan quadratic).
+// an interval's conflicts are the intervals placed before it that cover
+// one of the steps it spans, gathered from per-step lists instead of from
+// every interval placed before it (the scan over all earlier intervals
+// made a ~1000-node decode graph's plan quadratic).
 std::size_t plan_arena(std::vector<Interval>& items) {
     std::sort(items.begin(), items.end(), [](const Interval& a, const Interval& b) {
         if (a.bytes != b.bytes) return a.bytes > b.bytes;
@@ -61,7 +62,20 @@ std::size_t plan_arena(std::vector<Interval>& items) {
     });
     std::size_t steps = 0;
     for (const auto& it : items) steps = std::max(steps, it.death + 1);
-    std::vector<std::vector<std::size_t>> alive(steps);   // placed intervals per step
+    // The intervals covering each step, in placement order, in one flat
+    // array (cover[first[st] .. first[st + 1])): those placed before
+    // interval i are the entries below i.  One allocation instead of a
+    // growing list per step (~2,400 heap allocations per decode graph).
+    std::vector<std::size_t> first(steps + 1, 0);
+    for (const auto& it : items)
+        for (std::size_t st = it.birth; st <= it.death; ++st) ++first[st + 1];
+    for (std::size_t st = 0; st < steps; ++st) first[st + 1] += first[st];
+    std::vector<std::size_t> cover(first[steps]);
+    {
+        std::vector<std::size_t> fill(first.begin(), first.end() - 1);
+        for (std::size_t i = 0; i < items.size(); ++i)
+            for (std::size_t st = items[i].birth; st <= items[i].death; ++st) cover[fill[st]++] = i;
+    }
     std::vector<std::size_t> seen(items.size(), SIZE_MAX);
     std::vector<const Interval*> live;
     std::vector<std::size_t> candidates;
@@ -70,11 +84,13 @@ std::size_t plan_arena(std::vector<Interval>& items) {
         Interval& cur = items[i];
         live.clear();
         for (std::size_t st = cur.birth; st <= cur.death; ++st)
-            for (std::size_t j : alive[st])
+            for (std::size_t e = first[st]; e < first[st + 1] && cover[e] < i; ++e) {
+                const std::size_t j = cover[e];
                 if (seen[j] != i) {
                     seen[j] = i;
                     live.push_back(&items[j]);
                 }
+            }
         candidates.assign(1, 0);
         for (const auto* p : live) candidates.push_back(p->offset + p->slot);
         std::sort(candidates.begin(), candidates.end());
@@ -92,7 +108,6 @@ std::size_t plan_arena(std::vector<Interval>& items) {
             }
         }
         total = std::max(total, cur.offset + cur.slot);
-        for (std::size_t st = cur.birth; st <= cur.death; ++st) alive[st].push_back(i);
     }
     return total;
 }
@@ -704,24 +719,28 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
             throw std::runtime_error("Graph::build: injected allocation-stage failure");
     };
     std::vector<std::shared_ptr<TensorStorage>> staged = tensors;
+    // Arena intermediates and byte-preserving aliases keep their storage
+    // objects: where their bytes live is recorded here and written into
+    // them just before the run plan is derived (undone if a later step
+    // throws), so the build allocates no second object per tensor.
+    struct Placement {
+        std::size_t tensor = 0;
+        void* data = nullptr;
+        std::size_t offset = 0, capacity = 0;
+        std::shared_ptr<void> owner;
+    };
+    std::vector<Placement> placed;
+    std::vector<std::size_t> placed_at(tensors.size(), SIZE_MAX);
+    placed.reserve(arena_items.size() + tensors.size() / 4);
     MemoryPlanStats stats;
     if (arena_bytes > 0) {
         auto arena = allocate_checked(arena_bytes, device);
         ++stats.allocation_count;
         count_allocation();
         for (const auto& it : arena_items) {
-            const auto& src = *tensors[it.tensor];
-            auto view = std::make_shared<TensorStorage>();
-            view->shape = src.shape;
-            view->strides = src.strides.empty() ? default_strides(src.shape) : src.strides;
-            view->dtype = src.dtype;
-            view->device = device;
-            view->size_bytes = src.size_bytes;
-            view->offset_bytes = it.offset;
-            view->capacity_bytes = arena->capacity_bytes;
-            view->data = static_cast<char*>(arena->data) + it.offset;
-            view->external_owner = arena;
-            staged[it.tensor] = std::move(view);
+            placed_at[it.tensor] = placed.size();
+            placed.push_back(Placement{it.tensor, static_cast<char*>(arena->data) + it.offset, it.offset,
+                                       arena->capacity_bytes, arena});
         }
     }
     std::size_t dedicated_bytes = 0;
@@ -741,19 +760,14 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
 
     for (std::size_t i = 0; i < tensors.size(); ++i) {
         if (root[i] == i) continue;
-        const auto& src = *tensors[i];
-        const auto& base = staged[root[i]];
-        auto view = std::make_shared<TensorStorage>();
-        view->shape = src.shape;
-        view->strides = src.strides.empty() ? default_strides(src.shape) : src.strides;
-        view->dtype = src.dtype;
-        view->device = device;
-        view->size_bytes = src.size_bytes;
-        view->offset_bytes = base->offset_bytes;
-        view->capacity_bytes = base->capacity_bytes;
-        view->data = base->data;
-        view->external_owner = base->external_owner ? base->external_owner : std::shared_ptr<void>(base);
-        staged[i] = std::move(view);
+        if (placed_at[root[i]] != SIZE_MAX) {
+            const Placement b = placed[placed_at[root[i]]];
+            placed.push_back(Placement{i, b.data, b.offset, b.capacity, b.owner});
+        } else {
+            const auto& base = staged[root[i]];
+            placed.push_back(Placement{i, base->data, base->offset_bytes, base->capacity_bytes,
+                                       base->external_owner ? base->external_owner : std::shared_ptr<void>(base)});
+        }
     }
 
     stats.peak_bytes = arena_bytes + dedicated_bytes;
@@ -838,7 +852,44 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
         cn.attrs = node_desc(node->op());
         impl->topo.push_back(std::move(cn));
     }
-    impl->derive_run_plan();
+    // Placements into the graph's own storages, then nothing may fail: a
+    // throw from here on restores the fields written.
+    struct Prior {
+        bool no_strides;
+        DeviceType device;
+        std::size_t offset, capacity;
+        void* data;
+        std::shared_ptr<void> owner;
+    };
+    std::vector<Prior> prior;
+    prior.reserve(placed.size());
+    for (const auto& pl : placed) {
+        auto& t = *tensors[pl.tensor];
+        prior.push_back(Prior{t.strides.empty(), t.device, t.offset_bytes, t.capacity_bytes, t.data, t.external_owner});
+        if (t.strides.empty()) t.strides = default_strides(t.shape);
+        t.device = device;
+        t.offset_bytes = pl.offset;
+        t.capacity_bytes = pl.capacity;
+        t.data = pl.data;
+        t.external_owner = pl.owner;
+    }
+    std::unique_ptr<Executable> exec;
+    try {
+        impl->derive_run_plan();
+        exec = std::make_unique<Executable>();
+    } catch (...) {
+        for (std::size_t j = 0; j < placed.size(); ++j) {
+            auto& t = *tensors[placed[j].tensor];
+            const auto& pr = prior[j];
+            if (pr.no_strides) t.strides.clear();
+            t.device = pr.device;
+            t.offset_bytes = pr.offset;
+            t.capacity_bytes = pr.capacity;
+            t.data = pr.data;
+            t.external_owner = pr.owner;
+        }
+        throw;
+    }
 
     // Commit.
     graph._tensors.swap(staged);
@@ -850,7 +901,6 @@ auto GraphCompiler::compile(Graph& graph, DeviceType device) -> std::unique_ptr<
     graph._built = true;
     graph._bound_device = device;
     graph._plan_stats = stats;
-    auto exec = std::make_unique<Executable>();
     exec->_impl = std::move(impl);
     return exec;
 }

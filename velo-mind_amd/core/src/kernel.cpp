@@ -38,7 +38,14 @@ auto op_signature(Op op, std::span<const pConstTensorStorage> inputs, const OpAt
         if (!t) throw std::invalid_argument("Graph::op: null input storage");
         if (t->size_bytes < storage_nbytes(*t)) throw std::invalid_argument("Graph::op: invalid input capacity");
     }
-    const OpAttrs effective = std::holds_alternative<NoAttrs>(attrs) ? default_op_attrs(op) : attrs;
+    // The node's own attributes by reference (a copy allocates for every
+    // vector-valued attribute, twice per node and decode step); the
+    // operator's defaults only when it carries none.
+    if (!std::holds_alternative<NoAttrs>(attrs)) {
+        validate_op_metadata(op, inputs, attrs);
+        return fn(inputs, attrs);
+    }
+    const OpAttrs effective = default_op_attrs(op);
     validate_op_metadata(op, inputs, effective);
     return fn(inputs, effective);
 }
