@@ -19,6 +19,7 @@
 #include "internal/graph_compiler.h"
 
 #include <algorithm>
+#include <array>
 #include <cstdint>
 #include <span>
 #include <cstdlib>
@@ -131,8 +132,52 @@ std::size_t injected_failure_point() {
 // tensor it reads is already available there; memory lifetimes are planned
 // on the steps, so tensors the group writes early never share arena space
 // with anything still live.  VELOMIND_GROUP_QMM=0 keeps every node on its own.
+// The nodes of a step: up to kInline in place, more on the heap (most
+// steps run one node; a vector allocated once per step and build).
+class StepNodes {
+public:
+    static constexpr std::size_t kInline = 4;
+    StepNodes() = default;
+    StepNodes(const StepNodes& o) { *this = o; }
+    StepNodes& operator=(const StepNodes& o) {
+        if (this == &o) return *this;
+        _n = 0;
+        _heap.clear();
+        for (auto* p : o) push_back(p);
+        return *this;
+    }
+    StepNodes(StepNodes&& o) noexcept : _in(o._in), _heap(std::move(o._heap)), _n(o._n) { o._n = 0; }
+    StepNodes& operator=(StepNodes&& o) noexcept {
+        _in = o._in;
+        _heap = std::move(o._heap);
+        _n = o._n;
+        o._heap.clear();
+        o._n = 0;
+        return *this;
+    }
+    void push_back(pConstNode p) {
+        if (_heap.empty() && _n < kInline) {
+            _in[_n++] = p;
+            return;
+        }
+        if (_heap.empty()) _heap.assign(_in.begin(), _in.begin() + static_cast<std::ptrdiff_t>(_n));
+        _heap.push_back(p);
+        _n = _heap.size();
+    }
+    std::size_t size() const noexcept { return _n; }
+    bool empty() const noexcept { return _n == 0; }
+    const pConstNode* begin() const noexcept { return _heap.empty() ? _in.data() : _heap.data(); }
+    const pConstNode* end() const noexcept { return begin() + _n; }
+    pConstNode front() const noexcept { return *begin(); }
+
+private:
+    std::array<pConstNode, kInline> _in{};
+    std::vector<pConstNode> _heap;   // all nodes once there are more than kInline
+    std::size_t _n = 0;
+};
+
 struct Step {
-    std::vector<pConstNode> nodes;            // graph nodes the step runs
+    StepNodes nodes;                          // graph nodes the step runs
     int fused = -1;                           // FusedKind, or -1
     std::vector<pConstTensorStorage> ins;     // fused: the chain's external operands
     std::vector<pConstTensorStorage> outs;
