@@ -5,6 +5,7 @@
 // include/velomind/graph.h:50-137.
 #pragma once
 
+#include <array>
 #include <cstddef>
 #include <memory>
 #include <optional>
@@ -102,7 +103,7 @@ public:
     auto node_tot() const -> std::size_t { return _nodes.size(); }
 
 private:
-    auto _op_impl(OpDescriptor desc, std::vector<pConstTensorStorage> inputs) -> Tensor;
+    auto _op_impl(OpDescriptor desc, std::span<const pConstTensorStorage> inputs) -> Tensor;
     auto _compute_required_nodes() const -> std::vector<bool>;
     auto _topological_order() const -> std::vector<pConstNode>;
     auto _topological_order(const std::vector<bool>& req) const -> std::vector<pConstNode>;
@@ -137,8 +138,8 @@ auto Graph::op(OpDescriptor desc, Inputs&&... inputs) -> Tensor {
     if (_built) throw std::logic_error("Graph::op: graph is already built");
     if (((inputs.graph() != this || inputs.storage() == nullptr) || ...))
         throw std::invalid_argument("Graph::op: invalid or foreign tensor handle");
-    std::vector<pConstTensorStorage> ptrs{inputs.storage()...};
-    return _op_impl(std::move(desc), std::move(ptrs));
+    const std::array<pConstTensorStorage, sizeof...(Inputs)> ptrs{inputs.storage()...};
+    return _op_impl(std::move(desc), std::span<const pConstTensorStorage>(ptrs.data(), ptrs.size()));
 }
 
 VELOMIND_EXPORT_PTR(Graph);

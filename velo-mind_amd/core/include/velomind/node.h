@@ -5,6 +5,7 @@
 #include <span>
 #include <vector>
 
+#include "velomind/inline_list.h"
 #include "velomind/ops.h"
 #include "velomind/tensor_storage.h"
 #include "velomind_core_export.h"
@@ -20,8 +21,8 @@ class VELOMIND_CORE_EXPORT Node {
 public:
     Node() = default;
     auto op() const -> const OpDescriptor& { return _op; }
-    auto inputs() const -> std::span<const pConstTensorStorage> { return _inputs; }
-    auto outputs() const -> std::span<const pTensorStorage> { return _outputs; }
+    auto inputs() const -> std::span<const pConstTensorStorage> { return {_inputs.data(), _inputs.size()}; }
+    auto outputs() const -> std::span<const pTensorStorage> { return {_outputs.data(), _outputs.size()}; }
 
 private:
     friend class Graph;
@@ -29,8 +30,8 @@ private:
     friend class internal::GraphCompiler;
 
     OpDescriptor _op;
-    std::vector<pConstTensorStorage> _inputs;
-    std::vector<pTensorStorage> _outputs;
+    InlineList<pConstTensorStorage, 4> _inputs;
+    InlineList<pTensorStorage, 1> _outputs;
 };
 
 VELOMIND_EXPORT_PTR(Node);

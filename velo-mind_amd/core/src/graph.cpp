@@ -79,7 +79,7 @@ auto Graph::input(std::shared_ptr<TensorStorage> storage) -> Tensor {
     return Tensor{this, _tensors.size() - 1};
 }
 
-auto Graph::_op_impl(OpDescriptor desc, std::vector<pConstTensorStorage> inputs) -> Tensor {
+auto Graph::_op_impl(OpDescriptor desc, std::span<const pConstTensorStorage> inputs) -> Tensor {
     if (std::holds_alternative<NoAttrs>(desc.attrs)) desc.attrs = default_op_attrs(desc.op);
     // Shapes and dtypes come only from the signature registry.
     auto sig = internal::op_signature(desc.op, inputs, desc.attrs);
@@ -92,8 +92,9 @@ auto Graph::_op_impl(OpDescriptor desc, std::vector<pConstTensorStorage> inputs)
     _tensors.push_back(std::move(out));
     Node node;
     node._op = std::move(desc);
-    node._inputs = std::move(inputs);
-    node._outputs = {_tensors.back().get()};
+    node._inputs.reserve(inputs.size());
+    for (auto* in : inputs) node._inputs.push_back(in);
+    node._outputs.push_back(_tensors.back().get());
     _nodes.push_back(std::move(node));
     return Tensor{this, _tensors.size() - 1};
 }
